@@ -1,0 +1,280 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decoder hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): q4 GEMV achieved HBM GB/s on the
+Qwen3-0.6B lm_head shape [151936 x 1024], batch 1, with the weights rotated
+over more than 2 GB of copies so that every call streams from HBM (the 256 MB
+Infinity Cache holds one copy). A step is one qwh_linear call (activation
+prepare + GEMV). Also reported: the GEMV kernel alone (HIP events on the
+library stream), the rest of the 0.6B sweep, the 1.7B decoder step in tokens/s
+at batch 1 and 16 with a q8 cache at 4096 positions, configs 1, 3
+and 4, and the single-core CPU restatement of the same GEMV.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "q4 GEMV achieved HBM GB/s (% peak); decoder tokens/sec at 1.7B shape, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def q4_gemv_bytes(rows, cols):
+    # Algorithmic bytes of one batch-1 call: codes + f16 scales (34 B per 64
+    # weights), f32 activations in, f32 outputs out.
+    return rows * cols * 34 // 64 + 4 * cols + 4 * rows
+
+
+def time_events(ctx, fn, steps):
+    ctx.sync()
+    ctx.event_record(0)
+    for i in range(steps):
+        fn(i)
+    ctx.event_record(1)
+    ms = ctx.event_elapsed_ms(0, 1)
+    ctx.sync()
+    return ms / steps
+
+
+def bench_gemv(ctx, qa, rows, cols, steps, warmup, rotate_bytes, seed=1, stream=8):
+    per = rows * cols * 34 // 64
+    copies = max(1, math.ceil(rotate_bytes / per))
+    mats = [ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, seed, stream + 1000 * c, 0.02) for c in range(copies)]
+    x = ctx.buffer(cols * 4)
+    ctx.synth_normal(seed, 100 + stream, cols, 1.0, x.ptr)
+    out = ctx.buffer(rows * 4)
+    prep = ctx.buffer(ctx.activation_bytes(cols, 1))
+    ctx.activation_prepare(x.ptr, cols, 1, prep.ptr)
+
+    def call(i):
+        ctx.linear(mats[i % copies], x.ptr, cols, 1, out.ptr)
+
+    def kernel(i):
+        ctx.linear_prepared(mats[i % copies], prep.ptr, 1, out.ptr)
+
+    for i in range(warmup):
+        call(i)
+    call_ms = time_events(ctx, call, steps)
+    kernel_ms = time_events(ctx, kernel, steps)
+    for m in mats:
+        ctx.matrix_release(m)
+    planes = None
+    for b in (x, out, prep):
+        b.free()
+    return dict(copies=copies, call_ms=call_ms, kernel_ms=kernel_ms, bytes=q4_gemv_bytes(rows, cols)), planes
+
+
+def cpu_baseline(ctx, qa, seconds):
+    """The oracle's linearQuantized restatement on the lm_head shape, one
+    thread (the reference CPU path is single threaded), bounded to ~seconds."""
+    from oracle import oracle as o
+
+    rows, cols = 151936, 1024
+    handle = ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, 1, 8, 0.02)
+    sp, dp = ctx.matrix_planes(handle)
+    scales = np.empty(rows * cols // 64 * 2, np.uint8)
+    data = np.empty(rows * cols // 2, np.uint8)
+    ctx._check(ctx.lib.qwh_download(ctx.handle, scales.ctypes.data, sp, scales.nbytes))
+    ctx._check(ctx.lib.qwh_download(ctx.handle, data.ctypes.data, dp, data.nbytes))
+    ctx.matrix_release(handle)
+    x = o.normal(cols, 1, 108)
+    o.set_threads(1)
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        o.linear_quantized(o.Q4, scales, data, rows, cols, x, 1)
+        calls += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / calls
+    return dict(value=q4_gemv_bytes(rows, cols) / dt / 1e9, unit="GB/s", cores=1, kind="port",
+                sample=f"{calls} calls of the oracle's linearQuantized on the lm_head [151936x1024] q4 "
+                       f"shape, 1 thread, {dt * 1e3:.1f} ms/call")
+
+
+def bench_decoder(ctx, qa, batch, steps, warmup):
+    cfg = dict(hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151936,
+               max_positions=4352, eps=1e-6, theta=1e6)
+    dec = qa.Decoder(ctx, batch=batch, **cfg)
+    t0 = time.perf_counter()
+    dec.init_synthetic(4)
+    for b in range(batch):
+        dec.prefill_random(b, 4096, 4)
+    log(f"decoder B={batch}: model + cache ready in {time.perf_counter() - t0:.1f} s")
+    tokens = np.arange(batch, dtype=np.uint32) * 7919 % cfg["vocab"]
+    ids = dec.generate(tokens, warmup)
+    ctx.sync()
+    ctx.event_record(2)
+    ids = dec.generate(ids[-1], steps)
+    ctx.event_record(3)
+    ms = ctx.event_elapsed_ms(2, 3)
+    dec.close()
+    weights = 0
+    hs, ffn, qw, kvw, vocab = 2048, 6144, 2048, 1024, 151936
+    per_layer = qw * hs + 2 * kvw * hs + hs * qw + 2 * ffn * hs + hs * ffn
+    weights = (28 * per_layer + vocab * hs) * 34 // 64
+    pos_mid = 4096 + warmup + steps / 2
+    kv = batch * 28 * 2 * pos_mid * (kvw + kvw // 64 * 2)
+    step_ms = ms / steps
+    gbs = (weights + kv) / (step_ms * 1e-3) / 1e9
+    return dict(batch=batch, tokens_per_s=batch * steps / (ms * 1e-3), ms_per_step=step_ms,
+                bytes_per_step=int(weights + kv), achieved_GBs=gbs, frac=gbs / HBM_PEAK_GBS,
+                context=f"4096..{4096 + warmup + steps}")
+
+
+def bench_small(ctx, qa, steps):
+    from_seed = 1
+    out = {}
+    # Rest of the 0.6B sweep, cache resident (each matrix is
+    # 0.6-1.7 MB; these calls are launch and latency bound).
+    shapes = {"q": (2048, 1024), "k": (1024, 1024), "o": (1024, 2048), "gate": (3072, 1024), "down": (1024, 3072)}
+    sweep = {}
+    for name, (rows, cols) in shapes.items():
+        m = ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, from_seed, 1, 0.02)
+        x = ctx.buffer(cols * 4)
+        ctx.synth_normal(from_seed, 101, cols, 1.0, x.ptr)
+        y = ctx.buffer(rows * 4)
+        ms = time_events(ctx, lambda i: ctx.linear(m, x.ptr, cols, 1, y.ptr), steps)
+        sweep[name] = dict(us=ms * 1e3, GBs=q4_gemv_bytes(rows, cols) / (ms * 1e-3) / 1e9)
+        ctx.matrix_release(m)
+        x.free()
+        y.free()
+    out["q4_sweep_0p6b"] = sweep
+    # q8 GEMV [1024 x 3072].
+    m = ctx.matrix_synthetic(qa.FORMAT_Q8, 1024, 3072, 0, 0, 0.02)
+    x = ctx.buffer(3072 * 4)
+    ctx.synth_normal(0, 1, 3072, 1.0, x.ptr)
+    y = ctx.buffer(1024 * 4)
+    ms = time_events(ctx, lambda i: ctx.linear(m, x.ptr, 3072, 1, y.ptr), steps)
+    out["q8_gemv_1024x3072"] = dict(us=ms * 1e3, GBs=3260416 / (ms * 1e-3) / 1e9)
+    ctx.matrix_release(m)
+    x.free()
+    y.free()
+    # q4 GEMM, bf16 activations, M = 1500 at [6144 x 2048].
+    gemm = {}
+    for rows, cols in ((6144, 2048), (2048, 6144)):
+        m = ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, 2, 1, 0.02)
+        for M in (128, 512, 1500):
+            xf = ctx.buffer(M * cols * 4)
+            ctx.synth_normal(2, 10 + M, M * cols, 1.0, xf.ptr)
+            xb = ctx.buffer(M * cols * 2)
+            # bf16 bits: the top half of each f32 (the bench only needs a
+            # valid bf16 input of the right shape).
+            host = xf.download(np.float32)
+            xb.upload((host.view(np.uint32) >> 16).astype(np.uint16))
+            y = ctx.buffer(M * rows * 4)
+            ms = time_events(ctx, lambda i: ctx.linear_bf16(m, xb.ptr, cols, M, y.ptr), max(3, steps // 3))
+            tflops = 2 * M * rows * cols / (ms * 1e-3) / 1e12
+            gemm[f"M{M}_{rows}x{cols}"] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / MFMA_BF16_PEAK_TFLOPS)
+            for b in (xf, xb, y):
+                b.free()
+        ctx.matrix_release(m)
+    out["q4_gemm_bf16"] = gemm
+    # q8 attention, 16 / 8 heads, head_dim 128.
+    att = {}
+    heads, kvh, hd = 16, 8, 128
+    kvw = kvh * hd
+    for ctx_len, batch in ((4096, 1), (8192, 1), (8192, 8)):
+        vals = ctx.buffer(ctx_len * kvw * 4)
+        ks, kc, vs, vc = [ctx.buffer(batch * ctx_len * n) for n in (kvw // 64 * 2, kvw, kvw // 64 * 2, kvw)]
+        for b in range(batch):
+            for planes, stream in (((ks, kc), 0), ((vs, vc), 1)):
+                ctx.synth_normal(3, 10 * b + stream, ctx_len * kvw, 1.0, vals.ptr)
+                ctx.quantize_rows(qa.FORMAT_Q8, vals.ptr, ctx_len, kvw, planes[0].ptr + b * ctx_len * kvw // 32,
+                                  planes[1].ptr + b * ctx_len * kvw)
+        q = ctx.buffer(batch * heads * hd * 4)
+        ctx.synth_normal(3, 999, batch * heads * hd, 1.0, q.ptr)
+        o_ = ctx.buffer(batch * heads * hd * 4)
+        ms = time_events(ctx, lambda i: ctx.decode_attention_q8(o_.ptr, q.ptr, ks.ptr, kc.ptr, vs.ptr, vc.ptr, ctx_len,
+                                                              heads, kvh, hd, batch, ctx_len * kvw // 32,
+                                                              ctx_len * kvw), steps)
+        nbytes = batch * ctx_len * 2 * kvw * 66 // 64 + batch * heads * hd * 8
+        att[f"ctx{ctx_len}_b{batch}"] = dict(us=ms * 1e3, GBs=nbytes / (ms * 1e-3) / 1e9)
+        for b in (vals, ks, kc, vs, vc, q, o_):
+            b.free()
+    out["q8_attention"] = att
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-decoder", action="store_true")
+    ap.add_argument("--skip-extra", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the hot path is "
+              "single-device; sharding is a design note). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import qwenscriber_amd as qa
+
+    ctx = qa.Context(0)
+    cus = ctx.cus()
+    log(f"device 0: {cus} CUs")
+    rows, cols = 151936, 1024
+    log("lm_head q4 GEMV (rotated over >= 2 GB)")
+    gemv, _ = bench_gemv(ctx, qa, rows, cols, args.steps, args.warmup, 2.1e9)
+    nbytes = gemv["bytes"]
+    value = nbytes / (gemv["call_ms"] * 1e-3) / 1e9
+    achieved = nbytes / (gemv["kernel_ms"] * 1e-3) / 1e9
+    log(f"lm_head: call {gemv['call_ms'] * 1e3:.2f} us ({value:.0f} GB/s), kernel {gemv['kernel_ms'] * 1e3:.2f} us "
+        f"({achieved:.0f} GB/s)")
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": gemv["call_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i4 x i4 -> i32 dot products, f32 combine and accumulate (q4 weights, f32 activations)",
+        "data": "synthetic",
+        "config": {"workload": "q4 GEMV, Qwen3-0.6B lm_head [151936 x 1024], batch 1, group-64 f16 scales "
+                               "(configs[1] graded shape), weights rotated over %d copies (%.2f GB)"
+                               % (gemv["copies"], gemv["copies"] * rows * cols * 34 / 64 / 1e9),
+                   "rows": rows, "cols": cols, "batch": 1, "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_q4_kernel<1,2,4>", "kernel_us": round(gemv["kernel_ms"] * 1e3, 3)},
+    }
+    if not args.skip_decoder:
+        dec = {}
+        for batch in (1, 16):
+            log(f"decoder 1.7B, batch {batch}")
+            dec[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8)
+            log(f"decoder batch {batch}: {dec[f'b{batch}']['tokens_per_s']:.0f} tok/s")
+        result["decoder_1p7b_q4_q8kv_ctx4096"] = dec
+    if not args.skip_extra:
+        log("configs 1, 2 (small shapes), 3, 4")
+        result["kernels"] = bench_small(ctx, qa, max(10, args.steps // 2))
+    if args.cpu_seconds > 0:
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s)")
+        result["cpu_baseline"] = cpu_baseline(ctx, qa, args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,265 @@
+/*
+ * qwhip.h -- C ABI of the MI355X (gfx950) backend for Qwenscriber's quantized
+ * decoder hot path.
+ *
+ * The reference (mattneel/qwenscriber) runs this path in Zig on the CPU
+ * (src/core/qwen3_asr/kernels.zig, decoder.zig) and in WGSL on WebGPU
+ * (the gpu/shaders directory, driven by packages/qwenscriber/src/gpu/text_decoder.ts).
+ * This library is one more backend behind the same operator surface: the
+ * caller keeps the reference's packed weight planes (quant.zig:8-41: groups of
+ * 64, one f16 scale per group in a scale plane, biased unsigned codes in a
+ * data plane) and its q8 key/value cache layout (decoder.zig:58-106), and
+ * calls these entry points instead of the Zig kernels.
+ *
+ * Conventions (mirroring src/wasm/abi.zig and kernels.zig):
+ *   - every entry point returns an int32 status; 0 is success, failures are
+ *     the negative values of abi.zig:50-73 (QWH_E_*), plus QWH_E_DEVICE for a
+ *     HIP runtime failure, which has no counterpart in the reference;
+ *   - shapes are checked before any device work, and a mismatch returns
+ *     QWH_E_SHAPE_MISMATCH, as kernels.zig's Error.ShapeMismatch does;
+ *   - plain pointers and sizes only. `*_dev` pointers are device addresses
+ *     (from qwh_alloc or any HIP allocation on the context's device); other
+ *     pointers are host memory;
+ *   - a context owns one device and one stream. Calls are stream ordered and
+ *     return without waiting, except where a host output is produced (those
+ *     synchronize the stream). A context is used by one host thread at a time.
+ */
+#ifndef QWHIP_H
+#define QWHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWH_ABI_VERSION 0x00010000 /* major << 16 | minor, as abi.zig's abi_version */
+
+/* Status codes: src/wasm/abi.zig:50-73. */
+#define QWH_OK 0
+#define QWH_E_INVALID_ARGUMENT (-1)
+#define QWH_E_OUT_OF_MEMORY (-2)
+#define QWH_E_UNSUPPORTED (-3)
+#define QWH_E_SHAPE_MISMATCH (-7)
+#define QWH_E_INVALID_STATE (-8)
+#define QWH_E_LIMIT_EXCEEDED (-9)
+#define QWH_E_NOT_FOUND (-10)
+/* A HIP runtime error. Not in the reference (it has no device runtime). */
+#define QWH_E_DEVICE (-64)
+
+/* Format ids: src/core/dtype.zig:17-108 (on-disk values, never renumbered). */
+#define QWH_FORMAT_Q4 16
+#define QWH_FORMAT_Q5 17
+#define QWH_FORMAT_Q8 18
+
+/* Quantization group: src/core/quant.zig:49. */
+#define QWH_GROUP_SIZE 64
+
+typedef struct qwh_ctx qwh_ctx;
+
+/* ---------------------------------------------------------------------- */
+/* Context, memory, timing                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces wasm/exports.zig `qw_abi_version`. */
+int32_t qwh_abi_version(void);
+/* Human-readable name of a status code (static storage). */
+const char *qwh_status_string(int32_t status);
+/* Opens device `device_index` with a stream of its own. No reference
+ * counterpart: the Zig core has no device (it replaces model arena setup,
+ * wasm/model.zig:197-204, for the device side). */
+int32_t qwh_create(uint32_t device_index, qwh_ctx **out);
+int32_t qwh_destroy(qwh_ctx *ctx);
+/* Waits for all work queued on the context's stream. */
+int32_t qwh_sync(qwh_ctx *ctx);
+/* Text of the last failure on this context (empty when none). */
+const char *qwh_last_error(qwh_ctx *ctx);
+/* Number of compute units of the context's device. */
+int32_t qwh_device_cus(qwh_ctx *ctx, uint32_t *out);
+
+/* Device buffers for callers without a HIP allocator of their own (a Zig or
+ * JavaScript host). Copies are stream ordered; downloads synchronize. */
+int32_t qwh_alloc(qwh_ctx *ctx, uint64_t bytes, void **out_dev);
+int32_t qwh_free(qwh_ctx *ctx, void *dev);
+int32_t qwh_upload(qwh_ctx *ctx, void *dst_dev, const void *src, uint64_t bytes);
+int32_t qwh_download(qwh_ctx *ctx, void *dst, const void *src_dev, uint64_t bytes);
+int32_t qwh_memset(qwh_ctx *ctx, void *dst_dev, int32_t value, uint64_t bytes);
+
+/* Stream-ordered timing: records event `slot` (0..63) on the context stream;
+ * qwh_event_elapsed synchronizes on `end` and returns milliseconds. */
+int32_t qwh_event_record(qwh_ctx *ctx, uint32_t slot);
+int32_t qwh_event_elapsed(qwh_ctx *ctx, uint32_t start, uint32_t end, float *out_ms);
+
+/* ---------------------------------------------------------------------- */
+/* Quantized matrices (quant.zig planeLayout + kernels.zig Matrix)          */
+/* ---------------------------------------------------------------------- */
+
+/* Uploads a rows x cols quantized matrix given as the two planes
+ * quant.planeLayout (quant.zig:144-176) describes: `scales` is rows *
+ * cols/64 f16 values (little endian, groups row major), `data` the packed
+ * codes. The row count must agree with the scale plane as Matrix.rows
+ * derives it (kernels.zig:170-178). Replaces Binding.matrix
+ * (model.zig:92-114) for the device. */
+int32_t qwh_matrix_upload(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols,
+                          const uint8_t *scales, uint64_t scales_len, const uint8_t *data,
+                          uint64_t data_len, uint64_t *out_matrix);
+/* Borrows planes already resident on the device (for example a whole .qw
+ * shard uploaded at once): the caller keeps them alive until release, as the
+ * reference's Matrix borrows shard bytes (wasm/model.zig:28-42). */
+int32_t qwh_matrix_wrap(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols,
+                        const void *scales_dev, const void *data_dev, uint64_t *out_matrix);
+/* A matrix whose values are f32(N(0,1)) * value_scale from the synthetic
+ * generator (seed, stream), quantized on the device bit-exactly as
+ * quant.quantizeRow. For benchmarks and tests with random-init weights. */
+int32_t qwh_matrix_synthetic(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols,
+                             uint32_t seed, uint32_t stream, float value_scale,
+                             uint64_t *out_matrix);
+/* Device addresses of a matrix's two planes. */
+int32_t qwh_matrix_planes(qwh_ctx *ctx, uint64_t matrix, void **scales_dev, void **data_dev);
+int32_t qwh_matrix_release(qwh_ctx *ctx, uint64_t matrix);
+
+/* kernels.zig:182-206 Matrix.apply / :118-158 linearQuantized:
+ * out[tokens][rows] = W[rows][cols] * x[tokens][cols], f32 in, f32 out.
+ * `cols` must equal the matrix's column count. */
+int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t cols,
+                   uint32_t tokens, float *out_dev);
+/* qwh_linear in two halves, for callers that apply several matrices to the
+ * same activations (decoder.zig:174-176 applies q, k and v to one `normed`
+ * row): qwh_activation_prepare encodes x once into `prepared_dev` (at least
+ * qwh_activation_bytes(cols, tokens) bytes), qwh_linear_prepared multiplies a
+ * q4 matrix by it. The results equal qwh_linear's. */
+int32_t qwh_activation_bytes(uint32_t cols, uint32_t tokens, uint64_t *out_bytes);
+int32_t qwh_activation_prepare(qwh_ctx *ctx, const float *x_dev, uint32_t cols, uint32_t tokens,
+                               void *prepared_dev);
+int32_t qwh_linear_prepared(qwh_ctx *ctx, uint64_t matrix, const void *prepared_dev,
+                            uint32_t tokens, float *out_dev);
+/* The same product with bf16 activations (the prefill / audio-token GEMM of
+ * the reference's tokens > 1 path, kernels.zig:118-158 with tokens = M). The
+ * reference widens each bf16 to f32 (half_float.zig:42-45) before the dot. */
+int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, uint32_t cols,
+                        uint32_t tokens, float *out_dev);
+
+/* ---------------------------------------------------------------------- */
+/* Device quantization (quant.zig:197-288)                                 */
+/* ---------------------------------------------------------------------- */
+
+/* quant.quantizeRow applied to `rows` rows of `cols` f32 values on the
+ * device, bit exact: scales_dev receives rows*cols/64 f16 values, data_dev the
+ * packed codes. Formats q4, q5, q8. */
+int32_t qwh_quantize_rows(qwh_ctx *ctx, int32_t format, const float *values_dev, uint32_t rows,
+                          uint32_t cols, uint8_t *scales_dev, uint8_t *data_dev);
+/* Fills `count` f32 values with the synthetic generator (value i of stream
+ * `stream` under `seed`, times value_scale). */
+int32_t qwh_synth_normal(qwh_ctx *ctx, uint32_t seed, uint32_t stream, uint64_t count,
+                         float value_scale, float *out_dev);
+
+/* ---------------------------------------------------------------------- */
+/* q8 key/value cache and decode attention                                 */
+/* ---------------------------------------------------------------------- */
+
+/* kernels.zig:697-767 decodeAttentionStepQ8, with device pointers:
+ * query_dev [heads*head_dim] f32, the four planes of one layer's cache
+ * (decoder.zig:58-65 cachePlane: k/v scales [positions][kv_heads*head_dim/64]
+ * f16, k/v codes [positions][kv_heads*head_dim] u8), `cached` positions read.
+ * `batch` independent sequences are laid out back to back: query and out
+ * advance by heads*head_dim floats, the planes by `plane_stride_bytes`
+ * (scales) and `code_stride_bytes` (codes) per sequence. */
+int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query_dev,
+                                const uint8_t *k_scales_dev, const uint8_t *k_codes_dev,
+                                const uint8_t *v_scales_dev, const uint8_t *v_codes_dev,
+                                uint32_t cached, uint32_t heads, uint32_t kv_heads,
+                                uint32_t head_dim, uint32_t batch, uint64_t scale_stride_bytes,
+                                uint64_t code_stride_bytes);
+
+/* decoder.zig:68-106 appendCacheRow (q8): quantizes one key row and one value
+ * row of kv_width f32 values into row `position` of a layer's planes, bit
+ * exact with quant.quantizeRow(.q8). */
+int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_dev,
+                         uint32_t kv_width, uint32_t position, uint8_t *k_scales_dev,
+                         uint8_t *k_codes_dev, uint8_t *v_scales_dev, uint8_t *v_codes_dev);
+
+/* ---------------------------------------------------------------------- */
+/* Decoder step (decoder.zig:133-339)                                      */
+/* ---------------------------------------------------------------------- */
+
+/* model_config.zig:110-258, the fields the decoder step reads. */
+typedef struct {
+    uint32_t hidden;        /* text_hidden_size */
+    uint32_t layers;        /* text_layers */
+    uint32_t heads;         /* text_attention_heads */
+    uint32_t kv_heads;      /* text_key_value_heads */
+    uint32_t head_dim;      /* text_head_dim */
+    uint32_t ffn;           /* text_ffn_dim */
+    uint32_t vocab;         /* vocab_size */
+    uint32_t max_positions; /* max_positions (model.zig:62 caps it at 8192) */
+    float eps;              /* text_rms_norm_eps */
+    float theta;            /* rope_theta */
+} qwh_decoder_config;
+
+/* Tensor kinds a decoder binds (layout.zig decoder tensors). */
+#define QWH_T_EMBED 0
+#define QWH_T_Q 1
+#define QWH_T_K 2
+#define QWH_T_V 3
+#define QWH_T_O 4
+#define QWH_T_GATE 5
+#define QWH_T_UP 6
+#define QWH_T_DOWN 7
+#define QWH_T_LM_HEAD 8
+#define QWH_T_ATTN_NORM 16
+#define QWH_T_Q_NORM 17
+#define QWH_T_K_NORM 18
+#define QWH_T_FFN_NORM 19
+#define QWH_T_FINAL_NORM 20
+
+typedef struct qwh_decoder qwh_decoder;
+
+/* Creates a decoder for `batch` independent sequences, each with its own q8
+ * key/value cache of config->max_positions positions (decoder.zig:58-65
+ * layout, per layer [scales][codes]). RoPE tables are built on the host by
+ * kernels.zig:534-564 (buildRopeTables) semantics, as model.zig:400-407 does. */
+int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch,
+                           qwh_decoder **out);
+int32_t qwh_decoder_destroy(qwh_decoder *decoder);
+/* Binds a quantized matrix (QWH_T_EMBED..QWH_T_LM_HEAD). The decoder copies
+ * the q/k/v and gate/up planes into fused row blocks; the others are borrowed.
+ * Layer is ignored for EMBED and LM_HEAD. */
+int32_t qwh_decoder_set_matrix(qwh_decoder *decoder, uint32_t kind, uint32_t layer,
+                               uint64_t matrix);
+/* Binds an f32 norm weight vector (host pointer, copied). */
+int32_t qwh_decoder_set_vector(qwh_decoder *decoder, uint32_t kind, uint32_t layer,
+                               const float *values, uint32_t count);
+/* Binds every matrix from the synthetic generator: each linear q4 with
+ * values f32(N(0,1)) * 0.02, stream ids as the oracle's synthetic model,
+ * all norm weights 1.0. */
+int32_t qwh_decoder_init_synthetic(qwh_decoder *decoder, uint32_t seed);
+/* decoder.zig:109-121 reset: zeroes every cache and sets positions to 0. */
+int32_t qwh_decoder_reset(qwh_decoder *decoder);
+/* Fills positions [0, count) of sequence `seq`'s caches with quantizeRow(.q8)
+ * of synthetic N(0,1) rows and sets its position to `count`. */
+int32_t qwh_decoder_prefill_random(qwh_decoder *decoder, uint32_t seq, uint32_t count,
+                                   uint32_t seed);
+/* Device addresses of sequence `seq`, layer `layer`'s cache planes. */
+int32_t qwh_decoder_cache_planes(qwh_decoder *decoder, uint32_t seq, uint32_t layer,
+                                 void **k_scales, void **k_codes, void **v_scales,
+                                 void **v_codes);
+int32_t qwh_decoder_position(qwh_decoder *decoder, uint32_t seq, uint32_t *out);
+int32_t qwh_decoder_set_position(qwh_decoder *decoder, uint32_t seq, uint32_t position);
+/* decoder.zig:133-287 forwardToken for every sequence at once: tokens[b] is
+ * sequence b's token. With want_logits the logits stay on the device. */
+int32_t qwh_decoder_forward(qwh_decoder *decoder, const uint32_t *tokens, int32_t want_logits);
+/* decoder.zig:336-339 step: forwardToken then argmaxLogits (:290-301, first
+ * maximum wins) for every sequence; next_tokens receives batch ids. */
+int32_t qwh_decoder_step(qwh_decoder *decoder, const uint32_t *tokens, uint32_t *next_tokens);
+/* Runs `steps` greedy steps, feeding each argmax back, entirely on the device
+ * (the step graph is replayed without host round trips); ids_out receives
+ * steps x batch ids, step major. */
+int32_t qwh_decoder_generate(qwh_decoder *decoder, const uint32_t *tokens, uint32_t steps,
+                             uint32_t *ids_out);
+/* Copies sequence `seq`'s last logits (vocab f32) to the host. */
+int32_t qwh_decoder_logits(qwh_decoder *decoder, uint32_t seq, float *out, uint32_t count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,347 @@
+"""ctypes binding of the CPU oracle (oracle/build/libqwref.so). TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker or the timed CPU baseline. The functions
+mirror the reference's Zig kernels; see qwref.c for the file:line each follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libqwref.so")
+
+Q4, Q5, Q8 = 16, 17, 18
+GROUP = 64
+DATA_BYTES = {Q4: 32, Q5: 40, Q8: 64}
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [
+        ("scales_offset_bytes", ctypes.c_uint64),
+        ("scales_len_bytes", ctypes.c_uint64),
+        ("data_offset_bytes", ctypes.c_uint64),
+        ("data_len_bytes", ctypes.c_uint64),
+        ("total_len_bytes", ctypes.c_uint64),
+        ("group_count", ctypes.c_uint32),
+        ("groups_per_row", ctypes.c_uint32),
+    ]
+
+
+class DecoderConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_uint32),
+        ("layers", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("ffn", ctypes.c_uint32),
+        ("vocab", ctypes.c_uint32),
+        ("max_positions", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("theta", ctypes.c_float),
+    ]
+
+
+_P = ctypes.c_void_p
+_U8 = ctypes.c_uint8
+_U16 = ctypes.c_uint16
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+
+_SIGNATURES = {
+    "qwref_to_f16": (_U16, [_F]),
+    "qwref_from_f16": (_F, [_U16]),
+    "qwref_to_bf16": (_U16, [_F]),
+    "qwref_from_bf16": (_F, [_U16]),
+    "qwref_bias": (_I32, [_I32]),
+    "qwref_data_bytes_per_group": (_I32, [_I32]),
+    "qwref_plane_layout": (_I32, [_I32, _U32, _U32, _U64, _U64, ctypes.POINTER(Layout)]),
+    "qwref_plane_bytes": (_U64, [_I32, _U32, _U32]),
+    "qwref_quantize_row": (None, [_I32, _P, _U32, _P, _P]),
+    "qwref_quantize_rows": (None, [_I32, _P, _U32, _U32, _P, _P]),
+    "qwref_dequantize_row": (None, [_I32, _P, _P, _P, _U32]),
+    "qwref_dot_row": (_F, [_I32, _P, _P, _P, _U32]),
+    "qwref_quant_hash": (_U64, []),
+    "qwref_fnv1a64": (_U64, [_P, _U64, _U64]),
+    "qwref_dot_f32": (_F, [_P, _P, _U32]),
+    "qwref_linear_quantized": (_I32, [_P, _P, _I32, _P, _U64, _P, _U64, _U32, _U32, _U32]),
+    "qwref_linear_f32": (_I32, [_P, _P, _P, _U32, _U32, _U32]),
+    "qwref_add_in_place": (None, [_P, _P, _U32]),
+    "qwref_silu_mul": (None, [_P, _P, _P, _U32]),
+    "qwref_silu": (_F, [_F]),
+    "qwref_softmax_in_place": (None, [_P, _U32]),
+    "qwref_rms_norm": (None, [_P, _P, _U32, _U32, _F]),
+    "qwref_inverse_frequency": (_F, [_U32, _U32, _F]),
+    "qwref_build_rope_tables": (None, [_P, _P, _U32, _F, _U32, _U32]),
+    "qwref_rope_in_place": (None, [_P, _P, _U32, _U32, _U32, _P, _P, _U32]),
+    "qwref_decode_attention_step": (_I32, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
+    "qwref_decode_attention_step_q8": (_I32, [_P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32]),
+    "qwref_argmax": (_U32, [_P, _U32]),
+    "qwref_mulberry32_at": (_U32, [_U32, _U64]),
+    "qwref_normal_at": (_F, [_U32, _U32, _U64]),
+    "qwref_fill_normal": (None, [_P, _U64, _U32, _U32, _F]),
+    "qwref_stream_base": (_U32, [_U32, _U32]),
+    "qwref_decoder_create_synthetic": (_P, [ctypes.POINTER(DecoderConfig), _U32, _U32]),
+    "qwref_decoder_destroy": (None, [_P]),
+    "qwref_decoder_prefill_random": (_I32, [_P, _U32, _U32]),
+    "qwref_decoder_forward": (_I32, [_P, _U32, _U32, _I32]),
+    "qwref_decoder_logits": (ctypes.POINTER(ctypes.c_float), [_P, _U32]),
+    "qwref_decoder_position": (_U32, [_P, _U32]),
+    "qwref_decoder_step": (_I32, [_P, _U32, _U32, ctypes.POINTER(_U32)]),
+    "qwref_decoder_weights_hash": (_U64, [_P]),
+    "qwref_decoder_cache_hash": (_U64, [_P, _U32]),
+    "qwref_synthetic_start_token": (_U32, [_U32, _U32, _U32]),
+    "qwref_set_threads": (None, [_I32]),
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def _ptr(array: np.ndarray) -> int:
+    assert array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data
+
+
+def set_threads(n: int) -> None:
+    lib().qwref_set_threads(int(n))
+
+
+def to_f16(value: float) -> int:
+    return lib().qwref_to_f16(value)
+
+
+def from_f16(bits: int) -> float:
+    return lib().qwref_from_f16(bits)
+
+
+def quant_hash() -> int:
+    return lib().qwref_quant_hash()
+
+
+def fnv1a64(data: bytes | np.ndarray, state: int = 0xCBF29CE484222325) -> int:
+    buf = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8) if isinstance(data, bytes) else data).view(np.uint8)
+    return lib().qwref_fnv1a64(_ptr(buf), buf.size, state)
+
+
+def plane_layout(fmt: int, rows: int, cols: int, base: int = 0, alignment: int = 16):
+    out = Layout()
+    status = lib().qwref_plane_layout(fmt, rows, cols, base, alignment, ctypes.byref(out))
+    return status, out
+
+
+def plane_bytes(fmt: int, positions: int, cols: int) -> int:
+    return lib().qwref_plane_bytes(fmt, positions, cols)
+
+
+def quantize_rows(fmt: int, values: np.ndarray):
+    """quantizeRow per row: returns (scales u8 [rows*gpr*2], data u8)."""
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    rows, cols = values.shape if values.ndim == 2 else (1, values.shape[0])
+    gpr = cols // GROUP
+    scales = np.zeros(rows * gpr * 2, np.uint8)
+    data = np.zeros(rows * gpr * DATA_BYTES[fmt], np.uint8)
+    lib().qwref_quantize_rows(fmt, _ptr(values), rows, cols, _ptr(scales), _ptr(data))
+    return scales, data
+
+
+def dequantize_rows(fmt: int, scales: np.ndarray, data: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    gpr = cols // GROUP
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        s = np.ascontiguousarray(scales[r * gpr * 2:(r + 1) * gpr * 2])
+        d = np.ascontiguousarray(data[r * gpr * DATA_BYTES[fmt]:(r + 1) * gpr * DATA_BYTES[fmt]])
+        row = np.zeros(cols, np.float32)
+        lib().qwref_dequantize_row(fmt, _ptr(s), _ptr(d), _ptr(row), cols)
+        out[r] = row
+    return out
+
+
+def dot_row(fmt: int, scales: np.ndarray, data: np.ndarray, x: np.ndarray) -> float:
+    x = np.ascontiguousarray(x, np.float32)
+    return lib().qwref_dot_row(fmt, _ptr(np.ascontiguousarray(scales)), _ptr(np.ascontiguousarray(data)), _ptr(x), x.size)
+
+
+def dot_f32(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().qwref_dot_f32(_ptr(a), _ptr(b), a.size)
+
+
+def linear_quantized(fmt: int, scales: np.ndarray, data: np.ndarray, rows: int, cols: int,
+                     x: np.ndarray, tokens: int = 1) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(tokens * rows, np.float32)
+    scales = np.ascontiguousarray(scales)
+    data = np.ascontiguousarray(data)
+    status = lib().qwref_linear_quantized(_ptr(out), _ptr(x), fmt, _ptr(scales), scales.size,
+                                          _ptr(data), data.size, rows, cols, tokens)
+    if status != 0:
+        raise ValueError(f"linear_quantized status {status}")
+    return out.reshape(tokens, rows)
+
+
+def linear_f32(weights: np.ndarray, x: np.ndarray, tokens: int = 1) -> np.ndarray:
+    weights = np.ascontiguousarray(weights, np.float32)
+    rows, cols = weights.shape
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(tokens * rows, np.float32)
+    lib().qwref_linear_f32(_ptr(out), _ptr(x), _ptr(weights), rows, cols, tokens)
+    return out.reshape(tokens, rows)
+
+
+def silu(x: float) -> float:
+    return lib().qwref_silu(x)
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, np.float32)
+    up = np.ascontiguousarray(up, np.float32)
+    out = np.zeros_like(gate)
+    lib().qwref_silu_mul(_ptr(out), _ptr(gate), _ptr(up), gate.size)
+    return out
+
+
+def softmax(row: np.ndarray) -> np.ndarray:
+    row = np.array(row, np.float32)
+    lib().qwref_softmax_in_place(_ptr(row), row.size)
+    return row
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray, width: int, eps: float) -> np.ndarray:
+    x = np.array(x, np.float32).reshape(-1)
+    weight = np.ascontiguousarray(weight, np.float32)
+    lib().qwref_rms_norm(_ptr(x), _ptr(weight), width, x.size // width, eps)
+    return x
+
+
+def inverse_frequency(index: int, head_dim: int, theta: float) -> float:
+    return lib().qwref_inverse_frequency(index, head_dim, theta)
+
+
+def rope_tables(half: int, theta: float, max_positions: int):
+    cos = np.zeros(max_positions * half, np.float32)
+    sin = np.zeros(max_positions * half, np.float32)
+    lib().qwref_build_rope_tables(_ptr(cos), _ptr(sin), half, theta, max_positions, half)
+    return cos, sin
+
+
+def rope(x: np.ndarray, positions, heads: int, head_dim: int, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    x = np.array(x, np.float32).reshape(-1)
+    positions = np.ascontiguousarray(positions, np.uint32)
+    lib().qwref_rope_in_place(_ptr(x), _ptr(positions), positions.size, heads, head_dim, _ptr(cos), _ptr(sin), head_dim // 2)
+    return x
+
+
+def decode_attention(query, keys, values, cached, heads, kv_heads, head_dim) -> np.ndarray:
+    query = np.ascontiguousarray(query, np.float32)
+    keys = np.ascontiguousarray(keys, np.float32)
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.zeros(heads * head_dim, np.float32)
+    status = lib().qwref_decode_attention_step(_ptr(out), _ptr(query), _ptr(keys), _ptr(values), cached, heads, kv_heads, head_dim)
+    if status != 0:
+        raise ValueError(f"decode_attention status {status}")
+    return out
+
+
+def decode_attention_q8(query, k_scales, k_codes, v_scales, v_codes, cached, heads, kv_heads, head_dim) -> np.ndarray:
+    arrays = [np.ascontiguousarray(a) for a in (query, k_scales, k_codes, v_scales, v_codes)]
+    out = np.zeros(heads * head_dim, np.float32)
+    status = lib().qwref_decode_attention_step_q8(_ptr(out), *[_ptr(a) for a in arrays], cached, heads, kv_heads, head_dim)
+    if status != 0:
+        raise ValueError(f"decode_attention_q8 status {status}")
+    return out
+
+
+def argmax(logits: np.ndarray) -> int:
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().qwref_argmax(_ptr(logits), logits.size)
+
+
+def mulberry32_at(base: int, draw: int) -> int:
+    return lib().qwref_mulberry32_at(base, draw)
+
+
+def stream_base(seed: int, stream: int) -> int:
+    return lib().qwref_stream_base(seed, stream)
+
+
+def normal(count: int, seed: int, stream: int = 0, scale: float = 1.0) -> np.ndarray:
+    out = np.zeros(count, np.float32)
+    lib().qwref_fill_normal(_ptr(out), count, seed, stream, scale)
+    return out
+
+
+class Decoder:
+    """decoder.zig restatement over a synthetic q4 model with a q8 cache."""
+
+    def __init__(self, seed: int, batch: int = 1, **config):
+        self.config = DecoderConfig(**config)
+        self.handle = lib().qwref_decoder_create_synthetic(ctypes.byref(self.config), seed, batch)
+        self.seed = seed
+        self.batch = batch
+
+    def close(self):
+        if self.handle:
+            lib().qwref_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def prefill_random(self, seq: int, count: int) -> None:
+        assert lib().qwref_decoder_prefill_random(self.handle, seq, count) == 0
+
+    def forward(self, seq: int, token: int, want_logits: bool = True) -> None:
+        status = lib().qwref_decoder_forward(self.handle, seq, token, int(want_logits))
+        if status != 0:
+            raise ValueError(f"forward status {status}")
+
+    def logits(self, seq: int) -> np.ndarray:
+        ptr = lib().qwref_decoder_logits(self.handle, seq)
+        return np.ctypeslib.as_array(ptr, shape=(self.config.vocab,)).copy()
+
+    def position(self, seq: int) -> int:
+        return lib().qwref_decoder_position(self.handle, seq)
+
+    def step(self, seq: int, token: int) -> int:
+        out = ctypes.c_uint32(0)
+        status = lib().qwref_decoder_step(self.handle, seq, token, ctypes.byref(out))
+        if status != 0:
+            raise ValueError(f"step status {status}")
+        return out.value
+
+    def weights_hash(self) -> int:
+        return lib().qwref_decoder_weights_hash(self.handle)
+
+    def cache_hash(self, seq: int) -> int:
+        return lib().qwref_decoder_cache_hash(self.handle, seq)
+
+
+def start_token(seed: int, seq: int, vocab: int) -> int:
+    return lib().qwref_synthetic_start_token(seed, seq, vocab)

@@ -1,0 +1,354 @@
+"""ctypes binding of libqwhip.so (include/qwhip.h).
+
+Names follow the reference's operator surface (kernels.zig Matrix.apply /
+linearQuantized / decodeAttentionStepQ8, quant.zig quantizeRow, decoder.zig
+forwardToken / step): the methods below are one-line forwards to the C ABI.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+FORMAT_Q4, FORMAT_Q5, FORMAT_Q8 = 16, 17, 18
+GROUP_SIZE = 64
+DATA_BYTES = {FORMAT_Q4: 32, FORMAT_Q5: 40, FORMAT_Q8: 64}
+
+T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(9)
+T_ATTN_NORM, T_Q_NORM, T_K_NORM, T_FFN_NORM, T_FINAL_NORM = 16, 17, 18, 19, 20
+
+STATUS = {
+    0: "ok", -1: "invalid_argument", -2: "out_of_memory", -3: "unsupported",
+    -7: "shape_mismatch", -8: "invalid_state", -9: "limit_exceeded", -10: "not_found", -64: "device",
+}
+
+
+def library_path() -> str:
+    return os.environ.get("QWHIP_LIBRARY", os.path.join(HERE, "build", "libqwhip.so"))
+
+
+class QwhError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)} ({status}): {message}")
+        self.status = status
+
+
+class DecoderConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_uint32),
+        ("layers", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("ffn", ctypes.c_uint32),
+        ("vocab", ctypes.c_uint32),
+        ("max_positions", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("theta", ctypes.c_float),
+    ]
+
+
+_P = ctypes.c_void_p
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_U16 = ctypes.c_uint16
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+
+# Every entry point of include/qwhip.h with its ctypes signature.
+SIGNATURES = {
+    "qwh_abi_version": (_I32, []),
+    "qwh_status_string": (ctypes.c_char_p, [_I32]),
+    "qwh_create": (_I32, [_U32, _PP]),
+    "qwh_destroy": (_I32, [_P]),
+    "qwh_sync": (_I32, [_P]),
+    "qwh_last_error": (ctypes.c_char_p, [_P]),
+    "qwh_device_cus": (_I32, [_P, ctypes.POINTER(_U32)]),
+    "qwh_alloc": (_I32, [_P, _U64, _PP]),
+    "qwh_free": (_I32, [_P, _P]),
+    "qwh_upload": (_I32, [_P, _P, _P, _U64]),
+    "qwh_download": (_I32, [_P, _P, _P, _U64]),
+    "qwh_memset": (_I32, [_P, _P, _I32, _U64]),
+    "qwh_event_record": (_I32, [_P, _U32]),
+    "qwh_event_elapsed": (_I32, [_P, _U32, _U32, ctypes.POINTER(_F)]),
+    "qwh_matrix_upload": (_I32, [_P, _I32, _U32, _U32, _P, _U64, _P, _U64, ctypes.POINTER(_U64)]),
+    "qwh_matrix_wrap": (_I32, [_P, _I32, _U32, _U32, _P, _P, ctypes.POINTER(_U64)]),
+    "qwh_matrix_synthetic": (_I32, [_P, _I32, _U32, _U32, _U32, _U32, _F, ctypes.POINTER(_U64)]),
+    "qwh_matrix_planes": (_I32, [_P, _U64, _PP, _PP]),
+    "qwh_matrix_release": (_I32, [_P, _U64]),
+    "qwh_linear": (_I32, [_P, _U64, _P, _U32, _U32, _P]),
+    "qwh_linear_bf16": (_I32, [_P, _U64, _P, _U32, _U32, _P]),
+    "qwh_activation_bytes": (_I32, [_U32, _U32, ctypes.POINTER(_U64)]),
+    "qwh_activation_prepare": (_I32, [_P, _P, _U32, _U32, _P]),
+    "qwh_linear_prepared": (_I32, [_P, _U64, _P, _U32, _P]),
+    "qwh_quantize_rows": (_I32, [_P, _I32, _P, _U32, _U32, _P, _P]),
+    "qwh_synth_normal": (_I32, [_P, _U32, _U32, _U64, _F, _P]),
+    "qwh_decode_attention_q8": (_I32, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U64, _U64]),
+    "qwh_kv_append_q8": (_I32, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "qwh_decoder_create": (_I32, [_P, ctypes.POINTER(DecoderConfig), _U32, _PP]),
+    "qwh_decoder_destroy": (_I32, [_P]),
+    "qwh_decoder_set_matrix": (_I32, [_P, _U32, _U32, _U64]),
+    "qwh_decoder_set_vector": (_I32, [_P, _U32, _U32, _P, _U32]),
+    "qwh_decoder_init_synthetic": (_I32, [_P, _U32]),
+    "qwh_decoder_reset": (_I32, [_P]),
+    "qwh_decoder_prefill_random": (_I32, [_P, _U32, _U32, _U32]),
+    "qwh_decoder_cache_planes": (_I32, [_P, _U32, _U32, _PP, _PP, _PP, _PP]),
+    "qwh_decoder_position": (_I32, [_P, _U32, ctypes.POINTER(_U32)]),
+    "qwh_decoder_set_position": (_I32, [_P, _U32, _U32]),
+    "qwh_decoder_forward": (_I32, [_P, _P, _I32]),
+    "qwh_decoder_step": (_I32, [_P, _P, _P]),
+    "qwh_decoder_generate": (_I32, [_P, _P, _U32, _P]),
+    "qwh_decoder_logits": (_I32, [_P, _U32, _P, _U32]),
+}
+
+_lib = None
+
+
+def load():
+    """Loads libqwhip.so; raises if it is not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        path = library_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"libqwhip.so not found at {path}: build it with `make -C qwenscriber_amd` "
+                "(or __graft_entry__.build()). There is no CPU fallback.")
+        lib = ctypes.CDLL(path)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def _ptr(array: np.ndarray) -> int:
+    if not array.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C contiguous")
+    return array.ctypes.data
+
+
+class DeviceBuffer:
+    """A device allocation owned by a Context (qwh_alloc / qwh_free)."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        out = ctypes.c_void_p()
+        ctx._check(load().qwh_alloc(ctx.handle, self.nbytes, ctypes.byref(out)))
+        self.ptr = out.value
+
+    def free(self) -> None:
+        if self.ptr is not None and self.ctx.handle:
+            self.ctx._check(load().qwh_free(self.ctx.handle, self.ptr))
+        self.ptr = None
+
+    def upload(self, array: np.ndarray, offset: int = 0) -> None:
+        array = np.ascontiguousarray(array)
+        if offset + array.nbytes > self.nbytes:
+            raise ValueError("upload past the end of the buffer")
+        self.ctx._check(load().qwh_upload(self.ctx.handle, self.ptr + offset, _ptr(array), array.nbytes))
+
+    def download(self, dtype, count: Optional[int] = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download past the end of the buffer")
+        self.ctx._check(load().qwh_download(self.ctx.handle, _ptr(out), self.ptr + offset, out.nbytes))
+        return out
+
+
+class Context:
+    """One device and one stream (qwh_create)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load()
+        out = ctypes.c_void_p()
+        status = self.lib.qwh_create(device, ctypes.byref(out))
+        if status != 0:
+            raise QwhError(status, f"qwh_create({device}) failed")
+        self.handle = out.value
+        self._buffers = []
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.qwh_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _check(self, status: int) -> None:
+        if status != 0:
+            message = self.lib.qwh_last_error(self.handle).decode() if self.handle else ""
+            raise QwhError(status, message)
+
+    # -- memory and timing -------------------------------------------------
+    def buffer(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, array: np.ndarray) -> DeviceBuffer:
+        array = np.ascontiguousarray(array)
+        buf = DeviceBuffer(self, max(array.nbytes, 1))
+        buf.upload(array)
+        return buf
+
+    def sync(self) -> None:
+        self._check(self.lib.qwh_sync(self.handle))
+
+    def cus(self) -> int:
+        out = ctypes.c_uint32()
+        self._check(self.lib.qwh_device_cus(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def event_record(self, slot: int) -> None:
+        self._check(self.lib.qwh_event_record(self.handle, slot))
+
+    def event_elapsed_ms(self, start: int, end: int) -> float:
+        out = ctypes.c_float()
+        self._check(self.lib.qwh_event_elapsed(self.handle, start, end, ctypes.byref(out)))
+        return out.value
+
+    # -- matrices (kernels.zig Matrix) ------------------------------------
+    def matrix_upload(self, fmt: int, rows: int, cols: int, scales: np.ndarray, data: np.ndarray) -> int:
+        scales = np.ascontiguousarray(scales, np.uint8)
+        data = np.ascontiguousarray(data, np.uint8)
+        out = ctypes.c_uint64()
+        self._check(self.lib.qwh_matrix_upload(self.handle, fmt, rows, cols, _ptr(scales), scales.size,
+                                               _ptr(data), data.size, ctypes.byref(out)))
+        return out.value
+
+    def matrix_wrap(self, fmt: int, rows: int, cols: int, scales_dev: int, data_dev: int) -> int:
+        out = ctypes.c_uint64()
+        self._check(self.lib.qwh_matrix_wrap(self.handle, fmt, rows, cols, scales_dev, data_dev, ctypes.byref(out)))
+        return out.value
+
+    def matrix_synthetic(self, fmt: int, rows: int, cols: int, seed: int, stream: int, scale: float = 0.02) -> int:
+        out = ctypes.c_uint64()
+        self._check(self.lib.qwh_matrix_synthetic(self.handle, fmt, rows, cols, seed, stream, scale, ctypes.byref(out)))
+        return out.value
+
+    def matrix_planes(self, matrix: int):
+        s = ctypes.c_void_p()
+        d = ctypes.c_void_p()
+        self._check(self.lib.qwh_matrix_planes(self.handle, matrix, ctypes.byref(s), ctypes.byref(d)))
+        return s.value, d.value
+
+    def matrix_release(self, matrix: int) -> None:
+        self._check(self.lib.qwh_matrix_release(self.handle, matrix))
+
+    def linear(self, matrix: int, x_dev: int, cols: int, tokens: int, out_dev: int) -> None:
+        """kernels.zig Matrix.apply: out[tokens][rows] = W x."""
+        self._check(self.lib.qwh_linear(self.handle, matrix, x_dev, cols, tokens, out_dev))
+
+    def activation_bytes(self, cols: int, tokens: int) -> int:
+        out = ctypes.c_uint64()
+        self._check(self.lib.qwh_activation_bytes(cols, tokens, ctypes.byref(out)))
+        return out.value
+
+    def activation_prepare(self, x_dev: int, cols: int, tokens: int, prepared_dev: int) -> None:
+        self._check(self.lib.qwh_activation_prepare(self.handle, x_dev, cols, tokens, prepared_dev))
+
+    def linear_prepared(self, matrix: int, prepared_dev: int, tokens: int, out_dev: int) -> None:
+        self._check(self.lib.qwh_linear_prepared(self.handle, matrix, prepared_dev, tokens, out_dev))
+
+    def linear_bf16(self, matrix: int, x_dev: int, cols: int, tokens: int, out_dev: int) -> None:
+        self._check(self.lib.qwh_linear_bf16(self.handle, matrix, x_dev, cols, tokens, out_dev))
+
+    # -- quantization and synthetic inputs ---------------------------------
+    def quantize_rows(self, fmt: int, values_dev: int, rows: int, cols: int, scales_dev: int, data_dev: int) -> None:
+        self._check(self.lib.qwh_quantize_rows(self.handle, fmt, values_dev, rows, cols, scales_dev, data_dev))
+
+    def synth_normal(self, seed: int, stream: int, count: int, scale: float, out_dev: int) -> None:
+        self._check(self.lib.qwh_synth_normal(self.handle, seed, stream, count, scale, out_dev))
+
+    # -- attention ----------------------------------------------------------
+    def decode_attention_q8(self, out_dev, query_dev, k_scales, k_codes, v_scales, v_codes, cached, heads,
+                            kv_heads, head_dim, batch=1, scale_stride=0, code_stride=0) -> None:
+        self._check(self.lib.qwh_decode_attention_q8(self.handle, out_dev, query_dev, k_scales, k_codes, v_scales,
+                                                     v_codes, cached, heads, kv_heads, head_dim, batch,
+                                                     scale_stride, code_stride))
+
+    def kv_append_q8(self, key_dev, value_dev, kv_width, position, k_scales, k_codes, v_scales, v_codes) -> None:
+        self._check(self.lib.qwh_kv_append_q8(self.handle, key_dev, value_dev, kv_width, position, k_scales,
+                                              k_codes, v_scales, v_codes))
+
+
+class Decoder:
+    """decoder.zig Decoder over `batch` sequences (qwh_decoder_*)."""
+
+    def __init__(self, ctx: Context, batch: int = 1, **config):
+        self.ctx = ctx
+        self.config = DecoderConfig(**config)
+        self.batch = batch
+        out = ctypes.c_void_p()
+        ctx._check(ctx.lib.qwh_decoder_create(ctx.handle, ctypes.byref(self.config), batch, ctypes.byref(out)))
+        self.handle = out.value
+
+    def close(self) -> None:
+        if self.handle:
+            self.ctx.lib.qwh_decoder_destroy(self.handle)
+            self.handle = None
+
+    def _check(self, status):
+        self.ctx._check(status)
+
+    def set_matrix(self, kind: int, layer: int, matrix: int) -> None:
+        self._check(self.ctx.lib.qwh_decoder_set_matrix(self.handle, kind, layer, matrix))
+
+    def set_vector(self, kind: int, layer: int, values: np.ndarray) -> None:
+        values = np.ascontiguousarray(values, np.float32)
+        self._check(self.ctx.lib.qwh_decoder_set_vector(self.handle, kind, layer, _ptr(values), values.size))
+
+    def init_synthetic(self, seed: int) -> None:
+        self._check(self.ctx.lib.qwh_decoder_init_synthetic(self.handle, seed))
+
+    def reset(self) -> None:
+        self._check(self.ctx.lib.qwh_decoder_reset(self.handle))
+
+    def prefill_random(self, seq: int, count: int, seed: int) -> None:
+        self._check(self.ctx.lib.qwh_decoder_prefill_random(self.handle, seq, count, seed))
+
+    def cache_planes(self, seq: int, layer: int):
+        ptrs = [ctypes.c_void_p() for _ in range(4)]
+        self._check(self.ctx.lib.qwh_decoder_cache_planes(self.handle, seq, layer, *[ctypes.byref(p) for p in ptrs]))
+        return tuple(p.value for p in ptrs)
+
+    def position(self, seq: int) -> int:
+        out = ctypes.c_uint32()
+        self._check(self.ctx.lib.qwh_decoder_position(self.handle, seq, ctypes.byref(out)))
+        return out.value
+
+    def set_position(self, seq: int, position: int) -> None:
+        self._check(self.ctx.lib.qwh_decoder_set_position(self.handle, seq, position))
+
+    def forward(self, tokens, want_logits: bool = True) -> None:
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        self._check(self.ctx.lib.qwh_decoder_forward(self.handle, _ptr(tokens), int(want_logits)))
+
+    def step(self, tokens) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        out = np.zeros(self.batch, np.uint32)
+        self._check(self.ctx.lib.qwh_decoder_step(self.handle, _ptr(tokens), _ptr(out)))
+        return out
+
+    def generate(self, tokens, steps: int) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        out = np.zeros(steps * self.batch, np.uint32)
+        self._check(self.ctx.lib.qwh_decoder_generate(self.handle, _ptr(tokens), steps, _ptr(out)))
+        return out.reshape(steps, self.batch)
+
+    def logits(self, seq: int) -> np.ndarray:
+        out = np.zeros(self.config.vocab, np.float32)
+        self._check(self.ctx.lib.qwh_decoder_logits(self.handle, seq, _ptr(out), out.size))
+        return out

@@ -1,0 +1,497 @@
+// C ABI entry points: context, device memory, matrices, the linear products,
+// device quantization and attention. The decoder entry points are in
+// decoder.hip.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "common.h"
+
+namespace qwh {
+
+int32_t fail(qwh_ctx *ctx, int32_t status, const char *fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list args;
+        va_start(args, fmt);
+        vsnprintf(buf, sizeof buf, fmt, args);
+        va_end(args);
+        ctx->last_error = buf;
+    }
+    return status;
+}
+
+int32_t check_hip(qwh_ctx *ctx, hipError_t err, const char *what) {
+    if (err == hipSuccess) return QWH_OK;
+    (void)hipGetLastError();
+    return fail(ctx, QWH_E_DEVICE, "%s: %s (%d)", what, hipGetErrorString(err), (int)err);
+}
+
+int32_t ensure_workspace(qwh_ctx *ctx, Workspace &ws, size_t bytes) {
+    if (ws.bytes >= bytes) return QWH_OK;
+    if (ws.ptr) {
+        // Work already queued may still read the old buffer.
+        QWH_TRY(check_hip(ctx, hipStreamSynchronize(ctx->stream), "workspace sync"));
+        (void)hipFree(ws.ptr);
+        ws.ptr = nullptr;
+        ws.bytes = 0;
+    }
+    const size_t rounded = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    const hipError_t err = hipMalloc(&ws.ptr, rounded);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        ws.ptr = nullptr;
+        return fail(ctx, QWH_E_OUT_OF_MEMORY, "workspace of %zu bytes: %s", rounded, hipGetErrorString(err));
+    }
+    ws.bytes = rounded;
+    return QWH_OK;
+}
+
+const Matrix *find_matrix(qwh_ctx *ctx, uint64_t handle) {
+    auto it = ctx->matrices.find(handle);
+    return it == ctx->matrices.end() ? nullptr : &it->second;
+}
+
+namespace {
+
+bool is_quant_format(int32_t format) {
+    return format == QWH_FORMAT_Q4 || format == QWH_FORMAT_Q5 || format == QWH_FORMAT_Q8;
+}
+
+int32_t check_device_ptr(qwh_ctx *ctx, const void *p, const char *what) {
+    if (!p) return fail(ctx, QWH_E_INVALID_ARGUMENT, "%s is null", what);
+    return QWH_OK;
+}
+
+// Plane sizes of a rows x cols matrix (quant.zig:77-99).
+int32_t plane_sizes(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, size_t &scales, size_t &data) {
+    if (!is_quant_format(format)) return fail(ctx, QWH_E_UNSUPPORTED, "format %d is not quantized", format);
+    if (cols == 0 || cols % kGroup != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "cols %u is not a whole number of groups of 64", cols);
+    const size_t groups = (size_t)rows * (cols / kGroup);
+    scales = groups * 2;
+    data = groups * (size_t)data_bytes_per_group(format);
+    return QWH_OK;
+}
+
+uint64_t add_matrix(qwh_ctx *ctx, const Matrix &m) {
+    const uint64_t handle = ctx->next_handle++;
+    ctx->matrices[handle] = m;
+    return handle;
+}
+
+}  // namespace
+}  // namespace qwh
+
+using namespace qwh;
+
+extern "C" {
+
+int32_t qwh_abi_version(void) { return QWH_ABI_VERSION; }
+
+const char *qwh_status_string(int32_t status) {
+    switch (status) {
+    case QWH_OK: return "ok";
+    case QWH_E_INVALID_ARGUMENT: return "invalid_argument";
+    case QWH_E_OUT_OF_MEMORY: return "out_of_memory";
+    case QWH_E_UNSUPPORTED: return "unsupported";
+    case QWH_E_SHAPE_MISMATCH: return "shape_mismatch";
+    case QWH_E_INVALID_STATE: return "invalid_state";
+    case QWH_E_LIMIT_EXCEEDED: return "limit_exceeded";
+    case QWH_E_NOT_FOUND: return "not_found";
+    case QWH_E_DEVICE: return "device";
+    default: return "unknown";
+    }
+}
+
+int32_t qwh_create(uint32_t device_index, qwh_ctx **out) {
+    if (!out) return QWH_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    hipError_t err = hipGetDeviceCount(&count);
+    if (err != hipSuccess || count == 0) {
+        (void)hipGetLastError();
+        return QWH_E_DEVICE;
+    }
+    if ((int)device_index >= count) return QWH_E_INVALID_ARGUMENT;
+    if (hipSetDevice((int)device_index) != hipSuccess) return QWH_E_DEVICE;
+    qwh_ctx *ctx = new qwh_ctx();
+    ctx->device = (int)device_index;
+    hipDeviceProp_t prop{};
+    if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess) ctx->cus = prop.multiProcessorCount;
+    if (ctx->cus <= 0) ctx->cus = 256;
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return QWH_E_DEVICE;
+    }
+    for (auto &e : ctx->events) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            qwh_destroy(ctx);
+            return QWH_E_DEVICE;
+        }
+    }
+    *out = ctx;
+    return QWH_OK;
+}
+
+int32_t qwh_destroy(qwh_ctx *ctx) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->matrices) {
+        if (kv.second.owned) {
+            (void)hipFree(kv.second.scales);
+            (void)hipFree(kv.second.data);
+        }
+    }
+    for (auto &e : ctx->events)
+        if (e) (void)hipEventDestroy(e);
+    if (ctx->digits.ptr) (void)hipFree(ctx->digits.ptr);
+    if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return QWH_OK;
+}
+
+int32_t qwh_sync(qwh_ctx *ctx) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    return check_hip(ctx, hipStreamSynchronize(ctx->stream), "sync");
+}
+
+const char *qwh_last_error(qwh_ctx *ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+int32_t qwh_device_cus(qwh_ctx *ctx, uint32_t *out) {
+    if (!ctx || !out) return QWH_E_INVALID_ARGUMENT;
+    *out = (uint32_t)ctx->cus;
+    return QWH_OK;
+}
+
+int32_t qwh_alloc(qwh_ctx *ctx, uint64_t bytes, void **out_dev) {
+    if (!ctx || !out_dev) return QWH_E_INVALID_ARGUMENT;
+    *out_dev = nullptr;
+    const hipError_t err = hipMalloc(out_dev, bytes ? bytes : 1);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        *out_dev = nullptr;
+        return fail(ctx, QWH_E_OUT_OF_MEMORY, "hipMalloc(%llu): %s", (unsigned long long)bytes, hipGetErrorString(err));
+    }
+    return QWH_OK;
+}
+
+int32_t qwh_free(qwh_ctx *ctx, void *dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (!dev) return QWH_OK;
+    QWH_TRY(check_hip(ctx, hipStreamSynchronize(ctx->stream), "free sync"));
+    return check_hip(ctx, hipFree(dev), "free");
+}
+
+int32_t qwh_upload(qwh_ctx *ctx, void *dst_dev, const void *src, uint64_t bytes) {
+    if (!ctx || (!bytes ? false : (!dst_dev || !src))) return QWH_E_INVALID_ARGUMENT;
+    if (!bytes) return QWH_OK;
+    // The source is pageable host memory the caller may reuse on return:
+    // copy synchronously with respect to the host.
+    QWH_TRY(check_hip(ctx, hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, ctx->stream), "upload"));
+    return check_hip(ctx, hipStreamSynchronize(ctx->stream), "upload sync");
+}
+
+int32_t qwh_download(qwh_ctx *ctx, void *dst, const void *src_dev, uint64_t bytes) {
+    if (!ctx || (!bytes ? false : (!dst || !src_dev))) return QWH_E_INVALID_ARGUMENT;
+    if (!bytes) return QWH_OK;
+    QWH_TRY(check_hip(ctx, hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream), "download"));
+    return check_hip(ctx, hipStreamSynchronize(ctx->stream), "download sync");
+}
+
+int32_t qwh_memset(qwh_ctx *ctx, void *dst_dev, int32_t value, uint64_t bytes) {
+    if (!ctx || (bytes && !dst_dev)) return QWH_E_INVALID_ARGUMENT;
+    return check_hip(ctx, hipMemsetAsync(dst_dev, value, bytes, ctx->stream), "memset");
+}
+
+int32_t qwh_event_record(qwh_ctx *ctx, uint32_t slot) {
+    if (!ctx || slot >= (uint32_t)kMaxEvents) return QWH_E_INVALID_ARGUMENT;
+    return check_hip(ctx, hipEventRecord(ctx->events[slot], ctx->stream), "event record");
+}
+
+int32_t qwh_event_elapsed(qwh_ctx *ctx, uint32_t start, uint32_t end, float *out_ms) {
+    if (!ctx || !out_ms || start >= (uint32_t)kMaxEvents || end >= (uint32_t)kMaxEvents) return QWH_E_INVALID_ARGUMENT;
+    QWH_TRY(check_hip(ctx, hipEventSynchronize(ctx->events[end]), "event sync"));
+    return check_hip(ctx, hipEventElapsedTime(out_ms, ctx->events[start], ctx->events[end]), "event elapsed");
+}
+
+int32_t qwh_matrix_upload(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, const uint8_t *scales,
+                          uint64_t scales_len, const uint8_t *data, uint64_t data_len, uint64_t *out_matrix) {
+    if (!ctx || !out_matrix || !scales || !data) return QWH_E_INVALID_ARGUMENT;
+    size_t s_bytes, d_bytes;
+    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
+    if (scales_len != s_bytes)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "scale plane is %llu bytes, a %ux%u matrix needs %zu",
+                    (unsigned long long)scales_len, rows, cols, s_bytes);
+    if (data_len != d_bytes)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "data plane is %llu bytes, a %ux%u matrix needs %zu",
+                    (unsigned long long)data_len, rows, cols, d_bytes);
+    Matrix m;
+    m.format = format;
+    m.rows = rows;
+    m.cols = cols;
+    m.owned = true;
+    if (hipMalloc(&m.scales, s_bytes ? s_bytes : 1) != hipSuccess || hipMalloc(&m.data, d_bytes ? d_bytes : 1) != hipSuccess) {
+        (void)hipGetLastError();
+        if (m.scales) (void)hipFree(m.scales);
+        return fail(ctx, QWH_E_OUT_OF_MEMORY, "matrix planes of %zu + %zu bytes", s_bytes, d_bytes);
+    }
+    int32_t st = check_hip(ctx, hipMemcpyAsync(m.scales, scales, s_bytes, hipMemcpyHostToDevice, ctx->stream), "upload scales");
+    if (st == QWH_OK)
+        st = check_hip(ctx, hipMemcpyAsync(m.data, data, d_bytes, hipMemcpyHostToDevice, ctx->stream), "upload data");
+    if (st == QWH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "upload sync");
+    if (st != QWH_OK) {
+        (void)hipFree(m.scales);
+        (void)hipFree(m.data);
+        return st;
+    }
+    *out_matrix = add_matrix(ctx, m);
+    return QWH_OK;
+}
+
+int32_t qwh_matrix_wrap(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, const void *scales_dev,
+                        const void *data_dev, uint64_t *out_matrix) {
+    if (!ctx || !out_matrix) return QWH_E_INVALID_ARGUMENT;
+    size_t s_bytes, d_bytes;
+    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
+    QWH_TRY(check_device_ptr(ctx, scales_dev, "scales"));
+    QWH_TRY(check_device_ptr(ctx, data_dev, "data"));
+    if (((uintptr_t)data_dev & 15u) != 0)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "data plane must be 16-byte aligned (quant.zig:61-63)");
+    if (((uintptr_t)scales_dev & 1u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "scale plane must be 2-byte aligned");
+    Matrix m;
+    m.format = format;
+    m.rows = rows;
+    m.cols = cols;
+    m.scales = static_cast<uint8_t *>(const_cast<void *>(scales_dev));
+    m.data = static_cast<uint8_t *>(const_cast<void *>(data_dev));
+    m.owned = false;
+    *out_matrix = add_matrix(ctx, m);
+    return QWH_OK;
+}
+
+int32_t qwh_matrix_synthetic(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, uint32_t seed, uint32_t stream,
+                             float value_scale, uint64_t *out_matrix) {
+    if (!ctx || !out_matrix) return QWH_E_INVALID_ARGUMENT;
+    size_t s_bytes, d_bytes;
+    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
+    Matrix m;
+    m.format = format;
+    m.rows = rows;
+    m.cols = cols;
+    m.owned = true;
+    if (hipMalloc(&m.scales, s_bytes ? s_bytes : 1) != hipSuccess || hipMalloc(&m.data, d_bytes ? d_bytes : 1) != hipSuccess) {
+        (void)hipGetLastError();
+        if (m.scales) (void)hipFree(m.scales);
+        return fail(ctx, QWH_E_OUT_OF_MEMORY, "matrix planes of %zu + %zu bytes", s_bytes, d_bytes);
+    }
+    const size_t slab_values = (size_t)64 << 20;
+    float *temp = nullptr;
+    int32_t st = check_hip(ctx, hipMalloc(&temp, slab_values * 4), "synthetic temp");
+    const uint32_t slab_rows = (uint32_t)(slab_values / cols) ? (uint32_t)(slab_values / cols) : 1;
+    const size_t gpr = cols / kGroup;
+    const int db = data_bytes_per_group(format);
+    for (uint32_t r = 0; r < rows && st == QWH_OK; r += slab_rows) {
+        const uint32_t n = rows - r < slab_rows ? rows - r : slab_rows;
+        st = check_hip(ctx, launch_synth_normal(ctx->stream, seed, stream, (uint64_t)r * cols, (uint64_t)n * cols,
+                                                value_scale, temp), "synthetic values");
+        if (st == QWH_OK)
+            st = check_hip(ctx, launch_quantize_rows(ctx->stream, format, temp, (uint64_t)n * gpr,
+                                                     m.scales + (size_t)r * gpr * 2, m.data + (size_t)r * gpr * db),
+                           "quantize");
+    }
+    if (st == QWH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "synthetic sync");
+    if (temp) (void)hipFree(temp);
+    if (st != QWH_OK) {
+        (void)hipFree(m.scales);
+        (void)hipFree(m.data);
+        return st;
+    }
+    *out_matrix = add_matrix(ctx, m);
+    return QWH_OK;
+}
+
+int32_t qwh_matrix_planes(qwh_ctx *ctx, uint64_t matrix, void **scales_dev, void **data_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    const Matrix *m = find_matrix(ctx, matrix);
+    if (!m) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
+    if (scales_dev) *scales_dev = m->scales;
+    if (data_dev) *data_dev = m->data;
+    return QWH_OK;
+}
+
+int32_t qwh_matrix_release(qwh_ctx *ctx, uint64_t matrix) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    auto it = ctx->matrices.find(matrix);
+    if (it == ctx->matrices.end()) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
+    if (it->second.owned) {
+        QWH_TRY(check_hip(ctx, hipStreamSynchronize(ctx->stream), "release sync"));
+        (void)hipFree(it->second.scales);
+        (void)hipFree(it->second.data);
+    }
+    ctx->matrices.erase(it);
+    return QWH_OK;
+}
+
+int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t cols, uint32_t tokens, float *out_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    const Matrix *m = find_matrix(ctx, matrix);
+    if (!m) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
+    // kernels.zig:129-139 shape checks.
+    if (cols != m->cols) return fail(ctx, QWH_E_SHAPE_MISMATCH, "x has %u columns, the matrix %u", cols, m->cols);
+    if (tokens == 0) return QWH_OK;
+    if (tokens > 65535) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "tokens %u > 65535", tokens);
+    QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    if (((uintptr_t)x_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (m->rows == 0) return QWH_OK;
+    if (m->format == QWH_FORMAT_Q4) {
+        QWH_TRY(ensure_workspace(ctx, ctx->digits, q4_digit_bytes(tokens, cols)));
+        QWH_TRY(check_hip(ctx, launch_prep_q4(ctx->stream, x_dev, tokens, cols, ctx->digits.ptr), "prep q4"));
+        return check_hip(ctx, launch_gemv_q4(ctx->stream, ctx->cus, ctx->digits.ptr, *m, tokens, out_dev, nullptr), "gemv q4");
+    }
+    if (m->format == QWH_FORMAT_Q8)
+        return check_hip(ctx, launch_gemv_q8(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, nullptr), "gemv q8");
+    return fail(ctx, QWH_E_UNSUPPORTED, "linear over format %d is not built", m->format);
+}
+
+int32_t qwh_activation_bytes(uint32_t cols, uint32_t tokens, uint64_t *out_bytes) {
+    if (!out_bytes) return QWH_E_INVALID_ARGUMENT;
+    if (cols == 0 || cols % kGroup != 0) return QWH_E_SHAPE_MISMATCH;
+    *out_bytes = q4_digit_bytes(tokens, cols);
+    return QWH_OK;
+}
+
+int32_t qwh_activation_prepare(qwh_ctx *ctx, const float *x_dev, uint32_t cols, uint32_t tokens, void *prepared_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (cols == 0 || cols % kGroup != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "cols %u is not a whole number of groups of 64", cols);
+    if (tokens == 0) return QWH_OK;
+    if (tokens > 65535) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "tokens %u > 65535", tokens);
+    QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
+    QWH_TRY(check_device_ptr(ctx, prepared_dev, "prepared"));
+    if ((((uintptr_t)x_dev) | ((uintptr_t)prepared_dev)) & 15u)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "x and prepared must be 16-byte aligned");
+    return check_hip(ctx, launch_prep_q4(ctx->stream, x_dev, tokens, cols, prepared_dev), "prepare activations");
+}
+
+int32_t qwh_linear_prepared(qwh_ctx *ctx, uint64_t matrix, const void *prepared_dev, uint32_t tokens, float *out_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    const Matrix *m = find_matrix(ctx, matrix);
+    if (!m) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
+    if (m->format != QWH_FORMAT_Q4) return fail(ctx, QWH_E_UNSUPPORTED, "prepared activations feed q4 matrices");
+    if (tokens == 0 || m->rows == 0) return QWH_OK;
+    if (tokens > 65535) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "tokens %u > 65535", tokens);
+    QWH_TRY(check_device_ptr(ctx, prepared_dev, "prepared"));
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    if (((uintptr_t)prepared_dev) & 15u) return fail(ctx, QWH_E_INVALID_ARGUMENT, "prepared must be 16-byte aligned");
+    return check_hip(ctx, launch_gemv_q4(ctx->stream, ctx->cus, prepared_dev, *m, tokens, out_dev, nullptr), "gemv q4");
+}
+
+int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, uint32_t cols, uint32_t tokens,
+                        float *out_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    const Matrix *m = find_matrix(ctx, matrix);
+    if (!m) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
+    if (cols != m->cols) return fail(ctx, QWH_E_SHAPE_MISMATCH, "x has %u columns, the matrix %u", cols, m->cols);
+    if (m->format != QWH_FORMAT_Q4) return fail(ctx, QWH_E_UNSUPPORTED, "bf16 GEMM is built for q4 only");
+    if (tokens == 0 || m->rows == 0) return QWH_OK;
+    if (tokens > 65535u * 128u) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "tokens %u", tokens);
+    QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    if (((uintptr_t)x_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    return check_hip(ctx, launch_gemm_q4_bf16(ctx->stream, x_dev, *m, tokens, out_dev), "gemm q4 bf16");
+}
+
+int32_t qwh_quantize_rows(qwh_ctx *ctx, int32_t format, const float *values_dev, uint32_t rows, uint32_t cols,
+                          uint8_t *scales_dev, uint8_t *data_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    size_t s_bytes, d_bytes;
+    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
+    if (rows == 0) return QWH_OK;
+    QWH_TRY(check_device_ptr(ctx, values_dev, "values"));
+    QWH_TRY(check_device_ptr(ctx, scales_dev, "scales"));
+    QWH_TRY(check_device_ptr(ctx, data_dev, "data"));
+    return check_hip(ctx, launch_quantize_rows(ctx->stream, format, values_dev, (uint64_t)rows * (cols / kGroup), scales_dev,
+                                               data_dev), "quantize rows");
+}
+
+int32_t qwh_synth_normal(qwh_ctx *ctx, uint32_t seed, uint32_t stream, uint64_t count, float value_scale, float *out_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (count == 0) return QWH_OK;
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    return check_hip(ctx, launch_synth_normal(ctx->stream, seed, stream, 0, count, value_scale, out_dev), "synth normal");
+}
+
+int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query_dev, const uint8_t *k_scales_dev,
+                                const uint8_t *k_codes_dev, const uint8_t *v_scales_dev, const uint8_t *v_codes_dev,
+                                uint32_t cached, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t batch,
+                                uint64_t scale_stride_bytes, uint64_t code_stride_bytes) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    // kernels.zig:712-723 shape checks.
+    if (head_dim == 0 || head_dim % kGroup != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "head_dim %u is not a multiple of 64", head_dim);
+    if (kv_heads == 0 || heads % kv_heads != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "heads %u not a multiple of kv_heads %u", heads, kv_heads);
+    if (cached == 0) return fail(ctx, QWH_E_SHAPE_MISMATCH, "no cached positions (softmax of an empty row)");
+    if (batch == 0) return QWH_OK;
+    const size_t kv_width = (size_t)kv_heads * head_dim;
+    if (batch > 1 && (scale_stride_bytes < (size_t)cached * (kv_width / kGroup) * 2 || code_stride_bytes < (size_t)cached * kv_width))
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "sequence strides smaller than %u cached rows", cached);
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    QWH_TRY(check_device_ptr(ctx, query_dev, "query"));
+    QWH_TRY(check_device_ptr(ctx, k_scales_dev, "k_scales"));
+    QWH_TRY(check_device_ptr(ctx, k_codes_dev, "k_codes"));
+    QWH_TRY(check_device_ptr(ctx, v_scales_dev, "v_scales"));
+    QWH_TRY(check_device_ptr(ctx, v_codes_dev, "v_codes"));
+    if (((uintptr_t)k_codes_dev | (uintptr_t)v_codes_dev | (uintptr_t)query_dev) & 15u)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "query and code planes must be 16-byte aligned");
+    if (((uintptr_t)k_scales_dev | (uintptr_t)v_scales_dev) & 1u)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "scale planes must be 2-byte aligned");
+    if (batch > 1 && ((scale_stride_bytes & 1u) || (code_stride_bytes & 15u)))
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "sequence strides must keep the plane alignment");
+    const uint32_t ratio = heads / kv_heads;
+    const bool built = (head_dim == 64 && (ratio == 1 || ratio == 2 || ratio == 4)) ||
+                       (head_dim == 128 && (ratio == 1 || ratio == 2 || ratio == 4 || ratio == 8)) ||
+                       (head_dim == 256 && (ratio == 1 || ratio == 2));
+    if (!built) return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim, ratio);
+    AttentionArgs a{};
+    a.out = out_dev;
+    a.query = query_dev;
+    a.k_scales = k_scales_dev;
+    a.k_codes = k_codes_dev;
+    a.v_scales = v_scales_dev;
+    a.v_codes = v_codes_dev;
+    a.cached = cached;
+    a.cached_dev = nullptr;
+    a.capacity = cached;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.batch = batch;
+    a.scale_stride = scale_stride_bytes;
+    a.code_stride = code_stride_bytes;
+    QWH_TRY(ensure_workspace(ctx, ctx->scratch, attention_scratch_bytes(ctx->cus, a)));
+    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr), "decode attention q8");
+}
+
+int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_dev, uint32_t kv_width, uint32_t position,
+                         uint8_t *k_scales_dev, uint8_t *k_codes_dev, uint8_t *v_scales_dev, uint8_t *v_codes_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (kv_width == 0 || kv_width % kGroup != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "kv_width %u is not a multiple of 64", kv_width);
+    QWH_TRY(check_device_ptr(ctx, key_dev, "key"));
+    QWH_TRY(check_device_ptr(ctx, value_dev, "value"));
+    QWH_TRY(check_device_ptr(ctx, k_scales_dev, "k_scales"));
+    QWH_TRY(check_device_ptr(ctx, k_codes_dev, "k_codes"));
+    QWH_TRY(check_device_ptr(ctx, v_scales_dev, "v_scales"));
+    QWH_TRY(check_device_ptr(ctx, v_codes_dev, "v_codes"));
+    if (((uintptr_t)k_scales_dev | (uintptr_t)v_scales_dev) & 1u)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "scale planes must be 2-byte aligned");
+    return check_hip(ctx, launch_kv_append_q8(ctx->stream, key_dev, value_dev, kv_width, position, k_scales_dev, k_codes_dev,
+                                              v_scales_dev, v_codes_dev), "kv append q8");
+}
+
+}  // extern "C"

@@ -1,0 +1,124 @@
+// Internal declarations shared by the HIP sources of libqwhip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/qwhip.h"
+
+namespace qwh {
+
+constexpr int kGroup = 64;          // quant.zig:49
+constexpr int kMaxEvents = 64;
+
+inline int data_bytes_per_group(int format) {
+    switch (format) {
+    case QWH_FORMAT_Q4: return 32;  // quant.zig:53
+    case QWH_FORMAT_Q5: return 40;  // quant.zig:56
+    case QWH_FORMAT_Q8: return 64;  // quant.zig:59
+    default: return 0;
+    }
+}
+
+inline int format_bias(int format) {  // quant.zig:111-118
+    switch (format) {
+    case QWH_FORMAT_Q4: return 8;
+    case QWH_FORMAT_Q5: return 16;
+    case QWH_FORMAT_Q8: return 128;
+    default: return 0;
+    }
+}
+
+struct Matrix {
+    int32_t format = 0;
+    uint32_t rows = 0;
+    uint32_t cols = 0;
+    uint8_t *scales = nullptr;  // rows * cols/64 f16, little endian, row major
+    uint8_t *data = nullptr;    // rows * cols/64 * data_bytes_per_group
+    bool owned = false;
+};
+
+// A growable device buffer owned by the context (digit planes, attention
+// partials). Growth happens between kernels on the context stream.
+struct Workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace qwh
+
+struct qwh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int cus = 0;
+    std::string last_error;
+    hipEvent_t events[qwh::kMaxEvents] = {};
+    std::unordered_map<uint64_t, qwh::Matrix> matrices;
+    uint64_t next_handle = 1;
+    qwh::Workspace digits;  // x digit planes for the q4 GEMV
+    qwh::Workspace scratch; // attention partials and other per-call scratch
+};
+
+namespace qwh {
+
+// Records a failure on the context and returns `status`.
+int32_t fail(qwh_ctx *ctx, int32_t status, const char *fmt, ...);
+// Maps a HIP error to QWH_E_DEVICE with a message, or returns QWH_OK.
+int32_t check_hip(qwh_ctx *ctx, hipError_t err, const char *what);
+int32_t ensure_workspace(qwh_ctx *ctx, Workspace &ws, size_t bytes);
+const Matrix *find_matrix(qwh_ctx *ctx, uint64_t handle);
+
+// ---- kernels launched by the entry points (defined in the .hip files) ----
+
+// Synthetic generator and device quantizer (quantize.hip).
+// out[i] = value (first + i) of the stream, times scale, for i < count.
+hipError_t launch_synth_normal(hipStream_t s, uint32_t seed, uint32_t stream, uint64_t first,
+                               uint64_t count, float scale, float *out);
+hipError_t launch_quantize_rows(hipStream_t s, int format, const float *values, uint64_t groups,
+                                uint8_t *scales, uint8_t *data);
+
+// q4 activations as signed hex digit planes (gemv.hip).
+size_t q4_digit_bytes(uint32_t tokens, uint32_t cols);
+hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32_t cols,
+                          void *digits);
+// y[t][n] (+)= W x over the prepared digit planes; residual may alias out.
+hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w,
+                          uint32_t tokens, float *out, const float *residual);
+hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w,
+                          uint32_t tokens, float *out, const float *residual);
+
+// q4 GEMM with bf16 activations (gemm.hip).
+hipError_t launch_gemm_q4_bf16(hipStream_t s, const uint16_t *x, const Matrix &w,
+                               uint32_t tokens, float *out);
+
+// q8 decode attention (attention.hip). `cached` is per sequence when
+// cached_dev is non-null (device array of batch values), else uniform.
+struct AttentionArgs {
+    float *out;
+    const float *query;
+    const uint8_t *k_scales, *k_codes, *v_scales, *v_codes;
+    uint32_t cached;
+    const uint32_t *cached_dev;   // optional: positions; cached = value + cached_bias
+    uint32_t cached_bias;
+    uint32_t capacity;            // upper bound of cached (sizes the grid)
+    uint32_t heads, kv_heads, head_dim, batch;
+    uint64_t scale_stride, code_stride;  // per sequence, bytes
+};
+size_t attention_scratch_bytes(int cus, const AttentionArgs &a);
+hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArgs &a,
+                                      void *scratch);
+hipError_t launch_kv_append_q8(hipStream_t s, const float *key, const float *value,
+                               uint32_t kv_width, uint32_t position, uint8_t *k_scales,
+                               uint8_t *k_codes, uint8_t *v_scales, uint8_t *v_codes);
+
+}  // namespace qwh
+
+#define QWH_TRY(expr)                    \
+    do {                                 \
+        int32_t qwh_status_ = (expr);    \
+        if (qwh_status_ != QWH_OK) return qwh_status_; \
+    } while (0)

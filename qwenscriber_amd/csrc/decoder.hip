@@ -1,0 +1,848 @@
+// The decoder step of decoder.zig:133-339 (forwardToken / step /
+// argmaxLogits) for `batch` independent sequences, with its glue kernels.
+//
+// Everything a step depends on lives on the device: the tokens, each
+// sequence's position, the caches and all scratch. A step therefore captures
+// once into a HIP graph and replays without host work; a greedy loop replays
+// it back to back, the argmax of one step feeding the embedding of the next.
+//
+// Per layer (decoder.zig:164-272):
+//   rmsnorm_digits  rmsNormInto(attention_norm) -> activation digit planes
+//   gemv q4         q | k | v rows fused into one matrix
+//   qk_rope_append  per-head rmsNorm of q and k, ropeInPlace at the position,
+//                   appendCacheRow (q8, bit exact) of k and v
+//   attention       decodeAttentionStepQ8 over position + 1 rows
+//   prep + gemv q4  out projection, residual added in the GEMV epilogue
+//   rmsnorm_digits  rmsNormInto(ffn_norm)
+//   gemv q4         gate | up rows fused
+//   silu_digits     siluMul
+//   gemv q4         down projection, residual added in the epilogue
+// then rmsNormInto(final) -> lm_head GEMV -> argmax (first maximum wins).
+#include <cfloat>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+#include "device.h"
+
+namespace qwh {
+namespace {
+
+// Synthetic model stream ids: identical to the CPU oracle's (the synthetic
+// model specification shared by both sides).
+constexpr uint32_t kStreamEmbed = 1;
+constexpr uint32_t kStreamLmHead = 2;
+constexpr uint32_t kStreamLayerBase = 16;    // + 16 * layer + {0 q,1 k,2 v,3 o,4 gate,5 up,6 down}
+constexpr uint32_t kStreamCacheBase = 0x10000; // + 0x100 * seq + 2 * layer + {0 keys, 1 values}
+
+// Writes this thread's 8 activations as digit-plane column q of chunk
+// `chunk`. The 4 threads of a chunk are consecutive lanes and all call this.
+__device__ __forceinline__ void emit_digits(const float v[8], bool valid, size_t chunk, uint32_t q,
+                                            uint32_t *words, float *mult) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const int e = dev::chunk_exponent(amax);
+    uint32_t planes[6];
+    dev::encode_digits8(v, e, planes);
+    if (valid) {
+        uint32_t *dst = words + chunk * dev::kChunkWords + q;
+#pragma unroll
+        for (int j = 0; j < 6; ++j) dst[j * 4] = planes[j];
+        if (q == 0) mult[chunk] = __builtin_ldexpf(1.0f, e - 22);
+    }
+}
+
+// Deterministic block sum (256 threads): wave sums, then the four wave totals
+// in order.
+__device__ __forceinline__ float block_sum256(float v, float *lds) {
+    v = dev::wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    const float total = ((lds[0] + lds[1]) + lds[2]) + lds[3];
+    __syncthreads();
+    return total;
+}
+
+// decoder.zig:346-376 embeddingRow, q4: f32(u - 8) then times the scale.
+__global__ __launch_bounds__(256) void embed_q4_kernel(const uint32_t *tokens, const uint16_t *scales,
+                                                       const uint8_t *data, uint32_t cols, float *hidden) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t token = tokens[b];
+    const uint32_t gpr = cols / 64;
+    const uint8_t *row = data + (size_t)token * (cols / 2);
+    float *out = hidden + (size_t)b * cols;
+    for (uint32_t i = threadIdx.x; i < cols / 2; i += blockDim.x) {
+        const uint32_t byte = row[i];
+        const float s = dev::f16_bits_to_f32(scales[(size_t)token * gpr + (2 * i) / 64]);
+        out[2 * i] = __fmul_rn((float)((int)(byte & 0xfu) - 8), s);
+        out[2 * i + 1] = __fmul_rn((float)((int)(byte >> 4) - 8), s);
+    }
+}
+
+// kernels.zig:274-300 rmsNormInto + math.zig:120-130, emitting the
+// normalized row as digit planes for the next GEMV. One block per sequence.
+__global__ __launch_bounds__(256) void rmsnorm_digits_kernel(const float *x, const float *weight,
+                                                             uint32_t cols, float eps, uint32_t *words,
+                                                             float *mult) {
+    __shared__ float lds[4];
+    const uint32_t b = blockIdx.x;
+    const float *row = x + (size_t)b * cols;
+    const uint32_t groups8 = cols / 8;
+    const uint32_t iters = (groups8 + 255) / 256;
+    float ss = 0.0f;
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t g8 = threadIdx.x + it * 256;
+        if (g8 < groups8) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float v = row[g8 * 8 + k];
+                ss = __fadd_rn(ss, __fmul_rn(v, v));
+            }
+        }
+    }
+    const float sum_squares = block_sum256(ss, lds);
+    const float mean_square = __fdiv_rn(sum_squares, (float)cols);
+    const float inverse_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean_square, eps)));
+    const uint32_t T = cols / 32;
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t g8 = threadIdx.x + it * 256;
+        const bool valid = g8 < groups8;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            v[k] = valid ? __fmul_rn(__fmul_rn(row[g8 * 8 + k], inverse_rms), weight[g8 * 8 + k]) : 0.0f;
+        emit_digits(v, valid, (size_t)b * T + g8 / 4, g8 & 3u, words, mult);
+    }
+}
+
+// kernels.zig:233-239 siluMul (math.zig:69-71 silu) over the fused gate|up
+// output, emitting digit planes for the down projection.
+__global__ __launch_bounds__(256) void silu_digits_kernel(const float *gu, uint32_t ffn, uint32_t *words,
+                                                          float *mult) {
+    const uint32_t b = blockIdx.x;
+    const float *gate = gu + (size_t)b * 2 * ffn;
+    const float *up = gate + ffn;
+    const uint32_t groups8 = ffn / 8;
+    const uint32_t iters = (groups8 + 255) / 256;
+    const uint32_t T = ffn / 32;
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t g8 = threadIdx.x + it * 256;
+        const bool valid = g8 < groups8;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (valid) {
+                const float g = gate[g8 * 8 + k];
+                const float silu = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
+                v[k] = __fmul_rn(silu, up[g8 * 8 + k]);
+            } else {
+                v[k] = 0.0f;
+            }
+        }
+        emit_digits(v, valid, (size_t)b * T + g8 / 4, g8 & 3u, words, mult);
+    }
+}
+
+struct QkArgs {
+    const float *qkv;          // batch x (heads + 2 kv_heads) * 128
+    const float *q_norm, *k_norm;
+    const float *rope_cos, *rope_sin;  // [max_positions][64]
+    const uint32_t *pos;
+    float *q_out;              // batch x heads * 128
+    uint8_t *k_scales, *k_codes, *v_scales, *v_codes;  // this layer, sequence 0
+    uint64_t seq_stride;
+    uint32_t heads, kv_heads;
+    float eps;
+};
+
+// decoder.zig:180-216 for head_dim 128: per-head rmsNorm of q and k
+// (kernels.zig:288-300), ropeInPlace with the precomputed tables
+// (kernels.zig:495-527, pair (i, i + 64)), and appendCacheRow(.q8) of k and v
+// (quant.zig:197-288). One wavefront per head row; lane i holds dims i, i+64.
+__global__ __launch_bounds__(64) void qk_rope_append_kernel(const QkArgs a) {
+    constexpr int D = 128;
+    const uint32_t b = blockIdx.x;
+    const uint32_t hh = blockIdx.y;
+    const int lane = threadIdx.x;
+    const uint32_t qw = a.heads * D;
+    const uint32_t kvw = a.kv_heads * D;
+    const float *row = a.qkv + (size_t)b * (qw + 2 * kvw);
+    const uint32_t pos = a.pos[b];
+    int kind;  // 0 q, 1 k, 2 v
+    uint32_t head;
+    const float *src;
+    if (hh < a.heads) {
+        kind = 0; head = hh; src = row + head * D;
+    } else if (hh < a.heads + a.kv_heads) {
+        kind = 1; head = hh - a.heads; src = row + qw + head * D;
+    } else {
+        kind = 2; head = hh - a.heads - a.kv_heads; src = row + qw + kvw + head * D;
+    }
+    float x0 = src[lane];
+    float x1 = src[lane + 64];
+    if (kind != 2) {
+        const float *w = kind == 0 ? a.q_norm : a.k_norm;
+        const float ss = dev::wave_sum(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)));
+        const float inverse_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
+        x0 = __fmul_rn(__fmul_rn(x0, inverse_rms), w[lane]);
+        x1 = __fmul_rn(__fmul_rn(x1, inverse_rms), w[lane + 64]);
+        const float c = a.rope_cos[(size_t)pos * 64 + lane];
+        const float s = a.rope_sin[(size_t)pos * 64 + lane];
+        const float y0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+        const float y1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
+        x0 = y0;
+        x1 = y1;
+    }
+    if (kind == 0) {
+        float *dst = a.q_out + (size_t)b * qw + head * D;
+        dst[lane] = x0;
+        dst[lane + 64] = x1;
+        return;
+    }
+    uint8_t *scales = (kind == 1 ? a.k_scales : a.v_scales) + b * a.seq_stride;
+    uint8_t *codes = (kind == 1 ? a.k_codes : a.v_codes) + b * a.seq_stride;
+    const uint32_t gpr = kvw / 64;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const float v = g == 0 ? x0 : x1;
+        const float amax = dev::wave_max(fabsf(v));
+        const uint16_t bits = dev::f32_to_f16_bits(__fdiv_rn(amax, 128.0f));
+        const float stored = dev::f16_bits_to_f32(bits);
+        codes[(size_t)pos * kvw + head * D + g * 64 + lane] =
+            (uint8_t)(dev::quantize_one(v, stored, -128, 127) + 128);
+        if (lane == 0) reinterpret_cast<uint16_t *>(scales)[(size_t)pos * gpr + head * 2 + g] = bits;
+    }
+}
+
+// argmaxLogits (decoder.zig:290-301): the largest value, the lowest index
+// among equal maxima. Stage 1: one partial per block.
+__device__ __forceinline__ void better(float &v, uint32_t &i, float v2, uint32_t i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits, uint32_t count,
+                                                             uint32_t per_block, float *pv, uint32_t *pi) {
+    const uint32_t b = blockIdx.y;
+    const float *row = logits + (size_t)b * count;
+    const uint32_t start = blockIdx.x * per_block;
+    uint32_t end = start + per_block;
+    if (end > count) end = count;
+    float bv = -FLT_MAX;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t i = start + threadIdx.x; i < end; i += blockDim.x) better(bv, bi, row[i], i);
+    __shared__ float sv[256];
+    __shared__ uint32_t si[256];
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) {
+            float v = sv[threadIdx.x];
+            uint32_t i = si[threadIdx.x];
+            better(v, i, sv[threadIdx.x + w], si[threadIdx.x + w]);
+            sv[threadIdx.x] = v;
+            si[threadIdx.x] = i;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        pv[(size_t)b * gridDim.x + blockIdx.x] = sv[0];
+        pi[(size_t)b * gridDim.x + blockIdx.x] = si[0];
+    }
+}
+
+// Stage 2: merges the partials, writes the next token, records it in the
+// history at (position - history base), and advances the position.
+__global__ __launch_bounds__(64) void argmax_finish_kernel(const float *pv, const uint32_t *pi,
+                                                           uint32_t parts, uint32_t *tokens, uint32_t *pos,
+                                                           const uint32_t *hist_base, uint32_t *history,
+                                                           uint32_t batch, uint32_t history_rows) {
+    const uint32_t b = blockIdx.x;
+    float bv = -FLT_MAX;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t p = threadIdx.x; p < parts; p += 64) better(bv, bi, pv[(size_t)b * parts + p], pi[(size_t)b * parts + p]);
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const float v2 = __shfl_xor(bv, mask, 64);
+        const uint32_t i2 = __shfl_xor(bi, mask, 64);
+        better(bv, bi, v2, i2);
+    }
+    if (threadIdx.x == 0) {
+        // A row of NaN logits leaves no index; the reference then returns 0.
+        const uint32_t token = bi == 0xffffffffu ? 0u : bi;
+        tokens[b] = token;
+        const uint32_t p = pos[b];
+        if (history) {
+            const uint32_t row = p - hist_base[b];
+            if (row < history_rows) history[(size_t)row * batch + b] = token;
+        }
+        pos[b] = p + 1;
+    }
+}
+
+__global__ void advance_kernel(uint32_t *pos, uint32_t batch) {
+    const uint32_t b = threadIdx.x;
+    if (b < batch) pos[b] += 1;
+}
+
+__global__ void fill_kernel(float *dst, uint64_t count, float value) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) dst[i] = value;
+}
+
+}  // namespace
+}  // namespace qwh
+
+using qwh::Matrix;
+
+struct qwh_decoder {
+    qwh_ctx *ctx = nullptr;
+    qwh_decoder_config c{};
+    uint32_t batch = 0;
+    uint32_t qw = 0, kvw = 0;
+    struct Layer {
+        Matrix qkv, o, gu, down;
+        float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
+    };
+    std::vector<Layer> layers;
+    Matrix embed, lm_head;
+    float *final_norm = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    uint8_t *keys = nullptr, *values = nullptr;
+    size_t cache_scales = 0, cache_codes = 0, layer_stride = 0, seq_stride = 0;
+    uint32_t *tokens_dev = nullptr, *pos_dev = nullptr, *hist_base_dev = nullptr, *history_dev = nullptr;
+    uint32_t history_rows = 0;
+    float *hidden = nullptr, *qkv = nullptr, *q_rot = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+    void *digits = nullptr;
+    void *attn_scratch = nullptr;
+    float *arg_v = nullptr;
+    uint32_t *arg_i = nullptr;
+    uint32_t arg_parts = 0, arg_per_block = 0;
+    uint32_t *host_stage = nullptr;  // pinned: tokens in / ids out
+    std::vector<uint32_t> pos_host;
+    std::vector<void *> allocations;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};
+    bool use_graph = true;
+};
+
+namespace qwh {
+namespace {
+
+int32_t dalloc(qwh_decoder *d, size_t bytes, void **out) {
+    void *p = nullptr;
+    const hipError_t err = hipMalloc(&p, bytes ? bytes : 1);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(d->ctx, QWH_E_OUT_OF_MEMORY, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(err));
+    }
+    d->allocations.push_back(p);
+    *out = p;
+    return QWH_OK;
+}
+
+int32_t alloc_matrix(qwh_decoder *d, Matrix &m, uint32_t rows, uint32_t cols) {
+    m.format = QWH_FORMAT_Q4;
+    m.rows = rows;
+    m.cols = cols;
+    m.owned = false;  // freed with the decoder's allocations
+    const size_t groups = (size_t)rows * (cols / 64);
+    QWH_TRY(dalloc(d, groups * 2, reinterpret_cast<void **>(&m.scales)));
+    QWH_TRY(dalloc(d, groups * 32, reinterpret_cast<void **>(&m.data)));
+    return QWH_OK;
+}
+
+int32_t fill_ones(qwh_decoder *d, float *dst, uint64_t count) {
+    fill_kernel<<<(unsigned)((count + 255) / 256 < 1024 ? (count + 255) / 256 : 1024), 256, 0, d->ctx->stream>>>(
+        dst, count, 1.0f);
+    return check_hip(d->ctx, hipGetLastError(), "fill");
+}
+
+// Enqueues one decoder step for every sequence (tokens and positions read
+// from device memory).
+int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
+    qwh_ctx *ctx = d->ctx;
+    hipStream_t s = ctx->stream;
+    const qwh_decoder_config &c = d->c;
+    const uint32_t B = d->batch;
+    uint32_t *words = static_cast<uint32_t *>(d->digits);
+    auto mult_of = [&](uint32_t cols) {
+        return reinterpret_cast<float *>(words + (size_t)B * (cols / 32) * dev::kChunkWords);
+    };
+    hipError_t err = hipSuccess;
+    embed_q4_kernel<<<B, 256, 0, s>>>(d->tokens_dev, reinterpret_cast<const uint16_t *>(d->embed.scales),
+                                      d->embed.data, c.hidden, d->hidden);
+    for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
+        qwh_decoder::Layer &L = d->layers[l];
+        rmsnorm_digits_kernel<<<B, 256, 0, s>>>(d->hidden, L.attn_norm, c.hidden, c.eps, words, mult_of(c.hidden));
+        err = launch_gemv_q4(s, ctx->cus, words, L.qkv, B, d->qkv, nullptr);
+        if (err != hipSuccess) break;
+        QkArgs qa{};
+        qa.qkv = d->qkv;
+        qa.q_norm = L.q_norm;
+        qa.k_norm = L.k_norm;
+        qa.rope_cos = d->rope_cos;
+        qa.rope_sin = d->rope_sin;
+        qa.pos = d->pos_dev;
+        qa.q_out = d->q_rot;
+        uint8_t *kl = d->keys + (size_t)l * d->layer_stride;
+        uint8_t *vl = d->values + (size_t)l * d->layer_stride;
+        qa.k_scales = kl;
+        qa.k_codes = kl + d->cache_scales;
+        qa.v_scales = vl;
+        qa.v_codes = vl + d->cache_scales;
+        qa.seq_stride = d->seq_stride;
+        qa.heads = c.heads;
+        qa.kv_heads = c.kv_heads;
+        qa.eps = c.eps;
+        qk_rope_append_kernel<<<dim3(B, c.heads + 2 * c.kv_heads), 64, 0, s>>>(qa);
+        AttentionArgs aa{};
+        aa.out = d->attn;
+        aa.query = d->q_rot;
+        aa.k_scales = kl;
+        aa.k_codes = kl + d->cache_scales;
+        aa.v_scales = vl;
+        aa.v_codes = vl + d->cache_scales;
+        aa.cached_dev = d->pos_dev;
+        aa.cached_bias = 1;
+        aa.capacity = c.max_positions;
+        aa.heads = c.heads;
+        aa.kv_heads = c.kv_heads;
+        aa.head_dim = c.head_dim;
+        aa.batch = B;
+        aa.scale_stride = d->seq_stride;
+        aa.code_stride = d->seq_stride;
+        err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch);
+        if (err != hipSuccess) break;
+        err = launch_prep_q4(s, d->attn, B, d->qw, words);
+        if (err != hipSuccess) break;
+        err = launch_gemv_q4(s, ctx->cus, words, L.o, B, d->hidden, d->hidden);
+        if (err != hipSuccess) break;
+        rmsnorm_digits_kernel<<<B, 256, 0, s>>>(d->hidden, L.ffn_norm, c.hidden, c.eps, words, mult_of(c.hidden));
+        err = launch_gemv_q4(s, ctx->cus, words, L.gu, B, d->gu, nullptr);
+        if (err != hipSuccess) break;
+        silu_digits_kernel<<<B, 256, 0, s>>>(d->gu, c.ffn, words, mult_of(c.ffn));
+        err = launch_gemv_q4(s, ctx->cus, words, L.down, B, d->hidden, d->hidden);
+    }
+    if (err == hipSuccess) {
+        if (want_logits) {
+            rmsnorm_digits_kernel<<<B, 256, 0, s>>>(d->hidden, d->final_norm, c.hidden, c.eps, words, mult_of(c.hidden));
+            err = launch_gemv_q4(s, ctx->cus, words, d->lm_head, B, d->logits, nullptr);
+            if (err == hipSuccess) {
+                argmax_partial_kernel<<<dim3(d->arg_parts, B), 256, 0, s>>>(d->logits, c.vocab, d->arg_per_block,
+                                                                             d->arg_v, d->arg_i);
+                argmax_finish_kernel<<<B, 64, 0, s>>>(d->arg_v, d->arg_i, d->arg_parts, d->tokens_dev, d->pos_dev,
+                                                      d->hist_base_dev, d->history_dev, B, d->history_rows);
+                err = hipGetLastError();
+            }
+        } else {
+            advance_kernel<<<1, 64 * ((B + 63) / 64), 0, s>>>(d->pos_dev, B);
+            err = hipGetLastError();
+        }
+    }
+    if (err == hipSuccess) err = hipGetLastError();
+    return check_hip(ctx, err, "decoder step launch");
+}
+
+int32_t run_step(qwh_decoder *d, bool want_logits) {
+    qwh_ctx *ctx = d->ctx;
+    if (!d->use_graph) return enqueue_step(d, want_logits);
+    hipGraphExec_t &exec = d->graph[want_logits ? 1 : 0];
+    if (!exec) {
+        QWH_TRY(check_hip(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "begin capture"));
+        const int32_t st = enqueue_step(d, want_logits);
+        hipGraph_t graph = nullptr;
+        const hipError_t end = hipStreamEndCapture(ctx->stream, &graph);
+        if (st != QWH_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return st;
+        }
+        QWH_TRY(check_hip(ctx, end, "end capture"));
+        const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        QWH_TRY(check_hip(ctx, inst, "graph instantiate"));
+    }
+    return check_hip(ctx, hipGraphLaunch(exec, ctx->stream), "graph launch");
+}
+
+// kernels.zig:534-564 buildRopeTables / inverseFrequency, in f32 on the host
+// as model.zig:400-407 does at load time.
+void build_rope_tables(std::vector<float> &cos_t, std::vector<float> &sin_t, uint32_t half, float theta,
+                       uint32_t max_positions) {
+    const uint32_t head_dim = half * 2;
+    cos_t.assign((size_t)max_positions * half, 0.0f);
+    sin_t.assign((size_t)max_positions * half, 0.0f);
+    for (uint32_t p = 0; p < max_positions; ++p) {
+        for (uint32_t i = 0; i < half; ++i) {
+            const volatile float exponent = -2.0f * (float)i / (float)head_dim;
+            const float inv = powf(theta, exponent);
+            const volatile float angle = (float)p * inv;
+            cos_t[(size_t)p * half + i] = cosf(angle);
+            sin_t[(size_t)p * half + i] = sinf(angle);
+        }
+    }
+}
+
+int32_t copy_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, const Matrix &src) {
+    const size_t gpr = dst.cols / 64;
+    hipStream_t s = d->ctx->stream;
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(dst.scales + (size_t)row_offset * gpr * 2, src.scales,
+                                             (size_t)src.rows * gpr * 2, hipMemcpyDeviceToDevice, s), "copy scales"));
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(dst.data + (size_t)row_offset * gpr * 32, src.data,
+                                             (size_t)src.rows * gpr * 32, hipMemcpyDeviceToDevice, s), "copy data"));
+    return QWH_OK;
+}
+
+// Synthetic values for rows [row_offset, row_offset + rows) of `dst` from
+// rows [0, rows) of `stream`, generated in slabs through a temporary f32
+// buffer and quantized to q4 on the device.
+int32_t synth_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, uint32_t rows, uint32_t seed,
+                   uint32_t stream, float scale, float *temp, size_t temp_values) {
+    const uint32_t cols = dst.cols;
+    const size_t gpr = cols / 64;
+    uint32_t slab = (uint32_t)(temp_values / cols);
+    if (slab == 0) return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "synthetic slab too small");
+    hipStream_t s = d->ctx->stream;
+    for (uint32_t r = 0; r < rows; r += slab) {
+        const uint32_t n = rows - r < slab ? rows - r : slab;
+        QWH_TRY(check_hip(d->ctx, launch_synth_normal(s, seed, stream, (uint64_t)r * cols, (uint64_t)n * cols, scale, temp),
+                          "synthetic values"));
+        QWH_TRY(check_hip(d->ctx, launch_quantize_rows(s, QWH_FORMAT_Q4, temp, (uint64_t)n * gpr,
+                                                      dst.scales + (size_t)(row_offset + r) * gpr * 2,
+                                                      dst.data + (size_t)(row_offset + r) * gpr * 32),
+                          "quantize"));
+    }
+    return QWH_OK;
+}
+
+int32_t check_matrix(qwh_decoder *d, const Matrix *m, uint32_t rows, uint32_t cols) {
+    if (!m) return fail(d->ctx, QWH_E_NOT_FOUND, "unknown matrix handle");
+    if (m->format != QWH_FORMAT_Q4)
+        return fail(d->ctx, QWH_E_UNSUPPORTED, "decoder matrices must be q4 (format 16), got %d", m->format);
+    if (m->rows != rows || m->cols != cols)
+        return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "matrix is %ux%u, expected %ux%u", m->rows, m->cols, rows, cols);
+    return QWH_OK;
+}
+
+}  // namespace
+}  // namespace qwh
+
+using namespace qwh;
+
+extern "C" {
+
+int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch, qwh_decoder **out) {
+    if (!ctx || !config || !out || batch == 0) return QWH_E_INVALID_ARGUMENT;
+    const qwh_decoder_config &c = *config;
+    if (c.head_dim != 128)
+        return fail(ctx, QWH_E_UNSUPPORTED, "the decoder step supports head_dim 128 (got %u)", c.head_dim);
+    if (c.kv_heads == 0 || c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "heads %u / kv_heads %u", c.heads, c.kv_heads);
+    if (c.hidden % 64 || c.ffn % 64 || c.hidden == 0 || c.ffn == 0 || c.layers == 0 || c.vocab == 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "hidden and ffn must be multiples of 64");
+    // model.zig:62 position_limit and :1006-1009 validateCapacity.
+    if (c.max_positions == 0 || c.max_positions > 8192)
+        return fail(ctx, QWH_E_LIMIT_EXCEEDED, "max_positions %u outside 1..8192", c.max_positions);
+    qwh_decoder *d = new qwh_decoder();
+    d->ctx = ctx;
+    d->c = c;
+    d->batch = batch;
+    d->qw = c.heads * c.head_dim;
+    d->kvw = c.kv_heads * c.head_dim;
+    d->use_graph = getenv("QWH_NO_GRAPH") == nullptr;
+    auto cleanup = [&](int32_t st) {
+        qwh_decoder_destroy(d);
+        return st;
+    };
+    int32_t st = QWH_OK;
+    d->layers.resize(c.layers);
+    for (uint32_t l = 0; l < c.layers && st == QWH_OK; ++l) {
+        qwh_decoder::Layer &L = d->layers[l];
+        st = alloc_matrix(d, L.qkv, d->qw + 2 * d->kvw, c.hidden);
+        if (st == QWH_OK) st = alloc_matrix(d, L.o, c.hidden, d->qw);
+        if (st == QWH_OK) st = alloc_matrix(d, L.gu, 2 * c.ffn, c.hidden);
+        if (st == QWH_OK) st = alloc_matrix(d, L.down, c.hidden, c.ffn);
+        if (st == QWH_OK) st = dalloc(d, sizeof(float) * c.hidden, reinterpret_cast<void **>(&L.attn_norm));
+        if (st == QWH_OK) st = dalloc(d, sizeof(float) * c.hidden, reinterpret_cast<void **>(&L.ffn_norm));
+        if (st == QWH_OK) st = dalloc(d, sizeof(float) * c.head_dim, reinterpret_cast<void **>(&L.q_norm));
+        if (st == QWH_OK) st = dalloc(d, sizeof(float) * c.head_dim, reinterpret_cast<void **>(&L.k_norm));
+        if (st == QWH_OK) st = fill_ones(d, L.attn_norm, c.hidden);
+        if (st == QWH_OK) st = fill_ones(d, L.ffn_norm, c.hidden);
+        if (st == QWH_OK) st = fill_ones(d, L.q_norm, c.head_dim);
+        if (st == QWH_OK) st = fill_ones(d, L.k_norm, c.head_dim);
+    }
+    if (st == QWH_OK) st = alloc_matrix(d, d->embed, c.vocab, c.hidden);
+    if (st == QWH_OK) st = alloc_matrix(d, d->lm_head, c.vocab, c.hidden);
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * c.hidden, reinterpret_cast<void **>(&d->final_norm));
+    if (st == QWH_OK) st = fill_ones(d, d->final_norm, c.hidden);
+    // RoPE tables.
+    std::vector<float> cos_t, sin_t;
+    const uint32_t half = c.head_dim / 2;
+    build_rope_tables(cos_t, sin_t, half, c.theta, c.max_positions);
+    if (st == QWH_OK) st = dalloc(d, cos_t.size() * 4, reinterpret_cast<void **>(&d->rope_cos));
+    if (st == QWH_OK) st = dalloc(d, sin_t.size() * 4, reinterpret_cast<void **>(&d->rope_sin));
+    if (st == QWH_OK) st = check_hip(ctx, hipMemcpy(d->rope_cos, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice), "rope");
+    if (st == QWH_OK) st = check_hip(ctx, hipMemcpy(d->rope_sin, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice), "rope");
+    // Caches: per sequence, per layer [scales][codes] (decoder.zig:58-65).
+    d->cache_scales = (size_t)c.max_positions * (d->kvw / 64) * 2;
+    d->cache_codes = (size_t)c.max_positions * d->kvw;
+    d->layer_stride = d->cache_scales + d->cache_codes;
+    d->seq_stride = d->layer_stride * c.layers;
+    if (st == QWH_OK) st = dalloc(d, d->seq_stride * batch, reinterpret_cast<void **>(&d->keys));
+    if (st == QWH_OK) st = dalloc(d, d->seq_stride * batch, reinterpret_cast<void **>(&d->values));
+    if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->keys, 0, d->seq_stride * batch, ctx->stream), "cache");
+    if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->values, 0, d->seq_stride * batch, ctx->stream), "cache");
+    // State.
+    d->history_rows = c.max_positions;
+    if (st == QWH_OK) st = dalloc(d, 4 * batch, reinterpret_cast<void **>(&d->tokens_dev));
+    if (st == QWH_OK) st = dalloc(d, 4 * batch, reinterpret_cast<void **>(&d->pos_dev));
+    if (st == QWH_OK) st = dalloc(d, 4 * batch, reinterpret_cast<void **>(&d->hist_base_dev));
+    if (st == QWH_OK) st = dalloc(d, 4 * (size_t)batch * d->history_rows, reinterpret_cast<void **>(&d->history_dev));
+    if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->tokens_dev, 0, 4 * batch, ctx->stream), "state");
+    if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->pos_dev, 0, 4 * batch, ctx->stream), "state");
+    if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->hist_base_dev, 0, 4 * batch, ctx->stream), "state");
+    d->pos_host.assign(batch, 0);
+    // Scratch.
+    const uint32_t widest = c.ffn > c.hidden ? (c.ffn > d->qw ? c.ffn : d->qw) : (c.hidden > d->qw ? c.hidden : d->qw);
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.hidden, reinterpret_cast<void **>(&d->hidden));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (d->qw + 2 * d->kvw), reinterpret_cast<void **>(&d->qkv));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->qw, reinterpret_cast<void **>(&d->q_rot));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->qw, reinterpret_cast<void **>(&d->attn));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * 2 * c.ffn, reinterpret_cast<void **>(&d->gu));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (size_t)c.vocab, reinterpret_cast<void **>(&d->logits));
+    if (st == QWH_OK) st = dalloc(d, q4_digit_bytes(batch, widest), &d->digits);
+    AttentionArgs aa{};
+    aa.capacity = c.max_positions;
+    aa.heads = c.heads;
+    aa.kv_heads = c.kv_heads;
+    aa.head_dim = c.head_dim;
+    aa.batch = batch;
+    if (st == QWH_OK) st = dalloc(d, attention_scratch_bytes(ctx->cus, aa), &d->attn_scratch);
+    d->arg_per_block = 4096;
+    d->arg_parts = (c.vocab + d->arg_per_block - 1) / d->arg_per_block;
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_v));
+    if (st == QWH_OK) st = dalloc(d, 4 * (size_t)batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_i));
+    if (st == QWH_OK) {
+        void *p = nullptr;
+        st = check_hip(ctx, hipHostMalloc(&p, 4 * (size_t)batch, hipHostMallocDefault), "pinned staging");
+        d->host_stage = static_cast<uint32_t *>(p);
+    }
+    if (st == QWH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "decoder create");
+    if (st != QWH_OK) return cleanup(st);
+    *out = d;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_destroy(qwh_decoder *d) {
+    if (!d) return QWH_E_INVALID_ARGUMENT;
+    if (d->ctx) (void)hipStreamSynchronize(d->ctx->stream);
+    for (hipGraphExec_t &g : d->graph)
+        if (g) (void)hipGraphExecDestroy(g);
+    for (void *p : d->allocations) (void)hipFree(p);
+    if (d->host_stage) (void)hipHostFree(d->host_stage);
+    delete d;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_set_matrix(qwh_decoder *d, uint32_t kind, uint32_t layer, uint64_t handle) {
+    if (!d) return QWH_E_INVALID_ARGUMENT;
+    const Matrix *m = find_matrix(d->ctx, handle);
+    const qwh_decoder_config &c = d->c;
+    if (kind == QWH_T_EMBED || kind == QWH_T_LM_HEAD) {
+        QWH_TRY(check_matrix(d, m, c.vocab, c.hidden));
+        return copy_rows(d, kind == QWH_T_EMBED ? d->embed : d->lm_head, 0, *m);
+    }
+    if (layer >= c.layers) return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "layer %u of %u", layer, c.layers);
+    qwh_decoder::Layer &L = d->layers[layer];
+    switch (kind) {
+    case QWH_T_Q: QWH_TRY(check_matrix(d, m, d->qw, c.hidden)); return copy_rows(d, L.qkv, 0, *m);
+    case QWH_T_K: QWH_TRY(check_matrix(d, m, d->kvw, c.hidden)); return copy_rows(d, L.qkv, d->qw, *m);
+    case QWH_T_V: QWH_TRY(check_matrix(d, m, d->kvw, c.hidden)); return copy_rows(d, L.qkv, d->qw + d->kvw, *m);
+    case QWH_T_O: QWH_TRY(check_matrix(d, m, c.hidden, d->qw)); return copy_rows(d, L.o, 0, *m);
+    case QWH_T_GATE: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, 0, *m);
+    case QWH_T_UP: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, c.ffn, *m);
+    case QWH_T_DOWN: QWH_TRY(check_matrix(d, m, c.hidden, c.ffn)); return copy_rows(d, L.down, 0, *m);
+    default: return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "unknown matrix kind %u", kind);
+    }
+}
+
+int32_t qwh_decoder_set_vector(qwh_decoder *d, uint32_t kind, uint32_t layer, const float *values, uint32_t count) {
+    if (!d || !values) return QWH_E_INVALID_ARGUMENT;
+    const qwh_decoder_config &c = d->c;
+    float *dst = nullptr;
+    uint32_t expect = 0;
+    if (kind == QWH_T_FINAL_NORM) {
+        dst = d->final_norm;
+        expect = c.hidden;
+    } else {
+        if (layer >= c.layers) return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "layer %u of %u", layer, c.layers);
+        qwh_decoder::Layer &L = d->layers[layer];
+        switch (kind) {
+        case QWH_T_ATTN_NORM: dst = L.attn_norm; expect = c.hidden; break;
+        case QWH_T_FFN_NORM: dst = L.ffn_norm; expect = c.hidden; break;
+        case QWH_T_Q_NORM: dst = L.q_norm; expect = c.head_dim; break;
+        case QWH_T_K_NORM: dst = L.k_norm; expect = c.head_dim; break;
+        default: return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "unknown vector kind %u", kind);
+        }
+    }
+    if (count != expect) return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "vector of %u values, expected %u", count, expect);
+    QWH_TRY(check_hip(d->ctx, hipMemcpy(dst, values, sizeof(float) * count, hipMemcpyHostToDevice), "set vector"));
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_init_synthetic(qwh_decoder *d, uint32_t seed) {
+    if (!d) return QWH_E_INVALID_ARGUMENT;
+    const qwh_decoder_config &c = d->c;
+    const size_t temp_values = (size_t)64 << 20;
+    float *temp = nullptr;
+    QWH_TRY(check_hip(d->ctx, hipMalloc(&temp, temp_values * 4), "synthetic temp"));
+    int32_t st = synth_rows(d, d->embed, 0, c.vocab, seed, kStreamEmbed, 0.02f, temp, temp_values);
+    if (st == QWH_OK) st = synth_rows(d, d->lm_head, 0, c.vocab, seed, kStreamLmHead, 0.02f, temp, temp_values);
+    for (uint32_t l = 0; l < c.layers && st == QWH_OK; ++l) {
+        qwh_decoder::Layer &L = d->layers[l];
+        const uint32_t sb = kStreamLayerBase + 16 * l;
+        st = synth_rows(d, L.qkv, 0, d->qw, seed, sb + 0, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, L.qkv, d->qw, d->kvw, seed, sb + 1, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, L.qkv, d->qw + d->kvw, d->kvw, seed, sb + 2, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, L.o, 0, c.hidden, seed, sb + 3, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, L.gu, 0, c.ffn, seed, sb + 4, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, L.gu, c.ffn, c.ffn, seed, sb + 5, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, L.down, 0, c.hidden, seed, sb + 6, 0.02f, temp, temp_values);
+    }
+    const int32_t sync = check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "synthetic model");
+    (void)hipFree(temp);
+    return st != QWH_OK ? st : sync;
+}
+
+int32_t qwh_decoder_reset(qwh_decoder *d) {
+    if (!d) return QWH_E_INVALID_ARGUMENT;
+    hipStream_t s = d->ctx->stream;
+    QWH_TRY(check_hip(d->ctx, hipMemsetAsync(d->keys, 0, d->seq_stride * d->batch, s), "reset"));
+    QWH_TRY(check_hip(d->ctx, hipMemsetAsync(d->values, 0, d->seq_stride * d->batch, s), "reset"));
+    QWH_TRY(check_hip(d->ctx, hipMemsetAsync(d->pos_dev, 0, 4 * d->batch, s), "reset"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "reset"));
+    d->pos_host.assign(d->batch, 0);
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_prefill_random(qwh_decoder *d, uint32_t seq, uint32_t count, uint32_t seed) {
+    if (!d || seq >= d->batch) return QWH_E_INVALID_ARGUMENT;
+    if (count > d->c.max_positions) return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "%u positions of %u", count, d->c.max_positions);
+    hipStream_t s = d->ctx->stream;
+    const size_t values = (size_t)count * d->kvw;
+    float *temp = nullptr;
+    if (values) QWH_TRY(check_hip(d->ctx, hipMalloc(&temp, values * 4), "prefill temp"));
+    int32_t st = QWH_OK;
+    for (uint32_t l = 0; l < d->c.layers && st == QWH_OK && values; ++l) {
+        for (int kv = 0; kv < 2 && st == QWH_OK; ++kv) {
+            const uint32_t stream = kStreamCacheBase + 0x100 * seq + 2 * l + kv;
+            uint8_t *base = (kv == 0 ? d->keys : d->values) + (size_t)seq * d->seq_stride + (size_t)l * d->layer_stride;
+            st = check_hip(d->ctx, launch_synth_normal(s, seed, stream, 0, values, 1.0f, temp), "prefill values");
+            if (st == QWH_OK)
+                st = check_hip(d->ctx, launch_quantize_rows(s, QWH_FORMAT_Q8, temp, values / 64, base, base + d->cache_scales),
+                               "prefill quantize");
+        }
+    }
+    if (st == QWH_OK) {
+        d->host_stage[0] = count;
+        st = check_hip(d->ctx, hipMemcpyAsync(d->pos_dev + seq, d->host_stage, 4, hipMemcpyHostToDevice, s), "position");
+    }
+    const int32_t sync = check_hip(d->ctx, hipStreamSynchronize(s), "prefill");
+    if (temp) (void)hipFree(temp);
+    if (st == QWH_OK && sync == QWH_OK) d->pos_host[seq] = count;
+    return st != QWH_OK ? st : sync;
+}
+
+int32_t qwh_decoder_cache_planes(qwh_decoder *d, uint32_t seq, uint32_t layer, void **k_scales, void **k_codes,
+                                 void **v_scales, void **v_codes) {
+    if (!d || seq >= d->batch || layer >= d->c.layers) return QWH_E_INVALID_ARGUMENT;
+    uint8_t *kb = d->keys + (size_t)seq * d->seq_stride + (size_t)layer * d->layer_stride;
+    uint8_t *vb = d->values + (size_t)seq * d->seq_stride + (size_t)layer * d->layer_stride;
+    if (k_scales) *k_scales = kb;
+    if (k_codes) *k_codes = kb + d->cache_scales;
+    if (v_scales) *v_scales = vb;
+    if (v_codes) *v_codes = vb + d->cache_scales;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_position(qwh_decoder *d, uint32_t seq, uint32_t *out) {
+    if (!d || !out || seq >= d->batch) return QWH_E_INVALID_ARGUMENT;
+    *out = d->pos_host[seq];
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_set_position(qwh_decoder *d, uint32_t seq, uint32_t position) {
+    if (!d || seq >= d->batch) return QWH_E_INVALID_ARGUMENT;
+    if (position > d->c.max_positions) return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "position %u", position);
+    d->host_stage[0] = position;
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->pos_dev + seq, d->host_stage, 4, hipMemcpyHostToDevice, d->ctx->stream), "position"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "position"));
+    d->pos_host[seq] = position;
+    return QWH_OK;
+}
+
+static int32_t upload_tokens(qwh_decoder *d, const uint32_t *tokens, uint32_t steps) {
+    for (uint32_t b = 0; b < d->batch; ++b) {
+        if (tokens[b] >= d->c.vocab) return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "token %u >= vocab %u", tokens[b], d->c.vocab);
+        // decoder.zig:142 PositionExceeded.
+        if ((uint64_t)d->pos_host[b] + steps > d->c.max_positions)
+            return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "sequence %u: position %u + %u steps exceeds %u", b,
+                        d->pos_host[b], steps, d->c.max_positions);
+    }
+    memcpy(d->host_stage, tokens, 4 * (size_t)d->batch);
+    return check_hip(d->ctx, hipMemcpyAsync(d->tokens_dev, d->host_stage, 4 * (size_t)d->batch, hipMemcpyHostToDevice,
+                                            d->ctx->stream), "tokens");
+}
+
+int32_t qwh_decoder_forward(qwh_decoder *d, const uint32_t *tokens, int32_t want_logits) {
+    if (!d || !tokens) return QWH_E_INVALID_ARGUMENT;
+    QWH_TRY(upload_tokens(d, tokens, 1));
+    // The history is written only by generate; park its base past any row.
+    QWH_TRY(run_step(d, want_logits != 0));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "forward"));
+    for (uint32_t &p : d->pos_host) p += 1;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_step(qwh_decoder *d, const uint32_t *tokens, uint32_t *next_tokens) {
+    if (!d || !tokens || !next_tokens) return QWH_E_INVALID_ARGUMENT;
+    QWH_TRY(upload_tokens(d, tokens, 1));
+    QWH_TRY(run_step(d, true));
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->host_stage, d->tokens_dev, 4 * (size_t)d->batch, hipMemcpyDeviceToHost,
+                                             d->ctx->stream), "next tokens"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "step"));
+    memcpy(next_tokens, d->host_stage, 4 * (size_t)d->batch);
+    for (uint32_t &p : d->pos_host) p += 1;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_generate(qwh_decoder *d, const uint32_t *tokens, uint32_t steps, uint32_t *ids_out) {
+    if (!d || !tokens || !ids_out) return QWH_E_INVALID_ARGUMENT;
+    if (steps == 0) return QWH_OK;
+    QWH_TRY(upload_tokens(d, tokens, steps));
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->hist_base_dev, d->pos_dev, 4 * (size_t)d->batch, hipMemcpyDeviceToDevice,
+                                             d->ctx->stream), "history base"));
+    for (uint32_t i = 0; i < steps; ++i) QWH_TRY(run_step(d, true));
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(ids_out, d->history_dev, 4 * (size_t)d->batch * steps, hipMemcpyDeviceToHost,
+                                             d->ctx->stream), "history"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "generate"));
+    for (uint32_t &p : d->pos_host) p += steps;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_logits(qwh_decoder *d, uint32_t seq, float *out, uint32_t count) {
+    if (!d || !out || seq >= d->batch) return QWH_E_INVALID_ARGUMENT;
+    if (count != d->c.vocab) return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "logits count %u, vocab %u", count, d->c.vocab);
+    QWH_TRY(check_hip(d->ctx, hipMemcpy(out, d->logits + (size_t)seq * d->c.vocab, 4 * (size_t)count, hipMemcpyDeviceToHost),
+                      "logits"));
+    return QWH_OK;
+}
+
+}  // extern "C"

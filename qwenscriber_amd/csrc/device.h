@@ -1,0 +1,116 @@
+// Device-side helpers shared by the kernels: f16 codec, wave reductions,
+// the bit-exact quantizer of one value, and the signed-hex-digit encoding of
+// activations consumed by the q4 GEMV.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qwh {
+namespace dev {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) v = fmaxf(v, __shfl_xor(v, mask, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, kWave);
+    return v;
+}
+
+// f32 -> f16 bits, round to nearest even, overflow to infinity
+// (half_float.zig:14-17). Integer arithmetic only, so the result does not
+// depend on the hardware rounding mode.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float value) {
+    uint32_t bits = __float_as_uint(value);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int exponent = (int)((bits >> 23) & 0xffu);
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent == 0xff) return (uint16_t)(sign | 0x7c00u | (mantissa ? 0x200u : 0u));
+    int half_exponent = exponent - 112;  // -127 + 15
+    if (half_exponent >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    uint32_t shift;
+    uint32_t base;
+    if (half_exponent <= 0) {
+        if (half_exponent < -10) return (uint16_t)sign;
+        mantissa |= 0x800000u;
+        shift = (uint32_t)(14 - half_exponent);
+        base = 0;
+    } else {
+        shift = 13;
+        base = (uint32_t)half_exponent << 10;
+    }
+    uint32_t kept = mantissa >> shift;
+    uint32_t rest = mantissa & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    uint32_t rounded = kept + ((rest > half || (rest == half && (kept & 1u))) ? 1u : 0u);
+    return (uint16_t)(sign | (base + rounded));
+}
+
+// f16 bits -> f32, exact (the hardware conversion keeps f16 subnormals).
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// quant.zig:280-288 `quantizeOne`: round half away from zero against the
+// stored scale, clamp to [min_code, max_code].
+__device__ __forceinline__ int quantize_one(float value, float stored_scale, int min_code,
+                                            int max_code) {
+    if (stored_scale == 0.0f) return 0;
+    float scaled = __fdiv_rn(value, stored_scale);
+    float rounded = scaled >= 0.0f ? floorf(__fadd_rn(scaled, 0.5f)) : ceilf(__fsub_rn(scaled, 0.5f));
+    if (rounded <= (float)min_code) return min_code;
+    if (rounded >= (float)max_code) return max_code;
+    return (int)rounded;
+}
+
+// ---------------------------------------------------------------------------
+// Activation digits for the q4 GEMV.
+//
+// A chunk of 32 consecutive activations x_k is written as
+//     x_k ~= m * sum_{j<6} d_{j,k} 16^j,   d in [-8, 7],   m = 2^(e-22),
+// where 2^e bounds the chunk's largest |x|: x_int = rint(x * 2^(22-e)) is a
+// 23-bit signed integer, and u = x_int + 0x888888 has hex digit j equal to
+// d_j + 8. Digit plane j of 8 consecutive activations packs (d_j mod 16) into
+// the 8 nibbles of one dword, in element order -- the order of the q4 code
+// nibbles (quant.zig:36-41), so v_dot8_i32_i4 multiplies matching elements.
+// A chunk is 6 planes x 4 dwords, plane major, followed by nothing: the
+// per-chunk multiplier m lives in a separate f32 array.
+// ---------------------------------------------------------------------------
+constexpr int kDigitPlanes = 6;
+constexpr int kChunk = 32;                       // activations per chunk
+constexpr int kChunkWords = kDigitPlanes * 4;    // u32 per chunk
+
+// Encodes 8 activations (this thread's dword column q of its chunk) given the
+// chunk exponent e. Writes plane j of this column to planes[j].
+__device__ __forceinline__ void encode_digits8(const float v[8], int e, uint32_t planes[6]) {
+    const float up = __builtin_ldexpf(1.0f, 22 - e);
+    uint32_t u[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) u[k] = (uint32_t)((int)__builtin_rintf(v[k] * up) + 0x888888);
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w |= (((u[k] >> (4 * j)) & 0xfu) ^ 0x8u) << (4 * k);
+        planes[j] = w;
+    }
+}
+
+// Exponent e with |x| <= 2^e for the chunk maximum `amax` (clamped so that
+// 2^(22-e) stays finite; an all-zero chunk uses e = 0).
+__device__ __forceinline__ int chunk_exponent(float amax) {
+    if (!(amax > 0.0f)) return 0;
+    int e;
+    (void)__builtin_frexpf(amax, &e);  // amax = f 2^e, f in [0.5, 1)
+    return e < -100 ? -100 : e;
+}
+
+}  // namespace dev
+}  // namespace qwh

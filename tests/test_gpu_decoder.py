@@ -1,0 +1,117 @@
+"""GPU parity of the decoder step (decoder.zig:133-339) against the oracle's
+restatement, on synthetic q4 models with a q8 cache."""
+import os
+
+import numpy as np
+import pytest
+
+import qwenscriber_amd as qa
+from oracle import oracle as o
+from util import assert_close
+
+pytestmark = pytest.mark.gpu
+o.set_threads(min(16, os.cpu_count() or 1))
+
+TINY = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=1000,
+            max_positions=64, eps=1e-6, theta=1e6)
+
+
+def cache_hash(ctx, dec, seq, config):
+    """FNV-1a over a sequence's key planes then value planes, all layers, in
+    the decoder.zig:58-65 layout (as the oracle's qwref_decoder_cache_hash)."""
+    kvw = config["kv_heads"] * config["head_dim"]
+    layer_stride = config["max_positions"] * (kvw // 64) * 2 + config["max_positions"] * kvw
+    total = layer_stride * config["layers"]
+    ks, _, vs, _ = dec.cache_planes(seq, 0)
+    h = 0xCBF29CE484222325
+    for base in (ks, vs):
+        buf = np.empty(total, np.uint8)
+        ctx._check(ctx.lib.qwh_download(ctx.handle, buf.ctypes.data, base, total))
+        h = o.fnv1a64(buf, h)
+    return h
+
+
+@pytest.fixture
+def tiny_pair(ctx):
+    seed, batch = 9, 3
+    gpu = qa.Decoder(ctx, batch=batch, **TINY)
+    gpu.init_synthetic(seed)
+    ref = o.Decoder(seed, batch, **TINY)
+    for b, n in enumerate([0, 5, 17]):
+        gpu.prefill_random(b, n, seed)
+        ref.prefill_random(b, n)
+    yield gpu, ref
+    gpu.close()
+    ref.close()
+
+
+def test_prefilled_cache_is_bit_exact(ctx, tiny_pair):
+    gpu, ref = tiny_pair
+    for b in range(3):
+        assert cache_hash(ctx, gpu, b, TINY) == ref.cache_hash(b)
+        assert gpu.position(b) == ref.position(b)
+
+
+def test_teacher_forced_logits(ctx, tiny_pair):
+    gpu, ref = tiny_pair
+    for step in range(8):
+        tokens = [(step * 37 + b * 101) % TINY["vocab"] for b in range(3)]
+        gpu.forward(tokens, True)
+        for b in range(3):
+            ref.forward(b, tokens[b], True)
+            assert_close(gpu.logits(b), ref.logits(b), what=f"step {step} seq {b}")
+    for b in range(3):
+        assert gpu.position(b) == ref.position(b)
+
+
+def test_free_running_token_ids(ctx, tiny_pair):
+    gpu, ref = tiny_pair
+    start = [o.start_token(9, b, TINY["vocab"]) for b in range(3)]
+    ids = gpu.generate(start, 30)
+    for b in range(3):
+        t = start[b]
+        expected = []
+        for _ in range(30):
+            t = ref.step(b, t)
+            expected.append(t)
+        assert ids[:, b].tolist() == expected, b
+
+
+def test_step_and_generate_agree(ctx):
+    seed = 11
+    a = qa.Decoder(ctx, batch=2, **TINY)
+    b = qa.Decoder(ctx, batch=2, **TINY)
+    try:
+        for d in (a, b):
+            d.init_synthetic(seed)
+            d.prefill_random(0, 3, seed)
+            d.prefill_random(1, 9, seed)
+        tokens = np.array([1, 2], np.uint32)
+        stepped = []
+        t = tokens
+        for _ in range(12):
+            t = a.step(t)
+            stepped.append(t.copy())
+        generated = b.generate(tokens, 12)
+        assert np.array_equal(np.stack(stepped), generated)
+        assert a.position(0) == b.position(0) == 15
+    finally:
+        a.close()
+        b.close()
+
+
+def test_position_limit_and_token_range(ctx):
+    d = qa.Decoder(ctx, batch=1, **{**TINY, "max_positions": 4})
+    try:
+        d.init_synthetic(1)
+        d.prefill_random(0, 3, 1)
+        d.step([5])
+        with pytest.raises(qa.QwhError) as err:
+            d.step([5])   # decoder.zig:142 PositionExceeded
+        assert err.value.status == -9
+        d.reset()
+        with pytest.raises(qa.QwhError) as err:
+            d.step([TINY["vocab"]])
+        assert err.value.status == -7
+    finally:
+        d.close()
