@@ -348,6 +348,13 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
     if (((uintptr_t)x_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "x must be 16-byte aligned");
     if (m->rows == 0) return QWH_OK;
     if (m->format == QWH_FORMAT_Q4) {
+        if (gemv_q4_fused_supported(m->rows, m->cols)) {
+            // One kernel: each wavefront encodes its own activations.
+            GemvInput in;
+            in.mode = GemvInput::F32;
+            in.x = x_dev;
+            return check_hip(ctx, launch_gemv_q4_src(ctx->stream, ctx->cus, in, *m, tokens, out_dev, nullptr), "gemv q4");
+        }
         QWH_TRY(ensure_workspace(ctx, ctx->digits, q4_digit_bytes(tokens, cols)));
         QWH_TRY(check_hip(ctx, launch_prep_q4(ctx->stream, x_dev, tokens, cols, ctx->digits.ptr), "prep q4"));
         return check_hip(ctx, launch_gemv_q4(ctx->stream, ctx->cus, ctx->digits.ptr, *m, tokens, out_dev, nullptr), "gemv q4");

@@ -85,7 +85,21 @@ hipError_t launch_quantize_rows(hipStream_t s, int format, const float *values, 
 size_t q4_digit_bytes(uint32_t tokens, uint32_t cols);
 hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32_t cols,
                           void *digits);
-// y[t][n] (+)= W x over the prepared digit planes; residual may alias out.
+// The activations a q4 GEMV reads: prepared digit planes, or f32 values the
+// kernel encodes itself -- as they are, after RMSNorm with `norm` / `eps`,
+// or as silu(gate) * up of a tokens x 2K gate | up buffer.
+struct GemvInput {
+    enum Mode { Digits = 0, F32 = 1, RmsNorm = 2, Silu = 3 } mode = Digits;
+    const void *digits = nullptr;
+    const float *x = nullptr;
+    const float *norm = nullptr;
+    float eps = 0.0f;
+};
+// True when a q4 matrix of this shape has a kernel for the f32 input forms.
+bool gemv_q4_fused_supported(uint32_t rows, uint32_t cols);
+// y[t][n] (+)= W x; residual may alias out.
+hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const Matrix &w,
+                              uint32_t tokens, float *out, const float *residual);
 hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
 hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w,

@@ -331,6 +331,7 @@ struct qwh_decoder {
     std::vector<void *> allocations;
     hipGraphExec_t graph[2] = {nullptr, nullptr};
     bool use_graph = true;
+    bool fused = true;  // every GEMV forms its own activations (no norm / prep kernels)
 };
 
 namespace qwh {
@@ -377,12 +378,33 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         return reinterpret_cast<float *>(words + (size_t)B * (cols / 32) * dev::kChunkWords);
     };
     hipError_t err = hipSuccess;
+    // W * f(x) for one of the decoder's activation forms: in one kernel when
+    // the GEMV forms them itself, else through a digit-plane pass.
+    auto gemv = [&](GemvInput::Mode mode, const float *x, const float *norm, const Matrix &w, float *out,
+                    const float *residual) -> hipError_t {
+        if (d->fused) {
+            GemvInput in;
+            in.mode = mode;
+            in.x = x;
+            in.norm = norm;
+            in.eps = c.eps;
+            return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
+        }
+        if (mode == GemvInput::RmsNorm) {
+            rmsnorm_digits_kernel<<<B, 256, 0, s>>>(x, norm, w.cols, c.eps, words, mult_of(w.cols));
+        } else if (mode == GemvInput::Silu) {
+            silu_digits_kernel<<<B, 256, 0, s>>>(x, w.cols, words, mult_of(w.cols));
+        } else {
+            const hipError_t e = launch_prep_q4(s, x, B, w.cols, words);
+            if (e != hipSuccess) return e;
+        }
+        return launch_gemv_q4(s, ctx->cus, words, w, B, out, residual);
+    };
     embed_q4_kernel<<<B, 256, 0, s>>>(d->tokens_dev, reinterpret_cast<const uint16_t *>(d->embed.scales),
                                       d->embed.data, c.hidden, d->hidden);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
-        rmsnorm_digits_kernel<<<B, 256, 0, s>>>(d->hidden, L.attn_norm, c.hidden, c.eps, words, mult_of(c.hidden));
-        err = launch_gemv_q4(s, ctx->cus, words, L.qkv, B, d->qkv, nullptr);
+        err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr);
         if (err != hipSuccess) break;
         QkArgs qa{};
         qa.qkv = d->qkv;
@@ -421,20 +443,15 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         aa.code_stride = d->seq_stride;
         err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch);
         if (err != hipSuccess) break;
-        err = launch_prep_q4(s, d->attn, B, d->qw, words);
+        err = gemv(GemvInput::F32, d->attn, nullptr, L.o, d->hidden, d->hidden);
         if (err != hipSuccess) break;
-        err = launch_gemv_q4(s, ctx->cus, words, L.o, B, d->hidden, d->hidden);
+        err = gemv(GemvInput::RmsNorm, d->hidden, L.ffn_norm, L.gu, d->gu, nullptr);
         if (err != hipSuccess) break;
-        rmsnorm_digits_kernel<<<B, 256, 0, s>>>(d->hidden, L.ffn_norm, c.hidden, c.eps, words, mult_of(c.hidden));
-        err = launch_gemv_q4(s, ctx->cus, words, L.gu, B, d->gu, nullptr);
-        if (err != hipSuccess) break;
-        silu_digits_kernel<<<B, 256, 0, s>>>(d->gu, c.ffn, words, mult_of(c.ffn));
-        err = launch_gemv_q4(s, ctx->cus, words, L.down, B, d->hidden, d->hidden);
+        err = gemv(GemvInput::Silu, d->gu, nullptr, L.down, d->hidden, d->hidden);
     }
     if (err == hipSuccess) {
         if (want_logits) {
-            rmsnorm_digits_kernel<<<B, 256, 0, s>>>(d->hidden, d->final_norm, c.hidden, c.eps, words, mult_of(c.hidden));
-            err = launch_gemv_q4(s, ctx->cus, words, d->lm_head, B, d->logits, nullptr);
+            err = gemv(GemvInput::RmsNorm, d->hidden, d->final_norm, d->lm_head, d->logits, nullptr);
             if (err == hipSuccess) {
                 argmax_partial_kernel<<<dim3(d->arg_parts, B), 256, 0, s>>>(d->logits, c.vocab, d->arg_per_block,
                                                                              d->arg_v, d->arg_i);
@@ -557,6 +574,11 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     d->qw = c.heads * c.head_dim;
     d->kvw = c.kv_heads * c.head_dim;
     d->use_graph = getenv("QWH_NO_GRAPH") == nullptr;
+    // QWH_DECODER_UNFUSED forces the separate norm / prep kernels (for tests).
+    d->fused = getenv("QWH_DECODER_UNFUSED") == nullptr &&
+               gemv_q4_fused_supported(d->qw + 2 * d->kvw, c.hidden) && gemv_q4_fused_supported(c.hidden, d->qw) &&
+               gemv_q4_fused_supported(2 * c.ffn, c.hidden) && gemv_q4_fused_supported(c.hidden, c.ffn) &&
+               gemv_q4_fused_supported(c.vocab, c.hidden);
     auto cleanup = [&](int32_t st) {
         qwh_decoder_destroy(d);
         return st;

@@ -87,20 +87,47 @@ constexpr int kDigitPlanes = 6;
 constexpr int kChunk = 32;                       // activations per chunk
 constexpr int kChunkWords = kDigitPlanes * 4;    // u32 per chunk
 
+// Transposes an 8 x 8 matrix of nibbles held as 8 words (row k = word k,
+// column j = nibble j): afterwards nibble k of w[j] is what nibble j of w[k]
+// was. Three rounds swap the off-diagonal blocks of 16-bit, 8-bit and 4-bit
+// width.
+__device__ __forceinline__ void transpose_nibbles8(uint32_t (&w)[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t a = w[k], b = w[k + 4];
+        w[k] = (a & 0x0000ffffu) | (b << 16);
+        w[k + 4] = (a >> 16) | (b & 0xffff0000u);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k += (k & 1) ? 3 : 1) {  // k = 0, 1, 4, 5
+        const uint32_t a = w[k], b = w[k + 2];
+        w[k] = (a & 0x00ff00ffu) | ((b & 0x00ff00ffu) << 8);
+        w[k + 2] = ((a >> 8) & 0x00ff00ffu) | (b & 0xff00ff00u);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+        const uint32_t a = w[k], b = w[k + 1];
+        w[k] = (a & 0x0f0f0f0fu) | ((b & 0x0f0f0f0fu) << 4);
+        w[k + 1] = ((a >> 4) & 0x0f0f0f0fu) | (b & 0xf0f0f0f0u);
+    }
+}
+
+// Signed hex digits of x_int in nibbles 0..5: adding 0x888888 makes every
+// digit d + 8 (no carries), and XOR 0x888888 turns d + 8 into d mod 16.
+__device__ __forceinline__ uint32_t digit_word(float v, float up) {
+    return (uint32_t)((int)__builtin_rintf(v * up) + 0x888888) ^ 0x888888u;
+}
+
 // Encodes 8 activations (this thread's dword column q of its chunk) given the
 // chunk exponent e. Writes plane j of this column to planes[j].
 __device__ __forceinline__ void encode_digits8(const float v[8], int e, uint32_t planes[6]) {
     const float up = __builtin_ldexpf(1.0f, 22 - e);
-    uint32_t u[8];
+    uint32_t w[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) u[k] = (uint32_t)((int)__builtin_rintf(v[k] * up) + 0x888888);
+    for (int k = 0; k < 8; ++k) w[k] = digit_word(v[k], up);
+    transpose_nibbles8(w);
 #pragma unroll
-    for (int j = 0; j < 6; ++j) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) w |= (((u[k] >> (4 * j)) & 0xfu) ^ 0x8u) << (4 * k);
-        planes[j] = w;
-    }
+    for (int j = 0; j < 6; ++j) planes[j] = w[j];
 }
 
 // Exponent e with |x| <= 2^e for the chunk maximum `amax` (clamped so that
@@ -110,6 +137,26 @@ __device__ __forceinline__ int chunk_exponent(float amax) {
     int e;
     (void)__builtin_frexpf(amax, &e);  // amax = f 2^e, f in [0.5, 1)
     return e < -100 ? -100 : e;
+}
+
+// Encodes a whole chunk of 32 activations held by one lane: D[j * 4 + q] is
+// digit plane j of activations 8q .. 8q+7, m the chunk's multiplier.
+__device__ __forceinline__ void encode_chunk32(const float (&v)[32], uint32_t (&D)[kChunkWords], float &m) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    const int e = chunk_exponent(amax);
+    const float up = __builtin_ldexpf(1.0f, 22 - e);
+    m = __builtin_ldexpf(1.0f, e - 22);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w[k] = digit_word(v[q * 8 + k], up);
+        transpose_nibbles8(w);
+#pragma unroll
+        for (int j = 0; j < 6; ++j) D[j * 4 + q] = w[j];
+    }
 }
 
 }  // namespace dev

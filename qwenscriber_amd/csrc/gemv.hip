@@ -5,23 +5,33 @@
 // row's codes are streamed once from HBM with 128-bit loads and multiplied in
 // registers without ever forming a dequantized weight:
 //
-//   q4: the activations are first written as signed hex digit planes (see
-//       device.h); each 16-byte load of codes holds 32 weights, XOR 0x8 turns
-//       every biased nibble u into the signed code u - 8, and six
-//       v_dot8_i32_i4 chains per dword give exact integer dot products
-//       against the six digit planes. The integers are combined in f32 and
-//       scaled by the group's f16 scale times the chunk's power-of-two
-//       activation multiplier.
+//   q4: the activations are written as signed hex digit planes (device.h);
+//       each 16-byte load of codes holds 32 weights, XOR 0x8 turns every
+//       biased nibble u into the signed code u - 8, and a Horner chain of
+//       v_dot8_i32_i4 over the six digit planes gives the exact integer dot
+//       product, converted once to f32 and scaled by the group's f16 scale
+//       times the chunk's power-of-two activation multiplier.
 //   q8: each 16-byte load holds 16 codes, converted to f32 (exact) and
 //       multiplied with f32 activations.
 //
-// Lane mapping: a wavefront owns RG consecutive rows (a "row group") at a
-// time, and lane l always handles the same 16-byte column slices of those
-// rows (slots s = 0..S-1 of the row group's flat slice list), so its
-// activation operands stay in registers for the whole kernel while the wave
-// walks row groups. U row groups are loaded per iteration to keep several
-// 128-bit loads in flight per lane; the U*RG row sums are then reduced with
-// one transposed butterfly across the wavefront.
+// Lane mapping: a row of K codes is T = K/32 (q4) or K/16 (q8) 16-byte
+// slices. L = gcd(T, 64) lanes share a row, so a wavefront covers RG = 64/L
+// consecutive rows (a "row group") and each lane always handles the same S =
+// T/L slices of its row: its activation operands stay in registers for the
+// whole kernel while the wave walks row groups. A wavefront takes a
+// contiguous range of units of U row groups (the grid holds no more blocks
+// than can be resident), issues the next unit's 128-bit loads before it
+// multiplies the current one, and reduces the U row sums of each row with one
+// transposed butterfly over the row's L lanes.
+//
+// The q4 kernel takes its activations in one of four forms: prepared digit
+// planes, or f32 values that each wavefront encodes itself -- as they are,
+// after RMSNorm (kernels.zig:274-300, decoder.zig:165-172: the statistics of
+// the row are reduced over the lanes that hold it), or as siluMul of a
+// gate | up pair (kernels.zig:233-239). The last three let the decoder step
+// feed a GEMV straight from the previous kernel's f32 output.
+#include <cstdlib>
+
 #include "common.h"
 #include "device.h"
 
@@ -38,6 +48,12 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// f16 scale `index` of a plane below 4 GiB, addressed with a 32-bit byte
+// offset so the load uses the plane's scalar base.
+__device__ __forceinline__ uint16_t load_scale(const uint16_t *plane, uint32_t index) {
+    return *reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(plane) + index * 2u);
+}
+
 template <int V>
 struct Log2 {
     static constexpr int value = 1 + Log2<V / 2>::value;
@@ -47,29 +63,59 @@ struct Log2<1> {
     static constexpr int value = 0;
 };
 
-// Sums acc[0..V) over the 64 lanes. Afterwards lane l holds the total of
-// index (l >> (6 - log2 V)) in acc[0].
-template <int V>
-__device__ __forceinline__ void butterfly_reduce(float (&acc)[V], int lane) {
-    constexpr int log_v = Log2<V>::value;
-#pragma unroll
-    for (int step = 0; step < log_v; ++step) {
-        const int width = V >> step;
-        const int mask = 32 >> step;
-        const bool upper = (lane & mask) != 0;
-#pragma unroll
-        for (int i = 0; i < width / 2; ++i) {
-            const float send = upper ? acc[i] : acc[i + width / 2];
-            const float keep = upper ? acc[i + width / 2] : acc[i];
-            acc[i] = keep + __shfl_xor(send, mask, kWave);
-        }
+// One exchange step of the transposed reduction: the lanes with `mask` set
+// keep b and send a, the others keep a and send b; returns keep + received.
+__device__ __forceinline__ float exchange(float a, float b, bool upper, int mask) {
+    const float send = upper ? a : b;
+    const float keep = upper ? b : a;
+    return keep + __shfl_xor(send, mask, kWave);
+}
+
+// Sums acc[0..U) (U <= 8) over the L lanes of each row (lanes l and l ^ m
+// with m < L share a row). Returns, in every lane, the total of value
+// ((l % L) >> (log2 L - log2 U)) of its row.
+template <int U, int L>
+__device__ __forceinline__ float reduce_rows(const float (&acc)[U], int lane) {
+    static_assert(U == 1 || U == 2 || U == 4 || U == 8, "U must be 1, 2, 4 or 8");
+    static_assert(U <= L, "more values than lanes per row");
+    constexpr int log_u = Log2<U>::value;
+    float v;
+    if constexpr (U == 1) {
+        v = acc[0];
+    } else if constexpr (U == 2) {
+        v = exchange(acc[0], acc[1], (lane & (L / 2)) != 0, L / 2);
+    } else if constexpr (U == 4) {
+        const bool up1 = (lane & (L / 2)) != 0;
+        const float b0 = exchange(acc[0], acc[2], up1, L / 2);
+        const float b1 = exchange(acc[1], acc[3], up1, L / 2);
+        v = exchange(b0, b1, (lane & (L / 4)) != 0, L / 4);
+    } else {
+        const bool up1 = (lane & (L / 2)) != 0;
+        const bool up2 = (lane & (L / 4)) != 0;
+        const float b0 = exchange(acc[0], acc[4], up1, L / 2);
+        const float b1 = exchange(acc[1], acc[5], up1, L / 2);
+        const float b2 = exchange(acc[2], acc[6], up1, L / 2);
+        const float b3 = exchange(acc[3], acc[7], up1, L / 2);
+        const float c0 = exchange(b0, b2, up2, L / 4);
+        const float c1 = exchange(b1, b3, up2, L / 4);
+        v = exchange(c0, c1, (lane & (L / 8)) != 0, L / 8);
     }
 #pragma unroll
-    for (int mask = 32 >> log_v; mask >= 1; mask >>= 1) acc[0] += __shfl_xor(acc[0], mask, kWave);
+    for (int mask = (L / 2) >> log_u; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, kWave);
+    return v;
+}
+
+// Sum of v over the L lanes of a row.
+template <int L>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+    for (int mask = L / 2; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, kWave);
+    return v;
 }
 
 // ---------------------------------------------------------------------------
-// Digit planes of the activations: one thread per 8 consecutive values, four
+// Digit planes of the activations as a separate pass (for the shapes the
+// fused kernels do not cover): one thread per 8 consecutive values, four
 // threads per 32-value chunk.
 // Layout: words[(t * T + c) * 24 + plane * 4 + q], mult[t * T + c].
 // ---------------------------------------------------------------------------
@@ -105,33 +151,37 @@ __global__ __launch_bounds__(256) void prep_q4_kernel(const float *x, uint32_t t
     }
 }
 
-// Exact integer dot products of one 16-byte slice of q4 codes (32 weights)
-// against the six digit planes of its activations, combined in f32:
-// returns sum_k (u_k - 8) * x_int_k with one rounding.
-__device__ __forceinline__ float q4_slice_dot(const uint4 codes, const uint32_t (&d)[24]) {
+// Exact integer dot product of one 16-byte slice of q4 codes (32 weights)
+// with its activations' digit planes: sum_k (u_k - 8) * x_int_k, evaluated
+// as a Horner chain over the six digit planes (plane 5 first), each plane a
+// chain of four v_dot8_i32_i4. Every partial value is bounded by
+// 32 * 8 * 2^22 = 2^30, so the int32 result is exact.
+__device__ __forceinline__ int q4_slice_dot(const uint4 codes, const uint32_t (&d)[24]) {
     const int c0 = (int)(codes.x ^ 0x88888888u);
     const int c1 = (int)(codes.y ^ 0x88888888u);
     const int c2 = (int)(codes.z ^ 0x88888888u);
     const int c3 = (int)(codes.w ^ 0x88888888u);
-    int I[6];
+    int acc = 0;
 #pragma unroll
-    for (int j = 0; j < 6; ++j) {
-        int acc = __builtin_amdgcn_sdot8(c0, (int)d[j * 4 + 0], 0, false);
+    for (int j = 5; j >= 0; --j) {
+        if (j != 5) acc = acc * 16;
+        acc = __builtin_amdgcn_sdot8(c0, (int)d[j * 4 + 0], acc, false);
         acc = __builtin_amdgcn_sdot8(c1, (int)d[j * 4 + 1], acc, false);
         acc = __builtin_amdgcn_sdot8(c2, (int)d[j * 4 + 2], acc, false);
         acc = __builtin_amdgcn_sdot8(c3, (int)d[j * 4 + 3], acc, false);
-        I[j] = acc;
     }
-    // |I_j| <= 32 * 8 * 8, so both three-digit partial sums are exact in i32
-    // and in f32.
-    const int hi = (I[5] * 16 + I[4]) * 16 + I[3];
-    const int lo = (I[2] * 16 + I[1]) * 16 + I[0];
-    return fmaf((float)hi, 4096.0f, (float)lo);
+    return acc;
 }
 
+// Forms of the q4 GEMV's activations.
+enum class Src : int { Digits = 0, F32 = 1, RmsNorm = 2, Silu = 3 };
+
 struct GemvQ4Args {
-    const uint32_t *words;  // digit planes, per token T * 24 words
-    const float *mult;      // per token T multipliers
+    const uint32_t *words;  // Digits: planes, per token T * 24 words
+    const float *mult;      // Digits: per token T multipliers
+    const float *x;         // F32 / RmsNorm: tokens x K; Silu: tokens x 2K (gate | up)
+    const float *norm;      // RmsNorm: K weights
+    float eps;              // RmsNorm epsilon
     const uint16_t *scales; // N * K/64
     const uint8_t *data;    // N * K/2
     float *out;             // tokens x N
@@ -139,83 +189,187 @@ struct GemvQ4Args {
     uint32_t n, k, t, row_groups;
 };
 
-template <int S, int RG, int U>
-__global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
-    constexpr int V = U * RG;
-    const int lane = threadIdx.x & 63;
-    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
-    const uint32_t token = blockIdx.y;
-    const uint32_t T = a.t;
-    const uint32_t gpr = a.k >> 6;
-    const size_t row_bytes = a.k >> 1;
+// One 16-byte slice of codes and its group scale.
+struct Slice {
+    uint4 codes;
+    uint16_t scale;
+};
 
-    int rrow[S];
-    uint32_t chunk[S];
-    uint32_t D[S][24];
-    float m[S];
+__device__ __forceinline__ void load32(const float *p, float (&v)[32]) {
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-        const uint32_t f = (uint32_t)lane + 64u * s;
-        rrow[s] = (int)(f / T);
-        chunk[s] = f - (uint32_t)rrow[s] * T;
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.words + ((size_t)token * T + chunk[s]) * 24);
-#pragma unroll
-        for (int j = 0; j < 6; ++j) {
-            const uint4 w = src[j];
-            D[s][j * 4 + 0] = w.x;
-            D[s][j * 4 + 1] = w.y;
-            D[s][j * 4 + 2] = w.z;
-            D[s][j * 4 + 3] = w.w;
-        }
-        m[s] = a.mult[(size_t)token * T + chunk[s]];
+    for (int i = 0; i < 8; ++i) {
+        const float4 f = reinterpret_cast<const float4 *>(p)[i];
+        v[i * 4 + 0] = f.x; v[i * 4 + 1] = f.y; v[i * 4 + 2] = f.z; v[i * 4 + 3] = f.w;
     }
+}
 
+// This lane's activation operands for slices c = li + s * L.
+template <int S, int L, Src M>
+__device__ __forceinline__ void lane_activations(const GemvQ4Args &a, int li, uint32_t token,
+                                                 uint32_t (&D)[S][24], float (&m)[S]) {
+    const uint32_t T = a.t;
+    if constexpr (M == Src::Digits) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const uint32_t c = li + s * L;
+            const uint4 *src = reinterpret_cast<const uint4 *>(a.words + ((size_t)token * T + c) * 24);
+#pragma unroll
+            for (int j = 0; j < 6; ++j) {
+                const uint4 w = src[j];
+                D[s][j * 4 + 0] = w.x;
+                D[s][j * 4 + 1] = w.y;
+                D[s][j * 4 + 2] = w.z;
+                D[s][j * 4 + 3] = w.w;
+            }
+            m[s] = a.mult[(size_t)token * T + c];
+        }
+    } else {
+        const float *row = a.x + (size_t)token * a.k * (M == Src::Silu ? 2 : 1);
+        float v[S][32];
+#pragma unroll
+        for (int s = 0; s < S; ++s) load32(row + (size_t)(li + s * L) * 32, v[s]);
+        if constexpr (M == Src::Silu) {
+            // silu(g) * u with silu(g) = g / (1 + exp(-g)) (math.zig:69-71).
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                float u[32];
+                load32(row + a.k + (size_t)(li + s * L) * 32, u);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const float g = v[s][i];
+                    v[s][i] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u[i]);
+                }
+            }
+        }
+        if constexpr (M == Src::RmsNorm) {
+            // math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w. The row's
+            // sum of squares is reduced over the L lanes that hold it.
+            float ss = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < 32; ++i) ss = __fadd_rn(ss, __fmul_rn(v[s][i], v[s][i]));
+            ss = row_sum<L>(ss);
+            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)a.k), a.eps)));
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                float w[32];
+                load32(a.norm + (size_t)(li + s * L) * 32, w);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[s][i] = __fmul_rn(__fmul_rn(v[s][i], inv), w[i]);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) dev::encode_chunk32(v[s], D[s], m[s]);
+    }
+}
+
+// The wavefront owns a contiguous range of units (U row groups of RG = 64/L
+// rows each). Lane l works on row l / L of each row group and on slices
+// (l % L) + s * L, s < S, of that row.
+template <int S, int L, int U, Src M>
+__global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
+    constexpr int RG = 64 / L;
+    constexpr int log_l = Log2<L>::value;
+    constexpr int log_u = Log2<U>::value;
+    const int lane = threadIdx.x & 63;
+    const int rr = lane >> log_l;
+    const int li = lane & (L - 1);
+    // Wave-uniform (scalar) indices: the unit loop and the full/tail choice
+    // branch on scalars instead of masking lanes.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t token = blockIdx.y;
+    const uint32_t gpr = a.k >> 6;
+    // The launcher picks this kernel only when the data plane is below 4 GiB
+    // and units * waves fits 32 bits, so 32-bit arithmetic suffices.
+    const uint32_t row_bytes = a.k >> 1;
     const uint32_t units = (a.row_groups + U - 1) / U;
+    const uint32_t u0 = wave * units / nwaves;
+    const uint32_t u1 = (wave + 1) * units / nwaves;
+    const uint32_t full_units = a.n / (U * RG);
+    const uint32_t f1 = u1 < full_units ? u1 : full_units;
     float *out = a.out + (size_t)token * a.n;
     const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
-    for (uint32_t unit = wave; unit < units; unit += nwaves) {
-        uint4 code[U][S];
-        uint16_t sc[U][S];
+
+    // Unmasked loads of a unit whose rows all exist.
+    auto load = [&](Slice (&dst)[U][S], uint32_t unit) {
+        const uint32_t row0 = unit * (U * RG) + rr;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t rg = unit * U + u;
-#pragma unroll
-            for (int s = 0; s < S; ++s) {
-                const uint32_t row = rg * RG + rrow[s];
-                if (rg < a.row_groups && row < a.n) {
-                    code[u][s] = load_stream16(a.data + row * row_bytes + (size_t)chunk[s] * 16);
-                    sc[u][s] = a.scales[(size_t)row * gpr + (chunk[s] >> 1)];
-                } else {
-                    code[u][s] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-                    sc[u][s] = 0;
-                }
-            }
-        }
-        float acc[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const float val = q4_slice_dot(code[u][s], D[s]) * (dev::f16_bits_to_f32(sc[u][s]) * m[s]);
-                if (RG == 1) {
-                    acc[u] += val;
-                } else {
+                const uint32_t row = row0 + u * RG;
+                const uint32_t c = li + s * L;
+                dst[u][s].codes = load_stream16(a.data + (row * row_bytes + c * 16));
+                dst[u][s].scale = load_scale(a.scales, row * gpr + (c >> 1));
+            }
+    };
+    // The last, partial unit: rows past the end contribute nothing.
+    auto load_tail = [&](Slice (&dst)[U][S], uint32_t unit) {
+        const uint32_t row0 = unit * (U * RG) + rr;
 #pragma unroll
-                    for (int r = 0; r < RG; ++r) acc[u * RG + r] += (rrow[s] == r) ? val : 0.0f;
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const uint32_t row = row0 + u * RG;
+                const uint32_t c = li + s * L;
+                if (row < a.n) {
+                    dst[u][s].codes = load_stream16(a.data + (row * row_bytes + c * 16));
+                    dst[u][s].scale = load_scale(a.scales, row * gpr + (c >> 1));
+                } else {
+                    dst[u][s].codes = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+                    dst[u][s].scale = 0;
                 }
             }
+    };
+
+    Slice A[U][S], B[U][S];
+    // The first unit's loads go out before the activations are formed, so
+    // their latency covers that work.
+    if (u0 < f1) load(A, u0);
+
+    uint32_t D[S][24];
+    float m[S];
+    lane_activations<S, L, M>(a, li, token, D, m);
+
+    auto process = [&](const Slice (&src)[U][S], uint32_t unit) {
+        float acc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const float part = (float)q4_slice_dot(src[u][s].codes, D[s]) *
+                                   (dev::f16_bits_to_f32(src[u][s].scale) * m[s]);
+                acc[u] = s == 0 ? part : acc[u] + part;
+            }
         }
-        butterfly_reduce<V>(acc, lane);
-        constexpr int lanes_per_value = 64 / V;
-        if ((lane & (lanes_per_value - 1)) == 0) {
-            const int idx = lane / lanes_per_value;
-            const uint32_t rg = unit * U + idx / RG;
-            const uint32_t row = rg * RG + idx % RG;
-            if (rg < a.row_groups && row < a.n) out[row] = (residual ? residual[row] : 0.0f) + acc[0];
+        const float total = reduce_rows<U, L>(acc, lane);
+        if ((li & ((L >> log_u) - 1)) == 0) {
+            const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+            if (row < a.n) out[row] = (residual ? residual[row] : 0.0f) + total;
         }
+    };
+
+    // Full units, software pipelined: the loads of the next unit are in
+    // flight while the current one is multiplied. The prefetch index is
+    // clamped rather than branched on, so the body is straight-line code and
+    // the wait before each multiply covers only that unit's loads.
+    if (u0 < f1) {
+        const uint32_t last = f1 - 1;
+        uint32_t unit = u0;
+        for (; unit + 1 < f1; unit += 2) {
+            load(B, unit + 1);
+            process(A, unit);
+            load(A, unit + 2 < last ? unit + 2 : last);
+            process(B, unit + 1);
+        }
+        if (unit < f1) process(A, unit);
+    }
+    // The partial unit, if this wave owns it.
+    for (uint32_t unit = u0 > full_units ? u0 : full_units; unit < u1; ++unit) {
+        load_tail(B, unit);
+        process(B, unit);
     }
 }
 
@@ -243,7 +397,7 @@ __global__ __launch_bounds__(256) void gemv_q4_generic_kernel(const GemvQ4Args a
                 d[j * 4 + 0] = w.x; d[j * 4 + 1] = w.y; d[j * 4 + 2] = w.z; d[j * 4 + 3] = w.w;
             }
             const float mult = a.mult[(size_t)token * T + c];
-            acc += q4_slice_dot(code, d) * (dev::f16_bits_to_f32(a.scales[(size_t)row * gpr + (c >> 1)]) * mult);
+            acc += (float)q4_slice_dot(code, d) * (dev::f16_bits_to_f32(a.scales[(size_t)row * gpr + (c >> 1)]) * mult);
         }
         acc = dev::wave_sum(acc);
         if (lane == 0) out[row] = (residual ? residual[row] : 0.0f) + acc;
@@ -279,24 +433,23 @@ __device__ __forceinline__ float q8_slice_dot(const uint4 codes, const float (&x
     return acc;
 }
 
-template <int S, int RG, int U>
+template <int S, int L, int U>
 __global__ __launch_bounds__(256) void gemv_q8_kernel(const GemvQ8Args a) {
-    constexpr int V = U * RG;
+    constexpr int RG = 64 / L;
+    constexpr int log_l = Log2<L>::value;
+    constexpr int log_u = Log2<U>::value;
     const int lane = threadIdx.x & 63;
-    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int rr = lane >> log_l;
+    const int li = lane & (L - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
     const uint32_t token = blockIdx.y;
-    const uint32_t T = a.t;
     const uint32_t gpr = a.k >> 6;
-    int rrow[S];
-    uint32_t slice[S];
     float X[S][16];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        const uint32_t f = (uint32_t)lane + 64u * s;
-        rrow[s] = (int)(f / T);
-        slice[s] = f - (uint32_t)rrow[s] * T;
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k + slice[s] * 16);
+        const uint32_t c = li + s * L;
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k + c * 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 v = src[i];
@@ -304,49 +457,40 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(const GemvQ8Args a) {
         }
     }
     const uint32_t units = (a.row_groups + U - 1) / U;
+    const uint32_t u0 = wave * units / nwaves;
+    const uint32_t u1 = (wave + 1) * units / nwaves;
     float *out = a.out + (size_t)token * a.n;
     const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
-    for (uint32_t unit = wave; unit < units; unit += nwaves) {
-        uint4 code[U][S];
-        uint16_t sc[U][S];
+    for (uint32_t unit = u0; unit < u1; ++unit) {
+        Slice sl[U][S];
+        const uint32_t row0 = unit * (U * RG) + rr;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t rg = unit * U + u;
+        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const uint32_t row = rg * RG + rrow[s];
-                if (rg < a.row_groups && row < a.n) {
-                    code[u][s] = load_stream16(a.data + (size_t)row * a.k + (size_t)slice[s] * 16);
-                    sc[u][s] = a.scales[(size_t)row * gpr + (slice[s] >> 2)];
+                const uint32_t row = row0 + u * RG;
+                const uint32_t c = li + s * L;
+                if (row < a.n) {
+                    sl[u][s].codes = load_stream16(a.data + (row * a.k + c * 16));
+                    sl[u][s].scale = load_scale(a.scales, row * gpr + (c >> 2));
                 } else {
-                    code[u][s] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-                    sc[u][s] = 0;
+                    sl[u][s].codes = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+                    sl[u][s].scale = 0;
                 }
             }
-        }
-        float acc[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+        float acc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const float val = q8_slice_dot(code[u][s], X[s]) * dev::f16_bits_to_f32(sc[u][s]);
-                if (RG == 1) {
-                    acc[u] += val;
-                } else {
-#pragma unroll
-                    for (int r = 0; r < RG; ++r) acc[u * RG + r] += (rrow[s] == r) ? val : 0.0f;
-                }
+                const float part = q8_slice_dot(sl[u][s].codes, X[s]) * dev::f16_bits_to_f32(sl[u][s].scale);
+                acc[u] = s == 0 ? part : acc[u] + part;
             }
         }
-        butterfly_reduce<V>(acc, lane);
-        constexpr int lanes_per_value = 64 / V;
-        if ((lane & (lanes_per_value - 1)) == 0) {
-            const int idx = lane / lanes_per_value;
-            const uint32_t rg = unit * U + idx / RG;
-            const uint32_t row = rg * RG + idx % RG;
-            if (rg < a.row_groups && row < a.n) out[row] = (residual ? residual[row] : 0.0f) + acc[0];
+        const float total = reduce_rows<U, L>(acc, lane);
+        if ((li & ((L >> log_u) - 1)) == 0) {
+            const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+            if (row < a.n) out[row] = (residual ? residual[row] : 0.0f) + total;
         }
     }
 }
@@ -386,29 +530,99 @@ uint32_t gcd_u32(uint32_t a, uint32_t b) {
     return a;
 }
 
-// Waves to launch: enough to cover every unit, capped at a few per SIMD.
-unsigned grid_blocks(uint32_t units, int cus) {
-    const uint32_t waves = units;
-    uint32_t blocks = (waves + 3) / 4;
-    const uint32_t cap = (uint32_t)(cus > 0 ? cus : 256) * 8;
-    if (blocks > cap) blocks = cap;
+// At most this many blocks (of four wavefronts) per compute unit: fewer
+// concurrent streams keep HBM pages open. QWH_GEMV_BLOCKS_PER_CU overrides it
+// for tuning.
+constexpr int kBlocksPerCu = 4;
+// Row groups per unit for the one-slice q4 kernels (the common shapes).
+constexpr int kUnitRows = 4;
+
+int blocks_per_cu_cap() {
+    static int cap = 0;
+    if (cap == 0) {
+        cap = kBlocksPerCu;
+        if (const char *env = getenv("QWH_GEMV_BLOCKS_PER_CU")) {
+            const int v = atoi(env);
+            if (v > 0) cap = v;
+        }
+    }
+    return cap;
+}
+
+// Blocks to launch: every unit covered, no more blocks than can be resident
+// at once (so each wave walks a contiguous range of units).
+template <typename Kernel>
+unsigned grid_blocks(Kernel kernel, uint32_t units, int cus) {
+    static int resident = 0;
+    if (resident == 0) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0) {
+            (void)hipGetLastError();
+            per_cu = 4;
+        }
+        const int cap = blocks_per_cu_cap();
+        resident = per_cu < cap ? per_cu : cap;
+    }
+    uint32_t blocks = (units + 3) / 4;
+    uint32_t limit = (uint32_t)(cus > 0 ? cus : 256) * (uint32_t)resident;
+    // At most 4096 wavefronts: with rows * 4096 < 2^32 (checked by the
+    // launcher) the kernels' wave * units products stay within 32 bits.
+    if (limit > 1024) limit = 1024;
+    if (blocks > limit) blocks = limit;
     if (blocks == 0) blocks = 1;
     return blocks;
 }
 
-#define QWH_GEMV_CASE(KERNEL, S_, RG_, U_)                                                        \
-    if (S == S_ && RG == RG_) {                                                                   \
-        args.row_groups = (args.n + RG_ - 1) / RG_;                                               \
-        const uint32_t units = (args.row_groups + U_ - 1) / U_;                                   \
-        KERNEL<S_, RG_, U_><<<dim3(grid_blocks(units, cus), tokens), 256, 0, s>>>(args);          \
-        return hipGetLastError();                                                                 \
-    }
+template <int S, int L, int U, Src M>
+hipError_t launch_q4(hipStream_t s, int cus, GemvQ4Args args, uint32_t tokens) {
+    args.row_groups = (args.n + (64 / L) - 1) / (64 / L);
+    const uint32_t units = (args.row_groups + U - 1) / U;
+    auto kernel = gemv_q4_kernel<S, L, U, M>;
+    kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);
+    return hipGetLastError();
+}
+
+template <Src M>
+hipError_t dispatch_q4(hipStream_t s, int cus, const GemvQ4Args &args, uint32_t tokens, uint32_t S, uint32_t L,
+                       bool &done) {
+    done = true;
+    if (S == 1 && L == 64) return launch_q4<1, 64, kUnitRows, M>(s, cus, args, tokens);
+    if (S == 1 && L == 32) return launch_q4<1, 32, kUnitRows, M>(s, cus, args, tokens);
+    if (S == 1 && L == 16) return launch_q4<1, 16, kUnitRows, M>(s, cus, args, tokens);
+    if (S == 1 && L == 8) return launch_q4<1, 8, 4, M>(s, cus, args, tokens);
+    if (S == 1 && L == 4) return launch_q4<1, 4, 4, M>(s, cus, args, tokens);
+    if (S == 1 && L == 2) return launch_q4<1, 2, 2, M>(s, cus, args, tokens);
+    if (S == 2 && L == 64) return launch_q4<2, 64, 4, M>(s, cus, args, tokens);
+    if (S == 3 && L == 64) return launch_q4<3, 64, 2, M>(s, cus, args, tokens);
+    if (S == 3 && L == 32) return launch_q4<3, 32, 2, M>(s, cus, args, tokens);
+    if (S == 3 && L == 16) return launch_q4<3, 16, 2, M>(s, cus, args, tokens);
+    if (S == 3 && L == 2) return launch_q4<3, 2, 2, M>(s, cus, args, tokens);
+    done = false;
+    return hipSuccess;
+}
+
+// Shapes with a templated kernel: one, two or three slices per lane, a data
+// plane below 4 GiB and few enough units for 32-bit unit arithmetic.
+bool fused_shape(uint32_t rows, uint32_t cols, uint32_t &S, uint32_t &L) {
+    const uint32_t T = cols / 32;
+    L = gcd_u32(T, 64);
+    S = T / L;
+    const bool small = (uint64_t)rows * (cols / 2) < (1ull << 32) && (uint64_t)rows * 4096ull < (1ull << 32);
+    const bool built = (S == 1 && (L == 64 || L == 32 || L == 16 || L == 8 || L == 4 || L == 2)) ||
+                       (S == 2 && L == 64) || (S == 3 && (L == 64 || L == 32 || L == 16 || L == 2));
+    return small && built;
+}
 
 }  // namespace
 
 size_t q4_digit_bytes(uint32_t tokens, uint32_t cols) {
     const size_t chunks = (size_t)tokens * (cols / 32);
     return chunks * dev::kChunkWords * 4 + chunks * 4 + 256;
+}
+
+bool gemv_q4_fused_supported(uint32_t rows, uint32_t cols) {
+    uint32_t S, L;
+    return fused_shape(rows, cols, S, L);
 }
 
 hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32_t cols, void *digits) {
@@ -420,13 +634,10 @@ hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w, uint32_t tokens,
-                          float *out, const float *residual) {
+hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
+                              float *out, const float *residual) {
     GemvQ4Args args{};
     const uint32_t T = w.cols / 32;
-    const size_t chunks = (size_t)tokens * T;
-    args.words = static_cast<const uint32_t *>(digits);
-    args.mult = reinterpret_cast<const float *>(args.words + chunks * dev::kChunkWords);
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
     args.data = w.data;
     args.out = out;
@@ -434,22 +645,49 @@ hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matr
     args.n = w.rows;
     args.k = w.cols;
     args.t = T;
-    const uint32_t g = gcd_u32(T, 64);
-    const uint32_t RG = 64 / g;
-    const uint32_t S = T / g;
-    QWH_GEMV_CASE(gemv_q4_kernel, 1, 1, 4)
-    QWH_GEMV_CASE(gemv_q4_kernel, 1, 2, 4)
-    QWH_GEMV_CASE(gemv_q4_kernel, 1, 4, 2)
-    QWH_GEMV_CASE(gemv_q4_kernel, 1, 8, 1)
-    QWH_GEMV_CASE(gemv_q4_kernel, 1, 16, 1)
-    QWH_GEMV_CASE(gemv_q4_kernel, 1, 32, 1)
-    QWH_GEMV_CASE(gemv_q4_kernel, 2, 1, 2)
-    QWH_GEMV_CASE(gemv_q4_kernel, 3, 1, 2)
-    QWH_GEMV_CASE(gemv_q4_kernel, 3, 2, 2)
-    QWH_GEMV_CASE(gemv_q4_kernel, 3, 4, 1)
-    gemv_q4_generic_kernel<<<dim3(grid_blocks(w.rows, cus), tokens), 256, 0, s>>>(args);
+    args.x = in.x;
+    args.norm = in.norm;
+    args.eps = in.eps;
+    if (in.mode == GemvInput::Digits) {
+        const size_t chunks = (size_t)tokens * T;
+        args.words = static_cast<const uint32_t *>(in.digits);
+        args.mult = reinterpret_cast<const float *>(args.words + chunks * dev::kChunkWords);
+    }
+    uint32_t S = 0, L = 0;
+    const bool fused = fused_shape(w.rows, w.cols, S, L);
+    bool done = false;
+    hipError_t err = hipSuccess;
+    if (fused) {
+        switch (in.mode) {
+        case GemvInput::Digits: err = dispatch_q4<Src::Digits>(s, cus, args, tokens, S, L, done); break;
+        case GemvInput::F32: err = dispatch_q4<Src::F32>(s, cus, args, tokens, S, L, done); break;
+        case GemvInput::RmsNorm: err = dispatch_q4<Src::RmsNorm>(s, cus, args, tokens, S, L, done); break;
+        case GemvInput::Silu: err = dispatch_q4<Src::Silu>(s, cus, args, tokens, S, L, done); break;
+        }
+    }
+    if (done) return err;
+    if (in.mode != GemvInput::Digits) return hipErrorNotSupported;
+    args.row_groups = w.rows;
+    gemv_q4_generic_kernel<<<dim3(grid_blocks(gemv_q4_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
     return hipGetLastError();
 }
+
+hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w, uint32_t tokens,
+                          float *out, const float *residual) {
+    GemvInput in{};
+    in.mode = GemvInput::Digits;
+    in.digits = digits;
+    return launch_gemv_q4_src(s, cus, in, w, tokens, out, residual);
+}
+
+#define QWH_GEMV8_CASE(S_, L_, U_)                                                                 \
+    if (S == S_ && L == L_ && small_plane) {                                                       \
+        args.row_groups = (args.n + (64 / L_) - 1) / (64 / L_);                                    \
+        const uint32_t units = (args.row_groups + U_ - 1) / U_;                                    \
+        auto kernel = gemv_q8_kernel<S_, L_, U_>;                                                  \
+        kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);                \
+        return hipGetLastError();                                                                  \
+    }
 
 hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w, uint32_t tokens,
                           float *out, const float *residual) {
@@ -463,18 +701,19 @@ hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &
     args.n = w.rows;
     args.k = w.cols;
     args.t = T;
-    const uint32_t g = gcd_u32(T, 64);
-    const uint32_t RG = 64 / g;
-    const uint32_t S = T / g;
-    QWH_GEMV_CASE(gemv_q8_kernel, 1, 1, 4)
-    QWH_GEMV_CASE(gemv_q8_kernel, 1, 2, 4)
-    QWH_GEMV_CASE(gemv_q8_kernel, 1, 4, 2)
-    QWH_GEMV_CASE(gemv_q8_kernel, 1, 8, 1)
-    QWH_GEMV_CASE(gemv_q8_kernel, 1, 16, 1)
-    QWH_GEMV_CASE(gemv_q8_kernel, 2, 1, 2)
-    QWH_GEMV_CASE(gemv_q8_kernel, 3, 1, 2)
-    QWH_GEMV_CASE(gemv_q8_kernel, 3, 2, 2)
-    gemv_q8_generic_kernel<<<dim3(grid_blocks(w.rows, cus), tokens), 256, 0, s>>>(args);
+    const uint32_t L = gcd_u32(T, 64);
+    const uint32_t S = T / L;
+    const bool small_plane = (uint64_t)w.rows * w.cols < (1ull << 32) && (uint64_t)w.rows * 4096ull < (1ull << 32);
+    QWH_GEMV8_CASE(1, 64, 4)
+    QWH_GEMV8_CASE(1, 32, 4)
+    QWH_GEMV8_CASE(1, 16, 4)
+    QWH_GEMV8_CASE(1, 8, 4)
+    QWH_GEMV8_CASE(1, 4, 4)
+    QWH_GEMV8_CASE(2, 64, 2)
+    QWH_GEMV8_CASE(3, 64, 2)
+    QWH_GEMV8_CASE(3, 16, 2)
+    args.row_groups = w.rows;
+    gemv_q8_generic_kernel<<<dim3(grid_blocks(gemv_q8_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
     return hipGetLastError();
 }
 
