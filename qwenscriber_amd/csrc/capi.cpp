@@ -348,6 +348,17 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
     if (((uintptr_t)x_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "x must be 16-byte aligned");
     if (m->rows == 0) return QWH_OK;
     if (m->format == QWH_FORMAT_Q4) {
+        if (tokens >= 2) {
+            // Several tokens: int8 digit planes, then one matrix-core pass
+            // over the weights per 16 tokens.
+            GemvInput in;
+            in.mode = GemvInput::F32;
+            in.x = x_dev;
+            QWH_TRY(ensure_workspace(ctx, ctx->digits, batch_digit_bytes(tokens, cols)));
+            QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
+            return check_hip(ctx, launch_gemv_q4_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr),
+                             "gemv q4 batch");
+        }
         if (gemv_q4_fused_supported(m->rows, m->cols)) {
             // One kernel: each wavefront encodes its own activations.
             GemvInput in;
@@ -460,17 +471,15 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
     if (batch > 1 && ((scale_stride_bytes & 1u) || (code_stride_bytes & 15u)))
         return fail(ctx, QWH_E_INVALID_ARGUMENT, "sequence strides must keep the plane alignment");
     const uint32_t ratio = heads / kv_heads;
-    const bool built = (head_dim == 64 && (ratio == 1 || ratio == 2 || ratio == 4)) ||
-                       (head_dim == 128 && (ratio == 1 || ratio == 2 || ratio == 4 || ratio == 8)) ||
-                       (head_dim == 256 && (ratio == 1 || ratio == 2));
-    if (!built) return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim, ratio);
+    if (!attention_supported(head_dim, ratio)) return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim, ratio);
     AttentionArgs a{};
     a.out = out_dev;
     a.query = query_dev;
-    a.k_scales = k_scales_dev;
-    a.k_codes = k_codes_dev;
-    a.v_scales = v_scales_dev;
-    a.v_codes = v_codes_dev;
+    // The kernel only reads the cache planes in this form.
+    a.k_scales = const_cast<uint8_t *>(k_scales_dev);
+    a.k_codes = const_cast<uint8_t *>(k_codes_dev);
+    a.v_scales = const_cast<uint8_t *>(v_scales_dev);
+    a.v_codes = const_cast<uint8_t *>(v_codes_dev);
     a.cached = cached;
     a.cached_dev = nullptr;
     a.capacity = cached;

@@ -105,6 +105,14 @@ hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matr
 hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
 
+// Small-batch q4 GEMV on the matrix cores (gemv_batch.hip): activations as
+// int8 digit planes per 16-token tile, then one MFMA pass over the weights.
+size_t batch_digit_bytes(uint32_t tokens, uint32_t cols);
+hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols,
+                             void *digits);
+hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
+                                float *out, const float *residual);
+
 // q4 GEMM with bf16 activations (gemm.hip).
 hipError_t launch_gemm_q4_bf16(hipStream_t s, const uint16_t *x, const Matrix &w,
                                uint32_t tokens, float *out);
@@ -112,16 +120,23 @@ hipError_t launch_gemm_q4_bf16(hipStream_t s, const uint16_t *x, const Matrix &w
 // q8 decode attention (attention.hip). `cached` is per sequence when
 // cached_dev is non-null (device array of batch values), else uniform.
 struct AttentionArgs {
-    float *out;
-    const float *query;
-    const uint8_t *k_scales, *k_codes, *v_scales, *v_codes;
-    uint32_t cached;
-    const uint32_t *cached_dev;   // optional: positions; cached = value + cached_bias
-    uint32_t cached_bias;
-    uint32_t capacity;            // upper bound of cached (sizes the grid)
-    uint32_t heads, kv_heads, head_dim, batch;
-    uint64_t scale_stride, code_stride;  // per sequence, bytes
+    float *out = nullptr;
+    const float *query = nullptr;  // head h of sequence b at query + b * query_stride + h * head_dim
+    uint32_t query_stride = 0;     // floats; 0 means heads * head_dim
+    uint8_t *k_scales = nullptr, *k_codes = nullptr, *v_scales = nullptr, *v_codes = nullptr;
+    uint32_t cached = 0;
+    const uint32_t *cached_dev = nullptr;  // optional: positions; cached = value + cached_bias
+    uint32_t cached_bias = 0;
+    uint32_t capacity = 0;         // upper bound of cached (sizes the grid)
+    uint32_t heads = 0, kv_heads = 0, head_dim = 0, batch = 0;
+    uint64_t scale_stride = 0, code_stride = 0;  // per sequence, bytes
+    // Decoder form (q_norm non-null): each query row is the q | k | v
+    // projection of the newest position cached - 1. q and k get per-head
+    // RMSNorm and RoPE at that position; k and v are appended to the cache.
+    const float *q_norm = nullptr, *k_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+    float eps = 0.0f;
 };
+bool attention_supported(uint32_t head_dim, uint32_t ratio);
 size_t attention_scratch_bytes(int cus, const AttentionArgs &a);
 hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArgs &a,
                                       void *scratch);

@@ -6,18 +6,18 @@
 // once into a HIP graph and replays without host work; a greedy loop replays
 // it back to back, the argmax of one step feeding the embedding of the next.
 //
-// Per layer (decoder.zig:164-272):
-//   rmsnorm_digits  rmsNormInto(attention_norm) -> activation digit planes
-//   gemv q4         q | k | v rows fused into one matrix
-//   qk_rope_append  per-head rmsNorm of q and k, ropeInPlace at the position,
-//                   appendCacheRow (q8, bit exact) of k and v
-//   attention       decodeAttentionStepQ8 over position + 1 rows
-//   prep + gemv q4  out projection, residual added in the GEMV epilogue
-//   rmsnorm_digits  rmsNormInto(ffn_norm)
-//   gemv q4         gate | up rows fused
-//   silu_digits     siluMul
-//   gemv q4         down projection, residual added in the epilogue
-// then rmsNormInto(final) -> lm_head GEMV -> argmax (first maximum wins).
+// Per layer (decoder.zig:164-272), five launches:
+//   gemv q4     rmsNormInto(attention_norm) formed in the GEMV prologue;
+//               q | k | v rows fused into one matrix
+//   attention   per-head rmsNorm of q and k, ropeInPlace at the position,
+//               appendCacheRow (q8) of k and v, decodeAttentionStepQ8 over
+//               position + 1 rows
+//   gemv q4     out projection, residual added in the GEMV epilogue
+//   gemv q4     rmsNormInto(ffn_norm) in the prologue; gate | up rows fused
+//   gemv q4     siluMul in the prologue; down projection, residual added
+// then rmsNormInto(final) + lm_head GEMV -> argmax (first maximum wins).
+// Shapes without a fused GEMV kernel (or QWH_DECODER_UNFUSED set) run the
+// norm / SiLU / digit-plane kernels below as separate launches instead.
 #include <cfloat>
 #include <cmath>
 #include <cstring>
@@ -148,77 +148,6 @@ __global__ __launch_bounds__(256) void silu_digits_kernel(const float *gu, uint3
     }
 }
 
-struct QkArgs {
-    const float *qkv;          // batch x (heads + 2 kv_heads) * 128
-    const float *q_norm, *k_norm;
-    const float *rope_cos, *rope_sin;  // [max_positions][64]
-    const uint32_t *pos;
-    float *q_out;              // batch x heads * 128
-    uint8_t *k_scales, *k_codes, *v_scales, *v_codes;  // this layer, sequence 0
-    uint64_t seq_stride;
-    uint32_t heads, kv_heads;
-    float eps;
-};
-
-// decoder.zig:180-216 for head_dim 128: per-head rmsNorm of q and k
-// (kernels.zig:288-300), ropeInPlace with the precomputed tables
-// (kernels.zig:495-527, pair (i, i + 64)), and appendCacheRow(.q8) of k and v
-// (quant.zig:197-288). One wavefront per head row; lane i holds dims i, i+64.
-__global__ __launch_bounds__(64) void qk_rope_append_kernel(const QkArgs a) {
-    constexpr int D = 128;
-    const uint32_t b = blockIdx.x;
-    const uint32_t hh = blockIdx.y;
-    const int lane = threadIdx.x;
-    const uint32_t qw = a.heads * D;
-    const uint32_t kvw = a.kv_heads * D;
-    const float *row = a.qkv + (size_t)b * (qw + 2 * kvw);
-    const uint32_t pos = a.pos[b];
-    int kind;  // 0 q, 1 k, 2 v
-    uint32_t head;
-    const float *src;
-    if (hh < a.heads) {
-        kind = 0; head = hh; src = row + head * D;
-    } else if (hh < a.heads + a.kv_heads) {
-        kind = 1; head = hh - a.heads; src = row + qw + head * D;
-    } else {
-        kind = 2; head = hh - a.heads - a.kv_heads; src = row + qw + kvw + head * D;
-    }
-    float x0 = src[lane];
-    float x1 = src[lane + 64];
-    if (kind != 2) {
-        const float *w = kind == 0 ? a.q_norm : a.k_norm;
-        const float ss = dev::wave_sum(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)));
-        const float inverse_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
-        x0 = __fmul_rn(__fmul_rn(x0, inverse_rms), w[lane]);
-        x1 = __fmul_rn(__fmul_rn(x1, inverse_rms), w[lane + 64]);
-        const float c = a.rope_cos[(size_t)pos * 64 + lane];
-        const float s = a.rope_sin[(size_t)pos * 64 + lane];
-        const float y0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-        const float y1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
-        x0 = y0;
-        x1 = y1;
-    }
-    if (kind == 0) {
-        float *dst = a.q_out + (size_t)b * qw + head * D;
-        dst[lane] = x0;
-        dst[lane + 64] = x1;
-        return;
-    }
-    uint8_t *scales = (kind == 1 ? a.k_scales : a.v_scales) + b * a.seq_stride;
-    uint8_t *codes = (kind == 1 ? a.k_codes : a.v_codes) + b * a.seq_stride;
-    const uint32_t gpr = kvw / 64;
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const float v = g == 0 ? x0 : x1;
-        const float amax = dev::wave_max(fabsf(v));
-        const uint16_t bits = dev::f32_to_f16_bits(__fdiv_rn(amax, 128.0f));
-        const float stored = dev::f16_bits_to_f32(bits);
-        codes[(size_t)pos * kvw + head * D + g * 64 + lane] =
-            (uint8_t)(dev::quantize_one(v, stored, -128, 127) + 128);
-        if (lane == 0) reinterpret_cast<uint16_t *>(scales)[(size_t)pos * gpr + head * 2 + g] = bits;
-    }
-}
-
 // argmaxLogits (decoder.zig:290-301): the largest value, the lowest index
 // among equal maxima. Stage 1: one partial per block.
 __device__ __forceinline__ void better(float &v, uint32_t &i, float v2, uint32_t i2) {
@@ -320,7 +249,7 @@ struct qwh_decoder {
     size_t cache_scales = 0, cache_codes = 0, layer_stride = 0, seq_stride = 0;
     uint32_t *tokens_dev = nullptr, *pos_dev = nullptr, *hist_base_dev = nullptr, *history_dev = nullptr;
     uint32_t history_rows = 0;
-    float *hidden = nullptr, *qkv = nullptr, *q_rot = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+    float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
     void *digits = nullptr;
     void *attn_scratch = nullptr;
     float *arg_v = nullptr;
@@ -332,6 +261,8 @@ struct qwh_decoder {
     hipGraphExec_t graph[2] = {nullptr, nullptr};
     bool use_graph = true;
     bool fused = true;  // every GEMV forms its own activations (no norm / prep kernels)
+    bool batched = false;  // batch > 1: int8 digit planes + matrix-core GEMV
+    void *batch_digits = nullptr;
 };
 
 namespace qwh {
@@ -382,6 +313,16 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
     // the GEMV forms them itself, else through a digit-plane pass.
     auto gemv = [&](GemvInput::Mode mode, const float *x, const float *norm, const Matrix &w, float *out,
                     const float *residual) -> hipError_t {
+        if (d->batched) {
+            GemvInput in;
+            in.mode = mode;
+            in.x = x;
+            in.norm = norm;
+            in.eps = c.eps;
+            const hipError_t e = launch_prep_batch(s, in, B, w.cols, d->batch_digits);
+            if (e != hipSuccess) return e;
+            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual);
+        }
         if (d->fused) {
             GemvInput in;
             in.mode = mode;
@@ -406,28 +347,19 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         qwh_decoder::Layer &L = d->layers[l];
         err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr);
         if (err != hipSuccess) break;
-        QkArgs qa{};
-        qa.qkv = d->qkv;
-        qa.q_norm = L.q_norm;
-        qa.k_norm = L.k_norm;
-        qa.rope_cos = d->rope_cos;
-        qa.rope_sin = d->rope_sin;
-        qa.pos = d->pos_dev;
-        qa.q_out = d->q_rot;
+        // Per-head norms, RoPE, the cache append and the attention itself
+        // (decoder.zig:180-253) in one launch.
         uint8_t *kl = d->keys + (size_t)l * d->layer_stride;
         uint8_t *vl = d->values + (size_t)l * d->layer_stride;
-        qa.k_scales = kl;
-        qa.k_codes = kl + d->cache_scales;
-        qa.v_scales = vl;
-        qa.v_codes = vl + d->cache_scales;
-        qa.seq_stride = d->seq_stride;
-        qa.heads = c.heads;
-        qa.kv_heads = c.kv_heads;
-        qa.eps = c.eps;
-        qk_rope_append_kernel<<<dim3(B, c.heads + 2 * c.kv_heads), 64, 0, s>>>(qa);
         AttentionArgs aa{};
         aa.out = d->attn;
-        aa.query = d->q_rot;
+        aa.query = d->qkv;
+        aa.query_stride = d->qw + 2 * d->kvw;
+        aa.q_norm = L.q_norm;
+        aa.k_norm = L.k_norm;
+        aa.rope_cos = d->rope_cos;
+        aa.rope_sin = d->rope_sin;
+        aa.eps = c.eps;
         aa.k_scales = kl;
         aa.k_codes = kl + d->cache_scales;
         aa.v_scales = vl;
@@ -558,10 +490,11 @@ extern "C" {
 int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch, qwh_decoder **out) {
     if (!ctx || !config || !out || batch == 0) return QWH_E_INVALID_ARGUMENT;
     const qwh_decoder_config &c = *config;
-    if (c.head_dim != 128)
-        return fail(ctx, QWH_E_UNSUPPORTED, "the decoder step supports head_dim 128 (got %u)", c.head_dim);
-    if (c.kv_heads == 0 || c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8)
+    if (c.kv_heads == 0 || c.heads % c.kv_heads != 0)
         return fail(ctx, QWH_E_SHAPE_MISMATCH, "heads %u / kv_heads %u", c.heads, c.kv_heads);
+    if (!attention_supported(c.head_dim, c.heads / c.kv_heads))
+        return fail(ctx, QWH_E_UNSUPPORTED, "no attention kernel for head_dim %u with %u heads per kv head",
+                    c.head_dim, c.heads / c.kv_heads);
     if (c.hidden % 64 || c.ffn % 64 || c.hidden == 0 || c.ffn == 0 || c.layers == 0 || c.vocab == 0)
         return fail(ctx, QWH_E_SHAPE_MISMATCH, "hidden and ffn must be multiples of 64");
     // model.zig:62 position_limit and :1006-1009 validateCapacity.
@@ -635,11 +568,13 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     const uint32_t widest = c.ffn > c.hidden ? (c.ffn > d->qw ? c.ffn : d->qw) : (c.hidden > d->qw ? c.hidden : d->qw);
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.hidden, reinterpret_cast<void **>(&d->hidden));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (d->qw + 2 * d->kvw), reinterpret_cast<void **>(&d->qkv));
-    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->qw, reinterpret_cast<void **>(&d->q_rot));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->qw, reinterpret_cast<void **>(&d->attn));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * 2 * c.ffn, reinterpret_cast<void **>(&d->gu));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (size_t)c.vocab, reinterpret_cast<void **>(&d->logits));
     if (st == QWH_OK) st = dalloc(d, q4_digit_bytes(batch, widest), &d->digits);
+    // QWH_DECODER_PER_TOKEN keeps batch > 1 on the per-token GEMV (for tests).
+    d->batched = batch > 1 && getenv("QWH_DECODER_PER_TOKEN") == nullptr;
+    if (st == QWH_OK && d->batched) st = dalloc(d, batch_digit_bytes(batch, widest), &d->batch_digits);
     AttentionArgs aa{};
     aa.capacity = c.max_positions;
     aa.heads = c.heads;

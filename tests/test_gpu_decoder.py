@@ -77,6 +77,38 @@ def test_free_running_token_ids(ctx, tiny_pair):
         assert ids[:, b].tolist() == expected, b
 
 
+@pytest.mark.parametrize("batch,env", [
+    (1, ()),                                                   # lane-per-row GEMVs, fused inputs
+    (2, ("QWH_DECODER_PER_TOKEN",)),                           # batch > 1 on the per-token GEMVs
+    (2, ("QWH_DECODER_PER_TOKEN", "QWH_DECODER_UNFUSED")),     # separate norm / SiLU / digit kernels
+])
+def test_token_ids_on_each_gemv_path(ctx, batch, env, monkeypatch):
+    # The default batch > 1 path (matrix-core GEMVs) is covered above; the
+    # environment switches are read when the decoder is created.
+    for name in env:
+        monkeypatch.setenv(name, "1")
+    seed = 13
+    gpu = qa.Decoder(ctx, batch=batch, **TINY)
+    ref = o.Decoder(seed, batch, **TINY)
+    try:
+        gpu.init_synthetic(seed)
+        for b in range(batch):
+            gpu.prefill_random(b, 4 + 7 * b, seed)
+            ref.prefill_random(b, 4 + 7 * b)
+        start = [o.start_token(seed, b, TINY["vocab"]) for b in range(batch)]
+        ids = gpu.generate(start, 20)
+        for b in range(batch):
+            t = start[b]
+            expected = []
+            for _ in range(20):
+                t = ref.step(b, t)
+                expected.append(t)
+            assert ids[:, b].tolist() == expected, (b, env)
+    finally:
+        gpu.close()
+        ref.close()
+
+
 def test_step_and_generate_agree(ctx):
     seed = 11
     a = qa.Decoder(ctx, batch=2, **TINY)

@@ -106,6 +106,42 @@ def test_q4_gemv_edge_shapes(ctx, rows, cols, tokens):
     check(ctx, o.Q4, w, x, tokens, f"q4 {rows}x{cols} tokens {tokens}")
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [
+    (4096, 2048, 16),   # configs[4] q|k|v rows at batch 16
+    (2048, 6144, 16),   # configs[4] down projection at batch 16
+    (100, 1024, 7),     # partial row tile, partial token tile
+    (17, 64, 17),       # one group per row (three idle wavefronts), two token tiles
+    (33, 192, 33),      # three groups, three token tiles
+    (64, 256, 2),
+])
+def test_q4_batch_gemv(ctx, rows, cols, tokens):
+    # Two or more tokens run on the matrix-core kernel.
+    w = o.normal(rows * cols, 8, rows, 0.02).reshape(rows, cols)
+    x = o.normal(tokens * cols, 8, 2000 + cols)
+    check(ctx, o.Q4, w, x, tokens, f"q4 batch {rows}x{cols} tokens {tokens}")
+
+
+def test_q4_batch_awkward_values(ctx):
+    # Per token: an all-zero group, a huge dynamic range inside a group,
+    # tiny values; plus an all-zero token and a zero weight row.
+    rows, cols, tokens = 48, 512, 5
+    w = o.normal(rows * cols, 9, 0, 0.02).reshape(rows, cols)
+    w[7] = 0.0
+    w[8, :64] = np.float32(-7.5)
+    x = o.normal(tokens * cols, 9, 1).reshape(tokens, cols)
+    x[0, :64] = 0.0
+    x[1, 64] = np.float32(3e4)
+    x[1, 65] = np.float32(1e-12)
+    x[2, 128:192] = np.float32(1e-30)
+    x[3] = 0.0
+    x[4, 200] = np.float32(-1e-3)
+    scales, data = o.quantize_rows(o.Q4, w)
+    expected = o.linear_quantized(o.Q4, scales, data, rows, cols, x.reshape(-1), tokens)
+    actual = run_linear(ctx, o.Q4, scales, data, rows, cols, x.reshape(-1), tokens)
+    assert np.all(actual[:, 7] == 0.0) and np.all(actual[3] == 0.0)
+    assert_close(actual, expected, what="batch awkward values")
+
+
 @pytest.mark.parametrize("rows,cols,tokens", [(1001, 1024, 1), (33, 64, 2), (130, 6144, 1), (48, 192, 1)])
 def test_q8_gemv_edge_shapes(ctx, rows, cols, tokens):
     w = o.normal(rows * cols, 6, rows, 0.02).reshape(rows, cols)
