@@ -85,7 +85,7 @@ int32_t qwh_upload(qwh_ctx *ctx, void *dst_dev, const void *src, uint64_t bytes)
 int32_t qwh_download(qwh_ctx *ctx, void *dst, const void *src_dev, uint64_t bytes);
 int32_t qwh_memset(qwh_ctx *ctx, void *dst_dev, int32_t value, uint64_t bytes);
 
-/* Stream-ordered timing: records event `slot` (0..63) on the context stream;
+/* Stream-ordered timing: records event `slot` (0..255) on the context stream;
  * qwh_event_elapsed synchronizes on `end` and returns milliseconds. */
 int32_t qwh_event_record(qwh_ctx *ctx, uint32_t slot);
 int32_t qwh_event_elapsed(qwh_ctx *ctx, uint32_t start, uint32_t end, float *out_ms);

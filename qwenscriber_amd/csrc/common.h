@@ -13,7 +13,7 @@
 namespace qwh {
 
 constexpr int kGroup = 64;          // quant.zig:49
-constexpr int kMaxEvents = 64;
+constexpr int kMaxEvents = 256;
 
 inline int data_bytes_per_group(int format) {
     switch (format) {
