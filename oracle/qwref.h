@@ -13,8 +13,9 @@
  * no multiply-add is fused behind the restatement's back.
  *
  * Pinning (what checks each part beyond retyping it):
- *   f16 codec        half_float.zig:47-77 known answers + exhaustive comparison
- *                    against the compiler's _Float16 conversion (tests).
+ *   f16 codec        half_float.zig:47-77 known answers + comparison against
+ *                    numpy's float16 casts (every f16 pattern widened; a sweep
+ *                    of f32 values, ties included, narrowed) in the tests.
  *   quantize/pack    selftest.zig:294 golden quant_hash 0xf247917b05691fd1,
  *                    quant.zig:527-554 exact values, plane offsets :423-448.
  *   dequant / dot    kernels.zig:932-971 (ones row -> 56.0), f64 brute force.
