@@ -222,7 +222,9 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
                            qwh_decoder **out);
 int32_t qwh_decoder_destroy(qwh_decoder *decoder);
 /* Binds a quantized matrix (QWH_T_EMBED..QWH_T_LM_HEAD). The decoder copies
- * the q/k/v and gate/up planes into fused row blocks; the others are borrowed.
+ * the q/k/v planes into one fused row block and the gate/up planes into one
+ * matrix with their rows interleaved (gate row j, then up row j); the others
+ * are borrowed.
  * Layer is ignored for EMBED and LM_HEAD. */
 int32_t qwh_decoder_set_matrix(qwh_decoder *decoder, uint32_t kind, uint32_t layer,
                                uint64_t matrix);

@@ -12,18 +12,20 @@
 // (Merging in the last workgroup to finish needs device-scope fences, which
 // write back and invalidate the L2 of every die and measured slower.)
 // Position count is unbounded (the WGSL kernel's 4096-position cap,
-// decode_attention_q8.wgsl:56, does not apply).
+// decode_attention_q8.wgsl:56, does not apply). The softmax runs in base 2
+// (scores carry a factor log2(e), exponentials are exp2): the same weights.
 //
 // The decoder form also does the work decoder.zig:180-216 does between the
 // q/k/v projection and the attention: per-head RMSNorm of q and k, RoPE at the
-// new position, and the q8 append of the new key and value rows. Every
-// workgroup normalizes and rotates its own query heads; the workgroup whose
-// range holds the new position also quantizes the new key/value rows, stores
-// them in the cache, and attends to them from registers.
+// new position, and the q8 append of the new key and value rows. The range
+// kernel normalizes and rotates its query heads and attends to every row
+// before the new one; the merge kernel (one workgroup per query head, a
+// thread per dimension) forms the new key and value rows, stores them in the
+// cache, and adds the new position's score and value to the merged state.
 //
-// Lane mapping: a head row of D codes is D/16 lanes of 16 bytes ("lane
-// group"); a wavefront scores 64/(D/16) positions per load. Each lane holds
-// its 16 query values for every head of the group in registers.
+// Lane mapping of the range kernel: a head row of D codes is D/16 lanes of 16
+// bytes ("lane group"); a wavefront scores 64/(D/16) positions per load. Each
+// lane holds its 16 query values for every head of the group in registers.
 #include <cfloat>
 
 #include "common.h"
@@ -32,7 +34,8 @@
 namespace qwh {
 namespace {
 
-constexpr float kNeg = -1.0e30f;  // running-max sentinel: finite, so exp(kNeg - kNeg) is defined
+constexpr float kNeg = -1.0e30f;  // running-max sentinel: finite, so exp2(kNeg - kNeg) is defined
+constexpr float kLog2e = 1.44269504088896340736f;
 constexpr int kBlockPositions = 4; // positions per lane group between softmax rescales
 constexpr int kWaves = 4;
 constexpr uint32_t kMaxSplits = 512;
@@ -43,11 +46,12 @@ struct AttnKernelArgs {
     uint8_t *k_scales, *k_codes, *v_scales, *v_codes;
     const uint32_t *cached_dev;
     uint32_t cached, cached_bias;
+    uint32_t rows;       // cache rows that may be read (>= every sequence's cached)
     uint32_t heads, kv_heads;
     uint32_t chunk;      // positions per workgroup
     uint32_t splits;
     uint64_t scale_stride, code_stride;
-    float scaling;
+    float scaling;       // log2(e) / sqrt(D)
     float *partial;      // [batch][kv_heads][splits] records of R*D + 4*R floats
     float *out;          // [batch][heads][D]
     // Decoder form.
@@ -55,12 +59,16 @@ struct AttnKernelArgs {
     float eps;
 };
 
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The 16 codes of a 16-byte slice as the exact signed values u - 128:
+// XOR 0x80 makes each byte the two's complement of u - 128.
 __device__ __forceinline__ void unpack16(const uint4 w, float (&c)[16]) {
-    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t v[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) c[i * 4 + b] = (float)((v[i] >> (8 * b)) & 0xffu);
+        for (int b = 0; b < 4; ++b) c[i * 4 + b] = (float)(signed char)(v[i] >> (8 * b));
     }
 }
 
@@ -72,12 +80,10 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // math.rmsNormInPlace (math.zig:120-130) of one head row spread over the LPP
-// lanes of a lane group (16 values per lane), then rotate_half RoPE
-// (kernels.zig:495-527) with the tables' row for `pos`: the partner of
-// dimension d < D/2 is d + D/2, held by lane sub ^ LPP/2.
+// lanes of a lane group (16 values per lane); `weight` holds this lane's 16
+// weights.
 template <int D>
-__device__ __forceinline__ void norm_rope16(float (&x)[16], const float *weight, const float *cos_row,
-                                            const float *sin_row, int sub, float eps) {
+__device__ __forceinline__ void rms_norm16(float (&x)[16], const float (&weight)[16], float eps) {
     constexpr int LPP = D / 16;
     float ss = 0.0f;
 #pragma unroll
@@ -85,38 +91,33 @@ __device__ __forceinline__ void norm_rope16(float (&x)[16], const float *weight,
     ss = group_sum<LPP>(ss);
     const float inverse_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = __fmul_rn(__fmul_rn(x[i], inverse_rms), weight[sub * 16 + i]);
+    for (int i = 0; i < 16; ++i) x[i] = __fmul_rn(__fmul_rn(x[i], inverse_rms), weight[i]);
+}
+
+// rotate_half RoPE (kernels.zig:495-527) with the tables' row for the
+// position: the partner of dimension d < D/2 is d + D/2, held by lane
+// sub ^ LPP/2. c[i], s[i] are the table entries of this lane's dimensions.
+template <int D>
+__device__ __forceinline__ void rope16(float (&x)[16], const float (&c)[16], const float (&s)[16], int sub) {
+    constexpr int LPP = D / 16;
     const bool first = sub < LPP / 2;
-    const int j0 = (sub % (LPP / 2)) * 16;
     float y[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const float partner = __shfl_xor(x[i], LPP / 2, 64);
-        const float c = cos_row[j0 + i];
-        const float s = sin_row[j0 + i];
-        y[i] = first ? __fsub_rn(__fmul_rn(x[i], c), __fmul_rn(partner, s))
-                     : __fadd_rn(__fmul_rn(x[i], c), __fmul_rn(partner, s));
+        y[i] = first ? __fsub_rn(__fmul_rn(x[i], c[i]), __fmul_rn(partner, s[i]))
+                     : __fadd_rn(__fmul_rn(x[i], c[i]), __fmul_rn(partner, s[i]));
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = y[i];
 }
 
-// quantizeRow(.q8) (quant.zig:197-288) of a head row: the 64-value groups are
-// 4 consecutive lanes of a lane group. Returns this lane's 16 codes packed in
-// byte order, and its group's stored scale (bits and value).
-__device__ __forceinline__ uint4 quantize16(const float (&x)[16], uint16_t &bits, float &stored) {
-    float amax = 0.0f;
+__device__ __forceinline__ void load16(const float *p, float (&v)[16]) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    bits = dev::f32_to_f16_bits(__fdiv_rn(amax, 128.0f));
-    stored = dev::f16_bits_to_f32(bits);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-        w[i / 4] |= (uint32_t)(dev::quantize_one(x[i], stored, -128, 127) + 128) << (8 * (i % 4));
-    return make_uint4(w[0], w[1], w[2], w[3]);
+    for (int i = 0; i < 16; i += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(p + i);
+        v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+    }
 }
 
 template <int R>
@@ -127,13 +128,13 @@ struct SoftmaxState {
 // One block of NB positions per lane group: scores against the lane's query
 // slices, online-softmax update, value accumulation.
 template <int D, int R, int NB>
-__device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][16], const float (&qsum)[R],
-                                       const uint4 (&kc)[NB], const uint4 (&vc)[NB], const float (&ks)[NB],
-                                       const float (&vs)[NB], const bool (&valid)[NB], float scaling) {
+__device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][16], const uint4 (&kc)[NB],
+                                       const uint4 (&vc)[NB], const float (&ks)[NB], const float (&vs)[NB],
+                                       const bool (&valid)[NB], float scaling) {
     constexpr int LPP = D / 16;
-    // Scores: sum_i (u_i - 128) q_i = sum_i u_i q_i - 128 sum_i q_i, per
-    // 16-value slice, times the slice's group scale, summed over the LPP
-    // lanes of the position, times 1/sqrt(D).
+    // Scores: sum_i (u_i - 128) q_i per 16-value slice, times the slice's
+    // group scale, summed over the LPP lanes of the position, times the
+    // scaling.
     float score[NB][R];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -144,7 +145,7 @@ __device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][
             float dot = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) dot = fmaf(c[i], q[r][i], dot);
-            const float part = group_sum<LPP>((dot - qsum[r]) * ks[nb]);
+            const float part = group_sum<LPP>(dot * ks[nb]);
             score[nb][r] = valid[nb] ? part * scaling : kNeg;
         }
     }
@@ -155,11 +156,11 @@ __device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][
 #pragma unroll
         for (int nb = 1; nb < NB; ++nb) bm = fmaxf(bm, score[nb][r]);
         const float m_new = fmaxf(st.m[r], bm);
-        const float alpha = expf(st.m[r] - m_new);
+        const float alpha = fast_exp2(st.m[r] - m_new);
         float sum = 0.0f;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            w[nb][r] = valid[nb] ? expf(score[nb][r] - m_new) : 0.0f;
+            w[nb][r] = valid[nb] ? fast_exp2(score[nb][r] - m_new) : 0.0f;
             sum += w[nb][r];
         }
         st.l[r] = st.l[r] * alpha + sum;
@@ -167,13 +168,11 @@ __device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][
 #pragma unroll
         for (int i = 0; i < 16; ++i) st.acc[r][i] *= alpha;
     }
-    // Values: acc += (p * scale) * (u - 128), the code offset taken exactly.
+    // Values: acc += (p * scale) * (u - 128).
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         float c[16];
         unpack16(vc[nb], c);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) c[i] -= 128.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float wv = w[nb][r] * vs[nb];
@@ -183,68 +182,17 @@ __device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][
     }
 }
 
-// out[h][d] = sum_s e^{m_s - M} acc_s[d] / sum_s e^{m_s - M} l_s over the
-// ranges that hold positions, in range order, for the R heads of kv head
-// `kvh`. Thread t takes four dimensions of one head (column t % COLS) for the
-// ranges congruent to t / COLS; the SL partial merges are then combined in
-// order.
-template <int D, int R>
-__device__ __forceinline__ void merge_ranges(const AttnKernelArgs &a, uint32_t b, uint32_t kvh, uint32_t cached) {
-    constexpr int REC = R * D + 4 * R;
-    constexpr int COLS = R * D / 4;
-    static_assert(COLS <= 256, "one float4 column per thread");
-    constexpr int SL = 256 / COLS;
-    const uint32_t used = (cached + a.chunk - 1) / a.chunk < a.splits ? (cached + a.chunk - 1) / a.chunk : a.splits;
-    const int t = threadIdx.x;
-    const int col = t % COLS;
-    const int j = t / COLS;
-    const int r = col / (D / 4);
-    const int d4 = col % (D / 4);
-    float M = kNeg, L = 0.0f;
-    float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const float *recs = a.partial + ((size_t)b * a.kv_heads + kvh) * a.splits * REC;
-    if (j < SL) {
-        for (uint32_t s = j; s < used; s += SL) {
-            const float *rec = recs + (size_t)s * REC;
-            const float m = rec[R * D + 4 * r];
-            const float l = rec[R * D + 4 * r + 1];
-            const float4 v = *reinterpret_cast<const float4 *>(rec + r * D + 4 * d4);
-            const float m_new = fmaxf(M, m);
-            const float fa = expf(M - m_new);
-            const float fb = expf(m - m_new);
-            L = L * fa + l * fb;
-            A.x = A.x * fa + v.x * fb;
-            A.y = A.y * fa + v.y * fb;
-            A.z = A.z * fa + v.z * fb;
-            A.w = A.w * fa + v.w * fb;
-            M = m_new;
-        }
-    }
-    __shared__ float lds_m[256], lds_l[256];
-    __shared__ float4 lds_a[256];
-    lds_m[t] = M;
-    lds_l[t] = L;
-    lds_a[t] = A;
-    __syncthreads();
-    if (t < COLS) {
-        for (int k = 1; k < SL; ++k) {
-            const float m = lds_m[k * COLS + col];
-            const float l = lds_l[k * COLS + col];
-            const float4 v = lds_a[k * COLS + col];
-            const float m_new = fmaxf(M, m);
-            const float fa = expf(M - m_new);
-            const float fb = expf(m - m_new);
-            L = L * fa + l * fb;
-            A.x = A.x * fa + v.x * fb;
-            A.y = A.y * fa + v.y * fb;
-            A.z = A.z * fa + v.z * fb;
-            A.w = A.w * fa + v.w * fb;
-            M = m_new;
-        }
-        const float inv = 1.0f / L;
-        float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
-        *reinterpret_cast<float4 *>(a.out + ((size_t)b * a.heads + kvh * R + r) * D + 4 * d4) = o;
-    }
+// Online-softmax merge of (m, l, acc) into a running (M, L, A).
+__device__ __forceinline__ void merge_state(float &M, float &L, float4 &A, float m, float l, float4 v) {
+    const float m_new = fmaxf(M, m);
+    const float fa = fast_exp2(M - m_new);
+    const float fb = fast_exp2(m - m_new);
+    L = L * fa + l * fb;
+    A.x = A.x * fa + v.x * fb;
+    A.y = A.y * fa + v.y * fb;
+    A.z = A.z * fa + v.z * fb;
+    A.w = A.w * fa + v.w * fb;
+    M = m_new;
 }
 
 template <int D, int R, bool Decoder>
@@ -263,181 +211,313 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     const uint32_t b = blockIdx.z;
     const uint32_t kv_width = a.kv_heads * D;
     const uint32_t gpr = kv_width / 64;
-    const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
     const uint32_t begin = split * a.chunk;
+    const uint16_t *k_scales = reinterpret_cast<const uint16_t *>(a.k_scales + b * a.scale_stride);
+    const uint16_t *v_scales = reinterpret_cast<const uint16_t *>(a.v_scales + b * a.scale_stride);
+    const uint8_t *k_codes = a.k_codes + b * a.code_stride;
+    const uint8_t *v_codes = a.v_codes + b * a.code_stride;
+    const uint32_t scale_col = kvh * GPH + sub / 4;   // group of this lane's slice
+    const uint32_t code_col = kvh * D + sub * 16;
+    constexpr uint32_t kSpan = STEP * kBlockPositions;
+
+    // A block of cache rows: this lane's slice of kBlockPositions positions.
+    struct Block {
+        uint4 kc[kBlockPositions], vc[kBlockPositions];
+        float ks[kBlockPositions], vs[kBlockPositions];
+        bool valid[kBlockPositions];
+    };
+    // Loads rows base + ..., those below `limit`; the others read as empty.
+    auto load_block = [&](Block &blk, uint32_t base, uint32_t limit) {
+#pragma unroll
+        for (int nb = 0; nb < kBlockPositions; ++nb) {
+            const uint32_t p = base + nb * STEP + wave * PPW + group;
+            blk.valid[nb] = p < limit;
+            if (blk.valid[nb]) {
+                blk.kc[nb] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)p * kv_width + code_col);
+                blk.vc[nb] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)p * kv_width + code_col);
+                blk.ks[nb] = dev::f16_bits_to_f32(k_scales[(size_t)p * gpr + scale_col]);
+                blk.vs[nb] = dev::f16_bits_to_f32(v_scales[(size_t)p * gpr + scale_col]);
+            } else {
+                blk.kc[nb] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+                blk.vc[nb] = blk.kc[nb];
+                blk.ks[nb] = 0.0f;
+                blk.vs[nb] = 0.0f;
+            }
+        }
+    };
+    // The first block is loaded before the sequence's position is known
+    // (in the decoder it is a device value, one memory round trip away):
+    // every allocated row is readable, and rows past the position are
+    // dropped below once it has arrived. The query slices and norm weights
+    // do not depend on it either.
+    Block cur, nxt;
+    load_block(cur, begin, a.rows);
+    const float *row = a.query + (size_t)b * a.query_stride;
+    float q[R][16];
+#pragma unroll
+    for (int r = 0; r < R; ++r) load16(row + (kvh * R + r) * D + sub * 16, q[r]);
+    float wq[16];
+    if (Decoder) load16(a.q_norm + sub * 16, wq);
+    const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
+    // The decoder form leaves the newest row (cached - 1) to the merge kernel.
+    const uint32_t attended = Decoder ? cached - 1 : cached;
     uint32_t end = begin + a.chunk;
-    if (end > cached) end = cached;
+    if (end > attended) end = attended;
 
     __shared__ float lds_acc[kWaves][R][D];
     __shared__ float lds_ml[kWaves][R][2];
 
-    if (begin < cached) {
-        const uint16_t *k_scales = reinterpret_cast<const uint16_t *>(a.k_scales + b * a.scale_stride);
-        const uint16_t *v_scales = reinterpret_cast<const uint16_t *>(a.v_scales + b * a.scale_stride);
-        const uint8_t *k_codes = a.k_codes + b * a.code_stride;
-        const uint8_t *v_codes = a.v_codes + b * a.code_stride;
-        const uint32_t scale_col = kvh * GPH + sub / 4;   // group of this lane's slice
-        const uint32_t code_col = kvh * D + sub * 16;
-        // The decoder form's new row (position cached - 1) is attended from
-        // registers by the workgroup that holds it, so the loop stops short.
-        const uint32_t newest = cached - 1;
-        const bool owner = Decoder && end == cached;
-        const uint32_t loop_end = owner ? newest : end;
-
-        // Query slices: heads kvh*R .. kvh*R+R-1, dims sub*16 .. +16.
-        const float *row = a.query + (size_t)b * a.query_stride;
-        float q[R][16];
+    if (begin >= cached) return;  // no record: the merge reads ranges below cached only
+#pragma unroll
+    for (int nb = 0; nb < kBlockPositions; ++nb) {
+        const uint32_t p = begin + nb * STEP + wave * PPW + group;
+        if (!(p < end)) {
+            // Row beyond the position (possibly never written): no score,
+            // and a zero value scale so no stale bits reach the sums.
+            cur.valid[nb] = false;
+            cur.ks[nb] = 0.0f;
+            cur.vs[nb] = 0.0f;
+        }
+    }
+    if (Decoder) {
+        const int j0 = (sub % (LPP / 2)) * 16;
+        float rc[16], rs[16];
+        load16(a.rope_cos + (size_t)(cached - 1) * (D / 2) + j0, rc);
+        load16(a.rope_sin + (size_t)(cached - 1) * (D / 2) + j0, rs);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float4 *src = reinterpret_cast<const float4 *>(row + (kvh * R + r) * D + sub * 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v = src[i];
-                q[r][i * 4 + 0] = v.x; q[r][i * 4 + 1] = v.y; q[r][i * 4 + 2] = v.z; q[r][i * 4 + 3] = v.w;
-            }
-        }
-        if (Decoder) {
-            const float *cos_row = a.rope_cos + (size_t)newest * (D / 2);
-            const float *sin_row = a.rope_sin + (size_t)newest * (D / 2);
-#pragma unroll
-            for (int r = 0; r < R; ++r) norm_rope16<D>(q[r], a.q_norm, cos_row, sin_row, sub, a.eps);
-        }
-        float qsum[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s += q[r][i];
-            qsum[r] = 128.0f * s;
-        }
-
-        SoftmaxState<R> st;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            st.m[r] = kNeg;
-            st.l[r] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) st.acc[r][i] = 0.0f;
-        }
-
-        for (uint32_t base = begin; base < loop_end; base += STEP * kBlockPositions) {
-            uint4 kc[kBlockPositions], vc[kBlockPositions];
-            float ks[kBlockPositions], vs[kBlockPositions];
-            bool valid[kBlockPositions];
-#pragma unroll
-            for (int nb = 0; nb < kBlockPositions; ++nb) {
-                const uint32_t p = base + nb * STEP + wave * PPW + group;
-                valid[nb] = p < loop_end;
-                if (valid[nb]) {
-                    kc[nb] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)p * kv_width + code_col);
-                    vc[nb] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)p * kv_width + code_col);
-                    ks[nb] = dev::f16_bits_to_f32(k_scales[(size_t)p * gpr + scale_col]);
-                    vs[nb] = dev::f16_bits_to_f32(v_scales[(size_t)p * gpr + scale_col]);
-                } else {
-                    kc[nb] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-                    vc[nb] = kc[nb];
-                    ks[nb] = 0.0f;
-                    vs[nb] = 0.0f;
-                }
-            }
-            attend<D, R, kBlockPositions>(st, q, qsum, kc, vc, ks, vs, valid, a.scaling);
-        }
-
-        if (owner) {
-            // decoder.zig:180-216 for the kv head of this workgroup: RMSNorm
-            // and RoPE of the key, then the q8 append of key and value.
-            const float *key = row + a.heads * D + kvh * D + sub * 16;
-            const float *value = row + a.heads * D + kv_width + kvh * D + sub * 16;
-            float kx[16], vx[16];
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                const float4 kv4 = *reinterpret_cast<const float4 *>(key + i);
-                const float4 vv4 = *reinterpret_cast<const float4 *>(value + i);
-                kx[i] = kv4.x; kx[i + 1] = kv4.y; kx[i + 2] = kv4.z; kx[i + 3] = kv4.w;
-                vx[i] = vv4.x; vx[i + 1] = vv4.y; vx[i + 2] = vv4.z; vx[i + 3] = vv4.w;
-            }
-            norm_rope16<D>(kx, a.k_norm, a.rope_cos + (size_t)newest * (D / 2), a.rope_sin + (size_t)newest * (D / 2),
-                           sub, a.eps);
-            uint16_t kbits, vbits;
-            uint4 kc[1], vc[1];
-            float ks[1], vs[1];
-            kc[0] = quantize16(kx, kbits, ks[0]);
-            vc[0] = quantize16(vx, vbits, vs[0]);
-            if (wave == 0 && group == 0) {
-                *reinterpret_cast<uint4 *>(a.k_codes + b * a.code_stride + (size_t)newest * kv_width + code_col) = kc[0];
-                *reinterpret_cast<uint4 *>(a.v_codes + b * a.code_stride + (size_t)newest * kv_width + code_col) = vc[0];
-                if (sub % 4 == 0) {
-                    reinterpret_cast<uint16_t *>(a.k_scales + b * a.scale_stride)[(size_t)newest * gpr + scale_col] = kbits;
-                    reinterpret_cast<uint16_t *>(a.v_scales + b * a.scale_stride)[(size_t)newest * gpr + scale_col] = vbits;
-                }
-            }
-            const bool valid[1] = {wave == 0 && group == 0};
-            attend<D, R, 1>(st, q, qsum, kc, vc, ks, vs, valid, a.scaling);
-        }
-
-        // Merge the lane groups of this wave (lanes l and l ^ (k * LPP) hold
-        // the same slice for different positions).
-#pragma unroll
-        for (int mask = LPP; mask < 64; mask <<= 1) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float m_o = __shfl_xor(st.m[r], mask, 64);
-                const float l_o = __shfl_xor(st.l[r], mask, 64);
-                const float m_new = fmaxf(st.m[r], m_o);
-                const float a_self = expf(st.m[r] - m_new);
-                const float a_other = expf(m_o - m_new);
-                st.l[r] = st.l[r] * a_self + l_o * a_other;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float o = __shfl_xor(st.acc[r][i], mask, 64);
-                    st.acc[r][i] = st.acc[r][i] * a_self + o * a_other;
-                }
-                st.m[r] = m_new;
-            }
-        }
-        if (group == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) lds_acc[wave][r][sub * 16 + i] = st.acc[r][i];
-                if (sub == 0) {
-                    lds_ml[wave][r][0] = st.m[r];
-                    lds_ml[wave][r][1] = st.l[r];
-                }
-            }
-        }
-        __syncthreads();
-        // Merge the waves in wave order into this range's record.
-        float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
-        for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
-            const int r = idx / D;
-            const int d = idx % D;
-            float M = lds_ml[0][r][0];
-#pragma unroll
-            for (int w2 = 1; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2][r][0]);
-            float L = 0.0f, A = 0.0f;
-#pragma unroll
-            for (int w2 = 0; w2 < kWaves; ++w2) {
-                const float f = expf(lds_ml[w2][r][0] - M);
-                L += lds_ml[w2][r][1] * f;
-                A += lds_acc[w2][r][d] * f;
-            }
-            rec[idx] = A;
-            if (d == 0) {
-                rec[R * D + 4 * r + 0] = M;
-                rec[R * D + 4 * r + 1] = L;
-            }
+            rms_norm16<D>(q[r], wq, a.eps);
+            rope16<D>(q[r], rc, rs, sub);
         }
     }
 
+    SoftmaxState<R> st;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        st.m[r] = kNeg;
+        st.l[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.acc[r][i] = 0.0f;
+    }
+
+    // Double buffered: the next block's loads are in flight while the
+    // current one is scored and accumulated.
+    for (uint32_t base = begin; base < end; base += kSpan) {
+        const bool more = base + kSpan < end;
+        if (more) load_block(nxt, base + kSpan, end);
+        attend<D, R, kBlockPositions>(st, q, cur.kc, cur.vc, cur.ks, cur.vs, cur.valid, a.scaling);
+        if (more) cur = nxt;
+    }
+
+    // Merge the lane groups of this wave (lanes l and l ^ (k * LPP) hold the
+    // same slice for different positions).
+#pragma unroll
+    for (int mask = LPP; mask < 64; mask <<= 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float m_o = __shfl_xor(st.m[r], mask, 64);
+            const float l_o = __shfl_xor(st.l[r], mask, 64);
+            const float m_new = fmaxf(st.m[r], m_o);
+            const float a_self = fast_exp2(st.m[r] - m_new);
+            const float a_other = fast_exp2(m_o - m_new);
+            st.l[r] = st.l[r] * a_self + l_o * a_other;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float o = __shfl_xor(st.acc[r][i], mask, 64);
+                st.acc[r][i] = st.acc[r][i] * a_self + o * a_other;
+            }
+            st.m[r] = m_new;
+        }
+    }
+    if (group == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lds_acc[wave][r][sub * 16 + i] = st.acc[r][i];
+            if (sub == 0) {
+                lds_ml[wave][r][0] = st.m[r];
+                lds_ml[wave][r][1] = st.l[r];
+            }
+        }
+    }
+    __syncthreads();
+    // Merge the waves in wave order into this range's record.
+    float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
+    for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
+        const int r = idx / D;
+        const int d = idx % D;
+        float M = lds_ml[0][r][0];
+#pragma unroll
+        for (int w2 = 1; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2][r][0]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+            const float f = fast_exp2(lds_ml[w2][r][0] - M);
+            L += lds_ml[w2][r][1] * f;
+            A += lds_acc[w2][r][d] * f;
+        }
+        rec[idx] = A;
+        if (d == 0) {
+            rec[R * D + 4 * r + 0] = M;
+            rec[R * D + 4 * r + 1] = L;
+        }
+    }
 }
 
-template <int D, int R>
+// Sum over the D threads 0..D-1 (D/64 whole wavefronts) of the workgroup,
+// in a fixed order; `slots` is LDS scratch of D/64 floats. Every thread of
+// the workgroup must call it.
+template <int D>
+__device__ __forceinline__ float head_sum(float v, float *slots) {
+    const int t = threadIdx.x;
+    v = dev::wave_sum(v);
+    if (t < D && (t & 63) == 0) slots[t >> 6] = v;
+    __syncthreads();
+    float s = slots[0];
+#pragma unroll
+    for (int w = 1; w < D / 64; ++w) s += slots[w];
+    __syncthreads();
+    return s;
+}
+
+// out[h][d] = sum_s e^{m_s - M} acc_s[d] / sum_s e^{m_s - M} l_s over the
+// ranges that hold positions, in range order, for query head h = kvh * R + r.
+// Thread t takes four dimensions (column t % COLS) of the ranges congruent to
+// t / COLS; the SL partial merges are then combined in order. The first
+// kFirst ranges of each thread are loaded before the sequence's position is
+// known (every record of the scratch is readable; those of ranges past the
+// position are skipped).
+//
+// Decoder form: thread d < D also forms dimension d of the new position
+// (cached - 1): q and k get RMSNorm and RoPE, k and v are quantized to q8 per
+// 64-value group (one wavefront per group) and stored by the first query head
+// of the kv head, and the new row's score and dequantized value join the
+// merge last.
+template <int D, int R, bool Decoder>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernelArgs a) {
-    const uint32_t kvh = blockIdx.x;
+    constexpr int REC = R * D + 4 * R;
+    constexpr int COLS = D / 4;
+    constexpr int SL = 256 / COLS;
+    constexpr int kFirst = 8;
+    static_assert(D <= 256, "one thread per dimension");
+    const uint32_t h = blockIdx.x;
     const uint32_t b = blockIdx.y;
+    const uint32_t kvh = h / R;
+    const int r = (int)(h % R);
+    const int t = threadIdx.x;
+    const int col = t % COLS;
+    const int j = t / COLS;
+    const float *recs = a.partial + ((size_t)b * a.kv_heads + kvh) * a.splits * REC;
+    float m[kFirst], l[kFirst];
+    float4 v[kFirst];
+#pragma unroll
+    for (int q = 0; q < kFirst; ++q) {
+        const uint32_t s = j + q * SL;
+        if (s < a.splits) {
+            const float *rec = recs + (size_t)s * REC;
+            m[q] = rec[R * D + 4 * r];
+            l[q] = rec[R * D + 4 * r + 1];
+            v[q] = *reinterpret_cast<const float4 *>(rec + r * D + 4 * col);
+        }
+    }
+    const uint32_t kv_width = a.kv_heads * D;
+    const float *row = a.query + (size_t)b * a.query_stride;
+    float qx = 0.0f, kx = 0.0f, vx = 0.0f, wq = 0.0f, wk = 0.0f;
+    if (Decoder && t < D) {
+        qx = row[h * D + t];
+        kx = row[a.heads * D + kvh * D + t];
+        vx = row[a.heads * D + kv_width + kvh * D + t];
+        wq = a.q_norm[t];
+        wk = a.k_norm[t];
+    }
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
-    merge_ranges<D, R>(a, b, kvh, cached);
+    const uint32_t needed = (cached + a.chunk - 1) / a.chunk;
+    const uint32_t used = needed < a.splits ? needed : a.splits;
+    float M = kNeg, L = 0.0f;
+    float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int q = 0; q < kFirst; ++q)
+        if (j + q * SL < used) merge_state(M, L, A, m[q], l[q], v[q]);
+    for (uint32_t s = j + kFirst * SL; s < used; s += SL) {
+        const float *rec = recs + (size_t)s * REC;
+        merge_state(M, L, A, rec[R * D + 4 * r], rec[R * D + 4 * r + 1],
+                    *reinterpret_cast<const float4 *>(rec + r * D + 4 * col));
+    }
+    __shared__ float lds_m[256], lds_l[256];
+    __shared__ float4 lds_a[256];
+    __shared__ float lds_qk[2][D];
+    __shared__ float lds_v[D];
+    __shared__ float lds_sum[D / 64];
+    __shared__ float lds_score;
+    lds_m[t] = M;
+    lds_l[t] = L;
+    lds_a[t] = A;
+
+    if (Decoder) {
+        // decoder.zig:180-216 for dimension t of the new position.
+        const uint32_t newest = cached - 1;
+        const float ssq = head_sum<D>(t < D ? __fmul_rn(qx, qx) : 0.0f, lds_sum);
+        const float ssk = head_sum<D>(t < D ? __fmul_rn(kx, kx) : 0.0f, lds_sum);
+        if (t < D) {
+            const float inv_q = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssq, (float)D), a.eps)));
+            const float inv_k = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssk, (float)D), a.eps)));
+            lds_qk[0][t] = __fmul_rn(__fmul_rn(qx, inv_q), wq);
+            lds_qk[1][t] = __fmul_rn(__fmul_rn(kx, inv_k), wk);
+        }
+        __syncthreads();
+        float qr = 0.0f, code_k = 0.0f, scale_k = 0.0f;
+        if (t < D) {
+            const int half = D / 2;
+            const float c = a.rope_cos[(size_t)newest * half + (t % half)];
+            const float s = a.rope_sin[(size_t)newest * half + (t % half)];
+            const float qn = lds_qk[0][t], kn = lds_qk[1][t];
+            const float qp = lds_qk[0][t ^ half], kp = lds_qk[1][t ^ half];
+            qr = t < half ? __fsub_rn(__fmul_rn(qn, c), __fmul_rn(qp, s)) : __fadd_rn(__fmul_rn(qn, c), __fmul_rn(qp, s));
+            const float kr = t < half ? __fsub_rn(__fmul_rn(kn, c), __fmul_rn(kp, s))
+                                      : __fadd_rn(__fmul_rn(kn, c), __fmul_rn(kp, s));
+            // quantizeRow(.q8): this wavefront is one 64-value group.
+            const uint16_t kbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(kr)), 128.0f));
+            const uint16_t vbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(vx)), 128.0f));
+            scale_k = dev::f16_bits_to_f32(kbits);
+            const float scale_v = dev::f16_bits_to_f32(vbits);
+            const int ck = dev::quantize_one(kr, scale_k, -128, 127);
+            const int cv = dev::quantize_one(vx, scale_v, -128, 127);
+            code_k = (float)ck;
+            lds_v[t] = (float)cv * scale_v;
+            if (r == 0) {
+                const size_t pos_codes = (size_t)newest * kv_width + kvh * D + t;
+                const size_t pos_scales = (size_t)newest * (kv_width / 64) + kvh * (D / 64) + (t >> 6);
+                a.k_codes[b * a.code_stride + pos_codes] = (uint8_t)(ck + 128);
+                a.v_codes[b * a.code_stride + pos_codes] = (uint8_t)(cv + 128);
+                if ((t & 63) == 0) {
+                    reinterpret_cast<uint16_t *>(a.k_scales + b * a.scale_stride)[pos_scales] = kbits;
+                    reinterpret_cast<uint16_t *>(a.v_scales + b * a.scale_stride)[pos_scales] = vbits;
+                }
+            }
+        }
+        // Score of the new position (kernels.zig:727-735): per group
+        // scale * sum (u - 128) q, summed over groups, times the scaling.
+        const float part = dev::wave_sum(t < D ? code_k * qr : 0.0f);
+        if (t < D && (t & 63) == 0) lds_sum[t >> 6] = part * scale_k;
+        __syncthreads();
+        if (t == 0) {
+            float sc = lds_sum[0];
+#pragma unroll
+            for (int w = 1; w < D / 64; ++w) sc += lds_sum[w];
+            lds_score = sc * a.scaling;
+        }
+    }
+    __syncthreads();
+    if (t < COLS) {
+        for (int k = 1; k < SL; ++k) merge_state(M, L, A, lds_m[k * COLS + col], lds_l[k * COLS + col], lds_a[k * COLS + col]);
+        if (Decoder) {
+            const float4 vn = make_float4(lds_v[4 * col], lds_v[4 * col + 1], lds_v[4 * col + 2], lds_v[4 * col + 3]);
+            merge_state(M, L, A, lds_score, 1.0f, vn);
+        }
+        const float inv = 1.0f / L;
+        const float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+        *reinterpret_cast<float4 *>(a.out + ((size_t)b * a.heads + h) * D + 4 * col) = o;
+    }
 }
 
 // decoder.zig:94-105: quantizeRow(.q8) of one key row and one value row into
@@ -497,11 +577,13 @@ bool attention_supported(uint32_t head_dim, uint32_t ratio) {
 
 #define QWH_ATTN_CASE(D_, R_)                                                                       \
     if (a.head_dim == D_ && R == R_) {                                                              \
-        if (decoder)                                                                                \
+        if (decoder) {                                                                              \
             attention_kernel<D_, R_, true><<<dim3(splits, a.kv_heads, a.batch), 256, 0, s>>>(k);    \
-        else                                                                                        \
+            attention_combine_kernel<D_, R_, true><<<dim3(a.heads, a.batch), 256, 0, s>>>(k);       \
+        } else {                                                                                    \
             attention_kernel<D_, R_, false><<<dim3(splits, a.kv_heads, a.batch), 256, 0, s>>>(k);   \
-        attention_combine_kernel<D_, R_><<<dim3(a.kv_heads, a.batch), 256, 0, s>>>(k);              \
+            attention_combine_kernel<D_, R_, false><<<dim3(a.heads, a.batch), 256, 0, s>>>(k);      \
+        }                                                                                           \
         return hipGetLastError();                                                                   \
     }
 
@@ -520,13 +602,14 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
     k.cached_dev = a.cached_dev;
     k.cached = a.cached;
     k.cached_bias = a.cached_bias;
+    k.rows = a.capacity;
     k.heads = a.heads;
     k.kv_heads = a.kv_heads;
     k.chunk = chunk;
     k.splits = splits;
     k.scale_stride = a.scale_stride;
     k.code_stride = a.code_stride;
-    k.scaling = 1.0f / sqrtf((float)a.head_dim);  // kernels.zig:727
+    k.scaling = kLog2e / sqrtf((float)a.head_dim);  // kernels.zig:727, in base 2
     k.partial = static_cast<float *>(scratch);
     k.out = a.out;
     k.q_norm = a.q_norm;

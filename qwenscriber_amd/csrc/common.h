@@ -86,14 +86,17 @@ size_t q4_digit_bytes(uint32_t tokens, uint32_t cols);
 hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32_t cols,
                           void *digits);
 // The activations a q4 GEMV reads: prepared digit planes, or f32 values the
-// kernel encodes itself -- as they are, after RMSNorm with `norm` / `eps`,
-// or as silu(gate) * up of a tokens x 2K gate | up buffer.
+// kernel encodes itself -- as they are, or after RMSNorm with `norm` / `eps`.
+// With `pairs`, rows 2j and 2j+1 of the matrix are a gate row and its up row
+// (kernels.zig:233-239 siluMul): the GEMV writes silu(gate_j) * up_j to
+// out[t][j] (N/2 values per token) instead of the N products.
 struct GemvInput {
-    enum Mode { Digits = 0, F32 = 1, RmsNorm = 2, Silu = 3 } mode = Digits;
+    enum Mode { Digits = 0, F32 = 1, RmsNorm = 2 } mode = Digits;
     const void *digits = nullptr;
     const float *x = nullptr;
     const float *norm = nullptr;
     float eps = 0.0f;
+    bool pairs = false;
 };
 // True when a q4 matrix of this shape has a kernel for the f32 input forms.
 bool gemv_q4_fused_supported(uint32_t rows, uint32_t cols);
@@ -111,7 +114,7 @@ size_t batch_digit_bytes(uint32_t tokens, uint32_t cols);
 hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols,
                              void *digits);
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                float *out, const float *residual);
+                                float *out, const float *residual, bool pairs = false);
 
 // q4 GEMM with bf16 activations (gemm.hip).
 hipError_t launch_gemm_q4_bf16(hipStream_t s, const uint16_t *x, const Matrix &w,

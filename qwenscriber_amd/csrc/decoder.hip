@@ -6,18 +6,21 @@
 // once into a HIP graph and replays without host work; a greedy loop replays
 // it back to back, the argmax of one step feeding the embedding of the next.
 //
-// Per layer (decoder.zig:164-272), five launches:
+// Per layer (decoder.zig:164-272), at batch 1:
 //   gemv q4     rmsNormInto(attention_norm) formed in the GEMV prologue;
 //               q | k | v rows fused into one matrix
 //   attention   per-head rmsNorm of q and k, ropeInPlace at the position,
 //               appendCacheRow (q8) of k and v, decodeAttentionStepQ8 over
-//               position + 1 rows
+//               position + 1 rows (split over position ranges)
+//   combine     merge of the ranges
 //   gemv q4     out projection, residual added in the GEMV epilogue
-//   gemv q4     rmsNormInto(ffn_norm) in the prologue; gate | up rows fused
-//   gemv q4     siluMul in the prologue; down projection, residual added
+//   gemv q4     rmsNormInto(ffn_norm) in the prologue; gate and up rows
+//               interleaved, siluMul of each pair in the epilogue
+//   gemv q4     down projection, residual added
 // then rmsNormInto(final) + lm_head GEMV -> argmax (first maximum wins).
+// At batch > 1 each GEMV is a digit-plane pass plus the matrix-core GEMV.
 // Shapes without a fused GEMV kernel (or QWH_DECODER_UNFUSED set) run the
-// norm / SiLU / digit-plane kernels below as separate launches instead.
+// norm / digit-plane kernels below as separate launches instead.
 #include <cfloat>
 #include <cmath>
 #include <cstring>
@@ -116,34 +119,6 @@ __global__ __launch_bounds__(256) void rmsnorm_digits_kernel(const float *x, con
 #pragma unroll
         for (int k = 0; k < 8; ++k)
             v[k] = valid ? __fmul_rn(__fmul_rn(row[g8 * 8 + k], inverse_rms), weight[g8 * 8 + k]) : 0.0f;
-        emit_digits(v, valid, (size_t)b * T + g8 / 4, g8 & 3u, words, mult);
-    }
-}
-
-// kernels.zig:233-239 siluMul (math.zig:69-71 silu) over the fused gate|up
-// output, emitting digit planes for the down projection.
-__global__ __launch_bounds__(256) void silu_digits_kernel(const float *gu, uint32_t ffn, uint32_t *words,
-                                                          float *mult) {
-    const uint32_t b = blockIdx.x;
-    const float *gate = gu + (size_t)b * 2 * ffn;
-    const float *up = gate + ffn;
-    const uint32_t groups8 = ffn / 8;
-    const uint32_t iters = (groups8 + 255) / 256;
-    const uint32_t T = ffn / 32;
-    for (uint32_t it = 0; it < iters; ++it) {
-        const uint32_t g8 = threadIdx.x + it * 256;
-        const bool valid = g8 < groups8;
-        float v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (valid) {
-                const float g = gate[g8 * 8 + k];
-                const float silu = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
-                v[k] = __fmul_rn(silu, up[g8 * 8 + k]);
-            } else {
-                v[k] = 0.0f;
-            }
-        }
         emit_digits(v, valid, (size_t)b * T + g8 / 4, g8 & 3u, words, mult);
     }
 }
@@ -312,40 +287,36 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
     // W * f(x) for one of the decoder's activation forms: in one kernel when
     // the GEMV forms them itself, else through a digit-plane pass.
     auto gemv = [&](GemvInput::Mode mode, const float *x, const float *norm, const Matrix &w, float *out,
-                    const float *residual) -> hipError_t {
+                    const float *residual, bool pairs) -> hipError_t {
+        GemvInput in;
+        in.mode = mode;
+        in.x = x;
+        in.norm = norm;
+        in.eps = c.eps;
+        in.pairs = pairs;
         if (d->batched) {
-            GemvInput in;
-            in.mode = mode;
-            in.x = x;
-            in.norm = norm;
-            in.eps = c.eps;
             const hipError_t e = launch_prep_batch(s, in, B, w.cols, d->batch_digits);
             if (e != hipSuccess) return e;
-            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual);
+            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs);
         }
-        if (d->fused) {
-            GemvInput in;
-            in.mode = mode;
-            in.x = x;
-            in.norm = norm;
-            in.eps = c.eps;
-            return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
-        }
+        if (d->fused) return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
         if (mode == GemvInput::RmsNorm) {
             rmsnorm_digits_kernel<<<B, 256, 0, s>>>(x, norm, w.cols, c.eps, words, mult_of(w.cols));
-        } else if (mode == GemvInput::Silu) {
-            silu_digits_kernel<<<B, 256, 0, s>>>(x, w.cols, words, mult_of(w.cols));
         } else {
             const hipError_t e = launch_prep_q4(s, x, B, w.cols, words);
             if (e != hipSuccess) return e;
         }
-        return launch_gemv_q4(s, ctx->cus, words, w, B, out, residual);
+        GemvInput pre;
+        pre.mode = GemvInput::Digits;
+        pre.digits = words;
+        pre.pairs = pairs;
+        return launch_gemv_q4_src(s, ctx->cus, pre, w, B, out, residual);
     };
     embed_q4_kernel<<<B, 256, 0, s>>>(d->tokens_dev, reinterpret_cast<const uint16_t *>(d->embed.scales),
                                       d->embed.data, c.hidden, d->hidden);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
-        err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr);
+        err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
         if (err != hipSuccess) break;
         // Per-head norms, RoPE, the cache append and the attention itself
         // (decoder.zig:180-253) in one launch.
@@ -375,15 +346,16 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         aa.code_stride = d->seq_stride;
         err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch);
         if (err != hipSuccess) break;
-        err = gemv(GemvInput::F32, d->attn, nullptr, L.o, d->hidden, d->hidden);
+        err = gemv(GemvInput::F32, d->attn, nullptr, L.o, d->hidden, d->hidden, false);
         if (err != hipSuccess) break;
-        err = gemv(GemvInput::RmsNorm, d->hidden, L.ffn_norm, L.gu, d->gu, nullptr);
+        // gate | up rows interleaved: the GEMV writes siluMul(gate, up).
+        err = gemv(GemvInput::RmsNorm, d->hidden, L.ffn_norm, L.gu, d->gu, nullptr, true);
         if (err != hipSuccess) break;
-        err = gemv(GemvInput::Silu, d->gu, nullptr, L.down, d->hidden, d->hidden);
+        err = gemv(GemvInput::F32, d->gu, nullptr, L.down, d->hidden, d->hidden, false);
     }
     if (err == hipSuccess) {
         if (want_logits) {
-            err = gemv(GemvInput::RmsNorm, d->hidden, d->final_norm, d->lm_head, d->logits, nullptr);
+            err = gemv(GemvInput::RmsNorm, d->hidden, d->final_norm, d->lm_head, d->logits, nullptr, false);
             if (err == hipSuccess) {
                 argmax_partial_kernel<<<dim3(d->arg_parts, B), 256, 0, s>>>(d->logits, c.vocab, d->arg_per_block,
                                                                              d->arg_v, d->arg_i);
@@ -439,13 +411,16 @@ void build_rope_tables(std::vector<float> &cos_t, std::vector<float> &sin_t, uin
     }
 }
 
-int32_t copy_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, const Matrix &src) {
+// Copies src's rows to rows row_offset + i * stride of dst (stride 1: a
+// contiguous block; stride 2: every other row, for the gate / up pairs).
+int32_t copy_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, const Matrix &src, uint32_t stride = 1) {
     const size_t gpr = dst.cols / 64;
     hipStream_t s = d->ctx->stream;
-    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(dst.scales + (size_t)row_offset * gpr * 2, src.scales,
-                                             (size_t)src.rows * gpr * 2, hipMemcpyDeviceToDevice, s), "copy scales"));
-    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(dst.data + (size_t)row_offset * gpr * 32, src.data,
-                                             (size_t)src.rows * gpr * 32, hipMemcpyDeviceToDevice, s), "copy data"));
+    const size_t sb = gpr * 2, db = gpr * 32;  // scale and code bytes per row
+    QWH_TRY(check_hip(d->ctx, hipMemcpy2DAsync(dst.scales + (size_t)row_offset * sb, sb * stride, src.scales, sb, sb,
+                                               src.rows, hipMemcpyDeviceToDevice, s), "copy scales"));
+    QWH_TRY(check_hip(d->ctx, hipMemcpy2DAsync(dst.data + (size_t)row_offset * db, db * stride, src.data, db, db,
+                                               src.rows, hipMemcpyDeviceToDevice, s), "copy data"));
     return QWH_OK;
 }
 
@@ -569,7 +544,7 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.hidden, reinterpret_cast<void **>(&d->hidden));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (d->qw + 2 * d->kvw), reinterpret_cast<void **>(&d->qkv));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->qw, reinterpret_cast<void **>(&d->attn));
-    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * 2 * c.ffn, reinterpret_cast<void **>(&d->gu));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.ffn, reinterpret_cast<void **>(&d->gu));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (size_t)c.vocab, reinterpret_cast<void **>(&d->logits));
     if (st == QWH_OK) st = dalloc(d, q4_digit_bytes(batch, widest), &d->digits);
     // QWH_DECODER_PER_TOKEN keeps batch > 1 on the per-token GEMV (for tests).
@@ -623,8 +598,8 @@ int32_t qwh_decoder_set_matrix(qwh_decoder *d, uint32_t kind, uint32_t layer, ui
     case QWH_T_K: QWH_TRY(check_matrix(d, m, d->kvw, c.hidden)); return copy_rows(d, L.qkv, d->qw, *m);
     case QWH_T_V: QWH_TRY(check_matrix(d, m, d->kvw, c.hidden)); return copy_rows(d, L.qkv, d->qw + d->kvw, *m);
     case QWH_T_O: QWH_TRY(check_matrix(d, m, c.hidden, d->qw)); return copy_rows(d, L.o, 0, *m);
-    case QWH_T_GATE: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, 0, *m);
-    case QWH_T_UP: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, c.ffn, *m);
+    case QWH_T_GATE: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, 0, *m, 2);
+    case QWH_T_UP: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, 1, *m, 2);
     case QWH_T_DOWN: QWH_TRY(check_matrix(d, m, c.hidden, c.ffn)); return copy_rows(d, L.down, 0, *m);
     default: return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "unknown matrix kind %u", kind);
     }
@@ -660,7 +635,18 @@ int32_t qwh_decoder_init_synthetic(qwh_decoder *d, uint32_t seed) {
     const size_t temp_values = (size_t)64 << 20;
     float *temp = nullptr;
     QWH_TRY(check_hip(d->ctx, hipMalloc(&temp, temp_values * 4), "synthetic temp"));
-    int32_t st = synth_rows(d, d->embed, 0, c.vocab, seed, kStreamEmbed, 0.02f, temp, temp_values);
+    // Gate and up are generated into a staging matrix, then interleaved.
+    Matrix stage;
+    stage.format = QWH_FORMAT_Q4;
+    stage.rows = c.ffn;
+    stage.cols = c.hidden;
+    const size_t stage_gpr = (size_t)c.hidden / 64;
+    int32_t st = check_hip(d->ctx, hipMalloc(reinterpret_cast<void **>(&stage.scales), (size_t)c.ffn * stage_gpr * 2),
+                           "synthetic staging");
+    if (st == QWH_OK)
+        st = check_hip(d->ctx, hipMalloc(reinterpret_cast<void **>(&stage.data), (size_t)c.ffn * stage_gpr * 32),
+                       "synthetic staging");
+    if (st == QWH_OK) st = synth_rows(d, d->embed, 0, c.vocab, seed, kStreamEmbed, 0.02f, temp, temp_values);
     if (st == QWH_OK) st = synth_rows(d, d->lm_head, 0, c.vocab, seed, kStreamLmHead, 0.02f, temp, temp_values);
     for (uint32_t l = 0; l < c.layers && st == QWH_OK; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
@@ -669,12 +655,16 @@ int32_t qwh_decoder_init_synthetic(qwh_decoder *d, uint32_t seed) {
         if (st == QWH_OK) st = synth_rows(d, L.qkv, d->qw, d->kvw, seed, sb + 1, 0.02f, temp, temp_values);
         if (st == QWH_OK) st = synth_rows(d, L.qkv, d->qw + d->kvw, d->kvw, seed, sb + 2, 0.02f, temp, temp_values);
         if (st == QWH_OK) st = synth_rows(d, L.o, 0, c.hidden, seed, sb + 3, 0.02f, temp, temp_values);
-        if (st == QWH_OK) st = synth_rows(d, L.gu, 0, c.ffn, seed, sb + 4, 0.02f, temp, temp_values);
-        if (st == QWH_OK) st = synth_rows(d, L.gu, c.ffn, c.ffn, seed, sb + 5, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = synth_rows(d, stage, 0, c.ffn, seed, sb + 4, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = copy_rows(d, L.gu, 0, stage, 2);
+        if (st == QWH_OK) st = synth_rows(d, stage, 0, c.ffn, seed, sb + 5, 0.02f, temp, temp_values);
+        if (st == QWH_OK) st = copy_rows(d, L.gu, 1, stage, 2);
         if (st == QWH_OK) st = synth_rows(d, L.down, 0, c.hidden, seed, sb + 6, 0.02f, temp, temp_values);
     }
     const int32_t sync = check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "synthetic model");
     (void)hipFree(temp);
+    if (stage.scales) (void)hipFree(stage.scales);
+    if (stage.data) (void)hipFree(stage.data);
     return st != QWH_OK ? st : sync;
 }
 

@@ -24,12 +24,15 @@
 // multiplies the current one, and reduces the U row sums of each row with one
 // transposed butterfly over the row's L lanes.
 //
-// The q4 kernel takes its activations in one of four forms: prepared digit
-// planes, or f32 values that each wavefront encodes itself -- as they are,
+// The q4 kernel takes its activations in one of three forms: prepared digit
+// planes, or f32 values that each wavefront encodes itself -- as they are, or
 // after RMSNorm (kernels.zig:274-300, decoder.zig:165-172: the statistics of
-// the row are reduced over the lanes that hold it), or as siluMul of a
-// gate | up pair (kernels.zig:233-239). The last three let the decoder step
-// feed a GEMV straight from the previous kernel's f32 output.
+// the row are reduced over the lanes that hold it). The last two let the
+// decoder step feed a GEMV straight from the previous kernel's f32 output.
+// Its output is either the N row products (plus an optional residual) or,
+// for a matrix whose rows alternate gate and up rows, siluMul of each pair
+// (kernels.zig:233-239), so the gate/up projection hands the down projection
+// its f32 input directly.
 #include <cstdlib>
 
 #include "common.h"
@@ -174,20 +177,26 @@ __device__ __forceinline__ int q4_slice_dot(const uint4 codes, const uint32_t (&
 }
 
 // Forms of the q4 GEMV's activations.
-enum class Src : int { Digits = 0, F32 = 1, RmsNorm = 2, Silu = 3 };
+enum class Src : int { Digits = 0, F32 = 1, RmsNorm = 2 };
 
 struct GemvQ4Args {
     const uint32_t *words;  // Digits: planes, per token T * 24 words
     const float *mult;      // Digits: per token T multipliers
-    const float *x;         // F32 / RmsNorm: tokens x K; Silu: tokens x 2K (gate | up)
+    const float *x;         // F32 / RmsNorm: tokens x K
     const float *norm;      // RmsNorm: K weights
     float eps;              // RmsNorm epsilon
     const uint16_t *scales; // N * K/64
     const uint8_t *data;    // N * K/2
-    float *out;             // tokens x N
-    const float *residual;  // optional, tokens x N (may alias out)
+    float *out;             // tokens x N, or tokens x N/2 with pairs
+    const float *residual;  // optional, tokens x N (may alias out); not with pairs
     uint32_t n, k, t, row_groups;
+    uint32_t pairs;         // rows 2j, 2j+1 are gate_j, up_j: write silu(gate_j) * up_j
 };
+
+// siluMul of one gate / up pair (math.zig:69-71: silu(g) = g / (1 + exp(-g))).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+}
 
 // One 16-byte slice of codes and its group scale.
 struct Slice {
@@ -224,23 +233,10 @@ __device__ __forceinline__ void lane_activations(const GemvQ4Args &a, int li, ui
             m[s] = a.mult[(size_t)token * T + c];
         }
     } else {
-        const float *row = a.x + (size_t)token * a.k * (M == Src::Silu ? 2 : 1);
+        const float *row = a.x + (size_t)token * a.k;
         float v[S][32];
 #pragma unroll
         for (int s = 0; s < S; ++s) load32(row + (size_t)(li + s * L) * 32, v[s]);
-        if constexpr (M == Src::Silu) {
-            // silu(g) * u with silu(g) = g / (1 + exp(-g)) (math.zig:69-71).
-#pragma unroll
-            for (int s = 0; s < S; ++s) {
-                float u[32];
-                load32(row + a.k + (size_t)(li + s * L) * 32, u);
-#pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const float g = v[s][i];
-                    v[s][i] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u[i]);
-                }
-            }
-        }
         if constexpr (M == Src::RmsNorm) {
             // math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w. The row's
             // sum of squares is reduced over the L lanes that hold it.
@@ -289,7 +285,7 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
     const uint32_t u1 = (wave + 1) * units / nwaves;
     const uint32_t full_units = a.n / (U * RG);
     const uint32_t f1 = u1 < full_units ? u1 : full_units;
-    float *out = a.out + (size_t)token * a.n;
+    float *out = a.out + (size_t)token * (a.pairs ? a.n / 2 : a.n);
     const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
 
     // Unmasked loads of a unit whose rows all exist.
@@ -324,16 +320,27 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
             }
     };
 
+    // The residual of the row this lane writes for a unit, fetched with the
+    // unit's weights so the epilogue does not wait on another load.
+    auto load_res = [&](uint32_t unit) -> float {
+        const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+        return residual && row < a.n ? residual[row] : 0.0f;
+    };
+
     Slice A[U][S], B[U][S];
+    float resA = 0.0f, resB = 0.0f;
     // The first unit's loads go out before the activations are formed, so
     // their latency covers that work.
-    if (u0 < f1) load(A, u0);
+    if (u0 < f1) {
+        load(A, u0);
+        resA = load_res(u0);
+    }
 
     uint32_t D[S][24];
     float m[S];
     lane_activations<S, L, M>(a, li, token, D, m);
 
-    auto process = [&](const Slice (&src)[U][S], uint32_t unit) {
+    auto process = [&](const Slice (&src)[U][S], float res, uint32_t unit) {
         float acc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -345,9 +352,15 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
             }
         }
         const float total = reduce_rows<U, L>(acc, lane);
-        if ((li & ((L >> log_u) - 1)) == 0) {
-            const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
-            if (row < a.n) out[row] = (residual ? residual[row] : 0.0f) + total;
+        const bool writer = (li & ((L >> log_u) - 1)) == 0;
+        const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+        if (a.pairs) {
+            // Row + 1 sits in the next row of the row group (RG > 1), else
+            // in the next of the unit's U row groups.
+            const float partner = __shfl_down(total, RG > 1 ? L : (L >> log_u), kWave);
+            if (writer && (row & 1u) == 0 && row < a.n) out[row >> 1] = silu_mul(total, partner);
+        } else if (writer && row < a.n) {
+            out[row] = res + total;
         }
     };
 
@@ -360,16 +373,19 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
         uint32_t unit = u0;
         for (; unit + 1 < f1; unit += 2) {
             load(B, unit + 1);
-            process(A, unit);
-            load(A, unit + 2 < last ? unit + 2 : last);
-            process(B, unit + 1);
+            resB = load_res(unit + 1);
+            process(A, resA, unit);
+            const uint32_t next = unit + 2 < last ? unit + 2 : last;
+            load(A, next);
+            resA = load_res(next);
+            process(B, resB, unit + 1);
         }
-        if (unit < f1) process(A, unit);
+        if (unit < f1) process(A, resA, unit);
     }
     // The partial unit, if this wave owns it.
     for (uint32_t unit = u0 > full_units ? u0 : full_units; unit < u1; ++unit) {
         load_tail(B, unit);
-        process(B, unit);
+        process(B, load_res(unit), unit);
     }
 }
 
@@ -537,6 +553,21 @@ constexpr int kBlocksPerCu = 4;
 // Row groups per unit for the one-slice q4 kernels (the common shapes).
 constexpr int kUnitRows = 4;
 
+// Units each wavefront takes at least, when the kernel forms its own
+// activations (that prologue is paid once per wavefront). QWH_GEMV_MIN_UNITS
+// overrides it for tuning.
+int min_units_per_wave() {
+    static int units = 0;
+    if (units == 0) {
+        units = 1;
+        if (const char *env = getenv("QWH_GEMV_MIN_UNITS")) {
+            const int v = atoi(env);
+            if (v > 0) units = v;
+        }
+    }
+    return units;
+}
+
 int blocks_per_cu_cap() {
     static int cap = 0;
     if (cap == 0) {
@@ -552,7 +583,7 @@ int blocks_per_cu_cap() {
 // Blocks to launch: every unit covered, no more blocks than can be resident
 // at once (so each wave walks a contiguous range of units).
 template <typename Kernel>
-unsigned grid_blocks(Kernel kernel, uint32_t units, int cus) {
+unsigned grid_blocks(Kernel kernel, uint32_t units, int cus, uint32_t per_wave = 1) {
     static int resident = 0;
     if (resident == 0) {
         int per_cu = 0;
@@ -563,7 +594,7 @@ unsigned grid_blocks(Kernel kernel, uint32_t units, int cus) {
         const int cap = blocks_per_cu_cap();
         resident = per_cu < cap ? per_cu : cap;
     }
-    uint32_t blocks = (units + 3) / 4;
+    uint32_t blocks = (units + 4 * per_wave - 1) / (4 * per_wave);
     uint32_t limit = (uint32_t)(cus > 0 ? cus : 256) * (uint32_t)resident;
     // At most 4096 wavefronts: with rows * 4096 < 2^32 (checked by the
     // launcher) the kernels' wave * units products stay within 32 bits.
@@ -578,7 +609,8 @@ hipError_t launch_q4(hipStream_t s, int cus, GemvQ4Args args, uint32_t tokens) {
     args.row_groups = (args.n + (64 / L) - 1) / (64 / L);
     const uint32_t units = (args.row_groups + U - 1) / U;
     auto kernel = gemv_q4_kernel<S, L, U, M>;
-    kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);
+    const uint32_t per_wave = M == Src::Digits ? 1u : (uint32_t)min_units_per_wave();
+    kernel<<<dim3(grid_blocks(kernel, units, cus, per_wave), tokens), 256, 0, s>>>(args);
     return hipGetLastError();
 }
 
@@ -636,6 +668,7 @@ hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32
 
 hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
                               float *out, const float *residual) {
+    if (in.pairs && (w.rows & 1u)) return hipErrorInvalidValue;
     GemvQ4Args args{};
     const uint32_t T = w.cols / 32;
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
@@ -648,6 +681,7 @@ hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const
     args.x = in.x;
     args.norm = in.norm;
     args.eps = in.eps;
+    args.pairs = in.pairs ? 1u : 0u;
     if (in.mode == GemvInput::Digits) {
         const size_t chunks = (size_t)tokens * T;
         args.words = static_cast<const uint32_t *>(in.digits);
@@ -662,11 +696,10 @@ hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const
         case GemvInput::Digits: err = dispatch_q4<Src::Digits>(s, cus, args, tokens, S, L, done); break;
         case GemvInput::F32: err = dispatch_q4<Src::F32>(s, cus, args, tokens, S, L, done); break;
         case GemvInput::RmsNorm: err = dispatch_q4<Src::RmsNorm>(s, cus, args, tokens, S, L, done); break;
-        case GemvInput::Silu: err = dispatch_q4<Src::Silu>(s, cus, args, tokens, S, L, done); break;
         }
     }
     if (done) return err;
-    if (in.mode != GemvInput::Digits) return hipErrorNotSupported;
+    if (in.mode != GemvInput::Digits || in.pairs) return hipErrorNotSupported;
     args.row_groups = w.rows;
     gemv_q4_generic_kernel<<<dim3(grid_blocks(gemv_q4_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
     return hipGetLastError();

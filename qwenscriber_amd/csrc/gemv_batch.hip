@@ -56,10 +56,16 @@ struct BatchArgs {
     const float *mult;       // [token tiles][groups][16]
     const uint16_t *scales;  // N * K/64
     const uint8_t *data;     // N * K/2
-    float *out;              // tokens x N
-    const float *residual;   // optional, tokens x N (may alias out)
+    float *out;              // tokens x N, or tokens x N/2 with pairs
+    const float *residual;   // optional, tokens x N (may alias out); not with pairs
     uint32_t n, k, tokens;
+    uint32_t pairs;          // rows 2j, 2j+1 are gate_j, up_j: write silu(gate_j) * up_j
 };
+
+// siluMul of one gate / up pair (math.zig:69-71: silu(g) = g / (1 + exp(-g))).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+}
 
 struct Stage {
     v4i a[kStage][3];
@@ -97,6 +103,17 @@ __global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
                 st.a[i][p] = *reinterpret_cast<const v4i *>(dig + (size_t)gi * kGroupBytes + p * kPlaneBytes);
         }
     };
+    // Wave 0 writes the tile: its residuals are fetched now, with the first
+    // weights, rather than after the reduction.
+    float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t out_row = row0 + col;
+    if (wave == 0 && a.residual && out_row < a.n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t t = tile * kTokenTile + blk * 4 + r;
+            if (t < a.tokens) res[r] = a.residual[(size_t)t * a.n + out_row];
+        }
+    }
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     auto process = [&](const Stage &st, uint32_t g) {
 #pragma unroll
@@ -139,15 +156,18 @@ __global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
     for (int r = 0; r < 4; ++r) part[wave][r][lane] = acc[r];
     __syncthreads();
     if (wave != 0) return;
-    const uint32_t out_row = row0 + col;
-    if (out_row >= a.n) return;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const uint32_t t = tile * kTokenTile + blk * 4 + r;
-        if (t >= a.tokens) break;
         const float total = ((part[0][r][lane] + part[1][r][lane]) + part[2][r][lane]) + part[3][r][lane];
-        const size_t idx = (size_t)t * a.n + out_row;
-        a.out[idx] = (a.residual ? a.residual[idx] : 0.0f) + total;
+        if (a.pairs) {
+            // Row + 1 is the next lane's row (same token).
+            const float partner = __shfl_down(total, 1, 64);
+            if (t < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
+                a.out[(size_t)t * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
+        } else if (t < a.tokens && out_row < a.n) {
+            a.out[(size_t)t * a.n + out_row] = res[r] + total;
+        }
     }
 }
 
@@ -155,13 +175,12 @@ __global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
 // Activation digits. One workgroup per token (padding tokens write zeros);
 // thread i takes 8 consecutive values 8i .. 8i+7 of each 2048-value stretch,
 // so the 8 threads of a group are consecutive lanes. Forms as in the q4 GEMV:
-// f32 values as they are, RMSNorm (math.zig:120-130), or siluMul of a
-// gate | up row (kernels.zig:233-239, math.zig:69-71).
+// f32 values as they are, or RMSNorm (math.zig:120-130).
 // ---------------------------------------------------------------------------
-enum class Prep : int { F32 = 0, RmsNorm = 1, Silu = 2 };
+enum class Prep : int { F32 = 0, RmsNorm = 1 };
 
 struct PrepArgs {
-    const float *x;      // tokens x K (Silu: tokens x 2K)
+    const float *x;      // tokens x K
     const float *norm;   // RmsNorm weights
     float eps;
     uint32_t k, tokens;
@@ -183,7 +202,7 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
     const uint32_t tile = t / kTokenTile;
     const uint32_t tt = t % kTokenTile;
     const bool real = t < a.tokens;
-    const float *row = a.x + (size_t)(real ? t : 0) * a.k * (M == Prep::Silu ? 2 : 1);
+    const float *row = a.x + (size_t)(real ? t : 0) * a.k;
     float inv = 1.0f;
     if constexpr (M == Prep::RmsNorm) {
         // Sum of squares of the row: per thread, then across the workgroup
@@ -206,12 +225,6 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
         float v[8];
         if (real) {
             load8(row + e, v);
-            if constexpr (M == Prep::Silu) {
-                float u[8];
-                load8(row + a.k + e, u);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], __fadd_rn(1.0f, expf(-v[i]))), u[i]);
-            }
             if constexpr (M == Prep::RmsNorm) {
                 float w[8];
                 load8(a.norm + e, w);
@@ -272,14 +285,14 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     switch (in.mode) {
     case GemvInput::F32: prep_batch_kernel<Prep::F32><<<grid, 256, 0, s>>>(p); break;
     case GemvInput::RmsNorm: prep_batch_kernel<Prep::RmsNorm><<<grid, 256, 0, s>>>(p); break;
-    case GemvInput::Silu: prep_batch_kernel<Prep::Silu><<<grid, 256, 0, s>>>(p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens, float *out,
-                                const float *residual) {
+                                const float *residual, bool pairs) {
+    if (pairs && (w.rows & 1u)) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     BatchArgs a{};
     a.digits = static_cast<const uint8_t *>(digits);
@@ -291,6 +304,7 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
     a.n = w.rows;
     a.k = w.cols;
     a.tokens = tokens;
+    a.pairs = pairs ? 1u : 0u;
     gemv_q4_batch_kernel<<<dim3((w.rows + kRowTile - 1) / kRowTile, tiles), 256, 0, s>>>(a);
     return hipGetLastError();
 }
