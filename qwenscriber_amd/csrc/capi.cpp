@@ -420,7 +420,10 @@ int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, ui
     QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
     QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
     if (((uintptr_t)x_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "x must be 16-byte aligned");
-    return check_hip(ctx, launch_gemm_q4_bf16(ctx->stream, x_dev, *m, tokens, out_dev), "gemm q4 bf16");
+    const size_t scratch = gemm_scratch_bytes(ctx->cus, tokens, *m);
+    if (scratch) QWH_TRY(ensure_workspace(ctx, ctx->scratch, scratch));
+    return check_hip(ctx, launch_gemm_q4_bf16(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, ctx->scratch.ptr),
+                     "gemm q4 bf16");
 }
 
 int32_t qwh_quantize_rows(qwh_ctx *ctx, int32_t format, const float *values_dev, uint32_t rows, uint32_t cols,

@@ -116,9 +116,11 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
                                 float *out, const float *residual, bool pairs = false);
 
-// q4 GEMM with bf16 activations (gemm.hip).
-hipError_t launch_gemm_q4_bf16(hipStream_t s, const uint16_t *x, const Matrix &w,
-                               uint32_t tokens, float *out);
+// q4 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
+// partials: gemm_scratch_bytes (0 when the tiles alone fill the device).
+size_t gemm_scratch_bytes(int cus, uint32_t tokens, const Matrix &w);
+hipError_t launch_gemm_q4_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w,
+                               uint32_t tokens, float *out, void *scratch);
 
 // q8 decode attention (attention.hip). `cached` is per sequence when
 // cached_dev is non-null (device array of batch values), else uniform.

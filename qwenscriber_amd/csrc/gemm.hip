@@ -9,9 +9,16 @@
 // group's f16 scale (folding the scale into bf16 weights would round it).
 //
 // Tiling: a 256-thread workgroup computes a 128 x 128 tile of out; each wave a
-// 64 x 64 quarter as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16. Per group, the
-// activation tile (128 x 64 bf16) and the decoded weight tile (128 x 64 bf16)
-// are staged through LDS.
+// 64 x 64 quarter as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16. The K loop runs
+// over quantization groups and is software pipelined: while group g is
+// multiplied out of one LDS buffer, group g+1's activations and codes wait in
+// registers to be written (codes decoded to bf16) into the other buffer
+// before the iteration's single barrier, and group g+2's are in flight from
+// global memory.
+//
+// Split K: when the tiles alone cannot fill the device (few tokens, or few
+// weight rows), grid.z splits the groups into ranges; each range writes a
+// partial tile and a second kernel adds the ranges in order (deterministic).
 #include "common.h"
 #include "device.h"
 
@@ -23,20 +30,76 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int BK = 64;        // one quantization group
+constexpr int BK = 64;              // one quantization group
 constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row (padding against bank conflicts)
 
 struct GemmArgs {
     const uint16_t *x;       // M x K bf16
     const uint16_t *scales;  // N x K/64 f16
     const uint8_t *data;     // N x K/2 q4 codes
-    float *out;              // M x N
+    float *out;              // M x N, or splits x M x N partials
     uint32_t m, n, k;
+    uint32_t splits;
 };
 
-__global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(const GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds_a[BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint16_t lds_b[BN * LDS_STRIDE];
+// A group's tile data held in registers between its global loads and its
+// LDS stores: 4 x 16 B of activations and 16 B of codes per thread.
+struct Staged {
+    uint4 a[4];
+    uint4 codes;
+};
+
+__device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32_t m0, uint32_t n0, uint32_t g,
+                                           int tid) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int idx = tid + it * 256;  // 0..1023: 128 rows x 8 chunks of 8 bf16
+        const int row = idx >> 3;
+        const int col = (idx & 7) * 8;
+        st.a[it] = make_uint4(0, 0, 0, 0);
+        if (m0 + row < a.m) st.a[it] = *reinterpret_cast<const uint4 *>(a.x + (size_t)(m0 + row) * a.k + g * BK + col);
+    }
+    const int row = tid >> 1;
+    const int half = tid & 1;
+    st.codes = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+    if (n0 + row < a.n)
+        st.codes = *reinterpret_cast<const uint4 *>(a.data + (size_t)(n0 + row) * (a.k / 2) + g * 32 + half * 16);
+}
+
+// Activations as they are; codes decoded to the bf16 of u - 8.
+__device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, uint16_t *lds_b, int tid) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int idx = tid + it * 256;
+        const int row = idx >> 3;
+        const int col = (idx & 7) * 8;
+        *reinterpret_cast<uint4 *>(&lds_a[row * LDS_STRIDE + col]) = st.a[it];
+    }
+    const int row = tid >> 1;
+    const int half = tid & 1;
+    const uint32_t w[4] = {st.codes.x, st.codes.y, st.codes.z, st.codes.w};
+    uint32_t packed[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t sw = w[i] ^ 0x88888888u;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            // Nibbles 2p, 2p+1 of the dword are weights 8i + 2p, +1; the
+            // sign-extended nibble of u ^ 8 is u - 8, exact in bf16 (the top
+            // half of its f32).
+            const int c0 = (int)(sw << (28 - 8 * p)) >> 28;
+            const int c1 = (int)(sw << (24 - 8 * p)) >> 28;
+            packed[i * 4 + p] = (__float_as_uint((float)c0) >> 16) | (__float_as_uint((float)c1) & 0xffff0000u);
+        }
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(&lds_b[row * LDS_STRIDE + half * 32]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]);
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * LDS_STRIDE];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -44,8 +107,22 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(const GemmArgs a) {
     const int wn = wave & 1;   // wave's 64-column half
     const uint32_t n0 = blockIdx.x * BN;
     const uint32_t m0 = blockIdx.y * BM;
-    const uint32_t groups = a.k / BK;
-    const uint32_t gpr = groups;
+    const uint32_t gpr = a.k / BK;
+    const uint32_t g0 = blockIdx.z * gpr / a.splits;
+    const uint32_t g1 = (blockIdx.z + 1) * gpr / a.splits;
+
+    // MFMA operand coordinates (32x32x16 layout): lane -> row/col l % 32,
+    // k block 8 * (l / 32).
+    const int li = lane & 31;
+    const int kb = (lane >> 5) * 8;
+    // This lane's two output columns (one per 32-column MFMA tile).
+    uint32_t ncol[2];
+    const uint16_t *srow[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        ncol[j] = n0 + wn * 64 + j * 32 + li;
+        srow[j] = a.scales + (size_t)(ncol[j] < a.n ? ncol[j] : 0) * gpr;
+    }
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -53,122 +130,133 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(const GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-    // MFMA operand coordinates (32x32x16 layout): lane -> row/col l % 32,
-    // k block 8 * (l / 32).
-    const int li = lane & 31;
-    const int kb = (lane >> 5) * 8;
+    // Two groups in flight ahead of the one being multiplied: group g + 2's
+    // loads are issued while g is multiplied and g + 1 waits in registers.
+    Staged st0, st1;
+    if (g0 < g1) {
+        stage_load(a, st0, m0, n0, g0, tid);
+        if (g0 + 1 < g1) stage_load(a, st1, m0, n0, g0 + 1, tid);
+        stage_store(st0, lds_a[0], lds_b[0], tid);
+    }
+    __syncthreads();
 
-    for (uint32_t g = 0; g < groups; ++g) {
-        // Stage activations: 128 rows x 64 bf16 = 128 B per row, 16 B per
-        // thread-load, 4 loads per thread.
+    // One group: loads for g + 2 into `next2` (its previous content, group
+    // g, is already in LDS), multiply group g from LDS buffer `buf`, then
+    // store group g + 1 (in `next1`) into the other buffer.
+    auto step = [&](uint32_t g, int buf, Staged &next2, const Staged &next1) {
+        if (g + 2 < g1) stage_load(a, next2, m0, n0, g + 2, tid);
+        float s[2];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int idx = tid + it * 256;  // 0..1023
-            const int row = idx >> 3;
-            const int col = (idx & 7) * 8;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (m0 + row < a.m)
-                v = *reinterpret_cast<const uint4 *>(a.x + (size_t)(m0 + row) * a.k + g * BK + col);
-            *reinterpret_cast<uint4 *>(&lds_a[row * LDS_STRIDE + col]) = v;
-        }
-        // Stage decoded weights: row = tid / 2, 32 codes (16 bytes) per thread.
-        {
-            const int row = tid >> 1;
-            const int half = tid & 1;
-            uint4 codes = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-            if (n0 + row < a.n)
-                codes = *reinterpret_cast<const uint4 *>(a.data + (size_t)(n0 + row) * (a.k / 2) + g * 32 + half * 16);
-            const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
-            uint32_t packed[16];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t sw = w[i] ^ 0x88888888u;
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    // Nibbles 2p, 2p+1 of the dword are weights 8i + 2p, +1;
-                    // the sign-extended nibble of u ^ 8 is u - 8.
-                    const int c0 = (int)(sw << (28 - 8 * p)) >> 28;
-                    const int c1 = (int)(sw << (24 - 8 * p)) >> 28;
-                    const uint32_t b0 = __float_as_uint((float)c0) >> 16;
-                    const uint32_t b1 = __float_as_uint((float)c1) >> 16;
-                    packed[i * 4 + p] = b0 | (b1 << 16);
-                }
-            }
-            uint4 *dst = reinterpret_cast<uint4 *>(&lds_b[row * LDS_STRIDE + half * 32]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                dst[q] = make_uint4(packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]);
-        }
-        __syncthreads();
+        for (int j = 0; j < 2; ++j) s[j] = ncol[j] < a.n ? dev::f16_bits_to_f32(srow[j][g]) : 0.0f;
 
+        const uint16_t *la = lds_a[buf];
+        const uint16_t *lb = lds_b[buf];
         f32x16 part[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) part[i][j] = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             bf16x8 fa[2], fb[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int row = wm * 64 + i * 32 + li;
-                fa[i] = *reinterpret_cast<const bf16x8 *>(&lds_a[row * LDS_STRIDE + ks * 16 + kb]);
+                fa[i] = *reinterpret_cast<const bf16x8 *>(&la[row * LDS_STRIDE + ks * 16 + kb]);
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int row = wn * 64 + j * 32 + li;
-                fb[j] = *reinterpret_cast<const bf16x8 *>(&lds_b[row * LDS_STRIDE + ks * 16 + kb]);
+                fb[j] = *reinterpret_cast<const bf16x8 *>(&lb[row * LDS_STRIDE + ks * 16 + kb]);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], part[i][j], 0, 0, 0);
+                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], ks == 0 ? f32x16{} : part[i][j],
+                                                                         0, 0, 0);
         }
         // Scale each group's partial product by its weight row's scale: in the
         // 32x32 output layout every value a lane holds lies in column l % 32.
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t n = n0 + wn * 64 + j * 32 + li;
-            const float s = n < a.n ? dev::f16_bits_to_f32(a.scales[(size_t)n * gpr + g]) : 0.0f;
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(s, part[i][j][r], acc[i][j][r]);
-        }
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(s[j], part[i][j][r], acc[i][j][r]);
+        if (g + 1 < g1) stage_store(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
         __syncthreads();
+    };
+    // Unrolled by two so the staging registers are addressed statically.
+    uint32_t g = g0;
+    for (; g + 1 < g1; g += 2) {
+        step(g, 0, st0, st1);
+        step(g + 1, 1, st1, st0);
     }
+    if (g < g1) step(g, 0, st0, st1);
 
     // Store: value r of a lane is row 8 * (r / 4) + 4 * (l / 32) + r % 4 of the
     // 32x32 tile, column l % 32.
+    float *out = a.out + (size_t)blockIdx.z * a.m * a.n;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const uint32_t n = n0 + wn * 64 + j * 32 + li;
+            const uint32_t n = ncol[j];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-                if (m < a.m && n < a.n) a.out[(size_t)m * a.n + n] = acc[i][j][r];
+                if (m < a.m && n < a.n) out[(size_t)m * a.n + n] = acc[i][j][r];
             }
         }
     }
 }
 
+// out[i] = sum over ranges z (in order) of partial[z][i].
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *partial, uint32_t splits, size_t count,
+                                                          float *out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
+        float s = partial[i];
+        for (uint32_t z = 1; z < splits; ++z) s += partial[(size_t)z * count + i];
+        out[i] = s;
+    }
+}
+
+// Ranges of groups per tile so that the grid holds about one workgroup per
+// compute unit, each range at least two groups long, at most 8 ranges (the
+// partials cost 8 bytes of traffic per output per range).
+uint32_t gemm_splits(int cus, uint32_t tokens, const Matrix &w) {
+    const uint32_t tiles = ((w.rows + BN - 1) / BN) * ((tokens + BM - 1) / BM);
+    const uint32_t groups = w.cols / BK;
+    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256);
+    uint32_t splits = (target + tiles - 1) / tiles;
+    if (splits > groups / 2) splits = groups / 2;
+    if (splits > 8) splits = 8;
+    return splits < 1 ? 1 : splits;
+}
+
 }  // namespace
 
-hipError_t launch_gemm_q4_bf16(hipStream_t s, const uint16_t *x, const Matrix &w, uint32_t tokens,
-                               float *out) {
+size_t gemm_scratch_bytes(int cus, uint32_t tokens, const Matrix &w) {
+    const uint32_t splits = gemm_splits(cus, tokens, w);
+    return splits > 1 ? (size_t)splits * tokens * w.rows * sizeof(float) : 0;
+}
+
+hipError_t launch_gemm_q4_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w, uint32_t tokens,
+                               float *out, void *scratch) {
     GemmArgs args{};
     args.x = x;
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
     args.data = w.data;
-    args.out = out;
     args.m = tokens;
     args.n = w.rows;
     args.k = w.cols;
-    dim3 grid((w.rows + BN - 1) / BN, (tokens + BM - 1) / BM);
+    args.splits = gemm_splits(cus, tokens, w);
+    args.out = args.splits > 1 ? static_cast<float *>(scratch) : out;
+    dim3 grid((w.rows + BN - 1) / BN, (tokens + BM - 1) / BM, args.splits);
     gemm_q4_bf16_kernel<<<grid, 256, 0, s>>>(args);
+    if (args.splits > 1) {
+        const size_t count = (size_t)tokens * w.rows;
+        size_t blocks = (count + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        gemm_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(args.out, args.splits, count, out);
+    }
     return hipGetLastError();
 }
 
