@@ -18,11 +18,12 @@
 // slices. L = gcd(T, 64) lanes share a row, so a wavefront covers RG = 64/L
 // consecutive rows (a "row group") and each lane always handles the same S =
 // T/L slices of its row: its activation operands stay in registers for the
-// whole kernel while the wave walks row groups. A wavefront takes a
-// contiguous range of units of U row groups (the grid holds no more blocks
-// than can be resident), issues the next unit's 128-bit loads before it
-// multiplies the current one, and reduces the U row sums of each row with one
-// transposed butterfly over the row's L lanes.
+// whole kernel while the wave walks row groups. Units of U row groups are
+// dealt out grid-stride (wave w takes units w, w + waves, ...; the grid holds
+// no more blocks than can be resident), so the waves together stream one
+// compact window of the matrix; a wave issues its next unit's 128-bit loads
+// before it multiplies the current one, and reduces the U row sums of each
+// row with one transposed butterfly over the row's L lanes.
 //
 // The q4 kernel takes its activations in one of three forms: prepared digit
 // planes, or f32 values that each wavefront encodes itself -- as they are, or
@@ -260,8 +261,8 @@ __device__ __forceinline__ void lane_activations(const GemvQ4Args &a, int li, ui
     }
 }
 
-// The wavefront owns a contiguous range of units (U row groups of RG = 64/L
-// rows each). Lane l works on row l / L of each row group and on slices
+// The wavefront takes every nwaves-th unit (U row groups of RG = 64/L rows
+// each). Lane l works on row l / L of each row group and on slices
 // (l % L) + s * L, s < S, of that row.
 template <int S, int L, int U, Src M>
 __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
@@ -281,10 +282,10 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
     // and units * waves fits 32 bits, so 32-bit arithmetic suffices.
     const uint32_t row_bytes = a.k >> 1;
     const uint32_t units = (a.row_groups + U - 1) / U;
-    const uint32_t u0 = wave * units / nwaves;
-    const uint32_t u1 = (wave + 1) * units / nwaves;
     const uint32_t full_units = a.n / (U * RG);
-    const uint32_t f1 = u1 < full_units ? u1 : full_units;
+    // Grid-stride units: wave w takes units w, w + nwaves, ..., so at any
+    // moment the waves stream one compact window of the matrix.
+    const uint32_t count = full_units > wave ? (full_units - wave + nwaves - 1) / nwaves : 0;
     float *out = a.out + (size_t)token * (a.pairs ? a.n / 2 : a.n);
     const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
 
@@ -331,9 +332,9 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
     float resA = 0.0f, resB = 0.0f;
     // The first unit's loads go out before the activations are formed, so
     // their latency covers that work.
-    if (u0 < f1) {
-        load(A, u0);
-        resA = load_res(u0);
+    if (count) {
+        load(A, wave);
+        resA = load_res(wave);
     }
 
     uint32_t D[S][24];
@@ -368,24 +369,23 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
     // flight while the current one is multiplied. The prefetch index is
     // clamped rather than branched on, so the body is straight-line code and
     // the wait before each multiply covers only that unit's loads.
-    if (u0 < f1) {
-        const uint32_t last = f1 - 1;
-        uint32_t unit = u0;
-        for (; unit + 1 < f1; unit += 2) {
-            load(B, unit + 1);
-            resB = load_res(unit + 1);
-            process(A, resA, unit);
-            const uint32_t next = unit + 2 < last ? unit + 2 : last;
-            load(A, next);
-            resA = load_res(next);
-            process(B, resB, unit + 1);
-        }
-        if (unit < f1) process(A, resA, unit);
+    uint32_t i = 0;
+    for (; i + 1 < count; i += 2) {
+        const uint32_t ua = wave + i * nwaves, ub = ua + nwaves;
+        load(B, ub);
+        resB = load_res(ub);
+        process(A, resA, ua);
+        const uint32_t un = i + 2 < count ? ub + nwaves : ub;
+        load(A, un);
+        resA = load_res(un);
+        process(B, resB, ub);
     }
-    // The partial unit, if this wave owns it.
-    for (uint32_t unit = u0 > full_units ? u0 : full_units; unit < u1; ++unit) {
-        load_tail(B, unit);
-        process(B, load_res(unit), unit);
+    if (i < count) process(A, resA, wave + i * nwaves);
+    // The partial unit (rows past the end contribute nothing), taken by the
+    // wave whose stride reaches it.
+    if (full_units < units && full_units % nwaves == wave) {
+        load_tail(B, full_units);
+        process(B, load_res(full_units), full_units);
     }
 }
 
@@ -581,7 +581,7 @@ int blocks_per_cu_cap() {
 }
 
 // Blocks to launch: every unit covered, no more blocks than can be resident
-// at once (so each wave walks a contiguous range of units).
+// at once (each wave then walks its share of the units).
 template <typename Kernel>
 unsigned grid_blocks(Kernel kernel, uint32_t units, int cus, uint32_t per_wave = 1) {
     static int resident = 0;
