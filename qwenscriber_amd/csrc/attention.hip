@@ -72,12 +72,7 @@ __device__ __forceinline__ void unpack16(const uint4 w, float (&c)[16]) {
     }
 }
 
-template <int LPP>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int mask = 1; mask < LPP; mask <<= 1) v += __shfl_xor(v, mask, 64);
-    return v;
-}
+using dev::group_sum;
 
 // math.rmsNormInPlace (math.zig:120-130) of one head row spread over the LPP
 // lanes of a lane group (16 values per lane); `weight` holds this lane's 16
@@ -104,7 +99,7 @@ __device__ __forceinline__ void rope16(float (&x)[16], const float (&c)[16], con
     float y[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const float partner = __shfl_xor(x[i], LPP / 2, 64);
+        const float partner = dev::xor_lane<LPP / 2>(x[i]);
         y[i] = first ? __fsub_rn(__fmul_rn(x[i], c[i]), __fmul_rn(partner, s[i]))
                      : __fadd_rn(__fmul_rn(x[i], c[i]), __fmul_rn(partner, s[i]));
     }
@@ -193,6 +188,35 @@ __device__ __forceinline__ void merge_state(float &M, float &L, float4 &A, float
     A.z = A.z * fa + v.z * fb;
     A.w = A.w * fa + v.w * fb;
     M = m_new;
+}
+
+// One step of the merge of the lane groups: lanes l and l ^ MASK combine
+// their online-softmax states.
+template <int MASK, int R>
+__device__ __forceinline__ void merge_step(SoftmaxState<R> &st) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float m_o = dev::xor_lane<MASK>(st.m[r]);
+        const float l_o = dev::xor_lane<MASK>(st.l[r]);
+        const float m_new = fmaxf(st.m[r], m_o);
+        const float a_self = fast_exp2(st.m[r] - m_new);
+        const float a_other = fast_exp2(m_o - m_new);
+        st.l[r] = st.l[r] * a_self + l_o * a_other;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float o = dev::xor_lane<MASK>(st.acc[r][i]);
+            st.acc[r][i] = st.acc[r][i] * a_self + o * a_other;
+        }
+        st.m[r] = m_new;
+    }
+}
+
+template <int LPP, int R>
+__device__ __forceinline__ void merge_lane_groups(SoftmaxState<R> &st) {
+    if constexpr (LPP <= 4) merge_step<4, R>(st);
+    if constexpr (LPP <= 8) merge_step<8, R>(st);
+    if constexpr (LPP <= 16) merge_step<16, R>(st);
+    merge_step<32, R>(st);
 }
 
 template <int D, int R, bool Decoder>
@@ -311,24 +335,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
 
     // Merge the lane groups of this wave (lanes l and l ^ (k * LPP) hold the
     // same slice for different positions).
-#pragma unroll
-    for (int mask = LPP; mask < 64; mask <<= 1) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float m_o = __shfl_xor(st.m[r], mask, 64);
-            const float l_o = __shfl_xor(st.l[r], mask, 64);
-            const float m_new = fmaxf(st.m[r], m_o);
-            const float a_self = fast_exp2(st.m[r] - m_new);
-            const float a_other = fast_exp2(m_o - m_new);
-            st.l[r] = st.l[r] * a_self + l_o * a_other;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float o = __shfl_xor(st.acc[r][i], mask, 64);
-                st.acc[r][i] = st.acc[r][i] * a_self + o * a_other;
-            }
-            st.m[r] = m_new;
-        }
-    }
+    merge_lane_groups<LPP, R>(st);
     if (group == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {

@@ -46,8 +46,8 @@ __device__ __forceinline__ void emit_digits(const float v[8], bool valid, size_t
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, dev::xor_lane<1>(amax));
+    amax = fmaxf(amax, dev::xor_lane<2>(amax));
     const int e = dev::chunk_exponent(amax);
     uint32_t planes[6];
     dev::encode_digits8(v, e, planes);

@@ -12,15 +12,65 @@ namespace dev {
 
 constexpr int kWave = 64;
 
+// v of lane (lane ^ MASK) for a compile-time MASK < 64, without a trip
+// through LDS: DPP row permutes for 1, 2 (quad_perm), 4 (row_shr / row_shl
+// by 4, picked by lane bit 2) and 8 (row_ror:8, which is xor 8 within a row
+// of 16), and the gfx950 permlane swaps for 16 and 32 (each returns both
+// halves; lane bit 4 or 5 picks the partner's).
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float v) {
+    static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8 || MASK == 16 || MASK == 32, "mask");
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (MASK == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    } else if constexpr (MASK == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    } else if constexpr (MASK == 4) {
+        const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        const int down = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // lane - 4
+        const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);    // lane + 4
+        return __builtin_bit_cast(float, (lane & 4) ? down : up);
+    } else if constexpr (MASK == 8) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    } else if constexpr (MASK == 16) {
+        const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        const auto p = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+        return __builtin_bit_cast(float, (lane & 16) ? p[0] : p[1]);
+    } else {
+        const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        const auto p = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+        return __builtin_bit_cast(float, (lane & 32) ? p[0] : p[1]);
+    }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) v = fmaxf(v, __shfl_xor(v, mask, kWave));
-    return v;
+    v = fmaxf(v, xor_lane<32>(v));
+    v = fmaxf(v, xor_lane<16>(v));
+    v = fmaxf(v, xor_lane<8>(v));
+    v = fmaxf(v, xor_lane<4>(v));
+    v = fmaxf(v, xor_lane<2>(v));
+    return fmaxf(v, xor_lane<1>(v));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, kWave);
+    v += xor_lane<32>(v);
+    v += xor_lane<16>(v);
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    return v + xor_lane<1>(v);
+}
+
+// Sum over the lanes that differ from this one only in bits below N (N a
+// power of two <= 64): an all-reduce within aligned groups of N lanes.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 64) v += xor_lane<32>(v);
+    if constexpr (N >= 32) v += xor_lane<16>(v);
+    if constexpr (N >= 16) v += xor_lane<8>(v);
+    if constexpr (N >= 8) v += xor_lane<4>(v);
+    if constexpr (N >= 4) v += xor_lane<2>(v);
+    if constexpr (N >= 2) v += xor_lane<1>(v);
     return v;
 }
 

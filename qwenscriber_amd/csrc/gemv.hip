@@ -67,12 +67,14 @@ struct Log2<1> {
     static constexpr int value = 0;
 };
 
-// One exchange step of the transposed reduction: the lanes with `mask` set
+// One exchange step of the transposed reduction: the lanes with bit MASK set
 // keep b and send a, the others keep a and send b; returns keep + received.
-__device__ __forceinline__ float exchange(float a, float b, bool upper, int mask) {
+template <int MASK>
+__device__ __forceinline__ float exchange(float a, float b, int lane) {
+    const bool upper = (lane & MASK) != 0;
     const float send = upper ? a : b;
     const float keep = upper ? b : a;
-    return keep + __shfl_xor(send, mask, kWave);
+    return keep + dev::xor_lane<MASK>(send);
 }
 
 // Sums acc[0..U) (U <= 8) over the L lanes of each row (lanes l and l ^ m
@@ -87,34 +89,27 @@ __device__ __forceinline__ float reduce_rows(const float (&acc)[U], int lane) {
     if constexpr (U == 1) {
         v = acc[0];
     } else if constexpr (U == 2) {
-        v = exchange(acc[0], acc[1], (lane & (L / 2)) != 0, L / 2);
+        v = exchange<L / 2>(acc[0], acc[1], lane);
     } else if constexpr (U == 4) {
-        const bool up1 = (lane & (L / 2)) != 0;
-        const float b0 = exchange(acc[0], acc[2], up1, L / 2);
-        const float b1 = exchange(acc[1], acc[3], up1, L / 2);
-        v = exchange(b0, b1, (lane & (L / 4)) != 0, L / 4);
+        const float b0 = exchange<L / 2>(acc[0], acc[2], lane);
+        const float b1 = exchange<L / 2>(acc[1], acc[3], lane);
+        v = exchange<L / 4>(b0, b1, lane);
     } else {
-        const bool up1 = (lane & (L / 2)) != 0;
-        const bool up2 = (lane & (L / 4)) != 0;
-        const float b0 = exchange(acc[0], acc[4], up1, L / 2);
-        const float b1 = exchange(acc[1], acc[5], up1, L / 2);
-        const float b2 = exchange(acc[2], acc[6], up1, L / 2);
-        const float b3 = exchange(acc[3], acc[7], up1, L / 2);
-        const float c0 = exchange(b0, b2, up2, L / 4);
-        const float c1 = exchange(b1, b3, up2, L / 4);
-        v = exchange(c0, c1, (lane & (L / 8)) != 0, L / 8);
+        const float b0 = exchange<L / 2>(acc[0], acc[4], lane);
+        const float b1 = exchange<L / 2>(acc[1], acc[5], lane);
+        const float b2 = exchange<L / 2>(acc[2], acc[6], lane);
+        const float b3 = exchange<L / 2>(acc[3], acc[7], lane);
+        const float c0 = exchange<L / 4>(b0, b2, lane);
+        const float c1 = exchange<L / 4>(b1, b3, lane);
+        v = exchange<L / 8>(c0, c1, lane);
     }
-#pragma unroll
-    for (int mask = (L / 2) >> log_u; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, kWave);
-    return v;
+    return dev::group_sum<(L >> log_u)>(v);
 }
 
 // Sum of v over the L lanes of a row.
 template <int L>
 __device__ __forceinline__ float row_sum(float v) {
-#pragma unroll
-    for (int mask = L / 2; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask, kWave);
-    return v;
+    return dev::group_sum<L>(v);
 }
 
 // ---------------------------------------------------------------------------
@@ -140,8 +135,8 @@ __global__ __launch_bounds__(256) void prep_q4_kernel(const float *x, uint32_t t
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+    amax = fmaxf(amax, dev::xor_lane<1>(amax));
+    amax = fmaxf(amax, dev::xor_lane<2>(amax));
     const int e = dev::chunk_exponent(amax);
     uint32_t planes[6];
     dev::encode_digits8(v, e, planes);

@@ -238,9 +238,9 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = fmaxf(amax, dev::xor_lane<1>(amax));
+        amax = fmaxf(amax, dev::xor_lane<2>(amax));
+        amax = fmaxf(amax, dev::xor_lane<4>(amax));
         const int ex = dev::chunk_exponent(amax);
         const float up = __builtin_ldexpf(1.0f, 22 - ex);
         uint32_t u[8];
