@@ -55,7 +55,8 @@ struct AttnKernelArgs {
     float *partial;      // [batch][kv_heads][splits] records of R*D + 4*R floats
     float *out;          // [batch][heads][D]
     // Decoder form.
-    const float *q_norm, *k_norm, *rope_cos, *rope_sin;
+    const float *q_norm, *k_norm;
+    const float *rope_now;  // [batch][D]: cos (D/2) then sin (D/2) of the new position
     float eps;
 };
 
@@ -306,8 +307,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     if (Decoder) {
         const int j0 = (sub % (LPP / 2)) * 16;
         float rc[16], rs[16];
-        load16(a.rope_cos + (size_t)(cached - 1) * (D / 2) + j0, rc);
-        load16(a.rope_sin + (size_t)(cached - 1) * (D / 2) + j0, rs);
+        load16(a.rope_now + (size_t)b * D + j0, rc);
+        load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             rms_norm16<D>(q[r], wq, a.eps);
@@ -475,8 +476,8 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
         float qr = 0.0f, code_k = 0.0f, scale_k = 0.0f;
         if (t < D) {
             const int half = D / 2;
-            const float c = a.rope_cos[(size_t)newest * half + (t % half)];
-            const float s = a.rope_sin[(size_t)newest * half + (t % half)];
+            const float c = a.rope_now[(size_t)b * D + (t % half)];
+            const float s = a.rope_now[(size_t)b * D + half + (t % half)];
             const float qn = lds_qk[0][t], kn = lds_qk[1][t];
             const float qp = lds_qk[0][t ^ half], kp = lds_qk[1][t ^ half];
             qr = t < half ? __fsub_rn(__fmul_rn(qn, c), __fmul_rn(qp, s)) : __fadd_rn(__fmul_rn(qn, c), __fmul_rn(qp, s));
@@ -621,8 +622,7 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
     k.out = a.out;
     k.q_norm = a.q_norm;
     k.k_norm = a.k_norm;
-    k.rope_cos = a.rope_cos;
-    k.rope_sin = a.rope_sin;
+    k.rope_now = a.rope_now;
     k.eps = a.eps;
     QWH_ATTN_CASE(64, 1)
     QWH_ATTN_CASE(64, 2)

@@ -137,8 +137,10 @@ struct AttentionArgs {
     uint64_t scale_stride = 0, code_stride = 0;  // per sequence, bytes
     // Decoder form (q_norm non-null): each query row is the q | k | v
     // projection of the newest position cached - 1. q and k get per-head
-    // RMSNorm and RoPE at that position; k and v are appended to the cache.
-    const float *q_norm = nullptr, *k_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+    // RMSNorm and RoPE at that position (rope_now: per sequence, that
+    // position's table row, head_dim/2 cos then head_dim/2 sin); k and v are
+    // appended to the cache.
+    const float *q_norm = nullptr, *k_norm = nullptr, *rope_now = nullptr;
     float eps = 0.0f;
 };
 bool attention_supported(uint32_t head_dim, uint32_t ratio);

@@ -72,9 +72,19 @@ __device__ __forceinline__ float block_sum256(float v, float *lds) {
 }
 
 // decoder.zig:346-376 embeddingRow, q4: f32(u - 8) then times the scale.
+// Also copies the RoPE table row of the sequence's position (cos then sin,
+// 2 * half values) to rope_now, so the step's attention kernels read it
+// without first waiting for the position.
 __global__ __launch_bounds__(256) void embed_q4_kernel(const uint32_t *tokens, const uint16_t *scales,
-                                                       const uint8_t *data, uint32_t cols, float *hidden) {
+                                                       const uint8_t *data, uint32_t cols, float *hidden,
+                                                       const uint32_t *pos, const float *rope_cos,
+                                                       const float *rope_sin, uint32_t half, float *rope_now) {
     const uint32_t b = blockIdx.x;
+    if (threadIdx.x < 2 * half) {
+        const uint32_t p = pos[b];
+        const uint32_t t = threadIdx.x;
+        rope_now[(size_t)b * 2 * half + t] = t < half ? rope_cos[(size_t)p * half + t] : rope_sin[(size_t)p * half + t - half];
+    }
     const uint32_t token = tokens[b];
     const uint32_t gpr = cols / 64;
     const uint8_t *row = data + (size_t)token * (cols / 2);
@@ -220,6 +230,7 @@ struct qwh_decoder {
     Matrix embed, lm_head;
     float *final_norm = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
+    float *rope_now = nullptr;  // per sequence: the table row of its current position
     uint8_t *keys = nullptr, *values = nullptr;
     size_t cache_scales = 0, cache_codes = 0, layer_stride = 0, seq_stride = 0;
     uint32_t *tokens_dev = nullptr, *pos_dev = nullptr, *hist_base_dev = nullptr, *history_dev = nullptr;
@@ -313,7 +324,8 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         return launch_gemv_q4_src(s, ctx->cus, pre, w, B, out, residual);
     };
     embed_q4_kernel<<<B, 256, 0, s>>>(d->tokens_dev, reinterpret_cast<const uint16_t *>(d->embed.scales),
-                                      d->embed.data, c.hidden, d->hidden);
+                                      d->embed.data, c.hidden, d->hidden, d->pos_dev, d->rope_cos, d->rope_sin,
+                                      c.head_dim / 2, d->rope_now);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
         err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
@@ -328,8 +340,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         aa.query_stride = d->qw + 2 * d->kvw;
         aa.q_norm = L.q_norm;
         aa.k_norm = L.k_norm;
-        aa.rope_cos = d->rope_cos;
-        aa.rope_sin = d->rope_sin;
+        aa.rope_now = d->rope_now;
         aa.eps = c.eps;
         aa.k_scales = kl;
         aa.k_codes = kl + d->cache_scales;
@@ -545,6 +556,7 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (d->qw + 2 * d->kvw), reinterpret_cast<void **>(&d->qkv));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->qw, reinterpret_cast<void **>(&d->attn));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.ffn, reinterpret_cast<void **>(&d->gu));
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.head_dim, reinterpret_cast<void **>(&d->rope_now));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (size_t)c.vocab, reinterpret_cast<void **>(&d->logits));
     if (st == QWH_OK) st = dalloc(d, q4_digit_bytes(batch, widest), &d->digits);
     // QWH_DECODER_PER_TOKEN keeps batch > 1 on the per-token GEMV (for tests).

@@ -22,9 +22,10 @@
 // column. Layout of the digits, per 16-token tile and group:
 //   digits[tile][g][plane][token 0..15][64 bytes],  mult[tile][g][16] f32.
 //
-// Work split: a workgroup owns a 16-row tile of the output for one 16-token
-// tile; its four wavefronts take consecutive quarters of the groups and their
-// partial sums are added in wavefront order through LDS (deterministic).
+// Work split: a workgroup owns TILES 16-row tiles of the output (1, 2 or 4,
+// by the row count) for one 16-token tile; its four wavefronts take
+// consecutive quarters of the groups and their partial sums are added in
+// wavefront order through LDS (deterministic).
 #include "common.h"
 #include "device.h"
 
@@ -67,106 +68,138 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
+// Groups per pipeline stage: fewer when a wave has more tiles (registers).
+template <int TILES>
+constexpr int stage_groups() { return TILES >= 4 ? 2 : kStage; }
+
+template <int TILES>
 struct Stage {
-    v4i a[kStage][3];
-    uint2 w[kStage];
-    uint16_t s[kStage];
-    float4 m[kStage];
+    static constexpr int G = stage_groups<TILES>();
+    v4i a[G][3];
+    uint2 w[G][TILES];
+    uint16_t s[G][TILES];
+    float4 m[G];
 };
 
+// TILES 16-row tiles per wavefront: the activation digits of a group, loaded
+// once, feed TILES x 3 MFMAs.
+template <int TILES>
 __global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
+    constexpr int ROWS = kRowTile * TILES;  // rows of the workgroup (and of each wave)
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int col = lane & 15;     // weight row within the tile / token within the tile
+    const int col = lane & 15;     // weight row within a tile / token within the token tile
     const int blk = lane >> 4;     // 16-column block of the group
     const uint32_t gpr = a.k >> 6;
     const uint32_t tile = blockIdx.y;
-    const uint32_t row0 = blockIdx.x * kRowTile;
+    const uint32_t row0 = blockIdx.x * ROWS;
     const uint32_t g0 = wave * gpr / 4;
     const uint32_t g1 = (wave + 1) * gpr / 4;
-    uint32_t row = row0 + col;
-    if (row >= a.n) row = a.n - 1;  // loads stay in the matrix; the store is skipped
-    const uint8_t *wrow = a.data + (size_t)row * (a.k >> 1) + blk * 8;
-    const uint16_t *srow = a.scales + (size_t)row * gpr;
+    const uint8_t *wrow[TILES];
+    const uint16_t *srow[TILES];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+        uint32_t row = row0 + t * kRowTile + col;
+        if (row >= a.n) row = a.n - 1;  // loads stay in the matrix; the store is skipped
+        wrow[t] = a.data + (size_t)row * (a.k >> 1) + blk * 8;
+        srow[t] = a.scales + (size_t)row * gpr;
+    }
     const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes + col * 64 + blk * 16;
     const float *mul = a.mult + (size_t)tile * gpr * kTokenTile + blk * 4;
 
-    auto load = [&](Stage &st, uint32_t g) {
+    constexpr int G = stage_groups<TILES>();
+    auto load = [&](Stage<TILES> &st, uint32_t g) {
 #pragma unroll
-        for (int i = 0; i < kStage; ++i) {
+        for (int i = 0; i < G; ++i) {
             const uint32_t gi = g + i < g1 ? g + i : g1 - 1;  // clamped: no branch in the stage
-            st.w[i] = *reinterpret_cast<const uint2 *>(wrow + (size_t)gi * 32);
-            st.s[i] = srow[gi];
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                st.w[i][t] = *reinterpret_cast<const uint2 *>(wrow[t] + (size_t)gi * 32);
+                st.s[i][t] = srow[t][gi];
+            }
             st.m[i] = *reinterpret_cast<const float4 *>(mul + (size_t)gi * kTokenTile);
 #pragma unroll
             for (int p = 0; p < 3; ++p)
                 st.a[i][p] = *reinterpret_cast<const v4i *>(dig + (size_t)gi * kGroupBytes + p * kPlaneBytes);
         }
     };
-    // Wave 0 writes the tile: its residuals are fetched now, with the first
+    // Wave 0 writes the tiles: its residuals are fetched now, with the first
     // weights, rather than after the reduction.
-    float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t out_row = row0 + col;
-    if (wave == 0 && a.residual && out_row < a.n) {
+    float res[TILES][4] = {};
+    if (wave == 0 && a.residual) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t t = tile * kTokenTile + blk * 4 + r;
-            if (t < a.tokens) res[r] = a.residual[(size_t)t * a.n + out_row];
-        }
-    }
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto process = [&](const Stage &st, uint32_t g) {
-#pragma unroll
-        for (int i = 0; i < kStage; ++i) {
-            if (g + i >= g1) break;
-            const v4i b = expand_q4(st.w[i]);
-            const v4i zero = {0, 0, 0, 0};
-            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][0], b, zero, 0, 0, 0);
-            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][1], b, zero, 0, 0, 0);
-            const v4i d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][2], b, zero, 0, 0, 0);
-            const float s = dev::f16_bits_to_f32(st.s[i]);
-            const float m[4] = {st.m[i].x, st.m[i].y, st.m[i].z, st.m[i].w};
-            const int p0[4] = {d0.x, d0.y, d0.z, d0.w};
-            const int p1[4] = {d1.x, d1.y, d1.z, d1.w};
-            const int p2[4] = {d2.x, d2.y, d2.z, d2.w};
+        for (int t = 0; t < TILES; ++t) {
+            const uint32_t out_row = row0 + t * kRowTile + col;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float f = (float)(p0[r] + p1[r] * 256) + 65536.0f * (float)p2[r];
-                acc[r] = fmaf(f, s * m[r], acc[r]);
+                const uint32_t tok = tile * kTokenTile + blk * 4 + r;
+                if (out_row < a.n && tok < a.tokens) res[t][r] = a.residual[(size_t)tok * a.n + out_row];
+            }
+        }
+    }
+    float acc[TILES][4] = {};
+    auto process = [&](const Stage<TILES> &st, uint32_t g) {
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            if (g + i >= g1) break;
+            const float m[4] = {st.m[i].x, st.m[i].y, st.m[i].z, st.m[i].w};
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                const v4i b = expand_q4(st.w[i][t]);
+                const v4i zero = {0, 0, 0, 0};
+                const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][0], b, zero, 0, 0, 0);
+                const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][1], b, zero, 0, 0, 0);
+                const v4i d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][2], b, zero, 0, 0, 0);
+                const float s = dev::f16_bits_to_f32(st.s[i][t]);
+                const int p0[4] = {d0.x, d0.y, d0.z, d0.w};
+                const int p1[4] = {d1.x, d1.y, d1.z, d1.w};
+                const int p2[4] = {d2.x, d2.y, d2.z, d2.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float f = (float)(p0[r] + p1[r] * 256) + 65536.0f * (float)p2[r];
+                    acc[t][r] = fmaf(f, s * m[r], acc[t][r]);
+                }
             }
         }
     };
 
     if (g0 < g1) {
-        Stage A, B;
+        Stage<TILES> A, B;
         load(A, g0);
         uint32_t g = g0;
-        for (; g + kStage < g1; g += 2 * kStage) {
-            load(B, g + kStage);
+        for (; g + G < g1; g += 2 * G) {
+            load(B, g + G);
             process(A, g);
-            load(A, g + 2 * kStage < g1 ? g + 2 * kStage : g);
-            process(B, g + kStage);
+            load(A, g + 2 * G < g1 ? g + 2 * G : g);
+            process(B, g + G);
         }
         if (g < g1) process(A, g);
     }
 
-    // Lane l holds tokens 4 * (l / 16) + r of weight row l % 16.
-    __shared__ float part[4][4][64];
+    // Lane l holds tokens 4 * (l / 16) + r of weight row l % 16 of each tile.
+    __shared__ float part[4][TILES][4][64];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) part[wave][r][lane] = acc[r];
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[wave][t][r][lane] = acc[t][r];
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint32_t t = tile * kTokenTile + blk * 4 + r;
-        const float total = ((part[0][r][lane] + part[1][r][lane]) + part[2][r][lane]) + part[3][r][lane];
-        if (a.pairs) {
-            // Row + 1 is the next lane's row (same token).
-            const float partner = __shfl_down(total, 1, 64);
-            if (t < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
-                a.out[(size_t)t * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
-        } else if (t < a.tokens && out_row < a.n) {
-            a.out[(size_t)t * a.n + out_row] = res[r] + total;
+    for (int t = 0; t < TILES; ++t) {
+        const uint32_t out_row = row0 + t * kRowTile + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = tile * kTokenTile + blk * 4 + r;
+            const float total =
+                ((part[0][t][r][lane] + part[1][t][r][lane]) + part[2][t][r][lane]) + part[3][t][r][lane];
+            if (a.pairs) {
+                // Row + 1 is the next lane's row (same token).
+                const float partner = __shfl_down(total, 1, 64);
+                if (tok < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
+                    a.out[(size_t)tok * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
+            } else if (tok < a.tokens && out_row < a.n) {
+                a.out[(size_t)tok * a.n + out_row] = res[t][r] + total;
+            }
         }
     }
 }
@@ -305,7 +338,16 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
     a.k = w.cols;
     a.tokens = tokens;
     a.pairs = pairs ? 1u : 0u;
-    gemv_q4_batch_kernel<<<dim3((w.rows + kRowTile - 1) / kRowTile, tiles), 256, 0, s>>>(a);
+    // Tiles per wave: as many as keep about a workgroup per compute unit
+    // (each added tile divides the digit-plane reads per weight byte).
+    const uint32_t row_tiles = (w.rows + kRowTile - 1) / kRowTile;
+    if (row_tiles >= 4u * 256u) {
+        gemv_q4_batch_kernel<4><<<dim3((row_tiles + 3) / 4, tiles), 256, 0, s>>>(a);
+    } else if (row_tiles >= 2u * 256u) {
+        gemv_q4_batch_kernel<2><<<dim3((row_tiles + 1) / 2, tiles), 256, 0, s>>>(a);
+    } else {
+        gemv_q4_batch_kernel<1><<<dim3(row_tiles, tiles), 256, 0, s>>>(a);
+    }
     return hipGetLastError();
 }
 

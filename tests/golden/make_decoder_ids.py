@@ -1,0 +1,58 @@
+#!/usr/bin/env python3
+"""Writes tests/golden/decoder_1p7b_ids.json: greedy token ids of the CPU
+oracle (oracle/qwref.c, a restatement of decoder.zig:133-339) for the
+configs[4] decoder shape -- 28 layers, hidden 2048, 16 / 8 heads of 128,
+SwiGLU 6144, vocab 151936, RMSNorm eps 1e-6, RoPE theta 1e6, q4 weights from
+the synthetic generator under seed 4, each sequence's q8 cache prefilled with
+4096 random rows, then 256 greedy steps from the synthetic start token.
+
+Usage: python3 tests/golden/make_decoder_ids.py [--batch 16] [--steps 256]
+(the oracle is single-sequence at a time; about 0.3 s per step on 8 threads).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from oracle import oracle as o  # noqa: E402
+
+CONFIG = dict(hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151936,
+              max_positions=4352, eps=1e-6, theta=1e6)
+SEED = 4
+PREFILL = 4096
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--threads", type=int, default=os.cpu_count() or 1)
+    ap.add_argument("--out", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "decoder_1p7b_ids.json"))
+    args = ap.parse_args()
+    o.set_threads(args.threads)
+    t0 = time.time()
+    dec = o.Decoder(SEED, args.batch, **CONFIG)
+    print(f"model built in {time.time() - t0:.0f} s", flush=True)
+    ids = []
+    for b in range(args.batch):
+        dec.prefill_random(b, PREFILL)
+        t = o.start_token(SEED, b, CONFIG["vocab"])
+        seq = [t]
+        for s in range(args.steps):
+            t = dec.step(b, t)
+            seq.append(t)
+        ids.append(seq)
+        print(f"sequence {b}: {args.steps} steps, {time.time() - t0:.0f} s", flush=True)
+        with open(args.out, "w") as f:
+            json.dump({"config": CONFIG, "seed": SEED, "prefill": PREFILL, "steps": args.steps,
+                       "note": "ids[b][0] is the start token; ids[b][1:] the greedy steps",
+                       "ids": ids}, f)
+    dec.close()
+
+
+if __name__ == "__main__":
+    main()
