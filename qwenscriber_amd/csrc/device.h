@@ -189,25 +189,5 @@ __device__ __forceinline__ int chunk_exponent(float amax) {
     return e < -100 ? -100 : e;
 }
 
-// Encodes a whole chunk of 32 activations held by one lane: D[j * 4 + q] is
-// digit plane j of activations 8q .. 8q+7, m the chunk's multiplier.
-__device__ __forceinline__ void encode_chunk32(const float (&v)[32], uint32_t (&D)[kChunkWords], float &m) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
-    const int e = chunk_exponent(amax);
-    const float up = __builtin_ldexpf(1.0f, 22 - e);
-    m = __builtin_ldexpf(1.0f, e - 22);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        uint32_t w[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) w[k] = digit_word(v[q * 8 + k], up);
-        transpose_nibbles8(w);
-#pragma unroll
-        for (int j = 0; j < 6; ++j) D[j * 4 + q] = w[j];
-    }
-}
-
 }  // namespace dev
 }  // namespace qwh

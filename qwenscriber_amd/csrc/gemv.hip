@@ -200,59 +200,117 @@ struct Slice {
     uint16_t scale;
 };
 
-__device__ __forceinline__ void load32(const float *p, float (&v)[32]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = reinterpret_cast<const float4 *>(p)[i];
-        v[i * 4 + 0] = f.x; v[i * 4 + 1] = f.y; v[i * 4 + 2] = f.z; v[i * 4 + 3] = f.w;
-    }
 }
 
 // This lane's activation operands for slices c = li + s * L.
+// Activation digits of a whole row, encoded once per workgroup into LDS:
+// thread t takes values 8t .. 8t+7 of each 2048-value stretch (the four
+// threads of a 32-value chunk are consecutive lanes), so the block shares the
+// work instead of every wavefront encoding the row for itself. K is at most
+// 3 * 64 * 32 = 6144 (the fused shapes), i.e. at most 3 stretches.
+constexpr int kMaxChunks = 192;
+struct ActLds {
+    uint32_t words[kMaxChunks * 24];
+    float mult[kMaxChunks];
+    float partial[4];
+};
+
+template <Src M>
+__device__ __forceinline__ void block_encode(const GemvQ4Args &a, uint32_t token, ActLds &lds) {
+    const int tid = threadIdx.x;
+    const uint32_t k8 = a.k / 8;
+    const float *row = a.x + (size_t)token * a.k;
+    float v[3][8];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const uint32_t e8 = tid + p * 256;
+        if (e8 < k8) {
+            const float4 lo = reinterpret_cast<const float4 *>(row)[e8 * 2];
+            const float4 hi = reinterpret_cast<const float4 *>(row)[e8 * 2 + 1];
+            v[p][0] = lo.x; v[p][1] = lo.y; v[p][2] = lo.z; v[p][3] = lo.w;
+            v[p][4] = hi.x; v[p][5] = hi.y; v[p][6] = hi.z; v[p][7] = hi.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[p][i] = 0.0f;
+        }
+    }
+    if constexpr (M == Src::RmsNorm) {
+        // math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w, the sum of
+        // squares reduced over the block (threads, then the four waves in
+        // order).
+        float w[3][8];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+            const uint32_t e8 = tid + p * 256;
+            if (e8 < k8) {
+                const float4 lo = reinterpret_cast<const float4 *>(a.norm)[e8 * 2];
+                const float4 hi = reinterpret_cast<const float4 *>(a.norm)[e8 * 2 + 1];
+                w[p][0] = lo.x; w[p][1] = lo.y; w[p][2] = lo.z; w[p][3] = lo.w;
+                w[p][4] = hi.x; w[p][5] = hi.y; w[p][6] = hi.z; w[p][7] = hi.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[p][i] = 0.0f;
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[p][i], v[p][i]));
+        ss = dev::wave_sum(ss);
+        if ((tid & 63) == 0) lds.partial[tid >> 6] = ss;
+        __syncthreads();
+        ss = ((lds.partial[0] + lds.partial[1]) + lds.partial[2]) + lds.partial[3];
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)a.k), a.eps)));
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[p][i] = __fmul_rn(__fmul_rn(v[p][i], inv), w[p][i]);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const uint32_t e8 = tid + p * 256;
+        if (p * 256 >= (int)k8) break;  // uniform: no thread has values in this stretch
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[p][i]));
+        amax = fmaxf(amax, dev::xor_lane<1>(amax));
+        amax = fmaxf(amax, dev::xor_lane<2>(amax));
+        const int e = dev::chunk_exponent(amax);
+        uint32_t planes[6];
+        dev::encode_digits8(v[p], e, planes);
+        if (e8 < k8) {
+            const uint32_t chunk = e8 >> 2;
+            const uint32_t q = e8 & 3u;
+#pragma unroll
+            for (int j = 0; j < 6; ++j) lds.words[chunk * 24 + j * 4 + q] = planes[j];
+            if (q == 0) lds.mult[chunk] = __builtin_ldexpf(1.0f, e - 22);
+        }
+    }
+    __syncthreads();
+}
+
+// This lane's activation operands for slices c = li + s * L: from the
+// prepared planes in global memory, or from the block's LDS encoding.
 template <int S, int L, Src M>
 __device__ __forceinline__ void lane_activations(const GemvQ4Args &a, int li, uint32_t token,
-                                                 uint32_t (&D)[S][24], float (&m)[S]) {
+                                                 uint32_t (&D)[S][24], float (&m)[S], const ActLds &lds) {
     const uint32_t T = a.t;
-    if constexpr (M == Src::Digits) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const uint32_t c = li + s * L;
-            const uint4 *src = reinterpret_cast<const uint4 *>(a.words + ((size_t)token * T + c) * 24);
+    for (int s = 0; s < S; ++s) {
+        const uint32_t c = li + s * L;
+        const uint4 *src = M == Src::Digits
+                               ? reinterpret_cast<const uint4 *>(a.words + ((size_t)token * T + c) * 24)
+                               : reinterpret_cast<const uint4 *>(&lds.words[c * 24]);
 #pragma unroll
-            for (int j = 0; j < 6; ++j) {
-                const uint4 w = src[j];
-                D[s][j * 4 + 0] = w.x;
-                D[s][j * 4 + 1] = w.y;
-                D[s][j * 4 + 2] = w.z;
-                D[s][j * 4 + 3] = w.w;
-            }
-            m[s] = a.mult[(size_t)token * T + c];
+        for (int j = 0; j < 6; ++j) {
+            const uint4 w = src[j];
+            D[s][j * 4 + 0] = w.x;
+            D[s][j * 4 + 1] = w.y;
+            D[s][j * 4 + 2] = w.z;
+            D[s][j * 4 + 3] = w.w;
         }
-    } else {
-        const float *row = a.x + (size_t)token * a.k;
-        float v[S][32];
-#pragma unroll
-        for (int s = 0; s < S; ++s) load32(row + (size_t)(li + s * L) * 32, v[s]);
-        if constexpr (M == Src::RmsNorm) {
-            // math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w. The row's
-            // sum of squares is reduced over the L lanes that hold it.
-            float ss = 0.0f;
-#pragma unroll
-            for (int s = 0; s < S; ++s)
-#pragma unroll
-                for (int i = 0; i < 32; ++i) ss = __fadd_rn(ss, __fmul_rn(v[s][i], v[s][i]));
-            ss = row_sum<L>(ss);
-            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)a.k), a.eps)));
-#pragma unroll
-            for (int s = 0; s < S; ++s) {
-                float w[32];
-                load32(a.norm + (size_t)(li + s * L) * 32, w);
-#pragma unroll
-                for (int i = 0; i < 32; ++i) v[s][i] = __fmul_rn(__fmul_rn(v[s][i], inv), w[i]);
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < S; ++s) dev::encode_chunk32(v[s], D[s], m[s]);
+        m[s] = M == Src::Digits ? a.mult[(size_t)token * T + c] : lds.mult[c];
     }
 }
 
@@ -332,9 +390,11 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
         resA = load_res(wave);
     }
 
+    __shared__ __attribute__((aligned(16))) ActLds lds;
+    if constexpr (M != Src::Digits) block_encode<M>(a, token, lds);
     uint32_t D[S][24];
     float m[S];
-    lane_activations<S, L, M>(a, li, token, D, m);
+    lane_activations<S, L, M>(a, li, token, D, m, lds);
 
     auto process = [&](const Slice (&src)[U][S], float res, uint32_t unit) {
         float acc[U];

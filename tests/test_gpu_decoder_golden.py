@@ -1,0 +1,58 @@
+"""Greedy token ids at the configs[4] decoder shape (Qwen3-ASR-1.7B: 28
+layers, hidden 2048, 16 / 8 heads of 128, SwiGLU 6144, vocab 151936, q4
+weights, q8 cache prefilled to 4096 positions, seed 4) against the CPU
+oracle's ids in tests/golden/decoder_1p7b_ids.json (written by
+tests/golden/make_decoder_ids.py)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import qwenscriber_amd as qa
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "decoder_1p7b_ids.json")
+
+
+def load_golden():
+    if not os.path.exists(GOLDEN):
+        pytest.skip("golden ids not generated (tests/golden/make_decoder_ids.py)")
+    with open(GOLDEN) as f:
+        return json.load(f)
+
+
+def run(ctx, golden, batch):
+    cfg = golden["config"]
+    dec = qa.Decoder(ctx, batch=batch, **cfg)
+    try:
+        dec.init_synthetic(golden["seed"])
+        for b in range(batch):
+            dec.prefill_random(b, golden["prefill"], golden["seed"])
+        start = np.array([golden["ids"][b][0] for b in range(batch)], np.uint32)
+        return dec.generate(start, golden["steps"])
+    finally:
+        dec.close()
+
+
+def check(ids, golden, batch):
+    for b in range(batch):
+        expected = golden["ids"][b][1:]
+        got = ids[:, b].tolist()
+        first = next((i for i, (x, y) in enumerate(zip(got, expected)) if x != y), None)
+        assert first is None, f"sequence {b}: first difference at step {first}: {got[first]} != {expected[first]}"
+
+
+def test_batch1_greedy_ids_match_oracle(ctx):
+    # Batch 1 runs the lane-per-row GEMVs with fused activation forms.
+    golden = load_golden()
+    check(run(ctx, golden, 1), golden, 1)
+
+
+def test_batch16_greedy_ids_match_oracle(ctx):
+    # Batch 16 runs the matrix-core GEMVs; every sequence has its own cache.
+    golden = load_golden()
+    batch = len(golden["ids"])
+    if batch < 2:
+        pytest.skip("golden file holds one sequence")
+    check(run(ctx, golden, batch), golden, batch)
