@@ -200,9 +200,6 @@ struct Slice {
     uint16_t scale;
 };
 
-}
-
-// This lane's activation operands for slices c = li + s * L.
 // Activation digits of a whole row, encoded once per workgroup into LDS:
 // thread t takes values 8t .. 8t+7 of each 2048-value stretch (the four
 // threads of a 32-value chunk are consecutive lanes), so the block shares the
