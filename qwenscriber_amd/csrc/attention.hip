@@ -245,30 +245,41 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     const uint32_t code_col = kvh * D + sub * 16;
     constexpr uint32_t kSpan = STEP * kBlockPositions;
 
-    // A block of cache rows: this lane's slice of kBlockPositions positions.
+    // A block of cache rows: this lane's slice of kBlockPositions positions,
+    // scales as raw f16 bits.
     struct Block {
         uint4 kc[kBlockPositions], vc[kBlockPositions];
-        float ks[kBlockPositions], vs[kBlockPositions];
-        bool valid[kBlockPositions];
+        uint32_t ks[kBlockPositions], vs[kBlockPositions];
     };
-    // Loads rows base + ..., those below `limit`; the others read as empty.
+    // Loads rows base + ...; a row at or past `limit` (>= 1) loads row
+    // limit - 1 instead, and is masked out when the block is used. Every
+    // load is unconditional, so all of them are in flight together (a load
+    // under a branch waits for its data before the next one issues).
     auto load_block = [&](Block &blk, uint32_t base, uint32_t limit) {
 #pragma unroll
         for (int nb = 0; nb < kBlockPositions; ++nb) {
             const uint32_t p = base + nb * STEP + wave * PPW + group;
-            blk.valid[nb] = p < limit;
-            if (blk.valid[nb]) {
-                blk.kc[nb] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)p * kv_width + code_col);
-                blk.vc[nb] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)p * kv_width + code_col);
-                blk.ks[nb] = dev::f16_bits_to_f32(k_scales[(size_t)p * gpr + scale_col]);
-                blk.vs[nb] = dev::f16_bits_to_f32(v_scales[(size_t)p * gpr + scale_col]);
-            } else {
-                blk.kc[nb] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-                blk.vc[nb] = blk.kc[nb];
-                blk.ks[nb] = 0.0f;
-                blk.vs[nb] = 0.0f;
-            }
+            const uint32_t row = p < limit ? p : limit - 1;
+            blk.kc[nb] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)row * kv_width + code_col);
+            blk.vc[nb] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)row * kv_width + code_col);
+            blk.ks[nb] = k_scales[(size_t)row * gpr + scale_col];
+            blk.vs[nb] = v_scales[(size_t)row * gpr + scale_col];
         }
+    };
+    // Rows base + ... below `end` take part; the others (possibly never
+    // written, so their bits are arbitrary) get no score and zero scales, so
+    // no stale bits reach the sums.
+    auto use_block = [&](SoftmaxState<R> &st, const float (&q)[R][16], const Block &blk, uint32_t base,
+                         uint32_t end) {
+        bool valid[kBlockPositions];
+        float ks[kBlockPositions], vs[kBlockPositions];
+#pragma unroll
+        for (int nb = 0; nb < kBlockPositions; ++nb) {
+            valid[nb] = base + nb * STEP + wave * PPW + group < end;
+            ks[nb] = valid[nb] ? dev::f16_bits_to_f32((uint16_t)blk.ks[nb]) : 0.0f;
+            vs[nb] = valid[nb] ? dev::f16_bits_to_f32((uint16_t)blk.vs[nb]) : 0.0f;
+        }
+        attend<D, R, kBlockPositions>(st, q, blk.kc, blk.vc, ks, vs, valid, a.scaling);
     };
     // The first block is loaded before the sequence's position is known
     // (in the decoder it is a device value, one memory round trip away):
@@ -281,8 +292,13 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     float q[R][16];
 #pragma unroll
     for (int r = 0; r < R; ++r) load16(row + (kvh * R + r) * D + sub * 16, q[r]);
-    float wq[16];
-    if (Decoder) load16(a.q_norm + sub * 16, wq);
+    float wq[16], rc[16], rs[16];
+    if (Decoder) {
+        const int j0 = (sub % (LPP / 2)) * 16;
+        load16(a.q_norm + sub * 16, wq);
+        load16(a.rope_now + (size_t)b * D + j0, rc);
+        load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
+    }
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
     // The decoder form leaves the newest row (cached - 1) to the merge kernel.
     const uint32_t attended = Decoder ? cached - 1 : cached;
@@ -293,22 +309,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     __shared__ float lds_ml[kWaves][R][2];
 
     if (begin >= cached) return;  // no record: the merge reads ranges below cached only
-#pragma unroll
-    for (int nb = 0; nb < kBlockPositions; ++nb) {
-        const uint32_t p = begin + nb * STEP + wave * PPW + group;
-        if (!(p < end)) {
-            // Row beyond the position (possibly never written): no score,
-            // and a zero value scale so no stale bits reach the sums.
-            cur.valid[nb] = false;
-            cur.ks[nb] = 0.0f;
-            cur.vs[nb] = 0.0f;
-        }
-    }
     if (Decoder) {
-        const int j0 = (sub % (LPP / 2)) * 16;
-        float rc[16], rs[16];
-        load16(a.rope_now + (size_t)b * D + j0, rc);
-        load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             rms_norm16<D>(q[r], wq, a.eps);
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     for (uint32_t base = begin; base < end; base += kSpan) {
         const bool more = base + kSpan < end;
         if (more) load_block(nxt, base + kSpan, end);
-        attend<D, R, kBlockPositions>(st, q, cur.kc, cur.vc, cur.ks, cur.vs, cur.valid, a.scaling);
+        use_block(st, q, cur, base, end);
         if (more) cur = nxt;
     }
 
@@ -418,25 +419,27 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
     const float *recs = a.partial + ((size_t)b * a.kv_heads + kvh) * a.splits * REC;
     float m[kFirst], l[kFirst];
     float4 v[kFirst];
+    // Unconditional loads (a range past the last reads the last record and is
+    // dropped below), so that all kFirst of them are in flight together.
 #pragma unroll
     for (int q = 0; q < kFirst; ++q) {
-        const uint32_t s = j + q * SL;
-        if (s < a.splits) {
-            const float *rec = recs + (size_t)s * REC;
-            m[q] = rec[R * D + 4 * r];
-            l[q] = rec[R * D + 4 * r + 1];
-            v[q] = *reinterpret_cast<const float4 *>(rec + r * D + 4 * col);
-        }
+        const uint32_t s = j + q * SL < a.splits ? j + q * SL : a.splits - 1;
+        const float *rec = recs + (size_t)s * REC;
+        m[q] = rec[R * D + 4 * r];
+        l[q] = rec[R * D + 4 * r + 1];
+        v[q] = *reinterpret_cast<const float4 *>(rec + r * D + 4 * col);
     }
     const uint32_t kv_width = a.kv_heads * D;
     const float *row = a.query + (size_t)b * a.query_stride;
-    float qx = 0.0f, kx = 0.0f, vx = 0.0f, wq = 0.0f, wk = 0.0f;
+    float qx = 0.0f, kx = 0.0f, vx = 0.0f, wq = 0.0f, wk = 0.0f, rope_c = 0.0f, rope_s = 0.0f;
     if (Decoder && t < D) {
         qx = row[h * D + t];
         kx = row[a.heads * D + kvh * D + t];
         vx = row[a.heads * D + kv_width + kvh * D + t];
         wq = a.q_norm[t];
         wk = a.k_norm[t];
+        rope_c = a.rope_now[(size_t)b * D + (t % (D / 2))];
+        rope_s = a.rope_now[(size_t)b * D + D / 2 + (t % (D / 2))];
     }
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
     const uint32_t needed = (cached + a.chunk - 1) / a.chunk;
@@ -476,8 +479,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
         float qr = 0.0f, code_k = 0.0f, scale_k = 0.0f;
         if (t < D) {
             const int half = D / 2;
-            const float c = a.rope_now[(size_t)b * D + (t % half)];
-            const float s = a.rope_now[(size_t)b * D + half + (t % half)];
+            const float c = rope_c, s = rope_s;
             const float qn = lds_qk[0][t], kn = lds_qk[1][t];
             const float qp = lds_qk[0][t ^ half], kp = lds_qk[1][t ^ half];
             qr = t < half ? __fsub_rn(__fmul_rn(qn, c), __fmul_rn(qp, s)) : __fadd_rn(__fmul_rn(qn, c), __fmul_rn(qp, s));

@@ -5,6 +5,9 @@ configs[4] decoder shape -- 28 layers, hidden 2048, 16 / 8 heads of 128,
 SwiGLU 6144, vocab 151936, RMSNorm eps 1e-6, RoPE theta 1e6, q4 weights from
 the synthetic generator under seed 4, each sequence's q8 cache prefilled with
 4096 random rows, then 256 greedy steps from the synthetic start token.
+Each step also records the oracle's runner-up token and the two largest
+logits, so that a consumer can tell a flip between near-tied tokens (float
+summation order) from a wrong result.
 
 Usage: python3 tests/golden/make_decoder_ids.py [--batch 16] [--steps 256]
 (the oracle is single-sequence at a time; about 0.3 s per step on 8 threads).
@@ -14,6 +17,8 @@ import json
 import os
 import sys
 import time
+
+import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
@@ -37,20 +42,32 @@ def main():
     t0 = time.time()
     dec = o.Decoder(SEED, args.batch, **CONFIG)
     print(f"model built in {time.time() - t0:.0f} s", flush=True)
-    ids = []
+    ids, runner_up, top, second = [], [], [], []
     for b in range(args.batch):
         dec.prefill_random(b, PREFILL)
         t = o.start_token(SEED, b, CONFIG["vocab"])
-        seq = [t]
+        seq, ru, l1, l2 = [t], [], [], []
         for s in range(args.steps):
             t = dec.step(b, t)
+            logits = dec.logits(b)
+            rest = logits.copy()
+            rest[t] = -np.inf
+            r = int(np.argmax(rest))
             seq.append(t)
+            ru.append(r)
+            l1.append(float(logits[t]))
+            l2.append(float(logits[r]))
         ids.append(seq)
+        runner_up.append(ru)
+        top.append(l1)
+        second.append(l2)
         print(f"sequence {b}: {args.steps} steps, {time.time() - t0:.0f} s", flush=True)
         with open(args.out, "w") as f:
             json.dump({"config": CONFIG, "seed": SEED, "prefill": PREFILL, "steps": args.steps,
-                       "note": "ids[b][0] is the start token; ids[b][1:] the greedy steps",
-                       "ids": ids}, f)
+                       "note": "ids[b][0] is the start token; ids[b][1:] the greedy steps; "
+                               "runner_up[b][s], top[b][s], second[b][s]: the second-best token of "
+                               "step s and the two largest logits",
+                       "ids": ids, "runner_up": runner_up, "top": top, "second": second}, f)
     dec.close()
 
 

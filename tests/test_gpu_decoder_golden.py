@@ -35,12 +35,28 @@ def run(ctx, golden, batch):
         dec.close()
 
 
+# A step whose two best oracle logits lie within this fraction of the best
+# one may pick either: each logit is within 1e-3 relative of the oracle's
+# (float summation order differs), so their order is not fixed there.
+TIE = 2e-3
+
+
 def check(ids, golden, batch):
+    """Every sequence matches the oracle's greedy ids. The one exception is a
+    near tie: at the first differing step the GPU took the oracle's runner-up,
+    and the oracle's two best logits lie within TIE of each other. From there
+    the sequence continues from another token, so the comparison ends."""
     for b in range(batch):
         expected = golden["ids"][b][1:]
         got = ids[:, b].tolist()
         first = next((i for i, (x, y) in enumerate(zip(got, expected)) if x != y), None)
-        assert first is None, f"sequence {b}: first difference at step {first}: {got[first]} != {expected[first]}"
+        if first is None:
+            continue
+        msg = f"sequence {b}: first difference at step {first}: {got[first]} != {expected[first]}"
+        assert "runner_up" in golden, msg
+        top, second = golden["top"][b][first], golden["second"][b][first]
+        assert got[first] == golden["runner_up"][b][first], f"{msg} (runner-up {golden['runner_up'][b][first]})"
+        assert top - second <= TIE * abs(top), f"{msg}: oracle logits {top} and {second} are not a near tie"
 
 
 def test_batch1_greedy_ids_match_oracle(ctx):
