@@ -58,6 +58,9 @@ struct AttnKernelArgs {
     const float *q_norm, *k_norm;
     const float *rope_now;  // [batch][D]: cos (D/2) then sin (D/2) of the new position
     float eps;
+    // Optional digit-plane copy of the output (small-batch GEMV layout).
+    uint8_t *digits;
+    float *digit_mult;
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -389,6 +392,48 @@ __device__ __forceinline__ float head_sum(float v, float *slots) {
     return s;
 }
 
+// The output row of sequence b, head h, dimensions 4 col .. 4 col + 3, also
+// as the small-batch GEMV's activation digits (the layout and arithmetic of
+// prep_batch_kernel for F32 input, so the GEMV sees the same integers): per
+// 64-value group (16 consecutive threads), x_int = rint(x * 2^(22-e)) with
+// 2^e bounding the group's largest |x|, three signed base-256 digit planes;
+// within each 8-value block the even columns' bytes come first, then the odd
+// ones'. Threads 0 .. D/4 - 1 (whole rows of 16 lanes) call it together.
+template <int D>
+__device__ __forceinline__ void write_digits(const AttnKernelArgs &a, uint32_t b, uint32_t h, int col, float4 o) {
+    constexpr uint32_t kTokens = 16, kPlane = kTokens * 64, kGroup = 3 * kPlane;
+    float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+    amax = fmaxf(amax, dev::xor_lane<1>(amax));
+    amax = fmaxf(amax, dev::xor_lane<2>(amax));
+    amax = fmaxf(amax, dev::xor_lane<4>(amax));
+    amax = fmaxf(amax, dev::xor_lane<8>(amax));
+    const int ex = dev::chunk_exponent(amax);
+    const float up = __builtin_ldexpf(1.0f, 22 - ex);
+    const float v[4] = {o.x, o.y, o.z, o.w};
+    uint32_t u[4], pu[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
+        pu[i] = __builtin_bit_cast(uint32_t, dev::xor_lane<1>(__builtin_bit_cast(float, u[i])));
+    }
+    // Columns k = 0..3 of the 8-value block are the even thread's, 4..7 its
+    // partner's: the even thread writes the even columns, the odd one the
+    // odd columns.
+    const bool odd = col & 1;
+    const uint32_t c0 = odd ? pu[1] : u[0], c1 = odd ? pu[3] : u[2], c2 = odd ? u[1] : pu[0], c3 = odd ? u[3] : pu[2];
+    const uint32_t gpr = a.heads * D / 64;
+    const uint32_t g = (h * D + 4 * col) / 64;
+    const uint32_t tile = b / kTokens, tt = b % kTokens;
+    uint8_t *dst = a.digits + ((size_t)tile * gpr + g) * kGroup + tt * 64 + ((4 * col) % 64 / 8) * 8 + (odd ? 4 : 0);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const int sh = 8 * p;
+        *reinterpret_cast<uint32_t *>(dst + p * kPlane) = ((c0 >> sh) & 0xffu) | (((c1 >> sh) & 0xffu) << 8) |
+                                                           (((c2 >> sh) & 0xffu) << 16) | (((c3 >> sh) & 0xffu) << 24);
+    }
+    if (col % 16 == 0) a.digit_mult[((size_t)tile * gpr + g) * kTokens + tt] = __builtin_ldexpf(1.0f, ex - 22);
+}
+
 // out[h][d] = sum_s e^{m_s - M} acc_s[d] / sum_s e^{m_s - M} l_s over the
 // ranges that hold positions, in range order, for query head h = kvh * R + r.
 // Thread t takes four dimensions (column t % COLS) of the ranges congruent to
@@ -527,6 +572,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
         const float inv = 1.0f / L;
         const float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
         *reinterpret_cast<float4 *>(a.out + ((size_t)b * a.heads + h) * D + 4 * col) = o;
+        if (a.digits) write_digits<D>(a, b, h, col, o);
     }
 }
 
@@ -626,6 +672,11 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
     k.k_norm = a.k_norm;
     k.rope_now = a.rope_now;
     k.eps = a.eps;
+    if (a.digits) {
+        const uint32_t tiles = (a.batch + 15) / 16;
+        k.digits = static_cast<uint8_t *>(a.digits);
+        k.digit_mult = reinterpret_cast<float *>(k.digits + (size_t)tiles * (a.heads * a.head_dim / 64) * 3 * 16 * 64);
+    }
     QWH_ATTN_CASE(64, 1)
     QWH_ATTN_CASE(64, 2)
     QWH_ATTN_CASE(64, 4)

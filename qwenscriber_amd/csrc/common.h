@@ -142,6 +142,10 @@ struct AttentionArgs {
     // appended to the cache.
     const float *q_norm = nullptr, *k_norm = nullptr, *rope_now = nullptr;
     float eps = 0.0f;
+    // Optional: the output rows also as the small-batch GEMV's activation
+    // digit planes (launch_prep_batch's layout for batch rows of heads *
+    // head_dim values), so the output projection needs no separate pass.
+    void *digits = nullptr;
 };
 bool attention_supported(uint32_t head_dim, uint32_t ratio);
 size_t attention_scratch_bytes(int cus, const AttentionArgs &a);

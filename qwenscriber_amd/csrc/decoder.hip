@@ -261,6 +261,16 @@ int32_t dalloc(qwh_decoder *d, size_t bytes, void **out) {
         (void)hipGetLastError();
         return fail(d->ctx, QWH_E_OUT_OF_MEMORY, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(err));
     }
+    // Zeroed once here (at set-up, outside any graph), so that no buffer
+    // starts with stale bits: e.g. the digit planes of token slots past the
+    // batch, which some writers leave alone. On the context's stream, which
+    // does not wait for the default stream: the writes that follow on it
+    // must come after the zeros.
+    const hipError_t zero = hipMemsetAsync(p, 0, bytes ? bytes : 1, d->ctx->stream);
+    if (zero != hipSuccess) {
+        (void)hipFree(p);
+        return fail(d->ctx, QWH_E_DEVICE, "hipMemset(%zu) failed: %s", bytes, hipGetErrorString(zero));
+    }
     d->allocations.push_back(p);
     *out = p;
     return QWH_OK;
@@ -306,8 +316,10 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         in.eps = c.eps;
         in.pairs = pairs;
         if (d->batched) {
-            const hipError_t e = launch_prep_batch(s, in, B, w.cols, d->batch_digits);
-            if (e != hipSuccess) return e;
+            if (mode != GemvInput::Digits) {  // Digits: the planes are already in batch_digits
+                const hipError_t e = launch_prep_batch(s, in, B, w.cols, d->batch_digits);
+                if (e != hipSuccess) return e;
+            }
             return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs);
         }
         if (d->fused) return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
@@ -355,9 +367,13 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         aa.batch = B;
         aa.scale_stride = d->seq_stride;
         aa.code_stride = d->seq_stride;
+        // Batched: the attention output also arrives as the O projection's
+        // digit planes.
+        aa.digits = d->batched ? d->batch_digits : nullptr;
         err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch);
         if (err != hipSuccess) break;
-        err = gemv(GemvInput::F32, d->attn, nullptr, L.o, d->hidden, d->hidden, false);
+        err = gemv(d->batched ? GemvInput::Digits : GemvInput::F32, d->attn, nullptr, L.o, d->hidden, d->hidden,
+                   false);
         if (err != hipSuccess) break;
         // gate | up rows interleaved: the GEMV writes siluMul(gate, up).
         err = gemv(GemvInput::RmsNorm, d->hidden, L.ffn_norm, L.gu, d->gu, nullptr, true);

@@ -80,7 +80,9 @@ def test_config4_gqa_attention(ctx, ctx_len, batch):
 
 
 @pytest.mark.parametrize("cached,hd,heads,kvh", [(1, 128, 16, 8), (1000, 128, 16, 8), (129, 64, 8, 4),
-                                                 (300, 256, 4, 2), (77, 128, 8, 8), (513, 128, 16, 4)])
+                                                 (300, 256, 4, 2), (77, 128, 8, 8), (513, 128, 16, 4),
+                                                 (200, 64, 4, 4), (150, 64, 8, 2), (400, 128, 16, 2),
+                                                 (260, 256, 2, 2), (17, 128, 16, 8), (4099, 128, 16, 8)])
 def test_attention_edge_shapes(ctx, cached, hd, heads, kvh):
     kvw = kvh * hd
     planes = make_cache(cached, kvw, 12, 0)
