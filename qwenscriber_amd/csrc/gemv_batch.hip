@@ -22,10 +22,9 @@
 // column. Layout of the digits, per 16-token tile and group:
 //   digits[tile][g][plane][token 0..15][64 bytes],  mult[tile][g][16] f32.
 //
-// Work split: a workgroup owns TILES 16-row tiles of the output (1, 2 or 4,
-// by the row count) for one 16-token tile; its four wavefronts take
-// consecutive quarters of the groups and their partial sums are added in
-// wavefront order through LDS (deterministic).
+// Work split: see gemv_q4_batch_kernel.
+#include <cstdlib>
+
 #include "common.h"
 #include "device.h"
 
@@ -38,7 +37,6 @@ constexpr int kTokenTile = 16;
 constexpr int kRowTile = 16;
 constexpr int kPlaneBytes = kTokenTile * 64;           // one digit plane of a group
 constexpr int kGroupBytes = 3 * kPlaneBytes;            // three planes
-constexpr int kStage = 4;                               // groups per pipeline stage
 
 // Signed-byte codes of 8 packed q4 bytes (16 codes), in the column order
 // described above: (nibble + 0x78) ^ 0x80 = nibble - 8 as a two's complement
@@ -68,61 +66,53 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
-// Groups per pipeline stage: fewer when a wave has more tiles (registers).
-template <int TILES>
-constexpr int stage_groups() { return TILES >= 4 ? 2 : kStage; }
-
-template <int TILES>
-struct Stage {
-    static constexpr int G = stage_groups<TILES>();
-    v4i a[G][3];
-    uint2 w[G][TILES];
-    uint16_t s[G][TILES];
-    float4 m[G];
+// Work split. A workgroup owns TILES 16-row tiles of the output for one
+// 16-token tile; its W wavefronts split K into units of GR groups (wave w
+// takes units w, w + W, ...), and their partial sums are added in wavefront
+// order through LDS (deterministic). A wavefront issues all loads of a unit
+// at once -- one memory round trip per unit:
+//   weights  TILES x 16 rows x GR x 32 B, as 16-byte pieces, 64/(2 GR) rows
+//            per load instruction (each instruction reads whole GR x 32-byte
+//            stretches of rows, which streams; 8-byte loads of 16 rows per
+//            instruction measured 35 % slower), then moved through this
+//            wavefront's LDS into the MFMA operand layout (piece p of row r at
+//            slot p ^ (r mod 2 GR): the 16 rows one read touches hit distinct
+//            banks);
+//   digits   GR x 3 planes x 16 bytes per lane;
+//   scales   GR per row (one load per tile), multipliers GR float4s.
+template <int TILES, int GR>
+struct BatchShape {
+    static constexpr int ROWS = kRowTile * TILES;
+    static constexpr int PPR = 2 * GR;            // 16-byte pieces of a row in a unit
+    static constexpr int RPI = 64 / PPR;          // rows per load instruction
+    static constexpr int NW = (ROWS + RPI - 1) / RPI;  // weight loads per lane and unit
+    static constexpr int WAVE_BYTES = ROWS * PPR * 16 + TILES * 4 * 64 * 4;  // transpose + partial sums
+    static_assert(RPI >= 1 && (ROWS % RPI == 0 || NW == 1), "unit shape");
 };
 
-// TILES 16-row tiles per wavefront: the activation digits of a group, loaded
-// once, feed TILES x 3 MFMAs.
+// Wavefronts per workgroup at most: 12 with one tile (up to K = 6144 in one
+// unit per wave), 8 otherwise (registers).
 template <int TILES>
-__global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
-    constexpr int ROWS = kRowTile * TILES;  // rows of the workgroup (and of each wave)
+constexpr int max_waves() { return TILES == 1 ? 12 : 8; }
+
+template <int TILES, int GR>
+__global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(const BatchArgs a) {
+    using S = BatchShape<TILES, GR>;
+    constexpr int ROWS = S::ROWS, PPR = S::PPR, RPI = S::RPI, NW = S::NW;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int waves = blockDim.x >> 6;
     const int col = lane & 15;     // weight row within a tile / token within the token tile
     const int blk = lane >> 4;     // 16-column block of the group
     const uint32_t gpr = a.k >> 6;
+    const uint32_t units = gpr / GR;
     const uint32_t tile = blockIdx.y;
     const uint32_t row0 = blockIdx.x * ROWS;
-    const uint32_t g0 = wave * gpr / 4;
-    const uint32_t g1 = (wave + 1) * gpr / 4;
-    const uint8_t *wrow[TILES];
-    const uint16_t *srow[TILES];
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-        uint32_t row = row0 + t * kRowTile + col;
-        if (row >= a.n) row = a.n - 1;  // loads stay in the matrix; the store is skipped
-        wrow[t] = a.data + (size_t)row * (a.k >> 1) + blk * 8;
-        srow[t] = a.scales + (size_t)row * gpr;
-    }
-    const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes + col * 64 + blk * 16;
-    const float *mul = a.mult + (size_t)tile * gpr * kTokenTile + blk * 4;
+    const size_t row_bytes = a.k >> 1;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint4 *wl = reinterpret_cast<uint4 *>(smem + (size_t)wave * ROWS * PPR * 16);   // this wave's transpose
+    float *part = reinterpret_cast<float *>(smem + (size_t)waves * ROWS * PPR * 16);  // [W][TILES][4][64]
 
-    constexpr int G = stage_groups<TILES>();
-    auto load = [&](Stage<TILES> &st, uint32_t g) {
-#pragma unroll
-        for (int i = 0; i < G; ++i) {
-            const uint32_t gi = g + i < g1 ? g + i : g1 - 1;  // clamped: no branch in the stage
-#pragma unroll
-            for (int t = 0; t < TILES; ++t) {
-                st.w[i][t] = *reinterpret_cast<const uint2 *>(wrow[t] + (size_t)gi * 32);
-                st.s[i][t] = srow[t][gi];
-            }
-            st.m[i] = *reinterpret_cast<const float4 *>(mul + (size_t)gi * kTokenTile);
-#pragma unroll
-            for (int p = 0; p < 3; ++p)
-                st.a[i][p] = *reinterpret_cast<const v4i *>(dig + (size_t)gi * kGroupBytes + p * kPlaneBytes);
-        }
-    };
     // Wave 0 writes the tiles: its residuals are fetched now, with the first
     // weights, rather than after the reduction.
     float res[TILES][4] = {};
@@ -137,51 +127,75 @@ __global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
             }
         }
     }
+    const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes + col * 64 + blk * 16;
+    const float *mul = a.mult + (size_t)tile * gpr * kTokenTile + blk * 4;
     float acc[TILES][4] = {};
-    auto process = [&](const Stage<TILES> &st, uint32_t g) {
+    for (uint32_t unit = wave; unit < units; unit += waves) {
+        const uint32_t g0 = unit * GR;
+        // Loads (rows past the matrix read its last row; their results are
+        // never stored).
+        uint4 wv[NW];
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
-            if (g + i >= g1) break;
-            const float m[4] = {st.m[i].x, st.m[i].y, st.m[i].z, st.m[i].w};
+        for (int i = 0; i < NW; ++i) {
+            uint32_t row = row0 + i * RPI + lane / PPR;
+            if (row >= a.n) row = a.n - 1;
+            wv[i] = *reinterpret_cast<const uint4 *>(a.data + (size_t)row * row_bytes + g0 * 32 + 16 * (lane % PPR));
+        }
+        v4i dg[GR][3];
+        float4 mt[GR];
+#pragma unroll
+        for (int i = 0; i < GR; ++i) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                dg[i][p] = *reinterpret_cast<const v4i *>(dig + (size_t)(g0 + i) * kGroupBytes + p * kPlaneBytes);
+            mt[i] = *reinterpret_cast<const float4 *>(mul + (size_t)(g0 + i) * kTokenTile);
+        }
+        uint32_t sc[TILES][(GR + 1) / 2];
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
+            uint32_t row = row0 + t * kRowTile + col;
+            if (row >= a.n) row = a.n - 1;
+            __builtin_memcpy(sc[t], a.scales + (size_t)row * gpr + g0, 2 * GR);
+        }
+        // Weights into the MFMA layout through LDS (this wavefront's region
+        // only: LDS operations of one wavefront complete in order).
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const int r = i * RPI + lane / PPR;
+            if (r < ROWS) wl[r * PPR + ((lane % PPR) ^ (r % PPR))] = wv[i];  // (rows past the tile: GR = 1)
+        }
+#pragma unroll
+        for (int i = 0; i < GR; ++i) {
+            const float m[4] = {mt[i].x, mt[i].y, mt[i].z, mt[i].w};
 #pragma unroll
             for (int t = 0; t < TILES; ++t) {
-                const v4i b = expand_q4(st.w[i][t]);
+                const int r = t * kRowTile + col;
+                const int piece = 2 * i + (blk >> 1);
+                const uint2 w8 = *reinterpret_cast<const uint2 *>(
+                    reinterpret_cast<const uint8_t *>(&wl[r * PPR + (piece ^ (r % PPR))]) + 8 * (blk & 1));
+                const v4i b = expand_q4(w8);
                 const v4i zero = {0, 0, 0, 0};
-                const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][0], b, zero, 0, 0, 0);
-                const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][1], b, zero, 0, 0, 0);
-                const v4i d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.a[i][2], b, zero, 0, 0, 0);
-                const float s = dev::f16_bits_to_f32(st.s[i][t]);
+                const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dg[i][0], b, zero, 0, 0, 0);
+                const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dg[i][1], b, zero, 0, 0, 0);
+                const v4i d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dg[i][2], b, zero, 0, 0, 0);
+                const float sv = dev::f16_bits_to_f32((uint16_t)(sc[t][i / 2] >> (16 * (i % 2))));
                 const int p0[4] = {d0.x, d0.y, d0.z, d0.w};
                 const int p1[4] = {d1.x, d1.y, d1.z, d1.w};
                 const int p2[4] = {d2.x, d2.y, d2.z, d2.w};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float f = (float)(p0[r] + p1[r] * 256) + 65536.0f * (float)p2[r];
-                    acc[t][r] = fmaf(f, s * m[r], acc[t][r]);
+                for (int r2 = 0; r2 < 4; ++r2) {
+                    const float f = (float)(p0[r2] + p1[r2] * 256) + 65536.0f * (float)p2[r2];
+                    acc[t][r2] = fmaf(f, sv * m[r2], acc[t][r2]);
                 }
             }
         }
-    };
-
-    if (g0 < g1) {
-        Stage<TILES> A, B;
-        load(A, g0);
-        uint32_t g = g0;
-        for (; g + G < g1; g += 2 * G) {
-            load(B, g + G);
-            process(A, g);
-            load(A, g + 2 * G < g1 ? g + 2 * G : g);
-            process(B, g + G);
-        }
-        if (g < g1) process(A, g);
     }
 
     // Lane l holds tokens 4 * (l / 16) + r of weight row l % 16 of each tile.
-    __shared__ float part[4][TILES][4][64];
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part[wave][t][r][lane] = acc[t][r];
+        for (int r = 0; r < 4; ++r) part[((wave * TILES + t) * 4 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
@@ -190,8 +204,8 @@ __global__ __launch_bounds__(256) void gemv_q4_batch_kernel(const BatchArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = tile * kTokenTile + blk * 4 + r;
-            const float total =
-                ((part[0][t][r][lane] + part[1][t][r][lane]) + part[2][t][r][lane]) + part[3][t][r][lane];
+            float total = part[(t * 4 + r) * 64 + lane];
+            for (int w = 1; w < waves; ++w) total += part[((w * TILES + t) * 4 + r) * 64 + lane];
             if (a.pairs) {
                 // Row + 1 is the next lane's row (same token).
                 const float partner = __shfl_down(total, 1, 64);
@@ -338,17 +352,37 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
     a.k = w.cols;
     a.tokens = tokens;
     a.pairs = pairs ? 1u : 0u;
-    // Tiles per wave: as many as keep about a workgroup per compute unit
-    // (each added tile divides the digit-plane reads per weight byte).
+    // Tiles per workgroup: one (measured fastest up to the 12288-row gate|up
+    // projection), four for the very tall vocabulary projection (each added
+    // tile divides the digit-plane reads per weight byte).
     const uint32_t row_tiles = (w.rows + kRowTile - 1) / kRowTile;
-    if (row_tiles >= 4u * 256u) {
-        gemv_q4_batch_kernel<4><<<dim3((row_tiles + 3) / 4, tiles), 256, 0, s>>>(a);
-    } else if (row_tiles >= 2u * 256u) {
-        gemv_q4_batch_kernel<2><<<dim3((row_tiles + 1) / 2, tiles), 256, 0, s>>>(a);
-    } else {
-        gemv_q4_batch_kernel<1><<<dim3(row_tiles, tiles), 256, 0, s>>>(a);
+    const uint32_t gpr = w.cols / 64;
+    int tiles_per = row_tiles >= 4096u ? 4 : 1;
+    if (const char *env = getenv("QWH_BATCH_TILES")) {  // tuning override: 1, 2 or 4
+        const int v = atoi(env);
+        if (v == 1 || v == 2 || v == 4) tiles_per = v;
     }
-    return hipGetLastError();
+    // Groups per unit: 8 (4 with 4 tiles, for registers), lowered to divide
+    // the row's groups.
+    int gr = tiles_per >= 4 ? 4 : 8;
+    while (gpr % (uint32_t)gr) gr >>= 1;
+    const uint32_t units = gpr / (uint32_t)gr;
+    dim3 grid((row_tiles + tiles_per - 1) / tiles_per, tiles);
+#define QWH_BATCH_CASE(T_, G_)                                                                       \
+    if (tiles_per == T_ && gr == G_) {                                                               \
+        using S = BatchShape<T_, G_>;                                                                \
+        /* Wavefronts: the largest divisor of the unit count within the cap and 64 KB of LDS. */     \
+        uint32_t waves = 1;                                                                          \
+        for (uint32_t c = 1; c <= (uint32_t)max_waves<T_>() && c * S::WAVE_BYTES <= 65536u; ++c)     \
+            if (units % c == 0) waves = c;                                                           \
+        gemv_q4_batch_kernel<T_, G_><<<grid, 64 * waves, waves * S::WAVE_BYTES, s>>>(a);             \
+        return hipGetLastError();                                                                    \
+    }
+    QWH_BATCH_CASE(1, 8) QWH_BATCH_CASE(1, 4) QWH_BATCH_CASE(1, 2) QWH_BATCH_CASE(1, 1)
+    QWH_BATCH_CASE(2, 8) QWH_BATCH_CASE(2, 4) QWH_BATCH_CASE(2, 2) QWH_BATCH_CASE(2, 1)
+    QWH_BATCH_CASE(4, 4) QWH_BATCH_CASE(4, 2) QWH_BATCH_CASE(4, 1)
+#undef QWH_BATCH_CASE
+    return hipErrorInvalidValue;
 }
 
 }  // namespace qwh
