@@ -242,7 +242,10 @@ __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-template <Prep M>
+// ITERS > 0: K <= 2048 ITERS, and each thread loads all its values (and norm
+// weights) at once, keeps them in registers for both passes, so the kernel
+// is one memory round trip; ITERS == 0: any K, loaded stretch by stretch.
+template <Prep M, int ITERS>
 __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
     const uint32_t t = blockIdx.x;
     const uint32_t gpr = a.k >> 6;
@@ -250,16 +253,35 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
     const uint32_t tt = t % kTokenTile;
     const bool real = t < a.tokens;
     const float *row = a.x + (size_t)(real ? t : 0) * a.k;
+    constexpr int kHeld = ITERS > 0 ? ITERS : 1;
+    float held[kHeld][8], norm_w[kHeld][8];
+    if constexpr (ITERS > 0) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint32_t e = threadIdx.x * 8 + 2048u * it;
+            const uint32_t ec = e < a.k ? e : 0;  // past the row: a valid address, never used
+            load8(row + ec, held[it]);
+            if constexpr (M == Prep::RmsNorm) load8(a.norm + ec, norm_w[it]);
+        }
+    }
     float inv = 1.0f;
     if constexpr (M == Prep::RmsNorm) {
         // Sum of squares of the row: per thread, then across the workgroup
         // in a fixed order.
         float ss = 0.0f;
-        for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
-            float v[8];
-            load8(row + e, v);
+        if constexpr (ITERS > 0) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+            for (int it = 0; it < ITERS; ++it)
+                if (threadIdx.x * 8 + 2048u * it < a.k)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(held[it][i], held[it][i]));
+        } else {
+            for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
+                float v[8];
+                load8(row + e, v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+            }
         }
         ss = dev::wave_sum(ss);
         __shared__ float wsum[4];
@@ -268,20 +290,7 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
         ss = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
         inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)a.k), a.eps)));
     }
-    for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
-        float v[8];
-        if (real) {
-            load8(row + e, v);
-            if constexpr (M == Prep::RmsNorm) {
-                float w[8];
-                load8(a.norm + e, w);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(v[i], inv), w[i]);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-        }
+    auto encode = [&](uint32_t e, float (&v)[8]) {
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -307,6 +316,38 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
             *reinterpret_cast<uint2 *>(dst + p * kPlaneBytes) = w;
         }
         if (j == 0) a.mult[((size_t)tile * gpr + g) * kTokenTile + tt] = __builtin_ldexpf(1.0f, ex - 22);
+    };
+    if constexpr (ITERS > 0) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const uint32_t e = threadIdx.x * 8 + 2048u * it;
+            if (e >= a.k) break;  // (whole 64-value groups: 8 consecutive threads stop together)
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float x = real ? held[it][i] : 0.0f;
+                if constexpr (M == Prep::RmsNorm) x = __fmul_rn(__fmul_rn(x, inv), norm_w[it][i]);
+                v[i] = x;
+            }
+            encode(e, v);
+        }
+    } else {
+        for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
+            float v[8];
+            if (real) {
+                load8(row + e, v);
+                if constexpr (M == Prep::RmsNorm) {
+                    float w[8];
+                    load8(a.norm + e, w);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(v[i], inv), w[i]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+            }
+            encode(e, v);
+        }
     }
 }
 
@@ -329,11 +370,21 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     p.digits = static_cast<uint8_t *>(digits);
     p.mult = reinterpret_cast<float *>(p.digits + (size_t)tiles * (cols / 64) * kGroupBytes);
     const dim3 grid(tiles * kTokenTile);
+    const uint32_t iters = (cols + 2047) / 2048;
+#define QWH_PREP_CASE(M_)                                                                             \
+    switch (iters) {                                                                                  \
+    case 1: prep_batch_kernel<M_, 1><<<grid, 256, 0, s>>>(p); break;                                 \
+    case 2: prep_batch_kernel<M_, 2><<<grid, 256, 0, s>>>(p); break;                                 \
+    case 3: prep_batch_kernel<M_, 3><<<grid, 256, 0, s>>>(p); break;                                 \
+    case 4: prep_batch_kernel<M_, 4><<<grid, 256, 0, s>>>(p); break;                                 \
+    default: prep_batch_kernel<M_, 0><<<grid, 256, 0, s>>>(p); break;                                \
+    }
     switch (in.mode) {
-    case GemvInput::F32: prep_batch_kernel<Prep::F32><<<grid, 256, 0, s>>>(p); break;
-    case GemvInput::RmsNorm: prep_batch_kernel<Prep::RmsNorm><<<grid, 256, 0, s>>>(p); break;
+    case GemvInput::F32: QWH_PREP_CASE(Prep::F32) break;
+    case GemvInput::RmsNorm: QWH_PREP_CASE(Prep::RmsNorm) break;
     default: return hipErrorInvalidValue;
     }
+#undef QWH_PREP_CASE
     return hipGetLastError();
 }
 

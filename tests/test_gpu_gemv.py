@@ -113,6 +113,9 @@ def test_q4_gemv_edge_shapes(ctx, rows, cols, tokens):
     (17, 64, 17),       # one group per row (three idle wavefronts), two token tiles
     (33, 192, 33),      # three groups, three token tiles
     (64, 256, 2),
+    (40, 10240, 3),     # K past 8192: activation prep stretch by stretch, two units per wave
+    (65600, 256, 2),    # over 4096 row tiles: four tiles per workgroup
+    (65600, 128, 3),    # four tiles, two groups per unit
 ])
 def test_q4_batch_gemv(ctx, rows, cols, tokens):
     # Two or more tokens run on the matrix-core kernel.
