@@ -355,8 +355,11 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
             in.mode = GemvInput::F32;
             in.x = x_dev;
             QWH_TRY(ensure_workspace(ctx, ctx->digits, batch_digit_bytes(tokens, cols)));
+            const size_t parts = batch_partial_bytes(tokens, *m);
+            if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
             QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
-            return check_hip(ctx, launch_gemv_q4_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr),
+            return check_hip(ctx, launch_gemv_q4_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr,
+                                                       false, static_cast<float *>(ctx->scratch.ptr)),
                              "gemv q4 batch");
         }
         if (gemv_q4_fused_supported(m->rows, m->cols)) {

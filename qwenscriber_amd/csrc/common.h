@@ -111,10 +111,30 @@ hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &
 // Small-batch q4 GEMV on the matrix cores (gemv_batch.hip): activations as
 // int8 digit planes per 16-token tile, then one MFMA pass over the weights.
 size_t batch_digit_bytes(uint32_t tokens, uint32_t cols);
+// The partial sums of a split GEMV (launch_gemv_q4_batch_parts) that a prep
+// folds into its input: RMSNorm of x + their sum (stored to x_out, which may
+// be x), or with pairs (rows = 2 cols) siluMul of the gate / up sums in place
+// of x.
+struct PartialSums {
+    const float *part = nullptr;  // [slices][tokens][rows]
+    uint32_t slices = 0, rows = 0;
+    bool pairs = false;
+    float *x_out = nullptr;
+};
 hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols,
-                             void *digits);
+                             void *digits, const PartialSums *sums = nullptr);
+// K slices the GEMV splits this shape into (0: no split form, K not a
+// multiple of 256), and the bytes of partial sums that takes.
+uint32_t batch_slices(const Matrix &w);
+size_t batch_partial_bytes(uint32_t tokens, const Matrix &w);
+// out (+)= W x; with several slices `partials` (batch_partial_bytes) is
+// required and a reduce kernel adds them.
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                float *out, const float *residual, bool pairs = false);
+                                float *out, const float *residual, bool pairs = false, float *partials = nullptr);
+// Partial sums only: batch_slices(w) planes [slice][token][row], for a prep
+// to add (the shape must have a split form).
+hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
+                                      float *partials);
 
 // q4 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
 // partials: gemm_scratch_bytes (0 when the tiles alone fill the device).

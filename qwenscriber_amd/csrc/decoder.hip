@@ -21,6 +21,7 @@
 // At batch > 1 each GEMV is a digit-plane pass plus the matrix-core GEMV.
 // Shapes without a fused GEMV kernel (or QWH_DECODER_UNFUSED set) run the
 // norm / digit-plane kernels below as separate launches instead.
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <cstring>
@@ -249,6 +250,12 @@ struct qwh_decoder {
     bool fused = true;  // every GEMV forms its own activations (no norm / prep kernels)
     bool batched = false;  // batch > 1: int8 digit planes + matrix-core GEMV
     void *batch_digits = nullptr;
+    // Batched: K-slice partial sums. When every layer matrix has a split
+    // form (split_parts), the o, gate|up and down GEMVs leave their partial
+    // sums here and the prep that follows adds them (q|k|v reduces its own).
+    float *parts = nullptr;
+    bool split_parts = false;
+    uint32_t slices_o = 0, slices_gu = 0, slices_down = 0;
 };
 
 namespace qwh {
@@ -307,6 +314,9 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
     hipError_t err = hipSuccess;
     // W * f(x) for one of the decoder's activation forms: in one kernel when
     // the GEMV forms them itself, else through a digit-plane pass.
+    // Batched with split_parts: the partial sums the next prep adds (the
+    // residual stream's pending update, or the gate / up pairs).
+    PartialSums pending;
     auto gemv = [&](GemvInput::Mode mode, const float *x, const float *norm, const Matrix &w, float *out,
                     const float *residual, bool pairs) -> hipError_t {
         GemvInput in;
@@ -317,10 +327,11 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         in.pairs = pairs;
         if (d->batched) {
             if (mode != GemvInput::Digits) {  // Digits: the planes are already in batch_digits
-                const hipError_t e = launch_prep_batch(s, in, B, w.cols, d->batch_digits);
+                const hipError_t e = launch_prep_batch(s, in, B, w.cols, d->batch_digits, &pending);
+                pending = PartialSums{};
                 if (e != hipSuccess) return e;
             }
-            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs);
+            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs, d->parts);
         }
         if (d->fused) return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
         if (mode == GemvInput::RmsNorm) {
@@ -372,6 +383,32 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         aa.digits = d->batched ? d->batch_digits : nullptr;
         err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch);
         if (err != hipSuccess) break;
+        if (d->split_parts) {
+            // o, gate|up, down as partial sums; each prep adds the previous
+            // one's (hidden += o; siluMul(gate, up); hidden += down at the
+            // next layer's or the final prep).
+            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.o, B, d->parts);
+            if (err != hipSuccess) break;
+            GemvInput norm_in;
+            norm_in.mode = GemvInput::RmsNorm;
+            norm_in.x = d->hidden;
+            norm_in.norm = L.ffn_norm;
+            norm_in.eps = c.eps;
+            const PartialSums o_sums{d->parts, d->slices_o, c.hidden, false, d->hidden};
+            err = launch_prep_batch(s, norm_in, B, c.hidden, d->batch_digits, &o_sums);
+            if (err != hipSuccess) break;
+            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.gu, B, d->parts);
+            if (err != hipSuccess) break;
+            GemvInput pairs_in;
+            pairs_in.mode = GemvInput::F32;
+            const PartialSums gu_sums{d->parts, d->slices_gu, 2 * c.ffn, true, nullptr};
+            err = launch_prep_batch(s, pairs_in, B, c.ffn, d->batch_digits, &gu_sums);
+            if (err != hipSuccess) break;
+            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.down, B, d->parts);
+            if (err != hipSuccess) break;
+            pending = PartialSums{d->parts, d->slices_down, c.hidden, false, d->hidden};
+            continue;
+        }
         err = gemv(d->batched ? GemvInput::Digits : GemvInput::F32, d->attn, nullptr, L.o, d->hidden, d->hidden,
                    false);
         if (err != hipSuccess) break;
@@ -578,6 +615,17 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     // QWH_DECODER_PER_TOKEN keeps batch > 1 on the per-token GEMV (for tests).
     d->batched = batch > 1 && getenv("QWH_DECODER_PER_TOKEN") == nullptr;
     if (st == QWH_OK && d->batched) st = dalloc(d, batch_digit_bytes(batch, widest), &d->batch_digits);
+    if (st == QWH_OK && d->batched) {
+        const qwh_decoder::Layer &L0 = d->layers[0];
+        d->slices_o = batch_slices(L0.o);
+        d->slices_gu = batch_slices(L0.gu);
+        d->slices_down = batch_slices(L0.down);
+        d->split_parts = d->slices_o && d->slices_gu && d->slices_down && getenv("QWH_DECODER_NO_SPLIT") == nullptr;
+        size_t parts = 0;
+        for (const Matrix *m : {&L0.qkv, &L0.o, &L0.gu, &L0.down, const_cast<const Matrix *>(&d->lm_head)})
+            parts = std::max(parts, batch_partial_bytes(batch, *m));
+        if (parts) st = dalloc(d, parts, reinterpret_cast<void **>(&d->parts));
+    }
     AttentionArgs aa{};
     aa.capacity = c.max_positions;
     aa.heads = c.heads;

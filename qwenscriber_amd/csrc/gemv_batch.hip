@@ -23,6 +23,7 @@
 //   digits[tile][g][plane][token 0..15][64 bytes],  mult[tile][g][16] f32.
 //
 // Work split: see gemv_q4_batch_kernel.
+#include <algorithm>
 #include <cstdlib>
 
 #include "common.h"
@@ -219,18 +220,258 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Split form. Every workgroup of the form above reads all of K's digit
+// planes (48 B per column for a 16-token tile), several times the weight
+// bytes of its few rows, and those reads set its time. Here a workgroup of
+// four wavefronts covers 4 x 16 TW rows (wavefront w: TW tiles from
+// 16 TW w) and one K slice; the slice is walked in chunks of KC groups whose
+// digit planes are read once per workgroup and staged in LDS for all four
+// wavefronts (in lane order: conflict-free 16-byte reads), while the next
+// chunk's weights, digits, multipliers and scales are already in flight.
+// Weights move into the MFMA layout through each wavefront's own LDS region
+// as above. The workgroup writes either the output (+ residual, silu pairs;
+// one slice only) or its slice's partial sums to part[slice][token][row],
+// which the next kernel adds in slice order: split_reduce_kernel, or the
+// batch prep that consumes them (the residual stream, silu pairs).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kMaxSlices = 8;
+
+struct SplitArgs {
+    const uint8_t *digits;
+    const float *mult;
+    const uint16_t *scales;
+    const uint8_t *data;
+    float *out;
+    const float *residual;
+    float *part;             // non-null: partial sums [slices][tokens][n] instead of out
+    uint32_t n, k, tokens;
+    uint32_t pairs;
+    uint32_t slice_groups;   // groups per K slice (a multiple of KC)
+};
+
+template <int TW, int KC>
+struct SplitShape {
+    static constexpr int ROWS = kRowTile * TW;      // rows per wavefront
+    static constexpr int PPR = 2 * KC;              // 16-byte pieces of a row in a chunk
+    static constexpr int RPI = 64 / PPR;            // rows per load instruction
+    static constexpr int NW = (ROWS + RPI - 1) / RPI;
+    static constexpr int DPIECES = KC * 3 * 64;     // 16-byte digit pieces per chunk
+    static constexpr int DPT = DPIECES / 256;       // ... per thread
+    static_assert(DPIECES % 256 == 0 && (PPR & (PPR - 1)) == 0 && ROWS % RPI == 0, "chunk shape");
+};
+
+template <int TW, int KC>
+__global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
+    using S = SplitShape<TW, KC>;
+    constexpr int ROWS = S::ROWS, PPR = S::PPR, RPI = S::RPI, NW = S::NW, DPT = S::DPT;
+    __shared__ v4i dl[2][S::DPIECES];          // digit planes, [group][plane][lane]
+    __shared__ float4 ml[2][KC * 4];             // multipliers, [group][lane / 16]
+    __shared__ v4i wls[4][ROWS * PPR];         // per-wavefront weight transpose
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 15;
+    const int blk = lane >> 4;
+    const uint32_t gpr = a.k >> 6;
+    const uint32_t tile = blockIdx.z;
+    const uint32_t row0 = (blockIdx.x * 4 + wave) * ROWS;
+    const size_t row_bytes = a.k >> 1;
+    const uint32_t g_first = blockIdx.y * a.slice_groups;
+    const uint32_t chunks = a.slice_groups / KC;
+    const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes;
+    const float *mul = a.mult + (size_t)tile * gpr * kTokenTile;
+    v4i *wl = wls[wave];
+
+    // (Native vector types: these stay in registers across the chunk loop.)
+    v4i rw[NW], rd[DPT];
+    float4 rm = {};
+    uint32_t rs[TW][KC / 2];
+    // One chunk's loads (rows past the matrix read its last row; their
+    // results are never stored).
+    auto load = [&](uint32_t g0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            uint32_t row = row0 + i * RPI + lane / PPR;
+            if (row >= a.n) row = a.n - 1;
+            rw[i] = *reinterpret_cast<const v4i *>(a.data + (size_t)row * row_bytes + g0 * 32 + 16 * (lane % PPR));
+        }
+#pragma unroll
+        for (int m = 0; m < DPT; ++m) {
+            // Piece q = (group, plane, lane L) of lane order; lane L reads
+            // column block L / 16 of token L % 16.
+            const int q = tid + 256 * m;
+            const int L = q & 63;
+            rd[m] = *reinterpret_cast<const v4i *>(dig + ((size_t)g0 * 3 + (q >> 6)) * kPlaneBytes +
+                                                     (L & 15) * 64 + (L >> 4) * 16);
+        }
+        if (tid < KC * 4) rm = *reinterpret_cast<const float4 *>(mul + (size_t)g0 * kTokenTile + tid * 4);
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            uint32_t row = row0 + t * kRowTile + col;
+            if (row >= a.n) row = a.n - 1;
+            __builtin_memcpy(rs[t], a.scales + (size_t)row * gpr + g0, 2 * KC);
+        }
+    };
+
+    float acc[TW][4] = {};
+    load(g_first);
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const int buf = c & 1;
+#pragma unroll
+        for (int m = 0; m < DPT; ++m) dl[buf][tid + 256 * m] = rd[m];
+        if (tid < KC * 4) ml[buf][tid] = rm;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const int r = i * RPI + lane / PPR;
+            wl[r * PPR + ((lane % PPR) ^ (r % PPR))] = rw[i];
+        }
+        uint32_t sc[TW][KC / 2];
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int j = 0; j < KC / 2; ++j) sc[t][j] = rs[t][j];
+        // The other wavefronts' digits are in; the buffer written next
+        // iteration was last read before this barrier.
+        __syncthreads();
+        if (c + 1 < chunks) load(g_first + (c + 1) * KC);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            const v4i d0 = dl[buf][(i * 3 + 0) * 64 + lane];
+            const v4i d1 = dl[buf][(i * 3 + 1) * 64 + lane];
+            const v4i d2 = dl[buf][(i * 3 + 2) * 64 + lane];
+            const float4 mm = ml[buf][i * 4 + blk];
+            const float m[4] = {mm.x, mm.y, mm.z, mm.w};
+#pragma unroll
+            for (int t = 0; t < TW; ++t) {
+                const int r = t * kRowTile + col;
+                const int piece = 2 * i + (blk >> 1);
+                const uint2 w8 = *reinterpret_cast<const uint2 *>(
+                    reinterpret_cast<const uint8_t *>(&wl[r * PPR + (piece ^ (r % PPR))]) + 8 * (blk & 1));
+                const v4i b = expand_q4(w8);
+                const v4i zero = {0, 0, 0, 0};
+                const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d0, b, zero, 0, 0, 0);
+                const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d1, b, zero, 0, 0, 0);
+                const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d2, b, zero, 0, 0, 0);
+                const float sv = dev::f16_bits_to_f32((uint16_t)(sc[t][i / 2] >> (16 * (i % 2))));
+                const int q0[4] = {p0.x, p0.y, p0.z, p0.w};
+                const int q1[4] = {p1.x, p1.y, p1.z, p1.w};
+                const int q2[4] = {p2.x, p2.y, p2.z, p2.w};
+#pragma unroll
+                for (int r2 = 0; r2 < 4; ++r2) {
+                    const float f = (float)(q0[r2] + q1[r2] * 256) + 65536.0f * (float)q2[r2];
+                    acc[t][r2] = fmaf(f, sv * m[r2], acc[t][r2]);
+                }
+            }
+        }
+    }
+
+    // Lane l holds tokens 4 (l / 16) + r of row l % 16 of each tile.
+    if (a.part) {
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            const uint32_t out_row = row0 + t * kRowTile + col;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = tile * kTokenTile + blk * 4 + r;
+                if (tok < a.tokens && out_row < a.n)
+                    a.part[((size_t)blockIdx.y * a.tokens + tok) * a.n + out_row] = acc[t][r];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const uint32_t out_row = row0 + t * kRowTile + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = tile * kTokenTile + blk * 4 + r;
+            const float total = acc[t][r];
+            if (a.pairs) {
+                const float partner = __shfl_down(total, 1, 64);
+                if (tok < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
+                    a.out[(size_t)tok * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
+            } else if (tok < a.tokens && out_row < a.n) {
+                const float res = a.residual ? a.residual[(size_t)tok * a.n + out_row] : 0.0f;
+                a.out[(size_t)tok * a.n + out_row] = res + total;
+            }
+        }
+    }
+}
+
+// Sum over the K slices, in slice order, of the partial sums at p (slices
+// planes `plane` floats apart). All loads are issued before the first add.
+__device__ __forceinline__ float slice_sum(const float *p, uint32_t slices, size_t plane) {
+    float w[kMaxSlices];
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxSlices; ++s)
+        if (s < slices) w[s] = p[s * plane];
+    float v = w[0];
+#pragma unroll
+    for (uint32_t s = 1; s < kMaxSlices; ++s)
+        if (s < slices) v += w[s];
+    return v;
+}
+
+__device__ __forceinline__ float4 slice_sum4(const float *p, uint32_t slices, size_t plane) {
+    float4 w[kMaxSlices];
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxSlices; ++s)
+        if (s < slices) w[s] = *reinterpret_cast<const float4 *>(p + s * plane);
+    float4 v = w[0];
+#pragma unroll
+    for (uint32_t s = 1; s < kMaxSlices; ++s)
+        if (s < slices) {
+            v.x += w[s].x;
+            v.y += w[s].y;
+            v.z += w[s].z;
+            v.w += w[s].w;
+        }
+    return v;
+}
+
+// out = residual + the slice sum (pairs: silu(sum of row 2j) * sum of row
+// 2j + 1), one output per thread.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, uint32_t slices, uint32_t tokens,
+                                                           uint32_t n, const float *residual, float *out,
+                                                           uint32_t pairs) {
+    const uint32_t width = pairs ? n / 2 : n;
+    const size_t plane = (size_t)tokens * n;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)tokens * width) return;
+    const size_t tok = i / width, j = i % width;
+    if (pairs) {
+        const size_t at = tok * n + 2 * j;
+        out[i] = silu_mul(slice_sum(part + at, slices, plane), slice_sum(part + at + 1, slices, plane));
+    } else {
+        const size_t at = tok * n + j;
+        const float v = slice_sum(part + at, slices, plane);
+        out[i] = residual ? residual[at] + v : v;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Activation digits. One workgroup per token (padding tokens write zeros);
 // thread i takes 8 consecutive values 8i .. 8i+7 of each 2048-value stretch,
 // so the 8 threads of a group are consecutive lanes. Forms as in the q4 GEMV:
-// f32 values as they are, or RMSNorm (math.zig:120-130).
+// f32 values as they are, or RMSNorm (math.zig:120-130); and with the
+// partial sums of a split GEMV folded in: RMSNorm of x + their sum (the
+// residual stream, written back), or siluMul of the gate / up sums
+// (math.zig:69-71).
 // ---------------------------------------------------------------------------
-enum class Prep : int { F32 = 0, RmsNorm = 1 };
+enum class Prep : int { F32 = 0, RmsNorm = 1, Pairs = 2 };
 
 struct PrepArgs {
-    const float *x;      // tokens x K
+    const float *x;      // tokens x K (F32, RmsNorm)
     const float *norm;   // RmsNorm weights
     float eps;
     uint32_t k, tokens;
+    // Partial sums [slices][tokens][part_n] of the GEMV that produced the
+    // input (slices 0: none). RmsNorm: x + their sum, also stored to x_out
+    // (may be x); Pairs (part_n = 2K): value j = silu(sum of row 2j) * sum of
+    // row 2j + 1.
+    const float *part;
+    uint32_t slices, part_n;
+    float *x_out;
     uint8_t *digits;
     float *mult;
 };
@@ -240,6 +481,38 @@ __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
     const float4 b = reinterpret_cast<const float4 *>(p)[1];
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void store8(float *p, const float (&v)[8]) {
+    reinterpret_cast<float4 *>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4 *>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// Input values e .. e + 7 of token t.
+template <Prep M>
+__device__ __forceinline__ void input8(const PrepArgs &a, uint32_t t, uint32_t e, float (&v)[8]) {
+    const size_t plane = (size_t)a.tokens * a.part_n;
+    if constexpr (M == Prep::Pairs) {
+        const float *p = a.part + (size_t)t * a.part_n + 2 * e;
+        float f[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 q = slice_sum4(p + 4 * j, a.slices, plane);
+            f[4 * j] = q.x; f[4 * j + 1] = q.y; f[4 * j + 2] = q.z; f[4 * j + 3] = q.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = silu_mul(f[2 * i], f[2 * i + 1]);
+    } else {
+        load8(a.x + (size_t)t * a.k + e, v);
+        if (M == Prep::RmsNorm && a.slices) {
+            const float *p = a.part + (size_t)t * a.part_n + e;
+            const float4 s0 = slice_sum4(p, a.slices, plane);
+            const float4 s1 = slice_sum4(p + 4, a.slices, plane);
+            const float sum[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = __fadd_rn(v[i], sum[i]);
+        }
+    }
 }
 
 // ITERS > 0: K <= 2048 ITERS, and each thread loads all its values (and norm
@@ -252,7 +525,8 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
     const uint32_t tile = t / kTokenTile;
     const uint32_t tt = t % kTokenTile;
     const bool real = t < a.tokens;
-    const float *row = a.x + (size_t)(real ? t : 0) * a.k;
+    const uint32_t src = real ? t : 0;  // padding tokens read token 0 and discard it
+    const bool write_back = M == Prep::RmsNorm && a.slices && real;
     constexpr int kHeld = ITERS > 0 ? ITERS : 1;
     float held[kHeld][8], norm_w[kHeld][8];
     if constexpr (ITERS > 0) {
@@ -260,8 +534,9 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
         for (int it = 0; it < ITERS; ++it) {
             const uint32_t e = threadIdx.x * 8 + 2048u * it;
             const uint32_t ec = e < a.k ? e : 0;  // past the row: a valid address, never used
-            load8(row + ec, held[it]);
+            input8<M>(a, src, ec, held[it]);
             if constexpr (M == Prep::RmsNorm) load8(a.norm + ec, norm_w[it]);
+            if (write_back && e < a.k) store8(a.x_out + (size_t)t * a.k + e, held[it]);
         }
     }
     float inv = 1.0f;
@@ -278,7 +553,7 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
         } else {
             for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
                 float v[8];
-                load8(row + e, v);
+                input8<M>(a, src, e, v);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
             }
@@ -332,10 +607,12 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
             encode(e, v);
         }
     } else {
+        // (x_out is written here, in the last pass over x: it may be x.)
         for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
             float v[8];
             if (real) {
-                load8(row + e, v);
+                input8<M>(a, t, e, v);
+                if (write_back) store8(a.x_out + (size_t)t * a.k + e, v);
                 if constexpr (M == Prep::RmsNorm) {
                     float w[8];
                     load8(a.norm + e, w);
@@ -359,7 +636,8 @@ size_t batch_digit_bytes(uint32_t tokens, uint32_t cols) {
     return tiles * groups * kGroupBytes + tiles * groups * kTokenTile * sizeof(float) + 256;
 }
 
-hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols, void *digits) {
+hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols, void *digits,
+                             const PartialSums *sums) {
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     PrepArgs p{};
     p.x = in.x;
@@ -369,6 +647,21 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     p.tokens = tokens;
     p.digits = static_cast<uint8_t *>(digits);
     p.mult = reinterpret_cast<float *>(p.digits + (size_t)tiles * (cols / 64) * kGroupBytes);
+    Prep form = in.mode == GemvInput::RmsNorm ? Prep::RmsNorm : Prep::F32;
+    if (in.mode != GemvInput::F32 && in.mode != GemvInput::RmsNorm) return hipErrorInvalidValue;
+    if (sums && sums->slices) {
+        if (sums->slices > kMaxSlices || !sums->part) return hipErrorInvalidValue;
+        p.part = sums->part;
+        p.slices = sums->slices;
+        if (sums->pairs) {
+            if (in.mode != GemvInput::F32 || sums->rows != 2 * cols) return hipErrorInvalidValue;
+            form = Prep::Pairs;
+        } else {
+            if (in.mode != GemvInput::RmsNorm || sums->rows != cols || !sums->x_out) return hipErrorInvalidValue;
+            p.x_out = sums->x_out;
+        }
+        p.part_n = sums->rows;
+    }
     const dim3 grid(tiles * kTokenTile);
     const uint32_t iters = (cols + 2047) / 2048;
 #define QWH_PREP_CASE(M_)                                                                             \
@@ -379,19 +672,117 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     case 4: prep_batch_kernel<M_, 4><<<grid, 256, 0, s>>>(p); break;                                 \
     default: prep_batch_kernel<M_, 0><<<grid, 256, 0, s>>>(p); break;                                \
     }
-    switch (in.mode) {
-    case GemvInput::F32: QWH_PREP_CASE(Prep::F32) break;
-    case GemvInput::RmsNorm: QWH_PREP_CASE(Prep::RmsNorm) break;
-    default: return hipErrorInvalidValue;
+    switch (form) {
+    case Prep::F32: QWH_PREP_CASE(Prep::F32) break;
+    case Prep::RmsNorm: QWH_PREP_CASE(Prep::RmsNorm) break;
+    case Prep::Pairs: QWH_PREP_CASE(Prep::Pairs) break;
     }
 #undef QWH_PREP_CASE
     return hipGetLastError();
 }
 
+namespace {
+
+// Split-form plan: TW tiles per wavefront, chunks of KC groups, K slices.
+// tw == 0: no split form for this shape (K not a multiple of 4 groups).
+struct SplitPlan {
+    int tw = 0, kc = 4;
+    uint32_t slices = 1, slice_groups = 0;
+};
+
+int env_int(const char *name, int fallback) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : fallback;
+}
+
+SplitPlan split_plan(const Matrix &w) {
+    // Tuning overrides, read once.
+    static const int env_tw = env_int("QWH_SPLIT_TW", 0), env_kc = env_int("QWH_SPLIT_KC", 0),
+                     env_s = env_int("QWH_SPLIT_S", 0), env_off = env_int("QWH_SPLIT_OFF", 0);
+    SplitPlan p;
+    const uint32_t gpr = w.cols / 64;
+    if (gpr % 4u || env_off) return p;
+    const uint32_t row_tiles = (w.rows + kRowTile - 1) / kRowTile;
+    // Two tiles per wavefront once that still leaves 64 workgroups, else one.
+    p.tw = row_tiles >= 4u * 2u * 64u ? 2 : 1;
+    if (env_tw == 1 || env_tw == 2) p.tw = env_tw;
+    if ((env_kc == 4 || env_kc == 8) && gpr % (uint32_t)env_kc == 0) p.kc = env_kc;
+    const uint32_t chunks = gpr / (uint32_t)p.kc;
+    const uint32_t blocks = (row_tiles + 4u * p.tw - 1) / (4u * p.tw);
+    // K slices: about 512 workgroups in all, a divisor of the chunk count,
+    // at most kMaxSlices.
+    uint32_t want = env_s > 0 ? (uint32_t)env_s : (512u + blocks - 1) / blocks;
+    p.slices = 1;
+    for (uint32_t c = 1; c <= chunks && c <= want && c <= kMaxSlices; ++c)
+        if (chunks % c == 0) p.slices = c;
+    p.slice_groups = gpr / p.slices;
+    return p;
+}
+
+void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint32_t tiles) {
+    const uint32_t row_tiles = (a.n + kRowTile - 1) / kRowTile;
+    const dim3 grid((row_tiles + 4u * plan.tw - 1) / (4u * plan.tw), plan.slices, tiles);
+    if (plan.tw == 2 && plan.kc == 4) gemv_q4_split_kernel<2, 4><<<grid, 256, 0, s>>>(a);
+    else if (plan.tw == 2) gemv_q4_split_kernel<2, 8><<<grid, 256, 0, s>>>(a);
+    else if (plan.kc == 4) gemv_q4_split_kernel<1, 4><<<grid, 256, 0, s>>>(a);
+    else gemv_q4_split_kernel<1, 8><<<grid, 256, 0, s>>>(a);
+}
+
+SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const SplitPlan &plan) {
+    const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+    SplitArgs a{};
+    a.digits = static_cast<const uint8_t *>(digits);
+    a.mult = reinterpret_cast<const float *>(a.digits + (size_t)tiles * (w.cols / 64) * kGroupBytes);
+    a.scales = reinterpret_cast<const uint16_t *>(w.scales);
+    a.data = w.data;
+    a.n = w.rows;
+    a.k = w.cols;
+    a.tokens = tokens;
+    a.slice_groups = plan.slice_groups;
+    return a;
+}
+
+}  // namespace
+
+uint32_t batch_slices(const Matrix &w) {
+    const SplitPlan p = split_plan(w);
+    return p.tw ? p.slices : 0;
+}
+
+size_t batch_partial_bytes(uint32_t tokens, const Matrix &w) {
+    return (size_t)batch_slices(w) * tokens * w.rows * sizeof(float);
+}
+
+hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
+                                      float *partials) {
+    const SplitPlan plan = split_plan(w);
+    if (!plan.tw || !partials) return hipErrorInvalidValue;
+    SplitArgs a = split_args(digits, w, tokens, plan);
+    a.part = partials;
+    launch_split(s, plan, a, (tokens + kTokenTile - 1) / kTokenTile);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens, float *out,
-                                const float *residual, bool pairs) {
+                                const float *residual, bool pairs, float *partials) {
     if (pairs && (w.rows & 1u)) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+    const SplitPlan plan = split_plan(w);
+    if (plan.tw && (plan.slices == 1 || partials)) {
+        SplitArgs a = split_args(digits, w, tokens, plan);
+        a.out = out;
+        a.residual = residual;
+        a.pairs = pairs ? 1u : 0u;
+        if (plan.slices > 1) a.part = partials;
+        launch_split(s, plan, a, tiles);
+        if (plan.slices > 1) {
+            const size_t items = (size_t)tokens * (pairs ? w.rows / 2 : w.rows);
+            split_reduce_kernel<<<(uint32_t)((items + 255) / 256), 256, 0, s>>>(partials, plan.slices, tokens, w.rows,
+                                                                               residual, out, pairs ? 1u : 0u);
+        }
+        return hipGetLastError();
+    }
+    // K not a multiple of 256: the unsplit form, one tile per workgroup.
     BatchArgs a{};
     a.digits = static_cast<const uint8_t *>(digits);
     a.mult = reinterpret_cast<const float *>(a.digits + (size_t)tiles * (w.cols / 64) * kGroupBytes);
@@ -403,35 +794,24 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
     a.k = w.cols;
     a.tokens = tokens;
     a.pairs = pairs ? 1u : 0u;
-    // Tiles per workgroup: one (measured fastest up to the 12288-row gate|up
-    // projection), four for the very tall vocabulary projection (each added
-    // tile divides the digit-plane reads per weight byte).
     const uint32_t row_tiles = (w.rows + kRowTile - 1) / kRowTile;
     const uint32_t gpr = w.cols / 64;
-    int tiles_per = row_tiles >= 4096u ? 4 : 1;
-    if (const char *env = getenv("QWH_BATCH_TILES")) {  // tuning override: 1, 2 or 4
-        const int v = atoi(env);
-        if (v == 1 || v == 2 || v == 4) tiles_per = v;
-    }
-    // Groups per unit: 8 (4 with 4 tiles, for registers), lowered to divide
-    // the row's groups.
-    int gr = tiles_per >= 4 ? 4 : 8;
+    // Groups per unit: 8, lowered to divide the row's groups.
+    int gr = 8;
     while (gpr % (uint32_t)gr) gr >>= 1;
     const uint32_t units = gpr / (uint32_t)gr;
-    dim3 grid((row_tiles + tiles_per - 1) / tiles_per, tiles);
-#define QWH_BATCH_CASE(T_, G_)                                                                       \
-    if (tiles_per == T_ && gr == G_) {                                                               \
-        using S = BatchShape<T_, G_>;                                                                \
+    const dim3 grid(row_tiles, tiles);
+#define QWH_BATCH_CASE(G_)                                                                           \
+    if (gr == G_) {                                                                                  \
+        using S = BatchShape<1, G_>;                                                                 \
         /* Wavefronts: the largest divisor of the unit count within the cap and 64 KB of LDS. */     \
         uint32_t waves = 1;                                                                          \
-        for (uint32_t c = 1; c <= (uint32_t)max_waves<T_>() && c * S::WAVE_BYTES <= 65536u; ++c)     \
+        for (uint32_t c = 1; c <= (uint32_t)max_waves<1>() && c * S::WAVE_BYTES <= 65536u; ++c)      \
             if (units % c == 0) waves = c;                                                           \
-        gemv_q4_batch_kernel<T_, G_><<<grid, 64 * waves, waves * S::WAVE_BYTES, s>>>(a);             \
+        gemv_q4_batch_kernel<1, G_><<<grid, 64 * waves, waves * S::WAVE_BYTES, s>>>(a);              \
         return hipGetLastError();                                                                    \
     }
-    QWH_BATCH_CASE(1, 8) QWH_BATCH_CASE(1, 4) QWH_BATCH_CASE(1, 2) QWH_BATCH_CASE(1, 1)
-    QWH_BATCH_CASE(2, 8) QWH_BATCH_CASE(2, 4) QWH_BATCH_CASE(2, 2) QWH_BATCH_CASE(2, 1)
-    QWH_BATCH_CASE(4, 4) QWH_BATCH_CASE(4, 2) QWH_BATCH_CASE(4, 1)
+    QWH_BATCH_CASE(8) QWH_BATCH_CASE(4) QWH_BATCH_CASE(2) QWH_BATCH_CASE(1)
 #undef QWH_BATCH_CASE
     return hipErrorInvalidValue;
 }
