@@ -123,6 +123,12 @@ struct PartialSums {
 };
 hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols,
                              void *digits, const PartialSums *sums = nullptr);
+// Activations that launch_prep_batch left in RMSNorm form (x * w, without
+// the 1 / rms factor): the GEMV applies each token's factor.
+struct BatchNorm {
+    bool rms = false;
+    float eps = 0.0f;
+};
 // K slices the GEMV splits this shape into (0: no split form, K not a
 // multiple of 256), and the bytes of partial sums that takes.
 uint32_t batch_slices(const Matrix &w);
@@ -130,11 +136,12 @@ size_t batch_partial_bytes(uint32_t tokens, const Matrix &w);
 // out (+)= W x; with several slices `partials` (batch_partial_bytes) is
 // required and a reduce kernel adds them.
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                float *out, const float *residual, bool pairs = false, float *partials = nullptr);
+                                float *out, const float *residual, bool pairs = false, float *partials = nullptr,
+                                const BatchNorm &norm = BatchNorm{});
 // Partial sums only: batch_slices(w) planes [slice][token][row], for a prep
 // to add (the shape must have a split form).
 hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                      float *partials);
+                                      float *partials, const BatchNorm &norm = BatchNorm{});
 
 // q4 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
 // partials: gemm_scratch_bytes (0 when the tiles alone fill the device).

@@ -331,7 +331,10 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
                 pending = PartialSums{};
                 if (e != hipSuccess) return e;
             }
-            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs, d->parts);
+            BatchNorm bn;
+            bn.rms = mode == GemvInput::RmsNorm;
+            bn.eps = c.eps;
+            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs, d->parts, bn);
         }
         if (d->fused) return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
         if (mode == GemvInput::RmsNorm) {
@@ -397,7 +400,10 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             const PartialSums o_sums{d->parts, d->slices_o, c.hidden, false, d->hidden};
             err = launch_prep_batch(s, norm_in, B, c.hidden, d->batch_digits, &o_sums);
             if (err != hipSuccess) break;
-            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.gu, B, d->parts);
+            BatchNorm bn;
+            bn.rms = true;
+            bn.eps = c.eps;
+            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.gu, B, d->parts, bn);
             if (err != hipSuccess) break;
             GemvInput pairs_in;
             pairs_in.mode = GemvInput::F32;

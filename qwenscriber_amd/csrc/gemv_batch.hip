@@ -58,6 +58,9 @@ struct BatchArgs {
     const uint8_t *data;     // N * K/2
     float *out;              // tokens x N, or tokens x N/2 with pairs
     const float *residual;   // optional, tokens x N (may alias out); not with pairs
+    const float *ss;         // non-null: RMSNorm sums of squares [token][ss_parts]; results x 1/rms
+    uint32_t ss_parts;
+    float eps;
     uint32_t n, k, tokens;
     uint32_t pairs;          // rows 2j, 2j+1 are gate_j, up_j: write silu(gate_j) * up_j
 };
@@ -65,6 +68,25 @@ struct BatchArgs {
 // siluMul of one gate / up pair (math.zig:69-71: silu(g) = g / (1 + exp(-g))).
 __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+}
+
+// 1 / sqrt(ss / K + eps) (math.zig:120-130), from the sums of squares the
+// prep left per 512-value stretch, added in stretch order.
+__device__ __forceinline__ float rms_inverse(const float *parts, uint32_t n, uint32_t k, float eps) {
+    float ss = 0.0f;
+    for (uint32_t p = 0; p < n; ++p) ss = __fadd_rn(ss, parts[p]);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)k), eps)));
+}
+
+// The factor of token 4 (lane / 16) + r for each r, with lane t < 16 of the
+// wavefront computing token t's once (`parts` = [token][n] for the 16-token
+// tile; a tile with tokens past the batch reads their zero sums).
+__device__ __forceinline__ void tile_rms_inverse(const float *parts, uint32_t n, uint32_t k, float eps, int lane,
+                                                 float (&inv)[4]) {
+    float mine = 1.0f;
+    if (lane < 16) mine = rms_inverse(parts + lane * n, n, k, eps);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv[r] = __shfl(mine, (lane >> 4) * 4 + r, 64);
 }
 
 // Work split. A workgroup owns TILES 16-row tiles of the output for one
@@ -199,6 +221,8 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(
         for (int r = 0; r < 4; ++r) part[((wave * TILES + t) * 4 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
     if (wave != 0) return;
+    float inv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (a.ss) tile_rms_inverse(a.ss + (size_t)tile * kTokenTile * a.ss_parts, a.ss_parts, a.k, a.eps, lane, inv);
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
         const uint32_t out_row = row0 + t * kRowTile + col;
@@ -207,6 +231,7 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(
             const uint32_t tok = tile * kTokenTile + blk * 4 + r;
             float total = part[(t * 4 + r) * 64 + lane];
             for (int w = 1; w < waves; ++w) total += part[((w * TILES + t) * 4 + r) * 64 + lane];
+            if (a.ss) total = __fmul_rn(total, inv[r]);
             if (a.pairs) {
                 // Row + 1 is the next lane's row (same token).
                 const float partner = __shfl_down(total, 1, 64);
@@ -244,10 +269,14 @@ struct SplitArgs {
     float *out;
     const float *residual;
     float *part;             // non-null: partial sums [slices][tokens][n] instead of out
+    const float *ss;         // non-null: RMSNorm sums of squares [token][ss_parts]; results x 1/rms
+    uint32_t ss_parts;
+    float eps;
     uint32_t n, k, tokens;
     uint32_t pairs;
     uint32_t slice_groups;   // groups per K slice (a multiple of KC)
 };
+
 
 template <int TW, int KC>
 struct SplitShape {
@@ -267,6 +296,7 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
     __shared__ v4i dl[2][S::DPIECES];          // digit planes, [group][plane][lane]
     __shared__ float4 ml[2][KC * 4];             // multipliers, [group][lane / 16]
     __shared__ v4i wls[4][ROWS * PPR];         // per-wavefront weight transpose
+    __shared__ float ssl[kTokenTile * 16];       // RMSNorm sums of squares of the token tile
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -304,7 +334,9 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
             rd[m] = *reinterpret_cast<const v4i *>(dig + ((size_t)g0 * 3 + (q >> 6)) * kPlaneBytes +
                                                      (L & 15) * 64 + (L >> 4) * 16);
         }
-        if (tid < KC * 4) rm = *reinterpret_cast<const float4 *>(mul + (size_t)g0 * kTokenTile + tid * 4);
+        // (Every thread loads, the first KC * 4 their own float4: a load
+        // under a branch would make the wait counts conservative.)
+        rm = *reinterpret_cast<const float4 *>(mul + (size_t)g0 * kTokenTile + (tid % (KC * 4)) * 4);
 #pragma unroll
         for (int t = 0; t < TW; ++t) {
             uint32_t row = row0 + t * kRowTile + col;
@@ -314,9 +346,14 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
     };
 
     float acc[TW][4] = {};
+    float inv[4] = {1.0f, 1.0f, 1.0f, 1.0f};  // 1 / rms of the lane's tokens (RMSNorm input)
+    // The token tile's sums of squares travel with the first chunk.
+    const bool has_ss = a.ss && (uint32_t)tid < kTokenTile * a.ss_parts;
+    const float ssv = has_ss ? a.ss[(size_t)tile * kTokenTile * a.ss_parts + tid] : 0.0f;
     load(g_first);
     for (uint32_t c = 0; c < chunks; ++c) {
         const int buf = c & 1;
+        if (c == 0 && has_ss) ssl[tid] = ssv;
 #pragma unroll
         for (int m = 0; m < DPT; ++m) dl[buf][tid + 256 * m] = rd[m];
         if (tid < KC * 4) ml[buf][tid] = rm;
@@ -325,15 +362,18 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
             const int r = i * RPI + lane / PPR;
             wl[r * PPR + ((lane % PPR) ^ (r % PPR))] = rw[i];
         }
-        uint32_t sc[TW][KC / 2];
+        float sc[TW][KC];  // this chunk's scales, converted before the next chunk's loads go out
 #pragma unroll
         for (int t = 0; t < TW; ++t)
 #pragma unroll
-            for (int j = 0; j < KC / 2; ++j) sc[t][j] = rs[t][j];
+            for (int i = 0; i < KC; ++i) sc[t][i] = dev::f16_bits_to_f32((uint16_t)(rs[t][i / 2] >> (16 * (i % 2))));
         // The other wavefronts' digits are in; the buffer written next
         // iteration was last read before this barrier.
         __syncthreads();
-        if (c + 1 < chunks) load(g_first + (c + 1) * KC);
+        // The next chunk's loads (the last iteration reloads its own chunk:
+        // an unconditional load keeps them in flight across the products).
+        load(g_first + (c + 1 < chunks ? c + 1 : c) * KC);
+        if (c == 0 && a.ss) tile_rms_inverse(ssl, a.ss_parts, a.k, a.eps, lane, inv);  // (beside the products)
 #pragma unroll
         for (int i = 0; i < KC; ++i) {
             const v4i d0 = dl[buf][(i * 3 + 0) * 64 + lane];
@@ -352,7 +392,7 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
                 const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d0, b, zero, 0, 0, 0);
                 const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d1, b, zero, 0, 0, 0);
                 const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d2, b, zero, 0, 0, 0);
-                const float sv = dev::f16_bits_to_f32((uint16_t)(sc[t][i / 2] >> (16 * (i % 2))));
+                const float sv = sc[t][i];
                 const int q0[4] = {p0.x, p0.y, p0.z, p0.w};
                 const int q1[4] = {p1.x, p1.y, p1.z, p1.w};
                 const int q2[4] = {p2.x, p2.y, p2.z, p2.w};
@@ -366,6 +406,11 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
     }
 
     // Lane l holds tokens 4 (l / 16) + r of row l % 16 of each tile.
+    if (a.ss)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < TW; ++t) acc[t][r] = __fmul_rn(acc[t][r], inv[r]);
     if (a.part) {
 #pragma unroll
         for (int t = 0; t < TW; ++t) {
@@ -450,20 +495,24 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, ui
 }
 
 // ---------------------------------------------------------------------------
-// Activation digits. One workgroup per token (padding tokens write zeros);
-// thread i takes 8 consecutive values 8i .. 8i+7 of each 2048-value stretch,
-// so the 8 threads of a group are consecutive lanes. Forms as in the q4 GEMV:
-// f32 values as they are, or RMSNorm (math.zig:120-130); and with the
-// partial sums of a split GEMV folded in: RMSNorm of x + their sum (the
-// residual stream, written back), or siluMul of the gate / up sums
-// (math.zig:69-71).
+// Activation digits. One wavefront per 512 values of a token (padding tokens
+// of the last tile write zeros): lane i takes values 8i .. 8i+7, so the 8
+// lanes of a 64-value group are consecutive. Forms: f32 values as they are;
+// RMSNorm (math.zig:120-130) of x, of which this kernel applies only the
+// weights -- it encodes x_k * w_k and leaves each wavefront's sum of squares
+// of x, and the GEMV multiplies its dot products by the token's
+// 1 / sqrt(sum / K + eps) (a per-token factor of a linear map), so no
+// wavefront waits for the rest of the row; and with the partial sums of a
+// split GEMV folded in: RMSNorm of x + their sum (the residual stream,
+// written back), or siluMul of the gate / up sums (math.zig:69-71).
 // ---------------------------------------------------------------------------
 enum class Prep : int { F32 = 0, RmsNorm = 1, Pairs = 2 };
+
+constexpr uint32_t kPrepValues = 512;  // values per wavefront
 
 struct PrepArgs {
     const float *x;      // tokens x K (F32, RmsNorm)
     const float *norm;   // RmsNorm weights
-    float eps;
     uint32_t k, tokens;
     // Partial sums [slices][tokens][part_n] of the GEMV that produced the
     // input (slices 0: none). RmsNorm: x + their sum, also stored to x_out
@@ -474,6 +523,7 @@ struct PrepArgs {
     float *x_out;
     uint8_t *digits;
     float *mult;
+    float *ss;           // RmsNorm: [token][K / 512] sums of squares
 };
 
 __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
@@ -515,117 +565,76 @@ __device__ __forceinline__ void input8(const PrepArgs &a, uint32_t t, uint32_t e
     }
 }
 
-// ITERS > 0: K <= 2048 ITERS, and each thread loads all its values (and norm
-// weights) at once, keeps them in registers for both passes, so the kernel
-// is one memory round trip; ITERS == 0: any K, loaded stretch by stretch.
-template <Prep M, int ITERS>
-__global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
-    const uint32_t t = blockIdx.x;
+template <Prep M>
+__global__ __launch_bounds__(64) void prep_batch_kernel(const PrepArgs a) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t e = blockIdx.x * kPrepValues + lane * 8;
     const uint32_t gpr = a.k >> 6;
     const uint32_t tile = t / kTokenTile;
     const uint32_t tt = t % kTokenTile;
     const bool real = t < a.tokens;
-    const uint32_t src = real ? t : 0;  // padding tokens read token 0 and discard it
-    const bool write_back = M == Prep::RmsNorm && a.slices && real;
-    constexpr int kHeld = ITERS > 0 ? ITERS : 1;
-    float held[kHeld][8], norm_w[kHeld][8];
-    if constexpr (ITERS > 0) {
+    const bool in_row = e < a.k;  // (whole groups: K is a multiple of 64)
+    float v[8];
+    input8<M>(a, real ? t : 0, in_row ? e : 0, v);  // padding tokens read token 0 and drop it
 #pragma unroll
-        for (int it = 0; it < ITERS; ++it) {
-            const uint32_t e = threadIdx.x * 8 + 2048u * it;
-            const uint32_t ec = e < a.k ? e : 0;  // past the row: a valid address, never used
-            input8<M>(a, src, ec, held[it]);
-            if constexpr (M == Prep::RmsNorm) load8(a.norm + ec, norm_w[it]);
-            if (write_back && e < a.k) store8(a.x_out + (size_t)t * a.k + e, held[it]);
-        }
-    }
-    float inv = 1.0f;
+    for (int i = 0; i < 8; ++i) v[i] = real && in_row ? v[i] : 0.0f;
     if constexpr (M == Prep::RmsNorm) {
-        // Sum of squares of the row: per thread, then across the workgroup
-        // in a fixed order.
+        float w[8];
+        load8(a.norm + (in_row ? e : 0), w);
+        if (a.slices && real && in_row) store8(a.x_out + (size_t)t * a.k + e, v);
         float ss = 0.0f;
-        if constexpr (ITERS > 0) {
 #pragma unroll
-            for (int it = 0; it < ITERS; ++it)
-                if (threadIdx.x * 8 + 2048u * it < a.k)
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(held[it][i], held[it][i]));
-        } else {
-            for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
-                float v[8];
-                input8<M>(a, src, e, v);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
-            }
-        }
+        for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
         ss = dev::wave_sum(ss);
-        __shared__ float wsum[4];
-        if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        ss = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-        inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)a.k), a.eps)));
+        if (lane == 0) a.ss[(size_t)t * gridDim.x + blockIdx.x] = ss;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(v[i], w[i]);
     }
-    auto encode = [&](uint32_t e, float (&v)[8]) {
-        float amax = 0.0f;
+    if (!in_row) return;
+    float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, dev::xor_lane<1>(amax));
-        amax = fmaxf(amax, dev::xor_lane<2>(amax));
-        amax = fmaxf(amax, dev::xor_lane<4>(amax));
-        const int ex = dev::chunk_exponent(amax);
-        const float up = __builtin_ldexpf(1.0f, 22 - ex);
-        uint32_t u[8];
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, dev::xor_lane<1>(amax));
+    amax = fmaxf(amax, dev::xor_lane<2>(amax));
+    amax = fmaxf(amax, dev::xor_lane<4>(amax));
+    const int ex = dev::chunk_exponent(amax);
+    const float up = __builtin_ldexpf(1.0f, 22 - ex);
+    uint32_t u[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
-        const uint32_t g = e >> 6;
-        const uint32_t j = (e >> 3) & 7u;  // 8-value block within the group
-        uint8_t *dst = a.digits + ((size_t)tile * gpr + g) * kGroupBytes + tt * 64 + j * 8;
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
+    const uint32_t g = e >> 6;
+    const uint32_t j = (e >> 3) & 7u;  // 8-value block within the group
+    uint8_t *dst = a.digits + ((size_t)tile * gpr + g) * kGroupBytes + tt * 64 + j * 8;
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
-            const int sh = 8 * p;
-            uint2 w;
-            w.x = ((u[0] >> sh) & 0xffu) | (((u[2] >> sh) & 0xffu) << 8) | (((u[4] >> sh) & 0xffu) << 16) |
-                  (((u[6] >> sh) & 0xffu) << 24);
-            w.y = ((u[1] >> sh) & 0xffu) | (((u[3] >> sh) & 0xffu) << 8) | (((u[5] >> sh) & 0xffu) << 16) |
-                  (((u[7] >> sh) & 0xffu) << 24);
-            *reinterpret_cast<uint2 *>(dst + p * kPlaneBytes) = w;
-        }
-        if (j == 0) a.mult[((size_t)tile * gpr + g) * kTokenTile + tt] = __builtin_ldexpf(1.0f, ex - 22);
-    };
-    if constexpr (ITERS > 0) {
-#pragma unroll
-        for (int it = 0; it < ITERS; ++it) {
-            const uint32_t e = threadIdx.x * 8 + 2048u * it;
-            if (e >= a.k) break;  // (whole 64-value groups: 8 consecutive threads stop together)
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float x = real ? held[it][i] : 0.0f;
-                if constexpr (M == Prep::RmsNorm) x = __fmul_rn(__fmul_rn(x, inv), norm_w[it][i]);
-                v[i] = x;
-            }
-            encode(e, v);
-        }
-    } else {
-        // (x_out is written here, in the last pass over x: it may be x.)
-        for (uint32_t e = threadIdx.x * 8; e < a.k; e += 256 * 8) {
-            float v[8];
-            if (real) {
-                input8<M>(a, t, e, v);
-                if (write_back) store8(a.x_out + (size_t)t * a.k + e, v);
-                if constexpr (M == Prep::RmsNorm) {
-                    float w[8];
-                    load8(a.norm + e, w);
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(__fmul_rn(v[i], inv), w[i]);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-            }
-            encode(e, v);
-        }
+    for (int p = 0; p < 3; ++p) {
+        const int sh = 8 * p;
+        uint2 w;
+        w.x = ((u[0] >> sh) & 0xffu) | (((u[2] >> sh) & 0xffu) << 8) | (((u[4] >> sh) & 0xffu) << 16) |
+              (((u[6] >> sh) & 0xffu) << 24);
+        w.y = ((u[1] >> sh) & 0xffu) | (((u[3] >> sh) & 0xffu) << 8) | (((u[5] >> sh) & 0xffu) << 16) |
+              (((u[7] >> sh) & 0xffu) << 24);
+        *reinterpret_cast<uint2 *>(dst + p * kPlaneBytes) = w;
     }
+    if (j == 0) a.mult[((size_t)tile * gpr + g) * kTokenTile + tt] = __builtin_ldexpf(1.0f, ex - 22);
+}
+
+}  // namespace
+
+namespace {
+
+// Layout of a batch activation buffer: digit planes, multipliers, then the
+// RMSNorm sums of squares [token][ss_parts].
+uint32_t ss_parts_of(uint32_t cols) { return (cols + kPrepValues - 1) / kPrepValues; }
+
+float *mult_of(void *digits, uint32_t tokens, uint32_t cols) {
+    const size_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+    return reinterpret_cast<float *>(static_cast<uint8_t *>(digits) + tiles * (cols / 64) * kGroupBytes);
+}
+
+float *ss_of(void *digits, uint32_t tokens, uint32_t cols) {
+    const size_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+    return mult_of(digits, tokens, cols) + tiles * (cols / 64) * kTokenTile;
 }
 
 }  // namespace
@@ -633,7 +642,8 @@ __global__ __launch_bounds__(256) void prep_batch_kernel(const PrepArgs a) {
 size_t batch_digit_bytes(uint32_t tokens, uint32_t cols) {
     const size_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     const size_t groups = cols / 64;
-    return tiles * groups * kGroupBytes + tiles * groups * kTokenTile * sizeof(float) + 256;
+    return tiles * groups * kGroupBytes + tiles * groups * kTokenTile * sizeof(float) +
+           tiles * kTokenTile * ss_parts_of(cols) * sizeof(float) + 256;
 }
 
 hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols, void *digits,
@@ -642,13 +652,14 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     PrepArgs p{};
     p.x = in.x;
     p.norm = in.norm;
-    p.eps = in.eps;
     p.k = cols;
     p.tokens = tokens;
     p.digits = static_cast<uint8_t *>(digits);
-    p.mult = reinterpret_cast<float *>(p.digits + (size_t)tiles * (cols / 64) * kGroupBytes);
+    p.mult = mult_of(digits, tokens, cols);
+    p.ss = ss_of(digits, tokens, cols);
     Prep form = in.mode == GemvInput::RmsNorm ? Prep::RmsNorm : Prep::F32;
     if (in.mode != GemvInput::F32 && in.mode != GemvInput::RmsNorm) return hipErrorInvalidValue;
+    if (form == Prep::RmsNorm && ss_parts_of(cols) > kTokenTile) return hipErrorInvalidValue;  // K > 8192
     if (sums && sums->slices) {
         if (sums->slices > kMaxSlices || !sums->part) return hipErrorInvalidValue;
         p.part = sums->part;
@@ -662,22 +673,12 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
         }
         p.part_n = sums->rows;
     }
-    const dim3 grid(tiles * kTokenTile);
-    const uint32_t iters = (cols + 2047) / 2048;
-#define QWH_PREP_CASE(M_)                                                                             \
-    switch (iters) {                                                                                  \
-    case 1: prep_batch_kernel<M_, 1><<<grid, 256, 0, s>>>(p); break;                                 \
-    case 2: prep_batch_kernel<M_, 2><<<grid, 256, 0, s>>>(p); break;                                 \
-    case 3: prep_batch_kernel<M_, 3><<<grid, 256, 0, s>>>(p); break;                                 \
-    case 4: prep_batch_kernel<M_, 4><<<grid, 256, 0, s>>>(p); break;                                 \
-    default: prep_batch_kernel<M_, 0><<<grid, 256, 0, s>>>(p); break;                                \
-    }
+    const dim3 grid(ss_parts_of(cols), tiles * kTokenTile);
     switch (form) {
-    case Prep::F32: QWH_PREP_CASE(Prep::F32) break;
-    case Prep::RmsNorm: QWH_PREP_CASE(Prep::RmsNorm) break;
-    case Prep::Pairs: QWH_PREP_CASE(Prep::Pairs) break;
+    case Prep::F32: prep_batch_kernel<Prep::F32><<<grid, 64, 0, s>>>(p); break;
+    case Prep::RmsNorm: prep_batch_kernel<Prep::RmsNorm><<<grid, 64, 0, s>>>(p); break;
+    case Prep::Pairs: prep_batch_kernel<Prep::Pairs><<<grid, 64, 0, s>>>(p); break;
     }
-#undef QWH_PREP_CASE
     return hipGetLastError();
 }
 
@@ -728,11 +729,16 @@ void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint
     else gemv_q4_split_kernel<1, 8><<<grid, 256, 0, s>>>(a);
 }
 
-SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const SplitPlan &plan) {
-    const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const SplitPlan &plan,
+                     const BatchNorm &norm) {
     SplitArgs a{};
     a.digits = static_cast<const uint8_t *>(digits);
-    a.mult = reinterpret_cast<const float *>(a.digits + (size_t)tiles * (w.cols / 64) * kGroupBytes);
+    a.mult = mult_of(const_cast<void *>(digits), tokens, w.cols);
+    if (norm.rms) {
+        a.ss = ss_of(const_cast<void *>(digits), tokens, w.cols);
+        a.ss_parts = ss_parts_of(w.cols);
+        a.eps = norm.eps;
+    }
     a.scales = reinterpret_cast<const uint16_t *>(w.scales);
     a.data = w.data;
     a.n = w.rows;
@@ -754,22 +760,24 @@ size_t batch_partial_bytes(uint32_t tokens, const Matrix &w) {
 }
 
 hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                      float *partials) {
+                                      float *partials, const BatchNorm &norm) {
     const SplitPlan plan = split_plan(w);
     if (!plan.tw || !partials) return hipErrorInvalidValue;
-    SplitArgs a = split_args(digits, w, tokens, plan);
+    if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
+    SplitArgs a = split_args(digits, w, tokens, plan, norm);
     a.part = partials;
     launch_split(s, plan, a, (tokens + kTokenTile - 1) / kTokenTile);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens, float *out,
-                                const float *residual, bool pairs, float *partials) {
+                                const float *residual, bool pairs, float *partials, const BatchNorm &norm) {
     if (pairs && (w.rows & 1u)) return hipErrorInvalidValue;
+    if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     const SplitPlan plan = split_plan(w);
     if (plan.tw && (plan.slices == 1 || partials)) {
-        SplitArgs a = split_args(digits, w, tokens, plan);
+        SplitArgs a = split_args(digits, w, tokens, plan, norm);
         a.out = out;
         a.residual = residual;
         a.pairs = pairs ? 1u : 0u;
@@ -785,7 +793,12 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
     // K not a multiple of 256: the unsplit form, one tile per workgroup.
     BatchArgs a{};
     a.digits = static_cast<const uint8_t *>(digits);
-    a.mult = reinterpret_cast<const float *>(a.digits + (size_t)tiles * (w.cols / 64) * kGroupBytes);
+    a.mult = mult_of(const_cast<void *>(digits), tokens, w.cols);
+    if (norm.rms) {
+        a.ss = ss_of(const_cast<void *>(digits), tokens, w.cols);
+        a.ss_parts = ss_parts_of(w.cols);
+        a.eps = norm.eps;
+    }
     a.scales = reinterpret_cast<const uint16_t *>(w.scales);
     a.data = w.data;
     a.out = out;
