@@ -27,6 +27,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (native: stays in registers)
 
 constexpr int BM = 128;
 constexpr int BN = 128;
@@ -45,25 +46,25 @@ struct GemmArgs {
 // A group's tile data held in registers between its global loads and its
 // LDS stores: 4 x 16 B of activations and 16 B of codes per thread.
 struct Staged {
-    uint4 a[4];
-    uint4 codes;
+    u32x4 a[4];
+    u32x4 codes;
 };
 
+// Rows past the matrix (tokens past M, weight rows past N) load its last row:
+// they only reach output rows or columns that are never stored. Every load
+// is unconditional, so all of them are in flight together.
 __device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32_t m0, uint32_t n0, uint32_t g,
                                            int tid) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int idx = tid + it * 256;  // 0..1023: 128 rows x 8 chunks of 8 bf16
-        const int row = idx >> 3;
+        const uint32_t row = min(m0 + (idx >> 3), a.m - 1);
         const int col = (idx & 7) * 8;
-        st.a[it] = make_uint4(0, 0, 0, 0);
-        if (m0 + row < a.m) st.a[it] = *reinterpret_cast<const uint4 *>(a.x + (size_t)(m0 + row) * a.k + g * BK + col);
+        st.a[it] = *reinterpret_cast<const u32x4 *>(a.x + (size_t)row * a.k + g * BK + col);
     }
-    const int row = tid >> 1;
+    const uint32_t row = min(n0 + (tid >> 1), a.n - 1);
     const int half = tid & 1;
-    st.codes = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-    if (n0 + row < a.n)
-        st.codes = *reinterpret_cast<const uint4 *>(a.data + (size_t)(n0 + row) * (a.k / 2) + g * 32 + half * 16);
+    st.codes = *reinterpret_cast<const u32x4 *>(a.data + (size_t)row * (a.k / 2) + g * 32 + half * 16);
 }
 
 // Activations as they are; codes decoded to the bf16 of u - 8.
@@ -73,7 +74,7 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, u
         const int idx = tid + it * 256;
         const int row = idx >> 3;
         const int col = (idx & 7) * 8;
-        *reinterpret_cast<uint4 *>(&lds_a[row * LDS_STRIDE + col]) = st.a[it];
+        *reinterpret_cast<u32x4 *>(&lds_a[row * LDS_STRIDE + col]) = st.a[it];
     }
     const int row = tid >> 1;
     const int half = tid & 1;
@@ -92,9 +93,9 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, u
             packed[i * 4 + p] = (__float_as_uint((float)c0) >> 16) | (__float_as_uint((float)c1) & 0xffff0000u);
         }
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(&lds_b[row * LDS_STRIDE + half * 32]);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(&lds_b[row * LDS_STRIDE + half * 32]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]);
+    for (int q = 0; q < 4; ++q) dst[q] = u32x4{packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]};
 }
 
 __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) {
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         ncol[j] = n0 + wn * 64 + j * 32 + li;
-        srow[j] = a.scales + (size_t)(ncol[j] < a.n ? ncol[j] : 0) * gpr;
+        srow[j] = a.scales + (size_t)min(ncol[j], a.n - 1) * gpr;
     }
 
     f32x16 acc[2][2];
@@ -133,21 +134,20 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
     // Two groups in flight ahead of the one being multiplied: group g + 2's
     // loads are issued while g is multiplied and g + 1 waits in registers.
     Staged st0, st1;
-    if (g0 < g1) {
-        stage_load(a, st0, m0, n0, g0, tid);
-        if (g0 + 1 < g1) stage_load(a, st1, m0, n0, g0 + 1, tid);
-        stage_store(st0, lds_a[0], lds_b[0], tid);
-    }
+    stage_load(a, st0, m0, n0, g0, tid);
+    stage_load(a, st1, m0, n0, min(g0 + 1, g1 - 1), tid);
+    stage_store(st0, lds_a[0], lds_b[0], tid);
     __syncthreads();
 
     // One group: loads for g + 2 into `next2` (its previous content, group
     // g, is already in LDS), multiply group g from LDS buffer `buf`, then
     // store group g + 1 (in `next1`) into the other buffer.
     auto step = [&](uint32_t g, int buf, Staged &next2, const Staged &next1) {
-        if (g + 2 < g1) stage_load(a, next2, m0, n0, g + 2, tid);
+        // (Past the range: the last group again, never used.)
+        stage_load(a, next2, m0, n0, min(g + 2, g1 - 1), tid);
         float s[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) s[j] = ncol[j] < a.n ? dev::f16_bits_to_f32(srow[j][g]) : 0.0f;
+        for (int j = 0; j < 2; ++j) s[j] = dev::f16_bits_to_f32(srow[j][g]);
 
         const uint16_t *la = lds_a[buf];
         const uint16_t *lb = lds_b[buf];
@@ -172,6 +172,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
                     part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], ks == 0 ? f32x16{} : part[i][j],
                                                                          0, 0, 0);
         }
+        // Group g + 1 into the other buffer first: its decode runs while the
+        // products above are still in the matrix pipeline.
+        stage_store(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
         // Scale each group's partial product by its weight row's scale: in the
         // 32x32 output layout every value a lane holds lies in column l % 32.
 #pragma unroll
@@ -180,7 +183,6 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(s[j], part[i][j][r], acc[i][j][r]);
-        if (g + 1 < g1) stage_store(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
         __syncthreads();
     };
     // Unrolled by two so the staging registers are addressed statically.
@@ -208,13 +210,35 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
     }
 }
 
-// out[i] = sum over ranges z (in order) of partial[z][i].
+// out[i] = sum over ranges z (in order) of partial[z][i], four outputs per
+// thread; every range's loads are issued before the first add.
+constexpr uint32_t kMaxSplits = 8;
+
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *partial, uint32_t splits, size_t count,
                                                           float *out) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
-        float s = partial[i];
-        for (uint32_t z = 1; z < splits; ++z) s += partial[(size_t)z * count + i];
-        out[i] = s;
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= count) return;
+    if ((count & 3) == 0) {  // (every range's slice 16-byte aligned)
+        float4 v[kMaxSplits];
+#pragma unroll
+        for (uint32_t z = 0; z < kMaxSplits; ++z)
+            if (z < splits) v[z] = *reinterpret_cast<const float4 *>(partial + (size_t)z * count + i);
+        float4 s = v[0];
+#pragma unroll
+        for (uint32_t z = 1; z < kMaxSplits; ++z)
+            if (z < splits) {
+                s.x += v[z].x;
+                s.y += v[z].y;
+                s.z += v[z].z;
+                s.w += v[z].w;
+            }
+        *reinterpret_cast<float4 *>(out + i) = s;
+        return;
+    }
+    for (size_t e = i; e < i + 4 && e < count; ++e) {
+        float s = partial[e];
+        for (uint32_t z = 1; z < splits; ++z) s += partial[(size_t)z * count + e];
+        out[e] = s;
     }
 }
 
@@ -227,7 +251,7 @@ uint32_t gemm_splits(int cus, uint32_t tokens, const Matrix &w) {
     const uint32_t target = (uint32_t)(cus > 0 ? cus : 256);
     uint32_t splits = (target + tiles - 1) / tiles;
     if (splits > groups / 2) splits = groups / 2;
-    if (splits > 8) splits = 8;
+    if (splits > kMaxSplits) splits = kMaxSplits;
     return splits < 1 ? 1 : splits;
 }
 
@@ -253,9 +277,7 @@ hipError_t launch_gemm_q4_bf16(hipStream_t s, int cus, const uint16_t *x, const 
     gemm_q4_bf16_kernel<<<grid, 256, 0, s>>>(args);
     if (args.splits > 1) {
         const size_t count = (size_t)tokens * w.rows;
-        size_t blocks = (count + 255) / 256;
-        if (blocks > 4096) blocks = 4096;
-        gemm_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(args.out, args.splits, count, out);
+        gemm_reduce_kernel<<<(unsigned)((count + 1023) / 1024), 256, 0, s>>>(args.out, args.splits, count, out);
     }
     return hipGetLastError();
 }
