@@ -78,7 +78,11 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, u
     }
     const int row = tid >> 1;
     const int half = tid & 1;
-    const uint32_t w[4] = {st.codes.x, st.codes.y, st.codes.z, st.codes.w};
+    // (The codes count as changed here, so their decode is not moved up to
+    // their load: using a load's value waits for every load issued before it.)
+    u32x4 codes = st.codes;
+    asm volatile("" : "+v"(codes));
+    const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
     uint32_t packed[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -142,12 +146,15 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
     // One group: loads for g + 2 into `next2` (its previous content, group
     // g, is already in LDS), multiply group g from LDS buffer `buf`, then
     // store group g + 1 (in `next1`) into the other buffer.
-    auto step = [&](uint32_t g, int buf, Staged &next2, const Staged &next1) {
+    // The scales of group g come from the step before, issued ahead of that
+    // step's tile loads (waiting for a load waits for every older one, so
+    // scales fetched in their own step would drain the tile prefetch).
+    auto step = [&](uint32_t g, int buf, Staged &next2, const Staged &next1, const uint32_t (&s_now)[2],
+                    uint32_t (&s_next)[2]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) s_next[j] = srow[j][min(g + 1, g1 - 1)];
         // (Past the range: the last group again, never used.)
         stage_load(a, next2, m0, n0, min(g + 2, g1 - 1), tid);
-        float s[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) s[j] = dev::f16_bits_to_f32(srow[j][g]);
 
         const uint16_t *la = lds_a[buf];
         const uint16_t *lb = lds_b[buf];
@@ -177,6 +184,13 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
         stage_store(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
         // Scale each group's partial product by its weight row's scale: in the
         // 32x32 output layout every value a lane holds lies in column l % 32.
+        float s[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t bits = s_now[j];
+            asm volatile("" : "+v"(bits));  // (converted here, not at its load)
+            s[j] = dev::f16_bits_to_f32((uint16_t)bits);
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -186,12 +200,15 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
         __syncthreads();
     };
     // Unrolled by two so the staging registers are addressed statically.
+    uint32_t sc0[2], sc1[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sc0[j] = srow[j][g0];
     uint32_t g = g0;
     for (; g + 1 < g1; g += 2) {
-        step(g, 0, st0, st1);
-        step(g + 1, 1, st1, st0);
+        step(g, 0, st0, st1, sc0, sc1);
+        step(g + 1, 1, st1, st0, sc1, sc0);
     }
-    if (g < g1) step(g, 0, st0, st1);
+    if (g < g1) step(g, 0, st0, st1, sc0, sc1);
 
     // Store: value r of a lane is row 8 * (r / 4) + 4 * (l / 32) + r % 4 of the
     // 32x32 tile, column l % 32.
