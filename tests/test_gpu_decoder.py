@@ -109,6 +109,42 @@ def test_token_ids_on_each_gemv_path(ctx, batch, env, monkeypatch):
         ref.close()
 
 
+# Widths that are not multiples of 256 (5, 7 and 15 groups): the small-batch
+# GEMV has no K-split form for them and runs its unsplit kernel.
+ODD = dict(hidden=320, layers=2, heads=5, kv_heads=5, head_dim=64, ffn=448, vocab=500,
+           max_positions=64, eps=1e-6, theta=1e6)
+
+
+@pytest.mark.parametrize("batch,config,env", [
+    (18, TINY, ()),                             # two 16-token tiles of partial sums and digit planes
+    (3, TINY, ("QWH_DECODER_NO_SPLIT",)),      # o / gate|up / down add their own slices
+    (3, ODD, ()),                               # unsplit kernel, RMSNorm factor in its epilogue
+])
+def test_token_ids_on_each_batched_form(ctx, batch, config, env, monkeypatch):
+    for name in env:
+        monkeypatch.setenv(name, "1")
+    seed = 21
+    gpu = qa.Decoder(ctx, batch=batch, **config)
+    ref = o.Decoder(seed, batch, **config)
+    try:
+        gpu.init_synthetic(seed)
+        for b in range(batch):
+            gpu.prefill_random(b, (3 * b) % 23, seed)
+            ref.prefill_random(b, (3 * b) % 23)
+        start = [o.start_token(seed, b, config["vocab"]) for b in range(batch)]
+        ids = gpu.generate(start, 12)
+        for b in range(batch):
+            t = start[b]
+            expected = []
+            for _ in range(12):
+                t = ref.step(b, t)
+                expected.append(t)
+            assert ids[:, b].tolist() == expected, (b, batch, env)
+    finally:
+        gpu.close()
+        ref.close()
+
+
 def test_step_and_generate_agree(ctx):
     seed = 11
     a = qa.Decoder(ctx, batch=2, **TINY)

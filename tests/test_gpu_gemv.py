@@ -116,6 +116,7 @@ def test_q4_gemv_edge_shapes(ctx, rows, cols, tokens):
     (40, 10240, 3),     # K past 8192: activation prep stretch by stretch, two units per wave
     (65600, 256, 2),    # over 4096 row tiles: four tiles per workgroup
     (65600, 128, 3),    # four tiles, two groups per unit
+    (300, 1024, 40),    # K split into 4 slices over three token tiles, partial row block
 ])
 def test_q4_batch_gemv(ctx, rows, cols, tokens):
     # Two or more tokens run on the matrix-core kernel.
