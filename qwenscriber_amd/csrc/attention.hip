@@ -600,8 +600,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float *key, const 
 }
 
 void attention_shape(int cus, const AttentionArgs &a, uint32_t &chunk, uint32_t &splits) {
-    // Positions per workgroup: a multiple of one full block (STEP * 4); enough
-    // workgroups to fill the device about twice, at most kMaxSplits ranges.
+    // Positions per workgroup: a multiple of one full block (STEP * 4), at
+    // least two of them; enough workgroups to fill the device about twice, at
+    // most kMaxSplits ranges. (At batch 1, 128-position ranges spend more on
+    // the per-range query prologue and the combine than their extra
+    // workgroups win back: 17 ranges of 256 beat 34 of 128 at 4096 positions.)
     const uint32_t lpp = a.head_dim / 16;
     const uint32_t step = (64 / lpp) * kWaves * kBlockPositions;
     const uint32_t target = (uint32_t)(cus > 0 ? cus : 256) * 2;
@@ -611,7 +614,7 @@ void attention_shape(int cus, const AttentionArgs &a, uint32_t &chunk, uint32_t 
     if (want_splits > kMaxSplits) want_splits = kMaxSplits;
     const uint32_t per = (a.capacity + want_splits - 1) / want_splits;
     chunk = ((per + step - 1) / step) * step;
-    if (chunk < step) chunk = step;
+    if (chunk < 2 * step) chunk = 2 * step;
     splits = (a.capacity + chunk - 1) / chunk;
     if (splits < 1) splits = 1;
 }

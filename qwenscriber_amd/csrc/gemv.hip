@@ -151,25 +151,30 @@ __global__ __launch_bounds__(256) void prep_q4_kernel(const float *x, uint32_t t
 }
 
 // Exact integer dot product of one 16-byte slice of q4 codes (32 weights)
-// with its activations' digit planes: sum_k (u_k - 8) * x_int_k, evaluated
-// as a Horner chain over the six digit planes (plane 5 first), each plane a
-// chain of four v_dot8_i32_i4. Every partial value is bounded by
-// 32 * 8 * 2^22 = 2^30, so the int32 result is exact.
+// with its activations' digit planes: sum_k (u_k - 8) * x_int_k. Two
+// independent Horner chains, planes 5..3 and planes 2..0, each step a run of
+// four v_dot8_i32_i4, joined as hi * 16^3 + lo. Two chains halve the
+// dependent-issue latency of one chain of 24; that latency is what the
+// last units of a launch pay after their data has arrived. Every partial
+// value is bounded by 32 * 8 * 2^22 = 2^30, so the int32 result is exact
+// (and equal to the single-chain Horner value).
 __device__ __forceinline__ int q4_slice_dot(const uint4 codes, const uint32_t (&d)[24]) {
-    const int c0 = (int)(codes.x ^ 0x88888888u);
-    const int c1 = (int)(codes.y ^ 0x88888888u);
-    const int c2 = (int)(codes.z ^ 0x88888888u);
-    const int c3 = (int)(codes.w ^ 0x88888888u);
-    int acc = 0;
+    const int c[4] = {(int)(codes.x ^ 0x88888888u), (int)(codes.y ^ 0x88888888u), (int)(codes.z ^ 0x88888888u),
+                      (int)(codes.w ^ 0x88888888u)};
+    int hi = 0, lo = 0;
 #pragma unroll
-    for (int j = 5; j >= 0; --j) {
-        if (j != 5) acc = acc * 16;
-        acc = __builtin_amdgcn_sdot8(c0, (int)d[j * 4 + 0], acc, false);
-        acc = __builtin_amdgcn_sdot8(c1, (int)d[j * 4 + 1], acc, false);
-        acc = __builtin_amdgcn_sdot8(c2, (int)d[j * 4 + 2], acc, false);
-        acc = __builtin_amdgcn_sdot8(c3, (int)d[j * 4 + 3], acc, false);
+    for (int j = 2; j >= 0; --j) {
+        if (j != 2) {
+            hi = hi * 16;
+            lo = lo * 16;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            hi = __builtin_amdgcn_sdot8(c[q], (int)d[(j + 3) * 4 + q], hi, false);
+            lo = __builtin_amdgcn_sdot8(c[q], (int)d[j * 4 + q], lo, false);
+        }
     }
-    return acc;
+    return hi * 4096 + lo;
 }
 
 // Forms of the q4 GEMV's activations.
