@@ -217,24 +217,46 @@ struct ActLds {
     float partial[4];
 };
 
+// The row's values (and RMSNorm weights) this thread encodes, fetched before
+// the first unit's weights are requested: the wait for them then leaves the
+// weight loads in flight (loads complete in issue order). Threads past the
+// row's end load its last 8 values and drop them in block_encode.
+struct RowValues {
+    float v[3][8];
+    float w[3][8];
+};
+
 template <Src M>
-__device__ __forceinline__ void block_encode(const GemvQ4Args &a, uint32_t token, ActLds &lds) {
+__device__ __forceinline__ void block_fetch(const GemvQ4Args &a, uint32_t token, RowValues &rv) {
     const int tid = threadIdx.x;
     const uint32_t k8 = a.k / 8;
-    const float *row = a.x + (size_t)token * a.k;
+    const float4 *row = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k);
+    const float4 *norm = reinterpret_cast<const float4 *>(a.norm);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        if (p * 256 >= (int)k8) break;  // uniform: no thread has values in this stretch
+        const uint32_t e8 = tid + p * 256 < k8 ? tid + p * 256 : k8 - 1;
+        const float4 lo = row[e8 * 2], hi = row[e8 * 2 + 1];
+        rv.v[p][0] = lo.x; rv.v[p][1] = lo.y; rv.v[p][2] = lo.z; rv.v[p][3] = lo.w;
+        rv.v[p][4] = hi.x; rv.v[p][5] = hi.y; rv.v[p][6] = hi.z; rv.v[p][7] = hi.w;
+        if constexpr (M == Src::RmsNorm) {
+            const float4 wl = norm[e8 * 2], wh = norm[e8 * 2 + 1];
+            rv.w[p][0] = wl.x; rv.w[p][1] = wl.y; rv.w[p][2] = wl.z; rv.w[p][3] = wl.w;
+            rv.w[p][4] = wh.x; rv.w[p][5] = wh.y; rv.w[p][6] = wh.z; rv.w[p][7] = wh.w;
+        }
+    }
+}
+
+template <Src M>
+__device__ __forceinline__ void block_encode(const GemvQ4Args &a, const RowValues &rv, ActLds &lds) {
+    const int tid = threadIdx.x;
+    const uint32_t k8 = a.k / 8;
     float v[3][8];
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
-        const uint32_t e8 = tid + p * 256;
-        if (e8 < k8) {
-            const float4 lo = reinterpret_cast<const float4 *>(row)[e8 * 2];
-            const float4 hi = reinterpret_cast<const float4 *>(row)[e8 * 2 + 1];
-            v[p][0] = lo.x; v[p][1] = lo.y; v[p][2] = lo.z; v[p][3] = lo.w;
-            v[p][4] = hi.x; v[p][5] = hi.y; v[p][6] = hi.z; v[p][7] = hi.w;
-        } else {
+        const bool in = p * 256 < (int)k8 && tid + p * 256 < k8;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[p][i] = 0.0f;
-        }
+        for (int i = 0; i < 8; ++i) v[p][i] = in ? rv.v[p][i] : 0.0f;
     }
     if constexpr (M == Src::RmsNorm) {
         // math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w, the sum of
@@ -242,18 +264,9 @@ __device__ __forceinline__ void block_encode(const GemvQ4Args &a, uint32_t token
         // order).
         float w[3][8];
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
-            const uint32_t e8 = tid + p * 256;
-            if (e8 < k8) {
-                const float4 lo = reinterpret_cast<const float4 *>(a.norm)[e8 * 2];
-                const float4 hi = reinterpret_cast<const float4 *>(a.norm)[e8 * 2 + 1];
-                w[p][0] = lo.x; w[p][1] = lo.y; w[p][2] = lo.z; w[p][3] = lo.w;
-                w[p][4] = hi.x; w[p][5] = hi.y; w[p][6] = hi.z; w[p][7] = hi.w;
-            } else {
+        for (int p = 0; p < 3; ++p)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) w[p][i] = 0.0f;
-            }
-        }
+            for (int i = 0; i < 8; ++i) w[p][i] = p * 256 < (int)k8 ? rv.w[p][i] : 0.0f;
         float ss = 0.0f;
 #pragma unroll
         for (int p = 0; p < 3; ++p)
@@ -385,18 +398,33 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
 
     Slice A[U][S], B[U][S];
     float resA = 0.0f, resB = 0.0f;
-    // The first unit's loads go out before the activations are formed, so
-    // their latency covers that work.
-    if (count) {
-        load(A, wave);
-        resA = load_res(wave);
+    // Issue order: the row's values, then the first unit's weights, so that
+    // their latency covers the encoding. The weight loads are unconditional
+    // (a wave without full units loads a clamped unit it never uses): a
+    // branch around them would make the wait for the row's values wait for
+    // them as well.
+    RowValues rv;
+    if constexpr (M != Src::Digits) block_fetch<M>(a, token, rv);
+    {
+        const uint32_t first = count ? wave : (full_units ? full_units - 1 : 0);
+        const uint32_t row0 = first * (U * RG) + rr;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const uint32_t row = row0 + u * RG < a.n ? row0 + u * RG : a.n - 1;
+                const uint32_t c = li + s * L;
+                A[u][s].codes = load_stream16(a.data + (row * row_bytes + c * 16));
+                A[u][s].scale = load_scale(a.scales, row * gpr + (c >> 1));
+            }
     }
 
     __shared__ __attribute__((aligned(16))) ActLds lds;
-    if constexpr (M != Src::Digits) block_encode<M>(a, token, lds);
+    if constexpr (M != Src::Digits) block_encode<M>(a, rv, lds);
     uint32_t D[S][24];
     float m[S];
     lane_activations<S, L, M>(a, li, token, D, m, lds);
+    if (count) resA = load_res(wave);
 
     auto process = [&](const Slice (&src)[U][S], float res, uint32_t unit) {
         float acc[U];
