@@ -40,10 +40,10 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def q4_gemv_bytes(rows, cols):
+def q4_gemv_bytes(rows, cols, group_bytes=34):
     # Algorithmic bytes of one batch-1 call: codes + f16 scales (34 B per 64
-    # weights), f32 activations in, f32 outputs out.
-    return rows * cols * 34 // 64 + 4 * cols + 4 * rows
+    # weights for q4, 42 for q5), f32 activations in, f32 outputs out.
+    return rows * cols * group_bytes // 64 + 4 * cols + 4 * rows
 
 
 def profiled_traffic():
@@ -73,10 +73,12 @@ def time_events(ctx, fn, steps, warm=2):
     return ms / steps
 
 
-def bench_gemv(ctx, qa, rows, cols, steps, warmup, rotate_bytes, seed=1, stream=8):
-    per = rows * cols * 34 // 64
+def bench_gemv(ctx, qa, rows, cols, steps, warmup, rotate_bytes, seed=1, stream=8, fmt=None):
+    fmt = qa.FORMAT_Q4 if fmt is None else fmt
+    group_bytes = qa.DATA_BYTES[fmt] + 2
+    per = rows * cols * group_bytes // 64
     copies = max(1, math.ceil(rotate_bytes / per))
-    mats = [ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, seed, stream + 1000 * c, 0.02) for c in range(copies)]
+    mats = [ctx.matrix_synthetic(fmt, rows, cols, seed, stream + 1000 * c, 0.02) for c in range(copies)]
     x = ctx.buffer(cols * 4)
     ctx.synth_normal(seed, 100 + stream, cols, 1.0, x.ptr)
     out = ctx.buffer(rows * 4)
@@ -94,7 +96,7 @@ def bench_gemv(ctx, qa, rows, cols, steps, warmup, rotate_bytes, seed=1, stream=
         ctx.matrix_release(m)
     for b in (x, out):
         b.free()
-    return dict(copies=copies, call_ms=call_ms, bytes=q4_gemv_bytes(rows, cols))
+    return dict(copies=copies, call_ms=call_ms, bytes=q4_gemv_bytes(rows, cols, group_bytes))
 
 
 def pmc_pass(ctx, qa, steps):
@@ -203,6 +205,11 @@ def bench_small(ctx, qa, steps):
     ctx.matrix_release(m)
     x.free()
     y.free()
+    # The 0.6B lm_head shape in q5 (the WebGPU decoder's format), rotated over
+    # >= 2 GB of copies like the headline.
+    g5 = bench_gemv(ctx, qa, 151936, 1024, steps, 10, 2.1e9, stream=9, fmt=qa.FORMAT_Q5)
+    gbs = g5["bytes"] / (g5["call_ms"] * 1e-3) / 1e9
+    out["q5_gemv_lm_head_0p6b"] = dict(us=g5["call_ms"] * 1e3, GBs=gbs, frac=gbs / 8000.0)
     # q4 GEMM, bf16 activations, M = 1500 at [6144 x 2048].
     gemm = {}
     for rows, cols in ((6144, 2048), (2048, 6144)):

@@ -120,7 +120,9 @@ int32_t qwh_matrix_release(qwh_ctx *ctx, uint64_t matrix);
 
 /* kernels.zig:182-206 Matrix.apply / :118-158 linearQuantized:
  * out[tokens][rows] = W[rows][cols] * x[tokens][cols], f32 in, f32 out.
- * `cols` must equal the matrix's column count. */
+ * `cols` must equal the matrix's column count. Formats q4 and q8 at any
+ * shape; q5 (the WebGPU decoder's format, passes.ts:63-67) for cols <= 6144
+ * with an 8-byte aligned data plane below 4 GiB, else QWH_E_UNSUPPORTED. */
 int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t cols,
                    uint32_t tokens, float *out_dev);
 /* qwh_linear in two halves, for callers that apply several matrices to the

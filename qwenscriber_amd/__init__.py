@@ -8,6 +8,7 @@ binding fails loudly when the library is not built -- there is no CPU path.
 from __future__ import annotations
 
 from ._lib import (  # noqa: F401
+    DATA_BYTES,
     FORMAT_Q4,
     FORMAT_Q5,
     FORMAT_Q8,

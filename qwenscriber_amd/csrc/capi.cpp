@@ -375,6 +375,13 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
     }
     if (m->format == QWH_FORMAT_Q8)
         return check_hip(ctx, launch_gemv_q8(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, nullptr), "gemv q8");
+    if (m->format == QWH_FORMAT_Q5) {
+        if (!gemv_q5_supported(m->rows, m->cols))
+            return fail(ctx, QWH_E_UNSUPPORTED, "q5 linear is built for K <= 6144 and data planes below 4 GiB");
+        if (((uintptr_t)m->data & 7u) != 0)
+            return fail(ctx, QWH_E_INVALID_ARGUMENT, "q5 data plane must be 8-byte aligned");
+        return check_hip(ctx, launch_gemv_q5(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev), "gemv q5");
+    }
     return fail(ctx, QWH_E_UNSUPPORTED, "linear over format %d is not built", m->format);
 }
 

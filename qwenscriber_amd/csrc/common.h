@@ -105,6 +105,11 @@ hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const
                               uint32_t tokens, float *out, const float *residual);
 hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
+// q5 GEMV (quant.zig:253-269 planes) with f32 activations, any token count
+// (one launch; each token's workgroups encode its activations). Shapes with
+// K <= 6144 and a data plane below 4 GiB.
+bool gemv_q5_supported(uint32_t rows, uint32_t cols);
+hipError_t launch_gemv_q5(hipStream_t s, int cus, const float *x, const Matrix &w, uint32_t tokens, float *out);
 hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
 

@@ -622,6 +622,269 @@ __global__ __launch_bounds__(256) void gemv_q8_generic_kernel(const GemvQ8Args a
     }
 }
 
+// ---------------------------------------------------------------------------
+// q5 (quant.zig:253-269): per group of 64 codes, 32 bytes of low nibbles
+// (even column in the low nibble) and 8 bytes of fifth bits (bit j % 8 of
+// byte j / 8 is the fifth bit of column j). A lane takes a 32-column half
+// group ("slice"): two 8-byte loads of nibbles (a group is 40 bytes, so a
+// slice is only 8-byte aligned) and the slice's 4 bytes of fifth bits.
+//
+// Arithmetic. The codes are expanded to bytes u = nibble | fifth << 4 in
+// [0, 31], in the column order of the batch GEMV: within each 8-column block
+// the bytes of columns {0,2,4,6}, then {1,3,5,7} (a nibble mask splits the
+// packed bytes that way; the fifth bits of those four columns are bits
+// 0,2,4,6 of one byte, moved to bit 4 of bytes 0..3 by one multiply --
+// (b & 0x55) * 0x00410410 has them at bits 4, 12, 20, 28 and no carry reaches
+// those bits). The activations of a 32-column chunk are written as
+// x_int = rint(x * 2^(22-e)) (2^e bounds the chunk's |x|) in three signed
+// base-256 digit planes d0 + 256 d1 + 65536 d2, stored in the same column
+// order, so that v_dot4_i32_i8 multiplies matching columns. With S_j the
+// chunk's sum of plane j's digits,
+//     sum (u - 16) x_int = sum_j 256^j (sum u d_j - 16 S_j),
+// each plane's term exact in int32 (below 2^18), combined in f32 and scaled
+// by the group's f16 scale times 2^(e-22).
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+struct Slice5 {
+    u32x2 lo0, lo1;  // nibbles of columns 0..15 and 16..31
+    uint32_t hi;     // fifth bits of columns 0..31 (byte q: columns 8q..8q+7)
+    uint16_t scale;
+};
+
+struct Act5Lds {
+    uint32_t words[kMaxChunks * 24];  // chunk c: plane j dword m at 24c + 8j + m
+    int sums[kMaxChunks * 4];         // chunk c: S_j at 4c + j
+    float mult[kMaxChunks];
+};
+
+struct GemvQ5Args {
+    const float *x;         // tokens x K
+    const uint16_t *scales; // N * K/64
+    const uint8_t *data;    // N * K/64 * 40
+    float *out;             // tokens x N
+    uint32_t n, k, t, row_groups;  // t = K/32 slices per row
+};
+
+// Encodes the token's K activations into LDS (block-wide; thread t takes
+// values 8t .. 8t+7 of each 2048-value stretch, four threads per chunk).
+__device__ __forceinline__ void block_encode5(const GemvQ5Args &a, uint32_t token, Act5Lds &lds) {
+    const int tid = threadIdx.x;
+    const uint32_t k8 = a.k / 8;
+    const float4 *row = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        if (p * 256 >= (int)k8) break;  // uniform
+        const uint32_t e8 = tid + p * 256;
+        const bool in = e8 < k8;
+        const uint32_t ec = in ? e8 : k8 - 1;
+        const float4 lo = row[ec * 2], hi = row[ec * 2 + 1];
+        float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (!in) v[i] = 0.0f;
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+        amax = fmaxf(amax, dev::xor_lane<1>(amax));
+        amax = fmaxf(amax, dev::xor_lane<2>(amax));
+        const int e = dev::chunk_exponent(amax);
+        const float up = __builtin_ldexpf(1.0f, 22 - e);
+        // Bytes 0..2 of u[i] are the signed digits d0, d1, d2 of x_int
+        // (adding 0x808080 makes each digit d + 128 with no carries).
+        uint32_t u[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
+        uint32_t planes[6];
+        int sums[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+#pragma unroll
+            for (int par = 0; par < 2; ++par) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w |= ((u[2 * b + par] >> (8 * j)) & 0xffu) << (8 * b);
+                planes[2 * j + par] = w;
+            }
+            int sj = __builtin_amdgcn_sdot4((int)planes[2 * j], 0x01010101, 0, false);
+            sj = __builtin_amdgcn_sdot4((int)planes[2 * j + 1], 0x01010101, sj, false);
+            sj += __builtin_bit_cast(int, dev::xor_lane<1>(__builtin_bit_cast(float, sj)));
+            sj += __builtin_bit_cast(int, dev::xor_lane<2>(__builtin_bit_cast(float, sj)));
+            sums[j] = sj;
+        }
+        if (in) {
+            const uint32_t chunk = e8 >> 2;
+            const uint32_t q = e8 & 3u;
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                lds.words[chunk * 24 + j * 8 + 2 * q] = planes[2 * j];
+                lds.words[chunk * 24 + j * 8 + 2 * q + 1] = planes[2 * j + 1];
+            }
+            if (q == 0) {
+                lds.mult[chunk] = __builtin_ldexpf(1.0f, e - 22);
+#pragma unroll
+                for (int j = 0; j < 3; ++j) lds.sums[chunk * 4 + j] = sums[j];
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The activation operands of chunk c from LDS.
+struct Act5 {
+    uint32_t d[24];
+    int sum[3];
+    float mult;
+};
+
+__device__ __forceinline__ void load_act5(const Act5Lds &lds, uint32_t c, Act5 &x) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(&lds.words[c * 24]);
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        const uint4 w = src[j];
+        x.d[j * 4 + 0] = w.x;
+        x.d[j * 4 + 1] = w.y;
+        x.d[j * 4 + 2] = w.z;
+        x.d[j * 4 + 3] = w.w;
+    }
+    const int4 sv = *reinterpret_cast<const int4 *>(&lds.sums[c * 4]);
+    x.sum[0] = sv.x;
+    x.sum[1] = sv.y;
+    x.sum[2] = sv.z;
+    x.mult = lds.mult[c];
+}
+
+// sum (u - 16) x_int of one slice, in f32 (the integer plane terms exact).
+__device__ __forceinline__ float q5_slice_dot(const Slice5 &sl, const Act5 &x) {
+    const uint32_t w[4] = {sl.lo0.x, sl.lo0.y, sl.lo1.x, sl.lo1.y};
+    int p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            const uint32_t nib = (par ? w[q] >> 4 : w[q]) & 0x0f0f0f0fu;
+            const uint32_t fifth = (((sl.hi >> (8 * q + par)) & 0x55u) * 0x00410410u) & 0x10101010u;
+            const int um = (int)(nib | fifth);
+            const int m = 2 * q + par;
+            p0 = __builtin_amdgcn_sdot4(um, (int)x.d[m], p0, false);
+            p1 = __builtin_amdgcn_sdot4(um, (int)x.d[8 + m], p1, false);
+            p2 = __builtin_amdgcn_sdot4(um, (int)x.d[16 + m], p2, false);
+        }
+    }
+    p0 -= 16 * x.sum[0];
+    p1 -= 16 * x.sum[1];
+    p2 -= 16 * x.sum[2];
+    return ((float)p2 * 65536.0f + (float)p1 * 256.0f) + (float)p0;
+}
+
+__device__ __forceinline__ Slice5 load_slice5(const GemvQ5Args &a, uint32_t row, uint32_t c, uint32_t row_bytes,
+                                              uint32_t gpr) {
+    const uint8_t *base = a.data + (row * row_bytes + (c >> 1) * 40u);
+    Slice5 sl;
+    sl.lo0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base + (c & 1u) * 16u));
+    sl.lo1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base + (c & 1u) * 16u + 8u));
+    sl.hi = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(base + 32u + (c & 1u) * 4u));
+    sl.scale = load_scale(a.scales, row * gpr + (c >> 1));
+    return sl;
+}
+
+// Lane mapping and unit walk as the q4 kernel (RG = 64/L rows per row group,
+// S slices per lane, U row groups per unit, grid-stride units, the next
+// unit's loads issued before the current one is multiplied).
+template <int S, int L, int U>
+__global__ __launch_bounds__(256) void gemv_q5_kernel(const GemvQ5Args a) {
+    constexpr int RG = 64 / L;
+    constexpr int log_l = Log2<L>::value;
+    constexpr int log_u = Log2<U>::value;
+    const int lane = threadIdx.x & 63;
+    const int rr = lane >> log_l;
+    const int li = lane & (L - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t token = blockIdx.y;
+    const uint32_t gpr = a.k >> 6;
+    const uint32_t row_bytes = gpr * 40u;
+    const uint32_t units = (a.row_groups + U - 1) / U;
+    const uint32_t full_units = a.n / (U * RG);
+    const uint32_t count = full_units > wave ? (full_units - wave + nwaves - 1) / nwaves : 0;
+    float *out = a.out + (size_t)token * a.n;
+
+    // Rows past the end (only in the last, partial unit) load the last row
+    // and are dropped at the store.
+    auto load = [&](Slice5 (&dst)[U][S], uint32_t unit) __attribute__((always_inline)) {
+        const uint32_t row0 = unit * (U * RG) + rr;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const uint32_t row = row0 + u * RG < a.n ? row0 + u * RG : a.n - 1;
+                dst[u][s] = load_slice5(a, row, li + s * L, row_bytes, gpr);
+            }
+    };
+
+    Slice5 A[U][S], B[U][S];
+    __shared__ __attribute__((aligned(16))) Act5Lds lds;
+    load(A, count ? wave : (full_units ? full_units - 1 : 0));
+    block_encode5(a, token, lds);
+    Act5 X[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) load_act5(lds, li + s * L, X[s]);
+
+    auto process = [&](const Slice5 (&src)[U][S], uint32_t unit) __attribute__((always_inline)) {
+        float acc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const float part = q5_slice_dot(src[u][s], X[s]) * (dev::f16_bits_to_f32(src[u][s].scale) * X[s].mult);
+                acc[u] = s == 0 ? part : acc[u] + part;
+            }
+        }
+        const float total = reduce_rows<U, L>(acc, lane);
+        const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+        if ((li & ((L >> log_u) - 1)) == 0 && row < a.n) out[row] = total;
+    };
+
+    uint32_t i = 0;
+    for (; i + 1 < count; i += 2) {
+        const uint32_t ua = wave + i * nwaves, ub = ua + nwaves;
+        load(B, ub);
+        process(A, ua);
+        load(A, i + 2 < count ? ub + nwaves : ub);
+        process(B, ub);
+    }
+    if (i < count) process(A, wave + i * nwaves);
+    if (full_units < units && full_units % nwaves == wave) {
+        load(B, full_units);
+        process(B, full_units);
+    }
+}
+
+// Any K up to the LDS encoding's 6144: one wavefront per row, lanes striding
+// over the row's slices.
+__global__ __launch_bounds__(256) void gemv_q5_generic_kernel(const GemvQ5Args a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
+    const uint32_t token = blockIdx.y;
+    const uint32_t gpr = a.k >> 6;
+    const uint32_t row_bytes = gpr * 40u;
+    __shared__ __attribute__((aligned(16))) Act5Lds lds;
+    block_encode5(a, token, lds);
+    float *out = a.out + (size_t)token * a.n;
+    for (uint32_t row = wave; row < a.n; row += nwaves) {
+        float acc = 0.0f;
+        for (uint32_t c = lane; c < a.t; c += 64) {
+            Act5 x;
+            load_act5(lds, c, x);
+            const Slice5 sl = load_slice5(a, row, c, row_bytes, gpr);
+            acc += q5_slice_dot(sl, x) * (dev::f16_bits_to_f32(sl.scale) * x.mult);
+        }
+        acc = dev::wave_sum(acc);
+        if (lane == 0) out[row] = acc;
+    }
+}
+
 uint32_t gcd_u32(uint32_t a, uint32_t b) {
     while (b) {
         const uint32_t t = a % b;
@@ -832,6 +1095,46 @@ hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &
     QWH_GEMV8_CASE(3, 16, 2)
     args.row_groups = w.rows;
     gemv_q8_generic_kernel<<<dim3(grid_blocks(gemv_q8_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
+    return hipGetLastError();
+}
+
+bool gemv_q5_supported(uint32_t rows, uint32_t cols) {
+    // The activations are encoded into LDS (at most kMaxChunks chunks), and
+    // the kernels address the data plane with 32-bit offsets.
+    return cols % 64 == 0 && cols / 32 <= (uint32_t)kMaxChunks && (uint64_t)rows * (cols / 64) * 40 < (1ull << 32) &&
+           (uint64_t)rows * 4096ull < (1ull << 32);
+}
+
+#define QWH_GEMV5_CASE(S_, L_, U_)                                                                 \
+    if (S == S_ && L == L_) {                                                                      \
+        args.row_groups = (args.n + (64 / L_) - 1) / (64 / L_);                                    \
+        const uint32_t units = (args.row_groups + U_ - 1) / U_;                                    \
+        auto kernel = gemv_q5_kernel<S_, L_, U_>;                                                  \
+        kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);                \
+        return hipGetLastError();                                                                  \
+    }
+
+hipError_t launch_gemv_q5(hipStream_t s, int cus, const float *x, const Matrix &w, uint32_t tokens, float *out) {
+    if (!gemv_q5_supported(w.rows, w.cols)) return hipErrorNotSupported;
+    GemvQ5Args args{};
+    const uint32_t T = w.cols / 32;
+    args.x = x;
+    args.scales = reinterpret_cast<const uint16_t *>(w.scales);
+    args.data = w.data;
+    args.out = out;
+    args.n = w.rows;
+    args.k = w.cols;
+    args.t = T;
+    const uint32_t L = gcd_u32(T, 64);
+    const uint32_t S = T / L;
+    QWH_GEMV5_CASE(1, 64, 4)
+    QWH_GEMV5_CASE(1, 32, 4)
+    QWH_GEMV5_CASE(1, 16, 4)
+    QWH_GEMV5_CASE(2, 64, 2)
+    QWH_GEMV5_CASE(3, 64, 2)
+    QWH_GEMV5_CASE(3, 32, 2)
+    args.row_groups = w.rows;
+    gemv_q5_generic_kernel<<<dim3(grid_blocks(gemv_q5_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
     return hipGetLastError();
 }
 

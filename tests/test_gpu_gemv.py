@@ -153,6 +153,75 @@ def test_q8_gemv_edge_shapes(ctx, rows, cols, tokens):
     check(ctx, o.Q8, w, x, tokens, f"q8 {rows}x{cols} tokens {tokens}")
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [
+    (1001, 1024, 1),    # one slice per lane, 32 lanes per row (0.6B shapes)
+    (130, 2048, 2),     # one slice, 64 lanes per row
+    (64, 512, 1),       # 16 lanes per row
+    (96, 4096, 1),      # two slices per lane
+    (70, 3072, 3),      # three slices, 32 lanes per row
+    (33, 6144, 1),      # three slices, 64 lanes per row; the widest encoded row
+    (48, 320, 2),       # generic kernel (five groups)
+    (17, 896, 1),       # generic kernel (seven slices per lane group)
+    (1, 64, 4),
+])
+def test_q5_gemv_shapes(ctx, rows, cols, tokens):
+    # quant.zig:253-269 planes (fifth bits in their own 8 bytes per group).
+    w = o.normal(rows * cols, 10, rows, 0.02).reshape(rows, cols)
+    x = o.normal(tokens * cols, 10, 1000 + cols)
+    check(ctx, o.Q5, w, x, tokens, f"q5 {rows}x{cols} tokens {tokens}")
+
+
+def test_q5_gemv_awkward_values(ctx):
+    # Codes at both ends (-16 and 15 in one group), a zero row, a zero group
+    # of activations, a huge dynamic range inside one chunk.
+    rows, cols, tokens = 40, 1024, 2
+    w = o.normal(rows * cols, 11, 0, 0.02).reshape(rows, cols)
+    w[3] = 0.0
+    w[5, :32] = np.float32(-1.0)
+    w[5, 32:64] = np.float32(1.0)
+    w[6, ::2] = np.float32(0.5)
+    x = o.normal(tokens * cols, 11, 1).reshape(tokens, cols)
+    x[0, 64:128] = 0.0
+    x[1, 7] = np.float32(2e4)
+    x[1, 8] = np.float32(-3e-9)
+    scales, data = o.quantize_rows(o.Q5, w)
+    expected = o.linear_quantized(o.Q5, scales, data, rows, cols, x.reshape(-1), tokens)
+    actual = run_linear(ctx, o.Q5, scales, data, rows, cols, x.reshape(-1), tokens)
+    assert np.all(actual[:, 3] == 0.0)
+    assert_close(actual, expected, what="q5 awkward values")
+
+
+def test_q5_lm_head_synthetic_on_device(ctx):
+    # The 0.6B lm_head shape in q5, generated and quantized on the device.
+    rows, cols, seed, stream = 151936, 1024, 1, 9
+    handle = ctx.matrix_synthetic(qa.FORMAT_Q5, rows, cols, seed, stream, 0.02)
+    s_ref, d_ref = o.quantize_rows(o.Q5, o.normal(rows * cols, seed, stream, 0.02).reshape(rows, cols))
+    sp, dp = ctx.matrix_planes(handle)
+    d_gpu = np.empty(d_ref.size, np.uint8)
+    ctx._check(ctx.lib.qwh_download(ctx.handle, d_gpu.ctypes.data, dp, d_gpu.nbytes))
+    assert o.fnv1a64(d_gpu) == o.fnv1a64(d_ref)
+    x = o.normal(cols, 1, 109)
+    expected = o.linear_quantized(o.Q5, s_ref, d_ref, rows, cols, x, 1)
+    xb = ctx.to_device(x)
+    ob = ctx.buffer(rows * 4)
+    ctx.linear(handle, xb.ptr, cols, 1, ob.ptr)
+    actual = ob.download(np.float32).reshape(1, rows)
+    assert_close(actual, expected, what="q5 lm_head [151936x1024]")
+    ctx.matrix_release(handle)
+    xb.free()
+    ob.free()
+
+
+def test_q5_gemv_rejects_unbuilt_width(ctx):
+    # Rows wider than the in-LDS activation encoding (6144) are not built.
+    rows, cols = 2, 6208
+    w = o.normal(rows * cols, 12, 0, 0.02).reshape(rows, cols)
+    scales, data = o.quantize_rows(o.Q5, w)
+    with pytest.raises(qa.QwhError) as err:
+        run_linear(ctx, o.Q5, scales, data, rows, cols, o.normal(cols, 12, 1), 1)
+    assert err.value.status == -3
+
+
 def test_q4_gemv_awkward_values(ctx):
     # Zero rows, a subnormal-scale row, activations with zero chunks and a
     # huge dynamic range inside one chunk.
