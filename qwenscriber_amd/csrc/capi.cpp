@@ -424,7 +424,10 @@ int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, ui
     const Matrix *m = find_matrix(ctx, matrix);
     if (!m) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
     if (cols != m->cols) return fail(ctx, QWH_E_SHAPE_MISMATCH, "x has %u columns, the matrix %u", cols, m->cols);
-    if (m->format != QWH_FORMAT_Q4) return fail(ctx, QWH_E_UNSUPPORTED, "bf16 GEMM is built for q4 only");
+    if (m->format != QWH_FORMAT_Q4 && m->format != QWH_FORMAT_Q5)
+        return fail(ctx, QWH_E_UNSUPPORTED, "bf16 GEMM is built for q4 and q5");
+    if (m->format == QWH_FORMAT_Q5 && ((uintptr_t)m->data & 7u) != 0)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "q5 data plane must be 8-byte aligned");
     if (tokens == 0 || m->rows == 0) return QWH_OK;
     if (tokens > 65535u * 128u) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "tokens %u", tokens);
     QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
@@ -432,8 +435,8 @@ int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, ui
     if (((uintptr_t)x_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "x must be 16-byte aligned");
     const size_t scratch = gemm_scratch_bytes(ctx->cus, tokens, *m);
     if (scratch) QWH_TRY(ensure_workspace(ctx, ctx->scratch, scratch));
-    return check_hip(ctx, launch_gemm_q4_bf16(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, ctx->scratch.ptr),
-                     "gemm q4 bf16");
+    return check_hip(ctx, launch_gemm_bf16(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, ctx->scratch.ptr),
+                     "gemm bf16");
 }
 
 int32_t qwh_quantize_rows(qwh_ctx *ctx, int32_t format, const float *values_dev, uint32_t rows, uint32_t cols,

@@ -148,11 +148,11 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
 hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
                                       float *partials, const BatchNorm &norm = BatchNorm{});
 
-// q4 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
+// q4 / q5 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
 // partials: gemm_scratch_bytes (0 when the tiles alone fill the device).
 size_t gemm_scratch_bytes(int cus, uint32_t tokens, const Matrix &w);
-hipError_t launch_gemm_q4_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w,
-                               uint32_t tokens, float *out, void *scratch);
+hipError_t launch_gemm_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w,
+                            uint32_t tokens, float *out, void *scratch);
 
 // q8 decode attention (attention.hip). `cached` is per sequence when
 // cached_dev is non-null (device array of batch values), else uniform.

@@ -1,9 +1,11 @@
-// q4 GEMM with bf16 activations on the bf16 MFMA units: the prefill /
+// q4 / q5 GEMM with bf16 activations on the bf16 MFMA units: the prefill /
 // audio-token product of kernels.zig:118-158 with tokens = M > 1.
 //
-// out[m][n] = sum_k x[m][k] * (u[n][k] - 8) * s[n][k/64]
+// out[m][n] = sum_k x[m][k] * (u[n][k] - bias) * s[n][k/64]
 //
-// The codes (u - 8, in [-8, 7]) are exact in bf16, so the MFMA multiplies the
+// The codes (q4: u - 8 in [-8, 7]; q5: u - 16 in [-16, 15], the fifth bit of
+// each code in its group's last 8 bytes, quant.zig:253-269) are exact in
+// bf16, so the MFMA multiplies the
 // exact decoded integers by the exact bf16 activations; each 64-wide group's
 // partial product is accumulated in f32 on its own and then scaled by the
 // group's f16 scale (folding the scale into bf16 weights would round it).
@@ -37,22 +39,26 @@ constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row (padding agains
 struct GemmArgs {
     const uint16_t *x;       // M x K bf16
     const uint16_t *scales;  // N x K/64 f16
-    const uint8_t *data;     // N x K/2 q4 codes
+    const uint8_t *data;     // N x K/64 groups of 32 (q4) or 40 (q5) bytes
     float *out;              // M x N, or splits x M x N partials
     uint32_t m, n, k;
     uint32_t splits;
 };
 
 // A group's tile data held in registers between its global loads and its
-// LDS stores: 4 x 16 B of activations and 16 B of codes per thread.
+// LDS stores: 4 x 16 B of activations and 16 B of codes per thread (q5: and
+// the 4 bytes of those 32 codes' fifth bits).
 struct Staged {
     u32x4 a[4];
     u32x4 codes;
+    uint32_t fifth;
 };
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Rows past the matrix (tokens past M, weight rows past N) load its last row:
 // they only reach output rows or columns that are never stored. Every load
 // is unconditional, so all of them are in flight together.
+template <bool Q5>
 __device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32_t m0, uint32_t n0, uint32_t g,
                                            int tid) {
 #pragma unroll
@@ -64,10 +70,20 @@ __device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32
     }
     const uint32_t row = min(n0 + (tid >> 1), a.n - 1);
     const int half = tid & 1;
-    st.codes = *reinterpret_cast<const u32x4 *>(a.data + (size_t)row * (a.k / 2) + g * 32 + half * 16);
+    if constexpr (Q5) {
+        // A 40-byte group: the half row's nibbles are only 8-byte aligned.
+        const uint8_t *grp = a.data + (size_t)row * (a.k / 64) * 40 + g * 40;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(grp + half * 16);
+        const u32x2 hi = *reinterpret_cast<const u32x2 *>(grp + half * 16 + 8);
+        st.codes = u32x4{lo.x, lo.y, hi.x, hi.y};
+        st.fifth = *reinterpret_cast<const uint32_t *>(grp + 32 + half * 4);
+    } else {
+        st.codes = *reinterpret_cast<const u32x4 *>(a.data + (size_t)row * (a.k / 2) + g * 32 + half * 16);
+    }
 }
 
-// Activations as they are; codes decoded to the bf16 of u - 8.
+// Activations as they are; codes decoded to the bf16 of u - 8 (q5: u - 16).
+template <bool Q5>
 __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, uint16_t *lds_b, int tid) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -84,6 +100,21 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, u
     asm volatile("" : "+v"(codes));
     const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
     uint32_t packed[16];
+    if constexpr (Q5) {
+        uint32_t fifth = st.fifth;
+        asm volatile("" : "+v"(fifth));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                // Codes 8i + 2p (low nibble of byte p) and 8i + 2p + 1; their
+                // fifth bits are bits 8i + 2p and 8i + 2p + 1 of the word.
+                const int c0 = (int)(((w[i] >> (8 * p)) & 0xfu) | (((fifth >> (8 * i + 2 * p)) & 1u) << 4)) - 16;
+                const int c1 = (int)(((w[i] >> (8 * p + 4)) & 0xfu) | (((fifth >> (8 * i + 2 * p + 1)) & 1u) << 4)) - 16;
+                packed[i * 4 + p] = (__float_as_uint((float)c0) >> 16) | (__float_as_uint((float)c1) & 0xffff0000u);
+            }
+        }
+    } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t sw = w[i] ^ 0x88888888u;
@@ -97,12 +128,14 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, u
             packed[i * 4 + p] = (__float_as_uint((float)c0) >> 16) | (__float_as_uint((float)c1) & 0xffff0000u);
         }
     }
+    }
     u32x4 *dst = reinterpret_cast<u32x4 *>(&lds_b[row * LDS_STRIDE + half * 32]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dst[q] = u32x4{packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]};
 }
 
-__global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) {
+template <bool Q5>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * LDS_STRIDE];
     const int tid = threadIdx.x;
@@ -138,9 +171,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
     // Two groups in flight ahead of the one being multiplied: group g + 2's
     // loads are issued while g is multiplied and g + 1 waits in registers.
     Staged st0, st1;
-    stage_load(a, st0, m0, n0, g0, tid);
-    stage_load(a, st1, m0, n0, min(g0 + 1, g1 - 1), tid);
-    stage_store(st0, lds_a[0], lds_b[0], tid);
+    stage_load<Q5>(a, st0, m0, n0, g0, tid);
+    stage_load<Q5>(a, st1, m0, n0, min(g0 + 1, g1 - 1), tid);
+    stage_store<Q5>(st0, lds_a[0], lds_b[0], tid);
     __syncthreads();
 
     // One group: loads for g + 2 into `next2` (its previous content, group
@@ -154,7 +187,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
 #pragma unroll
         for (int j = 0; j < 2; ++j) s_next[j] = srow[j][min(g + 1, g1 - 1)];
         // (Past the range: the last group again, never used.)
-        stage_load(a, next2, m0, n0, min(g + 2, g1 - 1), tid);
+        stage_load<Q5>(a, next2, m0, n0, min(g + 2, g1 - 1), tid);
 
         const uint16_t *la = lds_a[buf];
         const uint16_t *lb = lds_b[buf];
@@ -181,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_bf16_kernel(const GemmArgs a) 
         }
         // Group g + 1 into the other buffer first: its decode runs while the
         // products above are still in the matrix pipeline.
-        stage_store(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
+        stage_store<Q5>(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
         // Scale each group's partial product by its weight row's scale: in the
         // 32x32 output layout every value a lane holds lies in column l % 32.
         float s[2];
@@ -279,8 +312,9 @@ size_t gemm_scratch_bytes(int cus, uint32_t tokens, const Matrix &w) {
     return splits > 1 ? (size_t)splits * tokens * w.rows * sizeof(float) : 0;
 }
 
-hipError_t launch_gemm_q4_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w, uint32_t tokens,
-                               float *out, void *scratch) {
+hipError_t launch_gemm_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w, uint32_t tokens,
+                            float *out, void *scratch) {
+    if (w.format != QWH_FORMAT_Q4 && w.format != QWH_FORMAT_Q5) return hipErrorNotSupported;
     GemmArgs args{};
     args.x = x;
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
@@ -291,7 +325,10 @@ hipError_t launch_gemm_q4_bf16(hipStream_t s, int cus, const uint16_t *x, const 
     args.splits = gemm_splits(cus, tokens, w);
     args.out = args.splits > 1 ? static_cast<float *>(scratch) : out;
     dim3 grid((w.rows + BN - 1) / BN, (tokens + BM - 1) / BM, args.splits);
-    gemm_q4_bf16_kernel<<<grid, 256, 0, s>>>(args);
+    if (w.format == QWH_FORMAT_Q5)
+        gemm_bf16_kernel<true><<<grid, 256, 0, s>>>(args);
+    else
+        gemm_bf16_kernel<false><<<grid, 256, 0, s>>>(args);
     if (args.splits > 1) {
         const size_t count = (size_t)tokens * w.rows;
         gemm_reduce_kernel<<<(unsigned)((count + 1023) / 1024), 256, 0, s>>>(args.out, args.splits, count, out);

@@ -22,8 +22,8 @@ def widen(bits: np.ndarray) -> np.ndarray:
     return (bits.astype(np.uint32) << 16).view(np.float32)
 
 
-def run_gemm(ctx, rows, cols, scales, data, xb16, tokens):
-    handle = ctx.matrix_upload(o.Q4, rows, cols, scales, data)
+def run_gemm(ctx, rows, cols, scales, data, xb16, tokens, fmt=o.Q4):
+    handle = ctx.matrix_upload(fmt, rows, cols, scales, data)
     xb = ctx.to_device(xb16)
     ob = ctx.buffer(tokens * rows * 4)
     ctx.linear_bf16(handle, xb.ptr, cols, tokens, ob.ptr)
@@ -60,3 +60,22 @@ def test_gemm_edge_shapes(ctx, rows, cols, m):
     expected = o.linear_quantized(o.Q4, scales, data, rows, cols, widen(xb16), m)
     actual = run_gemm(ctx, rows, cols, scales, data, xb16, m)
     assert_close(actual, expected, what=f"gemm {m}x{rows}x{cols}")
+
+
+@pytest.mark.parametrize("rows,cols,m", [(6144, 2048, 390), (2048, 6144, 128), (100, 128, 1), (130, 256, 7),
+                                         (257, 192, 33), (64, 64, 130)])
+def test_q5_gemm(ctx, rows, cols, m):
+    # q5 planes (quant.zig:253-269): 40-byte groups, fifth bits in the last 8.
+    # M = 390 is the audio-token count of a 30 s window.
+    w = o.normal(rows * cols, 15, rows, 0.02).reshape(rows, cols)
+    w[0, :64] = np.float32(-1.0)   # codes at both ends of [-16, 15]
+    w[0, 64:128] = np.float32(1.0)
+    scales, data = o.quantize_rows(o.Q5, w)
+    xb16 = to_bf16_bits(o.normal(m * cols, 15, 9))
+    actual = run_gemm(ctx, rows, cols, scales, data, xb16, m, fmt=o.Q5)
+    gpr = cols // 64
+    sample = np.unique(np.linspace(0, rows - 1, min(rows, 256)).astype(int))
+    s_sub = np.concatenate([scales[r * gpr * 2:(r + 1) * gpr * 2] for r in sample])
+    d_sub = np.concatenate([data[r * gpr * 40:(r + 1) * gpr * 40] for r in sample])
+    expected = o.linear_quantized(o.Q5, s_sub, d_sub, len(sample), cols, widen(xb16), m)
+    assert_close(actual[:, sample], expected, what=f"q5 GEMM M {m} {rows}x{cols}")
