@@ -44,6 +44,12 @@ extern "C" {
 #define QWH_E_INVALID_STATE (-8)
 #define QWH_E_LIMIT_EXCEEDED (-9)
 #define QWH_E_NOT_FOUND (-10)
+/* Shard statuses (abi.zig:58-63, :72-77; mapping abi.zig:90-146). */
+#define QWH_E_BAD_MAGIC (-4)
+#define QWH_E_BAD_VERSION (-5)
+#define QWH_E_CHECKSUM_MISMATCH (-6)
+#define QWH_E_TRUNCATED (-11)
+#define QWH_E_UNSUPPORTED_MODEL (-13)
 /* A HIP runtime error. Not in the reference (it has no device runtime). */
 #define QWH_E_DEVICE (-64)
 
@@ -117,6 +123,58 @@ int32_t qwh_matrix_synthetic(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32
 /* Device addresses of a matrix's two planes. */
 int32_t qwh_matrix_planes(qwh_ctx *ctx, uint64_t matrix, void **scales_dev, void **data_dev);
 int32_t qwh_matrix_release(qwh_ctx *ctx, uint64_t matrix);
+
+/* ---------------------------------------------------------------------- */
+/* `.qw` weight shards (container.zig)                                     */
+/* ---------------------------------------------------------------------- */
+
+/* One index entry as stored on disk (container.zig:103-125 Entry, 40 bytes):
+ * kind is a container.TensorKind value (:337-381), layer 0 for tensors of
+ * no layer, 1..text_layers for decoder layers, 1024 + i for audio layers;
+ * format is a dtype.Format value (0 f32, 1 f16, 2 bf16, 16 q4, 17 q5, 18 q8);
+ * offset_bytes is relative to the payload. */
+typedef struct qwh_tensor_entry {
+    uint16_t kind;
+    uint16_t layer;
+    uint8_t format;
+    uint8_t rank;
+    uint16_t reserved;
+    uint32_t dims[4];
+    uint64_t offset_bytes;
+    uint64_t len_bytes;
+} qwh_tensor_entry;
+
+/* container.File.parse (container.zig:175-217) on the host, no device
+ * needed: the header, then every entry in order (known format, shape, exact
+ * length), sorted by (layer, kind), ranges in order, 16-byte aligned and
+ * inside the payload. Statuses as the reference ABI maps File.parse's errors:
+ * QWH_E_BAD_MAGIC, QWH_E_BAD_VERSION, QWH_E_TRUNCATED, QWH_E_SHAPE_MISMATCH
+ * (shape or byte length), QWH_E_UNSUPPORTED_MODEL (unknown format),
+ * QWH_E_INVALID_ARGUMENT (index not sorted, ranges overlapping or
+ * misaligned). */
+int32_t qwh_shard_validate(const void *bytes, uint64_t len, uint32_t *tensor_count);
+/* File.verifyChecksum (container.zig:283-290): the header's checksum against
+ * the low 32 bits of FNV-1a 64 over the payload; QWH_E_CHECKSUM_MISMATCH. */
+int32_t qwh_shard_verify_checksum(const void *bytes, uint64_t len);
+/* File.find (container.zig:226-236): the entry of (kind, layer), or
+ * QWH_E_NOT_FOUND. */
+int32_t qwh_shard_find(const void *bytes, uint64_t len, uint16_t kind, uint16_t layer,
+                       qwh_tensor_entry *out);
+/* Validates a shard and copies its payload to the device once; the bytes may
+ * be freed afterwards. */
+int32_t qwh_shard_load(qwh_ctx *ctx, const void *bytes, uint64_t len, uint64_t *out_shard);
+/* File.tensorBytes (container.zig:238-243) on the device: the address of a
+ * tensor inside the loaded payload (and its entry, when `entry` is set). */
+int32_t qwh_shard_tensor(qwh_ctx *ctx, uint64_t shard, uint16_t kind, uint16_t layer, void **dev,
+                         qwh_tensor_entry *entry);
+/* File.quantizedPlanes (container.zig:245-262) as a matrix handle that
+ * borrows the two planes inside the loaded payload (no copy); element-format
+ * tensors return QWH_E_NOT_FOUND, as quantizedPlanes returns null. */
+int32_t qwh_shard_matrix(qwh_ctx *ctx, uint64_t shard, uint16_t kind, uint16_t layer,
+                         uint64_t *out_matrix);
+/* Frees the device payload; QWH_E_INVALID_STATE while a matrix borrows from
+ * it. */
+int32_t qwh_shard_release(qwh_ctx *ctx, uint64_t shard);
 
 /* kernels.zig:182-206 Matrix.apply / :118-158 linearQuantized:
  * out[tokens][rows] = W[rows][cols] * x[tokens][cols], f32 in, f32 out.

@@ -18,6 +18,10 @@ from ._lib import (  # noqa: F401
     DecoderConfig,
     DeviceBuffer,
     QwhError,
+    TensorEntry,
     library_path,
     load,
+    shard_find,
+    shard_validate,
+    shard_verify_checksum,
 )

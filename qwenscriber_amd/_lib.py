@@ -22,8 +22,9 @@ T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(9)
 T_ATTN_NORM, T_Q_NORM, T_K_NORM, T_FFN_NORM, T_FINAL_NORM = 16, 17, 18, 19, 20
 
 STATUS = {
-    0: "ok", -1: "invalid_argument", -2: "out_of_memory", -3: "unsupported",
-    -7: "shape_mismatch", -8: "invalid_state", -9: "limit_exceeded", -10: "not_found", -64: "device",
+    0: "ok", -1: "invalid_argument", -2: "out_of_memory", -3: "unsupported", -4: "bad_magic",
+    -5: "bad_version", -6: "checksum_mismatch", -7: "shape_mismatch", -8: "invalid_state",
+    -9: "limit_exceeded", -10: "not_found", -11: "truncated", -13: "unsupported_model", -64: "device",
 }
 
 
@@ -49,6 +50,20 @@ class DecoderConfig(ctypes.Structure):
         ("max_positions", ctypes.c_uint32),
         ("eps", ctypes.c_float),
         ("theta", ctypes.c_float),
+    ]
+
+
+class TensorEntry(ctypes.Structure):
+    """qwh_tensor_entry: one `.qw` index entry (container.zig Entry)."""
+    _fields_ = [
+        ("kind", ctypes.c_uint16),
+        ("layer", ctypes.c_uint16),
+        ("format", ctypes.c_uint8),
+        ("rank", ctypes.c_uint8),
+        ("reserved", ctypes.c_uint16),
+        ("dims", ctypes.c_uint32 * 4),
+        ("offset_bytes", ctypes.c_uint64),
+        ("len_bytes", ctypes.c_uint64),
     ]
 
 
@@ -104,6 +119,13 @@ SIGNATURES = {
     "qwh_decoder_step": (_I32, [_P, _P, _P]),
     "qwh_decoder_generate": (_I32, [_P, _P, _U32, _P]),
     "qwh_decoder_logits": (_I32, [_P, _U32, _P, _U32]),
+    "qwh_shard_validate": (_I32, [_P, _U64, ctypes.POINTER(_U32)]),
+    "qwh_shard_verify_checksum": (_I32, [_P, _U64]),
+    "qwh_shard_find": (_I32, [_P, _U64, _U16, _U16, ctypes.POINTER(TensorEntry)]),
+    "qwh_shard_load": (_I32, [_P, _P, _U64, ctypes.POINTER(_U64)]),
+    "qwh_shard_tensor": (_I32, [_P, _U64, _U16, _U16, _PP, ctypes.POINTER(TensorEntry)]),
+    "qwh_shard_matrix": (_I32, [_P, _U64, _U16, _U16, ctypes.POINTER(_U64)]),
+    "qwh_shard_release": (_I32, [_P, _U64]),
 }
 
 _lib = None
@@ -125,6 +147,32 @@ def load():
             fn.argtypes = argtypes
         _lib = lib
     return _lib
+
+
+def _bytes_arg(data) -> tuple:
+    buf = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data, np.uint8)
+    return buf, buf.ctypes.data, buf.size
+
+
+def shard_validate(data) -> tuple:
+    """qwh_shard_validate on host bytes: (status, tensor_count). No device."""
+    buf, ptr, n = _bytes_arg(data)
+    count = ctypes.c_uint32(0)
+    status = load().qwh_shard_validate(ptr, n, ctypes.byref(count))
+    return status, count.value
+
+
+def shard_verify_checksum(data) -> int:
+    buf, ptr, n = _bytes_arg(data)
+    return load().qwh_shard_verify_checksum(ptr, n)
+
+
+def shard_find(data, kind: int, layer: int) -> tuple:
+    """qwh_shard_find: (status, TensorEntry or None)."""
+    buf, ptr, n = _bytes_arg(data)
+    entry = TensorEntry()
+    status = load().qwh_shard_find(ptr, n, kind, layer, ctypes.byref(entry))
+    return status, (entry if status == 0 else None)
 
 
 def _ptr(array: np.ndarray) -> int:
@@ -237,6 +285,27 @@ class Context:
         out = ctypes.c_uint64()
         self._check(self.lib.qwh_matrix_synthetic(self.handle, fmt, rows, cols, seed, stream, scale, ctypes.byref(out)))
         return out.value
+
+    # -- `.qw` shards (container.zig) -------------------------------------
+    def shard_load(self, data) -> int:
+        buf, ptr, n = _bytes_arg(data)
+        out = ctypes.c_uint64()
+        self._check(self.lib.qwh_shard_load(self.handle, ptr, n, ctypes.byref(out)))
+        return out.value
+
+    def shard_tensor(self, shard: int, kind: int, layer: int):
+        dev = ctypes.c_void_p()
+        entry = TensorEntry()
+        self._check(self.lib.qwh_shard_tensor(self.handle, shard, kind, layer, ctypes.byref(dev), ctypes.byref(entry)))
+        return dev.value, entry
+
+    def shard_matrix(self, shard: int, kind: int, layer: int) -> int:
+        out = ctypes.c_uint64()
+        self._check(self.lib.qwh_shard_matrix(self.handle, shard, kind, layer, ctypes.byref(out)))
+        return out.value
+
+    def shard_release(self, shard: int) -> None:
+        self._check(self.lib.qwh_shard_release(self.handle, shard))
 
     def matrix_planes(self, matrix: int):
         s = ctypes.c_void_p()

@@ -74,13 +74,14 @@ int32_t plane_sizes(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, 
     return QWH_OK;
 }
 
+}  // namespace
+
 uint64_t add_matrix(qwh_ctx *ctx, const Matrix &m) {
     const uint64_t handle = ctx->next_handle++;
     ctx->matrices[handle] = m;
     return handle;
 }
 
-}  // namespace
 }  // namespace qwh
 
 using namespace qwh;
@@ -99,6 +100,11 @@ const char *qwh_status_string(int32_t status) {
     case QWH_E_INVALID_STATE: return "invalid_state";
     case QWH_E_LIMIT_EXCEEDED: return "limit_exceeded";
     case QWH_E_NOT_FOUND: return "not_found";
+    case QWH_E_BAD_MAGIC: return "bad_magic";
+    case QWH_E_BAD_VERSION: return "bad_version";
+    case QWH_E_CHECKSUM_MISMATCH: return "checksum_mismatch";
+    case QWH_E_TRUNCATED: return "truncated";
+    case QWH_E_UNSUPPORTED_MODEL: return "unsupported_model";
     case QWH_E_DEVICE: return "device";
     default: return "unknown";
     }
@@ -144,6 +150,7 @@ int32_t qwh_destroy(qwh_ctx *ctx) {
             (void)hipFree(kv.second.data);
         }
     }
+    for (auto &kv : ctx->shards) (void)hipFree(kv.second.payload);
     for (auto &e : ctx->events)
         if (e) (void)hipEventDestroy(e);
     if (ctx->digits.ptr) (void)hipFree(ctx->digits.ptr);

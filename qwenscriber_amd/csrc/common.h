@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/qwhip.h"
 
@@ -40,6 +41,15 @@ struct Matrix {
     uint8_t *scales = nullptr;  // rows * cols/64 f16, little endian, row major
     uint8_t *data = nullptr;    // rows * cols/64 * data_bytes_per_group
     bool owned = false;
+    uint64_t shard = 0;         // the shard whose payload it borrows, or 0
+};
+
+// A `.qw` shard's payload in device memory and its validated index
+// (shard.cpp).
+struct Shard {
+    void *payload = nullptr;
+    uint64_t payload_len = 0;
+    std::vector<qwh_tensor_entry> index;
 };
 
 // A growable device buffer owned by the context (digit planes, attention
@@ -58,6 +68,7 @@ struct qwh_ctx {
     std::string last_error;
     hipEvent_t events[qwh::kMaxEvents] = {};
     std::unordered_map<uint64_t, qwh::Matrix> matrices;
+    std::unordered_map<uint64_t, qwh::Shard> shards;
     uint64_t next_handle = 1;
     qwh::Workspace digits;  // x digit planes for the q4 GEMV
     qwh::Workspace scratch; // attention partials and other per-call scratch
@@ -71,6 +82,8 @@ int32_t fail(qwh_ctx *ctx, int32_t status, const char *fmt, ...);
 int32_t check_hip(qwh_ctx *ctx, hipError_t err, const char *what);
 int32_t ensure_workspace(qwh_ctx *ctx, Workspace &ws, size_t bytes);
 const Matrix *find_matrix(qwh_ctx *ctx, uint64_t handle);
+// Registers a matrix on the context and returns its handle.
+uint64_t add_matrix(qwh_ctx *ctx, const Matrix &m);
 
 // ---- kernels launched by the entry points (defined in the .hip files) ----
 
