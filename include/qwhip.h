@@ -292,6 +292,18 @@ int32_t qwh_decoder_set_matrix(qwh_decoder *decoder, uint32_t kind, uint32_t lay
 /* Binds an f32 norm weight vector (host pointer, copied). */
 int32_t qwh_decoder_set_vector(qwh_decoder *decoder, uint32_t kind, uint32_t layer,
                                const float *values, uint32_t count);
+/* Binds every decoder tensor a loaded `.qw` shard holds (qwh_shard_load):
+ * container.TensorKind 30..43 (container.zig:367-380) at layer 0 (embedding,
+ * final norm, output projection) and layers 1..layers (the decoder's layer
+ * L - 1); other kinds (audio tower, projector) are skipped. Matrices must
+ * be q4 and are copied (the shard may be released afterwards); norm vectors
+ * may be f32, f16 or bf16 and are widened to f32. With
+ * QWH_BIND_OUTPUT_TIED (config.bin flags bit 0, model_config.zig) the
+ * embedding is also bound as the output projection. A model split over
+ * several shards takes one call per shard. `bound` receives the number of
+ * slots filled. */
+#define QWH_BIND_OUTPUT_TIED 1u
+int32_t qwh_decoder_bind_shard(qwh_decoder *decoder, uint64_t shard, uint32_t flags, uint32_t *bound);
 /* Binds every matrix from the synthetic generator: each linear q4 with
  * values f32(N(0,1)) * 0.02, stream ids as the oracle's synthetic model,
  * all norm weights 1.0. */

@@ -126,6 +126,7 @@ SIGNATURES = {
     "qwh_shard_tensor": (_I32, [_P, _U64, _U16, _U16, _PP, ctypes.POINTER(TensorEntry)]),
     "qwh_shard_matrix": (_I32, [_P, _U64, _U16, _U16, ctypes.POINTER(_U64)]),
     "qwh_shard_release": (_I32, [_P, _U64]),
+    "qwh_decoder_bind_shard": (_I32, [_P, _U64, _U32, ctypes.POINTER(_U32)]),
 }
 
 _lib = None
@@ -378,6 +379,11 @@ class Decoder:
     def set_vector(self, kind: int, layer: int, values: np.ndarray) -> None:
         values = np.ascontiguousarray(values, np.float32)
         self._check(self.ctx.lib.qwh_decoder_set_vector(self.handle, kind, layer, _ptr(values), values.size))
+
+    def bind_shard(self, shard: int, output_tied: bool = False) -> int:
+        bound = ctypes.c_uint32(0)
+        self._check(self.ctx.lib.qwh_decoder_bind_shard(self.handle, shard, 1 if output_tied else 0, ctypes.byref(bound)))
+        return bound.value
 
     def init_synthetic(self, seed: int) -> None:
         self._check(self.ctx.lib.qwh_decoder_init_synthetic(self.handle, seed))

@@ -711,6 +711,91 @@ int32_t qwh_decoder_set_vector(qwh_decoder *d, uint32_t kind, uint32_t layer, co
     return QWH_OK;
 }
 
+// f16 bit pattern to f32 on the host (half_float.zig:24-45: exact widening).
+static float host_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    float v;
+    if (exp == 0x1f) {
+        const uint32_t bits = sign | 0x7f800000u | (man << 13);
+        std::memcpy(&v, &bits, 4);
+        return v;
+    }
+    v = exp == 0 ? std::ldexp((float)man, -24) : std::ldexp((float)(man | 0x400u), (int)exp - 25);
+    return sign ? -v : v;
+}
+
+int32_t qwh_decoder_bind_shard(qwh_decoder *d, uint64_t shard, uint32_t flags, uint32_t *bound) {
+    if (!d) return QWH_E_INVALID_ARGUMENT;
+    qwh_ctx *ctx = d->ctx;
+    auto it = ctx->shards.find(shard);
+    if (it == ctx->shards.end()) return fail(ctx, QWH_E_NOT_FOUND, "unknown shard handle %llu", (unsigned long long)shard);
+    // container.TensorKind (container.zig:337-381): the decoder's tensors are
+    // 30..43; layer 0 holds the embedding, final norm and output projection,
+    // layer L >= 1 the decoder's layer L - 1.
+    const std::vector<qwh_tensor_entry> index = it->second.index;
+    uint32_t count = 0;
+    for (const qwh_tensor_entry &e : index) {
+        if (e.kind < 30 || e.kind > 43 || e.layer >= 1024) continue;  // audio tower, projector
+        uint32_t slot = 0xffffffffu, layer = 0;
+        bool vector = false;
+        if (e.layer == 0) {
+            if (e.kind == 30) slot = QWH_T_EMBED;
+            else if (e.kind == 32) slot = QWH_T_LM_HEAD;
+            else if (e.kind == 31) { slot = QWH_T_FINAL_NORM; vector = true; }
+        } else if (e.kind >= 33) {
+            if (e.layer > d->c.layers)
+                return fail(ctx, QWH_E_SHAPE_MISMATCH, "shard holds decoder layer %u of %u", e.layer, d->c.layers);
+            layer = e.layer - 1u;
+            static const uint32_t per_layer[11] = {QWH_T_Q, QWH_T_K, QWH_T_V, QWH_T_O, QWH_T_Q_NORM, QWH_T_K_NORM,
+                                                   QWH_T_ATTN_NORM, QWH_T_FFN_NORM, QWH_T_GATE, QWH_T_UP, QWH_T_DOWN};
+            slot = per_layer[e.kind - 33];
+            vector = slot >= QWH_T_ATTN_NORM;
+        }
+        if (slot == 0xffffffffu) continue;
+        if (vector) {
+            // A norm weight vector: f32, f16 or bf16 values, widened to f32.
+            void *dev = nullptr;
+            QWH_TRY(qwh_shard_tensor(ctx, shard, e.kind, e.layer, &dev, nullptr));
+            const uint64_t n = e.len_bytes / (e.format == 0 ? 4 : 2);
+            std::vector<uint8_t> raw(e.len_bytes);
+            QWH_TRY(check_hip(ctx, hipMemcpy(raw.data(), dev, e.len_bytes, hipMemcpyDeviceToHost), "norm download"));
+            std::vector<float> values(n);
+            for (uint64_t i = 0; i < n; ++i) {
+                if (e.format == 0) {
+                    std::memcpy(&values[i], &raw[4 * i], 4);
+                } else {
+                    const uint16_t h = (uint16_t)(raw[2 * i] | (raw[2 * i + 1] << 8));
+                    if (e.format == 1) {
+                        values[i] = host_f16_to_f32(h);
+                    } else {
+                        const uint32_t bits = (uint32_t)h << 16;
+                        std::memcpy(&values[i], &bits, 4);
+                    }
+                }
+            }
+            QWH_TRY(qwh_decoder_set_vector(d, slot, layer, values.data(), (uint32_t)n));
+            ++count;
+        } else {
+            uint64_t m = 0;
+            QWH_TRY(qwh_shard_matrix(ctx, shard, e.kind, e.layer, &m));
+            int32_t st = qwh_decoder_set_matrix(d, slot, layer, m);
+            if (st == QWH_OK && slot == QWH_T_EMBED && (flags & QWH_BIND_OUTPUT_TIED)) {
+                st = qwh_decoder_set_matrix(d, QWH_T_LM_HEAD, 0, m);
+                if (st == QWH_OK) ++count;
+            }
+            // The decoder keeps copies: the borrowed handle goes at once.
+            const int32_t rel = qwh_matrix_release(ctx, m);
+            QWH_TRY(st);
+            QWH_TRY(rel);
+            ++count;
+        }
+    }
+    QWH_TRY(check_hip(ctx, hipStreamSynchronize(ctx->stream), "bind shard"));
+    if (bound) *bound = count;
+    return QWH_OK;
+}
+
 int32_t qwh_decoder_init_synthetic(qwh_decoder *d, uint32_t seed) {
     if (!d) return QWH_E_INVALID_ARGUMENT;
     const qwh_decoder_config &c = d->c;
