@@ -334,6 +334,59 @@ int32_t qwh_decoder_generate(qwh_decoder *decoder, const uint32_t *tokens, uint3
 /* Copies sequence `seq`'s last logits (vocab f32) to the host. */
 int32_t qwh_decoder_logits(qwh_decoder *decoder, uint32_t seq, float *out, uint32_t count);
 
+/* ---------------------------------------------------------------------- */
+/* config.bin (model_config.zig)                                           */
+/* ---------------------------------------------------------------------- */
+
+/* model_config.Config (model_config.zig:110-190), the 160-byte on-disk
+ * layout, little endian. */
+typedef struct qwh_model_config {
+    char magic[8]; /* "QWCFG001" */
+    uint32_t format_version;
+    uint32_t architecture; /* 1 = qwen3_asr */
+    uint32_t audio_d_model, audio_layers, audio_attention_heads, audio_ffn_dim;
+    uint32_t audio_downsample_hidden_size, audio_n_window, audio_n_window_infer;
+    uint32_t audio_max_position_steps, audio_output_dim, mel_bins;
+    float audio_layer_norm_eps;
+    uint32_t text_hidden_size, text_layers, text_attention_heads, text_key_value_heads;
+    uint32_t text_head_dim, text_ffn_dim, vocab_size;
+    float text_rms_norm_eps, rope_theta;
+    uint32_t max_positions, max_decode_tokens;
+    uint32_t token_audio_start, token_audio_end, token_audio_pad, token_im_start, token_im_end;
+    uint32_t token_endoftext, token_asr_text, token_eos_primary, token_eos_secondary, token_pad;
+    uint32_t flags;       /* bit 0: output projection tied to the embedding */
+    uint32_t reserved[3]; /* zero */
+} qwh_model_config;
+
+#define QWH_CONFIG_OUTPUT_TIED 1u
+/* Which check rejected a configuration: model_config.Error in its declared
+ * order (model_config.zig:89-106). */
+#define QWH_CONFIG_OK 0u
+#define QWH_CONFIG_BAD_MAGIC 1u
+#define QWH_CONFIG_BAD_VERSION 2u
+#define QWH_CONFIG_TRUNCATED 3u
+#define QWH_CONFIG_RESERVED_NOT_EMPTY 4u
+#define QWH_CONFIG_UNKNOWN_ARCHITECTURE 5u
+#define QWH_CONFIG_INVALID_DIMENSION 6u
+#define QWH_CONFIG_INVALID_HEAD_GEOMETRY 7u
+#define QWH_CONFIG_INVALID_MEL_GEOMETRY 8u
+#define QWH_CONFIG_INVALID_TOKEN_ID 9u
+#define QWH_CONFIG_INVALID_EPSILON 10u
+#define QWH_CONFIG_INVALID_ROPE_THETA 11u
+#define QWH_CONFIG_INVALID_CHUNK_GEOMETRY 12u
+#define QWH_CONFIG_MISALIGNED 13u
+
+/* model_config.parse (model_config.zig:354-360) + Config.validate
+ * (:260-327) on the host, no device: exactly 160 bytes, 4-byte aligned, then
+ * every check in the reference's order. Status as the reference ABI maps
+ * the errors (QWH_E_TRUNCATED, QWH_E_BAD_MAGIC, QWH_E_BAD_VERSION, else
+ * QWH_E_INVALID_ARGUMENT); `reason` (optional) receives the QWH_CONFIG_*
+ * value; `out` (optional) the configuration when it is valid. */
+int32_t qwh_config_parse(const void *bytes, uint64_t len, qwh_model_config *out, uint32_t *reason);
+/* The decoder dimensions of a configuration (text_* fields, vocab_size,
+ * max_positions, rope_theta), for qwh_decoder_create. */
+int32_t qwh_config_decoder(const qwh_model_config *model, qwh_decoder_config *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,8 +17,11 @@ from ._lib import (  # noqa: F401
     Decoder,
     DecoderConfig,
     DeviceBuffer,
+    ModelConfig,
     QwhError,
     TensorEntry,
+    config_decoder,
+    config_parse,
     library_path,
     load,
     shard_find,

@@ -67,6 +67,25 @@ class TensorEntry(ctypes.Structure):
     ]
 
 
+class ModelConfig(ctypes.Structure):
+    """qwh_model_config: config.bin's 160-byte model_config.Config."""
+    _fields_ = [("magic", ctypes.c_char * 8), ("format_version", ctypes.c_uint32), ("architecture", ctypes.c_uint32)] + [
+        (name, ctypes.c_uint32) for name in (
+            "audio_d_model", "audio_layers", "audio_attention_heads", "audio_ffn_dim",
+            "audio_downsample_hidden_size", "audio_n_window", "audio_n_window_infer",
+            "audio_max_position_steps", "audio_output_dim", "mel_bins")
+    ] + [("audio_layer_norm_eps", ctypes.c_float)] + [
+        (name, ctypes.c_uint32) for name in (
+            "text_hidden_size", "text_layers", "text_attention_heads", "text_key_value_heads",
+            "text_head_dim", "text_ffn_dim", "vocab_size")
+    ] + [("text_rms_norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)] + [
+        (name, ctypes.c_uint32) for name in (
+            "max_positions", "max_decode_tokens", "token_audio_start", "token_audio_end", "token_audio_pad",
+            "token_im_start", "token_im_end", "token_endoftext", "token_asr_text", "token_eos_primary",
+            "token_eos_secondary", "token_pad", "flags")
+    ] + [("reserved", ctypes.c_uint32 * 3)]
+
+
 _P = ctypes.c_void_p
 _PP = ctypes.POINTER(ctypes.c_void_p)
 _U16 = ctypes.c_uint16
@@ -127,6 +146,8 @@ SIGNATURES = {
     "qwh_shard_matrix": (_I32, [_P, _U64, _U16, _U16, ctypes.POINTER(_U64)]),
     "qwh_shard_release": (_I32, [_P, _U64]),
     "qwh_decoder_bind_shard": (_I32, [_P, _U64, _U32, ctypes.POINTER(_U32)]),
+    "qwh_config_parse": (_I32, [_P, _U64, ctypes.POINTER(ModelConfig), ctypes.POINTER(_U32)]),
+    "qwh_config_decoder": (_I32, [ctypes.POINTER(ModelConfig), ctypes.POINTER(DecoderConfig)]),
 }
 
 _lib = None
@@ -153,6 +174,30 @@ def load():
 def _bytes_arg(data) -> tuple:
     buf = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data, np.uint8)
     return buf, buf.ctypes.data, buf.size
+
+
+def config_parse(data, offset: int = 0) -> tuple:
+    """qwh_config_parse: (status, reason, ModelConfig or None). `offset`
+    shifts the bytes inside a 16-byte aligned buffer (alignment checks)."""
+    raw = bytes(data)
+    buf = np.zeros(len(raw) + 16, np.uint8)
+    base = (-buf.ctypes.data) % 16 + offset
+    if base + len(raw) > buf.size:
+        base -= 16
+    buf[base:base + len(raw)] = np.frombuffer(raw, np.uint8)
+    out = ModelConfig()
+    reason = ctypes.c_uint32(0)
+    status = load().qwh_config_parse(buf.ctypes.data + base, len(raw), ctypes.byref(out), ctypes.byref(reason))
+    return status, reason.value, (out if status == 0 else None)
+
+
+def config_decoder(model: "ModelConfig") -> dict:
+    """Decoder(**config) keyword arguments of a parsed configuration."""
+    out = DecoderConfig()
+    status = load().qwh_config_decoder(ctypes.byref(model), ctypes.byref(out))
+    if status != 0:
+        raise QwhError(status, "qwh_config_decoder")
+    return {name: getattr(out, name) for name, _ in DecoderConfig._fields_}
 
 
 def shard_validate(data) -> tuple:

@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 import qwenscriber_amd as qa
+from oracle import model_config as mc
 from oracle import shard as sh
 
 pytestmark = pytest.mark.gpu
@@ -90,18 +91,36 @@ def reference_decoder(ctx, nv, tied=False):
     return d
 
 
+def config_bin(tied: bool) -> bytes:
+    """A config.bin for the TINY decoder (model_config.zig layout; the audio
+    fields are the 0.6B model's, with the projector width the hidden size)."""
+    c = TINY
+    tokens = {k: 990 + i for i, k in enumerate(mc.TOKENS)}
+    return mc.pack(dict(mc.CONFIG_0P6B, text_hidden_size=c["hidden"], audio_output_dim=c["hidden"],
+                        text_layers=c["layers"], text_attention_heads=c["heads"],
+                        text_key_value_heads=c["kv_heads"], text_head_dim=c["head_dim"], text_ffn_dim=c["ffn"],
+                        vocab_size=c["vocab"], max_positions=c["max_positions"], flags=1 if tied else 0,
+                        **tokens))
+
+
 @pytest.mark.parametrize("tied", [False, True])
 def test_decoder_bound_from_shards(ctx, tied):
     blobs, nv = build_shards(ctx, with_output=not tied)
     for blob in blobs:
         assert sh.parse(blob)[0] == sh.OK
     ref = reference_decoder(ctx, nv, tied)
-    dec = qa.Decoder(ctx, batch=2, **TINY)
+    # The model as a loader sees it: config.bin, then the shards.
+    status, reason, model = qa.config_parse(config_bin(tied))
+    assert (status, reason) == (0, 0)
+    dims = qa.config_decoder(model)
+    assert {k: dims[k] for k in TINY if k not in ("eps", "theta")} == {k: v for k, v in TINY.items()
+                                                                     if k not in ("eps", "theta")}
+    dec = qa.Decoder(ctx, batch=2, **dims)
     try:
         counts = []
         for blob in blobs:
             shard = ctx.shard_load(blob)
-            counts.append(dec.bind_shard(shard, output_tied=tied))
+            counts.append(dec.bind_shard(shard, output_tied=bool(model.flags & 1)))
             ctx.shard_release(shard)   # the decoder holds copies
         assert counts == [3 + 11, 11]   # embed, final norm, output (or tied), and 11 per layer
         for d in (ref, dec):
