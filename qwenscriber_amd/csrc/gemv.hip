@@ -730,10 +730,12 @@ __device__ __forceinline__ void block_encode5(const GemvQ5Args &a, uint32_t toke
     __syncthreads();
 }
 
-// The activation operands of chunk c from LDS.
+// The activation operands of chunk c from LDS: digit planes, -16 times each
+// plane's digit sum (the bias term, the start of that plane's dot chain),
+// and the chunk multiplier.
 struct Act5 {
     uint32_t d[24];
-    int sum[3];
+    int bias[3];
     float mult;
 };
 
@@ -748,32 +750,32 @@ __device__ __forceinline__ void load_act5(const Act5Lds &lds, uint32_t c, Act5 &
         x.d[j * 4 + 3] = w.w;
     }
     const int4 sv = *reinterpret_cast<const int4 *>(&lds.sums[c * 4]);
-    x.sum[0] = sv.x;
-    x.sum[1] = sv.y;
-    x.sum[2] = sv.z;
+    x.bias[0] = -16 * sv.x;
+    x.bias[1] = -16 * sv.y;
+    x.bias[2] = -16 * sv.z;
     x.mult = lds.mult[c];
 }
 
 // sum (u - 16) x_int of one slice, in f32 (the integer plane terms exact).
 __device__ __forceinline__ float q5_slice_dot(const Slice5 &sl, const Act5 &x) {
     const uint32_t w[4] = {sl.lo0.x, sl.lo0.y, sl.lo1.x, sl.lo1.y};
-    int p0 = 0, p1 = 0, p2 = 0;
+    // Fifth bits of the even and of the odd columns, each byte's four at bits
+    // 0, 2, 4, 6 (so one bit-field extract per byte below).
+    const uint32_t fifths[2] = {sl.hi & 0x55555555u, (sl.hi >> 1) & 0x55555555u};
+    int p0 = x.bias[0], p1 = x.bias[1], p2 = x.bias[2];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int par = 0; par < 2; ++par) {
             const uint32_t nib = (par ? w[q] >> 4 : w[q]) & 0x0f0f0f0fu;
-            const uint32_t fifth = (((sl.hi >> (8 * q + par)) & 0x55u) * 0x00410410u) & 0x10101010u;
-            const int um = (int)(nib | fifth);
+            const uint32_t bits = __builtin_amdgcn_ubfe(fifths[par], 8 * q, 8);
+            const int um = (int)(((bits * 0x00410410u) & 0x10101010u) | nib);
             const int m = 2 * q + par;
             p0 = __builtin_amdgcn_sdot4(um, (int)x.d[m], p0, false);
             p1 = __builtin_amdgcn_sdot4(um, (int)x.d[8 + m], p1, false);
             p2 = __builtin_amdgcn_sdot4(um, (int)x.d[16 + m], p2, false);
         }
     }
-    p0 -= 16 * x.sum[0];
-    p1 -= 16 * x.sum[1];
-    p2 -= 16 * x.sum[2];
     return ((float)p2 * 65536.0f + (float)p1 * 256.0f) + (float)p0;
 }
 
