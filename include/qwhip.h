@@ -240,6 +240,64 @@ int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_
                          uint8_t *k_codes_dev, uint8_t *v_scales_dev, uint8_t *v_codes_dev);
 
 /* ---------------------------------------------------------------------- */
+/* Audio tower and projector (model.zig:646-735)                           */
+/* ---------------------------------------------------------------------- */
+
+/* kernels.zig:259-271 layerNormInto (math.zig:99-116 per row): out = (x -
+ * mean) / sqrt(variance + eps) * weight + bias over `tokens` rows of `width`
+ * floats. out may equal x (kernels.zig:242-255 layerNorm in place). */
+int32_t qwh_layer_norm(qwh_ctx *ctx, float *out_dev, const float *x_dev, const float *weight_dev,
+                       const float *bias_dev, uint32_t width, uint32_t tokens, float eps);
+
+/* kernels.zig:210-218 addBias: x[t][r] += bias[r] for `tokens` rows of `rows`. */
+int32_t qwh_add_bias(qwh_ctx *ctx, float *x_dev, const float *bias_dev, uint32_t rows, uint32_t tokens);
+
+/* math.zig:63-66 gelu over `count` values in place (model.zig:719, :868). */
+int32_t qwh_gelu(qwh_ctx *ctx, float *x_dev, uint64_t count);
+
+/* kernels.zig:429-484 audioAttentionWindow: non-causal attention of the steps
+ * [window_start, window_start + window_length) over the same steps, per head;
+ * row r of q / k / v / out starts at ptr + r * stride (floats). The scores
+ * scratch the reference takes is internal. Built for head_dim 32, 64 and
+ * 128; strides multiples of 4 and buffers 16-byte aligned. */
+int32_t qwh_audio_attention_window(qwh_ctx *ctx, float *out_dev, uint32_t out_stride, const float *q_dev,
+                                   uint32_t q_stride, const float *k_dev, uint32_t k_stride, const float *v_dev,
+                                   uint32_t v_stride, uint32_t window_start, uint32_t window_length,
+                                   uint32_t heads, uint32_t head_dim);
+
+/* model.zig:792-822 runWindowedAttention: every window of `window_steps`
+ * steps from step 0 (the last one ragged) in one launch; q / k / v share one
+ * row stride, as the reference's packed q | k | v buffer does. */
+int32_t qwh_audio_attention(qwh_ctx *ctx, float *out_dev, uint32_t out_stride, const float *q_dev,
+                            const float *k_dev, const float *v_dev, uint32_t qkv_stride, uint32_t steps,
+                            uint32_t window_steps, uint32_t heads, uint32_t head_dim);
+
+/* One audio tower layer's weights (model.zig AudioLayer): matrix handles of
+ * the context, and device f32 vectors. */
+typedef struct {
+    uint64_t q, k, v, o;       /* d_model x d_model */
+    uint64_t ffn_in;           /* ffn_dim x d_model */
+    uint64_t ffn_out;          /* d_model x ffn_dim */
+    const float *q_bias, *k_bias, *v_bias, *o_bias, *ffn_in_bias, *ffn_out_bias;
+    const float *attention_norm_weight, *attention_norm_bias;
+    const float *final_norm_weight, *final_norm_bias;
+} qwh_audio_layer_weights;
+
+/* model.zig:656-693, one iteration of runAudioTower's layer loop over the
+ * residual stream encoder[steps][d_model] (updated in place): LayerNorm,
+ * q / k / v + bias, windowed attention, o + bias + residual, LayerNorm,
+ * ffn_in + bias, GELU, ffn_out + bias + residual. Scratch is the context's. */
+int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *weights, float *encoder_dev,
+                        uint32_t steps, uint32_t d_model, uint32_t heads, uint32_t ffn_dim,
+                        uint32_t window_steps, float eps);
+
+/* model.zig:707-735 runProjector: out[steps][hidden] = W_out gelu(W_in x +
+ * b_in) + b_out, W_in d_model x d_model, W_out hidden x d_model. */
+int32_t qwh_audio_projector(qwh_ctx *ctx, uint64_t in_matrix, const float *in_bias_dev,
+                            uint64_t out_matrix, const float *out_bias_dev, const float *encoder_dev,
+                            uint32_t steps, float *out_dev);
+
+/* ---------------------------------------------------------------------- */
 /* Decoder step (decoder.zig:133-339)                                      */
 /* ---------------------------------------------------------------------- */
 

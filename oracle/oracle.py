@@ -106,6 +106,12 @@ _SIGNATURES = {
     "qwref_decoder_cache_hash": (_U64, [_P, _U32]),
     "qwref_synthetic_start_token": (_U32, [_U32, _U32, _U32]),
     "qwref_set_threads": (None, [_I32]),
+    "qwref_erf": (ctypes.c_float, [ctypes.c_float]),
+    "qwref_gelu": (ctypes.c_float, [ctypes.c_float]),
+    "qwref_gelu_in_place": (None, [_P, _U64]),
+    "qwref_add_bias": (_I32, [_P, _P, _U32, _U32]),
+    "qwref_layer_norm": (None, [_P, _P, _P, _U32, _U32, ctypes.c_float]),
+    "qwref_audio_attention_window": (_I32, [_P, _U32, _P, _U32, _P, _U32, _P, _U32, _U32, _U32, _U32, _U32]),
 }
 
 
@@ -345,3 +351,107 @@ class Decoder:
 
 def start_token(seed: int, seq: int, vocab: int) -> int:
     return lib().qwref_synthetic_start_token(seed, seq, vocab)
+
+
+# --------------------------------------------------------------------------
+# Audio tower (model.zig:646-735): the layer and projector are composed here
+# from the C restatements above, call for call in the reference's order.
+
+
+def erf(x: float) -> float:
+    return lib().qwref_erf(float(x))
+
+
+def gelu(x: float) -> float:
+    return lib().qwref_gelu(float(x))
+
+
+def gelu_array(x: np.ndarray) -> np.ndarray:
+    out = np.array(x, np.float32)
+    lib().qwref_gelu_in_place(_ptr(out), out.size)
+    return out
+
+
+def add_bias(x: np.ndarray, bias: np.ndarray, rows: int, tokens: int) -> np.ndarray:
+    """kernels.zig:210-218 addBias, on a copy."""
+    out = np.array(x, np.float32).reshape(-1)
+    bias = np.ascontiguousarray(bias, np.float32)
+    if out.size != rows * tokens or bias.size != rows:
+        raise ValueError("add_bias shape mismatch")
+    lib().qwref_add_bias(_ptr(out), _ptr(bias), rows, tokens)
+    return out
+
+
+def layer_norm(x: np.ndarray, weight: np.ndarray, bias: np.ndarray, width: int, eps: float) -> np.ndarray:
+    """kernels.zig:259-271 layerNormInto (math.zig:99-116 per row), on a copy."""
+    out = np.array(x, np.float32).reshape(-1)
+    weight = np.ascontiguousarray(weight, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    lib().qwref_layer_norm(_ptr(out), _ptr(weight), _ptr(bias), width, out.size // width, float(eps))
+    return out
+
+
+def audio_attention_window(out, q, k, v, strides, window_start, window_length, heads, head_dim) -> None:
+    """kernels.zig:429-484 audioAttentionWindow into `out` (f32, modified in place)."""
+    arrays = [np.ascontiguousarray(a, np.float32) for a in (q, k, v)]
+    assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+    so, sq, sk, sv = strides
+    status = lib().qwref_audio_attention_window(_ptr(out), so, _ptr(arrays[0]), sq, _ptr(arrays[1]), sk,
+                                                _ptr(arrays[2]), sv, window_start, window_length, heads, head_dim)
+    if status != 0:
+        raise ValueError(f"audio_attention_window status {status}")
+
+
+def audio_attention(q, k, v, steps, window_steps, heads, head_dim) -> np.ndarray:
+    """model.zig:792-822 runWindowedAttention over separate [steps][heads*head_dim]
+    q, k, v rows: windows of window_steps from step 0, the last one ragged."""
+    width = heads * head_dim
+    out = np.zeros(steps * width, np.float32)
+    start = 0
+    while start < steps:
+        length = min(window_steps, steps - start)
+        audio_attention_window(out, q, k, v, (width, width, width, width), start, length, heads, head_dim)
+        start += length
+    return out
+
+
+def audio_layer(encoder: np.ndarray, layer: dict, steps: int, d_model: int, heads: int, ffn_dim: int,
+                window_steps: int, eps: float) -> np.ndarray:
+    """One audio tower layer (model.zig:656-693 runAudioTower loop body).
+
+    `layer` holds (fmt, scales, data) triples under q, k, v, o, ffn_in, ffn_out
+    and f32 vectors under q_bias ... ffn_out_bias, attention_norm_weight / _bias
+    and final_norm_weight / _bias. Returns the new residual stream."""
+    enc = np.array(encoder, np.float32).reshape(-1)
+
+    def apply(name, x, rows, cols):
+        fmt, scales, data = layer[name]
+        return linear_quantized(fmt, scales, data, rows, cols, x, steps).reshape(-1)
+
+    normed = layer_norm(enc, layer["attention_norm_weight"], layer["attention_norm_bias"], d_model, eps)
+    # model.zig:765-786 projectQkv: each projection, then its bias.
+    q = add_bias(apply("q", normed, d_model, d_model), layer["q_bias"], d_model, steps)
+    k = add_bias(apply("k", normed, d_model, d_model), layer["k_bias"], d_model, steps)
+    v = add_bias(apply("v", normed, d_model, d_model), layer["v_bias"], d_model, steps)
+    block = audio_attention(q, k, v, steps, window_steps, heads, d_model // heads)
+    # model.zig:824-848 projectAttentionOutput, then :669 addInPlace.
+    block = add_bias(apply("o", block, d_model, d_model), layer["o_bias"], d_model, steps)
+    lib().qwref_add_in_place(_ptr(enc), _ptr(block), enc.size)
+    normed = layer_norm(enc, layer["final_norm_weight"], layer["final_norm_bias"], d_model, eps)
+    # model.zig:852-872 activateFfn, then :692 addInPlace.
+    wide = gelu_array(add_bias(apply("ffn_in", normed, ffn_dim, d_model), layer["ffn_in_bias"], ffn_dim, steps))
+    block = add_bias(apply("ffn_out", wide, d_model, ffn_dim), layer["ffn_out_bias"], d_model, steps)
+    lib().qwref_add_in_place(_ptr(enc), _ptr(block), enc.size)
+    return enc
+
+
+def audio_projector(encoder: np.ndarray, proj_in, in_bias, proj_out, out_bias, steps: int, d_model: int,
+                    hidden: int) -> np.ndarray:
+    """model.zig:707-735 runProjector: linear, bias, GELU, linear, bias.
+    proj_in / proj_out are (fmt, scales, data); proj_in is [d_model x d_model]."""
+    fmt, scales, data = proj_in
+    mid = linear_quantized(fmt, scales, data, d_model, d_model, np.asarray(encoder, np.float32), steps)
+    mid = gelu_array(add_bias(mid, in_bias, d_model, steps))
+    fmt, scales, data = proj_out
+    out = linear_quantized(fmt, scales, data, hidden, d_model, mid, steps)
+    return add_bias(out, out_bias, hidden, steps)

@@ -573,6 +573,104 @@ uint32_t qwref_argmax(const float *logits, uint32_t count) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Audio tower glue                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* math.zig:46-60 `erf`: the Chebyshev fit of erfc from Numerical Recipes
+ * (`erfcc`, fractional error below 1.2e-7), in f32, with expf standing in for
+ * the reference's exp (last-ulp parity unpinned). */
+float qwref_erf(float x) {
+    float sign = x < 0.0f ? -1.0f : 1.0f;
+    float magnitude = fabsf(x);
+    float t = 1.0f / (1.0f + 0.5f * magnitude);
+    float poly = -0.82215223f + t * 0.17087277f;
+    poly = 1.48851587f + t * poly;
+    poly = -1.13520398f + t * poly;
+    poly = 0.27886807f + t * poly;
+    poly = -0.18628806f + t * poly;
+    poly = 0.09678418f + t * poly;
+    poly = 0.37409196f + t * poly;
+    poly = 1.00002368f + t * poly;
+    float tau = t * expf(-magnitude * magnitude - 1.26551223f + t * poly);
+    return sign * (1.0f - tau);
+}
+
+/* math.zig:63-66 `gelu` (exact, error-function form). */
+float qwref_gelu(float x) {
+    const float inverse_sqrt_two = 0.70710678f;
+    return 0.5f * x * (1.0f + qwref_erf(x * inverse_sqrt_two));
+}
+
+/* model.zig:719 / :868: GELU applied over a whole projection output. */
+void qwref_gelu_in_place(float *x, uint64_t len) {
+    for (uint64_t i = 0; i < len; ++i) x[i] = qwref_gelu(x[i]);
+}
+
+/* kernels.zig:210-218 `addBias`: x[t][r] += bias[r]. */
+int32_t qwref_add_bias(float *x, const float *bias, uint32_t rows, uint32_t tokens) {
+    for (uint32_t t = 0; t < tokens; ++t) {
+        float *row = x + (size_t)t * rows;
+        for (uint32_t r = 0; r < rows; ++r) row[r] += bias[r];
+    }
+    return 0;
+}
+
+/* math.zig:99-116 `layerNormInPlace`, per token as kernels.zig:242-255
+ * `layerNorm`: mean, centred variance, 1/sqrt(variance + eps), then
+ * (x - mean) * inverse_std * weight + bias, each in f32 and in that order. */
+void qwref_layer_norm(float *x, const float *weight, const float *bias, uint32_t width, uint32_t tokens,
+                      float eps) {
+    for (uint32_t t = 0; t < tokens; ++t) {
+        float *row = x + (size_t)t * width;
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < width; ++i) sum += row[i];
+        float mean = sum / (float)width;
+        float sum_squares = 0.0f;
+        for (uint32_t i = 0; i < width; ++i) {
+            float centered = row[i] - mean;
+            sum_squares += centered * centered;
+        }
+        float variance = sum_squares / (float)width;
+        float inverse_std = 1.0f / sqrtf(variance + eps);
+        for (uint32_t i = 0; i < width; ++i) row[i] = (row[i] - mean) * inverse_std * weight[i] + bias[i];
+    }
+}
+
+/* kernels.zig:429-484 `audioAttentionWindow`: non-causal attention of every
+ * query in [window_start, window_start + window_length) over the keys of the
+ * same range, per head; rows `stride` floats apart. Scores are dotF32 times
+ * 1/sqrt(head_dim), softmaxInPlace, then out_row = sum_k weight_k * v_k with
+ * the reference's 4-lane vector accumulate (lane-wise, so element order). */
+int32_t qwref_audio_attention_window(float *out, uint32_t out_stride, const float *q, uint32_t q_stride,
+                                     const float *k, uint32_t k_stride, const float *v, uint32_t v_stride,
+                                     uint32_t window_start, uint32_t window_length, uint32_t heads,
+                                     uint32_t head_dim) {
+    if (window_length == 0) return -7;
+    float *scores = (float *)malloc(sizeof(float) * window_length);
+    if (!scores) return -2;
+    const float scaling = 1.0f / sqrtf((float)head_dim);
+    for (uint32_t head = 0; head < heads; ++head) {
+        for (uint32_t query = 0; query < window_length; ++query) {
+            const float *query_row = q + (size_t)(window_start + query) * q_stride + (size_t)head * head_dim;
+            for (uint32_t key = 0; key < window_length; ++key) {
+                const float *key_row = k + (size_t)(window_start + key) * k_stride + (size_t)head * head_dim;
+                scores[key] = qwref_dot_f32(query_row, key_row, head_dim) * scaling;
+            }
+            qwref_softmax_in_place(scores, window_length);
+            float *out_row = out + (size_t)(window_start + query) * out_stride + (size_t)head * head_dim;
+            for (uint32_t i = 0; i < head_dim; ++i) out_row[i] = 0.0f;
+            for (uint32_t key = 0; key < window_length; ++key) {
+                const float *value_row = v + (size_t)(window_start + key) * v_stride + (size_t)head * head_dim;
+                const float weight = scores[key];
+                for (uint32_t i = 0; i < head_dim; ++i) out_row[i] = out_row[i] + value_row[i] * weight;
+            }
+        }
+    }
+    free(scores);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Synthetic inputs. Not reference code: the seeded-input specification the  */
 /* oracle and the HIP backend both implement (independently) so that large    */
 /* configurations can be generated on either side and compared bit for bit.  */

@@ -23,6 +23,11 @@
  *   attention (q8)   kernels.zig:769-836 (q8 vs f32 within 0.05), closed forms
  *                    (one-hot query on identical keys = mean of V), f64 brute force.
  *   glue             math.zig:174-214 known answers, RoPE norm invariance.
+ *   audio glue       math.zig:134-171 erf / gelu known answers (C library erf
+ *                    at double precision), kernels.zig:1162-1171 addBias values,
+ *                    f64 numpy layer norm and windowed attention brute force,
+ *                    kernels.zig:1043-1078 windowed-attention known answers.
+ *   audio layer      composition of the pinned parts (no reference-held vectors).
  *   decoder step     composition of the pinned parts; no reference-held vectors
  *                    exist for random weights (parity unpinned end to end).
  *   transcendentals  expf/powf/sinf/cosf are glibc's, not Zig compiler_rt's:
@@ -110,6 +115,18 @@ int32_t qwref_decode_attention_step_q8(float *out, const float *query, const uin
                                        const uint8_t *v_codes, uint32_t cached, uint32_t heads,
                                        uint32_t kv_heads, uint32_t head_dim);
 uint32_t qwref_argmax(const float *logits, uint32_t count);
+
+/* Audio tower glue (kernels.zig:210-271, :429-484; math.zig:46-66, :99-116). */
+float qwref_erf(float x);
+float qwref_gelu(float x);
+void qwref_gelu_in_place(float *x, uint64_t len);
+int32_t qwref_add_bias(float *x, const float *bias, uint32_t rows, uint32_t tokens);
+void qwref_layer_norm(float *x, const float *weight, const float *bias, uint32_t width, uint32_t tokens,
+                      float eps);
+int32_t qwref_audio_attention_window(float *out, uint32_t out_stride, const float *q, uint32_t q_stride,
+                                     const float *k, uint32_t k_stride, const float *v, uint32_t v_stride,
+                                     uint32_t window_start, uint32_t window_length, uint32_t heads,
+                                     uint32_t head_dim);
 
 /* ---- synthetic inputs (test-input specification, not reference code) --- */
 uint32_t qwref_mulberry32_at(uint32_t seed, uint64_t draw);

@@ -21,6 +21,16 @@ DATA_BYTES = {FORMAT_Q4: 32, FORMAT_Q5: 40, FORMAT_Q8: 64}
 T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(9)
 T_ATTN_NORM, T_Q_NORM, T_K_NORM, T_FFN_NORM, T_FINAL_NORM = 16, 17, 18, 19, 20
 
+class AudioLayerWeights(ctypes.Structure):
+    """qwh_audio_layer_weights (model.zig AudioLayer): matrix handles and
+    device addresses of f32 vectors."""
+
+    MATRICES = ("q", "k", "v", "o", "ffn_in", "ffn_out")
+    VECTORS = ("q_bias", "k_bias", "v_bias", "o_bias", "ffn_in_bias", "ffn_out_bias", "attention_norm_weight",
+               "attention_norm_bias", "final_norm_weight", "final_norm_bias")
+    _fields_ = [(name, ctypes.c_uint64) for name in MATRICES] + [(name, ctypes.c_void_p) for name in VECTORS]
+
+
 STATUS = {
     0: "ok", -1: "invalid_argument", -2: "out_of_memory", -3: "unsupported", -4: "bad_magic",
     -5: "bad_version", -6: "checksum_mismatch", -7: "shape_mismatch", -8: "invalid_state",
@@ -124,6 +134,13 @@ SIGNATURES = {
     "qwh_synth_normal": (_I32, [_P, _U32, _U32, _U64, _F, _P]),
     "qwh_decode_attention_q8": (_I32, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U64, _U64]),
     "qwh_kv_append_q8": (_I32, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "qwh_layer_norm": (_I32, [_P, _P, _P, _P, _P, _U32, _U32, _F]),
+    "qwh_add_bias": (_I32, [_P, _P, _P, _U32, _U32]),
+    "qwh_gelu": (_I32, [_P, _P, _U64]),
+    "qwh_audio_attention_window": (_I32, [_P, _P, _U32, _P, _U32, _P, _U32, _P, _U32, _U32, _U32, _U32, _U32]),
+    "qwh_audio_attention": (_I32, [_P, _P, _U32, _P, _P, _P, _U32, _U32, _U32, _U32, _U32]),
+    "qwh_audio_layer": (_I32, [_P, ctypes.POINTER(AudioLayerWeights), _P, _U32, _U32, _U32, _U32, _U32, _F]),
+    "qwh_audio_projector": (_I32, [_P, _U64, _P, _U64, _P, _P, _U32, _P]),
     "qwh_decoder_create": (_I32, [_P, ctypes.POINTER(DecoderConfig), _U32, _PP]),
     "qwh_decoder_destroy": (_I32, [_P]),
     "qwh_decoder_set_matrix": (_I32, [_P, _U32, _U32, _U64]),
@@ -379,6 +396,44 @@ class Context:
 
     def linear_bf16(self, matrix: int, x_dev: int, cols: int, tokens: int, out_dev: int) -> None:
         self._check(self.lib.qwh_linear_bf16(self.handle, matrix, x_dev, cols, tokens, out_dev))
+
+    # -- audio tower (model.zig:646-735) -----------------------------------
+    def layer_norm(self, out_dev: int, x_dev: int, weight_dev: int, bias_dev: int, width: int, tokens: int,
+                   eps: float) -> None:
+        """kernels.zig layerNormInto (out may equal x: layerNorm in place)."""
+        self._check(self.lib.qwh_layer_norm(self.handle, out_dev, x_dev, weight_dev, bias_dev, width, tokens, eps))
+
+    def add_bias(self, x_dev: int, bias_dev: int, rows: int, tokens: int) -> None:
+        """kernels.zig addBias."""
+        self._check(self.lib.qwh_add_bias(self.handle, x_dev, bias_dev, rows, tokens))
+
+    def gelu(self, x_dev: int, count: int) -> None:
+        """math.zig gelu over count values in place."""
+        self._check(self.lib.qwh_gelu(self.handle, x_dev, count))
+
+    def audio_attention_window(self, out_dev, out_stride, q_dev, q_stride, k_dev, k_stride, v_dev, v_stride,
+                               window_start, window_length, heads, head_dim) -> None:
+        """kernels.zig audioAttentionWindow."""
+        self._check(self.lib.qwh_audio_attention_window(self.handle, out_dev, out_stride, q_dev, q_stride, k_dev,
+                                                        k_stride, v_dev, v_stride, window_start, window_length,
+                                                        heads, head_dim))
+
+    def audio_attention(self, out_dev, out_stride, q_dev, k_dev, v_dev, qkv_stride, steps, window_steps, heads,
+                        head_dim) -> None:
+        """model.zig runWindowedAttention: every window in one launch."""
+        self._check(self.lib.qwh_audio_attention(self.handle, out_dev, out_stride, q_dev, k_dev, v_dev, qkv_stride,
+                                                 steps, window_steps, heads, head_dim))
+
+    def audio_layer(self, weights: "AudioLayerWeights", encoder_dev: int, steps: int, d_model: int, heads: int,
+                    ffn_dim: int, window_steps: int, eps: float) -> None:
+        """model.zig runAudioTower, one layer over encoder[steps][d_model] in place."""
+        self._check(self.lib.qwh_audio_layer(self.handle, ctypes.byref(weights), encoder_dev, steps, d_model, heads,
+                                             ffn_dim, window_steps, eps))
+
+    def audio_projector(self, in_matrix, in_bias_dev, out_matrix, out_bias_dev, encoder_dev, steps, out_dev) -> None:
+        """model.zig runProjector."""
+        self._check(self.lib.qwh_audio_projector(self.handle, in_matrix, in_bias_dev, out_matrix, out_bias_dev,
+                                                 encoder_dev, steps, out_dev))
 
     # -- quantization and synthetic inputs ---------------------------------
     def quantize_rows(self, fmt: int, values_dev: int, rows: int, cols: int, scales_dev: int, data_dev: int) -> None:

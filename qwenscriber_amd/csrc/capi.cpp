@@ -155,6 +155,7 @@ int32_t qwh_destroy(qwh_ctx *ctx) {
         if (e) (void)hipEventDestroy(e);
     if (ctx->digits.ptr) (void)hipFree(ctx->digits.ptr);
     if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
+    if (ctx->audio.ptr) (void)hipFree(ctx->audio.ptr);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QWH_OK;
@@ -531,6 +532,189 @@ int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_
         return fail(ctx, QWH_E_INVALID_ARGUMENT, "scale planes must be 2-byte aligned");
     return check_hip(ctx, launch_kv_append_q8(ctx->stream, key_dev, value_dev, kv_width, position, k_scales_dev, k_codes_dev,
                                               v_scales_dev, v_codes_dev), "kv append q8");
+}
+
+
+// ---- audio tower (model.zig:646-735) ----
+
+int32_t qwh_layer_norm(qwh_ctx *ctx, float *out_dev, const float *x_dev, const float *weight_dev,
+                       const float *bias_dev, uint32_t width, uint32_t tokens, float eps) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (tokens == 0) return QWH_OK;
+    if (width == 0) return fail(ctx, QWH_E_SHAPE_MISMATCH, "layer norm over rows of width 0");
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
+    QWH_TRY(check_device_ptr(ctx, weight_dev, "weight"));
+    QWH_TRY(check_device_ptr(ctx, bias_dev, "bias"));
+    return check_hip(ctx, launch_layer_norm(ctx->stream, x_dev, out_dev, weight_dev, bias_dev, width, tokens, eps),
+                     "layer norm");
+}
+
+int32_t qwh_add_bias(qwh_ctx *ctx, float *x_dev, const float *bias_dev, uint32_t rows, uint32_t tokens) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if ((uint64_t)rows * tokens == 0) return QWH_OK;
+    QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
+    QWH_TRY(check_device_ptr(ctx, bias_dev, "bias"));
+    return check_hip(ctx, launch_bias_epilogue(ctx->stream, kBiasAdd, x_dev, bias_dev, nullptr, rows, tokens),
+                     "add bias");
+}
+
+int32_t qwh_gelu(qwh_ctx *ctx, float *x_dev, uint64_t count) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (count == 0) return QWH_OK;
+    if (count > 0xFFFFFFFFull) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "gelu over %llu values", (unsigned long long)count);
+    QWH_TRY(check_device_ptr(ctx, x_dev, "x"));
+    return check_hip(ctx, launch_bias_epilogue(ctx->stream, kBiasGelu, x_dev, nullptr, nullptr, (uint32_t)count, 1),
+                     "gelu");
+}
+
+namespace {
+
+int32_t check_audio_attention(qwh_ctx *ctx, const AudioAttentionArgs &a) {
+    QWH_TRY(check_device_ptr(ctx, a.out, "out"));
+    QWH_TRY(check_device_ptr(ctx, a.q, "q"));
+    QWH_TRY(check_device_ptr(ctx, a.k, "k"));
+    QWH_TRY(check_device_ptr(ctx, a.v, "v"));
+    if (!audio_attention_supported(a.head_dim))
+        return fail(ctx, QWH_E_UNSUPPORTED, "audio attention is built for head_dim 32, 64 and 128, not %u", a.head_dim);
+    const uint64_t width = (uint64_t)a.heads * a.head_dim;
+    if (a.out_stride < width || a.q_stride < width || a.k_stride < width || a.v_stride < width)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "a row stride is below heads * head_dim = %llu", (unsigned long long)width);
+    if ((a.out_stride | a.q_stride | a.k_stride | a.v_stride) & 3u)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "row strides must be multiples of 4 floats");
+    const uintptr_t bits = (uintptr_t)a.out | (uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v |
+                           (uintptr_t)a.q_bias | (uintptr_t)a.k_bias | (uintptr_t)a.v_bias;
+    if (bits & 15u) return fail(ctx, QWH_E_INVALID_ARGUMENT, "audio attention buffers must be 16-byte aligned");
+    return QWH_OK;
+}
+
+}  // namespace
+
+int32_t qwh_audio_attention_window(qwh_ctx *ctx, float *out_dev, uint32_t out_stride, const float *q_dev,
+                                   uint32_t q_stride, const float *k_dev, uint32_t k_stride, const float *v_dev,
+                                   uint32_t v_stride, uint32_t window_start, uint32_t window_length, uint32_t heads,
+                                   uint32_t head_dim) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (window_length == 0 || heads == 0) return QWH_OK;
+    if ((uint64_t)window_start + window_length > 0xFFFFFFFFull)
+        return fail(ctx, QWH_E_LIMIT_EXCEEDED, "window end past 2^32 steps");
+    AudioAttentionArgs a;
+    a.out = out_dev, a.q = q_dev, a.k = k_dev, a.v = v_dev;
+    a.out_stride = out_stride, a.q_stride = q_stride, a.k_stride = k_stride, a.v_stride = v_stride;
+    a.first = window_start, a.end = window_start + window_length, a.window_steps = window_length;
+    a.heads = heads, a.head_dim = head_dim;
+    a.scaling = 1.0f / sqrtf((float)head_dim);
+    QWH_TRY(check_audio_attention(ctx, a));
+    return check_hip(ctx, launch_audio_attention(ctx->stream, a), "audio attention");
+}
+
+int32_t qwh_audio_attention(qwh_ctx *ctx, float *out_dev, uint32_t out_stride, const float *q_dev,
+                            const float *k_dev, const float *v_dev, uint32_t qkv_stride, uint32_t steps,
+                            uint32_t window_steps, uint32_t heads, uint32_t head_dim) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (steps == 0 || heads == 0) return QWH_OK;
+    if (window_steps == 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "window_steps is 0");
+    AudioAttentionArgs a;
+    a.out = out_dev, a.q = q_dev, a.k = k_dev, a.v = v_dev;
+    a.out_stride = out_stride, a.q_stride = a.k_stride = a.v_stride = qkv_stride;
+    a.first = 0, a.end = steps, a.window_steps = window_steps;
+    a.heads = heads, a.head_dim = head_dim;
+    a.scaling = 1.0f / sqrtf((float)head_dim);
+    QWH_TRY(check_audio_attention(ctx, a));
+    return check_hip(ctx, launch_audio_attention(ctx->stream, a), "audio attention");
+}
+
+namespace {
+
+int32_t check_audio_matrix(qwh_ctx *ctx, uint64_t handle, uint32_t rows, uint32_t cols, const char *what) {
+    const Matrix *m = find_matrix(ctx, handle);
+    if (!m) return fail(ctx, QWH_E_NOT_FOUND, "%s: unknown matrix handle %llu", what, (unsigned long long)handle);
+    if (m->rows != rows || m->cols != cols)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "%s is %u x %u, the layer needs %u x %u", what, m->rows, m->cols, rows,
+                    cols);
+    return QWH_OK;
+}
+
+}  // namespace
+
+int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *encoder_dev, uint32_t steps,
+                        uint32_t d_model, uint32_t heads, uint32_t ffn_dim, uint32_t window_steps, float eps) {
+    if (!ctx || !w) return QWH_E_INVALID_ARGUMENT;
+    if (steps == 0) return QWH_OK;
+    if (heads == 0 || d_model % heads != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "d_model %u is not a multiple of %u heads", d_model, heads);
+    if (window_steps == 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "window_steps is 0");
+    QWH_TRY(check_device_ptr(ctx, encoder_dev, "encoder"));
+    QWH_TRY(check_audio_matrix(ctx, w->q, d_model, d_model, "q"));
+    QWH_TRY(check_audio_matrix(ctx, w->k, d_model, d_model, "k"));
+    QWH_TRY(check_audio_matrix(ctx, w->v, d_model, d_model, "v"));
+    QWH_TRY(check_audio_matrix(ctx, w->o, d_model, d_model, "o"));
+    QWH_TRY(check_audio_matrix(ctx, w->ffn_in, ffn_dim, d_model, "ffn_in"));
+    QWH_TRY(check_audio_matrix(ctx, w->ffn_out, d_model, ffn_dim, "ffn_out"));
+    const void *vectors[] = {w->q_bias, w->k_bias, w->v_bias, w->o_bias, w->ffn_in_bias, w->ffn_out_bias,
+                             w->attention_norm_weight, w->attention_norm_bias, w->final_norm_weight,
+                             w->final_norm_bias};
+    for (const void *p : vectors) QWH_TRY(check_device_ptr(ctx, p, "layer vector"));
+    const size_t plane = (size_t)steps * d_model;
+    QWH_TRY(ensure_workspace(ctx, ctx->audio, sizeof(float) * (5 * plane + (size_t)steps * ffn_dim)));
+    float *normed = static_cast<float *>(ctx->audio.ptr);
+    float *q = normed + plane, *k = q + plane, *v = k + plane, *block = v + plane, *wide = block + plane;
+    hipStream_t s = ctx->stream;
+
+    // model.zig:657-665 layerNormInto, :765-786 projectQkv (biases join in the attention's loads).
+    QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->attention_norm_weight, w->attention_norm_bias,
+                                             d_model, steps, eps), "audio attention norm"));
+    QWH_TRY(qwh_linear(ctx, w->q, normed, d_model, steps, q));
+    QWH_TRY(qwh_linear(ctx, w->k, normed, d_model, steps, k));
+    QWH_TRY(qwh_linear(ctx, w->v, normed, d_model, steps, v));
+    // :792-822 runWindowedAttention.
+    AudioAttentionArgs a;
+    a.out = block, a.q = q, a.k = k, a.v = v;
+    a.q_bias = w->q_bias, a.k_bias = w->k_bias, a.v_bias = w->v_bias;
+    a.out_stride = a.q_stride = a.k_stride = a.v_stride = d_model;
+    a.first = 0, a.end = steps, a.window_steps = window_steps;
+    a.heads = heads, a.head_dim = d_model / heads;
+    a.scaling = 1.0f / sqrtf((float)a.head_dim);
+    QWH_TRY(check_audio_attention(ctx, a));
+    QWH_TRY(check_hip(ctx, launch_audio_attention(s, a), "audio attention"));
+    // :824-848 projectAttentionOutput, :669 addInPlace.
+    QWH_TRY(qwh_linear(ctx, w->o, block, d_model, steps, normed));
+    QWH_TRY(check_hip(ctx, launch_bias_epilogue(s, kBiasResidual, normed, w->o_bias, encoder_dev, d_model, steps),
+                      "audio o bias + residual"));
+    // :671-679 layerNormInto, :852-872 activateFfn, :692 addInPlace.
+    QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->final_norm_weight, w->final_norm_bias, d_model,
+                                             steps, eps), "audio final norm"));
+    QWH_TRY(qwh_linear(ctx, w->ffn_in, normed, d_model, steps, wide));
+    QWH_TRY(check_hip(ctx, launch_bias_epilogue(s, kBiasGelu, wide, w->ffn_in_bias, nullptr, ffn_dim, steps),
+                      "audio ffn bias + gelu"));
+    QWH_TRY(qwh_linear(ctx, w->ffn_out, wide, ffn_dim, steps, block));
+    return check_hip(ctx, launch_bias_epilogue(s, kBiasResidual, block, w->ffn_out_bias, encoder_dev, d_model, steps),
+                     "audio ffn bias + residual");
+}
+
+int32_t qwh_audio_projector(qwh_ctx *ctx, uint64_t in_matrix, const float *in_bias_dev, uint64_t out_matrix,
+                            const float *out_bias_dev, const float *encoder_dev, uint32_t steps, float *out_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    const Matrix *mi = find_matrix(ctx, in_matrix);
+    const Matrix *mo = find_matrix(ctx, out_matrix);
+    if (!mi || !mo) return fail(ctx, QWH_E_NOT_FOUND, "unknown projector matrix handle");
+    // model.zig:707-735: in is d_model x d_model, out is hidden x d_model.
+    if (mi->rows != mi->cols || mo->cols != mi->rows)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "projector matrices %u x %u and %u x %u do not chain", mi->rows, mi->cols,
+                    mo->rows, mo->cols);
+    if (steps == 0) return QWH_OK;
+    QWH_TRY(check_device_ptr(ctx, in_bias_dev, "in bias"));
+    QWH_TRY(check_device_ptr(ctx, out_bias_dev, "out bias"));
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    QWH_TRY(ensure_workspace(ctx, ctx->audio, sizeof(float) * (size_t)steps * mi->rows));
+    float *mid = static_cast<float *>(ctx->audio.ptr);
+    const uint32_t d_model = mi->rows, hidden = mo->rows;
+    QWH_TRY(qwh_linear(ctx, in_matrix, encoder_dev, d_model, steps, mid));
+    QWH_TRY(check_hip(ctx, launch_bias_epilogue(ctx->stream, kBiasGelu, mid, in_bias_dev, nullptr, d_model, steps),
+                      "projector bias + gelu"));
+    QWH_TRY(qwh_linear(ctx, out_matrix, mid, d_model, steps, out_dev));
+    return check_hip(ctx, launch_bias_epilogue(ctx->stream, kBiasAdd, out_dev, out_bias_dev, nullptr, hidden, steps),
+                     "projector bias");
 }
 
 }  // extern "C"

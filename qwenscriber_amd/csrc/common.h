@@ -72,6 +72,7 @@ struct qwh_ctx {
     uint64_t next_handle = 1;
     qwh::Workspace digits;  // x digit planes for the q4 GEMV
     qwh::Workspace scratch; // attention partials and other per-call scratch
+    qwh::Workspace audio;   // audio tower layer / projector activations
 };
 
 namespace qwh {
@@ -199,6 +200,31 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
 hipError_t launch_kv_append_q8(hipStream_t s, const float *key, const float *value,
                                uint32_t kv_width, uint32_t position, uint8_t *k_scales,
                                uint8_t *k_codes, uint8_t *v_scales, uint8_t *v_codes);
+
+// Audio tower glue (audio.hip). LayerNorm per token row (out may alias x).
+hipError_t launch_layer_norm(hipStream_t s, const float *x, float *out, const float *weight, const float *bias,
+                             uint32_t width, uint32_t tokens, float eps);
+// x[t][r] + bias[r] (bias may be null): stored to x, GELU of it stored to x,
+// or added onto residual[t][r].
+enum BiasMode { kBiasAdd = 0, kBiasGelu = 1, kBiasResidual = 2 };
+hipError_t launch_bias_epilogue(hipStream_t s, int mode, float *x, const float *bias, float *residual, uint32_t rows,
+                                uint32_t tokens);
+// Non-causal attention inside windows of window_steps steps starting at
+// `first`, the last one ending at `end` (ragged). Row r of q / k / v / out
+// starts at ptr + r * stride; head h occupies columns [h * head_dim, (h+1) *
+// head_dim). Optional biases are added to q / k / v rows as they are read.
+// Strides and base pointers must keep rows 16-byte aligned.
+struct AudioAttentionArgs {
+    float *out = nullptr;
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    const float *q_bias = nullptr, *k_bias = nullptr, *v_bias = nullptr;
+    uint32_t out_stride = 0, q_stride = 0, k_stride = 0, v_stride = 0;
+    uint32_t first = 0, end = 0, window_steps = 0;
+    uint32_t heads = 0, head_dim = 0;
+    float scaling = 0.0f;
+};
+bool audio_attention_supported(uint32_t head_dim);
+hipError_t launch_audio_attention(hipStream_t s, const AudioAttentionArgs &a);
 
 }  // namespace qwh
 
