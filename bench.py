@@ -253,7 +253,61 @@ def bench_small(ctx, qa, steps):
         for b in (vals, ks, kc, vs, vc, q, o_):
             b.free()
     out["q8_attention"] = att
+    out["audio_tower_0p6b"] = bench_audio(ctx, qa, steps)
     return out
+
+
+def bench_audio(ctx, qa, steps):
+    """Audio tower row: one Qwen3-ASR-0.6B audio layer (d_model 896, 14 heads,
+    ffn 3584; tensor_names.zig:416-419) over 390 steps (30 s of audio) with
+    windows of 104 steps, q4 weights; plus the windowed attention alone and
+    the projector (896 -> 1024). Synthetic weights and activations."""
+    d, heads, ffn, T, window = 896, 14, 3584, 390, 104
+    mats = {}
+    for i, (name, rows, cols) in enumerate((("q", d, d), ("k", d, d), ("v", d, d), ("o", d, d),
+                                            ("ffn_in", ffn, d), ("ffn_out", d, ffn))):
+        mats[name] = ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, 5, i, 0.02)
+    weights = qa.AudioLayerWeights()
+    bufs = []
+    for name in qa.AudioLayerWeights.MATRICES:
+        setattr(weights, name, mats[name])
+    for j, name in enumerate(qa.AudioLayerWeights.VECTORS):
+        n = ffn if name == "ffn_in_bias" else d
+        b = ctx.buffer(n * 4)
+        ctx.synth_normal(5, 100 + j, n, 0.1, b.ptr)
+        bufs.append(b)
+        setattr(weights, name, b.ptr)
+    enc = ctx.buffer(T * d * 4)
+    ctx.synth_normal(5, 200, T * d, 1.0, enc.ptr)
+    # The residual stream changes every call (as a tower's layers do); the
+    # work per call does not depend on the values.
+    layer_ms = time_events(ctx, lambda i: ctx.audio_layer(weights, enc.ptr, T, d, heads, ffn, window, 1e-5), steps)
+    qkv = ctx.buffer(T * 3 * d * 4)
+    ctx.synth_normal(5, 201, T * 3 * d, 1.0, qkv.ptr)
+    att = ctx.buffer(T * d * 4)
+    att_ms = time_events(ctx, lambda i: ctx.audio_attention(att.ptr, d, qkv.ptr, qkv.ptr + 4 * d, qkv.ptr + 8 * d,
+                                                            3 * d, T, window, heads, d // heads), steps)
+    p_in = ctx.matrix_synthetic(qa.FORMAT_Q4, d, d, 5, 10, 0.02)
+    p_out = ctx.matrix_synthetic(qa.FORMAT_Q4, 1024, d, 5, 11, 0.02)
+    proj = ctx.buffer(T * 1024 * 4)
+    proj_ms = time_events(ctx, lambda i: ctx.audio_projector(p_in, bufs[0].ptr, p_out, bufs[1].ptr, enc.ptr, T,
+                                                             proj.ptr), steps)
+    layer_flops = 2 * T * (4 * d * d + 2 * d * ffn)
+    # Scores and weighted sums: 2 x 2 x head_dim flops per (query, key) pair.
+    pairs = sum(min(window, T - s) ** 2 for s in range(0, T, window))
+    att_flops = 4 * pairs * d
+    res = {
+        "workload": "Qwen3-ASR-0.6B audio layer, 390 steps, window 104, q4 weights, f32 activations",
+        "layer_us": layer_ms * 1e3, "layer_TFLOPs": (layer_flops + att_flops) / (layer_ms * 1e-3) / 1e12,
+        "tower_18_layers_ms": 18 * layer_ms,
+        "attention_us": att_ms * 1e3, "attention_GFLOPs": att_flops / (att_ms * 1e-3) / 1e9,
+        "projector_us": proj_ms * 1e3,
+    }
+    for m in list(mats.values()) + [p_in, p_out]:
+        ctx.matrix_release(m)
+    for b in bufs + [enc, qkv, att, proj]:
+        b.free()
+    return res
 
 
 def main():

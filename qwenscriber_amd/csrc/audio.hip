@@ -90,45 +90,117 @@ __global__ __launch_bounds__(256) void bias_epilogue_kernel(float *x, const floa
     }
 }
 
-// Windowed attention. Workgroup (query tile, window, head): 64 queries of
-// one window and head, G = HD / 32 lanes per query, each lane owning 32 of
-// the head's dimensions. Keys and values of the window pass through LDS in
-// chunks of 64 rows; each query keeps an online softmax (running maximum,
-// running sum, 32 accumulators per lane) and divides once at the end, which
-// equals softmax-then-weighted-sum up to f32 rounding.
-constexpr int kQueriesPerTile = 64;
+// Windowed attention. One workgroup per (query tile, window, head) of
+// kWaves wavefronts: G = HD / 16 lanes per query, each lane owning 16 of the
+// head's dimensions, so a tile is 64 / G queries, and every wavefront holds
+// the whole tile. Keys and values of the window pass through LDS in chunks of
+// 64 rows; the wavefronts split each chunk's keys four ways (lanes of one
+// query read different slices, the tile's queries the same ones:
+// broadcasts). Each wavefront keeps an online softmax per query (running
+// maximum, running sum, 16 accumulators per lane), two keys per step so
+// their dot products, reductions and exponentials overlap; at the end the
+// four partial states are merged through LDS and divided once:
+// softmax-then-weighted-sum up to f32 rounding.
+constexpr int kDimsPerLane = 16;
 constexpr int kKeysPerChunk = 64;
+constexpr int kWaves = 4;
 
 template <int HD>
-__global__ __launch_bounds__(kQueriesPerTile *(HD / 32)) void audio_attention_kernel(AudioAttentionArgs a) {
-    constexpr int G = HD / 32;
-    constexpr int kThreads = kQueriesPerTile * G;
+struct AudioTile {
+    static constexpr int G = HD / kDimsPerLane;
+    static constexpr int queries = 64 / G;
+};
+
+__device__ __forceinline__ float slice_dot(const float (&qv)[kDimsPerLane], const float *krow) {
+    const float4 *k4 = reinterpret_cast<const float4 *>(krow);
+    float even = 0.0f, odd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kDimsPerLane / 4; i += 2) {
+        const float4 a = k4[i], b = k4[i + 1];
+        even += qv[4 * i] * a.x + qv[4 * i + 1] * a.y + qv[4 * i + 2] * a.z + qv[4 * i + 3] * a.w;
+        odd += qv[4 * i + 4] * b.x + qv[4 * i + 5] * b.y + qv[4 * i + 6] * b.z + qv[4 * i + 7] * b.w;
+    }
+    return even + odd;
+}
+
+struct SoftmaxState {
+    float max = -INFINITY, sum = 0.0f;
+    float acc[kDimsPerLane];
+};
+
+// Folds scores s0 (and s1 when `two`) with value rows v0 / v1 into the state.
+template <bool two>
+__device__ __forceinline__ void softmax_fold(SoftmaxState &st, float s0, float s1, const float *v0, const float *v1) {
+    const float top = two ? fmaxf(s0, s1) : s0;
+    if (top > st.max) {
+        const float correction = expf(st.max - top);
+        st.sum *= correction;
+#pragma unroll
+        for (int i = 0; i < kDimsPerLane; ++i) st.acc[i] *= correction;
+        st.max = top;
+    }
+    const float p0 = expf(s0 - st.max);
+    st.sum += p0;
+    const float4 *x4 = reinterpret_cast<const float4 *>(v0);
+    if constexpr (two) {
+        const float p1 = expf(s1 - st.max);
+        st.sum += p1;
+        const float4 *y4 = reinterpret_cast<const float4 *>(v1);
+#pragma unroll
+        for (int i = 0; i < kDimsPerLane / 4; ++i) {
+            const float4 x = x4[i], y = y4[i];
+            st.acc[4 * i] += p0 * x.x + p1 * y.x;
+            st.acc[4 * i + 1] += p0 * x.y + p1 * y.y;
+            st.acc[4 * i + 2] += p0 * x.z + p1 * y.z;
+            st.acc[4 * i + 3] += p0 * x.w + p1 * y.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kDimsPerLane / 4; ++i) {
+            const float4 x = x4[i];
+            st.acc[4 * i] += p0 * x.x, st.acc[4 * i + 1] += p0 * x.y;
+            st.acc[4 * i + 2] += p0 * x.z, st.acc[4 * i + 3] += p0 * x.w;
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * kWaves) void audio_attention_kernel(AudioAttentionArgs a) {
+    constexpr int G = AudioTile<HD>::G;
+    constexpr int QT = AudioTile<HD>::queries;
     constexpr int kRow = HD + 4;  // LDS row pitch in floats (16-byte aligned, staggered banks)
-    __shared__ float4 lds_k[kKeysPerChunk * kRow / 4];
-    __shared__ float4 lds_v[kKeysPerChunk * kRow / 4];
+    constexpr int kState = 4 + kDimsPerLane;  // max, sum, two pad, accumulators
+    // Keys, then values, of one chunk; after the last chunk the same space
+    // holds the wavefronts' merge records.
+    constexpr int kChunkFloats = kKeysPerChunk * kRow;
+    constexpr int kRecordFloats = kWaves * 64 * kState;
+    constexpr int kLdsFloats = 2 * kChunkFloats > kRecordFloats ? 2 * kChunkFloats : kRecordFloats;
+    __shared__ float4 lds[kLdsFloats / 4];
+    float4 *lds_k = lds;
+    float4 *lds_v = lds + kChunkFloats / 4;
     const float *ks = reinterpret_cast<const float *>(lds_k);
     const float *vs = reinterpret_cast<const float *>(lds_v);
 
     const uint32_t start = a.first + blockIdx.y * a.window_steps;
     if (start >= a.end) return;
     const uint32_t length = min(a.window_steps, a.end - start);
-    const uint32_t q0 = blockIdx.x * kQueriesPerTile;
+    const uint32_t q0 = blockIdx.x * QT;
     if (q0 >= length) return;
-    const uint32_t head = blockIdx.z;
-    const uint32_t column = head * HD;
+    const uint32_t column = blockIdx.z * HD;
 
-    const int lane = threadIdx.x;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const uint32_t query = q0 + lane / G;
-    const int part = lane % G;
+    const int slice = (lane % G) * kDimsPerLane;
     const bool valid = query < length;
     const uint32_t query_row = start + (valid ? query : length - 1);
 
-    float qv[32];
+    float qv[kDimsPerLane];
     {
-        const float4 *src = reinterpret_cast<const float4 *>(a.q + (size_t)query_row * a.q_stride + column + part * 32);
-        const float4 *qb = a.q_bias ? reinterpret_cast<const float4 *>(a.q_bias + column + part * 32) : nullptr;
+        const float4 *src = reinterpret_cast<const float4 *>(a.q + (size_t)query_row * a.q_stride + column + slice);
+        const float4 *qb = a.q_bias ? reinterpret_cast<const float4 *>(a.q_bias + column + slice) : nullptr;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kDimsPerLane / 4; ++i) {
             float4 v = src[i];
             if (qb) {
                 const float4 b = qb[i];
@@ -137,15 +209,17 @@ __global__ __launch_bounds__(kQueriesPerTile *(HD / 32)) void audio_attention_ke
             qv[4 * i] = v.x, qv[4 * i + 1] = v.y, qv[4 * i + 2] = v.z, qv[4 * i + 3] = v.w;
         }
     }
-    float acc[32];
+    SoftmaxState st;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc[i] = 0.0f;
-    float running_max = -INFINITY, running_sum = 0.0f;
+    for (int i = 0; i < kDimsPerLane; ++i) st.acc[i] = 0.0f;
 
     for (uint32_t k0 = 0; k0 < length; k0 += kKeysPerChunk) {
         const uint32_t count = min((uint32_t)kKeysPerChunk, length - k0);
         __syncthreads();
-        for (int idx = threadIdx.x; idx < kKeysPerChunk * (HD / 4); idx += kThreads) {
+        // Every load is unconditional (rows past the window repeat its last
+        // row and are never read back), so all of them are in flight at once.
+#pragma unroll 4
+        for (int idx = threadIdx.x; idx < kKeysPerChunk * (HD / 4); idx += 64 * kWaves) {
             const int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
             const uint32_t row = start + k0 + min((uint32_t)r, count - 1);
             float4 kv = *reinterpret_cast<const float4 *>(a.k + (size_t)row * a.k_stride + column + c);
@@ -162,40 +236,52 @@ __global__ __launch_bounds__(kQueriesPerTile *(HD / 32)) void audio_attention_ke
             lds_v[(r * kRow + c) / 4] = vv;
         }
         __syncthreads();
-        for (uint32_t j = 0; j < count; ++j) {
-            const float4 *krow = reinterpret_cast<const float4 *>(ks + j * kRow + part * 32);
-            float dot = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 kk = krow[i];
-                dot += qv[4 * i] * kk.x + qv[4 * i + 1] * kk.y + qv[4 * i + 2] * kk.z + qv[4 * i + 3] * kk.w;
-            }
-            const float score = dev::group_sum<G>(dot) * a.scaling;
-            if (score > running_max) {
-                const float correction = expf(running_max - score);
-                running_sum *= correction;
-#pragma unroll
-                for (int i = 0; i < 32; ++i) acc[i] *= correction;
-                running_max = score;
-            }
-            const float p = expf(score - running_max);
-            running_sum += p;
-            const float4 *vrow = reinterpret_cast<const float4 *>(vs + j * kRow + part * 32);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 vv = vrow[i];
-                acc[4 * i] += p * vv.x, acc[4 * i + 1] += p * vv.y;
-                acc[4 * i + 2] += p * vv.z, acc[4 * i + 3] += p * vv.w;
-            }
+        // This wavefront's share of the chunk's keys: [lo, hi).
+        const uint32_t lo = count * wave / kWaves, hi = count * (wave + 1) / kWaves;
+        uint32_t j = lo;
+        for (; j + 1 < hi; j += 2) {
+            const float d0 = slice_dot(qv, ks + j * kRow + slice);
+            const float d1 = slice_dot(qv, ks + (j + 1) * kRow + slice);
+            const float s0 = dev::group_sum<G>(d0) * a.scaling;
+            const float s1 = dev::group_sum<G>(d1) * a.scaling;
+            softmax_fold<true>(st, s0, s1, vs + j * kRow + slice, vs + (j + 1) * kRow + slice);
+        }
+        if (j < hi) {
+            const float s0 = dev::group_sum<G>(slice_dot(qv, ks + j * kRow + slice)) * a.scaling;
+            softmax_fold<false>(st, s0, 0.0f, vs + j * kRow + slice, nullptr);
         }
     }
-    if (!valid) return;
-    const float inverse = 1.0f / running_sum;
-    float4 *dst = reinterpret_cast<float4 *>(a.out + (size_t)(start + query) * a.out_stride + column + part * 32);
+
+    // Merge the wavefronts' states: wavefront w finishes dimensions
+    // [4w, 4w + 4) of every lane's slice.
+    __syncthreads();
+    float *records = reinterpret_cast<float *>(lds);
+    {
+        float4 *mine = reinterpret_cast<float4 *>(records + (wave * 64 + lane) * kState);
+        mine[0] = make_float4(st.max, st.sum, 0.0f, 0.0f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        dst[i] = make_float4(acc[4 * i] * inverse, acc[4 * i + 1] * inverse, acc[4 * i + 2] * inverse,
-                             acc[4 * i + 3] * inverse);
+        for (int i = 0; i < kDimsPerLane / 4; ++i)
+            mine[1 + i] = make_float4(st.acc[4 * i], st.acc[4 * i + 1], st.acc[4 * i + 2], st.acc[4 * i + 3]);
+    }
+    __syncthreads();
+    if (!valid) return;
+    float top = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) top = fmaxf(top, records[(w * 64 + lane) * kState]);
+    float total = 0.0f;
+    float4 merged = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const float *rec = records + (w * 64 + lane) * kState;
+        const float weight = expf(rec[0] - top);  // 0 for a wavefront that saw no keys
+        total += rec[1] * weight;
+        const float4 part = reinterpret_cast<const float4 *>(rec + 4)[wave];
+        merged.x += part.x * weight, merged.y += part.y * weight;
+        merged.z += part.z * weight, merged.w += part.w * weight;
+    }
+    const float inverse = 1.0f / total;
+    float4 *dst = reinterpret_cast<float4 *>(a.out + (size_t)(start + query) * a.out_stride + column + slice);
+    dst[wave] = make_float4(merged.x * inverse, merged.y * inverse, merged.z * inverse, merged.w * inverse);
 }
 
 }  // namespace
@@ -230,11 +316,22 @@ hipError_t launch_audio_attention(hipStream_t s, const AudioAttentionArgs &a) {
     const uint32_t span = a.end - a.first;
     const uint32_t windows = (span + a.window_steps - 1) / a.window_steps;
     const uint32_t longest = std::min(a.window_steps, span);
-    const dim3 grid((longest + kQueriesPerTile - 1) / kQueriesPerTile, windows, a.heads);
     switch (a.head_dim) {
-    case 32: audio_attention_kernel<32><<<grid, kQueriesPerTile * 1, 0, s>>>(a); break;
-    case 64: audio_attention_kernel<64><<<grid, kQueriesPerTile * 2, 0, s>>>(a); break;
-    case 128: audio_attention_kernel<128><<<grid, kQueriesPerTile * 4, 0, s>>>(a); break;
+    case 32: {
+        const dim3 grid((longest + AudioTile<32>::queries - 1) / AudioTile<32>::queries, windows, a.heads);
+        audio_attention_kernel<32><<<grid, 64 * kWaves, 0, s>>>(a);
+        break;
+    }
+    case 64: {
+        const dim3 grid((longest + AudioTile<64>::queries - 1) / AudioTile<64>::queries, windows, a.heads);
+        audio_attention_kernel<64><<<grid, 64 * kWaves, 0, s>>>(a);
+        break;
+    }
+    case 128: {
+        const dim3 grid((longest + AudioTile<128>::queries - 1) / AudioTile<128>::queries, windows, a.heads);
+        audio_attention_kernel<128><<<grid, 64 * kWaves, 0, s>>>(a);
+        break;
+    }
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -5,6 +5,8 @@
 #include <cstdio>
 #include <cstring>
 
+#include <initializer_list>
+
 #include "common.h"
 
 namespace qwh {
@@ -637,6 +639,41 @@ int32_t check_audio_matrix(qwh_ctx *ctx, uint64_t handle, uint32_t rows, uint32_
 
 }  // namespace
 
+namespace {
+
+// Several linears over the same activations: for q4 matrices and two or more
+// tokens the digit planes are prepared once and each matrix reads them
+// (qwh_linear would prepare them per matrix); other formats go through
+// qwh_linear one by one.
+int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handles, const float *x, uint32_t cols,
+                            uint32_t tokens, std::initializer_list<float *> outs) {
+    bool shared = tokens >= 2 && ((uintptr_t)x & 15u) == 0;
+    for (uint64_t h : handles) {
+        const Matrix *m = find_matrix(ctx, h);
+        shared = shared && m && m->format == QWH_FORMAT_Q4 && m->cols == cols && m->rows > 0;
+    }
+    auto out = outs.begin();
+    if (!shared) {
+        for (uint64_t h : handles) QWH_TRY(qwh_linear(ctx, h, x, cols, tokens, *out++));
+        return QWH_OK;
+    }
+    size_t parts = 0;
+    for (uint64_t h : handles) parts = std::max(parts, batch_partial_bytes(tokens, *find_matrix(ctx, h)));
+    QWH_TRY(ensure_workspace(ctx, ctx->digits, batch_digit_bytes(tokens, cols)));
+    if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
+    GemvInput in;
+    in.mode = GemvInput::F32;
+    in.x = x;
+    QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
+    for (uint64_t h : handles)
+        QWH_TRY(check_hip(ctx, launch_gemv_q4_batch(ctx->stream, ctx->digits.ptr, *find_matrix(ctx, h), tokens, *out++,
+                                                    nullptr, false, static_cast<float *>(ctx->scratch.ptr)),
+                          "gemv q4 batch"));
+    return QWH_OK;
+}
+
+}  // namespace
+
 int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *encoder_dev, uint32_t steps,
                         uint32_t d_model, uint32_t heads, uint32_t ffn_dim, uint32_t window_steps, float eps) {
     if (!ctx || !w) return QWH_E_INVALID_ARGUMENT;
@@ -664,9 +701,7 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
     // model.zig:657-665 layerNormInto, :765-786 projectQkv (biases join in the attention's loads).
     QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->attention_norm_weight, w->attention_norm_bias,
                                              d_model, steps, eps), "audio attention norm"));
-    QWH_TRY(qwh_linear(ctx, w->q, normed, d_model, steps, q));
-    QWH_TRY(qwh_linear(ctx, w->k, normed, d_model, steps, k));
-    QWH_TRY(qwh_linear(ctx, w->v, normed, d_model, steps, v));
+    QWH_TRY(linear_shared_input(ctx, {w->q, w->k, w->v}, normed, d_model, steps, {q, k, v}));
     // :792-822 runWindowedAttention.
     AudioAttentionArgs a;
     a.out = block, a.q = q, a.k = k, a.v = v;
