@@ -91,6 +91,8 @@ def test_audio_attention_known_answers(ctx):
     (37, 13, 3, 128),
     (70, 70, 2, 32),
     (200, 64, 4, 64),     # windows of exactly one key chunk
+    (300, 150, 2, 128),   # three key chunks per window at the widest head
+    (5, 1, 2, 64),        # windows of one step: each output is its own value row
 ])
 def test_audio_attention_windows(ctx, steps, window, heads, head_dim):
     width = heads * head_dim
@@ -108,6 +110,28 @@ def test_audio_attention_windows(ctx, steps, window, heads, head_dim):
     ctx.audio_attention(ob.ptr, width, qb.ptr, qb.ptr + 4 * width, qb.ptr + 8 * width, 3 * width, steps, window,
                         heads, head_dim)
     assert_close(ob.download(np.float32), expected, rtol=1e-4, atol_rms=1e-4, what="audio attention")
+
+
+def test_audio_attention_window_inside_a_larger_buffer(ctx):
+    # One window [50, 110) of a 160-step buffer with distinct row strides:
+    # rows outside the window keep their contents.
+    steps, heads, hd = 160, 3, 64
+    width = heads * hd
+    q = normal(steps * (width + 64), 61)
+    k = normal(steps * (width + 128), 62)
+    v = normal(steps * width, 63)
+    out0 = normal(steps * (width + 32), 64)
+    strides = (width + 32, width + 64, width + 128, width)
+    expected = out0.copy()
+    o.audio_attention_window(expected, q, k, v, strides, 50, 60, heads, hd)
+    qb, kb, vb, ob = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v), ctx.to_device(out0)
+    ctx.audio_attention_window(ob.ptr, strides[0], qb.ptr, strides[1], kb.ptr, strides[2], vb.ptr, strides[3], 50, 60,
+                               heads, hd)
+    got = ob.download(np.float32)
+    rows = got.reshape(steps, -1)
+    assert np.array_equal(rows[:50], out0.reshape(steps, -1)[:50])
+    assert np.array_equal(rows[110:], out0.reshape(steps, -1)[110:])
+    assert_close(got, expected, rtol=1e-4, atol_rms=1e-4, what="audio attention window")
 
 
 def make_layer(ctx, fmt, d_model, ffn_dim, seed):
