@@ -381,6 +381,14 @@ int32_t qwh_decoder_set_position(qwh_decoder *decoder, uint32_t seq, uint32_t po
 /* decoder.zig:133-287 forwardToken for every sequence at once: tokens[b] is
  * sequence b's token. With want_logits the logits stay on the device. */
 int32_t qwh_decoder_forward(qwh_decoder *decoder, const uint32_t *tokens, int32_t want_logits);
+/* decoder.zig:133-150 forwardToken with audio_row: for every sequence whose
+ * row_mask byte is nonzero (every sequence when row_mask is null), row b of
+ * rows_dev (batch x hidden f32, device) replaces the token's embedding --
+ * the projected audio features spliced into a placeholder position, as
+ * decoder.zig:308-333 prefill does. Other sequences embed tokens[b]. Every
+ * sequence advances one position; logits are kept when want_logits. */
+int32_t qwh_decoder_forward_rows(qwh_decoder *decoder, const uint32_t *tokens, const float *rows_dev,
+                                 const uint8_t *row_mask, int32_t want_logits);
 /* decoder.zig:336-339 step: forwardToken then argmaxLogits (:290-301, first
  * maximum wins) for every sequence; next_tokens receives batch ids. */
 int32_t qwh_decoder_step(qwh_decoder *decoder, const uint32_t *tokens, uint32_t *next_tokens);

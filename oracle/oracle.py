@@ -99,6 +99,7 @@ _SIGNATURES = {
     "qwref_decoder_destroy": (None, [_P]),
     "qwref_decoder_prefill_random": (_I32, [_P, _U32, _U32]),
     "qwref_decoder_forward": (_I32, [_P, _U32, _U32, _I32]),
+    "qwref_decoder_forward_row": (_I32, [_P, _U32, _U32, _P, _I32]),
     "qwref_decoder_logits": (ctypes.POINTER(ctypes.c_float), [_P, _U32]),
     "qwref_decoder_position": (_U32, [_P, _U32]),
     "qwref_decoder_step": (_I32, [_P, _U32, _U32, ctypes.POINTER(_U32)]),
@@ -327,6 +328,13 @@ class Decoder:
         status = lib().qwref_decoder_forward(self.handle, seq, token, int(want_logits))
         if status != 0:
             raise ValueError(f"forward status {status}")
+
+    def forward_row(self, seq: int, token: int, row: np.ndarray, want_logits: bool = True) -> None:
+        """forwardToken with an audio row in place of the token's embedding."""
+        row = np.ascontiguousarray(row, np.float32)
+        status = lib().qwref_decoder_forward_row(self.handle, seq, token, _ptr(row), int(want_logits))
+        if status != 0:
+            raise ValueError(f"forward_row status {status}")
 
     def logits(self, seq: int) -> np.ndarray:
         ptr = lib().qwref_decoder_logits(self.handle, seq)

@@ -1002,15 +1002,30 @@ static int32_t embedding_row(const qmat *m, uint32_t row, float *out) {
 }
 
 /* decoder.zig:133-287 `forwardToken` with the q8 cache. */
+/* decoder.zig:133-150 forwardToken with an audio row: the row replaces the
+ * token embedding (the projected audio features spliced into a placeholder
+ * position); everything after the embedding is the same step. */
+int32_t qwref_decoder_forward_row(qwref_decoder *d, uint32_t seq, uint32_t token, const float *audio_row,
+                                  int32_t want_logits);
+
 int32_t qwref_decoder_forward(qwref_decoder *d, uint32_t seq, uint32_t token, int32_t want_logits) {
+    return qwref_decoder_forward_row(d, seq, token, NULL, want_logits);
+}
+
+int32_t qwref_decoder_forward_row(qwref_decoder *d, uint32_t seq, uint32_t token, const float *audio_row,
+                                  int32_t want_logits) {
     if (seq >= d->batch) return QWREF_INVALID_ARGUMENT;
     const qwref_decoder_config *c = &d->c;
     sequence_state *s = &d->seqs[seq];
     if (s->position >= c->max_positions) return QWREF_LIMIT_EXCEEDED;
     uint32_t hs = c->hidden;
     uint32_t qw = c->heads * c->head_dim, kvw = c->kv_heads * c->head_dim;
-    int32_t status = embedding_row(&d->embed, token, d->hidden);
-    if (status) return status;
+    if (audio_row) {
+        memcpy(d->hidden, audio_row, sizeof(float) * hs);
+    } else {
+        int32_t status = embedding_row(&d->embed, token, d->hidden);
+        if (status) return status;
+    }
     uint32_t position = s->position;
     for (uint32_t l = 0; l < c->layers; ++l) {
         layer_mats *m = &d->layers[l];

@@ -160,6 +160,8 @@ void qwref_decoder_destroy(qwref_decoder *decoder);
 int32_t qwref_decoder_prefill_random(qwref_decoder *decoder, uint32_t seq, uint32_t count);
 int32_t qwref_decoder_forward(qwref_decoder *decoder, uint32_t seq, uint32_t token,
                               int32_t want_logits);
+int32_t qwref_decoder_forward_row(qwref_decoder *decoder, uint32_t seq, uint32_t token, const float *audio_row,
+                                  int32_t want_logits);
 const float *qwref_decoder_logits(qwref_decoder *decoder, uint32_t seq);
 uint32_t qwref_decoder_position(qwref_decoder *decoder, uint32_t seq);
 int32_t qwref_decoder_step(qwref_decoder *decoder, uint32_t seq, uint32_t token,

@@ -152,6 +152,7 @@ SIGNATURES = {
     "qwh_decoder_position": (_I32, [_P, _U32, ctypes.POINTER(_U32)]),
     "qwh_decoder_set_position": (_I32, [_P, _U32, _U32]),
     "qwh_decoder_forward": (_I32, [_P, _P, _I32]),
+    "qwh_decoder_forward_rows": (_I32, [_P, _P, _P, _P, _I32]),
     "qwh_decoder_step": (_I32, [_P, _P, _P]),
     "qwh_decoder_generate": (_I32, [_P, _P, _U32, _P]),
     "qwh_decoder_logits": (_I32, [_P, _U32, _P, _U32]),
@@ -510,6 +511,14 @@ class Decoder:
     def forward(self, tokens, want_logits: bool = True) -> None:
         tokens = np.ascontiguousarray(tokens, np.uint32)
         self._check(self.ctx.lib.qwh_decoder_forward(self.handle, _ptr(tokens), int(want_logits)))
+
+    def forward_rows(self, tokens, rows_dev: int, mask=None, want_logits: bool = True) -> None:
+        """forwardToken with audio rows (batch x hidden f32 on the device) in
+        place of the embeddings of the sequences `mask` selects (all if None)."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        m = None if mask is None else np.ascontiguousarray(np.asarray(mask, bool).astype(np.uint8))
+        self._check(self.ctx.lib.qwh_decoder_forward_rows(self.handle, _ptr(tokens), rows_dev,
+                                                          None if m is None else _ptr(m), int(want_logits)))
 
     def step(self, tokens) -> np.ndarray:
         tokens = np.ascontiguousarray(tokens, np.uint32)

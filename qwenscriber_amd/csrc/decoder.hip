@@ -72,24 +72,31 @@ __device__ __forceinline__ float block_sum256(float v, float *lds) {
     return total;
 }
 
-// decoder.zig:346-376 embeddingRow, q4: f32(u - 8) then times the scale.
-// Also copies the RoPE table row of the sequence's position (cos then sin,
-// 2 * half values) to rope_now, so the step's attention kernels read it
-// without first waiting for the position.
+// decoder.zig:346-376 embeddingRow, q4: f32(u - 8) then times the scale;
+// or, for a sequence whose row flag is set, decoder.zig:144-147: the given
+// audio row replaces the embedding. Also copies the RoPE table row of the
+// sequence's position (cos then sin, 2 * half values) to rope_now, so the
+// step's attention kernels read it without first waiting for the position.
 __global__ __launch_bounds__(256) void embed_q4_kernel(const uint32_t *tokens, const uint16_t *scales,
                                                        const uint8_t *data, uint32_t cols, float *hidden,
                                                        const uint32_t *pos, const float *rope_cos,
-                                                       const float *rope_sin, uint32_t half, float *rope_now) {
+                                                       const float *rope_sin, uint32_t half, float *rope_now,
+                                                       const float *rows, const uint32_t *row_flags) {
     const uint32_t b = blockIdx.x;
     if (threadIdx.x < 2 * half) {
         const uint32_t p = pos[b];
         const uint32_t t = threadIdx.x;
         rope_now[(size_t)b * 2 * half + t] = t < half ? rope_cos[(size_t)p * half + t] : rope_sin[(size_t)p * half + t - half];
     }
+    float *out = hidden + (size_t)b * cols;
+    if (row_flags[b]) {
+        const float *src = rows + (size_t)b * cols;
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = src[i];
+        return;
+    }
     const uint32_t token = tokens[b];
     const uint32_t gpr = cols / 64;
     const uint8_t *row = data + (size_t)token * (cols / 2);
-    float *out = hidden + (size_t)b * cols;
     for (uint32_t i = threadIdx.x; i < cols / 2; i += blockDim.x) {
         const uint32_t byte = row[i];
         const float s = dev::f16_bits_to_f32(scales[(size_t)token * gpr + (2 * i) / 64]);
@@ -242,7 +249,9 @@ struct qwh_decoder {
     float *arg_v = nullptr;
     uint32_t *arg_i = nullptr;
     uint32_t arg_parts = 0, arg_per_block = 0;
-    uint32_t *host_stage = nullptr;  // pinned: tokens in / ids out
+    uint32_t *host_stage = nullptr;  // pinned: tokens in / ids out, then the row flags
+    float *rows_dev = nullptr;        // audio rows for the next forward_rows step
+    uint32_t *row_flags_dev = nullptr;  // per sequence: 1 = take rows_dev's row, not the embedding
     std::vector<uint32_t> pos_host;
     std::vector<void *> allocations;
     hipGraphExec_t graph[2] = {nullptr, nullptr};
@@ -351,7 +360,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
     };
     embed_q4_kernel<<<B, 256, 0, s>>>(d->tokens_dev, reinterpret_cast<const uint16_t *>(d->embed.scales),
                                       d->embed.data, c.hidden, d->hidden, d->pos_dev, d->rope_cos, d->rope_sin,
-                                      c.head_dim / 2, d->rope_now);
+                                      c.head_dim / 2, d->rope_now, d->rows_dev, d->row_flags_dev);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
         err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
@@ -608,6 +617,9 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->tokens_dev, 0, 4 * batch, ctx->stream), "state");
     if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->pos_dev, 0, 4 * batch, ctx->stream), "state");
     if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->hist_base_dev, 0, 4 * batch, ctx->stream), "state");
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.hidden, reinterpret_cast<void **>(&d->rows_dev));
+    if (st == QWH_OK) st = dalloc(d, 4 * batch, reinterpret_cast<void **>(&d->row_flags_dev));
+    if (st == QWH_OK) st = check_hip(ctx, hipMemsetAsync(d->row_flags_dev, 0, 4 * batch, ctx->stream), "state");
     d->pos_host.assign(batch, 0);
     // Scratch.
     const uint32_t widest = c.ffn > c.hidden ? (c.ffn > d->qw ? c.ffn : d->qw) : (c.hidden > d->qw ? c.hidden : d->qw);
@@ -645,7 +657,7 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = dalloc(d, 4 * (size_t)batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_i));
     if (st == QWH_OK) {
         void *p = nullptr;
-        st = check_hip(ctx, hipHostMalloc(&p, 4 * (size_t)batch, hipHostMallocDefault), "pinned staging");
+        st = check_hip(ctx, hipHostMalloc(&p, 8 * (size_t)batch, hipHostMallocDefault), "pinned staging");
         d->host_stage = static_cast<uint32_t *>(p);
     }
     if (st == QWH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "decoder create");
@@ -921,6 +933,29 @@ int32_t qwh_decoder_forward(qwh_decoder *d, const uint32_t *tokens, int32_t want
     // The history is written only by generate; park its base past any row.
     QWH_TRY(run_step(d, want_logits != 0));
     QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "forward"));
+    for (uint32_t &p : d->pos_host) p += 1;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_forward_rows(qwh_decoder *d, const uint32_t *tokens, const float *rows_dev,
+                                 const uint8_t *row_mask, int32_t want_logits) {
+    if (!d || !tokens || !rows_dev) return QWH_E_INVALID_ARGUMENT;
+    QWH_TRY(upload_tokens(d, tokens, 1));
+    const uint32_t B = d->batch, H = d->c.hidden;
+    uint32_t *flags = d->host_stage + B;
+    for (uint32_t b = 0; b < B; ++b) {
+        flags[b] = row_mask ? (row_mask[b] != 0) : 1u;
+        if (flags[b])
+            QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->rows_dev + (size_t)b * H, rows_dev + (size_t)b * H,
+                                                     sizeof(float) * H, hipMemcpyDeviceToDevice, d->ctx->stream),
+                              "audio row"));
+    }
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->row_flags_dev, flags, 4 * (size_t)B, hipMemcpyHostToDevice,
+                                             d->ctx->stream), "row flags"));
+    QWH_TRY(run_step(d, want_logits != 0));
+    // Later steps embed their tokens again (outside any captured graph).
+    QWH_TRY(check_hip(d->ctx, hipMemsetAsync(d->row_flags_dev, 0, 4 * (size_t)B, d->ctx->stream), "row flags"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "forward rows"));
     for (uint32_t &p : d->pos_host) p += 1;
     return QWH_OK;
 }

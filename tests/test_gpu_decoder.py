@@ -7,7 +7,7 @@ import pytest
 
 import qwenscriber_amd as qa
 from oracle import oracle as o
-from util import assert_close
+from util import assert_close, normal
 
 pytestmark = pytest.mark.gpu
 o.set_threads(min(16, os.cpu_count() or 1))
@@ -183,3 +183,41 @@ def test_position_limit_and_token_range(ctx):
         assert err.value.status == -7
     finally:
         d.close()
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_audio_rows_replace_embeddings(ctx, batch):
+    # decoder.zig:133-150 / :308-333: projected audio rows spliced into
+    # placeholder positions, mixed with embedded tokens, then greedy steps.
+    seed = 9
+    gpu = qa.Decoder(ctx, batch=batch, **TINY)
+    gpu.init_synthetic(seed)
+    ref = o.Decoder(seed, batch, **TINY)
+    for b in range(batch):
+        gpu.prefill_random(b, 3 + 4 * b, seed)
+        ref.prefill_random(b, 3 + 4 * b)
+    hidden = TINY["hidden"]
+    for step in range(5):
+        rows = normal(batch * hidden, 77, step).reshape(batch, hidden)
+        mask = [(step + b) % 2 == 0 for b in range(batch)]
+        tokens = [(step * 13 + b * 7) % TINY["vocab"] for b in range(batch)]
+        rb = ctx.to_device(rows)
+        gpu.forward_rows(tokens, rb.ptr, mask, True)
+        rb.free()
+        for b in range(batch):
+            if mask[b]:
+                ref.forward_row(b, tokens[b], rows[b], True)
+            else:
+                ref.forward(b, tokens[b], True)
+            assert_close(gpu.logits(b), ref.logits(b), what=f"audio step {step} seq {b}")
+    # Greedy steps after the splice embed their tokens again.
+    tokens = [int(o.argmax(ref.logits(b))) for b in range(batch)]
+    for _ in range(4):
+        got = gpu.step(tokens)
+        want = [ref.step(b, tokens[b]) for b in range(batch)]
+        assert list(got) == want
+        tokens = want
+    for b in range(batch):
+        assert gpu.position(b) == ref.position(b)
+    gpu.close()
+    ref.close()
