@@ -56,25 +56,6 @@ __global__ __launch_bounds__(kNormThreads) void layer_norm_kernel(const float *x
         dst[i] = (row[i] - mean) * inverse_std * weight[i] + bias[i];
 }
 
-// The reference's erf (math.zig:46-60): the Numerical Recipes Chebyshev fit
-// of erfc (`erfcc`), evaluated in f32 by Horner's rule.
-__device__ __forceinline__ float erf_fit(float x) {
-    const float magnitude = fabsf(x);
-    const float t = 1.0f / (1.0f + 0.5f * magnitude);
-    float poly = -0.82215223f + t * 0.17087277f;
-    poly = 1.48851587f + t * poly;
-    poly = -1.13520398f + t * poly;
-    poly = 0.27886807f + t * poly;
-    poly = -0.18628806f + t * poly;
-    poly = 0.09678418f + t * poly;
-    poly = 0.37409196f + t * poly;
-    poly = 1.00002368f + t * poly;
-    const float tau = t * expf(-magnitude * magnitude - 1.26551223f + t * poly);
-    return copysignf(1.0f - tau, x);
-}
-
-__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erf_fit(x * 0.70710678f)); }
-
 // x[t][r] + bias[r], then per mode: stored (addBias), GELU of it stored, or
 // added onto `residual` (x left as it was). `bias` may be null (no bias).
 template <int Mode>
@@ -85,7 +66,7 @@ __global__ __launch_bounds__(256) void bias_epilogue_kernel(float *x, const floa
         float v = x[i];
         if (bias) v += bias[i % rows];
         if constexpr (Mode == kBiasAdd) x[i] = v;
-        if constexpr (Mode == kBiasGelu) x[i] = gelu(v);
+        if constexpr (Mode == kBiasGelu) x[i] = dev::gelu(v);
         if constexpr (Mode == kBiasResidual) residual[i] = residual[i] + v;
     }
 }

@@ -720,9 +720,26 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
     QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->final_norm_weight, w->final_norm_bias, d_model,
                                              steps, eps), "audio final norm"));
     QWH_TRY(qwh_linear(ctx, w->ffn_in, normed, d_model, steps, wide));
-    QWH_TRY(check_hip(ctx, launch_bias_epilogue(s, kBiasGelu, wide, w->ffn_in_bias, nullptr, ffn_dim, steps),
-                      "audio ffn bias + gelu"));
-    QWH_TRY(qwh_linear(ctx, w->ffn_out, wide, ffn_dim, steps, block));
+    const Matrix *ffn_out = find_matrix(ctx, w->ffn_out);
+    if (ffn_out->format == QWH_FORMAT_Q4 && steps >= 2) {
+        // The bias and GELU are applied as ffn_out's activation prep reads
+        // `wide` (one pass and one launch fewer than a separate epilogue).
+        const size_t parts = batch_partial_bytes(steps, *ffn_out);
+        QWH_TRY(ensure_workspace(ctx, ctx->digits, batch_digit_bytes(steps, ffn_dim)));
+        if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
+        GemvInput in;
+        in.mode = GemvInput::F32;
+        in.x = wide;
+        in.gelu_bias = w->ffn_in_bias;
+        QWH_TRY(check_hip(ctx, launch_prep_batch(s, in, steps, ffn_dim, ctx->digits.ptr), "audio ffn prep"));
+        QWH_TRY(check_hip(ctx, launch_gemv_q4_batch(s, ctx->digits.ptr, *ffn_out, steps, block, nullptr, false,
+                                                    static_cast<float *>(ctx->scratch.ptr)),
+                          "audio ffn_out"));
+    } else {
+        QWH_TRY(check_hip(ctx, launch_bias_epilogue(s, kBiasGelu, wide, w->ffn_in_bias, nullptr, ffn_dim, steps),
+                          "audio ffn bias + gelu"));
+        QWH_TRY(qwh_linear(ctx, w->ffn_out, wide, ffn_dim, steps, block));
+    }
     return check_hip(ctx, launch_bias_epilogue(s, kBiasResidual, block, w->ffn_out_bias, encoder_dev, d_model, steps),
                      "audio ffn bias + residual");
 }

@@ -111,6 +111,9 @@ struct GemvInput {
     const float *norm = nullptr;
     float eps = 0.0f;
     bool pairs = false;
+    // launch_prep_batch, F32 mode only: the values it encodes are
+    // gelu(x + bias[col]) (model.zig:866-868) instead of x.
+    const float *gelu_bias = nullptr;
 };
 // True when a q4 matrix of this shape has a kernel for the f32 input forms.
 bool gemv_q4_fused_supported(uint32_t rows, uint32_t cols);

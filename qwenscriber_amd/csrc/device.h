@@ -61,6 +61,25 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v + xor_lane<1>(v);
 }
 
+// The reference's erf (math.zig:46-60): the Numerical Recipes Chebyshev fit
+// of erfc (`erfcc`), evaluated in f32 by Horner's rule.
+__device__ __forceinline__ float erf_fit(float x) {
+    const float magnitude = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.5f * magnitude);
+    float poly = -0.82215223f + t * 0.17087277f;
+    poly = 1.48851587f + t * poly;
+    poly = -1.13520398f + t * poly;
+    poly = 0.27886807f + t * poly;
+    poly = -0.18628806f + t * poly;
+    poly = 0.09678418f + t * poly;
+    poly = 0.37409196f + t * poly;
+    poly = 1.00002368f + t * poly;
+    const float tau = t * expf(-magnitude * magnitude - 1.26551223f + t * poly);
+    return copysignf(1.0f - tau, x);
+}
+
+__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erf_fit(x * 0.70710678f)); }
+
 // Sum over the lanes that differ from this one only in bits below N (N a
 // power of two <= 64): an all-reduce within aligned groups of N lanes.
 template <int N>

@@ -506,7 +506,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, ui
 // split GEMV folded in: RMSNorm of x + their sum (the residual stream,
 // written back), or siluMul of the gate / up sums (math.zig:69-71).
 // ---------------------------------------------------------------------------
-enum class Prep : int { F32 = 0, RmsNorm = 1, Pairs = 2 };
+enum class Prep : int { F32 = 0, RmsNorm = 1, Pairs = 2, BiasGelu = 3 };
 
 constexpr uint32_t kPrepValues = 512;  // values per wavefront
 
@@ -524,6 +524,7 @@ struct PrepArgs {
     uint8_t *digits;
     float *mult;
     float *ss;           // RmsNorm: [token][K / 512] sums of squares
+    const float *bias;   // BiasGelu: per-column bias added before the GELU
 };
 
 __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
@@ -554,6 +555,12 @@ __device__ __forceinline__ void input8(const PrepArgs &a, uint32_t t, uint32_t e
         for (int i = 0; i < 8; ++i) v[i] = silu_mul(f[2 * i], f[2 * i + 1]);
     } else {
         load8(a.x + (size_t)t * a.k + e, v);
+        if constexpr (M == Prep::BiasGelu) {
+            float b[8];
+            load8(a.bias + e, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = dev::gelu(v[i] + b[i]);
+        }
         if (M == Prep::RmsNorm && a.slices) {
             const float *p = a.part + (size_t)t * a.part_n + e;
             const float4 s0 = slice_sum4(p, a.slices, plane);
@@ -658,6 +665,11 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     p.mult = mult_of(digits, tokens, cols);
     p.ss = ss_of(digits, tokens, cols);
     Prep form = in.mode == GemvInput::RmsNorm ? Prep::RmsNorm : Prep::F32;
+    if (in.gelu_bias) {
+        if (in.mode != GemvInput::F32 || (sums && sums->slices)) return hipErrorInvalidValue;
+        p.bias = in.gelu_bias;
+        form = Prep::BiasGelu;
+    }
     if (in.mode != GemvInput::F32 && in.mode != GemvInput::RmsNorm) return hipErrorInvalidValue;
     if (form == Prep::RmsNorm && ss_parts_of(cols) > kTokenTile) return hipErrorInvalidValue;  // K > 8192
     if (sums && sums->slices) {
@@ -678,6 +690,7 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
     case Prep::F32: prep_batch_kernel<Prep::F32><<<grid, 64, 0, s>>>(p); break;
     case Prep::RmsNorm: prep_batch_kernel<Prep::RmsNorm><<<grid, 64, 0, s>>>(p); break;
     case Prep::Pairs: prep_batch_kernel<Prep::Pairs><<<grid, 64, 0, s>>>(p); break;
+    case Prep::BiasGelu: prep_batch_kernel<Prep::BiasGelu><<<grid, 64, 0, s>>>(p); break;
     }
     return hipGetLastError();
 }
