@@ -587,6 +587,11 @@ int32_t check_audio_attention(qwh_ctx *ctx, const AudioAttentionArgs &a) {
     const uintptr_t bits = (uintptr_t)a.out | (uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v |
                            (uintptr_t)a.q_bias | (uintptr_t)a.k_bias | (uintptr_t)a.v_bias;
     if (bits & 15u) return fail(ctx, QWH_E_INVALID_ARGUMENT, "audio attention buffers must be 16-byte aligned");
+    // One workgroup row per window and one layer per head (grid y and z).
+    const uint64_t windows = a.window_steps ? ((uint64_t)a.end - a.first + a.window_steps - 1) / a.window_steps : 0;
+    if (windows > 65535 || a.heads > 65535)
+        return fail(ctx, QWH_E_LIMIT_EXCEEDED, "%llu windows of %u heads: at most 65535 of each",
+                    (unsigned long long)windows, a.heads);
     return QWH_OK;
 }
 

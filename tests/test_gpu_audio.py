@@ -197,3 +197,12 @@ def test_audio_projector(ctx):
     ob = ctx.buffer(steps * hidden * 4)
     ctx.audio_projector(m_in, bi.ptr, m_out, bo.ptr, eb.ptr, steps, ob.ptr)
     assert_close(ob.download(np.float32), expected, rtol=1e-3, atol_rms=1e-3, what="audio projector")
+
+
+def test_audio_attention_rejects_too_many_windows(ctx):
+    # 70000 windows of one step exceed the launch's 65535 window rows: refused
+    # before any device work (the buffers are never read).
+    buf = ctx.buffer(4096)
+    with pytest.raises(qa.QwhError, match="limit_exceeded"):
+        ctx.audio_attention(buf.ptr, 32, buf.ptr, buf.ptr, buf.ptr, 32, 70000, 1, 1, 32)
+    buf.free()
