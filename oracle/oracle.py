@@ -17,6 +17,10 @@ LIB_PATH = os.path.join(HERE, "build", "libqwref.so")
 
 Q4, Q5, Q8 = 16, 17, 18
 GROUP = 64
+# Cache formats (model_config.zig:44-68 CacheFormat).
+CACHE_F32, CACHE_Q8 = 0, 1
+# Norm vector kinds (the library's QWH_T_* values for the same tensors).
+ATTN_NORM, Q_NORM, K_NORM, FFN_NORM, FINAL_NORM = 16, 17, 18, 19, 20
 DATA_BYTES = {Q4: 32, Q5: 40, Q8: 64}
 
 
@@ -97,6 +101,8 @@ _SIGNATURES = {
     "qwref_stream_base": (_U32, [_U32, _U32]),
     "qwref_decoder_create_synthetic": (_P, [ctypes.POINTER(DecoderConfig), _U32, _U32]),
     "qwref_decoder_destroy": (None, [_P]),
+    "qwref_decoder_create_synthetic_as": (_P, [_P, _U32, _U32, _I32, _I32]),
+    "qwref_decoder_set_vector": (_I32, [_P, _U32, _U32, _P, _U32]),
     "qwref_decoder_prefill_random": (_I32, [_P, _U32, _U32]),
     "qwref_decoder_forward": (_I32, [_P, _U32, _U32, _I32]),
     "qwref_decoder_forward_row": (_I32, [_P, _U32, _U32, _P, _I32]),
@@ -305,13 +311,27 @@ def normal(count: int, seed: int, stream: int = 0, scale: float = 1.0) -> np.nda
 
 
 class Decoder:
-    """decoder.zig restatement over a synthetic q4 model with a q8 cache."""
+    """decoder.zig restatement over a synthetic model: every linear in
+    `weight_format` (q4 by default), the cache in `cache_format` (q8 by
+    default), norm weights 1.0 until set_vector replaces them."""
 
-    def __init__(self, seed: int, batch: int = 1, **config):
+    def __init__(self, seed: int, batch: int = 1, weight_format: int = Q4, cache_format: int = CACHE_Q8,
+                 **config):
         self.config = DecoderConfig(**config)
-        self.handle = lib().qwref_decoder_create_synthetic(ctypes.byref(self.config), seed, batch)
+        self.handle = lib().qwref_decoder_create_synthetic_as(ctypes.byref(self.config), seed, batch,
+                                                              weight_format, cache_format)
+        if not self.handle:
+            raise ValueError(f"unsupported formats {weight_format} / {cache_format}")
         self.seed = seed
         self.batch = batch
+        self.weight_format = weight_format
+        self.cache_format = cache_format
+
+    def set_vector(self, kind: int, layer: int, values) -> None:
+        values = np.ascontiguousarray(values, np.float32)
+        status = lib().qwref_decoder_set_vector(self.handle, kind, layer, _ptr(values), values.size)
+        if status != 0:
+            raise ValueError(f"set_vector status {status}")
 
     def close(self):
         if self.handle:

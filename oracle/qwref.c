@@ -813,6 +813,7 @@ void qwref_fill_normal(float *out, uint64_t count, uint32_t seed, uint32_t strea
 /* ------------------------------------------------------------------------ */
 
 typedef struct {
+    int32_t format; /* QWREF_Q4, QWREF_Q5 or QWREF_Q8 */
     uint8_t *scales;
     uint8_t *data;
     uint64_t scales_len;
@@ -823,10 +824,15 @@ typedef struct {
 
 typedef struct {
     qmat q, k, v, o, gate, up, down;
+    /* decoder.zig:165-172, :180-193, :259-265: the layer's four norm weights */
+    float *attention_norm, *q_norm, *k_norm, *ffn_norm;
 } layer_mats;
 
 typedef struct {
-    uint8_t *keys;   /* layers x [max_pos x groups x 2 B scales][max_pos x kv_width codes] */
+    /* q8: layers x [max_pos x groups x 2 B scales][max_pos x kv_width codes]
+     * (decoder.zig:58-65); f32: layers x [max_pos x kv_width] f32
+     * (decoder.zig:77-83). */
+    uint8_t *keys;
     uint8_t *values;
     uint32_t position;
     float *logits;
@@ -836,9 +842,11 @@ struct qwref_decoder {
     qwref_decoder_config c;
     uint32_t seed;
     uint32_t batch;
+    int32_t weight_format;
+    int32_t cache_format; /* QWREF_CACHE_F32 or QWREF_CACHE_Q8 (model_config.zig:44-68) */
     qmat embed, lm_head;
     layer_mats *layers;
-    float *ones_hidden, *ones_head;
+    float *final_norm;
     float *rope_cos, *rope_sin;
     sequence_state *seqs;
     /* scratch, as model.zig:1063-1072 */
@@ -855,11 +863,12 @@ enum {
     STREAM_START_TOKEN = 0x20000, /* + seq */
 };
 
-static int make_qmat(qmat *m, uint32_t rows, uint32_t cols, uint32_t seed, uint32_t stream) {
+static int make_qmat(qmat *m, int32_t format, uint32_t rows, uint32_t cols, uint32_t seed, uint32_t stream) {
+    m->format = format;
     m->rows = rows;
     m->cols = cols;
     m->scales_len = (uint64_t)rows * (cols / QWREF_GROUP) * 2u;
-    m->data_len = (uint64_t)rows * (cols / QWREF_GROUP) * 32u;
+    m->data_len = (uint64_t)rows * (cols / QWREF_GROUP) * (uint64_t)qwref_data_bytes_per_group(format);
     m->scales = (uint8_t *)malloc(m->scales_len);
     m->data = (uint8_t *)malloc(m->data_len);
     float *values = (float *)malloc(sizeof(float) * (size_t)rows * cols);
@@ -868,7 +877,7 @@ static int make_qmat(qmat *m, uint32_t rows, uint32_t cols, uint32_t seed, uint3
         return -1;
     }
     qwref_fill_normal(values, (uint64_t)rows * cols, seed, stream, 0.02f);
-    qwref_quantize_rows(QWREF_Q4, values, rows, cols, m->scales, m->data);
+    qwref_quantize_rows(format, values, rows, cols, m->scales, m->data);
     free(values);
     return 0;
 }
@@ -878,43 +887,69 @@ static void free_qmat(qmat *m) {
     free(m->data);
 }
 
+static float *ones(uint32_t count) {
+    float *v = (float *)malloc(sizeof(float) * count);
+    for (uint32_t i = 0; i < count; ++i) v[i] = 1.0f;
+    return v;
+}
+
 uint32_t qwref_synthetic_start_token(uint32_t seed, uint32_t seq, uint32_t vocab) {
     return qwref_mulberry32_at(qwref_stream_base(seed, STREAM_START_TOKEN + seq), 1) % vocab;
 }
 
 qwref_decoder *qwref_decoder_create_synthetic(const qwref_decoder_config *config, uint32_t seed,
                                               uint32_t batch) {
+    return qwref_decoder_create_synthetic_as(config, seed, batch, QWREF_Q4, QWREF_CACHE_Q8);
+}
+
+qwref_decoder *qwref_decoder_create_synthetic_as(const qwref_decoder_config *config, uint32_t seed,
+                                                 uint32_t batch, int32_t weight_format,
+                                                 int32_t cache_format) {
+    if (qwref_data_bytes_per_group(weight_format) == 0 || weight_format == QWREF_F32) return NULL;
+    if (cache_format != QWREF_CACHE_F32 && cache_format != QWREF_CACHE_Q8) return NULL;
     qwref_decoder *d = (qwref_decoder *)calloc(1, sizeof *d);
     d->c = *config;
     d->seed = seed;
     d->batch = batch;
+    d->weight_format = weight_format;
+    d->cache_format = cache_format;
     const qwref_decoder_config *c = config;
+    int32_t f = weight_format;
     uint32_t qw = c->heads * c->head_dim, kvw = c->kv_heads * c->head_dim;
-    make_qmat(&d->embed, c->vocab, c->hidden, seed, STREAM_EMBED);
-    make_qmat(&d->lm_head, c->vocab, c->hidden, seed, STREAM_LM_HEAD);
+    make_qmat(&d->embed, f, c->vocab, c->hidden, seed, STREAM_EMBED);
+    make_qmat(&d->lm_head, f, c->vocab, c->hidden, seed, STREAM_LM_HEAD);
     d->layers = (layer_mats *)calloc(c->layers, sizeof(layer_mats));
     for (uint32_t l = 0; l < c->layers; ++l) {
         uint32_t s = STREAM_LAYER_BASE + 16 * l;
-        make_qmat(&d->layers[l].q, qw, c->hidden, seed, s + 0);
-        make_qmat(&d->layers[l].k, kvw, c->hidden, seed, s + 1);
-        make_qmat(&d->layers[l].v, kvw, c->hidden, seed, s + 2);
-        make_qmat(&d->layers[l].o, c->hidden, qw, seed, s + 3);
-        make_qmat(&d->layers[l].gate, c->ffn, c->hidden, seed, s + 4);
-        make_qmat(&d->layers[l].up, c->ffn, c->hidden, seed, s + 5);
-        make_qmat(&d->layers[l].down, c->hidden, c->ffn, seed, s + 6);
+        layer_mats *m = &d->layers[l];
+        make_qmat(&m->q, f, qw, c->hidden, seed, s + 0);
+        make_qmat(&m->k, f, kvw, c->hidden, seed, s + 1);
+        make_qmat(&m->v, f, kvw, c->hidden, seed, s + 2);
+        make_qmat(&m->o, f, c->hidden, qw, seed, s + 3);
+        make_qmat(&m->gate, f, c->ffn, c->hidden, seed, s + 4);
+        make_qmat(&m->up, f, c->ffn, c->hidden, seed, s + 5);
+        make_qmat(&m->down, f, c->hidden, c->ffn, seed, s + 6);
+        /* Norm weights start at 1.0; qwref_decoder_set_vector replaces them. */
+        m->attention_norm = ones(c->hidden);
+        m->ffn_norm = ones(c->hidden);
+        m->q_norm = ones(c->head_dim);
+        m->k_norm = ones(c->head_dim);
     }
-    d->ones_hidden = (float *)malloc(sizeof(float) * c->hidden);
-    for (uint32_t i = 0; i < c->hidden; ++i) d->ones_hidden[i] = 1.0f;
-    d->ones_head = (float *)malloc(sizeof(float) * c->head_dim);
-    for (uint32_t i = 0; i < c->head_dim; ++i) d->ones_head[i] = 1.0f;
+    d->final_norm = ones(c->hidden);
     uint32_t half = c->head_dim / 2;
     d->rope_cos = (float *)malloc(sizeof(float) * (size_t)c->max_positions * half);
     d->rope_sin = (float *)malloc(sizeof(float) * (size_t)c->max_positions * half);
     /* model.zig:400-407 */
     qwref_build_rope_tables(d->rope_cos, d->rope_sin, half, c->theta, c->max_positions, half);
-    /* decoder.zig:58-65 `cachePlane` */
-    d->cache_scales = (size_t)c->max_positions * (kvw / QWREF_GROUP) * 2u;
-    d->cache_codes = (size_t)c->max_positions * kvw;
+    if (cache_format == QWREF_CACHE_Q8) {
+        /* decoder.zig:58-65 `cachePlane` */
+        d->cache_scales = (size_t)c->max_positions * (kvw / QWREF_GROUP) * 2u;
+        d->cache_codes = (size_t)c->max_positions * kvw;
+    } else {
+        /* decoder.zig:77-83: one f32 per element, layer stride max_pos * kv_width */
+        d->cache_scales = 0;
+        d->cache_codes = (size_t)c->max_positions * kvw * sizeof(float);
+    }
     d->cache_stride = d->cache_scales + d->cache_codes;
     d->seqs = (sequence_state *)calloc(batch, sizeof(sequence_state));
     for (uint32_t b = 0; b < batch; ++b) {
@@ -941,6 +976,7 @@ void qwref_decoder_destroy(qwref_decoder *d) {
         layer_mats *m = &d->layers[l];
         free_qmat(&m->q); free_qmat(&m->k); free_qmat(&m->v); free_qmat(&m->o);
         free_qmat(&m->gate); free_qmat(&m->up); free_qmat(&m->down);
+        free(m->attention_norm); free(m->ffn_norm); free(m->q_norm); free(m->k_norm);
     }
     free(d->layers);
     for (uint32_t b = 0; b < d->batch; ++b) {
@@ -949,22 +985,52 @@ void qwref_decoder_destroy(qwref_decoder *d) {
         free(d->seqs[b].logits);
     }
     free(d->seqs);
-    free(d->ones_hidden); free(d->ones_head); free(d->rope_cos); free(d->rope_sin);
+    free(d->final_norm); free(d->rope_cos); free(d->rope_sin);
     free(d->hidden); free(d->normed); free(d->query); free(d->key); free(d->value);
     free(d->attention_out); free(d->gate); free(d->up);
     free(d);
 }
 
+int32_t qwref_decoder_set_vector(qwref_decoder *d, uint32_t kind, uint32_t layer, const float *values,
+                                 uint32_t count) {
+    float *dst = NULL;
+    uint32_t expect = 0;
+    if (kind == QWREF_VEC_FINAL_NORM) {
+        dst = d->final_norm;
+        expect = d->c.hidden;
+    } else {
+        if (layer >= d->c.layers) return QWREF_INVALID_ARGUMENT;
+        layer_mats *m = &d->layers[layer];
+        switch (kind) {
+        case QWREF_VEC_ATTENTION_NORM: dst = m->attention_norm; expect = d->c.hidden; break;
+        case QWREF_VEC_Q_NORM: dst = m->q_norm; expect = d->c.head_dim; break;
+        case QWREF_VEC_K_NORM: dst = m->k_norm; expect = d->c.head_dim; break;
+        case QWREF_VEC_FFN_NORM: dst = m->ffn_norm; expect = d->c.hidden; break;
+        default: return QWREF_INVALID_ARGUMENT;
+        }
+    }
+    if (count != expect) return QWREF_SHAPE_MISMATCH;
+    memcpy(dst, values, sizeof(float) * count);
+    return QWREF_OK;
+}
+
 static int32_t apply(const qmat *m, float *out, const float *x) {
-    return qwref_linear_quantized(out, x, QWREF_Q4, m->scales, m->scales_len, m->data, m->data_len,
+    return qwref_linear_quantized(out, x, m->format, m->scales, m->scales_len, m->data, m->data_len,
                                   m->rows, m->cols, 1);
 }
 
-/* decoder.zig:68-106 `appendCacheRow` (q8 branch). */
+/* decoder.zig:68-106 `appendCacheRow`: a copy into the f32 cache
+ * (:77-83), or quantizeRow(.q8) into the q8 planes (:85-105). */
 static void append_cache_row(qwref_decoder *d, sequence_state *s, uint32_t layer, uint32_t position,
                              const float *key, const float *value) {
     uint32_t kvw = d->c.kv_heads * d->c.head_dim;
     size_t layer_offset = (size_t)layer * d->cache_stride;
+    if (d->cache_format == QWREF_CACHE_F32) {
+        size_t offset = layer_offset + (size_t)position * kvw * sizeof(float);
+        memcpy(s->keys + offset, key, sizeof(float) * kvw);
+        memcpy(s->values + offset, value, sizeof(float) * kvw);
+        return;
+    }
     size_t scale_bytes = (size_t)(kvw / QWREF_GROUP) * 2u;
     size_t scale_offset = layer_offset + (size_t)position * scale_bytes;
     size_t code_offset = layer_offset + d->cache_scales + (size_t)position * kvw;
@@ -977,8 +1043,8 @@ int32_t qwref_decoder_prefill_random(qwref_decoder *d, uint32_t seq, uint32_t co
     if (count > d->c.max_positions) return QWREF_LIMIT_EXCEEDED;
     sequence_state *s = &d->seqs[seq];
     uint32_t kvw = d->c.kv_heads * d->c.head_dim;
-    float *rows_k = (float *)malloc(sizeof(float) * (size_t)count * kvw);
-    float *rows_v = (float *)malloc(sizeof(float) * (size_t)count * kvw);
+    float *rows_k = (float *)malloc(sizeof(float) * ((size_t)count * kvw + 1));
+    float *rows_v = (float *)malloc(sizeof(float) * ((size_t)count * kvw + 1));
     for (uint32_t l = 0; l < d->c.layers; ++l) {
         uint32_t stream = STREAM_CACHE_BASE + 0x100 * seq + 2 * l;
         qwref_fill_normal(rows_k, (uint64_t)count * kvw, d->seed, stream, 1.0f);
@@ -992,19 +1058,21 @@ int32_t qwref_decoder_prefill_random(qwref_decoder *d, uint32_t seq, uint32_t co
     return QWREF_OK;
 }
 
-/* decoder.zig:346-376 `embeddingRow` (quantized branch). */
+/* decoder.zig:346-376 `embeddingRow` (quantized branch): the row
+ * dequantized in the matrix's own format. */
 static int32_t embedding_row(const qmat *m, uint32_t row, float *out) {
     if (row >= m->rows) return QWREF_SHAPE_MISMATCH;
     uint32_t gpr = m->cols / QWREF_GROUP;
-    qwref_dequantize_row(QWREF_Q4, m->scales + (size_t)row * gpr * 2, m->data + (size_t)row * gpr * 32,
-                         out, m->cols);
+    size_t data_row = (size_t)gpr * (size_t)qwref_data_bytes_per_group(m->format);
+    qwref_dequantize_row(m->format, m->scales + (size_t)row * gpr * 2, m->data + (size_t)row * data_row, out,
+                         m->cols);
     return QWREF_OK;
 }
 
-/* decoder.zig:133-287 `forwardToken` with the q8 cache. */
-/* decoder.zig:133-150 forwardToken with an audio row: the row replaces the
- * token embedding (the projected audio features spliced into a placeholder
- * position); everything after the embedding is the same step. */
+/* decoder.zig:133-287 `forwardToken`; with an audio row (:133-150) the row
+ * replaces the token embedding (the projected audio features spliced into a
+ * placeholder position) and everything after the embedding is the same
+ * step. */
 int32_t qwref_decoder_forward_row(qwref_decoder *d, uint32_t seq, uint32_t token, const float *audio_row,
                                   int32_t want_logits);
 
@@ -1019,7 +1087,6 @@ int32_t qwref_decoder_forward_row(qwref_decoder *d, uint32_t seq, uint32_t token
     sequence_state *s = &d->seqs[seq];
     if (s->position >= c->max_positions) return QWREF_LIMIT_EXCEEDED;
     uint32_t hs = c->hidden;
-    uint32_t qw = c->heads * c->head_dim, kvw = c->kv_heads * c->head_dim;
     if (audio_row) {
         memcpy(d->hidden, audio_row, sizeof(float) * hs);
     } else {
@@ -1029,16 +1096,16 @@ int32_t qwref_decoder_forward_row(qwref_decoder *d, uint32_t seq, uint32_t token
     uint32_t position = s->position;
     for (uint32_t l = 0; l < c->layers; ++l) {
         layer_mats *m = &d->layers[l];
-        /* :165-172 rmsNormInto (weights are all ones in the synthetic model) */
+        /* :165-172 rmsNormInto(attention_norm) */
         memcpy(d->normed, d->hidden, sizeof(float) * hs);
-        qwref_rms_norm(d->normed, d->ones_hidden, hs, 1, c->eps);
+        qwref_rms_norm(d->normed, m->attention_norm, hs, 1, c->eps);
         /* :174-176 */
         apply(&m->q, d->query, d->normed);
         apply(&m->k, d->key, d->normed);
         apply(&m->v, d->value, d->normed);
-        /* :180-193 per-head norm before the rotation */
-        qwref_rms_norm(d->query, d->ones_head, c->head_dim, c->heads, c->eps);
-        qwref_rms_norm(d->key, d->ones_head, c->head_dim, c->kv_heads, c->eps);
+        /* :180-193 per-head norm (q_norm, k_norm) before the rotation */
+        qwref_rms_norm(d->query, m->q_norm, c->head_dim, c->heads, c->eps);
+        qwref_rms_norm(d->key, m->k_norm, c->head_dim, c->kv_heads, c->eps);
         /* :195-214 */
         qwref_rope_in_place(d->query, &position, 1, c->heads, c->head_dim, d->rope_cos, d->rope_sin,
                             c->head_dim / 2);
@@ -1046,31 +1113,35 @@ int32_t qwref_decoder_forward_row(qwref_decoder *d, uint32_t seq, uint32_t token
                             c->head_dim / 2);
         /* :216 */
         append_cache_row(d, s, l, position, d->key, d->value);
-        /* :239-253 */
+        /* :220-253 */
         size_t lo = (size_t)l * d->cache_stride;
-        qwref_decode_attention_step_q8(d->attention_out, d->query, s->keys + lo,
-                                       s->keys + lo + d->cache_scales, s->values + lo,
-                                       s->values + lo + d->cache_scales, position + 1, c->heads,
-                                       c->kv_heads, c->head_dim);
+        if (d->cache_format == QWREF_CACHE_F32) {
+            qwref_decode_attention_step(d->attention_out, d->query, (const float *)(s->keys + lo),
+                                        (const float *)(s->values + lo), position + 1, c->heads, c->kv_heads,
+                                        c->head_dim);
+        } else {
+            qwref_decode_attention_step_q8(d->attention_out, d->query, s->keys + lo,
+                                           s->keys + lo + d->cache_scales, s->values + lo,
+                                           s->values + lo + d->cache_scales, position + 1, c->heads,
+                                           c->kv_heads, c->head_dim);
+        }
         /* :256-257 */
         apply(&m->o, d->normed, d->attention_out);
         qwref_add_in_place(d->hidden, d->normed, hs);
-        /* :259-271 */
+        /* :259-271 rmsNormInto(ffn_norm) */
         memcpy(d->normed, d->hidden, sizeof(float) * hs);
-        qwref_rms_norm(d->normed, d->ones_hidden, hs, 1, c->eps);
+        qwref_rms_norm(d->normed, m->ffn_norm, hs, 1, c->eps);
         apply(&m->gate, d->gate, d->normed);
         apply(&m->up, d->up, d->normed);
         qwref_silu_mul(d->gate, d->gate, d->up, c->ffn);
         apply(&m->down, d->normed, d->gate);
         qwref_add_in_place(d->hidden, d->normed, hs);
     }
-    (void)qw;
-    (void)kvw;
     s->position += 1;
     if (!want_logits) return QWREF_OK;
-    /* :277-286 */
+    /* :277-286 rmsNormInto(final norm), output projection */
     memcpy(d->normed, d->hidden, sizeof(float) * hs);
-    qwref_rms_norm(d->normed, d->ones_hidden, hs, 1, c->eps);
+    qwref_rms_norm(d->normed, d->final_norm, hs, 1, c->eps);
     apply(&d->lm_head, s->logits, d->normed);
     return QWREF_OK;
 }

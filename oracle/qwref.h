@@ -28,8 +28,11 @@
  *                    f64 numpy layer norm and windowed attention brute force,
  *                    kernels.zig:1043-1078 windowed-attention known answers.
  *   audio layer      composition of the pinned parts (no reference-held vectors).
- *   decoder step     composition of the pinned parts; no reference-held vectors
- *                    exist for random weights (parity unpinned end to end).
+ *   decoder step     composition of the pinned parts (q4 / q5 / q8 weights,
+ *                    f32 / q8 cache, non-unit norm weights) checked against an
+ *                    independent float64 restatement; no reference-held
+ *                    vectors exist for random weights (parity unpinned end to
+ *                    end beyond that composition).
  *   transcendentals  expf/powf/sinf/cosf are glibc's, not Zig compiler_rt's:
  *                    parity unpinned at the last ulp (tolerance-pinned only).
  */
@@ -150,13 +153,37 @@ typedef struct {
 
 typedef struct qwref_decoder qwref_decoder;
 
+/* Cache formats: model_config.zig:44-68 CacheFormat values. */
+enum { QWREF_CACHE_F32 = 0, QWREF_CACHE_Q8 = 1 };
+/* Norm weight vectors a decoder holds (decoder.zig:165-172, :180-193,
+ * :259-265, :277-284); the values are the library's tensor kinds. */
+enum {
+    QWREF_VEC_ATTENTION_NORM = 16,
+    QWREF_VEC_Q_NORM = 17,
+    QWREF_VEC_K_NORM = 18,
+    QWREF_VEC_FFN_NORM = 19,
+    QWREF_VEC_FINAL_NORM = 20,
+};
+
 /* Builds a decoder whose every linear is q4, from the synthetic generator
- * (seed, stream ids documented in qwref.c), norm weights all 1.0. */
+ * (seed, stream ids documented in qwref.c), norm weights all 1.0, q8 cache. */
 qwref_decoder *qwref_decoder_create_synthetic(const qwref_decoder_config *config, uint32_t seed,
                                               uint32_t batch);
+/* The same synthetic values with every linear (and the embedding) quantized
+ * to `weight_format` (q4, q5 or q8), and the key/value cache in
+ * `cache_format`. NULL for an unknown format. */
+qwref_decoder *qwref_decoder_create_synthetic_as(const qwref_decoder_config *config, uint32_t seed,
+                                                 uint32_t batch, int32_t weight_format,
+                                                 int32_t cache_format);
 void qwref_decoder_destroy(qwref_decoder *decoder);
-/* Fills positions [0, count) of every layer's q8 cache of sequence `seq` from
- * the generator, as quantizeRow(.q8) of N(0,1) rows, and sets its position. */
+/* Replaces one norm weight vector (kind QWREF_VEC_*, layer ignored for the
+ * final norm); count must be hidden (attention, ffn, final) or head_dim
+ * (q, k). */
+int32_t qwref_decoder_set_vector(qwref_decoder *decoder, uint32_t kind, uint32_t layer,
+                                 const float *values, uint32_t count);
+/* Fills positions [0, count) of every layer's cache of sequence `seq` from
+ * the generator (N(0,1) rows, stored as f32 or as quantizeRow(.q8)), and
+ * sets its position. */
 int32_t qwref_decoder_prefill_random(qwref_decoder *decoder, uint32_t seq, uint32_t count);
 int32_t qwref_decoder_forward(qwref_decoder *decoder, uint32_t seq, uint32_t token,
                               int32_t want_logits);

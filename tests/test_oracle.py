@@ -366,6 +366,23 @@ def test_math_known_answers():
     assert abs(out[1] - o.silu(1.0) * 2) <= 1e-6 and abs(out[2] - o.silu(-1.0) * 3) <= 1e-6
 
 
+def test_rms_norm_applies_each_weight_to_its_own_element():
+    # math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w. A row of +-1 has
+    # mean square exactly 1, so with eps 0 the output is x_i * w_i exactly:
+    # distinct weights catch a dropped, shifted or reversed weight index.
+    x = np.array([1, -1, -1, 1, 1, 1, -1, 1], np.float32)
+    w = np.arange(1, 9, dtype=np.float32) * np.float32(0.25) + np.float32(0.5)
+    assert np.array_equal(o.rms_norm(x, w, 8, 0.0), x * w)
+    # Several rows (tokens): each row normalized by its own statistics, the
+    # same weight vector for every row; against float64.
+    rows = normal(3 * 64, 5).reshape(3, 64) * np.array([[0.1], [1.0], [7.0]], np.float32)
+    wv = 1.0 + 0.5 * normal(64, 6)
+    got = o.rms_norm(rows.reshape(-1), wv, 64, 1e-6).reshape(3, 64)
+    r64 = rows.astype(np.float64)
+    want = r64 / np.sqrt(np.mean(r64 * r64, axis=1, keepdims=True) + 1e-6) * wv.astype(np.float64)
+    assert np.allclose(got, want, rtol=2e-6, atol=0)
+
+
 def test_rope_rotation_and_frequencies():
     # kernels.zig:1080-1117
     cos, sin = o.rope_tables(2, 1e6, 8)
@@ -429,15 +446,15 @@ TINY = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, ffn=512, vo
             max_positions=64, eps=1e-6, theta=1e6)
 
 
-def _tiny_weights(seed):
+def _tiny_weights(seed, fmt=o.Q4):
     """The oracle's synthetic model, rebuilt through the public generator and
     quantizer (same stream ids), dequantized to f64."""
     c = TINY
     qw, kvw = c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
 
     def mat(rows, cols, stream):
-        s, d = o.quantize_rows(o.Q4, o.normal(rows * cols, seed, stream, 0.02).reshape(rows, cols))
-        return o.dequantize_rows(o.Q4, s, d, rows, cols).astype(np.float64)
+        s, d = o.quantize_rows(fmt, o.normal(rows * cols, seed, stream, 0.02).reshape(rows, cols))
+        return o.dequantize_rows(fmt, s, d, rows, cols).astype(np.float64)
 
     w = {"embed": mat(c["vocab"], c["hidden"], 1), "lm_head": mat(c["vocab"], c["hidden"], 2), "layers": []}
     for layer in range(c["layers"]):
@@ -449,15 +466,46 @@ def _tiny_weights(seed):
     return w
 
 
-def _forward_f64(w, tokens, c):
-    """decoder.zig:133-287 in f64 with an f64 cache (no q8): the composition
-    the oracle must follow, written independently."""
+def _random_norms(c, seed):
+    """Norm weight vectors with distinct entries around 1 (a real checkpoint's
+    learned norms are of this kind): per layer attention, q, k, ffn, and the
+    final norm."""
+    out = {"final": 1.0 + 0.5 * o.normal(c["hidden"], seed, 900)}
+    for layer in range(c["layers"]):
+        out[layer] = dict(attn=1.0 + 0.5 * o.normal(c["hidden"], seed, 901 + 8 * layer),
+                          q=1.0 + 0.5 * o.normal(c["head_dim"], seed, 902 + 8 * layer),
+                          k=1.0 + 0.5 * o.normal(c["head_dim"], seed, 903 + 8 * layer),
+                          ffn=1.0 + 0.5 * o.normal(c["hidden"], seed, 904 + 8 * layer))
+    return out
+
+
+def _set_norms(dec, norms, layers):
+    dec.set_vector(o.FINAL_NORM, 0, norms["final"])
+    for layer in range(layers):
+        n = norms[layer]
+        dec.set_vector(o.ATTN_NORM, layer, n["attn"])
+        dec.set_vector(o.Q_NORM, layer, n["q"])
+        dec.set_vector(o.K_NORM, layer, n["k"])
+        dec.set_vector(o.FFN_NORM, layer, n["ffn"])
+
+
+def _forward_f64(w, tokens, c, norms=None, cache="q8"):
+    """decoder.zig:133-287 in f64 (no rounding but the cache's): the
+    composition the oracle must follow, written independently. With
+    `norms`, every RMSNorm multiplies by its weight vector; `cache` "q8"
+    stores quantizeRow(.q8) of each new key / value row, "f32" stores the f32
+    rows."""
     hd, heads, kvh = c["head_dim"], c["heads"], c["kv_heads"]
     half = hd // 2
     inv = np.array([c["theta"] ** (-2 * i / hd) for i in range(half)])
 
-    def rms(x, eps=c["eps"]):
-        return x / np.sqrt(np.mean(x * x) + eps)
+    def weight(layer, name, size):
+        if norms is None:
+            return np.ones(size)
+        return np.asarray(norms["final"] if layer is None else norms[layer][name], np.float64)
+
+    def rms(x, wv, eps=c["eps"]):
+        return x / np.sqrt(np.mean(x * x) + eps) * wv
 
     def rope(x, p):
         x = x.reshape(-1, hd).copy()
@@ -472,14 +520,18 @@ def _forward_f64(w, tokens, c):
     for p, t in enumerate(tokens):
         h = w["embed"][t].copy()
         for layer, L in enumerate(w["layers"]):
-            n = rms(h)
-            q = rope(np.stack([rms(r) for r in (L["q"] @ n).reshape(heads, hd)]).reshape(-1), p)
-            k = rope(np.stack([rms(r) for r in (L["k"] @ n).reshape(kvh, hd)]).reshape(-1), p).reshape(-1)
+            n = rms(h, weight(layer, "attn", c["hidden"]))
+            wq, wk = weight(layer, "q", hd), weight(layer, "k", hd)
+            q = rope(np.stack([rms(r, wq) for r in (L["q"] @ n).reshape(heads, hd)]).reshape(-1), p)
+            k = rope(np.stack([rms(r, wk) for r in (L["k"] @ n).reshape(kvh, hd)]).reshape(-1), p).reshape(-1)
             v = (L["v"] @ n).reshape(kvh, hd)
-            # appendCacheRow stores q8 of the f32 rows (decoder.zig:94-105).
             for store, row in ((caches[layer][0], k), (caches[layer][1], v.reshape(-1))):
-                rs, rd = o.quantize_rows(o.Q8, row.astype(np.float32).reshape(1, -1))
-                store.append(o.dequantize_rows(o.Q8, rs, rd, 1, row.size).astype(np.float64).reshape(kvh, hd))
+                row32 = row.astype(np.float32).reshape(1, -1)
+                if cache == "q8":
+                    # appendCacheRow stores q8 of the f32 rows (decoder.zig:94-105).
+                    rs, rd = o.quantize_rows(o.Q8, row32)
+                    row32 = o.dequantize_rows(o.Q8, rs, rd, 1, row.size)
+                store.append(row32.astype(np.float64).reshape(kvh, hd))
             K = np.stack(caches[layer][0])
             V = np.stack(caches[layer][1])
             att = np.zeros((heads, hd))
@@ -489,29 +541,64 @@ def _forward_f64(w, tokens, c):
                 pr = np.exp(sc - sc.max())
                 att[hh] = (pr / pr.sum()) @ V[:, g]
             h = h + L["o"] @ att.reshape(-1)
-            n = rms(h)
+            n = rms(h, weight(layer, "ffn", c["hidden"]))
             g_ = L["gate"] @ n
             h = h + L["down"] @ (g_ / (1 + np.exp(-g_)) * (L["up"] @ n))
-        logits.append(w["lm_head"] @ rms(h))
+        logits.append(w["lm_head"] @ rms(h, weight(None, "final", c["hidden"])))
     return logits
 
 
-def test_decoder_composition_against_f64_restatement():
+@pytest.mark.parametrize("fmt,cache,with_norms", [
+    (o.Q4, o.CACHE_Q8, False),
+    (o.Q4, o.CACHE_Q8, True),
+    (o.Q8, o.CACHE_Q8, True),
+    (o.Q5, o.CACHE_F32, True),
+    (o.Q4, o.CACHE_F32, False),
+])
+def test_decoder_composition_against_f64_restatement(fmt, cache, with_norms):
     seed = 9
-    w = _tiny_weights(seed)
+    w = _tiny_weights(seed, fmt)
+    norms = _random_norms(TINY, 31) if with_norms else None
     tokens = [5, 977, 123, 42]
-    expected = _forward_f64(w, tokens, TINY)
-    dec = o.Decoder(seed, 1, **TINY)
+    expected = _forward_f64(w, tokens, TINY, norms, "q8" if cache == o.CACHE_Q8 else "f32")
+    dec = o.Decoder(seed, 1, fmt, cache, **TINY)
     try:
+        if norms is not None:
+            _set_norms(dec, norms, TINY["layers"])
         for i, t in enumerate(tokens):
             dec.forward(0, t, True)
             got = dec.logits(0)
-            # Both sides store the cache as q8; what remains is f32 rounding
+            # Both sides store the same cache; what remains is f32 rounding
             # (and, rarely, a q8 code that an f32-vs-f64 difference flips).
             assert np.max(np.abs(got - expected[i])) < 2e-4 * max(1.0, np.abs(expected[i]).max()), i
         assert dec.position(0) == len(tokens)
     finally:
         dec.close()
+
+
+def test_decoder_norm_weights_change_the_result():
+    # A norm vector that is set must reach the step: each of the five kinds,
+    # changed alone, changes the logits (a dropped weight would not).
+    seed = 9
+    # (A prefilled cache: with one position the softmax weight is 1 whatever
+    # the query, so the q norm could not show.)
+    base = o.Decoder(seed, 1, **TINY)
+    base.prefill_random(0, 6)
+    base.forward(0, 5, True)
+    ref = base.logits(0)
+    base.close()
+    for kind, size in ((o.ATTN_NORM, TINY["hidden"]), (o.Q_NORM, TINY["head_dim"]), (o.K_NORM, TINY["head_dim"]),
+                       (o.FFN_NORM, TINY["hidden"]), (o.FINAL_NORM, TINY["hidden"])):
+        dec = o.Decoder(seed, 1, **TINY)
+        try:
+            dec.set_vector(kind, 1, 1.0 + 0.5 * o.normal(size, 3, kind))
+            dec.prefill_random(0, 6)
+            dec.forward(0, 5, True)
+            assert np.max(np.abs(dec.logits(0) - ref)) > 1e-3, kind
+            with pytest.raises(ValueError):
+                dec.set_vector(kind, 0, np.ones(size + 1, np.float32))
+        finally:
+            dec.close()
 
 
 def test_decoder_step_argmax_and_position_limit():
