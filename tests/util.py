@@ -43,3 +43,33 @@ def lcg_values(count: int, state: int, divisor: float):
         state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
         out[i] = np.float32(((state >> 9) % 2001) - 1000) / np.float32(divisor)
     return out, state
+
+
+# Norm vector kinds (QWH_T_* / the oracle's QWREF_VEC_*).
+ATTN_NORM, Q_NORM, K_NORM, FFN_NORM, FINAL_NORM = 16, 17, 18, 19, 20
+
+
+def random_norms(config: dict, seed: int) -> dict:
+    """Norm weight vectors with distinct entries around 1, as a real
+    checkpoint's learned RMSNorm weights: per layer attention, q, k and ffn,
+    plus the final norm."""
+    hidden, head_dim = config["hidden"], config["head_dim"]
+    out = {"final": 1.0 + 0.5 * normal(hidden, seed, 900)}
+    for layer in range(config["layers"]):
+        out[layer] = dict(attn=1.0 + 0.5 * normal(hidden, seed, 901 + 8 * layer),
+                          q=1.0 + 0.5 * normal(head_dim, seed, 902 + 8 * layer),
+                          k=1.0 + 0.5 * normal(head_dim, seed, 903 + 8 * layer),
+                          ffn=1.0 + 0.5 * normal(hidden, seed, 904 + 8 * layer))
+    return out
+
+
+def set_norms(decoder, norms: dict, layers: int) -> None:
+    """Binds random_norms() vectors on an oracle or a device decoder (both
+    take set_vector(kind, layer, values))."""
+    decoder.set_vector(FINAL_NORM, 0, norms["final"])
+    for layer in range(layers):
+        n = norms[layer]
+        decoder.set_vector(ATTN_NORM, layer, n["attn"])
+        decoder.set_vector(Q_NORM, layer, n["q"])
+        decoder.set_vector(K_NORM, layer, n["k"])
+        decoder.set_vector(FFN_NORM, layer, n["ffn"])
