@@ -232,6 +232,16 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
                                 uint32_t head_dim, uint32_t batch, uint64_t scale_stride_bytes,
                                 uint64_t code_stride_bytes);
 
+/* kernels.zig:572-627 decodeAttentionStep over an f32 cache (the reference's
+ * default cache, model_config.zig:44-68): keys_dev / values_dev are
+ * [positions][kv_heads*head_dim] f32 (decoder.zig:77-83), `cached` positions
+ * read; `batch` sequences back to back, query and out advancing by
+ * heads*head_dim floats, keys and values by `stride_bytes`. Built for
+ * head_dim 64, 128, 256 (else QWH_E_UNSUPPORTED). */
+int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *query_dev, const float *keys_dev,
+                                 const float *values_dev, uint32_t cached, uint32_t heads, uint32_t kv_heads,
+                                 uint32_t head_dim, uint32_t batch, uint64_t stride_bytes);
+
 /* decoder.zig:68-106 appendCacheRow (q8): quantizes one key row and one value
  * row of kv_width f32 values into row `position` of a layer's planes, bit
  * exact with quant.quantizeRow(.q8). */
@@ -333,17 +343,33 @@ typedef struct {
 
 typedef struct qwh_decoder qwh_decoder;
 
+/* Key/value cache formats: model_config.zig:44-68 CacheFormat values. */
+#define QWH_CACHE_F32 0u
+#define QWH_CACHE_Q8 1u
+
 /* Creates a decoder for `batch` independent sequences, each with its own q8
  * key/value cache of config->max_positions positions (decoder.zig:58-65
  * layout, per layer [scales][codes]). RoPE tables are built on the host by
- * kernels.zig:534-564 (buildRopeTables) semantics, as model.zig:400-407 does. */
+ * kernels.zig:534-564 (buildRopeTables) semantics, as model.zig:400-407 does.
+ * Every matrix starts as a zero q4 matrix; bind them with
+ * qwh_decoder_set_matrix, qwh_decoder_bind_shard or qwh_decoder_init_synthetic. */
 int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch,
                            qwh_decoder **out);
+/* qwh_decoder_create with the cache in `cache_format` (model.zig's
+ * cache_format, chosen by transcribe.zig's --cache f32|q8):
+ * QWH_CACHE_F32 keeps per layer [max_positions][kv_heads * head_dim] f32 keys
+ * and values (decoder.zig:77-83) and attends with decodeAttentionStep
+ * (kernels.zig:572-627); QWH_CACHE_Q8 is qwh_decoder_create's cache. */
+int32_t qwh_decoder_create_cache(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch,
+                                 uint32_t cache_format, qwh_decoder **out);
 int32_t qwh_decoder_destroy(qwh_decoder *decoder);
-/* Binds a quantized matrix (QWH_T_EMBED..QWH_T_LM_HEAD). The decoder copies
- * the q/k/v planes into one fused row block and the gate/up planes into one
- * matrix with their rows interleaved (gate row j, then up row j); the others
- * are borrowed.
+/* Binds a quantized matrix (QWH_T_EMBED..QWH_T_LM_HEAD) in q4, q5 or q8:
+ * each matrix is applied in its own format, as Matrix.apply applies whatever
+ * storage it holds (kernels.zig:182-206). The decoder copies the planes into
+ * its own blocks: q / k / v into one fused row block and gate / up into one
+ * block with their rows interleaved (gate row j, then up row j). A fused
+ * block holds one format, so binding a member in another format re-creates
+ * the block (zeroed) and its other members are bound again after it.
  * Layer is ignored for EMBED and LM_HEAD. */
 int32_t qwh_decoder_set_matrix(qwh_decoder *decoder, uint32_t kind, uint32_t layer,
                                uint64_t matrix);
@@ -353,8 +379,9 @@ int32_t qwh_decoder_set_vector(qwh_decoder *decoder, uint32_t kind, uint32_t lay
 /* Binds every decoder tensor a loaded `.qw` shard holds (qwh_shard_load):
  * container.TensorKind 30..43 (container.zig:367-380) at layer 0 (embedding,
  * final norm, output projection) and layers 1..layers (the decoder's layer
- * L - 1); other kinds (audio tower, projector) are skipped. Matrices must
- * be q4 and are copied (the shard may be released afterwards); norm vectors
+ * L - 1); other kinds (audio tower, projector) are skipped. Matrices may be
+ * q4, q5 or q8 (the converter writes one format for all, layout.zig:49-53)
+ * and are copied (the shard may be released afterwards); norm vectors
  * may be f32, f16 or bf16 and are widened to f32. With
  * QWH_BIND_OUTPUT_TIED (config.bin flags bit 0, model_config.zig) the
  * embedding is also bound as the output projection. A model split over
@@ -363,16 +390,21 @@ int32_t qwh_decoder_set_vector(qwh_decoder *decoder, uint32_t kind, uint32_t lay
 #define QWH_BIND_OUTPUT_TIED 1u
 int32_t qwh_decoder_bind_shard(qwh_decoder *decoder, uint64_t shard, uint32_t flags, uint32_t *bound);
 /* Binds every matrix from the synthetic generator: each linear q4 with
- * values f32(N(0,1)) * 0.02, stream ids as the oracle's synthetic model,
- * all norm weights 1.0. */
+ * values f32(N(0,1)) * 0.02, stream ids as the oracle's synthetic model.
+ * Norm weights are left as they are (1.0 unless set). */
 int32_t qwh_decoder_init_synthetic(qwh_decoder *decoder, uint32_t seed);
+/* The same synthetic values quantized to `format` (q4, q5 or q8) for every
+ * matrix, the embedding included. */
+int32_t qwh_decoder_init_synthetic_format(qwh_decoder *decoder, uint32_t seed, int32_t format);
 /* decoder.zig:109-121 reset: zeroes every cache and sets positions to 0. */
 int32_t qwh_decoder_reset(qwh_decoder *decoder);
 /* Fills positions [0, count) of sequence `seq`'s caches with quantizeRow(.q8)
  * of synthetic N(0,1) rows and sets its position to `count`. */
 int32_t qwh_decoder_prefill_random(qwh_decoder *decoder, uint32_t seq, uint32_t count,
                                    uint32_t seed);
-/* Device addresses of sequence `seq`, layer `layer`'s cache planes. */
+/* Device addresses of sequence `seq`, layer `layer`'s cache planes (with an
+ * f32 cache the scale planes are NULL and the code planes hold the f32
+ * rows). */
 int32_t qwh_decoder_cache_planes(qwh_decoder *decoder, uint32_t seq, uint32_t layer,
                                  void **k_scales, void **k_codes, void **v_scales,
                                  void **v_codes);
@@ -397,6 +429,21 @@ int32_t qwh_decoder_step(qwh_decoder *decoder, const uint32_t *tokens, uint32_t 
  * steps x batch ids, step major. */
 int32_t qwh_decoder_generate(qwh_decoder *decoder, const uint32_t *tokens, uint32_t steps,
                              uint32_t *ids_out);
+/* Greedy decoding with the stop rules of wasm/model.zig:423-451 decodeStep
+ * (and :495-499 endsSequence), entirely on the device: tokens[b] is sequence
+ * b's next token (the prediction of its last prompt position). Per
+ * sequence, while it has not finished: a token among stop_tokens (at most 3:
+ * token_eos_primary, token_eos_secondary, token_endoftext) ends it and is not
+ * emitted; otherwise the token is emitted, and once max_tokens ids are out
+ * the sequence ends without another prediction; otherwise step() predicts
+ * the next token. A finished sequence is frozen (its position no longer
+ * advances) while the others continue. ids_out receives max_tokens x batch
+ * ids, step major (rows past a sequence's count are 0); counts_out[b] the
+ * number of ids sequence b emitted. Positions advance by the forwards each
+ * sequence ran. */
+int32_t qwh_decoder_generate_until(qwh_decoder *decoder, const uint32_t *tokens, uint32_t max_tokens,
+                                   const uint32_t *stop_tokens, uint32_t stop_count, uint32_t *ids_out,
+                                   uint32_t *counts_out);
 /* Copies sequence `seq`'s last logits (vocab f32) to the host. */
 int32_t qwh_decoder_logits(qwh_decoder *decoder, uint32_t seq, float *out, uint32_t count);
 

@@ -8,6 +8,8 @@ binding fails loudly when the library is not built -- there is no CPU path.
 from __future__ import annotations
 
 from ._lib import (  # noqa: F401
+    CACHE_F32,
+    CACHE_Q8,
     DATA_BYTES,
     FORMAT_Q4,
     FORMAT_Q5,
@@ -20,6 +22,20 @@ from ._lib import (  # noqa: F401
     DeviceBuffer,
     ModelConfig,
     QwhError,
+    T_ATTN_NORM,
+    T_DOWN,
+    T_EMBED,
+    T_FFN_NORM,
+    T_FINAL_NORM,
+    T_GATE,
+    T_K,
+    T_K_NORM,
+    T_LM_HEAD,
+    T_O,
+    T_Q,
+    T_Q_NORM,
+    T_UP,
+    T_V,
     TensorEntry,
     config_decoder,
     config_parse,

@@ -20,6 +20,7 @@ DATA_BYTES = {FORMAT_Q4: 32, FORMAT_Q5: 40, FORMAT_Q8: 64}
 
 T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(9)
 T_ATTN_NORM, T_Q_NORM, T_K_NORM, T_FFN_NORM, T_FINAL_NORM = 16, 17, 18, 19, 20
+CACHE_F32, CACHE_Q8 = 0, 1
 
 class AudioLayerWeights(ctypes.Structure):
     """qwh_audio_layer_weights (model.zig AudioLayer): matrix handles and
@@ -142,6 +143,10 @@ SIGNATURES = {
     "qwh_audio_layer": (_I32, [_P, ctypes.POINTER(AudioLayerWeights), _P, _U32, _U32, _U32, _U32, _U32, _F]),
     "qwh_audio_projector": (_I32, [_P, _U64, _P, _U64, _P, _P, _U32, _P]),
     "qwh_decoder_create": (_I32, [_P, ctypes.POINTER(DecoderConfig), _U32, _PP]),
+    "qwh_decoder_create_cache": (_I32, [_P, ctypes.POINTER(DecoderConfig), _U32, _U32, _PP]),
+    "qwh_decoder_init_synthetic_format": (_I32, [_P, _U32, _I32]),
+    "qwh_decoder_generate_until": (_I32, [_P, _P, _U32, _P, _U32, _P, _P]),
+    "qwh_decode_attention_f32": (_I32, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U64]),
     "qwh_decoder_destroy": (_I32, [_P]),
     "qwh_decoder_set_matrix": (_I32, [_P, _U32, _U32, _U64]),
     "qwh_decoder_set_vector": (_I32, [_P, _U32, _U32, _P, _U32]),
@@ -444,6 +449,11 @@ class Context:
         self._check(self.lib.qwh_synth_normal(self.handle, seed, stream, count, scale, out_dev))
 
     # -- attention ----------------------------------------------------------
+    def decode_attention_f32(self, out_dev, query_dev, keys_dev, values_dev, cached, heads, kv_heads, head_dim,
+                             batch=1, stride=0):
+        self._check(self.lib.qwh_decode_attention_f32(self.handle, out_dev, query_dev, keys_dev, values_dev, cached,
+                                                      heads, kv_heads, head_dim, batch, stride))
+
     def decode_attention_q8(self, out_dev, query_dev, k_scales, k_codes, v_scales, v_codes, cached, heads,
                             kv_heads, head_dim, batch=1, scale_stride=0, code_stride=0) -> None:
         self._check(self.lib.qwh_decode_attention_q8(self.handle, out_dev, query_dev, k_scales, k_codes, v_scales,
@@ -456,14 +466,17 @@ class Context:
 
 
 class Decoder:
-    """decoder.zig Decoder over `batch` sequences (qwh_decoder_*)."""
+    """decoder.zig Decoder over `batch` sequences (qwh_decoder_*), with a q8
+    (CACHE_Q8, the default here) or f32 (CACHE_F32) key/value cache."""
 
-    def __init__(self, ctx: Context, batch: int = 1, **config):
+    def __init__(self, ctx: Context, batch: int = 1, cache_format: int = CACHE_Q8, **config):
         self.ctx = ctx
         self.config = DecoderConfig(**config)
         self.batch = batch
+        self.cache_format = cache_format
         out = ctypes.c_void_p()
-        ctx._check(ctx.lib.qwh_decoder_create(ctx.handle, ctypes.byref(self.config), batch, ctypes.byref(out)))
+        ctx._check(ctx.lib.qwh_decoder_create_cache(ctx.handle, ctypes.byref(self.config), batch, cache_format,
+                                                    ctypes.byref(out)))
         self.handle = out.value
 
     def close(self) -> None:
@@ -486,8 +499,8 @@ class Decoder:
         self._check(self.ctx.lib.qwh_decoder_bind_shard(self.handle, shard, 1 if output_tied else 0, ctypes.byref(bound)))
         return bound.value
 
-    def init_synthetic(self, seed: int) -> None:
-        self._check(self.ctx.lib.qwh_decoder_init_synthetic(self.handle, seed))
+    def init_synthetic(self, seed: int, fmt: int = FORMAT_Q4) -> None:
+        self._check(self.ctx.lib.qwh_decoder_init_synthetic_format(self.handle, seed, fmt))
 
     def reset(self) -> None:
         self._check(self.ctx.lib.qwh_decoder_reset(self.handle))
@@ -531,6 +544,16 @@ class Decoder:
         out = np.zeros(steps * self.batch, np.uint32)
         self._check(self.ctx.lib.qwh_decoder_generate(self.handle, _ptr(tokens), steps, _ptr(out)))
         return out.reshape(steps, self.batch)
+
+    def generate_until(self, tokens, max_tokens: int, stop_tokens=()):
+        """qwh_decoder_generate_until: (ids [max_tokens x batch], counts [batch])."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        stops = np.ascontiguousarray(list(stop_tokens) or [0], np.uint32)
+        ids = np.zeros(max(1, max_tokens) * self.batch, np.uint32)
+        counts = np.zeros(self.batch, np.uint32)
+        self._check(self.ctx.lib.qwh_decoder_generate_until(self.handle, _ptr(tokens), max_tokens, _ptr(stops),
+                                                            len(stop_tokens), _ptr(ids), _ptr(counts)))
+        return ids[: max_tokens * self.batch].reshape(max_tokens, self.batch), counts
 
     def logits(self, seq: int) -> np.ndarray:
         out = np.zeros(self.config.vocab, np.float32)

@@ -124,6 +124,61 @@ struct SoftmaxState {
     float m[R], l[R], acc[R][16];
 };
 
+// Online-softmax update by a block of NB scores per query head: the running
+// maximum, the rescaled running sum and accumulator; w receives the block's
+// weights exp2(score - max) (0 for invalid positions).
+template <int R, int NB>
+__device__ __forceinline__ void softmax_update(SoftmaxState<R> &st, const float (&score)[NB][R], const bool (&valid)[NB],
+                                               float (&w)[NB][R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float bm = score[0][r];
+#pragma unroll
+        for (int nb = 1; nb < NB; ++nb) bm = fmaxf(bm, score[nb][r]);
+        const float m_new = fmaxf(st.m[r], bm);
+        const float alpha = fast_exp2(st.m[r] - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            w[nb][r] = valid[nb] ? fast_exp2(score[nb][r] - m_new) : 0.0f;
+            sum += w[nb][r];
+        }
+        st.l[r] = st.l[r] * alpha + sum;
+        st.m[r] = m_new;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.acc[r][i] *= alpha;
+    }
+}
+
+// f32 cache (kernels.zig:572-627 decodeAttentionStep): scores q . k per
+// position over the LPP lanes of a lane group, values accumulated as they
+// are.
+template <int D, int R, int NB>
+__device__ __forceinline__ void attend_f32(SoftmaxState<R> &st, const float (&q)[R][16], const float (&k)[NB][16],
+                                           const float (&v)[NB][16], const bool (&valid)[NB], float scaling) {
+    constexpr int LPP = D / 16;
+    float score[NB][R];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dot = fmaf(k[nb][i], q[r][i], dot);
+            const float part = group_sum<LPP>(dot);
+            score[nb][r] = valid[nb] ? part * scaling : kNeg;
+        }
+    }
+    float w[NB][R];
+    softmax_update<R, NB>(st, score, valid, w);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st.acc[r][i] = fmaf(w[nb][r], v[nb][i], st.acc[r][i]);
+}
+
 // One block of NB positions per lane group: scores against the lane's query
 // slices, online-softmax update, value accumulation.
 template <int D, int R, int NB>
@@ -149,24 +204,7 @@ __device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][
         }
     }
     float w[NB][R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float bm = score[0][r];
-#pragma unroll
-        for (int nb = 1; nb < NB; ++nb) bm = fmaxf(bm, score[nb][r]);
-        const float m_new = fmaxf(st.m[r], bm);
-        const float alpha = fast_exp2(st.m[r] - m_new);
-        float sum = 0.0f;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            w[nb][r] = valid[nb] ? fast_exp2(score[nb][r] - m_new) : 0.0f;
-            sum += w[nb][r];
-        }
-        st.l[r] = st.l[r] * alpha + sum;
-        st.m[r] = m_new;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st.acc[r][i] *= alpha;
-    }
+    softmax_update<R, NB>(st, score, valid, w);
     // Values: acc += (p * scale) * (u - 128).
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -223,13 +261,58 @@ __device__ __forceinline__ void merge_lane_groups(SoftmaxState<R> &st) {
     merge_step<32, R>(st);
 }
 
+// The end of a range kernel: merges the lane groups of each wave (lanes l
+// and l ^ (k * LPP) hold the same slice for different positions), then the
+// waves in wave order through LDS, into this range's (acc, m, l) record.
+template <int D, int R>
+__device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, SoftmaxState<R> &st, uint32_t b,
+                                                   uint32_t kvh, uint32_t split, int wave, int sub, int group) {
+    constexpr int LPP = D / 16;
+    constexpr int REC = R * D + 4 * R;
+    __shared__ float lds_acc[kWaves][R][D];
+    __shared__ float lds_ml[kWaves][R][2];
+    merge_lane_groups<LPP, R>(st);
+    if (group == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lds_acc[wave][r][sub * 16 + i] = st.acc[r][i];
+            if (sub == 0) {
+                lds_ml[wave][r][0] = st.m[r];
+                lds_ml[wave][r][1] = st.l[r];
+            }
+        }
+    }
+    __syncthreads();
+    // Merge the waves in wave order into this range's record.
+    float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
+    for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
+        const int r = idx / D;
+        const int d = idx % D;
+        float M = lds_ml[0][r][0];
+#pragma unroll
+        for (int w2 = 1; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2][r][0]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+            const float f = fast_exp2(lds_ml[w2][r][0] - M);
+            L += lds_ml[w2][r][1] * f;
+            A += lds_acc[w2][r][d] * f;
+        }
+        rec[idx] = A;
+        if (d == 0) {
+            rec[R * D + 4 * r + 0] = M;
+            rec[R * D + 4 * r + 1] = L;
+        }
+    }
+}
+
 template <int D, int R, bool Decoder>
 __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) {
     constexpr int LPP = D / 16;              // lanes per position
     constexpr int PPW = 64 / LPP;            // positions per wave per load
     constexpr int STEP = PPW * kWaves;       // positions per workgroup per load
     constexpr int GPH = D / 64;              // scale groups per head
-    constexpr int REC = R * D + 4 * R;       // floats per partial record
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane % LPP;              // 16-byte slice of the head row
@@ -308,9 +391,6 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     uint32_t end = begin + a.chunk;
     if (end > attended) end = attended;
 
-    __shared__ float lds_acc[kWaves][R][D];
-    __shared__ float lds_ml[kWaves][R][2];
-
     if (begin >= cached) return;  // no record: the merge reads ranges below cached only
     if (Decoder) {
 #pragma unroll
@@ -338,42 +418,109 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
         if (more) cur = nxt;
     }
 
-    // Merge the lane groups of this wave (lanes l and l ^ (k * LPP) hold the
-    // same slice for different positions).
-    merge_lane_groups<LPP, R>(st);
-    if (group == 0) {
+    write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
+}
+
+// The range kernel over an f32 cache (kernels.zig:572-627): the same lane
+// mapping (a lane group of D/16 lanes per position, 16 dimensions per lane,
+// four 16-byte loads per row), blocks of two positions per lane group (an f32
+// row is four times a q8 row's registers), and the same records.
+template <int D, int R, bool Decoder>
+__global__ __launch_bounds__(256) void attention_f32_kernel(const AttnKernelArgs a) {
+    constexpr int LPP = D / 16;
+    constexpr int PPW = 64 / LPP;
+    constexpr int STEP = PPW * kWaves;
+    constexpr int NB = 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = lane % LPP;
+    const int group = lane / LPP;
+    const uint32_t split = blockIdx.x;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t b = blockIdx.z;
+    const uint32_t kv_width = a.kv_heads * D;
+    const uint32_t begin = split * a.chunk;
+    const float *keys = reinterpret_cast<const float *>(a.k_codes + b * a.code_stride);
+    const float *values = reinterpret_cast<const float *>(a.v_codes + b * a.code_stride);
+    const uint32_t col = kvh * D + sub * 16;
+    constexpr uint32_t kSpan = STEP * NB;
+
+    struct Block {
+        float4 k[NB][4], v[NB][4];
+    };
+    // Unconditional loads, rows at or past `limit` clamped (as the q8 kernel).
+    auto load_block = [&](Block &blk, uint32_t base, uint32_t limit) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int nb = 0; nb < NB; ++nb) {
+            const uint32_t p = base + nb * STEP + wave * PPW + group;
+            const uint32_t row = p < limit ? p : limit - 1;
+            const float4 *kp = reinterpret_cast<const float4 *>(keys + (size_t)row * kv_width + col);
+            const float4 *vp = reinterpret_cast<const float4 *>(values + (size_t)row * kv_width + col);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) lds_acc[wave][r][sub * 16 + i] = st.acc[r][i];
-            if (sub == 0) {
-                lds_ml[wave][r][0] = st.m[r];
-                lds_ml[wave][r][1] = st.l[r];
+            for (int i = 0; i < 4; ++i) {
+                blk.k[nb][i] = kp[i];
+                blk.v[nb][i] = vp[i];
             }
         }
-    }
-    __syncthreads();
-    // Merge the waves in wave order into this range's record.
-    float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
-    for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
-        const int r = idx / D;
-        const int d = idx % D;
-        float M = lds_ml[0][r][0];
+    };
+    // Rows past `end` get no score and contribute zero values.
+    auto use_block = [&](SoftmaxState<R> &st, const float (&q)[R][16], const Block &blk, uint32_t base,
+                         uint32_t end) {
+        bool valid[NB];
+        float k[NB][16], v[NB][16];
 #pragma unroll
-        for (int w2 = 1; w2 < kWaves; ++w2) M = fmaxf(M, lds_ml[w2][r][0]);
-        float L = 0.0f, A = 0.0f;
+        for (int nb = 0; nb < NB; ++nb) {
+            valid[nb] = base + nb * STEP + wave * PPW + group < end;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
-            const float f = fast_exp2(lds_ml[w2][r][0] - M);
-            L += lds_ml[w2][r][1] * f;
-            A += lds_acc[w2][r][d] * f;
+            for (int i = 0; i < 4; ++i) {
+                k[nb][4 * i] = blk.k[nb][i].x; k[nb][4 * i + 1] = blk.k[nb][i].y;
+                k[nb][4 * i + 2] = blk.k[nb][i].z; k[nb][4 * i + 3] = blk.k[nb][i].w;
+                v[nb][4 * i] = valid[nb] ? blk.v[nb][i].x : 0.0f; v[nb][4 * i + 1] = valid[nb] ? blk.v[nb][i].y : 0.0f;
+                v[nb][4 * i + 2] = valid[nb] ? blk.v[nb][i].z : 0.0f; v[nb][4 * i + 3] = valid[nb] ? blk.v[nb][i].w : 0.0f;
+            }
         }
-        rec[idx] = A;
-        if (d == 0) {
-            rec[R * D + 4 * r + 0] = M;
-            rec[R * D + 4 * r + 1] = L;
+        attend_f32<D, R, NB>(st, q, k, v, valid, a.scaling);
+    };
+    Block cur, nxt;
+    load_block(cur, begin, a.rows);
+    const float *row = a.query + (size_t)b * a.query_stride;
+    float q[R][16];
+#pragma unroll
+    for (int r = 0; r < R; ++r) load16(row + (kvh * R + r) * D + sub * 16, q[r]);
+    float wq[16], rc[16], rs[16];
+    if (Decoder) {
+        const int j0 = (sub % (LPP / 2)) * 16;
+        load16(a.q_norm + sub * 16, wq);
+        load16(a.rope_now + (size_t)b * D + j0, rc);
+        load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
+    }
+    const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
+    const uint32_t attended = Decoder ? cached - 1 : cached;
+    uint32_t end = begin + a.chunk;
+    if (end > attended) end = attended;
+    if (begin >= cached) return;
+    if (Decoder) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            rms_norm16<D>(q[r], wq, a.eps);
+            rope16<D>(q[r], rc, rs, sub);
         }
     }
+    SoftmaxState<R> st;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        st.m[r] = kNeg;
+        st.l[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.acc[r][i] = 0.0f;
+    }
+    for (uint32_t base = begin; base < end; base += kSpan) {
+        const bool more = base + kSpan < end;
+        if (more) load_block(nxt, base + kSpan, end);
+        use_block(st, q, cur, base, end);
+        if (more) cur = nxt;
+    }
+    write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
 }
 
 // Sum over the D threads 0..D-1 (D/64 whole wavefronts) of the workgroup,
@@ -444,10 +591,10 @@ __device__ __forceinline__ void write_digits(const AttnKernelArgs &a, uint32_t b
 //
 // Decoder form: thread d < D also forms dimension d of the new position
 // (cached - 1): q and k get RMSNorm and RoPE, k and v are quantized to q8 per
-// 64-value group (one wavefront per group) and stored by the first query head
-// of the kv head, and the new row's score and dequantized value join the
-// merge last.
-template <int D, int R, bool Decoder>
+// 64-value group (one wavefront per group) -- or, with an f32 cache, kept as
+// they are -- and stored by the first query head of the kv head, and the new
+// row's score and (dequantized) value join the merge last.
+template <int D, int R, bool Decoder, bool F32C>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernelArgs a) {
     constexpr int REC = R * D + 4 * R;
     constexpr int COLS = D / 4;
@@ -530,28 +677,40 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
             qr = t < half ? __fsub_rn(__fmul_rn(qn, c), __fmul_rn(qp, s)) : __fadd_rn(__fmul_rn(qn, c), __fmul_rn(qp, s));
             const float kr = t < half ? __fsub_rn(__fmul_rn(kn, c), __fmul_rn(kp, s))
                                       : __fadd_rn(__fmul_rn(kn, c), __fmul_rn(kp, s));
-            // quantizeRow(.q8): this wavefront is one 64-value group.
-            const uint16_t kbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(kr)), 128.0f));
-            const uint16_t vbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(vx)), 128.0f));
-            scale_k = dev::f16_bits_to_f32(kbits);
-            const float scale_v = dev::f16_bits_to_f32(vbits);
-            const int ck = dev::quantize_one(kr, scale_k, -128, 127);
-            const int cv = dev::quantize_one(vx, scale_v, -128, 127);
-            code_k = (float)ck;
-            lds_v[t] = (float)cv * scale_v;
-            if (r == 0) {
-                const size_t pos_codes = (size_t)newest * kv_width + kvh * D + t;
-                const size_t pos_scales = (size_t)newest * (kv_width / 64) + kvh * (D / 64) + (t >> 6);
-                a.k_codes[b * a.code_stride + pos_codes] = (uint8_t)(ck + 128);
-                a.v_codes[b * a.code_stride + pos_codes] = (uint8_t)(cv + 128);
-                if ((t & 63) == 0) {
-                    reinterpret_cast<uint16_t *>(a.k_scales + b * a.scale_stride)[pos_scales] = kbits;
-                    reinterpret_cast<uint16_t *>(a.v_scales + b * a.scale_stride)[pos_scales] = vbits;
+            const size_t pos_codes = (size_t)newest * kv_width + kvh * D + t;
+            if constexpr (F32C) {
+                // decoder.zig:77-83: the f32 cache stores the rows as they are.
+                code_k = kr;
+                scale_k = 1.0f;
+                lds_v[t] = vx;
+                if (r == 0) {
+                    reinterpret_cast<float *>(a.k_codes + b * a.code_stride)[pos_codes] = kr;
+                    reinterpret_cast<float *>(a.v_codes + b * a.code_stride)[pos_codes] = vx;
+                }
+            } else {
+                // quantizeRow(.q8): this wavefront is one 64-value group.
+                const uint16_t kbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(kr)), 128.0f));
+                const uint16_t vbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(vx)), 128.0f));
+                scale_k = dev::f16_bits_to_f32(kbits);
+                const float scale_v = dev::f16_bits_to_f32(vbits);
+                const int ck = dev::quantize_one(kr, scale_k, -128, 127);
+                const int cv = dev::quantize_one(vx, scale_v, -128, 127);
+                code_k = (float)ck;
+                lds_v[t] = (float)cv * scale_v;
+                if (r == 0) {
+                    const size_t pos_scales = (size_t)newest * (kv_width / 64) + kvh * (D / 64) + (t >> 6);
+                    a.k_codes[b * a.code_stride + pos_codes] = (uint8_t)(ck + 128);
+                    a.v_codes[b * a.code_stride + pos_codes] = (uint8_t)(cv + 128);
+                    if ((t & 63) == 0) {
+                        reinterpret_cast<uint16_t *>(a.k_scales + b * a.scale_stride)[pos_scales] = kbits;
+                        reinterpret_cast<uint16_t *>(a.v_scales + b * a.scale_stride)[pos_scales] = vbits;
+                    }
                 }
             }
         }
         // Score of the new position (kernels.zig:727-735): per group
-        // scale * sum (u - 128) q, summed over groups, times the scaling.
+        // scale * sum (u - 128) q, summed over groups, times the scaling
+        // (f32 cache: k . q times the scaling, kernels.zig:603-608).
         const float part = dev::wave_sum(t < D ? code_k * qr : 0.0f);
         if (t < D && (t & 63) == 0) lds_sum[t >> 6] = part * scale_k;
         __syncthreads();
@@ -634,15 +793,30 @@ bool attention_supported(uint32_t head_dim, uint32_t ratio) {
            (head_dim == 256 && (ratio == 1 || ratio == 2));
 }
 
+template <int D, int R>
+void launch_attention_pair(hipStream_t s, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
+                           uint32_t kv_heads, uint32_t heads, uint32_t batch) {
+    const dim3 ranges(splits, kv_heads, batch), merge(heads, batch);
+    if (f32) {
+        if (decoder) {
+            attention_f32_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
+            attention_combine_kernel<D, R, true, true><<<merge, 256, 0, s>>>(k);
+        } else {
+            attention_f32_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
+            attention_combine_kernel<D, R, false, true><<<merge, 256, 0, s>>>(k);
+        }
+    } else if (decoder) {
+        attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
+        attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
+    } else {
+        attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
+        attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
+    }
+}
+
 #define QWH_ATTN_CASE(D_, R_)                                                                       \
     if (a.head_dim == D_ && R == R_) {                                                              \
-        if (decoder) {                                                                              \
-            attention_kernel<D_, R_, true><<<dim3(splits, a.kv_heads, a.batch), 256, 0, s>>>(k);    \
-            attention_combine_kernel<D_, R_, true><<<dim3(a.heads, a.batch), 256, 0, s>>>(k);       \
-        } else {                                                                                    \
-            attention_kernel<D_, R_, false><<<dim3(splits, a.kv_heads, a.batch), 256, 0, s>>>(k);   \
-            attention_combine_kernel<D_, R_, false><<<dim3(a.heads, a.batch), 256, 0, s>>>(k);      \
-        }                                                                                           \
+        launch_attention_pair<D_, R_>(s, k, decoder, a.f32_cache, splits, a.kv_heads, a.heads, a.batch); \
         return hipGetLastError();                                                                   \
     }
 

@@ -368,7 +368,7 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
             const size_t parts = batch_partial_bytes(tokens, *m);
             if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
             QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
-            return check_hip(ctx, launch_gemv_q4_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr,
+            return check_hip(ctx, launch_gemv_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr,
                                                        false, static_cast<float *>(ctx->scratch.ptr)),
                              "gemv q4 batch");
         }
@@ -383,14 +383,35 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
         QWH_TRY(check_hip(ctx, launch_prep_q4(ctx->stream, x_dev, tokens, cols, ctx->digits.ptr), "prep q4"));
         return check_hip(ctx, launch_gemv_q4(ctx->stream, ctx->cus, ctx->digits.ptr, *m, tokens, out_dev, nullptr), "gemv q4");
     }
-    if (m->format == QWH_FORMAT_Q8)
+    if (m->format == QWH_FORMAT_Q8) {
+        if (tokens >= 2) {
+            // Several tokens: the q4 path's int8 digit planes and one
+            // matrix-core pass over the codes per 16 tokens (u - 128 is
+            // already a signed byte), so W streams once, not once per token.
+            if (((uintptr_t)m->data & 15u) != 0)
+                return fail(ctx, QWH_E_INVALID_ARGUMENT, "q8 data plane must be 16-byte aligned");
+            GemvInput in;
+            in.mode = GemvInput::F32;
+            in.x = x_dev;
+            QWH_TRY(ensure_workspace(ctx, ctx->digits, batch_digit_bytes(tokens, cols)));
+            const size_t parts = batch_partial_bytes(tokens, *m);
+            if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
+            QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
+            return check_hip(ctx, launch_gemv_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr, false,
+                                                    static_cast<float *>(ctx->scratch.ptr)),
+                             "gemv q8 batch");
+        }
         return check_hip(ctx, launch_gemv_q8(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, nullptr), "gemv q8");
+    }
     if (m->format == QWH_FORMAT_Q5) {
-        if (!gemv_q5_supported(m->rows, m->cols))
+        if (!gemv_b8_supported(m->format, m->rows, m->cols))
             return fail(ctx, QWH_E_UNSUPPORTED, "q5 linear is built for K <= 6144 and data planes below 4 GiB");
         if (((uintptr_t)m->data & 7u) != 0)
             return fail(ctx, QWH_E_INVALID_ARGUMENT, "q5 data plane must be 8-byte aligned");
-        return check_hip(ctx, launch_gemv_q5(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev), "gemv q5");
+        GemvInput in;
+        in.mode = GemvInput::F32;
+        in.x = x_dev;
+        return check_hip(ctx, launch_gemv_b8(ctx->stream, ctx->cus, in, *m, tokens, out_dev, nullptr), "gemv q5");
     }
     return fail(ctx, QWH_E_UNSUPPORTED, "linear over format %d is not built", m->format);
 }
@@ -517,6 +538,47 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
     a.code_stride = code_stride_bytes;
     QWH_TRY(ensure_workspace(ctx, ctx->scratch, attention_scratch_bytes(ctx->cus, a)));
     return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr), "decode attention q8");
+}
+
+int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *query_dev, const float *keys_dev,
+                                 const float *values_dev, uint32_t cached, uint32_t heads, uint32_t kv_heads,
+                                 uint32_t head_dim, uint32_t batch, uint64_t stride_bytes) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    // kernels.zig:583-593 shape checks.
+    if (head_dim == 0 || kv_heads == 0 || heads % kv_heads != 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "heads %u not a multiple of kv_heads %u", heads, kv_heads);
+    if (cached == 0) return fail(ctx, QWH_E_SHAPE_MISMATCH, "no cached positions (softmax of an empty row)");
+    if (batch == 0) return QWH_OK;
+    const size_t kv_width = (size_t)kv_heads * head_dim;
+    if (batch > 1 && stride_bytes < (size_t)cached * kv_width * sizeof(float))
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "sequence stride smaller than %u cached rows", cached);
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    QWH_TRY(check_device_ptr(ctx, query_dev, "query"));
+    QWH_TRY(check_device_ptr(ctx, keys_dev, "keys"));
+    QWH_TRY(check_device_ptr(ctx, values_dev, "values"));
+    if (((uintptr_t)keys_dev | (uintptr_t)values_dev | (uintptr_t)query_dev) & 15u)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "query, keys and values must be 16-byte aligned");
+    if (batch > 1 && (stride_bytes & 15u))
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "the sequence stride must keep 16-byte alignment");
+    const uint32_t ratio = heads / kv_heads;
+    if (!attention_supported(head_dim, ratio))
+        return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim,
+                    ratio);
+    AttentionArgs a{};
+    a.out = out_dev;
+    a.query = query_dev;
+    a.k_codes = reinterpret_cast<uint8_t *>(const_cast<float *>(keys_dev));
+    a.v_codes = reinterpret_cast<uint8_t *>(const_cast<float *>(values_dev));
+    a.cached = cached;
+    a.capacity = cached;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.batch = batch;
+    a.code_stride = stride_bytes;
+    a.f32_cache = true;
+    QWH_TRY(ensure_workspace(ctx, ctx->scratch, attention_scratch_bytes(ctx->cus, a)));
+    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr), "decode attention f32");
 }
 
 int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_dev, uint32_t kv_width, uint32_t position,
@@ -646,16 +708,17 @@ int32_t check_audio_matrix(qwh_ctx *ctx, uint64_t handle, uint32_t rows, uint32_
 
 namespace {
 
-// Several linears over the same activations: for q4 matrices and two or more
-// tokens the digit planes are prepared once and each matrix reads them
-// (qwh_linear would prepare them per matrix); other formats go through
-// qwh_linear one by one.
+// Several linears over the same activations: for q4 / q8 matrices and two or
+// more tokens the digit planes are prepared once and each matrix reads them
+// (qwh_linear would prepare them per matrix); q5 goes through qwh_linear one
+// by one.
 int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handles, const float *x, uint32_t cols,
                             uint32_t tokens, std::initializer_list<float *> outs) {
     bool shared = tokens >= 2 && ((uintptr_t)x & 15u) == 0;
     for (uint64_t h : handles) {
         const Matrix *m = find_matrix(ctx, h);
-        shared = shared && m && m->format == QWH_FORMAT_Q4 && m->cols == cols && m->rows > 0;
+        shared = shared && m && gemv_batch_supported(*m) && ((uintptr_t)m->data & 15u) == 0 && m->cols == cols &&
+                 m->rows > 0;
     }
     auto out = outs.begin();
     if (!shared) {
@@ -671,9 +734,9 @@ int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handle
     in.x = x;
     QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
     for (uint64_t h : handles)
-        QWH_TRY(check_hip(ctx, launch_gemv_q4_batch(ctx->stream, ctx->digits.ptr, *find_matrix(ctx, h), tokens, *out++,
+        QWH_TRY(check_hip(ctx, launch_gemv_batch(ctx->stream, ctx->digits.ptr, *find_matrix(ctx, h), tokens, *out++,
                                                     nullptr, false, static_cast<float *>(ctx->scratch.ptr)),
-                          "gemv q4 batch"));
+                          "gemv batch"));
     return QWH_OK;
 }
 
@@ -697,17 +760,22 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
                              w->attention_norm_weight, w->attention_norm_bias, w->final_norm_weight,
                              w->final_norm_bias};
     for (const void *p : vectors) QWH_TRY(check_device_ptr(ctx, p, "layer vector"));
+    // Every check before the first launch, so a refused call leaves the
+    // residual stream untouched: the linears' token limit (the batch GEMV's
+    // grid rows), the attention's shape, and the 16-byte loads of ffn_in's
+    // bias by ffn_out's activation prep.
+    if (steps > 65535) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "steps %u > 65535", steps);
+    if (((uintptr_t)w->ffn_in_bias & 15u) != 0 || ((uintptr_t)encoder_dev & 15u) != 0)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "encoder and ffn_in bias must be 16-byte aligned");
+    if (d_model % 4u || ffn_dim % 64u)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "d_model %u / ffn_dim %u: whole float4 rows and groups of 64", d_model,
+                    ffn_dim);
     const size_t plane = (size_t)steps * d_model;
     QWH_TRY(ensure_workspace(ctx, ctx->audio, sizeof(float) * (5 * plane + (size_t)steps * ffn_dim)));
     float *normed = static_cast<float *>(ctx->audio.ptr);
     float *q = normed + plane, *k = q + plane, *v = k + plane, *block = v + plane, *wide = block + plane;
     hipStream_t s = ctx->stream;
-
-    // model.zig:657-665 layerNormInto, :765-786 projectQkv (biases join in the attention's loads).
-    QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->attention_norm_weight, w->attention_norm_bias,
-                                             d_model, steps, eps), "audio attention norm"));
-    QWH_TRY(linear_shared_input(ctx, {w->q, w->k, w->v}, normed, d_model, steps, {q, k, v}));
-    // :792-822 runWindowedAttention.
+    // :792-822 runWindowedAttention's arguments.
     AudioAttentionArgs a;
     a.out = block, a.q = q, a.k = k, a.v = v;
     a.q_bias = w->q_bias, a.k_bias = w->k_bias, a.v_bias = w->v_bias;
@@ -716,6 +784,11 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
     a.heads = heads, a.head_dim = d_model / heads;
     a.scaling = 1.0f / sqrtf((float)a.head_dim);
     QWH_TRY(check_audio_attention(ctx, a));
+
+    // model.zig:657-665 layerNormInto, :765-786 projectQkv (biases join in the attention's loads).
+    QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->attention_norm_weight, w->attention_norm_bias,
+                                             d_model, steps, eps), "audio attention norm"));
+    QWH_TRY(linear_shared_input(ctx, {w->q, w->k, w->v}, normed, d_model, steps, {q, k, v}));
     QWH_TRY(check_hip(ctx, launch_audio_attention(s, a), "audio attention"));
     // :824-848 projectAttentionOutput, :669 addInPlace.
     QWH_TRY(qwh_linear(ctx, w->o, block, d_model, steps, normed));
@@ -726,7 +799,7 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
                                              steps, eps), "audio final norm"));
     QWH_TRY(qwh_linear(ctx, w->ffn_in, normed, d_model, steps, wide));
     const Matrix *ffn_out = find_matrix(ctx, w->ffn_out);
-    if (ffn_out->format == QWH_FORMAT_Q4 && steps >= 2) {
+    if (gemv_batch_supported(*ffn_out) && ((uintptr_t)ffn_out->data & 15u) == 0 && steps >= 2) {
         // The bias and GELU are applied as ffn_out's activation prep reads
         // `wide` (one pass and one launch fewer than a separate epilogue).
         const size_t parts = batch_partial_bytes(steps, *ffn_out);
@@ -737,7 +810,7 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
         in.x = wide;
         in.gelu_bias = w->ffn_in_bias;
         QWH_TRY(check_hip(ctx, launch_prep_batch(s, in, steps, ffn_dim, ctx->digits.ptr), "audio ffn prep"));
-        QWH_TRY(check_hip(ctx, launch_gemv_q4_batch(s, ctx->digits.ptr, *ffn_out, steps, block, nullptr, false,
+        QWH_TRY(check_hip(ctx, launch_gemv_batch(s, ctx->digits.ptr, *ffn_out, steps, block, nullptr, false,
                                                     static_cast<float *>(ctx->scratch.ptr)),
                           "audio ffn_out"));
     } else {

@@ -122,18 +122,22 @@ hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const
                               uint32_t tokens, float *out, const float *residual);
 hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
-// q5 GEMV (quant.zig:253-269 planes) with f32 activations, any token count
-// (one launch; each token's workgroups encode its activations). Shapes with
-// K <= 6144 and a data plane below 4 GiB.
-bool gemv_q5_supported(uint32_t rows, uint32_t cols);
-hipError_t launch_gemv_q5(hipStream_t s, int cus, const float *x, const Matrix &w, uint32_t tokens, float *out);
+// q5 / q8 GEMV over byte digit planes (quant.zig:253-288 planes) with f32
+// activations in the F32 and RmsNorm forms, pairs and residual as the q4
+// GEMV; any token count (one launch; each token's workgroups encode its
+// activations). Shapes with K <= 6144 and a data plane below 4 GiB; the
+// data plane 8-byte (q5) or 16-byte (q8) aligned.
+bool gemv_b8_supported(int format, uint32_t rows, uint32_t cols);
+hipError_t launch_gemv_b8(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
+                          float *out, const float *residual);
 hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
 
-// Small-batch q4 GEMV on the matrix cores (gemv_batch.hip): activations as
-// int8 digit planes per 16-token tile, then one MFMA pass over the weights.
+// Small-batch q4 / q8 GEMV on the matrix cores (gemv_batch.hip): activations
+// as int8 digit planes per 16-token tile, then one MFMA pass over the
+// weights. gemv_batch_supported: the matrix has such a form.
 size_t batch_digit_bytes(uint32_t tokens, uint32_t cols);
-// The partial sums of a split GEMV (launch_gemv_q4_batch_parts) that a prep
+// The partial sums of a split GEMV (launch_gemv_batch_parts) that a prep
 // folds into its input: RMSNorm of x + their sum (stored to x_out, which may
 // be x), or with pairs (rows = 2 cols) siluMul of the gate / up sums in place
 // of x.
@@ -155,15 +159,16 @@ struct BatchNorm {
 // multiple of 256), and the bytes of partial sums that takes.
 uint32_t batch_slices(const Matrix &w);
 size_t batch_partial_bytes(uint32_t tokens, const Matrix &w);
+bool gemv_batch_supported(const Matrix &w);
 // out (+)= W x; with several slices `partials` (batch_partial_bytes) is
 // required and a reduce kernel adds them.
-hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                float *out, const float *residual, bool pairs = false, float *partials = nullptr,
-                                const BatchNorm &norm = BatchNorm{});
+hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
+                             float *out, const float *residual, bool pairs = false, float *partials = nullptr,
+                             const BatchNorm &norm = BatchNorm{});
 // Partial sums only: batch_slices(w) planes [slice][token][row], for a prep
 // to add (the shape must have a split form).
-hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                      float *partials, const BatchNorm &norm = BatchNorm{});
+hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
+                                   float *partials, const BatchNorm &norm = BatchNorm{});
 
 // q4 / q5 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
 // partials: gemm_scratch_bytes (0 when the tiles alone fill the device).
@@ -184,6 +189,9 @@ struct AttentionArgs {
     uint32_t capacity = 0;         // upper bound of cached (sizes the grid)
     uint32_t heads = 0, kv_heads = 0, head_dim = 0, batch = 0;
     uint64_t scale_stride = 0, code_stride = 0;  // per sequence, bytes
+    // f32 cache (decoder.zig:77-83, kernels.zig:572-627): k_codes / v_codes
+    // are [positions][kv_heads * head_dim] f32 planes; no scale planes.
+    bool f32_cache = false;
     // Decoder form (q_norm non-null): each query row is the q | k | v
     // projection of the newest position cached - 1. q and k get per-head
     // RMSNorm and RoPE at that position (rope_now: per sequence, that

@@ -21,6 +21,12 @@
 // At batch > 1 each GEMV is a digit-plane pass plus the matrix-core GEMV.
 // Shapes without a fused GEMV kernel (or QWH_DECODER_UNFUSED set) run the
 // norm / digit-plane kernels below as separate launches instead.
+//
+// Every matrix keeps the format it was bound in (kernels.zig:182-206 applies
+// whatever storage a Matrix holds): q4 runs the hex-digit GEMV, q5 and q8 the
+// byte-plane GEMV (batch 1 and the per-token path), and at batch > 1 q4 and
+// q8 share the matrix-core GEMV. The key/value cache is q8 or f32
+// (model_config.zig:44-68 CacheFormat; decoder.zig:68-106, :220-253).
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
@@ -72,16 +78,17 @@ __device__ __forceinline__ float block_sum256(float v, float *lds) {
     return total;
 }
 
-// decoder.zig:346-376 embeddingRow, q4: f32(u - 8) then times the scale;
-// or, for a sequence whose row flag is set, decoder.zig:144-147: the given
-// audio row replaces the embedding. Also copies the RoPE table row of the
-// sequence's position (cos then sin, 2 * half values) to rope_now, so the
-// step's attention kernels read it without first waiting for the position.
-__global__ __launch_bounds__(256) void embed_q4_kernel(const uint32_t *tokens, const uint16_t *scales,
-                                                       const uint8_t *data, uint32_t cols, float *hidden,
-                                                       const uint32_t *pos, const float *rope_cos,
-                                                       const float *rope_sin, uint32_t half, float *rope_now,
-                                                       const float *rows, const uint32_t *row_flags) {
+// decoder.zig:346-376 embeddingRow (quant.zig:315-345 dequantizeGroup in the
+// matrix's format): f32(u - bias) then times the group's scale; or, for a
+// sequence whose row flag is set, decoder.zig:144-147: the given audio row
+// replaces the embedding. Also copies the RoPE table row of the sequence's
+// position (cos then sin, 2 * half values) to rope_now, so the step's
+// attention kernels read it without first waiting for the position.
+__global__ __launch_bounds__(256) void embed_kernel(const uint32_t *tokens, int32_t format, const uint16_t *scales,
+                                                    const uint8_t *data, uint32_t cols, float *hidden,
+                                                    const uint32_t *pos, const float *rope_cos,
+                                                    const float *rope_sin, uint32_t half, float *rope_now,
+                                                    const float *rows, const uint32_t *row_flags) {
     const uint32_t b = blockIdx.x;
     if (threadIdx.x < 2 * half) {
         const uint32_t p = pos[b];
@@ -96,12 +103,29 @@ __global__ __launch_bounds__(256) void embed_q4_kernel(const uint32_t *tokens, c
     }
     const uint32_t token = tokens[b];
     const uint32_t gpr = cols / 64;
-    const uint8_t *row = data + (size_t)token * (cols / 2);
-    for (uint32_t i = threadIdx.x; i < cols / 2; i += blockDim.x) {
-        const uint32_t byte = row[i];
-        const float s = dev::f16_bits_to_f32(scales[(size_t)token * gpr + (2 * i) / 64]);
-        out[2 * i] = __fmul_rn((float)((int)(byte & 0xfu) - 8), s);
-        out[2 * i + 1] = __fmul_rn((float)((int)(byte >> 4) - 8), s);
+    const uint16_t *row_scales = scales + (size_t)token * gpr;
+    if (format == QWH_FORMAT_Q4) {
+        const uint8_t *row = data + (size_t)token * (cols / 2);
+        for (uint32_t i = threadIdx.x; i < cols / 2; i += blockDim.x) {
+            const uint32_t byte = row[i];
+            const float s = dev::f16_bits_to_f32(row_scales[(2 * i) / 64]);
+            out[2 * i] = __fmul_rn((float)((int)(byte & 0xfu) - 8), s);
+            out[2 * i + 1] = __fmul_rn((float)((int)(byte >> 4) - 8), s);
+        }
+    } else if (format == QWH_FORMAT_Q8) {
+        const uint8_t *row = data + (size_t)token * cols;
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x)
+            out[i] = __fmul_rn((float)((int)row[i] - 128), dev::f16_bits_to_f32(row_scales[i / 64]));
+    } else {
+        // q5: low nibble as q4, fifth bit j % 8 of byte 32 + j / 8 of the group.
+        const uint8_t *row = data + (size_t)token * gpr * 40;
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
+            const uint8_t *g = row + (size_t)(i / 64) * 40;
+            const uint32_t j = i % 64;
+            const uint32_t low = (g[j / 2] >> (4 * (j & 1))) & 0xfu;
+            const uint32_t high = (g[32 + j / 8] >> (j % 8)) & 1u;
+            out[i] = __fmul_rn((float)((int)(low | (high << 4)) - 16), dev::f16_bits_to_f32(row_scales[i / 64]));
+        }
     }
 }
 
@@ -181,12 +205,38 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits
     }
 }
 
-// Stage 2: merges the partials, writes the next token, records it in the
-// history at (position - history base), and advances the position.
+// Greedy generation with stop rules (wasm/model.zig:423-451 decodeStep,
+// :495-499 endsSequence), per sequence, in device memory: `mode` 0 = plain
+// steps; 1 = stop on a stop token or the token budget. done[b] freezes a
+// finished sequence (its position, token and history no longer change);
+// count[b] is the number of ids it has emitted into history rows.
+struct GenState {
+    uint32_t mode;
+    uint32_t budget;
+    uint32_t stops[3];
+    uint32_t stop_count;
+    uint32_t pad[2];
+    // then done[batch], count[batch]
+};
+
+__device__ __forceinline__ bool is_stop(const GenState *g, uint32_t token) {
+    for (uint32_t i = 0; i < g->stop_count && i < 3; ++i)
+        if (token == g->stops[i]) return true;
+    return false;
+}
+
+// Stage 2: merges the partials and writes the next token. Plain steps record
+// it in the history at (position - history base) and advance the position.
+// With stop rules (decodeStep): the forward that produced the token has run,
+// so the position advances; a stop token ends the sequence without being
+// emitted; otherwise it is emitted at row count[b], and the sequence ends
+// once it has emitted `budget` ids. A finished sequence is left unchanged
+// (its step recomputes the same row and writes nothing).
 __global__ __launch_bounds__(64) void argmax_finish_kernel(const float *pv, const uint32_t *pi,
                                                            uint32_t parts, uint32_t *tokens, uint32_t *pos,
                                                            const uint32_t *hist_base, uint32_t *history,
-                                                           uint32_t batch, uint32_t history_rows) {
+                                                           uint32_t batch, uint32_t history_rows,
+                                                           const GenState *gen, uint32_t *done, uint32_t *count) {
     const uint32_t b = blockIdx.x;
     float bv = -FLT_MAX;
     uint32_t bi = 0xffffffffu;
@@ -200,8 +250,22 @@ __global__ __launch_bounds__(64) void argmax_finish_kernel(const float *pv, cons
     if (threadIdx.x == 0) {
         // A row of NaN logits leaves no index; the reference then returns 0.
         const uint32_t token = bi == 0xffffffffu ? 0u : bi;
-        tokens[b] = token;
         const uint32_t p = pos[b];
+        if (gen->mode == 1) {
+            if (done[b]) return;
+            pos[b] = p + 1;
+            tokens[b] = token;
+            if (is_stop(gen, token)) {
+                done[b] = 1;
+                return;
+            }
+            const uint32_t n = count[b];
+            if (n < history_rows) history[(size_t)n * batch + b] = token;
+            count[b] = n + 1;
+            if (n + 1 >= gen->budget) done[b] = 1;
+            return;
+        }
+        tokens[b] = token;
         if (history) {
             const uint32_t row = p - hist_base[b];
             if (row < history_rows) history[(size_t)row * batch + b] = token;
@@ -249,14 +313,22 @@ struct qwh_decoder {
     float *arg_v = nullptr;
     uint32_t *arg_i = nullptr;
     uint32_t arg_parts = 0, arg_per_block = 0;
-    uint32_t *host_stage = nullptr;  // pinned: tokens in / ids out, then the row flags
+    uint32_t *host_stage = nullptr;  // pinned: tokens in / ids out, then the row flags, then generation state
     float *rows_dev = nullptr;        // audio rows for the next forward_rows step
     uint32_t *row_flags_dev = nullptr;  // per sequence: 1 = take rows_dev's row, not the embedding
     std::vector<uint32_t> pos_host;
     std::vector<void *> allocations;
     hipGraphExec_t graph[2] = {nullptr, nullptr};
     bool use_graph = true;
-    bool fused = true;  // every GEMV forms its own activations (no norm / prep kernels)
+    int32_t cache_format = QWH_CACHE_Q8;
+    // Generation state (GenState, then done[batch], count[batch]) and the
+    // mode last written to it.
+    void *gen = nullptr;
+    uint32_t gen_mode = 0;
+    // The step's kernel plan, decided from the bound matrices' formats before
+    // the step is first enqueued (and again after a matrix changes format).
+    bool planned = false;
+    bool fused = true;  // every q4 GEMV forms its own activations (no norm / prep kernels)
     bool batched = false;  // batch > 1: int8 digit planes + matrix-core GEMV
     void *batch_digits = nullptr;
     // Batched: K-slice partial sums. When every layer matrix has a split
@@ -292,21 +364,91 @@ int32_t dalloc(qwh_decoder *d, size_t bytes, void **out) {
     return QWH_OK;
 }
 
-int32_t alloc_matrix(qwh_decoder *d, Matrix &m, uint32_t rows, uint32_t cols) {
-    m.format = QWH_FORMAT_Q4;
+int32_t alloc_matrix(qwh_decoder *d, Matrix &m, uint32_t rows, uint32_t cols, int32_t format = QWH_FORMAT_Q4) {
+    m.format = format;
     m.rows = rows;
     m.cols = cols;
     m.owned = false;  // freed with the decoder's allocations
     const size_t groups = (size_t)rows * (cols / 64);
     QWH_TRY(dalloc(d, groups * 2, reinterpret_cast<void **>(&m.scales)));
-    QWH_TRY(dalloc(d, groups * 32, reinterpret_cast<void **>(&m.data)));
+    QWH_TRY(dalloc(d, groups * (size_t)data_bytes_per_group(format), reinterpret_cast<void **>(&m.data)));
     return QWH_OK;
+}
+
+void dfree(qwh_decoder *d, void *p) {
+    if (!p) return;
+    auto it = std::find(d->allocations.begin(), d->allocations.end(), p);
+    if (it != d->allocations.end()) d->allocations.erase(it);
+    (void)hipFree(p);
+}
+
+// Captured graphs hold the kernels' arguments (matrix planes among them):
+// dropped whenever a matrix moves, and the step planned again.
+void invalidate_step(qwh_decoder *d) {
+    for (hipGraphExec_t &g : d->graph)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
+    d->planned = false;
+}
+
+// Re-creates a decoder matrix (zeroed) in `format` when it holds another:
+// the planes of a fused block (q | k | v, gate | up) share one format, so a
+// member bound in a new format re-creates the whole block and the other
+// members are bound again after it.
+int32_t ensure_format(qwh_decoder *d, Matrix &m, int32_t format) {
+    if (m.format == format) return QWH_OK;
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "matrix format change"));
+    invalidate_step(d);
+    dfree(d, m.scales);
+    dfree(d, m.data);
+    m.scales = m.data = nullptr;
+    return alloc_matrix(d, m, m.rows, m.cols, format);
 }
 
 int32_t fill_ones(qwh_decoder *d, float *dst, uint64_t count) {
     fill_kernel<<<(unsigned)((count + 255) / 256 < 1024 ? (count + 255) / 256 : 1024), 256, 0, d->ctx->stream>>>(
         dst, count, 1.0f);
     return check_hip(d->ctx, hipGetLastError(), "fill");
+}
+
+// The step's kernels for the formats the matrices hold now: q5 / q8
+// matrices need the byte-plane GEMV's shapes; the matrix-core batch GEMV
+// runs when every matrix has that form (q4, q8), the split form with partial
+// sums when o, gate | up and down all split along K.
+int32_t plan_step(qwh_decoder *d) {
+    const qwh_decoder_config &c = d->c;
+    std::vector<const Matrix *> all;
+    for (const qwh_decoder::Layer &L : d->layers)
+        for (const Matrix *m : {&L.qkv, &L.o, &L.gu, &L.down}) all.push_back(m);
+    all.push_back(&d->lm_head);
+    bool q4_fused = getenv("QWH_DECODER_UNFUSED") == nullptr;
+    bool batch_form = d->batch > 1 && getenv("QWH_DECODER_PER_TOKEN") == nullptr;
+    for (const Matrix *m : all) {
+        if (m->format == QWH_FORMAT_Q4) {
+            q4_fused = q4_fused && gemv_q4_fused_supported(m->rows, m->cols);
+        } else if (!gemv_b8_supported(m->format, m->rows, m->cols)) {
+            return fail(d->ctx, QWH_E_UNSUPPORTED, "no GEMV for a %ux%u matrix of format %d", m->rows, m->cols,
+                        m->format);
+        }
+        batch_form = batch_form && gemv_batch_supported(*m);
+    }
+    d->fused = q4_fused;
+    d->batched = batch_form;
+    d->split_parts = false;
+    d->slices_o = d->slices_gu = d->slices_down = 0;
+    if (d->batched) {
+        const qwh_decoder::Layer &L0 = d->layers[0];
+        d->slices_o = batch_slices(L0.o);
+        d->slices_gu = batch_slices(L0.gu);
+        d->slices_down = batch_slices(L0.down);
+        d->split_parts = d->slices_o && d->slices_gu && d->slices_down && d->parts &&
+                         getenv("QWH_DECODER_NO_SPLIT") == nullptr;
+    }
+    (void)c;
+    d->planned = true;
+    return QWH_OK;
 }
 
 // Enqueues one decoder step for every sequence (tokens and positions read
@@ -343,8 +485,9 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             BatchNorm bn;
             bn.rms = mode == GemvInput::RmsNorm;
             bn.eps = c.eps;
-            return launch_gemv_q4_batch(s, d->batch_digits, w, B, out, residual, pairs, d->parts, bn);
+            return launch_gemv_batch(s, d->batch_digits, w, B, out, residual, pairs, d->parts, bn);
         }
+        if (w.format != QWH_FORMAT_Q4) return launch_gemv_b8(s, ctx->cus, in, w, B, out, residual);
         if (d->fused) return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
         if (mode == GemvInput::RmsNorm) {
             rmsnorm_digits_kernel<<<B, 256, 0, s>>>(x, norm, w.cols, c.eps, words, mult_of(w.cols));
@@ -358,9 +501,9 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         pre.pairs = pairs;
         return launch_gemv_q4_src(s, ctx->cus, pre, w, B, out, residual);
     };
-    embed_q4_kernel<<<B, 256, 0, s>>>(d->tokens_dev, reinterpret_cast<const uint16_t *>(d->embed.scales),
-                                      d->embed.data, c.hidden, d->hidden, d->pos_dev, d->rope_cos, d->rope_sin,
-                                      c.head_dim / 2, d->rope_now, d->rows_dev, d->row_flags_dev);
+    embed_kernel<<<B, 256, 0, s>>>(d->tokens_dev, d->embed.format, reinterpret_cast<const uint16_t *>(d->embed.scales),
+                                   d->embed.data, c.hidden, d->hidden, d->pos_dev, d->rope_cos, d->rope_sin,
+                                   c.head_dim / 2, d->rope_now, d->rows_dev, d->row_flags_dev);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
         err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
@@ -390,6 +533,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         aa.batch = B;
         aa.scale_stride = d->seq_stride;
         aa.code_stride = d->seq_stride;
+        aa.f32_cache = d->cache_format == QWH_CACHE_F32;
         // Batched: the attention output also arrives as the O projection's
         // digit planes.
         aa.digits = d->batched ? d->batch_digits : nullptr;
@@ -399,7 +543,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             // o, gate|up, down as partial sums; each prep adds the previous
             // one's (hidden += o; siluMul(gate, up); hidden += down at the
             // next layer's or the final prep).
-            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.o, B, d->parts);
+            err = launch_gemv_batch_parts(s, d->batch_digits, L.o, B, d->parts);
             if (err != hipSuccess) break;
             GemvInput norm_in;
             norm_in.mode = GemvInput::RmsNorm;
@@ -412,14 +556,14 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             BatchNorm bn;
             bn.rms = true;
             bn.eps = c.eps;
-            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.gu, B, d->parts, bn);
+            err = launch_gemv_batch_parts(s, d->batch_digits, L.gu, B, d->parts, bn);
             if (err != hipSuccess) break;
             GemvInput pairs_in;
             pairs_in.mode = GemvInput::F32;
             const PartialSums gu_sums{d->parts, d->slices_gu, 2 * c.ffn, true, nullptr};
             err = launch_prep_batch(s, pairs_in, B, c.ffn, d->batch_digits, &gu_sums);
             if (err != hipSuccess) break;
-            err = launch_gemv_q4_batch_parts(s, d->batch_digits, L.down, B, d->parts);
+            err = launch_gemv_batch_parts(s, d->batch_digits, L.down, B, d->parts);
             if (err != hipSuccess) break;
             pending = PartialSums{d->parts, d->slices_down, c.hidden, false, d->hidden};
             continue;
@@ -438,8 +582,11 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             if (err == hipSuccess) {
                 argmax_partial_kernel<<<dim3(d->arg_parts, B), 256, 0, s>>>(d->logits, c.vocab, d->arg_per_block,
                                                                              d->arg_v, d->arg_i);
+                const GenState *gen = static_cast<const GenState *>(d->gen);
+                uint32_t *done = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(d->gen) + sizeof(GenState));
                 argmax_finish_kernel<<<B, 64, 0, s>>>(d->arg_v, d->arg_i, d->arg_parts, d->tokens_dev, d->pos_dev,
-                                                      d->hist_base_dev, d->history_dev, B, d->history_rows);
+                                                      d->hist_base_dev, d->history_dev, B, d->history_rows, gen, done,
+                                                      done + B);
                 err = hipGetLastError();
             }
         } else {
@@ -453,6 +600,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
 
 int32_t run_step(qwh_decoder *d, bool want_logits) {
     qwh_ctx *ctx = d->ctx;
+    if (!d->planned) QWH_TRY(plan_step(d));
     if (!d->use_graph) return enqueue_step(d, want_logits);
     hipGraphExec_t &exec = d->graph[want_logits ? 1 : 0];
     if (!exec) {
@@ -495,7 +643,7 @@ void build_rope_tables(std::vector<float> &cos_t, std::vector<float> &sin_t, uin
 int32_t copy_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, const Matrix &src, uint32_t stride = 1) {
     const size_t gpr = dst.cols / 64;
     hipStream_t s = d->ctx->stream;
-    const size_t sb = gpr * 2, db = gpr * 32;  // scale and code bytes per row
+    const size_t sb = gpr * 2, db = gpr * (size_t)data_bytes_per_group(dst.format);  // scale and code bytes per row
     QWH_TRY(check_hip(d->ctx, hipMemcpy2DAsync(dst.scales + (size_t)row_offset * sb, sb * stride, src.scales, sb, sb,
                                                src.rows, hipMemcpyDeviceToDevice, s), "copy scales"));
     QWH_TRY(check_hip(d->ctx, hipMemcpy2DAsync(dst.data + (size_t)row_offset * db, db * stride, src.data, db, db,
@@ -505,11 +653,12 @@ int32_t copy_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, const Matrix
 
 // Synthetic values for rows [row_offset, row_offset + rows) of `dst` from
 // rows [0, rows) of `stream`, generated in slabs through a temporary f32
-// buffer and quantized to q4 on the device.
+// buffer and quantized to dst's format on the device.
 int32_t synth_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, uint32_t rows, uint32_t seed,
                    uint32_t stream, float scale, float *temp, size_t temp_values) {
     const uint32_t cols = dst.cols;
     const size_t gpr = cols / 64;
+    const size_t bpg = (size_t)data_bytes_per_group(dst.format);
     uint32_t slab = (uint32_t)(temp_values / cols);
     if (slab == 0) return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "synthetic slab too small");
     hipStream_t s = d->ctx->stream;
@@ -517,9 +666,9 @@ int32_t synth_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, uint32_t ro
         const uint32_t n = rows - r < slab ? rows - r : slab;
         QWH_TRY(check_hip(d->ctx, launch_synth_normal(s, seed, stream, (uint64_t)r * cols, (uint64_t)n * cols, scale, temp),
                           "synthetic values"));
-        QWH_TRY(check_hip(d->ctx, launch_quantize_rows(s, QWH_FORMAT_Q4, temp, (uint64_t)n * gpr,
+        QWH_TRY(check_hip(d->ctx, launch_quantize_rows(s, dst.format, temp, (uint64_t)n * gpr,
                                                       dst.scales + (size_t)(row_offset + r) * gpr * 2,
-                                                      dst.data + (size_t)(row_offset + r) * gpr * 32),
+                                                      dst.data + (size_t)(row_offset + r) * gpr * bpg),
                           "quantize"));
     }
     return QWH_OK;
@@ -527,8 +676,8 @@ int32_t synth_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, uint32_t ro
 
 int32_t check_matrix(qwh_decoder *d, const Matrix *m, uint32_t rows, uint32_t cols) {
     if (!m) return fail(d->ctx, QWH_E_NOT_FOUND, "unknown matrix handle");
-    if (m->format != QWH_FORMAT_Q4)
-        return fail(d->ctx, QWH_E_UNSUPPORTED, "decoder matrices must be q4 (format 16), got %d", m->format);
+    if (m->format != QWH_FORMAT_Q4 && m->format != QWH_FORMAT_Q5 && m->format != QWH_FORMAT_Q8)
+        return fail(d->ctx, QWH_E_UNSUPPORTED, "decoder matrices are q4, q5 or q8 (formats 16-18), got %d", m->format);
     if (m->rows != rows || m->cols != cols)
         return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "matrix is %ux%u, expected %ux%u", m->rows, m->cols, rows, cols);
     return QWH_OK;
@@ -542,7 +691,14 @@ using namespace qwh;
 extern "C" {
 
 int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch, qwh_decoder **out) {
+    return qwh_decoder_create_cache(ctx, config, batch, QWH_CACHE_Q8, out);
+}
+
+int32_t qwh_decoder_create_cache(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch,
+                                 uint32_t cache_format, qwh_decoder **out) {
     if (!ctx || !config || !out || batch == 0) return QWH_E_INVALID_ARGUMENT;
+    if (cache_format != QWH_CACHE_F32 && cache_format != QWH_CACHE_Q8)
+        return fail(ctx, QWH_E_UNSUPPORTED, "cache format %u is neither f32 (0) nor q8 (1)", cache_format);
     const qwh_decoder_config &c = *config;
     if (c.kv_heads == 0 || c.heads % c.kv_heads != 0)
         return fail(ctx, QWH_E_SHAPE_MISMATCH, "heads %u / kv_heads %u", c.heads, c.kv_heads);
@@ -560,12 +716,12 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     d->batch = batch;
     d->qw = c.heads * c.head_dim;
     d->kvw = c.kv_heads * c.head_dim;
+    d->cache_format = (int32_t)cache_format;
     d->use_graph = getenv("QWH_NO_GRAPH") == nullptr;
-    // QWH_DECODER_UNFUSED forces the separate norm / prep kernels (for tests).
-    d->fused = getenv("QWH_DECODER_UNFUSED") == nullptr &&
-               gemv_q4_fused_supported(d->qw + 2 * d->kvw, c.hidden) && gemv_q4_fused_supported(c.hidden, d->qw) &&
-               gemv_q4_fused_supported(2 * c.ffn, c.hidden) && gemv_q4_fused_supported(c.hidden, c.ffn) &&
-               gemv_q4_fused_supported(c.vocab, c.hidden);
+    // The kernel plan (plan_step) is made before the first step. Test
+    // switches it reads: QWH_DECODER_UNFUSED (separate norm / prep kernels
+    // for q4), QWH_DECODER_PER_TOKEN (batch > 1 on the per-token GEMVs),
+    // QWH_DECODER_NO_SPLIT (no K-split partial sums).
     auto cleanup = [&](int32_t st) {
         qwh_decoder_destroy(d);
         return st;
@@ -599,9 +755,15 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = dalloc(d, sin_t.size() * 4, reinterpret_cast<void **>(&d->rope_sin));
     if (st == QWH_OK) st = check_hip(ctx, hipMemcpy(d->rope_cos, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice), "rope");
     if (st == QWH_OK) st = check_hip(ctx, hipMemcpy(d->rope_sin, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice), "rope");
-    // Caches: per sequence, per layer [scales][codes] (decoder.zig:58-65).
-    d->cache_scales = (size_t)c.max_positions * (d->kvw / 64) * 2;
-    d->cache_codes = (size_t)c.max_positions * d->kvw;
+    // Caches: per sequence, per layer [scales][codes] (decoder.zig:58-65),
+    // or [max_positions][kv_width] f32 (decoder.zig:77-83).
+    if (cache_format == QWH_CACHE_Q8) {
+        d->cache_scales = (size_t)c.max_positions * (d->kvw / 64) * 2;
+        d->cache_codes = (size_t)c.max_positions * d->kvw;
+    } else {
+        d->cache_scales = 0;
+        d->cache_codes = (size_t)c.max_positions * d->kvw * sizeof(float);
+    }
     d->layer_stride = d->cache_scales + d->cache_codes;
     d->seq_stride = d->layer_stride * c.layers;
     if (st == QWH_OK) st = dalloc(d, d->seq_stride * batch, reinterpret_cast<void **>(&d->keys));
@@ -630,26 +792,24 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * c.head_dim, reinterpret_cast<void **>(&d->rope_now));
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * (size_t)c.vocab, reinterpret_cast<void **>(&d->logits));
     if (st == QWH_OK) st = dalloc(d, q4_digit_bytes(batch, widest), &d->digits);
-    // QWH_DECODER_PER_TOKEN keeps batch > 1 on the per-token GEMV (for tests).
-    d->batched = batch > 1 && getenv("QWH_DECODER_PER_TOKEN") == nullptr;
-    if (st == QWH_OK && d->batched) st = dalloc(d, batch_digit_bytes(batch, widest), &d->batch_digits);
-    if (st == QWH_OK && d->batched) {
+    // Batch > 1: digit planes and K-slice partial sums of the matrix-core
+    // GEMV (the split plan depends on shapes only, not on q4 / q8).
+    if (st == QWH_OK && batch > 1) st = dalloc(d, batch_digit_bytes(batch, widest), &d->batch_digits);
+    if (st == QWH_OK && batch > 1) {
         const qwh_decoder::Layer &L0 = d->layers[0];
-        d->slices_o = batch_slices(L0.o);
-        d->slices_gu = batch_slices(L0.gu);
-        d->slices_down = batch_slices(L0.down);
-        d->split_parts = d->slices_o && d->slices_gu && d->slices_down && getenv("QWH_DECODER_NO_SPLIT") == nullptr;
         size_t parts = 0;
         for (const Matrix *m : {&L0.qkv, &L0.o, &L0.gu, &L0.down, const_cast<const Matrix *>(&d->lm_head)})
             parts = std::max(parts, batch_partial_bytes(batch, *m));
         if (parts) st = dalloc(d, parts, reinterpret_cast<void **>(&d->parts));
     }
+    if (st == QWH_OK) st = dalloc(d, sizeof(GenState) + 8 * (size_t)batch, &d->gen);
     AttentionArgs aa{};
     aa.capacity = c.max_positions;
     aa.heads = c.heads;
     aa.kv_heads = c.kv_heads;
     aa.head_dim = c.head_dim;
     aa.batch = batch;
+    aa.f32_cache = cache_format == QWH_CACHE_F32;
     if (st == QWH_OK) st = dalloc(d, attention_scratch_bytes(ctx->cus, aa), &d->attn_scratch);
     d->arg_per_block = 4096;
     d->arg_parts = (c.vocab + d->arg_per_block - 1) / d->arg_per_block;
@@ -657,7 +817,8 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
     if (st == QWH_OK) st = dalloc(d, 4 * (size_t)batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_i));
     if (st == QWH_OK) {
         void *p = nullptr;
-        st = check_hip(ctx, hipHostMalloc(&p, 8 * (size_t)batch, hipHostMallocDefault), "pinned staging");
+        st = check_hip(ctx, hipHostMalloc(&p, 20 * (size_t)batch + sizeof(GenState) + 64, hipHostMallocDefault),
+                       "pinned staging");
         d->host_stage = static_cast<uint32_t *>(p);
     }
     if (st == QWH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "decoder create");
@@ -681,20 +842,25 @@ int32_t qwh_decoder_set_matrix(qwh_decoder *d, uint32_t kind, uint32_t layer, ui
     if (!d) return QWH_E_INVALID_ARGUMENT;
     const Matrix *m = find_matrix(d->ctx, handle);
     const qwh_decoder_config &c = d->c;
-    if (kind == QWH_T_EMBED || kind == QWH_T_LM_HEAD) {
-        QWH_TRY(check_matrix(d, m, c.vocab, c.hidden));
-        return copy_rows(d, kind == QWH_T_EMBED ? d->embed : d->lm_head, 0, *m);
-    }
+    // The matrix's rows are copied into the decoder's own block, which takes
+    // the matrix's format first (ensure_format).
+    auto bind = [&](Matrix &dst, uint32_t rows, uint32_t cols, uint32_t offset, uint32_t stride) -> int32_t {
+        QWH_TRY(check_matrix(d, m, rows, cols));
+        QWH_TRY(ensure_format(d, dst, m->format));
+        return copy_rows(d, dst, offset, *m, stride);
+    };
+    if (kind == QWH_T_EMBED) return bind(d->embed, c.vocab, c.hidden, 0, 1);
+    if (kind == QWH_T_LM_HEAD) return bind(d->lm_head, c.vocab, c.hidden, 0, 1);
     if (layer >= c.layers) return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "layer %u of %u", layer, c.layers);
     qwh_decoder::Layer &L = d->layers[layer];
     switch (kind) {
-    case QWH_T_Q: QWH_TRY(check_matrix(d, m, d->qw, c.hidden)); return copy_rows(d, L.qkv, 0, *m);
-    case QWH_T_K: QWH_TRY(check_matrix(d, m, d->kvw, c.hidden)); return copy_rows(d, L.qkv, d->qw, *m);
-    case QWH_T_V: QWH_TRY(check_matrix(d, m, d->kvw, c.hidden)); return copy_rows(d, L.qkv, d->qw + d->kvw, *m);
-    case QWH_T_O: QWH_TRY(check_matrix(d, m, c.hidden, d->qw)); return copy_rows(d, L.o, 0, *m);
-    case QWH_T_GATE: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, 0, *m, 2);
-    case QWH_T_UP: QWH_TRY(check_matrix(d, m, c.ffn, c.hidden)); return copy_rows(d, L.gu, 1, *m, 2);
-    case QWH_T_DOWN: QWH_TRY(check_matrix(d, m, c.hidden, c.ffn)); return copy_rows(d, L.down, 0, *m);
+    case QWH_T_Q: return bind(L.qkv, d->qw, c.hidden, 0, 1);
+    case QWH_T_K: return bind(L.qkv, d->kvw, c.hidden, d->qw, 1);
+    case QWH_T_V: return bind(L.qkv, d->kvw, c.hidden, d->qw + d->kvw, 1);
+    case QWH_T_O: return bind(L.o, c.hidden, d->qw, 0, 1);
+    case QWH_T_GATE: return bind(L.gu, c.ffn, c.hidden, 0, 2);
+    case QWH_T_UP: return bind(L.gu, c.ffn, c.hidden, 1, 2);
+    case QWH_T_DOWN: return bind(L.down, c.hidden, c.ffn, 0, 1);
     default: return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "unknown matrix kind %u", kind);
     }
 }
@@ -809,21 +975,33 @@ int32_t qwh_decoder_bind_shard(qwh_decoder *d, uint64_t shard, uint32_t flags, u
 }
 
 int32_t qwh_decoder_init_synthetic(qwh_decoder *d, uint32_t seed) {
+    return qwh_decoder_init_synthetic_format(d, seed, QWH_FORMAT_Q4);
+}
+
+int32_t qwh_decoder_init_synthetic_format(qwh_decoder *d, uint32_t seed, int32_t format) {
     if (!d) return QWH_E_INVALID_ARGUMENT;
+    if (format != QWH_FORMAT_Q4 && format != QWH_FORMAT_Q5 && format != QWH_FORMAT_Q8)
+        return fail(d->ctx, QWH_E_UNSUPPORTED, "synthetic decoder format %d is not q4, q5 or q8", format);
     const qwh_decoder_config &c = d->c;
+    QWH_TRY(ensure_format(d, d->embed, format));
+    QWH_TRY(ensure_format(d, d->lm_head, format));
+    for (qwh_decoder::Layer &L : d->layers)
+        for (Matrix *m : {&L.qkv, &L.o, &L.gu, &L.down}) QWH_TRY(ensure_format(d, *m, format));
     const size_t temp_values = (size_t)64 << 20;
     float *temp = nullptr;
     QWH_TRY(check_hip(d->ctx, hipMalloc(&temp, temp_values * 4), "synthetic temp"));
     // Gate and up are generated into a staging matrix, then interleaved.
     Matrix stage;
-    stage.format = QWH_FORMAT_Q4;
+    stage.format = format;
     stage.rows = c.ffn;
     stage.cols = c.hidden;
     const size_t stage_gpr = (size_t)c.hidden / 64;
     int32_t st = check_hip(d->ctx, hipMalloc(reinterpret_cast<void **>(&stage.scales), (size_t)c.ffn * stage_gpr * 2),
                            "synthetic staging");
     if (st == QWH_OK)
-        st = check_hip(d->ctx, hipMalloc(reinterpret_cast<void **>(&stage.data), (size_t)c.ffn * stage_gpr * 32),
+        st = check_hip(d->ctx,
+                       hipMalloc(reinterpret_cast<void **>(&stage.data),
+                                 (size_t)c.ffn * stage_gpr * (size_t)data_bytes_per_group(format)),
                        "synthetic staging");
     if (st == QWH_OK) st = synth_rows(d, d->embed, 0, c.vocab, seed, kStreamEmbed, 0.02f, temp, temp_values);
     if (st == QWH_OK) st = synth_rows(d, d->lm_head, 0, c.vocab, seed, kStreamLmHead, 0.02f, temp, temp_values);
@@ -864,12 +1042,18 @@ int32_t qwh_decoder_prefill_random(qwh_decoder *d, uint32_t seq, uint32_t count,
     hipStream_t s = d->ctx->stream;
     const size_t values = (size_t)count * d->kvw;
     float *temp = nullptr;
-    if (values) QWH_TRY(check_hip(d->ctx, hipMalloc(&temp, values * 4), "prefill temp"));
+    if (values && d->cache_format == QWH_CACHE_Q8) QWH_TRY(check_hip(d->ctx, hipMalloc(&temp, values * 4), "prefill temp"));
     int32_t st = QWH_OK;
     for (uint32_t l = 0; l < d->c.layers && st == QWH_OK && values; ++l) {
         for (int kv = 0; kv < 2 && st == QWH_OK; ++kv) {
             const uint32_t stream = kStreamCacheBase + 0x100 * seq + 2 * l + kv;
             uint8_t *base = (kv == 0 ? d->keys : d->values) + (size_t)seq * d->seq_stride + (size_t)l * d->layer_stride;
+            if (d->cache_format == QWH_CACHE_F32) {
+                // The f32 cache holds the rows themselves (decoder.zig:77-83).
+                st = check_hip(d->ctx, launch_synth_normal(s, seed, stream, 0, values, 1.0f, reinterpret_cast<float *>(base)),
+                               "prefill values");
+                continue;
+            }
             st = check_hip(d->ctx, launch_synth_normal(s, seed, stream, 0, values, 1.0f, temp), "prefill values");
             if (st == QWH_OK)
                 st = check_hip(d->ctx, launch_quantize_rows(s, QWH_FORMAT_Q8, temp, values / 64, base, base + d->cache_scales),
@@ -891,9 +1075,10 @@ int32_t qwh_decoder_cache_planes(qwh_decoder *d, uint32_t seq, uint32_t layer, v
     if (!d || seq >= d->batch || layer >= d->c.layers) return QWH_E_INVALID_ARGUMENT;
     uint8_t *kb = d->keys + (size_t)seq * d->seq_stride + (size_t)layer * d->layer_stride;
     uint8_t *vb = d->values + (size_t)seq * d->seq_stride + (size_t)layer * d->layer_stride;
-    if (k_scales) *k_scales = kb;
+    const bool f32 = d->cache_format == QWH_CACHE_F32;  // no scale planes; the "codes" are f32 rows
+    if (k_scales) *k_scales = f32 ? nullptr : kb;
     if (k_codes) *k_codes = kb + d->cache_scales;
-    if (v_scales) *v_scales = vb;
+    if (v_scales) *v_scales = f32 ? nullptr : vb;
     if (v_codes) *v_codes = vb + d->cache_scales;
     return QWH_OK;
 }
@@ -914,6 +1099,22 @@ int32_t qwh_decoder_set_position(qwh_decoder *d, uint32_t seq, uint32_t position
     return QWH_OK;
 }
 
+// Pinned staging of the generation state: after tokens (batch), row flags
+// (batch) and ids (batch), the GenState image followed by done and count.
+static GenState *gen_stage(qwh_decoder *d) { return reinterpret_cast<GenState *>(d->host_stage + 3 * (size_t)d->batch); }
+
+// Plain steps (forward, step, generate) run with the stop rules off.
+static int32_t plain_mode(qwh_decoder *d) {
+    if (d->gen_mode == 0) return QWH_OK;
+    GenState *g = gen_stage(d);
+    std::memset(g, 0, sizeof(GenState));
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->gen, g, sizeof(GenState), hipMemcpyHostToDevice, d->ctx->stream),
+                      "generation mode"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "generation mode"));
+    d->gen_mode = 0;
+    return QWH_OK;
+}
+
 static int32_t upload_tokens(qwh_decoder *d, const uint32_t *tokens, uint32_t steps) {
     for (uint32_t b = 0; b < d->batch; ++b) {
         if (tokens[b] >= d->c.vocab) return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "token %u >= vocab %u", tokens[b], d->c.vocab);
@@ -922,6 +1123,7 @@ static int32_t upload_tokens(qwh_decoder *d, const uint32_t *tokens, uint32_t st
             return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "sequence %u: position %u + %u steps exceeds %u", b,
                         d->pos_host[b], steps, d->c.max_positions);
     }
+    QWH_TRY(plain_mode(d));
     memcpy(d->host_stage, tokens, 4 * (size_t)d->batch);
     return check_hip(d->ctx, hipMemcpyAsync(d->tokens_dev, d->host_stage, 4 * (size_t)d->batch, hipMemcpyHostToDevice,
                                             d->ctx->stream), "tokens");
@@ -952,9 +1154,13 @@ int32_t qwh_decoder_forward_rows(qwh_decoder *d, const uint32_t *tokens, const f
     }
     QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->row_flags_dev, flags, 4 * (size_t)B, hipMemcpyHostToDevice,
                                              d->ctx->stream), "row flags"));
-    QWH_TRY(run_step(d, want_logits != 0));
-    // Later steps embed their tokens again (outside any captured graph).
-    QWH_TRY(check_hip(d->ctx, hipMemsetAsync(d->row_flags_dev, 0, 4 * (size_t)B, d->ctx->stream), "row flags"));
+    const int32_t st = run_step(d, want_logits != 0);
+    // Later steps embed their tokens again (outside any captured graph),
+    // also when this step failed: no later call may splice stale rows.
+    const int32_t clear =
+        check_hip(d->ctx, hipMemsetAsync(d->row_flags_dev, 0, 4 * (size_t)B, d->ctx->stream), "row flags");
+    QWH_TRY(st);
+    QWH_TRY(clear);
     QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "forward rows"));
     for (uint32_t &p : d->pos_host) p += 1;
     return QWH_OK;
@@ -983,6 +1189,77 @@ int32_t qwh_decoder_generate(qwh_decoder *d, const uint32_t *tokens, uint32_t st
                                              d->ctx->stream), "history"));
     QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "generate"));
     for (uint32_t &p : d->pos_host) p += steps;
+    return QWH_OK;
+}
+
+int32_t qwh_decoder_generate_until(qwh_decoder *d, const uint32_t *tokens, uint32_t max_tokens,
+                                   const uint32_t *stop_tokens, uint32_t stop_count, uint32_t *ids_out,
+                                   uint32_t *counts_out) {
+    if (!d || !tokens || !counts_out || (max_tokens && !ids_out) || (stop_count && !stop_tokens))
+        return QWH_E_INVALID_ARGUMENT;
+    if (stop_count > 3) return fail(d->ctx, QWH_E_INVALID_ARGUMENT, "at most 3 stop tokens, got %u", stop_count);
+    const uint32_t B = d->batch;
+    if (max_tokens > d->history_rows)
+        return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "max_tokens %u exceeds %u", max_tokens, d->history_rows);
+    // At most max_tokens - 1 forwards: the last emitted id needs none
+    // (decodeStep checks the budget before the next prediction).
+    const uint32_t forwards = max_tokens ? max_tokens - 1 : 0;
+    QWH_TRY(upload_tokens(d, tokens, forwards));
+    GenState *g = gen_stage(d);
+    std::memset(g, 0, sizeof(GenState));
+    g->mode = 1;
+    g->budget = max_tokens;
+    g->stop_count = stop_count;
+    for (uint32_t i = 0; i < stop_count; ++i) g->stops[i] = stop_tokens[i];
+    uint32_t *done = reinterpret_cast<uint32_t *>(g + 1);
+    uint32_t *count = done + B;
+    uint32_t *row0 = d->host_stage + 2 * (size_t)B;
+    bool any = false;
+    for (uint32_t b = 0; b < B; ++b) {
+        // decodeStep on the caller's next token: a stop token or an empty
+        // budget ends the sequence before anything is emitted; else the
+        // token is the first id.
+        bool stop = max_tokens == 0;
+        for (uint32_t i = 0; i < stop_count; ++i) stop = stop || tokens[b] == stop_tokens[i];
+        count[b] = stop ? 0u : 1u;
+        done[b] = stop || count[b] >= max_tokens ? 1u : 0u;
+        row0[b] = tokens[b];
+        any = any || !done[b];
+    }
+    hipStream_t s = d->ctx->stream;
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->gen, g, sizeof(GenState) + 8 * (size_t)B, hipMemcpyHostToDevice, s),
+                      "generation state"));
+    if (max_tokens)
+        QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->history_dev, row0, 4 * (size_t)B, hipMemcpyHostToDevice, s),
+                          "first ids"));
+    d->gen_mode = 1;
+    // Replays in rounds of 16, stopping once every sequence has finished.
+    constexpr uint32_t kRound = 16;
+    for (uint32_t i = 0; i < forwards && any;) {
+        const uint32_t n = std::min(kRound, forwards - i);
+        for (uint32_t j = 0; j < n; ++j) QWH_TRY(run_step(d, true));
+        i += n;
+        if (i >= forwards) break;
+        QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(done, static_cast<uint8_t *>(d->gen) + sizeof(GenState), 4 * (size_t)B,
+                                                 hipMemcpyDeviceToHost, s), "done flags"));
+        QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "done flags"));
+        any = false;
+        for (uint32_t b = 0; b < B; ++b) any = any || !done[b];
+    }
+    // Results: counts, ids, and the positions the forwards reached.
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(count, static_cast<uint8_t *>(d->gen) + sizeof(GenState) + 4 * (size_t)B,
+                                             4 * (size_t)B, hipMemcpyDeviceToHost, s), "counts"));
+    if (max_tokens)
+        QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(ids_out, d->history_dev, 4 * (size_t)B * max_tokens,
+                                                 hipMemcpyDeviceToHost, s), "ids"));
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(row0, d->pos_dev, 4 * (size_t)B, hipMemcpyDeviceToHost, s), "positions"));
+    QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "generate until"));
+    for (uint32_t b = 0; b < B; ++b) {
+        counts_out[b] = count[b];
+        d->pos_host[b] = row0[b];
+        // Rows past a sequence's count hold nothing it emitted.
+        for (uint32_t r = count[b]; r < max_tokens; ++r) ids_out[(size_t)r * B + b] = 0;
+    }
     return QWH_OK;
 }
 

@@ -623,69 +623,147 @@ __global__ __launch_bounds__(256) void gemv_q8_generic_kernel(const GemvQ8Args a
 }
 
 // ---------------------------------------------------------------------------
-// q5 (quant.zig:253-269): per group of 64 codes, 32 bytes of low nibbles
-// (even column in the low nibble) and 8 bytes of fifth bits (bit j % 8 of
-// byte j / 8 is the fifth bit of column j). A lane takes a 32-column half
-// group ("slice"): two 8-byte loads of nibbles (a group is 40 bytes, so a
-// slice is only 8-byte aligned) and the slice's 4 bytes of fifth bits.
+// Byte-plane GEMV for q5 and q8 (quant.zig:253-269 and :270-288 planes).
 //
-// Arithmetic. The codes are expanded to bytes u = nibble | fifth << 4 in
-// [0, 31], in the column order of the batch GEMV: within each 8-column block
-// the bytes of columns {0,2,4,6}, then {1,3,5,7} (a nibble mask splits the
-// packed bytes that way; the fifth bits of those four columns are bits
-// 0,2,4,6 of one byte, moved to bit 4 of bytes 0..3 by one multiply --
-// (b & 0x55) * 0x00410410 has them at bits 4, 12, 20, 28 and no carry reaches
-// those bits). The activations of a 32-column chunk are written as
-// x_int = rint(x * 2^(22-e)) (2^e bounds the chunk's |x|) in three signed
-// base-256 digit planes d0 + 256 d1 + 65536 d2, stored in the same column
-// order, so that v_dot4_i32_i8 multiplies matching columns. With S_j the
-// chunk's sum of plane j's digits,
-//     sum (u - 16) x_int = sum_j 256^j (sum u d_j - 16 S_j),
-// each plane's term exact in int32 (below 2^18), combined in f32 and scaled
+// A lane takes a 32-column half group ("slice") of its row:
+//   q5  two 8-byte loads of nibbles (a group is 40 bytes: 32 bytes of low
+//       nibbles, even column in the low nibble, then 8 bytes of fifth bits,
+//       bit j % 8 of byte j / 8 for column j; so a slice is only 8-byte
+//       aligned) and the slice's 4 bytes of fifth bits;
+//   q8  two 16-byte loads of 32 codes.
+//
+// Arithmetic. The codes are turned into bytes in one fixed column order:
+// within each 8-column block, columns {0,2,4,6} then {1,3,5,7}.
+//   q5  a nibble mask splits the packed bytes that way; the fifth bits of
+//       those four columns are bits 0,2,4,6 of one byte, moved to bit 4 of
+//       bytes 0..3 by one multiply ((b & 0x55) * 0x00410410 has them at bits
+//       4, 12, 20, 28 and no carry reaches those bits): u = nibble |
+//       fifth << 4 in [0, 31];
+//   q8  v_perm_b32 picks the even and the odd bytes of the block's two code
+//       words, and XOR 0x80 makes each byte the signed code u - 128.
+// The activations of a 32-column chunk are written as x_int = rint(x *
+// 2^(22-e)) (2^e bounds the chunk's |x|) in three signed base-256 digit
+// planes d0 + 256 d1 + 65536 d2, stored in the same column order, so that
+// v_dot4_i32_i8 multiplies matching columns. With S_j the chunk's sum of plane
+// j's digits,
+//     q5: sum (u - 16) x_int = sum_j 256^j (sum u d_j - 16 S_j),
+//     q8: sum (u - 128) x_int = sum_j 256^j sum (u - 128) d_j,
+// each plane's term exact in int32 (below 2^19), combined in f32 and scaled
 // by the group's f16 scale times 2^(e-22).
+//
+// The activations are f32 values each workgroup encodes into LDS once (as
+// they are, or after RMSNorm, kernels.zig:274-300); the output is the row
+// products plus an optional residual, or siluMul of gate / up row pairs
+// (kernels.zig:233-239), as in the q4 kernel.
 // ---------------------------------------------------------------------------
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-struct Slice5 {
+enum class Fmt8 : int { Q5 = 0, Q8 = 1 };
+
+template <Fmt8 F>
+struct Slice8;
+template <>
+struct Slice8<Fmt8::Q5> {
     u32x2 lo0, lo1;  // nibbles of columns 0..15 and 16..31
     uint32_t hi;     // fifth bits of columns 0..31 (byte q: columns 8q..8q+7)
     uint16_t scale;
 };
+template <>
+struct Slice8<Fmt8::Q8> {
+    u32x4 a, b;      // codes of columns 0..15 and 16..31
+    uint16_t scale;
+};
 
-struct Act5Lds {
+struct Act8Lds {
     uint32_t words[kMaxChunks * 24];  // chunk c: plane j dword m at 24c + 8j + m
     int sums[kMaxChunks * 4];         // chunk c: S_j at 4c + j
     float mult[kMaxChunks];
+    float partial[4];                 // RMSNorm: the waves' sums of squares
 };
 
-struct GemvQ5Args {
+struct GemvB8Args {
     const float *x;         // tokens x K
+    const float *norm;      // RmsNorm: K weights
+    float eps;
     const uint16_t *scales; // N * K/64
-    const uint8_t *data;    // N * K/64 * 40
-    float *out;             // tokens x N
+    const uint8_t *data;    // q5: N * K/64 * 40, q8: N * K
+    float *out;             // tokens x N, or tokens x N/2 with pairs
+    const float *residual;  // optional, tokens x N (may alias out); not with pairs
     uint32_t n, k, t, row_groups;  // t = K/32 slices per row
+    uint32_t pairs;         // rows 2j, 2j+1 are gate_j, up_j: write silu(gate_j) * up_j
 };
 
-// Encodes the token's K activations into LDS (block-wide; thread t takes
-// values 8t .. 8t+7 of each 2048-value stretch, four threads per chunk).
-__device__ __forceinline__ void block_encode5(const GemvQ5Args &a, uint32_t token, Act5Lds &lds) {
+template <Fmt8 F>
+__device__ __forceinline__ uint32_t b8_row_bytes(uint32_t gpr) {
+    return F == Fmt8::Q5 ? gpr * 40u : gpr * 64u;
+}
+
+// The row's values (and RMSNorm weights) this thread encodes: thread t takes
+// values 8t .. 8t+7 of each 2048-value stretch (threads past the row's end
+// load its last 8 values and drop them when encoding). Fetched before the
+// first unit's weights are requested, so the wait for them leaves the weight
+// loads in flight.
+template <Src M>
+__device__ __forceinline__ void fetch_row(const float *x, const float *norm, uint32_t k, RowValues &rv) {
     const int tid = threadIdx.x;
-    const uint32_t k8 = a.k / 8;
-    const float4 *row = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k);
+    const uint32_t k8 = k / 8;
+    const float4 *row = reinterpret_cast<const float4 *>(x);
+    const float4 *w = reinterpret_cast<const float4 *>(norm);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        if (p * 256 >= (int)k8) break;  // uniform
+        const uint32_t e8 = tid + p * 256 < k8 ? tid + p * 256 : k8 - 1;
+        const float4 lo = row[e8 * 2], hi = row[e8 * 2 + 1];
+        rv.v[p][0] = lo.x; rv.v[p][1] = lo.y; rv.v[p][2] = lo.z; rv.v[p][3] = lo.w;
+        rv.v[p][4] = hi.x; rv.v[p][5] = hi.y; rv.v[p][6] = hi.z; rv.v[p][7] = hi.w;
+        if constexpr (M == Src::RmsNorm) {
+            const float4 wl = w[e8 * 2], wh = w[e8 * 2 + 1];
+            rv.w[p][0] = wl.x; rv.w[p][1] = wl.y; rv.w[p][2] = wl.z; rv.w[p][3] = wl.w;
+            rv.w[p][4] = wh.x; rv.w[p][5] = wh.y; rv.w[p][6] = wh.z; rv.w[p][7] = wh.w;
+        }
+    }
+}
+
+// Encodes the fetched row into LDS as byte digit planes (block-wide; four
+// consecutive threads per 32-value chunk), after RMSNorm (math.zig:120-130:
+// x * (1 / sqrt(mean(x^2) + eps)) * w, the sum of squares reduced over the
+// block in a fixed order) in that form.
+template <Src M>
+__device__ __forceinline__ void block_encode8(const RowValues &rv, uint32_t k, float eps, Act8Lds &lds) {
+    const int tid = threadIdx.x;
+    const uint32_t k8 = k / 8;
+    float v[3][8];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const bool in = p * 256 < (int)k8 && tid + p * 256 < k8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[p][i] = in ? rv.v[p][i] : 0.0f;
+    }
+    if constexpr (M == Src::RmsNorm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss = __fadd_rn(ss, __fmul_rn(v[p][i], v[p][i]));
+        ss = dev::wave_sum(ss);
+        if ((tid & 63) == 0) lds.partial[tid >> 6] = ss;
+        __syncthreads();
+        ss = ((lds.partial[0] + lds.partial[1]) + lds.partial[2]) + lds.partial[3];
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)k), eps)));
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[p][i] = p * 256 < (int)k8 ? __fmul_rn(__fmul_rn(v[p][i], inv), rv.w[p][i]) : 0.0f;
+    }
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
         if (p * 256 >= (int)k8) break;  // uniform
         const uint32_t e8 = tid + p * 256;
         const bool in = e8 < k8;
-        const uint32_t ec = in ? e8 : k8 - 1;
-        const float4 lo = row[ec * 2], hi = row[ec * 2 + 1];
-        float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (!in) v[i] = 0.0f;
-            amax = fmaxf(amax, fabsf(v[i]));
-        }
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[p][i]));
         amax = fmaxf(amax, dev::xor_lane<1>(amax));
         amax = fmaxf(amax, dev::xor_lane<2>(amax));
         const int e = dev::chunk_exponent(amax);
@@ -694,7 +772,7 @@ __device__ __forceinline__ void block_encode5(const GemvQ5Args &a, uint32_t toke
         // (adding 0x808080 makes each digit d + 128 with no carries).
         uint32_t u[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
+        for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[p][i] * up) + 0x808080) ^ 0x808080u;
         uint32_t planes[6];
         int sums[3];
 #pragma unroll
@@ -730,16 +808,17 @@ __device__ __forceinline__ void block_encode5(const GemvQ5Args &a, uint32_t toke
     __syncthreads();
 }
 
-// The activation operands of chunk c from LDS: digit planes, -16 times each
-// plane's digit sum (the bias term, the start of that plane's dot chain),
-// and the chunk multiplier.
-struct Act5 {
+// The activation operands of chunk c from LDS: digit planes, the bias term
+// that starts each plane's dot chain (q5: -16 times the plane's digit sum;
+// q8: none), and the chunk multiplier.
+struct Act8 {
     uint32_t d[24];
     int bias[3];
     float mult;
 };
 
-__device__ __forceinline__ void load_act5(const Act5Lds &lds, uint32_t c, Act5 &x) {
+template <Fmt8 F>
+__device__ __forceinline__ void load_act8(const Act8Lds &lds, uint32_t c, Act8 &x) {
     const uint4 *src = reinterpret_cast<const uint4 *>(&lds.words[c * 24]);
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
@@ -749,15 +828,19 @@ __device__ __forceinline__ void load_act5(const Act5Lds &lds, uint32_t c, Act5 &
         x.d[j * 4 + 2] = w.z;
         x.d[j * 4 + 3] = w.w;
     }
-    const int4 sv = *reinterpret_cast<const int4 *>(&lds.sums[c * 4]);
-    x.bias[0] = -16 * sv.x;
-    x.bias[1] = -16 * sv.y;
-    x.bias[2] = -16 * sv.z;
+    if constexpr (F == Fmt8::Q5) {
+        const int4 sv = *reinterpret_cast<const int4 *>(&lds.sums[c * 4]);
+        x.bias[0] = -16 * sv.x;
+        x.bias[1] = -16 * sv.y;
+        x.bias[2] = -16 * sv.z;
+    } else {
+        x.bias[0] = x.bias[1] = x.bias[2] = 0;
+    }
     x.mult = lds.mult[c];
 }
 
-// sum (u - 16) x_int of one slice, in f32 (the integer plane terms exact).
-__device__ __forceinline__ float q5_slice_dot(const Slice5 &sl, const Act5 &x) {
+// sum (u - bias) x_int of one slice, in f32 (the integer plane terms exact).
+__device__ __forceinline__ float b8_slice_dot(const Slice8<Fmt8::Q5> &sl, const Act8 &x) {
     const uint32_t w[4] = {sl.lo0.x, sl.lo0.y, sl.lo1.x, sl.lo1.y};
     // Fifth bits of the even and of the odd columns, each byte's four at bits
     // 0, 2, 4, 6 (so one bit-field extract per byte below).
@@ -779,22 +862,49 @@ __device__ __forceinline__ float q5_slice_dot(const Slice5 &sl, const Act5 &x) {
     return ((float)p2 * 65536.0f + (float)p1 * 256.0f) + (float)p0;
 }
 
-__device__ __forceinline__ Slice5 load_slice5(const GemvQ5Args &a, uint32_t row, uint32_t c, uint32_t row_bytes,
-                                              uint32_t gpr) {
-    const uint8_t *base = a.data + (row * row_bytes + (c >> 1) * 40u);
-    Slice5 sl;
-    sl.lo0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base + (c & 1u) * 16u));
-    sl.lo1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base + (c & 1u) * 16u + 8u));
-    sl.hi = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(base + 32u + (c & 1u) * 4u));
+__device__ __forceinline__ float b8_slice_dot(const Slice8<Fmt8::Q8> &sl, const Act8 &x) {
+    const uint32_t w[8] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b.x, sl.b.y, sl.b.z, sl.b.w};
+    int p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // Bytes of columns {0,2,4,6} and {1,3,5,7} of block q, as u - 128.
+        const int even = (int)(__builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], 0x06040200u) ^ 0x80808080u);
+        const int odd = (int)(__builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], 0x07050301u) ^ 0x80808080u);
+        const int m = 2 * q;
+        p0 = __builtin_amdgcn_sdot4(even, (int)x.d[m], p0, false);
+        p1 = __builtin_amdgcn_sdot4(even, (int)x.d[8 + m], p1, false);
+        p2 = __builtin_amdgcn_sdot4(even, (int)x.d[16 + m], p2, false);
+        p0 = __builtin_amdgcn_sdot4(odd, (int)x.d[m + 1], p0, false);
+        p1 = __builtin_amdgcn_sdot4(odd, (int)x.d[8 + m + 1], p1, false);
+        p2 = __builtin_amdgcn_sdot4(odd, (int)x.d[16 + m + 1], p2, false);
+    }
+    return ((float)p2 * 65536.0f + (float)p1 * 256.0f) + (float)p0;
+}
+
+template <Fmt8 F>
+__device__ __forceinline__ Slice8<F> load_slice8(const GemvB8Args &a, uint32_t row, uint32_t c, uint32_t row_bytes,
+                                                 uint32_t gpr) {
+    Slice8<F> sl;
+    if constexpr (F == Fmt8::Q5) {
+        const uint8_t *base = a.data + (row * row_bytes + (c >> 1) * 40u);
+        sl.lo0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base + (c & 1u) * 16u));
+        sl.lo1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base + (c & 1u) * 16u + 8u));
+        sl.hi = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(base + 32u + (c & 1u) * 4u));
+    } else {
+        const uint8_t *base = a.data + (row * row_bytes + c * 32u);
+        sl.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base));
+        sl.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + 16u));
+    }
     sl.scale = load_scale(a.scales, row * gpr + (c >> 1));
     return sl;
 }
 
 // Lane mapping and unit walk as the q4 kernel (RG = 64/L rows per row group,
 // S slices per lane, U row groups per unit, grid-stride units, the next
-// unit's loads issued before the current one is multiplied).
-template <int S, int L, int U>
-__global__ __launch_bounds__(256) void gemv_q5_kernel(const GemvQ5Args a) {
+// unit's loads issued before the current one is multiplied; the row's
+// values are fetched before the first weights).
+template <Fmt8 F, int S, int L, int U, Src M>
+__global__ __launch_bounds__(256) void gemv_b8_kernel(const GemvB8Args a) {
     constexpr int RG = 64 / L;
     constexpr int log_l = Log2<L>::value;
     constexpr int log_u = Log2<U>::value;
@@ -805,85 +915,115 @@ __global__ __launch_bounds__(256) void gemv_q5_kernel(const GemvQ5Args a) {
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
     const uint32_t token = blockIdx.y;
     const uint32_t gpr = a.k >> 6;
-    const uint32_t row_bytes = gpr * 40u;
+    const uint32_t row_bytes = b8_row_bytes<F>(gpr);
     const uint32_t units = (a.row_groups + U - 1) / U;
     const uint32_t full_units = a.n / (U * RG);
     const uint32_t count = full_units > wave ? (full_units - wave + nwaves - 1) / nwaves : 0;
-    float *out = a.out + (size_t)token * a.n;
+    float *out = a.out + (size_t)token * (a.pairs ? a.n / 2 : a.n);
+    const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
 
     // Rows past the end (only in the last, partial unit) load the last row
     // and are dropped at the store.
-    auto load = [&](Slice5 (&dst)[U][S], uint32_t unit) __attribute__((always_inline)) {
+    auto load = [&](Slice8<F> (&dst)[U][S], uint32_t unit) __attribute__((always_inline)) {
         const uint32_t row0 = unit * (U * RG) + rr;
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 const uint32_t row = row0 + u * RG < a.n ? row0 + u * RG : a.n - 1;
-                dst[u][s] = load_slice5(a, row, li + s * L, row_bytes, gpr);
+                dst[u][s] = load_slice8<F>(a, row, li + s * L, row_bytes, gpr);
             }
     };
+    auto load_res = [&](uint32_t unit) -> float {
+        const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+        return residual && row < a.n ? residual[row] : 0.0f;
+    };
 
-    Slice5 A[U][S], B[U][S];
-    __shared__ __attribute__((aligned(16))) Act5Lds lds;
+    Slice8<F> A[U][S], B[U][S];
+    RowValues rv;
+    fetch_row<M>(a.x + (size_t)token * a.k, a.norm, a.k, rv);
     load(A, count ? wave : (full_units ? full_units - 1 : 0));
-    block_encode5(a, token, lds);
-    Act5 X[S];
+    __shared__ __attribute__((aligned(16))) Act8Lds lds;
+    block_encode8<M>(rv, a.k, a.eps, lds);
+    Act8 X[S];
 #pragma unroll
-    for (int s = 0; s < S; ++s) load_act5(lds, li + s * L, X[s]);
+    for (int s = 0; s < S; ++s) load_act8<F>(lds, li + s * L, X[s]);
+    float resA = count ? load_res(wave) : 0.0f, resB = 0.0f;
 
-    auto process = [&](const Slice5 (&src)[U][S], uint32_t unit) __attribute__((always_inline)) {
+    auto process = [&](const Slice8<F> (&src)[U][S], float res, uint32_t unit) __attribute__((always_inline)) {
         float acc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const float part = q5_slice_dot(src[u][s], X[s]) * (dev::f16_bits_to_f32(src[u][s].scale) * X[s].mult);
+                const float part = b8_slice_dot(src[u][s], X[s]) * (dev::f16_bits_to_f32(src[u][s].scale) * X[s].mult);
                 acc[u] = s == 0 ? part : acc[u] + part;
             }
         }
         const float total = reduce_rows<U, L>(acc, lane);
+        const bool writer = (li & ((L >> log_u) - 1)) == 0;
         const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
-        if ((li & ((L >> log_u) - 1)) == 0 && row < a.n) out[row] = total;
+        if (a.pairs) {
+            // Row + 1 sits in the next row of the row group (RG > 1), else
+            // in the next of the unit's U row groups.
+            const float partner = __shfl_down(total, RG > 1 ? L : (L >> log_u), kWave);
+            if (writer && (row & 1u) == 0 && row < a.n) out[row >> 1] = silu_mul(total, partner);
+        } else if (writer && row < a.n) {
+            out[row] = res + total;
+        }
     };
 
     uint32_t i = 0;
     for (; i + 1 < count; i += 2) {
         const uint32_t ua = wave + i * nwaves, ub = ua + nwaves;
         load(B, ub);
-        process(A, ua);
-        load(A, i + 2 < count ? ub + nwaves : ub);
-        process(B, ub);
+        resB = load_res(ub);
+        process(A, resA, ua);
+        const uint32_t un = i + 2 < count ? ub + nwaves : ub;
+        load(A, un);
+        resA = load_res(un);
+        process(B, resB, ub);
     }
-    if (i < count) process(A, wave + i * nwaves);
+    if (i < count) process(A, resA, wave + i * nwaves);
     if (full_units < units && full_units % nwaves == wave) {
         load(B, full_units);
-        process(B, full_units);
+        process(B, load_res(full_units), full_units);
     }
 }
 
-// Any K up to the LDS encoding's 6144: one wavefront per row, lanes striding
-// over the row's slices.
-__global__ __launch_bounds__(256) void gemv_q5_generic_kernel(const GemvQ5Args a) {
+// Any K up to the LDS encoding's 6144: one wavefront per row (per row pair
+// with pairs), lanes striding over the row's slices.
+template <Fmt8 F, Src M>
+__global__ __launch_bounds__(256) void gemv_b8_generic_kernel(const GemvB8Args a) {
     const int lane = threadIdx.x & 63;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
     const uint32_t token = blockIdx.y;
     const uint32_t gpr = a.k >> 6;
-    const uint32_t row_bytes = gpr * 40u;
-    __shared__ __attribute__((aligned(16))) Act5Lds lds;
-    block_encode5(a, token, lds);
-    float *out = a.out + (size_t)token * a.n;
-    for (uint32_t row = wave; row < a.n; row += nwaves) {
-        float acc = 0.0f;
-        for (uint32_t c = lane; c < a.t; c += 64) {
-            Act5 x;
-            load_act5(lds, c, x);
-            const Slice5 sl = load_slice5(a, row, c, row_bytes, gpr);
-            acc += q5_slice_dot(sl, x) * (dev::f16_bits_to_f32(sl.scale) * x.mult);
+    const uint32_t row_bytes = b8_row_bytes<F>(gpr);
+    __shared__ __attribute__((aligned(16))) Act8Lds lds;
+    RowValues rv;
+    fetch_row<M>(a.x + (size_t)token * a.k, a.norm, a.k, rv);
+    block_encode8<M>(rv, a.k, a.eps, lds);
+    float *out = a.out + (size_t)token * (a.pairs ? a.n / 2 : a.n);
+    const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
+    const uint32_t per = a.pairs ? 2u : 1u;
+    for (uint32_t first = wave * per; first < a.n; first += nwaves * per) {
+        float tot[2] = {0.0f, 0.0f};
+        for (uint32_t r = 0; r < per; ++r) {
+            float acc = 0.0f;
+            for (uint32_t c = lane; c < a.t; c += 64) {
+                Act8 x;
+                load_act8<F>(lds, c, x);
+                const Slice8<F> sl = load_slice8<F>(a, first + r, c, row_bytes, gpr);
+                acc += b8_slice_dot(sl, x) * (dev::f16_bits_to_f32(sl.scale) * x.mult);
+            }
+            tot[r] = dev::wave_sum(acc);
         }
-        acc = dev::wave_sum(acc);
-        if (lane == 0) out[row] = acc;
+        if (lane == 0) {
+            if (a.pairs) out[first >> 1] = silu_mul(tot[0], tot[1]);
+            else out[first] = (residual ? residual[first] : 0.0f) + tot[0];
+        }
     }
 }
 
@@ -1100,44 +1240,68 @@ hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &
     return hipGetLastError();
 }
 
-bool gemv_q5_supported(uint32_t rows, uint32_t cols) {
+bool gemv_b8_supported(int format, uint32_t rows, uint32_t cols) {
     // The activations are encoded into LDS (at most kMaxChunks chunks), and
     // the kernels address the data plane with 32-bit offsets.
-    return cols % 64 == 0 && cols / 32 <= (uint32_t)kMaxChunks && (uint64_t)rows * (cols / 64) * 40 < (1ull << 32) &&
-           (uint64_t)rows * 4096ull < (1ull << 32);
+    const uint64_t per_group = format == QWH_FORMAT_Q5 ? 40 : format == QWH_FORMAT_Q8 ? 64 : 0;
+    return per_group && cols % 64 == 0 && cols / 32 <= (uint32_t)kMaxChunks &&
+           (uint64_t)rows * (cols / 64) * per_group < (1ull << 32) && (uint64_t)rows * 4096ull < (1ull << 32);
 }
 
-#define QWH_GEMV5_CASE(S_, L_, U_)                                                                 \
+namespace {
+
+template <Fmt8 F, Src M>
+hipError_t dispatch_b8(hipStream_t s, int cus, GemvB8Args args, uint32_t tokens) {
+    const uint32_t L = gcd_u32(args.t, 64);
+    const uint32_t S = args.t / L;
+#define QWH_GEMV_B8_CASE(S_, L_, U_)                                                               \
     if (S == S_ && L == L_) {                                                                      \
         args.row_groups = (args.n + (64 / L_) - 1) / (64 / L_);                                    \
         const uint32_t units = (args.row_groups + U_ - 1) / U_;                                    \
-        auto kernel = gemv_q5_kernel<S_, L_, U_>;                                                  \
+        auto kernel = gemv_b8_kernel<F, S_, L_, U_, M>;                                            \
         kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);                \
         return hipGetLastError();                                                                  \
     }
+    QWH_GEMV_B8_CASE(1, 64, 4)
+    QWH_GEMV_B8_CASE(1, 32, 4)
+    QWH_GEMV_B8_CASE(1, 16, 4)
+    QWH_GEMV_B8_CASE(1, 8, 4)
+    QWH_GEMV_B8_CASE(2, 64, 2)
+    QWH_GEMV_B8_CASE(3, 64, 2)
+    QWH_GEMV_B8_CASE(3, 32, 2)
+#undef QWH_GEMV_B8_CASE
+    args.row_groups = args.n;
+    auto kernel = gemv_b8_generic_kernel<F, M>;
+    const uint32_t work = args.pairs ? args.n / 2 : args.n;
+    kernel<<<dim3(grid_blocks(kernel, work, cus), tokens), 256, 0, s>>>(args);
+    return hipGetLastError();
+}
 
-hipError_t launch_gemv_q5(hipStream_t s, int cus, const float *x, const Matrix &w, uint32_t tokens, float *out) {
-    if (!gemv_q5_supported(w.rows, w.cols)) return hipErrorNotSupported;
-    GemvQ5Args args{};
-    const uint32_t T = w.cols / 32;
-    args.x = x;
+}  // namespace
+
+hipError_t launch_gemv_b8(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens, float *out,
+                          const float *residual) {
+    if (!gemv_b8_supported(w.format, w.rows, w.cols)) return hipErrorNotSupported;
+    if (in.mode != GemvInput::F32 && in.mode != GemvInput::RmsNorm) return hipErrorNotSupported;
+    if (in.pairs && ((w.rows & 1u) || residual)) return hipErrorInvalidValue;
+    GemvB8Args args{};
+    args.x = in.x;
+    args.norm = in.norm;
+    args.eps = in.eps;
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
     args.data = w.data;
     args.out = out;
+    args.residual = residual;
     args.n = w.rows;
     args.k = w.cols;
-    args.t = T;
-    const uint32_t L = gcd_u32(T, 64);
-    const uint32_t S = T / L;
-    QWH_GEMV5_CASE(1, 64, 4)
-    QWH_GEMV5_CASE(1, 32, 4)
-    QWH_GEMV5_CASE(1, 16, 4)
-    QWH_GEMV5_CASE(2, 64, 2)
-    QWH_GEMV5_CASE(3, 64, 2)
-    QWH_GEMV5_CASE(3, 32, 2)
-    args.row_groups = w.rows;
-    gemv_q5_generic_kernel<<<dim3(grid_blocks(gemv_q5_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
-    return hipGetLastError();
+    args.t = w.cols / 32;
+    args.pairs = in.pairs ? 1u : 0u;
+    const bool rms = in.mode == GemvInput::RmsNorm;
+    if (w.format == QWH_FORMAT_Q5)
+        return rms ? dispatch_b8<Fmt8::Q5, Src::RmsNorm>(s, cus, args, tokens)
+                   : dispatch_b8<Fmt8::Q5, Src::F32>(s, cus, args, tokens);
+    return rms ? dispatch_b8<Fmt8::Q8, Src::RmsNorm>(s, cus, args, tokens)
+               : dispatch_b8<Fmt8::Q8, Src::F32>(s, cus, args, tokens);
 }
 
 }  // namespace qwh

@@ -1,11 +1,11 @@
-// Small-batch q4 GEMV on the matrix cores: kernels.zig:118-158
+// Small-batch q4 / q8 GEMV on the matrix cores: kernels.zig:118-158
 // linearQuantized for 2 or more tokens (the decoder step at batch > 1).
 //
 // One v_mfma_i32_16x16x64_i8 multiplies 16 tokens by 16 weight rows over 64
 // consecutive columns -- exactly one quantization group (quant.zig:49), so
 // its integer result takes that group's single f16 scale per row. The
 // operands are exact integers:
-//   weights      the q4 codes u - 8 as signed bytes;
+//   weights      the codes u - 8 (q4) or u - 128 (q8) as signed bytes;
 //   activations  per token and group, x_int = rint(x * 2^(22-e)) with 2^e
 //                bounding the group's largest |x| (|x_int| <= 2^22), written
 //                as three signed base-256 digit planes d0 + 256 d1 + 65536 d2
@@ -15,14 +15,14 @@
 //
 // Operand layout. Lane l of a wavefront feeds token (or weight row) l % 16
 // and the 16 columns 16 * (l / 16) .. +15 of the group. A lane's 16 codes are
-// 8 bytes of the row (two per byte, even column in the low nibble,
-// quant.zig:36-41); nibble masks split them into the bytes of columns
-// {0,2,4,6}, {1,3,5,7}, {8,10,12,14}, {9,11,13,15}. The activation digits are
-// stored in that same order, so byte b of both operands belongs to the same
-// column. Layout of the digits, per 16-token tile and group:
+// 8 bytes of a q4 row (two per byte, even column in the low nibble,
+// quant.zig:36-41), which nibble masks split into the bytes of columns
+// {0,2,4,6}, {1,3,5,7}, {8,10,12,14}, {9,11,13,15}; or 16 bytes of a q8 row,
+// which v_perm_b32 puts in that same order. The activation digits are stored
+// in that order too, so byte b of both operands belongs to the same column. Layout of the digits, per 16-token tile and group:
 //   digits[tile][g][plane][token 0..15][64 bytes],  mult[tile][g][16] f32.
 //
-// Work split: see gemv_q4_batch_kernel.
+// Work split: see gemv_batch_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -51,11 +51,39 @@ __device__ __forceinline__ v4i expand_q4(uint2 w) {
     return b;
 }
 
+// The same operand from 16 q8 codes (columns 0..15 in order): the even and
+// odd columns of each 8-column block picked by v_perm_b32, XOR 0x80 making
+// each byte the two's complement of u - 128.
+__device__ __forceinline__ v4i expand_q8(v4i n) {
+    v4i b;
+    b.x = (int)(__builtin_amdgcn_perm((uint32_t)n.y, (uint32_t)n.x, 0x06040200u) ^ 0x80808080u);
+    b.y = (int)(__builtin_amdgcn_perm((uint32_t)n.y, (uint32_t)n.x, 0x07050301u) ^ 0x80808080u);
+    b.z = (int)(__builtin_amdgcn_perm((uint32_t)n.w, (uint32_t)n.z, 0x06040200u) ^ 0x80808080u);
+    b.w = (int)(__builtin_amdgcn_perm((uint32_t)n.w, (uint32_t)n.z, 0x07050301u) ^ 0x80808080u);
+    return b;
+}
+
+// The weight operand of group i, rows r of a wavefront's LDS transpose
+// (PPR 16-byte pieces per row, piece p of row r at slot p ^ (r mod PPR)):
+// BPG = 32 (q4) or 64 (q8) code bytes per group.
+template <int BPG, int PPR>
+__device__ __forceinline__ v4i weight_operand(const v4i *wl, int r, int i, int blk) {
+    if constexpr (BPG == 32) {
+        const int piece = 2 * i + (blk >> 1);
+        const uint2 w8 = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(&wl[r * PPR + (piece ^ (r % PPR))]) +
+                                                          8 * (blk & 1));
+        return expand_q4(w8);
+    } else {
+        const int piece = 4 * i + blk;
+        return expand_q8(wl[r * PPR + (piece ^ (r % PPR))]);
+    }
+}
+
 struct BatchArgs {
     const uint8_t *digits;   // [token tiles][groups][3][16][64]
     const float *mult;       // [token tiles][groups][16]
     const uint16_t *scales;  // N * K/64
-    const uint8_t *data;     // N * K/2
+    const uint8_t *data;     // N * K/64 * BPG
     float *out;              // tokens x N, or tokens x N/2 with pairs
     const float *residual;   // optional, tokens x N (may alias out); not with pairs
     const float *ss;         // non-null: RMSNorm sums of squares [token][ss_parts]; results x 1/rms
@@ -94,7 +122,7 @@ __device__ __forceinline__ void tile_rms_inverse(const float *parts, uint32_t n,
 // takes units w, w + W, ...), and their partial sums are added in wavefront
 // order through LDS (deterministic). A wavefront issues all loads of a unit
 // at once -- one memory round trip per unit:
-//   weights  TILES x 16 rows x GR x 32 B, as 16-byte pieces, 64/(2 GR) rows
+//   weights  TILES x 16 rows x GR x BPG B, as 16-byte pieces, 64/PPR rows
 //            per load instruction (each instruction reads whole GR x 32-byte
 //            stretches of rows, which streams; 8-byte loads of 16 rows per
 //            instruction measured 35 % slower), then moved through this
@@ -103,10 +131,10 @@ __device__ __forceinline__ void tile_rms_inverse(const float *parts, uint32_t n,
 //            banks);
 //   digits   GR x 3 planes x 16 bytes per lane;
 //   scales   GR per row (one load per tile), multipliers GR float4s.
-template <int TILES, int GR>
+template <int TILES, int GR, int BPG>
 struct BatchShape {
     static constexpr int ROWS = kRowTile * TILES;
-    static constexpr int PPR = 2 * GR;            // 16-byte pieces of a row in a unit
+    static constexpr int PPR = BPG * GR / 16;     // 16-byte pieces of a row in a unit
     static constexpr int RPI = 64 / PPR;          // rows per load instruction
     static constexpr int NW = (ROWS + RPI - 1) / RPI;  // weight loads per lane and unit
     static constexpr int WAVE_BYTES = ROWS * PPR * 16 + TILES * 4 * 64 * 4;  // transpose + partial sums
@@ -118,9 +146,9 @@ struct BatchShape {
 template <int TILES>
 constexpr int max_waves() { return TILES == 1 ? 12 : 8; }
 
-template <int TILES, int GR>
-__global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(const BatchArgs a) {
-    using S = BatchShape<TILES, GR>;
+template <int TILES, int GR, int BPG>
+__global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_batch_kernel(const BatchArgs a) {
+    using S = BatchShape<TILES, GR, BPG>;
     constexpr int ROWS = S::ROWS, PPR = S::PPR, RPI = S::RPI, NW = S::NW;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -131,7 +159,7 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(
     const uint32_t units = gpr / GR;
     const uint32_t tile = blockIdx.y;
     const uint32_t row0 = blockIdx.x * ROWS;
-    const size_t row_bytes = a.k >> 1;
+    const size_t row_bytes = (size_t)gpr * BPG;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint4 *wl = reinterpret_cast<uint4 *>(smem + (size_t)wave * ROWS * PPR * 16);   // this wave's transpose
     float *part = reinterpret_cast<float *>(smem + (size_t)waves * ROWS * PPR * 16);  // [W][TILES][4][64]
@@ -162,7 +190,7 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(
         for (int i = 0; i < NW; ++i) {
             uint32_t row = row0 + i * RPI + lane / PPR;
             if (row >= a.n) row = a.n - 1;
-            wv[i] = *reinterpret_cast<const uint4 *>(a.data + (size_t)row * row_bytes + g0 * 32 + 16 * (lane % PPR));
+            wv[i] = *reinterpret_cast<const uint4 *>(a.data + (size_t)row * row_bytes + g0 * BPG + 16 * (lane % PPR));
         }
         v4i dg[GR][3];
         float4 mt[GR];
@@ -193,10 +221,7 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_q4_batch_kernel(
 #pragma unroll
             for (int t = 0; t < TILES; ++t) {
                 const int r = t * kRowTile + col;
-                const int piece = 2 * i + (blk >> 1);
-                const uint2 w8 = *reinterpret_cast<const uint2 *>(
-                    reinterpret_cast<const uint8_t *>(&wl[r * PPR + (piece ^ (r % PPR))]) + 8 * (blk & 1));
-                const v4i b = expand_q4(w8);
+                const v4i b = weight_operand<BPG, PPR>(reinterpret_cast<const v4i *>(wl), r, i, blk);
                 const v4i zero = {0, 0, 0, 0};
                 const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dg[i][0], b, zero, 0, 0, 0);
                 const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dg[i][1], b, zero, 0, 0, 0);
@@ -278,10 +303,10 @@ struct SplitArgs {
 };
 
 
-template <int TW, int KC>
+template <int TW, int KC, int BPG>
 struct SplitShape {
     static constexpr int ROWS = kRowTile * TW;      // rows per wavefront
-    static constexpr int PPR = 2 * KC;              // 16-byte pieces of a row in a chunk
+    static constexpr int PPR = BPG * KC / 16;       // 16-byte pieces of a row in a chunk
     static constexpr int RPI = 64 / PPR;            // rows per load instruction
     static constexpr int NW = (ROWS + RPI - 1) / RPI;
     static constexpr int DPIECES = KC * 3 * 64;     // 16-byte digit pieces per chunk
@@ -289,9 +314,9 @@ struct SplitShape {
     static_assert(DPIECES % 256 == 0 && (PPR & (PPR - 1)) == 0 && ROWS % RPI == 0, "chunk shape");
 };
 
-template <int TW, int KC>
-__global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
-    using S = SplitShape<TW, KC>;
+template <int TW, int KC, int BPG>
+__global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
+    using S = SplitShape<TW, KC, BPG>;
     constexpr int ROWS = S::ROWS, PPR = S::PPR, RPI = S::RPI, NW = S::NW, DPT = S::DPT;
     __shared__ v4i dl[2][S::DPIECES];          // digit planes, [group][plane][lane]
     __shared__ float4 ml[2][KC * 4];             // multipliers, [group][lane / 16]
@@ -305,7 +330,7 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
     const uint32_t gpr = a.k >> 6;
     const uint32_t tile = blockIdx.z;
     const uint32_t row0 = (blockIdx.x * 4 + wave) * ROWS;
-    const size_t row_bytes = a.k >> 1;
+    const size_t row_bytes = (size_t)gpr * BPG;
     const uint32_t g_first = blockIdx.y * a.slice_groups;
     const uint32_t chunks = a.slice_groups / KC;
     const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes;
@@ -323,7 +348,7 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
         for (int i = 0; i < NW; ++i) {
             uint32_t row = row0 + i * RPI + lane / PPR;
             if (row >= a.n) row = a.n - 1;
-            rw[i] = *reinterpret_cast<const v4i *>(a.data + (size_t)row * row_bytes + g0 * 32 + 16 * (lane % PPR));
+            rw[i] = *reinterpret_cast<const v4i *>(a.data + (size_t)row * row_bytes + g0 * BPG + 16 * (lane % PPR));
         }
 #pragma unroll
         for (int m = 0; m < DPT; ++m) {
@@ -384,10 +409,7 @@ __global__ __launch_bounds__(256) void gemv_q4_split_kernel(const SplitArgs a) {
 #pragma unroll
             for (int t = 0; t < TW; ++t) {
                 const int r = t * kRowTile + col;
-                const int piece = 2 * i + (blk >> 1);
-                const uint2 w8 = *reinterpret_cast<const uint2 *>(
-                    reinterpret_cast<const uint8_t *>(&wl[r * PPR + (piece ^ (r % PPR))]) + 8 * (blk & 1));
-                const v4i b = expand_q4(w8);
+                const v4i b = weight_operand<BPG, PPR>(wl, r, i, blk);
                 const v4i zero = {0, 0, 0, 0};
                 const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d0, b, zero, 0, 0, 0);
                 const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d1, b, zero, 0, 0, 0);
@@ -733,14 +755,24 @@ SplitPlan split_plan(const Matrix &w) {
     return p;
 }
 
-void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint32_t tiles) {
+template <int BPG>
+void launch_split_bpg(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, dim3 grid) {
+    if (plan.tw == 2 && plan.kc == 4) gemv_split_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(a);
+    else if (plan.tw == 2) gemv_split_kernel<2, 8, BPG><<<grid, 256, 0, s>>>(a);
+    else if (plan.kc == 4) gemv_split_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(a);
+    else gemv_split_kernel<1, 8, BPG><<<grid, 256, 0, s>>>(a);
+}
+
+void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint32_t tiles, int format) {
     const uint32_t row_tiles = (a.n + kRowTile - 1) / kRowTile;
     const dim3 grid((row_tiles + 4u * plan.tw - 1) / (4u * plan.tw), plan.slices, tiles);
-    if (plan.tw == 2 && plan.kc == 4) gemv_q4_split_kernel<2, 4><<<grid, 256, 0, s>>>(a);
-    else if (plan.tw == 2) gemv_q4_split_kernel<2, 8><<<grid, 256, 0, s>>>(a);
-    else if (plan.kc == 4) gemv_q4_split_kernel<1, 4><<<grid, 256, 0, s>>>(a);
-    else gemv_q4_split_kernel<1, 8><<<grid, 256, 0, s>>>(a);
+    if (format == QWH_FORMAT_Q8) launch_split_bpg<64>(s, plan, a, grid);
+    else launch_split_bpg<32>(s, plan, a, grid);
 }
+
+// Formats with a matrix-core form: q4 and q8 (the codes are whole bytes or
+// nibbles; q5's 40-byte groups are not 16-byte pieces).
+bool batch_format(int format) { return format == QWH_FORMAT_Q4 || format == QWH_FORMAT_Q8; }
 
 SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const SplitPlan &plan,
                      const BatchNorm &norm) {
@@ -763,7 +795,10 @@ SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const
 
 }  // namespace
 
+bool gemv_batch_supported(const Matrix &w) { return batch_format(w.format) && w.cols % 64 == 0; }
+
 uint32_t batch_slices(const Matrix &w) {
+    if (!batch_format(w.format)) return 0;
     const SplitPlan p = split_plan(w);
     return p.tw ? p.slices : 0;
 }
@@ -772,19 +807,21 @@ size_t batch_partial_bytes(uint32_t tokens, const Matrix &w) {
     return (size_t)batch_slices(w) * tokens * w.rows * sizeof(float);
 }
 
-hipError_t launch_gemv_q4_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                      float *partials, const BatchNorm &norm) {
+hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
+                                   float *partials, const BatchNorm &norm) {
+    if (!batch_format(w.format)) return hipErrorNotSupported;
     const SplitPlan plan = split_plan(w);
     if (!plan.tw || !partials) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     SplitArgs a = split_args(digits, w, tokens, plan, norm);
     a.part = partials;
-    launch_split(s, plan, a, (tokens + kTokenTile - 1) / kTokenTile);
+    launch_split(s, plan, a, (tokens + kTokenTile - 1) / kTokenTile, w.format);
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens, float *out,
-                                const float *residual, bool pairs, float *partials, const BatchNorm &norm) {
+hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens, float *out,
+                             const float *residual, bool pairs, float *partials, const BatchNorm &norm) {
+    if (!batch_format(w.format)) return hipErrorNotSupported;
     if (pairs && (w.rows & 1u)) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
@@ -795,7 +832,7 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
         a.residual = residual;
         a.pairs = pairs ? 1u : 0u;
         if (plan.slices > 1) a.part = partials;
-        launch_split(s, plan, a, tiles);
+        launch_split(s, plan, a, tiles, w.format);
         if (plan.slices > 1) {
             const size_t items = (size_t)tokens * (pairs ? w.rows / 2 : w.rows);
             split_reduce_kernel<<<(uint32_t)((items + 255) / 256), 256, 0, s>>>(partials, plan.slices, tokens, w.rows,
@@ -827,17 +864,19 @@ hipError_t launch_gemv_q4_batch(hipStream_t s, const void *digits, const Matrix 
     while (gpr % (uint32_t)gr) gr >>= 1;
     const uint32_t units = gpr / (uint32_t)gr;
     const dim3 grid(row_tiles, tiles);
-#define QWH_BATCH_CASE(G_)                                                                           \
-    if (gr == G_) {                                                                                  \
-        using S = BatchShape<1, G_>;                                                                 \
+#define QWH_BATCH_CASE(G_, B_)                                                                       \
+    if (gr == G_ && bpg == B_) {                                                                     \
+        using S = BatchShape<1, G_, B_>;                                                             \
         /* Wavefronts: the largest divisor of the unit count within the cap and 64 KB of LDS. */     \
         uint32_t waves = 1;                                                                          \
         for (uint32_t c = 1; c <= (uint32_t)max_waves<1>() && c * S::WAVE_BYTES <= 65536u; ++c)      \
             if (units % c == 0) waves = c;                                                           \
-        gemv_q4_batch_kernel<1, G_><<<grid, 64 * waves, waves * S::WAVE_BYTES, s>>>(a);              \
+        gemv_batch_kernel<1, G_, B_><<<grid, 64 * waves, waves * S::WAVE_BYTES, s>>>(a);             \
         return hipGetLastError();                                                                    \
     }
-    QWH_BATCH_CASE(8) QWH_BATCH_CASE(4) QWH_BATCH_CASE(2) QWH_BATCH_CASE(1)
+    const int bpg = w.format == QWH_FORMAT_Q8 ? 64 : 32;
+    QWH_BATCH_CASE(8, 32) QWH_BATCH_CASE(4, 32) QWH_BATCH_CASE(2, 32) QWH_BATCH_CASE(1, 32)
+    QWH_BATCH_CASE(8, 64) QWH_BATCH_CASE(4, 64) QWH_BATCH_CASE(2, 64) QWH_BATCH_CASE(1, 64)
 #undef QWH_BATCH_CASE
     return hipErrorInvalidValue;
 }

@@ -10,7 +10,10 @@ logits, so that a consumer can tell a flip between near-tied tokens (float
 summation order) from a wrong result.
 
 Usage: python3 tests/golden/make_decoder_ids.py [--batch 16] [--steps 256]
+                [--format 16|17|18]
 (the oracle is single-sequence at a time; about 0.3 s per step on 8 threads).
+--format quantizes every matrix of the same synthetic model to q4 (16, the
+default: decoder_1p7b_ids.json), q5 (17) or q8 (18: decoder_1p7b_q8_ids.json).
 """
 import argparse
 import json
@@ -36,11 +39,14 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--threads", type=int, default=os.cpu_count() or 1)
-    ap.add_argument("--out", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "decoder_1p7b_ids.json"))
+    ap.add_argument("--format", type=int, default=o.Q4, choices=(o.Q4, o.Q5, o.Q8))
+    ap.add_argument("--out", default=None)
     args = ap.parse_args()
+    suffix = {o.Q4: "", o.Q5: "_q5", o.Q8: "_q8"}[args.format]
+    out = args.out or os.path.join(os.path.dirname(os.path.abspath(__file__)), f"decoder_1p7b{suffix}_ids.json")
     o.set_threads(args.threads)
     t0 = time.time()
-    dec = o.Decoder(SEED, args.batch, **CONFIG)
+    dec = o.Decoder(SEED, args.batch, args.format, **CONFIG)
     print(f"model built in {time.time() - t0:.0f} s", flush=True)
     ids, runner_up, top, second = [], [], [], []
     for b in range(args.batch):
@@ -62,8 +68,8 @@ def main():
         top.append(l1)
         second.append(l2)
         print(f"sequence {b}: {args.steps} steps, {time.time() - t0:.0f} s", flush=True)
-        with open(args.out, "w") as f:
-            json.dump({"config": CONFIG, "seed": SEED, "prefill": PREFILL, "steps": args.steps,
+        with open(out, "w") as f:
+            json.dump({"config": CONFIG, "seed": SEED, "prefill": PREFILL, "steps": args.steps, "format": args.format,
                        "note": "ids[b][0] is the start token; ids[b][1:] the greedy steps; "
                                "runner_up[b][s], top[b][s], second[b][s]: the second-best token of "
                                "step s and the two largest logits",

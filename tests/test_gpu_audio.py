@@ -201,8 +201,10 @@ def test_audio_projector(ctx):
 
 def test_audio_attention_rejects_too_many_windows(ctx):
     # 70000 windows of one step exceed the launch's 65535 window rows: refused
-    # before any device work (the buffers are never read).
-    buf = ctx.buffer(4096)
+    # before any device work. The buffer covers every row the call names, so
+    # a regression of the guard fails the assertion instead of reading past
+    # the allocation.
+    buf = ctx.buffer(70000 * 32 * 4)
     with pytest.raises(qa.QwhError, match="limit_exceeded"):
         ctx.audio_attention(buf.ptr, 32, buf.ptr, buf.ptr, buf.ptr, 32, 70000, 1, 1, 32)
     buf.free()

@@ -281,3 +281,21 @@ def test_linear_rejects_shape_mismatch(ctx):
     ctx.matrix_release(handle)
     xb.free()
     ob.free()
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [
+    (4096, 2048, 16),     # the 1.7B q|k|v block at batch 16 (split form, 8 slices)
+    (12288, 2048, 3),     # gate|up
+    (2048, 6144, 33),     # down, three token tiles
+    (1001, 1024, 2),      # rows not a multiple of the tile
+    (130, 320, 5),        # five groups: the unsplit matrix-core form
+    (64, 448, 17),        # seven groups, two token tiles
+])
+def test_q8_multi_token_on_matrix_cores(ctx, rows, cols, tokens):
+    # kernels.zig:118-158 with tokens > 1 over q8 weights (the audio tower's
+    # and the batched decoder's products): one pass over the codes per 16
+    # tokens; codes at both ends of the range in the first row.
+    w = o.normal(rows * cols, 15, rows, 0.02).reshape(rows, cols)
+    w[0, :64] = np.where(np.arange(64) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    x = o.normal(tokens * cols, 15, 2000 + cols)
+    check(ctx, o.Q8, w, x, tokens, f"q8 {rows}x{cols} tokens {tokens}")
