@@ -232,6 +232,20 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
                                 uint32_t head_dim, uint32_t batch, uint64_t scale_stride_bytes,
                                 uint64_t code_stride_bytes);
 
+/* qwh_decode_attention_q8 without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, hosts that forbid it). The
+ * range records live in a static device array of 8 MiB per GPU, resolved at
+ * qwh_create; inputs needing more (about batch * kv_heads * ranges records of
+ * (heads/kv_heads) * (head_dim + 4) floats) return QWH_E_LIMIT_EXCEEDED.
+ * Calls on one GPU share that array: calls that overlap on one GPU (two
+ * contexts' streams) race. Results equal qwh_decode_attention_q8's. */
+int32_t qwh_decode_attention_q8_noalloc(qwh_ctx *ctx, float *out_dev, const float *query_dev,
+                                        const uint8_t *k_scales_dev, const uint8_t *k_codes_dev,
+                                        const uint8_t *v_scales_dev, const uint8_t *v_codes_dev, uint32_t cached,
+                                        uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t batch,
+                                        uint64_t scale_stride_bytes, uint64_t code_stride_bytes);
+
 /* kernels.zig:572-627 decodeAttentionStep over an f32 cache (the reference's
  * default cache, model_config.zig:44-68): keys_dev / values_dev are
  * [positions][kv_heads*head_dim] f32 (decoder.zig:77-83), `cached` positions

@@ -147,6 +147,7 @@ SIGNATURES = {
     "qwh_decoder_init_synthetic_format": (_I32, [_P, _U32, _I32]),
     "qwh_decoder_generate_until": (_I32, [_P, _P, _U32, _P, _U32, _P, _P]),
     "qwh_decode_attention_f32": (_I32, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U64]),
+    "qwh_decode_attention_q8_noalloc": (_I32, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U64, _U64]),
     "qwh_decoder_destroy": (_I32, [_P]),
     "qwh_decoder_set_matrix": (_I32, [_P, _U32, _U32, _U64]),
     "qwh_decoder_set_vector": (_I32, [_P, _U32, _U32, _P, _U32]),

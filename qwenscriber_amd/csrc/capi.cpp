@@ -6,6 +6,7 @@
 #include <cstring>
 
 #include <initializer_list>
+#include <mutex>
 
 #include "common.h"
 
@@ -88,6 +89,45 @@ uint64_t add_matrix(qwh_ctx *ctx, const Matrix &m) {
 
 using namespace qwh;
 
+// Device scratch of the allocation-free decode attention
+// (qwh_decode_attention_q8_noalloc): the per-range softmax records (m, l,
+// acc) that the range kernel writes and the merge kernel reads. Every GPU the
+// library runs on holds its own copy until the process ends. In host code the
+// name is only a handle for hipGetSymbolAddress: kernels and copies use the
+// per-device address it resolves (scratch_address below).
+constexpr size_t kNoAllocScratchBytes = 8u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_address[kMaxDevices] = {};
+
+// Resolves this device's copy of `scratch`, once per device, with that device
+// current (called from qwh_create after hipSetDevice).
+int32_t resolve_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return QWH_E_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_address[device]) return QWH_OK;
+    void *ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        return QWH_E_DEVICE;
+    }
+    g_scratch_address[device] = ptr;
+    return QWH_OK;
+}
+
+void *scratch_address(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    return g_scratch_address[device];
+}
+
+}  // namespace
+
 extern "C" {
 
 int32_t qwh_abi_version(void) { return QWH_ABI_VERSION; }
@@ -129,6 +169,12 @@ int32_t qwh_create(uint32_t device_index, qwh_ctx **out) {
     if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess) ctx->cus = prop.multiProcessorCount;
     if (ctx->cus <= 0) ctx->cus = 256;
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return QWH_E_DEVICE;
+    }
+    // The device's copy of the allocation-free entry point's scratch.
+    if (resolve_scratch(ctx->device) != QWH_OK) {
+        (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return QWH_E_DEVICE;
     }
@@ -490,17 +536,23 @@ int32_t qwh_synth_normal(qwh_ctx *ctx, uint32_t seed, uint32_t stream, uint64_t 
     return check_hip(ctx, launch_synth_normal(ctx->stream, seed, stream, 0, count, value_scale, out_dev), "synth normal");
 }
 
-int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query_dev, const uint8_t *k_scales_dev,
-                                const uint8_t *k_codes_dev, const uint8_t *v_scales_dev, const uint8_t *v_codes_dev,
-                                uint32_t cached, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t batch,
-                                uint64_t scale_stride_bytes, uint64_t code_stride_bytes) {
-    if (!ctx) return QWH_E_INVALID_ARGUMENT;
-    // kernels.zig:712-723 shape checks.
+}  // extern "C"
+
+namespace {
+
+// kernels.zig:712-723 shape checks and the kernels' alignment needs for the
+// q8 decode attention; fills `a` for launch_decode_attention_q8 (a.batch 0:
+// nothing to do).
+int32_t attention_q8_args(qwh_ctx *ctx, float *out_dev, const float *query_dev, const uint8_t *k_scales_dev,
+                          const uint8_t *k_codes_dev, const uint8_t *v_scales_dev, const uint8_t *v_codes_dev,
+                          uint32_t cached, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t batch,
+                          uint64_t scale_stride_bytes, uint64_t code_stride_bytes, AttentionArgs &a) {
     if (head_dim == 0 || head_dim % kGroup != 0)
         return fail(ctx, QWH_E_SHAPE_MISMATCH, "head_dim %u is not a multiple of 64", head_dim);
     if (kv_heads == 0 || heads % kv_heads != 0)
         return fail(ctx, QWH_E_SHAPE_MISMATCH, "heads %u not a multiple of kv_heads %u", heads, kv_heads);
     if (cached == 0) return fail(ctx, QWH_E_SHAPE_MISMATCH, "no cached positions (softmax of an empty row)");
+    a = AttentionArgs{};
     if (batch == 0) return QWH_OK;
     const size_t kv_width = (size_t)kv_heads * head_dim;
     if (batch > 1 && (scale_stride_bytes < (size_t)cached * (kv_width / kGroup) * 2 || code_stride_bytes < (size_t)cached * kv_width))
@@ -519,7 +571,6 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
         return fail(ctx, QWH_E_INVALID_ARGUMENT, "sequence strides must keep the plane alignment");
     const uint32_t ratio = heads / kv_heads;
     if (!attention_supported(head_dim, ratio)) return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim, ratio);
-    AttentionArgs a{};
     a.out = out_dev;
     a.query = query_dev;
     // The kernel only reads the cache planes in this form.
@@ -536,8 +587,45 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
     a.batch = batch;
     a.scale_stride = scale_stride_bytes;
     a.code_stride = code_stride_bytes;
+    return QWH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query_dev, const uint8_t *k_scales_dev,
+                                const uint8_t *k_codes_dev, const uint8_t *v_scales_dev, const uint8_t *v_codes_dev,
+                                uint32_t cached, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t batch,
+                                uint64_t scale_stride_bytes, uint64_t code_stride_bytes) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    AttentionArgs a;
+    QWH_TRY(attention_q8_args(ctx, out_dev, query_dev, k_scales_dev, k_codes_dev, v_scales_dev, v_codes_dev, cached,
+                              heads, kv_heads, head_dim, batch, scale_stride_bytes, code_stride_bytes, a));
+    if (a.batch == 0) return QWH_OK;
     QWH_TRY(ensure_workspace(ctx, ctx->scratch, attention_scratch_bytes(ctx->cus, a)));
     return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr), "decode attention q8");
+}
+
+int32_t qwh_decode_attention_q8_noalloc(qwh_ctx *ctx, float *out_dev, const float *query_dev,
+                                        const uint8_t *k_scales_dev, const uint8_t *k_codes_dev,
+                                        const uint8_t *v_scales_dev, const uint8_t *v_codes_dev, uint32_t cached,
+                                        uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t batch,
+                                        uint64_t scale_stride_bytes, uint64_t code_stride_bytes) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    AttentionArgs a;
+    QWH_TRY(attention_q8_args(ctx, out_dev, query_dev, k_scales_dev, k_codes_dev, v_scales_dev, v_codes_dev, cached,
+                              heads, kv_heads, head_dim, batch, scale_stride_bytes, code_stride_bytes, a));
+    if (a.batch == 0) return QWH_OK;
+    const size_t need = attention_scratch_bytes(ctx->cus, a);
+    if (need > kNoAllocScratchBytes)
+        return fail(ctx, QWH_E_LIMIT_EXCEEDED, "attention records need %zu bytes; the static scratch holds %zu", need,
+                    kNoAllocScratchBytes);
+    void *ptr = scratch_address(ctx->device);
+    if (!ptr) return fail(ctx, QWH_E_DEVICE, "device %d has no resolved scratch", ctx->device);
+    // The records need no clearing: each range writes its record before the
+    // merge reads it, and ranges past `cached` are never read.
+    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ptr), "decode attention q8 (no alloc)");
 }
 
 int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *query_dev, const float *keys_dev,
