@@ -11,8 +11,10 @@ call (HIP events on the library stream, which the kernel runs on); with one
 launch per call that is also the kernel's mean launch duration, so
 roofline.achieved is the same figure. Also reported: the rest of the 0.6B
 sweep, the 1.7B decoder step in tokens/s at batch 1 and 16 with a q8 cache at
-4096 positions, configs 1, 3 and 4, and the single-core CPU
-restatement of the same GEMV.
+4096 positions (configs[4]; also with q8 weights, and with an f32 cache),
+configs 1, 3 and 4, the 1.7B lm_head, a plain streaming read of the same
+rotated bytes (the achievable ceiling beside the 8 TB/s peak), and the
+single-core CPU restatement of the same GEMV and of the decoder step.
 
 --pmc-pass runs only the headline calls plus a calibration kernel of known
 traffic, for the FETCH_SIZE / WRITE_SIZE counter runs.
@@ -73,6 +75,26 @@ def time_events(ctx, fn, steps, warm=2):
     return ms / steps
 
 
+def bench_stream_read(ctx, nbytes, steps, rotate_bytes):
+    """A plain streaming read of `nbytes` per call, rotated over >= rotate_bytes
+    of buffers like the GEMV's weights: the best of 1, 2, 4 and 8 workgroups
+    per CU. Returns (us per call, GB/s, blocks per CU)."""
+    nbytes = (nbytes + 15) // 16 * 16
+    copies = max(1, math.ceil(rotate_bytes / nbytes))
+    bufs = [ctx.buffer(nbytes) for _ in range(copies)]
+    for b in bufs:
+        ctx.memset(b.ptr, 0x5A, nbytes)
+    sink = ctx.buffer(4 * 8 * 1024)
+    best = None
+    for bpc in (1, 2, 4, 8):
+        ms = time_events(ctx, lambda i: ctx.stream_read(bufs[i % copies].ptr, nbytes, bpc, sink.ptr), steps, warm=4)
+        if best is None or ms < best[0]:
+            best = (ms, bpc)
+    for b in bufs + [sink]:
+        b.free()
+    return best[0] * 1e3, nbytes / (best[0] * 1e-3) / 1e9, best[1]
+
+
 def bench_gemv(ctx, qa, rows, cols, steps, warmup, rotate_bytes, seed=1, stream=8, fmt=None):
     fmt = qa.FORMAT_Q4 if fmt is None else fmt
     group_bytes = qa.DATA_BYTES[fmt] + 2
@@ -119,9 +141,59 @@ def pmc_pass(ctx, qa, steps):
           flush=True)
 
 
+def host_cpu():
+    """The host's CPU model, its logical CPU count and the CPUs this process
+    may run on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": usable}
+
+
+def cpu_decoder(seconds):
+    """decoder.zig forwardToken (the oracle's restatement) at configs[4],
+    batch 1: the synthetic 1.7B q4 model and a q8 cache prefilled to 4096
+    positions are built with every usable core, then greedy steps are timed on
+    one thread (the reference CPU path is single threaded) until `seconds`
+    have passed. Returns tokens/s and the sample."""
+    from oracle import oracle as o
+
+    cfg = dict(hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151936,
+               max_positions=4352, eps=1e-6, theta=1e6)
+    o.set_threads(min(16, host_cpu()["usable_cpus"] or 1))
+    t0 = time.perf_counter()
+    dec = o.Decoder(4, 1, **cfg)
+    dec.prefill_random(0, 4096)
+    build_s = time.perf_counter() - t0
+    o.set_threads(1)
+    token, steps = o.start_token(4, 0, cfg["vocab"]), 0
+    t0 = time.perf_counter()
+    while True:
+        token = dec.step(0, token)
+        steps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / steps
+    dec.close()
+    return dict(value=1.0 / dt, unit="tokens/s", cores=1, kind="port",
+                sample=f"{steps} greedy steps of the oracle's forwardToken at the configs[4] shape (1.7B, q4 "
+                       f"weights, q8 cache from 4096 positions), batch 1, 1 thread, {dt * 1e3:.0f} ms/step "
+                       f"(model and cache built in {build_s:.0f} s on all cores, untimed)")
+
+
 def cpu_baseline(ctx, qa, seconds):
     """The oracle's linearQuantized restatement on the lm_head shape, one
-    thread (the reference CPU path is single threaded), bounded to ~seconds."""
+    thread (the reference CPU path is single threaded), bounded to ~seconds;
+    then the decoder step (cpu_decoder)."""
     from oracle import oracle as o
 
     rows, cols = 151936, 1024
@@ -142,17 +214,22 @@ def cpu_baseline(ctx, qa, seconds):
         if time.perf_counter() - t0 >= seconds:
             break
     dt = (time.perf_counter() - t0) / calls
-    return dict(value=q4_gemv_bytes(rows, cols) / dt / 1e9, unit="GB/s", cores=1, kind="port",
-                sample=f"{calls} calls of the oracle's linearQuantized on the lm_head [151936x1024] q4 "
-                       f"shape, 1 thread, {dt * 1e3:.1f} ms/call")
+    res = dict(value=q4_gemv_bytes(rows, cols) / dt / 1e9, unit="GB/s", cores=1, kind="port",
+               sample=f"{calls} calls of the oracle's linearQuantized on the lm_head [151936x1024] q4 "
+                      f"shape, 1 thread, {dt * 1e3:.1f} ms/call")
+    res["host"] = host_cpu()
+    res["decoder_1p7b_b1"] = cpu_decoder(seconds)
+    return res
 
 
-def bench_decoder(ctx, qa, batch, steps, warmup):
+def bench_decoder(ctx, qa, batch, steps, warmup, fmt=None, cache=None):
+    fmt = qa.FORMAT_Q4 if fmt is None else fmt
+    cache = qa.CACHE_Q8 if cache is None else cache
     cfg = dict(hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151936,
                max_positions=4352, eps=1e-6, theta=1e6)
-    dec = qa.Decoder(ctx, batch=batch, **cfg)
+    dec = qa.Decoder(ctx, batch=batch, cache_format=cache, **cfg)
     t0 = time.perf_counter()
-    dec.init_synthetic(4)
+    dec.init_synthetic(4, fmt)
     for b in range(batch):
         dec.prefill_random(b, 4096, 4)
     log(f"decoder B={batch}: model + cache ready in {time.perf_counter() - t0:.1f} s")
@@ -167,9 +244,10 @@ def bench_decoder(ctx, qa, batch, steps, warmup):
     weights = 0
     hs, ffn, qw, kvw, vocab = 2048, 6144, 2048, 1024, 151936
     per_layer = qw * hs + 2 * kvw * hs + hs * qw + 2 * ffn * hs + hs * ffn
-    weights = (28 * per_layer + vocab * hs) * 34 // 64
+    weights = (28 * per_layer + vocab * hs) * (qa.DATA_BYTES[fmt] + 2) // 64
     pos_mid = 4096 + warmup + steps / 2
-    kv = batch * 28 * 2 * pos_mid * (kvw + kvw // 64 * 2)
+    row = kvw + kvw // 64 * 2 if cache == qa.CACHE_Q8 else 4 * kvw
+    kv = batch * 28 * 2 * pos_mid * row
     step_ms = ms / steps
     gbs = (weights + kv) / (step_ms * 1e-3) / 1e9
     return dict(batch=batch, tokens_per_s=batch * steps / (ms * 1e-3), ms_per_step=step_ms,
@@ -195,16 +273,24 @@ def bench_small(ctx, qa, steps):
         x.free()
         y.free()
     out["q4_sweep_0p6b"] = sweep
-    # q8 GEMV [1024 x 3072].
+    # q8 GEMV [1024 x 3072], 1000 timed calls, cache resident;
+    # then rotated over >= 2 GB of copies (HBM).
     m = ctx.matrix_synthetic(qa.FORMAT_Q8, 1024, 3072, 0, 0, 0.02)
     x = ctx.buffer(3072 * 4)
     ctx.synth_normal(0, 1, 3072, 1.0, x.ptr)
     y = ctx.buffer(1024 * 4)
-    ms = time_events(ctx, lambda i: ctx.linear(m, x.ptr, 3072, 1, y.ptr), steps)
-    out["q8_gemv_1024x3072"] = dict(us=ms * 1e3, GBs=3260416 / (ms * 1e-3) / 1e9)
+    ms = time_events(ctx, lambda i: ctx.linear(m, x.ptr, 3072, 1, y.ptr), 1000, warm=10)
+    g8 = bench_gemv(ctx, qa, 1024, 3072, 1000, 10, 2.1e9, seed=0, stream=0, fmt=qa.FORMAT_Q8)
+    out["q8_gemv_1024x3072"] = dict(calls=1000, us=ms * 1e3, GBs=3260416 / (ms * 1e-3) / 1e9,
+                                    hbm_rotated_us=g8["call_ms"] * 1e3,
+                                    hbm_rotated_GBs=3260416 / (g8["call_ms"] * 1e-3) / 1e9)
     ctx.matrix_release(m)
     x.free()
     y.free()
+    # The 1.7B lm_head [151936 x 2048] in q4, rotated.
+    g17 = bench_gemv(ctx, qa, 151936, 2048, steps, 10, 2.1e9, stream=12)
+    gbs = g17["bytes"] / (g17["call_ms"] * 1e-3) / 1e9
+    out["q4_gemv_lm_head_1p7b"] = dict(us=g17["call_ms"] * 1e3, GBs=gbs, frac=gbs / HBM_PEAK_GBS)
     # The 0.6B lm_head shape in q5 (the WebGPU decoder's format), rotated over
     # >= 2 GB of copies like the headline.
     g5 = bench_gemv(ctx, qa, 151936, 1024, steps, 10, 2.1e9, stream=9, fmt=qa.FORMAT_Q5)
@@ -343,6 +429,8 @@ def main():
     value = nbytes / (gemv["call_ms"] * 1e-3) / 1e9
     achieved = value  # the call is the one kernel launch
     log(f"lm_head: {gemv['call_ms'] * 1e3:.2f} us per call = per launch ({value:.0f} GB/s)")
+    read_us, read_gbs, read_bpc = bench_stream_read(ctx, nbytes, args.steps, 2.1e9)
+    log(f"streaming read of the same {nbytes / 1e6:.1f} MB: {read_us:.2f} us ({read_gbs:.0f} GB/s)")
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -366,7 +454,12 @@ def main():
                                        "profiles/gemv_q4_lm_head_0p6b.md",
                      "kernel": "gemv_q4_kernel<1, 32, 4, Src::F32>", "kernel_us": round(gemv["call_ms"] * 1e3, 3),
                      "algorithmic_bytes": "151936 x 1024 q4 codes + f16 scales (34 B per 64 weights) "
-                                          "+ 4 KiB f32 x + 594 KiB f32 y per launch"},
+                                          "+ 4 KiB f32 x + 594 KiB f32 y per launch",
+                     "copy_ceiling": {"GBs": round(read_gbs, 2), "frac_of_peak": round(read_gbs / HBM_PEAK_GBS, 4),
+                                      "us": round(read_us, 3), "blocks_per_cu": read_bpc,
+                                      "what": "plain streaming read (16-byte non-temporal loads) of the same "
+                                              "bytes per call, rotated over >= 2 GB; value / ceiling = %.3f"
+                                              % (value / read_gbs)}},
     }
     if not args.skip_decoder:
         dec = {}
@@ -375,6 +468,17 @@ def main():
             dec[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8)
             log(f"decoder batch {batch}: {dec[f'b{batch}']['tokens_per_s']:.0f} tok/s")
         result["decoder_1p7b_q4_q8kv_ctx4096"] = dec
+        # The same model with q8 weights (the format the reference's status
+        # page finds transcribing), and with the f32 cache (the reference's
+        # default cache).
+        q8 = {}
+        for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
+            log(f"decoder 1.7B q8 weights, batch {batch}")
+            q8[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8, fmt=qa.FORMAT_Q8)
+        result["decoder_1p7b_q8_q8kv_ctx4096"] = q8
+        log("decoder 1.7B, f32 cache, batch 1")
+        result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=64, warmup=8,
+                                                                       cache=qa.CACHE_F32)}
     if not args.skip_extra:
         log("configs 1, 2 (small shapes), 3, 4")
         result["kernels"] = bench_small(ctx, qa, max(10, args.steps // 2))

@@ -96,6 +96,14 @@ int32_t qwh_memset(qwh_ctx *ctx, void *dst_dev, int32_t value, uint64_t bytes);
 int32_t qwh_event_record(qwh_ctx *ctx, uint32_t slot);
 int32_t qwh_event_elapsed(qwh_ctx *ctx, uint32_t start, uint32_t end, float *out_ms);
 
+/* Roofline calibration, no reference counterpart: a plain streaming read of
+ * `bytes` at src_dev (16-byte aligned, a multiple of 16) with the GEMVs' load
+ * form, by cus * blocks_per_cu (1..8) workgroups, each writing one word to
+ * sink_dev. The bench times it over the same buffers as a GEMV to give the
+ * achievable read bandwidth next to the HBM peak. */
+int32_t qwh_stream_read(qwh_ctx *ctx, const void *src_dev, uint64_t bytes, uint32_t blocks_per_cu,
+                        uint32_t *sink_dev);
+
 /* ---------------------------------------------------------------------- */
 /* Quantized matrices (quant.zig planeLayout + kernels.zig Matrix)          */
 /* ---------------------------------------------------------------------- */

@@ -120,6 +120,7 @@ SIGNATURES = {
     "qwh_download": (_I32, [_P, _P, _P, _U64]),
     "qwh_memset": (_I32, [_P, _P, _I32, _U64]),
     "qwh_event_record": (_I32, [_P, _U32]),
+    "qwh_stream_read": (_I32, [_P, _P, _U64, _U32, _P]),
     "qwh_event_elapsed": (_I32, [_P, _U32, _U32, ctypes.POINTER(_F)]),
     "qwh_matrix_upload": (_I32, [_P, _I32, _U32, _U32, _P, _U64, _P, _U64, ctypes.POINTER(_U64)]),
     "qwh_matrix_wrap": (_I32, [_P, _I32, _U32, _U32, _P, _P, ctypes.POINTER(_U64)]),
@@ -315,6 +316,9 @@ class Context:
     def buffer(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)
 
+    def memset(self, dev: int, value: int, nbytes: int) -> None:
+        self._check(self.lib.qwh_memset(self.handle, dev, value, nbytes))
+
     def to_device(self, array: np.ndarray) -> DeviceBuffer:
         array = np.ascontiguousarray(array)
         buf = DeviceBuffer(self, max(array.nbytes, 1))
@@ -331,6 +335,9 @@ class Context:
 
     def event_record(self, slot: int) -> None:
         self._check(self.lib.qwh_event_record(self.handle, slot))
+
+    def stream_read(self, src_dev: int, nbytes: int, blocks_per_cu: int, sink_dev: int) -> None:
+        self._check(self.lib.qwh_stream_read(self.handle, src_dev, nbytes, blocks_per_cu, sink_dev))
 
     def event_elapsed_ms(self, start: int, end: int) -> float:
         out = ctypes.c_float()

@@ -262,6 +262,19 @@ int32_t qwh_memset(qwh_ctx *ctx, void *dst_dev, int32_t value, uint64_t bytes) {
     return check_hip(ctx, hipMemsetAsync(dst_dev, value, bytes, ctx->stream), "memset");
 }
 
+int32_t qwh_stream_read(qwh_ctx *ctx, const void *src_dev, uint64_t bytes, uint32_t blocks_per_cu, uint32_t *sink_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (bytes == 0) return QWH_OK;
+    QWH_TRY(check_device_ptr(ctx, src_dev, "src"));
+    QWH_TRY(check_device_ptr(ctx, sink_dev, "sink"));
+    if (((uintptr_t)src_dev & 15u) || (bytes & 15u))
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "src and bytes must be 16-byte aligned");
+    if (blocks_per_cu == 0 || blocks_per_cu > 8)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "blocks_per_cu %u outside 1..8", blocks_per_cu);
+    return check_hip(ctx, launch_stream_read(ctx->stream, ctx->cus, src_dev, bytes, blocks_per_cu, sink_dev),
+                     "stream read");
+}
+
 int32_t qwh_event_record(qwh_ctx *ctx, uint32_t slot) {
     if (!ctx || slot >= (uint32_t)kMaxEvents) return QWH_E_INVALID_ARGUMENT;
     return check_hip(ctx, hipEventRecord(ctx->events[slot], ctx->stream), "event record");

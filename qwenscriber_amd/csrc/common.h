@@ -212,6 +212,12 @@ hipError_t launch_kv_append_q8(hipStream_t s, const float *key, const float *val
                                uint32_t kv_width, uint32_t position, uint8_t *k_scales,
                                uint8_t *k_codes, uint8_t *v_scales, uint8_t *v_codes);
 
+// Plain streaming read of `bytes` (a multiple of 16, 16-byte aligned) for
+// the roofline ceiling (measure.hip); `sink` receives one word per
+// workgroup (cus * blocks_per_cu of them).
+hipError_t launch_stream_read(hipStream_t s, int cus, const void *src, uint64_t bytes, uint32_t blocks_per_cu,
+                              uint32_t *sink);
+
 // Audio tower glue (audio.hip). LayerNorm per token row (out may alias x).
 hipError_t launch_layer_norm(hipStream_t s, const float *x, float *out, const float *weight, const float *bias,
                              uint32_t width, uint32_t tokens, float eps);
