@@ -406,6 +406,9 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true")
     ap.add_argument("--decoder-batches", default="1,16", help="comma-separated decoder batch sizes")
+    ap.add_argument("--decoders", default="q4,q8,f32kv",
+                    help="decoder variants: q4 (q4 weights, q8 cache), q8 (q8 weights), f32kv (q4, f32 cache)")
+    ap.add_argument("--skip-headline", action="store_true", help="skip the lm_head GEMV and its read ceiling")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -423,14 +426,19 @@ def main():
     cus = ctx.cus()
     log(f"device 0: {cus} CUs")
     rows, cols = 151936, 1024
-    log("lm_head q4 GEMV (rotated over >= 2 GB)")
-    gemv = bench_gemv(ctx, qa, rows, cols, args.steps, args.warmup, 2.1e9)
-    nbytes = gemv["bytes"]
+    nbytes = q4_gemv_bytes(rows, cols)
+    if args.skip_headline:
+        gemv = dict(copies=0, call_ms=float("nan"), bytes=nbytes)
+        read_us = read_gbs = float("nan")
+        read_bpc = 0
+    else:
+        log("lm_head q4 GEMV (rotated over >= 2 GB)")
+        gemv = bench_gemv(ctx, qa, rows, cols, args.steps, args.warmup, 2.1e9)
+        log(f"lm_head: {gemv['call_ms'] * 1e3:.2f} us per call = per launch")
+        read_us, read_gbs, read_bpc = bench_stream_read(ctx, nbytes, args.steps, 2.1e9)
+        log(f"streaming read of the same {nbytes / 1e6:.1f} MB: {read_us:.2f} us ({read_gbs:.0f} GB/s)")
     value = nbytes / (gemv["call_ms"] * 1e-3) / 1e9
     achieved = value  # the call is the one kernel launch
-    log(f"lm_head: {gemv['call_ms'] * 1e3:.2f} us per call = per launch ({value:.0f} GB/s)")
-    read_us, read_gbs, read_bpc = bench_stream_read(ctx, nbytes, args.steps, 2.1e9)
-    log(f"streaming read of the same {nbytes / 1e6:.1f} MB: {read_us:.2f} us ({read_gbs:.0f} GB/s)")
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -461,21 +469,24 @@ def main():
                                               "bytes per call, rotated over >= 2 GB; value / ceiling = %.3f"
                                               % (value / read_gbs)}},
     }
-    if not args.skip_decoder:
+    variants = [v for v in args.decoders.split(",") if v]
+    if not args.skip_decoder and "q4" in variants:
         dec = {}
         for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
             log(f"decoder 1.7B, batch {batch}")
             dec[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8)
             log(f"decoder batch {batch}: {dec[f'b{batch}']['tokens_per_s']:.0f} tok/s")
         result["decoder_1p7b_q4_q8kv_ctx4096"] = dec
-        # The same model with q8 weights (the format the reference's status
-        # page finds transcribing), and with the f32 cache (the reference's
-        # default cache).
+    # The same model with q8 weights (the format the reference's status page
+    # finds transcribing), and with the f32 cache (the reference's default
+    # cache).
+    if not args.skip_decoder and "q8" in variants:
         q8 = {}
         for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
             log(f"decoder 1.7B q8 weights, batch {batch}")
             q8[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8, fmt=qa.FORMAT_Q8)
         result["decoder_1p7b_q8_q8kv_ctx4096"] = q8
+    if not args.skip_decoder and "f32kv" in variants:
         log("decoder 1.7B, f32 cache, batch 1")
         result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=64, warmup=8,
                                                                        cache=qa.CACHE_F32)}

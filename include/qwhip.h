@@ -323,6 +323,38 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *weights, fl
                         uint32_t steps, uint32_t d_model, uint32_t heads, uint32_t ffn_dim,
                         uint32_t window_steps, float eps);
 
+/* kernels.zig:302-427 conv3x3Stride2Gelu over `batch` independent images:
+ * in [batch][in_channels][in_height][in_width] f32, weights
+ * [out_channels][in_channels][3][3] f16 bits (the checkpoint's layout), bias
+ * [out_channels]; out [batch][out_channels][(h-1)/2+1][(w-1)/2+1] =
+ * gelu(bias + the 3x3, stride 2, padding 1 convolution). */
+int32_t qwh_conv3x3s2_gelu(qwh_ctx *ctx, float *out_dev, const float *in_dev, const uint16_t *weights_dev,
+                           const float *bias_dev, uint32_t batch, uint32_t out_channels, uint32_t in_channels,
+                           uint32_t in_height, uint32_t in_width);
+
+/* The audio tower's convolution front end (model.zig AudioModel conv1..3,
+ * conv_out): device f16-bit conv weights [downsample][in][3][3] (conv1 has
+ * one input channel), f32 biases, and conv_out as a matrix handle of
+ * d_model x downsample * bins, bins = mel_bins after three halvings. */
+typedef struct {
+    const uint16_t *conv1_weight, *conv2_weight, *conv3_weight;
+    const float *conv1_bias, *conv2_bias, *conv3_bias;
+    uint64_t conv_out;
+} qwh_audio_frontend_weights;
+
+/* model.zig:509-644 convolveAndPack + projectConvStep: the log-mel
+ * spectrogram [mel_bins][frames] (f32, device) in chunks of 2 * n_window
+ * frames (the last zero filled), three conv3x3Stride2Gelu stages, each valid
+ * time step flattened channel-major over the remaining frequency bins,
+ * projected by conv_out, plus the sinusoidal position of the step within its
+ * chunk (model.zig:751-763). Writes the packed encoder rows [steps][d_model]
+ * (steps = model_config.zig:226-238 for `frames`) to encoder_dev, which holds
+ * encoder_rows rows (else QWH_E_LIMIT_EXCEEDED); steps_out receives steps.
+ * Scratch is the context's. */
+int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *weights, const float *log_mel_dev,
+                           uint32_t mel_bins, uint32_t frames, uint32_t n_window, uint32_t downsample,
+                           uint32_t d_model, float *encoder_dev, uint32_t encoder_rows, uint32_t *steps_out);
+
 /* model.zig:707-735 runProjector: out[steps][hidden] = W_out gelu(W_in x +
  * b_in) + b_out, W_in d_model x d_model, W_out hidden x d_model. */
 int32_t qwh_audio_projector(qwh_ctx *ctx, uint64_t in_matrix, const float *in_bias_dev,

@@ -119,6 +119,9 @@ _SIGNATURES = {
     "qwref_add_bias": (_I32, [_P, _P, _U32, _U32]),
     "qwref_layer_norm": (None, [_P, _P, _P, _U32, _U32, ctypes.c_float]),
     "qwref_audio_attention_window": (_I32, [_P, _U32, _P, _U32, _P, _U32, _P, _U32, _U32, _U32, _U32, _U32]),
+    "qwref_post_convolution_steps": (_U32, [_U32]),
+    "qwref_conv3x3s2_gelu": (_I32, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
+    "qwref_add_sinusoidal_position": (None, [_P, _U32, _U32]),
 }
 
 
@@ -483,3 +486,64 @@ def audio_projector(encoder: np.ndarray, proj_in, in_bias, proj_out, out_bias, s
     fmt, scales, data = proj_out
     out = linear_quantized(fmt, scales, data, hidden, d_model, mid, steps)
     return add_bias(out, out_bias, hidden, steps)
+
+
+# --------------------------------------------------------------------------
+# Audio convolution front end (model.zig:509-644 convolveAndPack and
+# projectConvStep), composed from the C restatements in the reference's order.
+
+
+def post_convolution_steps(frames: int) -> int:
+    return lib().qwref_post_convolution_steps(frames)
+
+
+def conv3x3s2_gelu(x: np.ndarray, weights_f16: np.ndarray, bias: np.ndarray, out_channels: int, in_channels: int,
+                   in_height: int, in_width: int) -> np.ndarray:
+    """kernels.zig:325-427 over one image: x [in][h][w] f32, weights
+    [out][in][3][3] f16 bits; returns [out][oh][ow]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    w = np.ascontiguousarray(weights_f16, np.uint16).reshape(-1)
+    b = np.ascontiguousarray(bias, np.float32)
+    oh, ow = (in_height - 1) // 2 + 1, (in_width - 1) // 2 + 1
+    out = np.zeros(out_channels * oh * ow, np.float32)
+    status = lib().qwref_conv3x3s2_gelu(_ptr(out), _ptr(x), _ptr(w), _ptr(b), out_channels, in_channels, in_height,
+                                        in_width)
+    if status != 0:
+        raise ValueError(f"conv status {status}")
+    return out.reshape(out_channels, oh, ow)
+
+
+def add_sinusoidal_position(row: np.ndarray, step: int) -> np.ndarray:
+    row = np.array(row, np.float32).reshape(-1)
+    lib().qwref_add_sinusoidal_position(_ptr(row), step, row.size)
+    return row
+
+
+def audio_frontend(log_mel: np.ndarray, mel_bins: int, frames: int, n_window: int, weights: dict,
+                   downsample: int, d_model: int) -> np.ndarray:
+    """model.zig:509-644: per chunk of 2 * n_window frames (the tail zero
+    filled), three conv3x3Stride2Gelu stages, then per valid time step the
+    (channel, frequency) flatten, the conv_out projection
+    (weights["conv_out"] = (format, scales, data)) and the sinusoidal
+    position of the step within its chunk. log_mel is [mel_bins][frames]."""
+    log_mel = np.asarray(log_mel, np.float32).reshape(mel_bins, frames)
+    chunk_frames = 2 * n_window
+    chunk_steps = post_convolution_steps(chunk_frames)
+    bins = post_convolution_steps(mel_bins)
+    features = downsample * bins
+    fmt, scales, data = weights["conv_out"]
+    rows = []
+    for start in range(0, frames, chunk_frames):
+        valid = min(frames - start, chunk_frames)
+        chunk = np.zeros((mel_bins, chunk_frames), np.float32)
+        chunk[:, :valid] = log_mel[:, start:start + valid]
+        h, w = mel_bins, chunk_frames
+        x = chunk
+        for stage, channels in (("conv1", 1), ("conv2", downsample), ("conv3", downsample)):
+            x = conv3x3s2_gelu(x, weights[stage + "_weight"], weights[stage + "_bias"], downsample, channels, h, w)
+            h, w = (h - 1) // 2 + 1, (w - 1) // 2 + 1
+        for step in range(min(chunk_steps, post_convolution_steps(valid))):
+            flat = np.ascontiguousarray(x[:, :, step].reshape(features))
+            row = linear_quantized(fmt, scales, data, d_model, features, flat, 1)[0]
+            rows.append(add_sinusoidal_position(row, step))
+    return np.stack(rows) if rows else np.zeros((0, d_model), np.float32)

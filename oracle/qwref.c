@@ -809,6 +809,82 @@ void qwref_fill_normal(float *out, uint64_t count, uint32_t seed, uint32_t strea
 }
 
 /* ------------------------------------------------------------------------ */
+/* Audio convolution front end (kernels.zig:302-427, model.zig:509-644,     */
+/* :751-763; model_config.zig:84-90)                                         */
+/* ------------------------------------------------------------------------ */
+
+/* model_config.zig:84-90 `postConvolutionSteps`: three (n - 1) / 2 + 1. */
+uint32_t qwref_post_convolution_steps(uint32_t frames) {
+    if (frames == 0) return 0;
+    uint32_t steps = frames;
+    for (int i = 0; i < 3; ++i) steps = (steps - 1) / 2 + 1;
+    return steps;
+}
+
+/* kernels.zig:386-427 `convolvePlane`: adds one input channel's 3x3 stride-2
+ * padding-1 contribution to an output plane; per output position the nine
+ * taps are summed in kernel order (taps outside the input skipped), then the
+ * sum is added to the output. */
+static void convolve_plane(float *out, const float *input, const uint16_t *weights, uint32_t in_height,
+                           uint32_t in_width) {
+    uint32_t out_height = (in_height - 1) / 2 + 1, out_width = (in_width - 1) / 2 + 1;
+    float kernel_weights[9];
+    for (int i = 0; i < 9; ++i) kernel_weights[i] = qwref_from_f16(weights[i]);
+    for (uint32_t out_row = 0; out_row < out_height; ++out_row) {
+        for (uint32_t out_column = 0; out_column < out_width; ++out_column) {
+            float accumulator = 0.0f;
+            for (int kernel_row = 0; kernel_row < 3; ++kernel_row) {
+                int64_t in_row = (int64_t)out_row * 2 + kernel_row - 1;
+                if (in_row < 0 || in_row >= (int64_t)in_height) continue;
+                for (int kernel_column = 0; kernel_column < 3; ++kernel_column) {
+                    int64_t in_column = (int64_t)out_column * 2 + kernel_column - 1;
+                    if (in_column < 0 || in_column >= (int64_t)in_width) continue;
+                    float sample = input[(size_t)in_row * in_width + (size_t)in_column];
+                    accumulator += kernel_weights[kernel_row * 3 + kernel_column] * sample;
+                }
+            }
+            out[(size_t)out_row * out_width + out_column] += accumulator;
+        }
+    }
+}
+
+/* kernels.zig:325-384 `conv3x3Stride2Gelu` / `convolveChannel`: per output
+ * channel the plane starts at the bias, every input channel's contribution is
+ * added in channel order, then GELU. Weights [out][in][3][3] f16 bits, input
+ * [in][h][w], output [out][oh][ow]. */
+int32_t qwref_conv3x3s2_gelu(float *out, const float *input, const uint16_t *weights, const float *bias,
+                             uint32_t out_channels, uint32_t in_channels, uint32_t in_height, uint32_t in_width) {
+    if (in_height == 0 || in_width == 0 || in_channels == 0) return QWREF_SHAPE_MISMATCH;
+    uint32_t out_height = (in_height - 1) / 2 + 1, out_width = (in_width - 1) / 2 + 1;
+    size_t in_plane = (size_t)in_height * in_width, out_plane = (size_t)out_height * out_width;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t channel = 0; channel < (int64_t)out_channels; ++channel) {
+        float *out_slice = out + (size_t)channel * out_plane;
+        for (size_t i = 0; i < out_plane; ++i) out_slice[i] = bias[channel];
+        const uint16_t *weight_base = weights + (size_t)channel * in_channels * 9;
+        for (uint32_t in_channel = 0; in_channel < in_channels; ++in_channel)
+            convolve_plane(out_slice, input + (size_t)in_channel * in_plane, weight_base + (size_t)in_channel * 9,
+                           in_height, in_width);
+        for (size_t i = 0; i < out_plane; ++i) out_slice[i] = qwref_gelu(out_slice[i]);
+    }
+    return QWREF_OK;
+}
+
+/* model.zig:751-763 `addSinusoidalPosition`: inverse timescales and angles in
+ * f64, each sine / cosine narrowed to f32 and added to the row. */
+void qwref_add_sinusoidal_position(float *row, uint32_t step, uint32_t channels) {
+    uint32_t half = channels / 2;
+    double log_timescale_increment = log(10000.0) / ((double)half - 1.0);
+    double position = (double)step;
+    for (uint32_t index = 0; index < half; ++index) {
+        double inverse_timescale = exp(-log_timescale_increment * (double)index);
+        double angle = position * inverse_timescale;
+        row[index] += (float)sin(angle);
+        row[half + index] += (float)cos(angle);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* decoder.zig restatement with a synthetic q4 model and q8 cache            */
 /* ------------------------------------------------------------------------ */
 

@@ -28,6 +28,11 @@
  *                    f64 numpy layer norm and windowed attention brute force,
  *                    kernels.zig:1043-1078 windowed-attention known answers.
  *   audio layer      composition of the pinned parts (no reference-held vectors).
+ *   audio front end  kernels.zig:973-1041 convolution known answers,
+ *                    model.zig:1136-1170 sinusoid known answers,
+ *                    model_config.zig:431 (3000 frames -> 375 steps), f64
+ *                    brute force of the convolution, and the composition
+ *                    (chunks, flatten, projection, positions) against float64.
  *   decoder step     composition of the pinned parts (q4 / q5 / q8 weights,
  *                    f32 / q8 cache, non-unit norm weights) checked against an
  *                    independent float64 restatement; no reference-held
@@ -130,6 +135,13 @@ int32_t qwref_audio_attention_window(float *out, uint32_t out_stride, const floa
                                      const float *k, uint32_t k_stride, const float *v, uint32_t v_stride,
                                      uint32_t window_start, uint32_t window_length, uint32_t heads,
                                      uint32_t head_dim);
+
+/* Audio convolution front end (kernels.zig:302-427; model.zig:509-644,
+ * :751-763; model_config.zig:84-90). Weights are f16 bits [out][in][3][3]. */
+uint32_t qwref_post_convolution_steps(uint32_t frames);
+int32_t qwref_conv3x3s2_gelu(float *out, const float *input, const uint16_t *weights, const float *bias,
+                             uint32_t out_channels, uint32_t in_channels, uint32_t in_height, uint32_t in_width);
+void qwref_add_sinusoidal_position(float *row, uint32_t step, uint32_t channels);
 
 /* ---- synthetic inputs (test-input specification, not reference code) --- */
 uint32_t qwref_mulberry32_at(uint32_t seed, uint64_t draw);

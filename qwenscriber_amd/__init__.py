@@ -15,6 +15,7 @@ from ._lib import (  # noqa: F401
     FORMAT_Q5,
     FORMAT_Q8,
     GROUP_SIZE,
+    AudioFrontendWeights,
     AudioLayerWeights,
     Context,
     Decoder,

@@ -32,6 +32,15 @@ class AudioLayerWeights(ctypes.Structure):
     _fields_ = [(name, ctypes.c_uint64) for name in MATRICES] + [(name, ctypes.c_void_p) for name in VECTORS]
 
 
+class AudioFrontendWeights(ctypes.Structure):
+    """qwh_audio_frontend_weights: device addresses of the three f16-bit
+    convolution weights and f32 biases, and the conv_out matrix handle."""
+
+    _fields_ = [("conv1_weight", ctypes.c_void_p), ("conv2_weight", ctypes.c_void_p), ("conv3_weight", ctypes.c_void_p),
+                ("conv1_bias", ctypes.c_void_p), ("conv2_bias", ctypes.c_void_p), ("conv3_bias", ctypes.c_void_p),
+                ("conv_out", ctypes.c_uint64)]
+
+
 STATUS = {
     0: "ok", -1: "invalid_argument", -2: "out_of_memory", -3: "unsupported", -4: "bad_magic",
     -5: "bad_version", -6: "checksum_mismatch", -7: "shape_mismatch", -8: "invalid_state",
@@ -121,6 +130,9 @@ SIGNATURES = {
     "qwh_memset": (_I32, [_P, _P, _I32, _U64]),
     "qwh_event_record": (_I32, [_P, _U32]),
     "qwh_stream_read": (_I32, [_P, _P, _U64, _U32, _P]),
+    "qwh_conv3x3s2_gelu": (_I32, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32]),
+    "qwh_audio_frontend": (_I32, [_P, ctypes.POINTER(AudioFrontendWeights), _P, _U32, _U32, _U32, _U32, _U32, _P, _U32,
+                                  ctypes.POINTER(_U32)]),
     "qwh_event_elapsed": (_I32, [_P, _U32, _U32, ctypes.POINTER(_F)]),
     "qwh_matrix_upload": (_I32, [_P, _I32, _U32, _U32, _P, _U64, _P, _U64, ctypes.POINTER(_U64)]),
     "qwh_matrix_wrap": (_I32, [_P, _I32, _U32, _U32, _P, _P, ctypes.POINTER(_U64)]),
@@ -448,6 +460,21 @@ class Context:
         """model.zig runProjector."""
         self._check(self.lib.qwh_audio_projector(self.handle, in_matrix, in_bias_dev, out_matrix, out_bias_dev,
                                                  encoder_dev, steps, out_dev))
+
+    def conv3x3s2_gelu(self, out_dev, in_dev, weights_dev, bias_dev, batch, out_channels, in_channels, in_height,
+                       in_width) -> None:
+        """kernels.zig conv3x3Stride2Gelu over `batch` images."""
+        self._check(self.lib.qwh_conv3x3s2_gelu(self.handle, out_dev, in_dev, weights_dev, bias_dev, batch, out_channels,
+                                                in_channels, in_height, in_width))
+
+    def audio_frontend(self, weights, log_mel_dev, mel_bins, frames, n_window, downsample, d_model, encoder_dev,
+                       encoder_rows) -> int:
+        """model.zig convolveAndPack: returns the number of encoder rows written."""
+        steps = ctypes.c_uint32(0)
+        self._check(self.lib.qwh_audio_frontend(self.handle, ctypes.byref(weights), log_mel_dev, mel_bins, frames,
+                                                n_window, downsample, d_model, encoder_dev, encoder_rows,
+                                                ctypes.byref(steps)))
+        return steps.value
 
     # -- quantization and synthetic inputs ---------------------------------
     def quantize_rows(self, fmt: int, values_dev: int, rows: int, cols: int, scales_dev: int, data_dev: int) -> None:

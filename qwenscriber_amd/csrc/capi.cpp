@@ -1,12 +1,14 @@
 // C ABI entry points: context, device memory, matrices, the linear products,
 // device quantization and attention. The decoder entry points are in
 // decoder.hip.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 
 #include <initializer_list>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 
@@ -204,6 +206,7 @@ int32_t qwh_destroy(qwh_ctx *ctx) {
     if (ctx->digits.ptr) (void)hipFree(ctx->digits.ptr);
     if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
     if (ctx->audio.ptr) (void)hipFree(ctx->audio.ptr);
+    if (ctx->front.ptr) (void)hipFree(ctx->front.ptr);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QWH_OK;
@@ -921,6 +924,118 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
     }
     return check_hip(ctx, launch_bias_epilogue(s, kBiasResidual, block, w->ffn_out_bias, encoder_dev, d_model, steps),
                      "audio ffn bias + residual");
+}
+
+int32_t qwh_conv3x3s2_gelu(qwh_ctx *ctx, float *out_dev, const float *in_dev, const uint16_t *weights_dev,
+                           const float *bias_dev, uint32_t batch, uint32_t out_channels, uint32_t in_channels,
+                           uint32_t in_height, uint32_t in_width) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    // kernels.zig:344-349: a kernel of 3, non-empty planes and channels.
+    if (in_height == 0 || in_width == 0 || in_channels == 0 || out_channels == 0)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "empty convolution geometry");
+    if (batch == 0) return QWH_OK;
+    const uint32_t oh = (in_height - 1) / 2 + 1, ow = (in_width - 1) / 2 + 1;
+    if ((uint64_t)((oh + 7) / 8) * ((ow + 7) / 8) > 0xFFFFFFFFull || batch > 65535)
+        return fail(ctx, QWH_E_LIMIT_EXCEEDED, "%u images of %u x %u", batch, in_height, in_width);
+    QWH_TRY(check_device_ptr(ctx, out_dev, "out"));
+    QWH_TRY(check_device_ptr(ctx, in_dev, "input"));
+    QWH_TRY(check_device_ptr(ctx, weights_dev, "weights"));
+    QWH_TRY(check_device_ptr(ctx, bias_dev, "bias"));
+    return check_hip(ctx, launch_conv3x3s2_gelu(ctx->stream, out_dev, in_dev, weights_dev, bias_dev, batch, out_channels,
+                                                in_channels, in_height, in_width), "conv3x3 stride 2");
+}
+
+namespace {
+
+// model_config.zig:84-90 postConvolutionSteps: three (n - 1) / 2 + 1.
+uint32_t post_convolution(uint32_t n) {
+    if (n == 0) return 0;
+    for (int i = 0; i < 3; ++i) n = (n - 1) / 2 + 1;
+    return n;
+}
+
+}  // namespace
+
+int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *w, const float *log_mel_dev,
+                           uint32_t mel_bins, uint32_t frames, uint32_t n_window, uint32_t downsample,
+                           uint32_t d_model, float *encoder_dev, uint32_t encoder_rows, uint32_t *steps_out) {
+    if (!ctx || !w || !steps_out) return QWH_E_INVALID_ARGUMENT;
+    *steps_out = 0;
+    if (mel_bins == 0 || n_window == 0 || downsample == 0 || d_model == 0 || d_model % 2)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "mel_bins, n_window, downsample and an even d_model are required");
+    const uint32_t chunk_frames = 2 * n_window;       // model_config.zig:196-198
+    const uint32_t chunk_steps = post_convolution(chunk_frames);
+    const uint32_t bins = post_convolution(mel_bins);  // audioFrequencyBinsAfterConvolutions
+    const uint32_t features = downsample * bins;       // audioConvOutInputFeatures
+    const Matrix *proj = find_matrix(ctx, w->conv_out);
+    if (!proj) return fail(ctx, QWH_E_NOT_FOUND, "unknown conv_out matrix handle");
+    if (proj->rows != d_model || proj->cols != features)
+        return fail(ctx, QWH_E_SHAPE_MISMATCH, "conv_out is %u x %u, the front end needs %u x %u", proj->rows,
+                    proj->cols, d_model, features);
+    // model_config.zig:226-238 audio steps of the clip.
+    const uint32_t chunks = (frames + chunk_frames - 1) / chunk_frames;
+    const uint64_t steps = (uint64_t)(frames / chunk_frames) * chunk_steps + post_convolution(frames % chunk_frames);
+    if (steps > encoder_rows)
+        return fail(ctx, QWH_E_LIMIT_EXCEEDED, "%llu encoder rows needed, %u given", (unsigned long long)steps,
+                    encoder_rows);
+    if (steps == 0) return QWH_OK;
+    QWH_TRY(check_device_ptr(ctx, log_mel_dev, "log_mel"));
+    QWH_TRY(check_device_ptr(ctx, encoder_dev, "encoder"));
+    const void *vectors[] = {w->conv1_weight, w->conv2_weight, w->conv3_weight, w->conv1_bias, w->conv2_bias,
+                             w->conv3_bias};
+    for (const void *p : vectors) QWH_TRY(check_device_ptr(ctx, p, "front-end weight"));
+    if (((uintptr_t)encoder_dev & 15u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "encoder must be 16-byte aligned");
+    // The three stages' planes per chunk, in chunk groups of at most 32.
+    const uint32_t h1 = (mel_bins - 1) / 2 + 1, w1 = (chunk_frames - 1) / 2 + 1;
+    const uint32_t h2 = (h1 - 1) / 2 + 1, w2 = (w1 - 1) / 2 + 1;
+    const size_t mel_plane = (size_t)mel_bins * chunk_frames;
+    const size_t p1 = (size_t)downsample * h1 * w1, p2 = (size_t)downsample * h2 * w2;
+    const size_t p3 = (size_t)downsample * bins * chunk_steps;
+    const uint32_t group = chunks < 32 ? chunks : 32;
+    auto align = [](size_t n) { return (n + 63) & ~(size_t)63; };  // floats: 256-byte aligned pieces
+    const size_t off1 = align(group * mel_plane), off2 = off1 + align(group * p1), off3 = off2 + align(group * p2);
+    const size_t off_flat = off3 + align(group * p3);
+    const size_t off_table = off_flat + align((size_t)group * chunk_steps * features);
+    const size_t total = off_table + align((size_t)chunk_steps * d_model);
+    QWH_TRY(ensure_workspace(ctx, ctx->front, total * sizeof(float)));
+    float *ws = static_cast<float *>(ctx->front.ptr);
+    // addSinusoidalPosition (model.zig:751-763) for the steps of a chunk, in
+    // f64 on the host, narrowed to f32 as the reference does.
+    std::vector<float> table((size_t)chunk_steps * d_model, 0.0f);
+    const uint32_t half = d_model / 2;
+    const double increment = std::log(10000.0) / ((double)half - 1.0);
+    for (uint32_t step = 0; step < chunk_steps; ++step)
+        for (uint32_t i = 0; i < half; ++i) {
+            const double angle = (double)step * std::exp(-increment * (double)i);
+            table[(size_t)step * d_model + i] = (float)std::sin(angle);
+            table[(size_t)step * d_model + half + i] = (float)std::cos(angle);
+        }
+    hipStream_t s = ctx->stream;
+    QWH_TRY(check_hip(ctx, hipMemcpyAsync(ws + off_table, table.data(), table.size() * 4, hipMemcpyHostToDevice, s),
+                      "position table"));
+    // The table copy reads host memory owned by this call.
+    QWH_TRY(check_hip(ctx, hipStreamSynchronize(s), "position table"));
+    for (uint32_t c0 = 0; c0 < chunks; c0 += group) {
+        const uint32_t count = chunks - c0 < group ? chunks - c0 : group;
+        const uint32_t row0 = c0 * chunk_steps;  // every chunk before the last is whole
+        const uint32_t rows = (uint32_t)(steps - row0 < (uint64_t)count * chunk_steps ? steps - row0 : count * chunk_steps);
+        QWH_TRY(check_hip(ctx, launch_gather_chunks(s, log_mel_dev, mel_bins, frames, chunk_frames, c0, count, ws),
+                          "front-end chunks"));
+        QWH_TRY(check_hip(ctx, launch_conv3x3s2_gelu(s, ws + off1, ws, w->conv1_weight, w->conv1_bias, count, downsample,
+                                                     1, mel_bins, chunk_frames), "conv1"));
+        QWH_TRY(check_hip(ctx, launch_conv3x3s2_gelu(s, ws + off2, ws + off1, w->conv2_weight, w->conv2_bias, count,
+                                                     downsample, downsample, h1, w1), "conv2"));
+        QWH_TRY(check_hip(ctx, launch_conv3x3s2_gelu(s, ws + off3, ws + off2, w->conv3_weight, w->conv3_bias, count,
+                                                     downsample, downsample, h2, w2), "conv3"));
+        QWH_TRY(check_hip(ctx, launch_pack_steps(s, ws + off3, downsample, bins, chunk_steps, rows, ws + off_flat),
+                          "front-end flatten"));
+        float *out = encoder_dev + (size_t)row0 * d_model;
+        QWH_TRY(qwh_linear(ctx, w->conv_out, ws + off_flat, features, rows, out));
+        QWH_TRY(check_hip(ctx, launch_add_positions(s, out, ws + off_table, row0, rows, d_model, chunk_steps),
+                          "front-end positions"));
+    }
+    *steps_out = (uint32_t)steps;
+    return QWH_OK;
 }
 
 int32_t qwh_audio_projector(qwh_ctx *ctx, uint64_t in_matrix, const float *in_bias_dev, uint64_t out_matrix,

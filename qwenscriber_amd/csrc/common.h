@@ -73,6 +73,7 @@ struct qwh_ctx {
     qwh::Workspace digits;  // x digit planes for the q4 GEMV
     qwh::Workspace scratch; // attention partials and other per-call scratch
     qwh::Workspace audio;   // audio tower layer / projector activations
+    qwh::Workspace front;   // audio front end: chunk planes, flattened steps, position table
 };
 
 namespace qwh {
@@ -211,6 +212,18 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
 hipError_t launch_kv_append_q8(hipStream_t s, const float *key, const float *value,
                                uint32_t kv_width, uint32_t position, uint8_t *k_scales,
                                uint8_t *k_codes, uint8_t *v_scales, uint8_t *v_codes);
+
+// Audio convolution front end (frontend.hip). conv3x3Stride2Gelu over
+// `batch` images [in_ch][h][w] -> [out_ch][(h-1)/2+1][(w-1)/2+1]; weights
+// [out_ch][in_ch][9] f16 bits.
+hipError_t launch_conv3x3s2_gelu(hipStream_t s, float *out, const float *in, const uint16_t *weights, const float *bias,
+                                 uint32_t batch, uint32_t out_ch, uint32_t in_ch, uint32_t h, uint32_t w);
+hipError_t launch_gather_chunks(hipStream_t s, const float *mel, uint32_t bins, uint32_t frames, uint32_t chunk_frames,
+                                uint32_t first, uint32_t count, float *out);
+hipError_t launch_pack_steps(hipStream_t s, const float *conv3, uint32_t channels, uint32_t bins, uint32_t steps_per_chunk,
+                             uint32_t rows, float *flat);
+hipError_t launch_add_positions(hipStream_t s, float *rows, const float *table, uint32_t first, uint32_t count,
+                                uint32_t width, uint32_t steps_per_chunk);
 
 // Plain streaming read of `bytes` (a multiple of 16, 16-byte aligned) for
 // the roofline ceiling (measure.hip); `sink` receives one word per

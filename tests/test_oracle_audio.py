@@ -15,6 +15,7 @@ import pytest
 from scipy.special import erf as erf64
 
 from oracle import oracle as o
+from util import normal
 
 
 @pytest.mark.parametrize("x,expected", [
@@ -156,3 +157,135 @@ def test_audio_layer_against_float64():
     x = x + h @ dense("ffn_out").T + layer["ffn_out_bias"]
     want = x.reshape(-1)
     assert np.max(np.abs(got - want)) <= 1e-4 * (1 + np.max(np.abs(want)))
+
+
+# ---------------------------------------------------------------- convolution front end
+def _f16(values):
+    return np.array([o.to_f16(float(v)) for v in np.asarray(values, np.float32).reshape(-1)], np.uint16)
+
+
+def test_conv_centre_tap_known_answer():
+    # kernels.zig:973-997: a 3x3 input, one output channel whose kernel picks
+    # the centre: the outputs are gelu of input positions (0,0), (0,2), (2,0),
+    # (2,2).
+    w = _f16([0, 0, 0, 0, 1, 0, 0, 0, 0])
+    out = o.conv3x3s2_gelu(np.arange(1, 10, dtype=np.float32), w, [0.0], 1, 1, 3, 3).reshape(-1)
+    for got, x in zip(out, (1.0, 3.0, 7.0, 9.0)):
+        assert abs(got - o.gelu(x)) <= 1e-5
+
+
+def test_conv_reduces_over_channels_in_weight_order():
+    # kernels.zig:999-1041: channel zero's centre tap plus channel one's
+    # top-left tap, which lands inside the input only for the last output
+    # position (reading 50): gelu(1), gelu(3), gelu(7), gelu(9 + 50).
+    w = _f16([0, 0, 0, 0, 1, 0, 0, 0, 0] + [1, 0, 0, 0, 0, 0, 0, 0, 0])
+    x = np.concatenate([np.arange(1, 10), 10 * np.arange(1, 10)]).astype(np.float32)
+    out = o.conv3x3s2_gelu(x, w, [0.0], 1, 2, 3, 3).reshape(-1)
+    for got, v in zip(out, (1.0, 3.0, 7.0, 59.0)):
+        assert abs(got - o.gelu(v)) <= 1e-5
+
+
+def _conv_f64(x, w, b, cout, cin, h, wd):
+    oh, ow = (h - 1) // 2 + 1, (wd - 1) // 2 + 1
+    xp = np.zeros((cin, h + 2, wd + 2))
+    xp[:, 1:h + 1, 1:wd + 1] = x.reshape(cin, h, wd)
+    w = w.reshape(cout, cin, 3, 3)
+    out = np.zeros((cout, oh, ow))
+    for i in range(3):
+        for j in range(3):
+            patch = xp[:, i:i + 2 * oh:2, j:j + 2 * ow:2]
+            out += np.einsum("oc,chw->ohw", w[:, :, i, j], patch)
+    out += np.asarray(b, np.float64)[:, None, None]
+    return out
+
+
+@pytest.mark.parametrize("cout,cin,h,w", [(5, 3, 9, 11), (4, 1, 16, 8), (2, 7, 4, 5), (3, 2, 1, 1), (6, 6, 2, 3)])
+def test_conv_against_f64_brute_force(cout, cin, h, w):
+    x = normal(cin * h * w, 51, cin)
+    wv = normal(cout * cin * 9, 52, cout, 0.3)
+    wb = _f16(wv)
+    wf = np.array([o.from_f16(int(v)) for v in wb], np.float64)
+    b = normal(cout, 53, 0, 0.1)
+    got = o.conv3x3s2_gelu(x, wb, b, cout, cin, h, w)
+    pre = _conv_f64(x.astype(np.float64), wf, b, cout, cin, h, w)
+    want = 0.5 * pre * (1.0 + erf64(pre / math.sqrt(2.0)))
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_post_convolution_steps():
+    # model_config.zig:431 and the three (n - 1) / 2 + 1 halvings.
+    assert o.post_convolution_steps(3000) == 375
+    assert o.post_convolution_steps(0) == 0
+    assert o.post_convolution_steps(1) == 1
+    assert o.post_convolution_steps(100) == 13
+    assert o.post_convolution_steps(128) == 16
+
+
+def test_sinusoidal_position_known_answers():
+    # model.zig:1136-1170.
+    row = o.add_sinusoidal_position(np.zeros(64, np.float32), 0)
+    assert np.all(row[:32] == 0.0) and np.allclose(row[32:], 1.0, atol=1e-6)
+    row = o.add_sinusoidal_position(np.zeros(64, np.float32), 1)
+    assert np.all(np.abs(row) <= 1.0) and np.all(np.isfinite(row))
+    assert abs(row[0] - math.sin(1.0)) <= 1e-6 and abs(row[32] - math.cos(1.0)) <= 1e-6
+    assert abs(row[1]) > abs(row[30]) and abs(row[62]) > abs(row[32])
+    assert abs(row[62] - 1.0) <= 1e-4
+    seeded = o.add_sinusoidal_position(np.full(64, 0.25, np.float32), 0)
+    assert np.allclose(seeded[:32], 0.25, atol=1e-6) and np.allclose(seeded[32:], 1.25, atol=1e-6)
+    # Against float64 at a later step and another width.
+    row = o.add_sinusoidal_position(np.zeros(896, np.float32), 12)
+    half = 448
+    inv = np.exp(-math.log(10000.0) / (half - 1) * np.arange(half))
+    assert np.allclose(row, np.concatenate([np.sin(12 * inv), np.cos(12 * inv)]), atol=1e-7)
+
+
+def _frontend_weights(seed, downsample, mel_bins, d_model, fmt=o.Q4):
+    bins = o.post_convolution_steps(mel_bins)
+    w = {}
+    for i, (name, cin) in enumerate((("conv1", 1), ("conv2", downsample), ("conv3", downsample))):
+        w[name + "_weight"] = _f16(normal(downsample * cin * 9, seed, 10 + i, 0.4))
+        w[name + "_bias"] = normal(downsample, seed, 20 + i, 0.1)
+    features = downsample * bins
+    vals = normal(d_model * features, seed, 30, 0.05).reshape(d_model, features)
+    s, d = o.quantize_rows(fmt, vals)
+    w["conv_out"] = (fmt, s, d)
+    return w
+
+
+def _frontend_f64(log_mel, mel_bins, frames, n_window, w, downsample, d_model):
+    """model.zig:509-644 in float64 (the reference's erf fit replaced by the
+    exact erf; chunks, flatten, projection and positions written out)."""
+    chunk = 2 * n_window
+    bins = o.post_convolution_steps(mel_bins)
+    fmt, s, d = w["conv_out"]
+    proj = o.dequantize_rows(fmt, s, d, d_model, downsample * bins).astype(np.float64)
+    rows = []
+    for start in range(0, frames, chunk):
+        valid = min(frames - start, chunk)
+        x = np.zeros((mel_bins, chunk))
+        x[:, :valid] = log_mel[:, start:start + valid]
+        h, wd, cin = mel_bins, chunk, 1
+        for stage in ("conv1", "conv2", "conv3"):
+            wf = np.array([o.from_f16(int(v)) for v in w[stage + "_weight"]], np.float64)
+            pre = _conv_f64(x, wf, w[stage + "_bias"], downsample, cin, h, wd)
+            x = 0.5 * pre * (1.0 + erf64(pre / math.sqrt(2.0)))
+            h, wd, cin = (h - 1) // 2 + 1, (wd - 1) // 2 + 1, downsample
+        half = d_model // 2
+        inv = np.exp(-math.log(10000.0) / (half - 1) * np.arange(half))
+        for step in range(min(o.post_convolution_steps(chunk), o.post_convolution_steps(valid))):
+            row = proj @ x[:, :, step].reshape(-1)
+            rows.append(row + np.concatenate([np.sin(step * inv), np.cos(step * inv)]))
+    return np.stack(rows)
+
+
+def test_frontend_composition_against_f64():
+    # Two full chunks and a ragged third (3 frames), so the zero-filled tail
+    # and the per-chunk step count both matter.
+    mel_bins, n_window, downsample, d_model, frames = 32, 4, 16, 8, 19  # 16 x 4 = 64 features
+    w = _frontend_weights(61, downsample, mel_bins, d_model)
+    log_mel = normal(mel_bins * frames, 62).reshape(mel_bins, frames)
+    got = o.audio_frontend(log_mel, mel_bins, frames, n_window, w, downsample, d_model)
+    want = _frontend_f64(log_mel, mel_bins, frames, n_window, w, downsample, d_model)
+    expected_steps = 2 * o.post_convolution_steps(8) + o.post_convolution_steps(3)
+    assert got.shape == (expected_steps, d_model) == want.shape
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
