@@ -382,8 +382,45 @@ def bench_audio(ctx, qa, steps):
     # Scores and weighted sums: 2 x 2 x head_dim flops per (query, key) pair.
     pairs = sum(min(window, T - s) ** 2 for s in range(0, T, window))
     att_flops = 4 * pairs * d
+    # The convolution front end over 30 s of audio (3000 frames: 30 chunks of
+    # 100, 375 encoder rows), 480 channels, conv_out 896 x 7680 in q4.
+    mel_bins, frames, n_window, ds = 128, 3000, 50, 480
+    fw = qa.AudioFrontendWeights()
+    fbufs = []
+    for j, (name, cin) in enumerate((("conv1", 1), ("conv2", ds), ("conv3", ds))):
+        wb = ctx.buffer(ds * cin * 9 * 4)
+        ctx.synth_normal(6, 300 + j, ds * cin * 9, 1.0 / math.sqrt(9 * cin), wb.ptr)
+        # f16 bits of the values: the low halves of a u32 view are not f16s,
+        # so convert on the host.
+        vals = wb.download(np.float32)
+        w16 = ctx.to_device(vals.astype(np.float16).view(np.uint16))
+        bb = ctx.buffer(ds * 4)
+        ctx.synth_normal(6, 310 + j, ds, 0.1, bb.ptr)
+        fbufs += [wb, w16, bb]
+        setattr(fw, name + "_weight", w16.ptr)
+        setattr(fw, name + "_bias", bb.ptr)
+    fw.conv_out = ctx.matrix_synthetic(qa.FORMAT_Q4, d, ds * 16, 6, 320, 0.02)
+    mel = ctx.buffer(mel_bins * frames * 4)
+    ctx.synth_normal(6, 330, mel_bins * frames, 1.0, mel.ptr)
+    rows = 375
+    fenc = ctx.buffer(rows * d * 4)
+    front_ms = time_events(ctx, lambda i: ctx.audio_frontend(fw, mel.ptr, mel_bins, frames, n_window, ds, d, fenc.ptr,
+                                                            rows), max(3, steps // 4))
+    # Multiply-adds of the three convolutions per chunk, and of conv_out.
+    h, w_ = mel_bins, 2 * n_window
+    conv_macs = 0
+    for cin in (1, ds, ds):
+        h, w_ = (h - 1) // 2 + 1, (w_ - 1) // 2 + 1
+        conv_macs += ds * h * w_ * cin * 9
+    front_flops = 2 * (30 * conv_macs + rows * d * ds * 16)
+    ctx.matrix_release(fw.conv_out)
+    for b in fbufs + [mel, fenc]:
+        b.free()
     res = {
         "workload": "Qwen3-ASR-0.6B audio layer, 390 steps, window 104, q4 weights, f32 activations",
+        "frontend_30s_ms": front_ms, "frontend_TFLOPs": front_flops / (front_ms * 1e-3) / 1e12,
+        "frontend_workload": "3000 mel frames x 128 bins, 30 chunks, 3 convolutions of 480 channels (f16 weights, "
+                             "f32 FMA), conv_out 896 x 7680 q4, 375 rows",
         "layer_us": layer_ms * 1e3, "layer_TFLOPs": (layer_flops + att_flops) / (layer_ms * 1e-3) / 1e12,
         "tower_18_layers_ms": 18 * layer_ms,
         "attention_us": att_ms * 1e3, "attention_GFLOPs": att_flops / (att_ms * 1e-3) / 1e9,
