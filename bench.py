@@ -320,7 +320,7 @@ def bench_small(ctx, qa, steps):
     att = {}
     heads, kvh, hd = 16, 8, 128
     kvw = kvh * hd
-    for ctx_len, batch in ((4096, 1), (8192, 1), (8192, 8)):
+    for ctx_len, batch in ((4096, 1), (8192, 1), (8192, 8), (4096, 16)):
         vals = ctx.buffer(ctx_len * kvw * 4)
         ks, kc, vs, vc = [ctx.buffer(batch * ctx_len * n) for n in (kvw // 64 * 2, kvw, kvw // 64 * 2, kvw)]
         for b in range(batch):
@@ -383,7 +383,8 @@ def bench_audio(ctx, qa, steps):
     pairs = sum(min(window, T - s) ** 2 for s in range(0, T, window))
     att_flops = 4 * pairs * d
     # The convolution front end over 30 s of audio (3000 frames: 30 chunks of
-    # 100, 375 encoder rows), 480 channels, conv_out 896 x 7680 in q4.
+    # 100 frames, 13 rows each after three stride-2 convolutions: 390 encoder
+    # rows), 480 channels, conv_out 896 x 7680 in q4.
     mel_bins, frames, n_window, ds = 128, 3000, 50, 480
     fw = qa.AudioFrontendWeights()
     fbufs = []
@@ -402,7 +403,7 @@ def bench_audio(ctx, qa, steps):
     fw.conv_out = ctx.matrix_synthetic(qa.FORMAT_Q4, d, ds * 16, 6, 320, 0.02)
     mel = ctx.buffer(mel_bins * frames * 4)
     ctx.synth_normal(6, 330, mel_bins * frames, 1.0, mel.ptr)
-    rows = 375
+    rows = 30 * 13
     fenc = ctx.buffer(rows * d * 4)
     front_ms = time_events(ctx, lambda i: ctx.audio_frontend(fw, mel.ptr, mel_bins, frames, n_window, ds, d, fenc.ptr,
                                                             rows), max(3, steps // 4))

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "qwref_decoder_step": (_I32, [_P, _U32, _U32, ctypes.POINTER(_U32)]),
     "qwref_decoder_weights_hash": (_U64, [_P]),
     "qwref_decoder_cache_hash": (_U64, [_P, _U32]),
+    "qwref_decoder_cache_row": (_U64, [_P, _U32, _U32, _U32, _P, _U64]),
     "qwref_synthetic_start_token": (_U32, [_U32, _U32, _U32]),
     "qwref_set_threads": (None, [_I32]),
     "qwref_erf": (ctypes.c_float, [ctypes.c_float]),
@@ -378,6 +379,16 @@ class Decoder:
 
     def cache_hash(self, seq: int) -> int:
         return lib().qwref_decoder_cache_hash(self.handle, seq)
+
+    def cache_row(self, seq: int, layer: int, position: int) -> bytes:
+        """One cache row as the decoder holds it: q8 key scales, key codes,
+        value scales, value codes (f32 cache: key row, value row)."""
+        kvw = self.config.kv_heads * self.config.head_dim
+        out = np.zeros(8 * kvw, np.uint8)
+        n = lib().qwref_decoder_cache_row(self.handle, seq, layer, position, out.ctypes.data, out.size)
+        if n == 0:
+            raise ValueError("cache_row: bad argument")
+        return out[:n].tobytes()
 
 
 def start_token(seed: int, seq: int, vocab: int) -> int:

@@ -1255,6 +1255,36 @@ uint64_t qwref_decoder_weights_hash(qwref_decoder *d) {
     return hash_qmat(&d->lm_head, h);
 }
 
+/* One cache row of a layer as the decoder holds it (decoder.zig:58-65):
+ * q8: the row's f16 key scales, its key codes, then the same for the values;
+ * f32: the key row then the value row. Returns the bytes written to `out`,
+ * 0 for a bad argument or a too small `capacity`. */
+uint64_t qwref_decoder_cache_row(qwref_decoder *d, uint32_t seq, uint32_t layer, uint32_t position, uint8_t *out,
+                                 uint64_t capacity) {
+    if (seq >= d->batch || layer >= d->c.layers || position >= d->c.max_positions) return 0;
+    const uint32_t kvw = d->c.kv_heads * d->c.head_dim;
+    const size_t layer_offset = (size_t)layer * d->cache_stride;
+    const sequence_state *s = &d->seqs[seq];
+    if (d->cache_format == QWREF_CACHE_F32) {
+        const size_t row = (size_t)kvw * sizeof(float);
+        if (capacity < 2 * row) return 0;
+        memcpy(out, s->keys + layer_offset + (size_t)position * row, row);
+        memcpy(out + row, s->values + layer_offset + (size_t)position * row, row);
+        return 2 * row;
+    }
+    const size_t scale_bytes = (size_t)(kvw / QWREF_GROUP) * 2u;
+    const size_t scale_offset = layer_offset + (size_t)position * scale_bytes;
+    const size_t code_offset = layer_offset + d->cache_scales + (size_t)position * kvw;
+    if (capacity < 2 * (scale_bytes + kvw)) return 0;
+    const uint8_t *planes[2] = {s->keys, s->values};
+    for (int kv = 0; kv < 2; ++kv) {
+        uint8_t *dst = out + kv * (scale_bytes + kvw);
+        memcpy(dst, planes[kv] + scale_offset, scale_bytes);
+        memcpy(dst + scale_bytes, planes[kv] + code_offset, kvw);
+    }
+    return 2 * (scale_bytes + kvw);
+}
+
 uint64_t qwref_decoder_cache_hash(qwref_decoder *d, uint32_t seq) {
     if (seq >= d->batch) return 0;
     uint64_t h = 0xcbf29ce484222325ull;

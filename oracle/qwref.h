@@ -209,6 +209,10 @@ int32_t qwref_decoder_step(qwref_decoder *decoder, uint32_t seq, uint32_t token,
  * gate up down, lm_head; scales then data). */
 uint64_t qwref_decoder_weights_hash(qwref_decoder *decoder);
 uint64_t qwref_decoder_cache_hash(qwref_decoder *decoder, uint32_t seq);
+/* One cache row: q8 key scales, key codes, value scales, value codes (f32:
+ * key row, value row); returns the bytes written, 0 on a bad argument. */
+uint64_t qwref_decoder_cache_row(qwref_decoder *decoder, uint32_t seq, uint32_t layer, uint32_t position,
+                                 uint8_t *out, uint64_t capacity);
 uint32_t qwref_synthetic_start_token(uint32_t seed, uint32_t seq, uint32_t vocab);
 
 void qwref_set_threads(int32_t threads);

@@ -36,7 +36,6 @@ namespace {
 
 constexpr float kNeg = -1.0e30f;  // running-max sentinel: finite, so exp2(kNeg - kNeg) is defined
 constexpr float kLog2e = 1.44269504088896340736f;
-constexpr int kBlockPositions = 4; // positions per lane group between softmax rescales
 constexpr int kWaves = 4;
 constexpr uint32_t kMaxSplits = 512;
 
@@ -179,44 +178,98 @@ __device__ __forceinline__ void attend_f32(SoftmaxState<R> &st, const float (&q)
             for (int i = 0; i < 16; ++i) st.acc[r][i] = fmaf(w[nb][r], v[nb][i], st.acc[r][i]);
 }
 
-// One block of NB positions per lane group: scores against the lane's query
-// slices, online-softmax update, value accumulation.
-template <int D, int R, int NB>
-__device__ __forceinline__ void attend(SoftmaxState<R> &st, const float (&q)[R][16], const uint4 (&kc)[NB],
-                                       const uint4 (&vc)[NB], const float (&ks)[NB], const float (&vs)[NB],
-                                       const bool (&valid)[NB], float scaling) {
-    constexpr int LPP = D / 16;
-    // Scores: sum_i (u_i - 128) q_i per 16-value slice, times the slice's
-    // group scale, summed over the LPP lanes of the position, times the
-    // scaling.
-    float score[NB][R];
+// ---- q8 range kernel: key scores on the matrix cores ----
+//
+// The scores of 16 positions against up to four query heads are one
+// v_mfma_i32_16x16x64_i8 per 64-value scale group, on exact integers:
+//   keys     the codes u - 128 as signed bytes (u ^ 0x80);
+//   query    per head and group, x_int = rint(q * 2^(22-e)) with 2^e bounding
+//            the group's largest |q| (|x_int| <= 2^22), as three signed
+//            base-256 digit planes d0 + 256 d1 + 65536 d2, the encoding of the
+//            small-batch GEMV's activations.
+// Operand rows (A) are (head, plane) = 4 * head + plane (plane 3 is zero),
+// operand columns (B) are positions, and both take the 64 group values in
+// the same order (lane l: values 16 * (l / 16) .. +15), so the sum runs over
+// the whole group. Lane l then holds the three plane sums of head l / 16 for
+// position l % 16 ("score layout"); their combination times the group's f16
+// key scale and 2^(e-22) is the group's share of the score
+// sum_g scale_g * sum_{d in g} (u_d - 128) q_d (kernels.zig:727-735).
+// Each plane sum is at most 64 * 128 * 128 = 2^20 in magnitude: the int32
+// results are exact.
+//
+// The values are accumulated on the vector ALUs in the "value layout": a head
+// row of D codes is D/16 lanes of 16 bytes (a lane group), each lane group
+// takes kTile / (64 / (D/16)) consecutive positions of the wavefront's tile.
+// The softmax weights cross from the score layout to the value layout
+// through a wavefront-private LDS row per head. The running maximum of each
+// head is one value for the whole wavefront (it is reduced over the 16
+// positions of a block and read back as a scalar), so the accumulators of
+// all lane groups share it, rescale by one scalar factor (skipped while the
+// maximum stands still), and merge at the end by plain sums.
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 32;                 // positions per wavefront per iteration
+constexpr int kTileBlocks = kTile / 16;   // 16-position MFMA blocks per tile
+constexpr int kWRow = kTile + 4;          // LDS row of a head's weights (floats)
+
+// LDS stores of this wavefront before its later LDS loads of other lanes'
+// data (LDS operations of one wavefront complete in order; the fences keep
+// the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 16 q8 codes as signed bytes u - 128.
+__device__ __forceinline__ v4i signed_codes(const uint4 w) {
+    v4i b;
+    b.x = (int)(w.x ^ 0x80808080u);
+    b.y = (int)(w.y ^ 0x80808080u);
+    b.z = (int)(w.z ^ 0x80808080u);
+    b.w = (int)(w.w ^ 0x80808080u);
+    return b;
+}
+
+// Digit plane `plane` of x_int = rint(x * up) for 16 values (byte b of the
+// result belongs to x[b]): (x_int + 0x808080) ^ 0x808080 holds the three
+// signed digits as its bytes.
+__device__ __forceinline__ v4i digit_plane16(const float *x, float up, int plane) {
+    v4i out;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        float c[16];
-        unpack16(kc[nb], c);
+    for (int w = 0; w < 4; ++w) {
+        uint32_t word = 0;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float dot = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dot = fmaf(c[i], q[r][i], dot);
-            const float part = group_sum<LPP>(dot * ks[nb]);
-            score[nb][r] = valid[nb] ? part * scaling : kNeg;
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t u = (uint32_t)((int)__builtin_rintf(x[4 * w + b] * up) + 0x808080) ^ 0x808080u;
+            word |= ((u >> (8 * plane)) & 0xffu) << (8 * b);
         }
+        out[w] = (int)word;
     }
-    float w[NB][R];
-    softmax_update<R, NB>(st, score, valid, w);
-    // Values: acc += (p * scale) * (u - 128).
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        float c[16];
-        unpack16(vc[nb], c);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float wv = w[nb][r] * vs[nb];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) st.acc[r][i] = fmaf(wv, c[i], st.acc[r][i]);
-        }
-    }
+    return out;
+}
+
+// Sum over the lanes that hold the same 16-byte slice for other positions
+// (lanes l ^ (k * LPP)).
+template <int LPP>
+__device__ __forceinline__ float sum_over_groups(float v) {
+    if constexpr (LPP <= 4) v += dev::xor_lane<4>(v);
+    if constexpr (LPP <= 8) v += dev::xor_lane<8>(v);
+    if constexpr (LPP <= 16) v += dev::xor_lane<16>(v);
+    return v + dev::xor_lane<32>(v);
+}
+
+// Maximum over the 16 lanes of a score-layout row (one head, 16 positions).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dev::xor_lane<1>(v));
+    v = fmaxf(v, dev::xor_lane<2>(v));
+    v = fmaxf(v, dev::xor_lane<4>(v));
+    return fmaxf(v, dev::xor_lane<8>(v));
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
 // Online-softmax merge of (m, l, acc) into a running (M, L, A).
@@ -261,17 +314,15 @@ __device__ __forceinline__ void merge_lane_groups(SoftmaxState<R> &st) {
     merge_step<32, R>(st);
 }
 
-// The end of a range kernel: merges the lane groups of each wave (lanes l
-// and l ^ (k * LPP) hold the same slice for different positions), then the
-// waves in wave order through LDS, into this range's (acc, m, l) record.
+// The end of a range kernel: the lanes of lane group 0 hold their wave's
+// merged state for their slice (the lane groups already merged), and the
+// waves merge in wave order through LDS into this range's (acc, m, l) record.
 template <int D, int R>
-__device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, SoftmaxState<R> &st, uint32_t b,
+__device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, const SoftmaxState<R> &st, uint32_t b,
                                                    uint32_t kvh, uint32_t split, int wave, int sub, int group) {
-    constexpr int LPP = D / 16;
     constexpr int REC = R * D + 4 * R;
     __shared__ float lds_acc[kWaves][R][D];
     __shared__ float lds_ml[kWaves][R][2];
-    merge_lane_groups<LPP, R>(st);
     if (group == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -308,15 +359,20 @@ __device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, Soft
 }
 
 template <int D, int R, bool Decoder>
-__global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) {
-    constexpr int LPP = D / 16;              // lanes per position
-    constexpr int PPW = 64 / LPP;            // positions per wave per load
-    constexpr int STEP = PPW * kWaves;       // positions per workgroup per load
-    constexpr int GPH = D / 64;              // scale groups per head
+__device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
+    constexpr int LPP = D / 16;              // value layout: lanes per position
+    constexpr int PPW = 64 / LPP;            // value layout: lane groups per wave
+    constexpr int NV = kTile / PPW;          // consecutive positions per lane group per tile
+    constexpr int G = D / 64;                // scale groups per head
+    constexpr int HS = (R + 3) / 4;          // MFMA row sets of four heads
+    constexpr uint32_t kSpan = kTile * kWaves;
+    static_assert(R <= PPW, "one lane group per head in the query prologue");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int sub = lane % LPP;              // 16-byte slice of the head row
-    const int group = lane / LPP;            // lane group within the wave
+    const int sub = lane % LPP;              // value layout: 16-byte slice of the head row
+    const int group = lane / LPP;            // value layout: lane group
+    const int n = lane & 15;                 // score layout: position in the block
+    const int quarter = lane >> 4;           // score layout: head in the row set; operand value slice
     const uint32_t split = blockIdx.x;
     const uint32_t kvh = blockIdx.y;
     const uint32_t b = blockIdx.z;
@@ -327,57 +383,60 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
     const uint16_t *v_scales = reinterpret_cast<const uint16_t *>(a.v_scales + b * a.scale_stride);
     const uint8_t *k_codes = a.k_codes + b * a.code_stride;
     const uint8_t *v_codes = a.v_codes + b * a.code_stride;
-    const uint32_t scale_col = kvh * GPH + sub / 4;   // group of this lane's slice
+    const uint32_t key_col = kvh * D + quarter * 16;   // + 64 g
     const uint32_t code_col = kvh * D + sub * 16;
-    constexpr uint32_t kSpan = STEP * kBlockPositions;
+    const uint32_t vscale_col = kvh * G + sub / 4;
 
-    // A block of cache rows: this lane's slice of kBlockPositions positions,
-    // scales as raw f16 bits.
-    struct Block {
-        uint4 kc[kBlockPositions], vc[kBlockPositions];
-        uint32_t ks[kBlockPositions], vs[kBlockPositions];
+    __shared__ float lds_q[R][D];
+    __shared__ int lds_exp[R][G];
+    __shared__ float lds_w[kWaves][R][kWRow];
+    float(&wrow)[R][kWRow] = lds_w[wave];
+
+    // A tile: the wavefront's kTile positions from base + wave * kTile; keys
+    // and key scales in the score layout, values and value scales in the
+    // value layout, scales as raw f16 bits.
+    struct Tile {
+        uint4 kc[kTileBlocks][G];
+        uint32_t ks[kTileBlocks][G];
+        uint4 vc[NV];
+        uint32_t vs[NV];
     };
-    // Loads rows base + ...; a row at or past `limit` (>= 1) loads row
-    // limit - 1 instead, and is masked out when the block is used. Every
-    // load is unconditional, so all of them are in flight together (a load
-    // under a branch waits for its data before the next one issues).
-    auto load_block = [&](Block &blk, uint32_t base, uint32_t limit) {
+    // A row at or past `limit` (>= 1) loads row limit - 1 instead and is
+    // masked out when the tile is used. Every load is unconditional, so all
+    // of them are in flight together.
+    auto load_tile = [&](Tile &t, uint32_t base, uint32_t limit) {
+        const uint32_t first = base + wave * kTile;
 #pragma unroll
-        for (int nb = 0; nb < kBlockPositions; ++nb) {
-            const uint32_t p = base + nb * STEP + wave * PPW + group;
+        for (int blk = 0; blk < kTileBlocks; ++blk) {
+            const uint32_t p = first + 16 * blk + n;
             const uint32_t row = p < limit ? p : limit - 1;
-            blk.kc[nb] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)row * kv_width + code_col);
-            blk.vc[nb] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)row * kv_width + code_col);
-            blk.ks[nb] = k_scales[(size_t)row * gpr + scale_col];
-            blk.vs[nb] = v_scales[(size_t)row * gpr + scale_col];
-        }
-    };
-    // Rows base + ... below `end` take part; the others (possibly never
-    // written, so their bits are arbitrary) get no score and zero scales, so
-    // no stale bits reach the sums.
-    auto use_block = [&](SoftmaxState<R> &st, const float (&q)[R][16], const Block &blk, uint32_t base,
-                         uint32_t end) {
-        bool valid[kBlockPositions];
-        float ks[kBlockPositions], vs[kBlockPositions];
 #pragma unroll
-        for (int nb = 0; nb < kBlockPositions; ++nb) {
-            valid[nb] = base + nb * STEP + wave * PPW + group < end;
-            ks[nb] = valid[nb] ? dev::f16_bits_to_f32((uint16_t)blk.ks[nb]) : 0.0f;
-            vs[nb] = valid[nb] ? dev::f16_bits_to_f32((uint16_t)blk.vs[nb]) : 0.0f;
+            for (int g = 0; g < G; ++g) {
+                t.kc[blk][g] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)row * kv_width + key_col + 64 * g);
+                t.ks[blk][g] = k_scales[(size_t)row * gpr + kvh * G + g];
+            }
         }
-        attend<D, R, kBlockPositions>(st, q, blk.kc, blk.vc, ks, vs, valid, a.scaling);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const uint32_t p = first + NV * group + v;
+            const uint32_t row = p < limit ? p : limit - 1;
+            t.vc[v] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)row * kv_width + code_col);
+            t.vs[v] = v_scales[(size_t)row * gpr + vscale_col];
+        }
     };
-    // The first block is loaded before the sequence's position is known
-    // (in the decoder it is a device value, one memory round trip away):
-    // every allocated row is readable, and rows past the position are
-    // dropped below once it has arrived. The query slices and norm weights
-    // do not depend on it either.
-    Block cur, nxt;
-    load_block(cur, begin, a.rows);
+
+    // The first tile is loaded before the sequence's position is known (in
+    // the decoder it is a device value, one memory round trip away): every
+    // allocated row is readable, and rows past the position are dropped once
+    // it has arrived. The query slices and norm weights do not depend on it
+    // either. Lane group r < R of wavefront 0 takes query head r.
+    Tile cur, nxt;
+    load_tile(cur, begin, a.rows);
+    const bool prologue = wave == 0 && group < R;
+    const int qh = prologue ? group : 0;
     const float *row = a.query + (size_t)b * a.query_stride;
-    float q[R][16];
-#pragma unroll
-    for (int r = 0; r < R; ++r) load16(row + (kvh * R + r) * D + sub * 16, q[r]);
+    float q[16];
+    load16(row + (kvh * R + qh) * D + sub * 16, q);
     float wq[16], rc[16], rs[16];
     if (Decoder) {
         const int j0 = (sub % (LPP / 2)) * 16;
@@ -393,32 +452,190 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) 
 
     if (begin >= cached) return;  // no record: the merge reads ranges below cached only
     if (Decoder) {
+        rms_norm16<D>(q, wq, a.eps);
+        rope16<D>(q, rc, rs, sub);
+    }
+    // The query heads and each group's exponent into LDS.
+    float amax = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            rms_norm16<D>(q[r], wq, a.eps);
-            rope16<D>(q[r], rc, rs, sub);
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(q[i]));
+    amax = fmaxf(amax, dev::xor_lane<1>(amax));
+    amax = fmaxf(amax, dev::xor_lane<2>(amax));
+    if (prologue) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+            *reinterpret_cast<float4 *>(&lds_q[qh][sub * 16 + i]) = make_float4(q[i], q[i + 1], q[i + 2], q[i + 3]);
+        if (sub % 4 == 0) lds_exp[qh][sub / 4] = dev::chunk_exponent(amax);
+    }
+    __syncthreads();
+    // Operand rows of this lane: head 4 hs + n / 4, plane n % 4; its values
+    // 64 g + 16 quarter .. +15. Score-layout multipliers: head 4 hs + quarter.
+    v4i qa[HS][G];
+    float qm[HS][G];
+#pragma unroll
+    for (int hs = 0; hs < HS; ++hs) {
+        const int ra = 4 * hs + n / 4, plane = n % 4;
+        const int rq = 4 * hs + quarter;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            v4i op = {0, 0, 0, 0};
+            if (ra < R && plane < 3)
+                op = digit_plane16(&lds_q[ra][64 * g + 16 * quarter], __builtin_ldexpf(1.0f, 22 - lds_exp[ra][g]), plane);
+            qa[hs][g] = op;
+            qm[hs][g] = rq < R ? __builtin_ldexpf(a.scaling, lds_exp[rq][g] - 22) : 0.0f;
         }
     }
 
+    // Running state: m (the same in every lane of a head's score row), the
+    // lane's share of l (score layout), acc (value layout).
+    float m[HS], l[HS];
+    float acc[R][16];
+#pragma unroll
+    for (int hs = 0; hs < HS; ++hs) {
+        m[hs] = kNeg;
+        l[hs] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
+
+    // Rows below `end` take part; the others (possibly never written, so
+    // their bits are arbitrary) get no weight and a zero value scale.
+    auto use_tile = [&](const Tile &t, uint32_t base) {
+        const uint32_t first = base + wave * kTile;
+        const v4i zero = {0, 0, 0, 0};
+        float s[HS][kTileBlocks];
+        bool valid[kTileBlocks];
+#pragma unroll
+        for (int blk = 0; blk < kTileBlocks; ++blk) {
+            valid[blk] = first + 16 * blk + n < end;
+            v4i kb[G];
+            float ks[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                kb[g] = signed_codes(t.kc[blk][g]);
+                ks[g] = dev::f16_bits_to_f32((uint16_t)t.ks[blk][g]);
+            }
+#pragma unroll
+            for (int hs = 0; hs < HS; ++hs) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[hs][g], kb[g], zero, 0, 0, 0);
+                    const float dot = (float)(c.x + 256 * c.y) + 65536.0f * (float)c.z;
+                    sc = fmaf(dot, qm[hs][g] * ks[g], sc);
+                }
+                s[hs][blk] = valid[blk] ? sc : kNeg;
+            }
+        }
+        // Online softmax per head over the tile; the weights go to this
+        // wavefront's LDS rows, the rescale factors become scalars.
+        float alpha[R];
+#pragma unroll
+        for (int hs = 0; hs < HS; ++hs) {
+            float mx = s[hs][0];
+#pragma unroll
+            for (int blk = 1; blk < kTileBlocks; ++blk) mx = fmaxf(mx, s[hs][blk]);
+            const float m_new = fmaxf(m[hs], row16_max(mx));
+            const float al = fast_exp2(m[hs] - m_new);
+            float sum = 0.0f;
+            const int rq = 4 * hs + quarter;
+#pragma unroll
+            for (int blk = 0; blk < kTileBlocks; ++blk) {
+                const float w = valid[blk] ? fast_exp2(s[hs][blk] - m_new) : 0.0f;
+                sum += w;
+                if (rq < R) wrow[rq][16 * blk + n] = w;
+            }
+            l[hs] = l[hs] * al + sum;
+            m[hs] = m_new;
+#pragma unroll
+            for (int k = 0; k < 4 && 4 * hs + k < R; ++k) alpha[4 * hs + k] = lane_value(al, 16 * k);
+        }
+        wave_lds_sync();
+        bool moved = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) moved |= alpha[r] != 1.0f;
+        if (moved) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[r][i] *= alpha[r];
+        }
+        // Values: acc += (w * scale) * (u - 128).
+        float w[R][NV];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) w[r][v] = wrow[r][NV * group + v];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const float vs = first + NV * group + v < end ? dev::f16_bits_to_f32((uint16_t)t.vs[v]) : 0.0f;
+            float c[16];
+            unpack16(t.vc[v], c);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float wv = w[r][v] * vs;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[r][i] = fmaf(wv, c[i], acc[r][i]);
+            }
+        }
+        wave_lds_sync();
+    };
+
+    // Double buffered, two tiles per trip: the next tile's loads are in
+    // flight while the current one is scored and accumulated. The loads are
+    // issued whether or not the tile holds positions (past `end` every lane
+    // reads row end - 1, one cached line): a load under a branch makes the
+    // compiler's wait for the current tile also wait for the loads issued
+    // after it. The scheduling barriers keep the work on the current tile
+    // (which waits for its data) from moving above the next tile's loads.
+    for (uint32_t base = begin; base < end; base += 2 * kSpan) {
+        load_tile(nxt, base + kSpan, end);
+        __builtin_amdgcn_sched_barrier(0);
+        use_tile(cur, base);
+        if (base + kSpan >= end) break;
+        load_tile(cur, base + 2 * kSpan, end);
+        __builtin_amdgcn_sched_barrier(0);
+        use_tile(nxt, base + kSpan);
+    }
+
+    // The wave's state: the lane groups share each head's maximum, so their
+    // accumulators merge by sums; l is summed over the head's score row.
     SoftmaxState<R> st;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        st.m[r] = kNeg;
-        st.l[r] = 0.0f;
+    for (int hs = 0; hs < HS; ++hs) {
+        float lsum = l[hs];
+        lsum += dev::xor_lane<1>(lsum);
+        lsum += dev::xor_lane<2>(lsum);
+        lsum += dev::xor_lane<4>(lsum);
+        lsum += dev::xor_lane<8>(lsum);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st.acc[r][i] = 0.0f;
+        for (int k = 0; k < 4 && 4 * hs + k < R; ++k) {
+            st.m[4 * hs + k] = lane_value(m[hs], 16 * k);
+            st.l[4 * hs + k] = lane_value(lsum, 16 * k);
+        }
     }
-
-    // Double buffered: the next block's loads are in flight while the
-    // current one is scored and accumulated.
-    for (uint32_t base = begin; base < end; base += kSpan) {
-        const bool more = base + kSpan < end;
-        if (more) load_block(nxt, base + kSpan, end);
-        use_block(st, q, cur, base, end);
-        if (more) cur = nxt;
-    }
-
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.acc[r][i] = sum_over_groups<LPP>(acc[r][i]);
     write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
+}
+
+// The q8 range kernel. Forms that fit three wavefronts per SIMD (168
+// registers) without spilling are compiled for that occupancy.
+template <int D, int R, bool Decoder>
+constexpr bool kThreeWaves = R <= 2 && (D == 64 || (D == 128 && Decoder));
+
+template <int D, int R, bool Decoder>
+__global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) {
+    attention_range<D, R, Decoder>(a);
+}
+
+template <int D, int R, bool Decoder>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel3(const AttnKernelArgs a) {
+    attention_range<D, R, Decoder>(a);
 }
 
 // The range kernel over an f32 cache (kernels.zig:572-627): the same lane
@@ -520,6 +737,7 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(const AttnKernelArgs
         use_block(st, q, cur, base, end);
         if (more) cur = nxt;
     }
+    merge_lane_groups<LPP, R>(st);
     write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
 }
 
@@ -758,15 +976,25 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float *key, const 
     if (lane == 0) reinterpret_cast<uint16_t *>(scales)[(size_t)position * gpr + g] = bits;
 }
 
-void attention_shape(int cus, const AttentionArgs &a, uint32_t &chunk, uint32_t &splits) {
-    // Positions per workgroup: a multiple of one full block (STEP * 4), at
-    // least two of them; enough workgroups to fill the device about twice, at
-    // most kMaxSplits ranges. (At batch 1, 128-position ranges spend more on
-    // the per-range query prologue and the combine than their extra
-    // workgroups win back: 17 ranges of 256 beat 34 of 128 at 4096 positions.)
-    const uint32_t lpp = a.head_dim / 16;
-    const uint32_t step = (64 / lpp) * kWaves * kBlockPositions;
-    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256) * 2;
+// Workgroups of the range kernel resident per CU: three where the kernel is
+// compiled for three wavefronts per SIMD (kThreeWaves), else two.
+uint32_t resident_groups(const AttentionArgs &a, bool decoder) {
+    const uint32_t ratio = a.heads / a.kv_heads;
+    return !a.f32_cache && ratio <= 2 && (a.head_dim == 64 || (a.head_dim == 128 && decoder)) ? 3 : 2;
+}
+
+// Ranges of `chunk` positions for the decoder form (q/k norms given: the
+// decoder step) or the plain form.
+void attention_shape(int cus, const AttentionArgs &a, bool decoder, uint32_t &chunk, uint32_t &splits) {
+    // Positions per workgroup: a multiple of one workgroup iteration of the
+    // q8 kernel (kTile * kWaves = 128 positions; the f32 kernel's iteration
+    // divides it), at least two of them; as many workgroups as the device
+    // holds at once, at most kMaxSplits ranges. (At batch 1, 128-position ranges
+    // spend more on the per-range query prologue and the combine than their
+    // extra workgroups win back: 17 ranges of 256 beat 34 of 128 at 4096
+    // positions.)
+    const uint32_t step = kTile * kWaves;
+    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256) * resident_groups(a, decoder);
     const uint32_t pairs = a.batch * a.kv_heads;
     uint32_t want_splits = (target + pairs - 1) / pairs;
     if (want_splits < 1) want_splits = 1;
@@ -780,11 +1008,22 @@ void attention_shape(int cus, const AttentionArgs &a, uint32_t &chunk, uint32_t 
 
 }  // namespace
 
-size_t attention_scratch_bytes(int cus, const AttentionArgs &a) {
-    uint32_t chunk, splits;
-    attention_shape(cus, a, chunk, splits);
+namespace {
+
+size_t record_bytes(const AttentionArgs &a, uint32_t splits) {
     const uint32_t R = a.heads / a.kv_heads;
     return (size_t)a.batch * a.kv_heads * splits * (R * a.head_dim + 4 * R) * sizeof(float) + 256;
+}
+
+}  // namespace
+
+// Enough for either form's ranges, so a buffer sized before the norm
+// pointers are known (the decoder's) holds the decoder form's records.
+size_t attention_scratch_bytes(int cus, const AttentionArgs &a) {
+    uint32_t chunk, plain, decoder;
+    attention_shape(cus, a, false, chunk, plain);
+    attention_shape(cus, a, true, chunk, decoder);
+    return record_bytes(a, plain > decoder ? plain : decoder);
 }
 
 bool attention_supported(uint32_t head_dim, uint32_t ratio) {
@@ -806,10 +1045,12 @@ void launch_attention_pair(hipStream_t s, const AttnKernelArgs &k, bool decoder,
             attention_combine_kernel<D, R, false, true><<<merge, 256, 0, s>>>(k);
         }
     } else if (decoder) {
-        attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
+        if constexpr (kThreeWaves<D, R, true>) attention_kernel3<D, R, true><<<ranges, 256, 0, s>>>(k);
+        else attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
         attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
     } else {
-        attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
+        if constexpr (kThreeWaves<D, R, false>) attention_kernel3<D, R, false><<<ranges, 256, 0, s>>>(k);
+        else attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
         attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     }
 }
@@ -820,11 +1061,14 @@ void launch_attention_pair(hipStream_t s, const AttnKernelArgs &k, bool decoder,
         return hipGetLastError();                                                                   \
     }
 
-hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArgs &a, void *scratch) {
-    uint32_t chunk, splits;
-    attention_shape(cus, a, chunk, splits);
-    const uint32_t R = a.heads / a.kv_heads;
+hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArgs &a, void *scratch,
+                                      size_t scratch_bytes) {
     const bool decoder = a.q_norm != nullptr;
+    uint32_t chunk, splits;
+    attention_shape(cus, a, decoder, chunk, splits);
+    // Every range writes a record: refuse a scratch that cannot hold them.
+    if (record_bytes(a, splits) > scratch_bytes) return hipErrorInvalidValue;
+    const uint32_t R = a.heads / a.kv_heads;
     AttnKernelArgs k{};
     k.query = a.query;
     k.query_stride = a.query_stride ? a.query_stride : a.heads * a.head_dim;

@@ -620,7 +620,8 @@ int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query
                               heads, kv_heads, head_dim, batch, scale_stride_bytes, code_stride_bytes, a));
     if (a.batch == 0) return QWH_OK;
     QWH_TRY(ensure_workspace(ctx, ctx->scratch, attention_scratch_bytes(ctx->cus, a)));
-    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr), "decode attention q8");
+    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr, ctx->scratch.bytes),
+                     "decode attention q8");
 }
 
 int32_t qwh_decode_attention_q8_noalloc(qwh_ctx *ctx, float *out_dev, const float *query_dev,
@@ -641,7 +642,8 @@ int32_t qwh_decode_attention_q8_noalloc(qwh_ctx *ctx, float *out_dev, const floa
     if (!ptr) return fail(ctx, QWH_E_DEVICE, "device %d has no resolved scratch", ctx->device);
     // The records need no clearing: each range writes its record before the
     // merge reads it, and ranges past `cached` are never read.
-    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ptr), "decode attention q8 (no alloc)");
+    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ptr, kNoAllocScratchBytes),
+                     "decode attention q8 (no alloc)");
 }
 
 int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *query_dev, const float *keys_dev,
@@ -682,7 +684,8 @@ int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *quer
     a.code_stride = stride_bytes;
     a.f32_cache = true;
     QWH_TRY(ensure_workspace(ctx, ctx->scratch, attention_scratch_bytes(ctx->cus, a)));
-    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr), "decode attention f32");
+    return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ctx->scratch.ptr, ctx->scratch.bytes),
+                     "decode attention f32");
 }
 
 int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_dev, uint32_t kv_width, uint32_t position,

@@ -206,9 +206,12 @@ struct AttentionArgs {
     void *digits = nullptr;
 };
 bool attention_supported(uint32_t head_dim, uint32_t ratio);
+// Scratch bytes for the range records of either form of the attention.
 size_t attention_scratch_bytes(int cus, const AttentionArgs &a);
+// Fails with hipErrorInvalidValue, launching nothing, when scratch_bytes
+// cannot hold the launch's range records.
 hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArgs &a,
-                                      void *scratch);
+                                      void *scratch, size_t scratch_bytes);
 hipError_t launch_kv_append_q8(hipStream_t s, const float *key, const float *value,
                                uint32_t kv_width, uint32_t position, uint8_t *k_scales,
                                uint8_t *k_codes, uint8_t *v_scales, uint8_t *v_codes);

@@ -310,6 +310,7 @@ struct qwh_decoder {
     float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
     void *digits = nullptr;
     void *attn_scratch = nullptr;
+    size_t attn_scratch_bytes = 0;
     float *arg_v = nullptr;
     uint32_t *arg_i = nullptr;
     uint32_t arg_parts = 0, arg_per_block = 0;
@@ -537,7 +538,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         // Batched: the attention output also arrives as the O projection's
         // digit planes.
         aa.digits = d->batched ? d->batch_digits : nullptr;
-        err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch);
+        err = launch_decode_attention_q8(s, ctx->cus, aa, d->attn_scratch, d->attn_scratch_bytes);
         if (err != hipSuccess) break;
         if (d->split_parts) {
             // o, gate|up, down as partial sums; each prep adds the previous
@@ -810,7 +811,8 @@ int32_t qwh_decoder_create_cache(qwh_ctx *ctx, const qwh_decoder_config *config,
     aa.head_dim = c.head_dim;
     aa.batch = batch;
     aa.f32_cache = cache_format == QWH_CACHE_F32;
-    if (st == QWH_OK) st = dalloc(d, attention_scratch_bytes(ctx->cus, aa), &d->attn_scratch);
+    d->attn_scratch_bytes = attention_scratch_bytes(ctx->cus, aa);
+    if (st == QWH_OK) st = dalloc(d, d->attn_scratch_bytes, &d->attn_scratch);
     d->arg_per_block = 4096;
     d->arg_parts = (c.vocab + d->arg_per_block - 1) / d->arg_per_block;
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_v));

@@ -2,11 +2,14 @@
 16 / 8 heads of 128, SwiGLU 6144, vocab 151936, q4 weights, q8 cache
 prefilled to 4096 positions, seed 4) against the CPU oracle:
 
-  - teacher-forced logits of every sequence's first steps against
-    tests/golden/decoder_1p7b_logits.json (the 16 largest, a fixed sample
-    across the vocabulary), within 1e-3 relative;
+  - teacher-forced logits of every sequence at steps 0, 1, 64, 127 and 255
+    against tests/golden/decoder_1p7b_logits.json (the 16 largest, a fixed
+    sample across the vocabulary), within 1e-3 relative and within the
+    per-step error bound below;
   - 256 greedy steps per sequence against the oracle's ids in
-    tests/golden/decoder_1p7b_ids.json (tests/golden/make_decoder_ids.py).
+    tests/golden/decoder_1p7b_ids.json (tests/golden/make_decoder_ids.py),
+    identical but for runner-up picks inside the tie window the error bound
+    gives (44 of the fixture's 4096 steps lie inside it).
 
 decoder.zig:133-339 (forwardToken, step, argmaxLogits)."""
 import json
@@ -23,12 +26,23 @@ HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 IDS = os.path.join(HERE, "decoder_1p7b_ids.json")
 LOGITS = os.path.join(HERE, "decoder_1p7b_logits.json")
 
-# The measured error of these logits against the oracle is about 1e-6 of
-# their magnitude (different float summation order; the tokens' logits are
-# 3.5 to 5.2). A step may pick the oracle's runner-up only when the oracle's
-# two best logits lie within ten times that: 1e-5 of the best one, which 1 of
-# the fixture's 4096 steps does.
-TIE = 1e-5
+# Teacher-forced logit error against the oracle, as a fraction of the step's
+# largest logit, bounded per recorded step: twice the worst measured over the
+# 16 sequences at batch 1 and batch 16 (measured: step 0 8.1e-6, step 1
+# 2.0e-5, step 64 9.8e-5, step 127 1.56e-4, step 255 1.97e-4). The error
+# grows with the step: each step appends key and value rows whose q8 codes
+# may round the other way at a tie (the device's products sum in another
+# order; test_gpu_decoder.py pins that those rows differ from the oracle's
+# only there), and later steps attend to more of those rows.
+ERROR_BOUND = {0: 2e-5, 1: 4e-5, 64: 2e-4, 127: 3.2e-4, 255: 4e-4}
+
+
+def tie_window(step):
+    """The largest gap between the oracle's two best logits (as a fraction
+    of the best) at which the device may pick the runner-up: the two logits
+    each carry at most the error bound of the first recorded step at or after
+    `step`."""
+    return 2 * ERROR_BOUND[min(s for s in ERROR_BOUND if s >= step)]
 
 
 def load(path):
@@ -58,10 +72,10 @@ def run(ctx, golden, batch):
 def check(ids, golden, batch):
     """Every sequence matches the oracle's greedy ids, but for a near tie: at
     the first differing step the GPU took the oracle's runner-up, and the
-    oracle's two best logits lie within TIE of each other. From there the
-    sequence continues from another token, so its comparison ends; the other
-    sequences are still compared in full. Returns (identical sequences,
-    identical steps)."""
+    oracle's two best logits lie within tie_window(step) of each other. From
+    there the sequence continues from another token, so its comparison ends;
+    the other sequences are still compared in full. Returns (identical
+    sequences, identical steps)."""
     same_seqs = same_steps = 0
     for b in range(batch):
         expected = golden["ids"][b][1:]
@@ -75,7 +89,9 @@ def check(ids, golden, batch):
         msg = f"sequence {b}: first difference at step {first}: {got[first]} != {expected[first]}"
         top, second = golden["top"][b][first], golden["second"][b][first]
         assert got[first] == golden["runner_up"][b][first], f"{msg} (runner-up {golden['runner_up'][b][first]})"
-        assert top - second <= TIE * abs(top), f"{msg}: oracle logits {top} and {second} are not a near tie"
+        assert top - second <= tie_window(first) * abs(top), \
+            f"{msg}: oracle logits {top} and {second} are not a near tie"
+        print(f"{msg}: the oracle's runner-up, {(top - second) / abs(top):.2e} below its best")
     print(f"identical: {same_seqs} of {batch} sequences, {same_steps} of {batch * golden['steps']} steps")
     return same_seqs, same_steps
 
@@ -107,6 +123,8 @@ def check_logits(ctx, golden, ref, batch):
         dec.close()
     print("teacher-forced logits, worst error / largest logit per step: " +
           ", ".join(f"{s}: {w:.2e}" for s, w in worst.items()))
+    for s, w in worst.items():
+        assert w <= ERROR_BOUND[s], f"step {s}: error {w:.2e} above its bound {ERROR_BOUND[s]:.1e}"
     return worst
 
 

@@ -613,3 +613,30 @@ def test_decoder_step_argmax_and_position_limit():
             dec.step(0, t)  # decoder.zig:142 PositionExceeded
     finally:
         dec.close()
+
+
+def test_decoder_cache_row_reads_the_prefilled_rows():
+    # decoder.zig:85-105: a prefilled q8 row is quantizeRow(.q8) of the
+    # generator's values (stream 0x10000 + 0x100 seq + 2 layer + kv); the f32
+    # cache keeps the values themselves (decoder.zig:77-83).
+    cfg = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=1000,
+               max_positions=16, eps=1e-6, theta=1e6)
+    kvw = cfg["kv_heads"] * cfg["head_dim"]
+    for cache in (o.CACHE_Q8, o.CACHE_F32):
+        d = o.Decoder(7, 2, o.Q4, cache, **cfg)
+        try:
+            d.prefill_random(1, 5)
+            for layer in range(2):
+                rows = [o.normal(5 * kvw, 7, 0x10000 + 0x100 * 1 + 2 * layer + kv).reshape(5, kvw) for kv in (0, 1)]
+                for p in (0, 4):
+                    got = d.cache_row(1, layer, p)
+                    if cache == o.CACHE_F32:
+                        want = rows[0][p].tobytes() + rows[1][p].tobytes()
+                    else:
+                        want = b"".join(s.tobytes() + c.tobytes()
+                                        for s, c in (o.quantize_rows(o.Q8, r[p:p + 1]) for r in rows))
+                    assert got == want, (cache, layer, p)
+            with pytest.raises(ValueError):
+                d.cache_row(2, 0, 0)
+        finally:
+            d.close()
