@@ -421,7 +421,7 @@ def bench_audio(ctx, qa, steps):
         "workload": "Qwen3-ASR-0.6B audio layer, 390 steps, window 104, q4 weights, f32 activations",
         "frontend_30s_ms": front_ms, "frontend_TFLOPs": front_flops / (front_ms * 1e-3) / 1e12,
         "frontend_workload": "3000 mel frames x 128 bins, 30 chunks, 3 convolutions of 480 channels (f16 weights, "
-                             "f32 FMA), conv_out 896 x 7680 q4, 375 rows",
+                             "f32 FMA), conv_out 896 x 7680 q4, 390 rows",
         "layer_us": layer_ms * 1e3, "layer_TFLOPs": (layer_flops + att_flops) / (layer_ms * 1e-3) / 1e12,
         "tower_18_layers_ms": 18 * layer_ms,
         "attention_us": att_ms * 1e3, "attention_GFLOPs": att_flops / (att_ms * 1e-3) / 1e9,
@@ -444,8 +444,9 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true")
     ap.add_argument("--decoder-batches", default="1,16", help="comma-separated decoder batch sizes")
-    ap.add_argument("--decoders", default="q4,q8,f32kv",
-                    help="decoder variants: q4 (q4 weights, q8 cache), q8 (q8 weights), f32kv (q4, f32 cache)")
+    ap.add_argument("--decoders", default="q4,q8,q5,f32kv",
+                    help="decoder variants: q4 (q4 weights, q8 cache), q8 (q8 weights), q5 (q5 weights), "
+                         "f32kv (q4, f32 cache)")
     ap.add_argument("--skip-headline", action="store_true", help="skip the lm_head GEMV and its read ceiling")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -524,6 +525,12 @@ def main():
             log(f"decoder 1.7B q8 weights, batch {batch}")
             q8[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8, fmt=qa.FORMAT_Q8)
         result["decoder_1p7b_q8_q8kv_ctx4096"] = q8
+    if not args.skip_decoder and "q5" in variants:
+        q5 = {}
+        for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
+            log(f"decoder 1.7B q5 weights, batch {batch}")
+            q5[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8, fmt=qa.FORMAT_Q5)
+        result["decoder_1p7b_q5_q8kv_ctx4096"] = q5
     if not args.skip_decoder and "f32kv" in variants:
         log("decoder 1.7B, f32 cache, batch 1")
         result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=64, warmup=8,

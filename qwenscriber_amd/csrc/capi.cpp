@@ -466,10 +466,24 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
         return check_hip(ctx, launch_gemv_q8(ctx->stream, ctx->cus, x_dev, *m, tokens, out_dev, nullptr), "gemv q8");
     }
     if (m->format == QWH_FORMAT_Q5) {
-        if (!gemv_b8_supported(m->format, m->rows, m->cols))
-            return fail(ctx, QWH_E_UNSUPPORTED, "q5 linear is built for K <= 6144 and data planes below 4 GiB");
         if (((uintptr_t)m->data & 7u) != 0)
             return fail(ctx, QWH_E_INVALID_ARGUMENT, "q5 data plane must be 8-byte aligned");
+        if (tokens >= 2 && gemv_batch_supported(*m)) {
+            // Several tokens (K a multiple of 256): the int8 digit planes and
+            // one matrix-core pass over the codes per 16 tokens.
+            GemvInput in;
+            in.mode = GemvInput::F32;
+            in.x = x_dev;
+            QWH_TRY(ensure_workspace(ctx, ctx->digits, batch_digit_bytes(tokens, cols)));
+            const size_t parts = batch_partial_bytes(tokens, *m);
+            if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
+            QWH_TRY(check_hip(ctx, launch_prep_batch(ctx->stream, in, tokens, cols, ctx->digits.ptr), "prep batch"));
+            return check_hip(ctx, launch_gemv_batch(ctx->stream, ctx->digits.ptr, *m, tokens, out_dev, nullptr, false,
+                                                    static_cast<float *>(ctx->scratch.ptr)),
+                             "gemv q5 batch");
+        }
+        if (!gemv_b8_supported(m->format, m->rows, m->cols))
+            return fail(ctx, QWH_E_UNSUPPORTED, "q5 linear is built for K <= 6144 and data planes below 4 GiB");
         GemvInput in;
         in.mode = GemvInput::F32;
         in.x = x_dev;

@@ -63,6 +63,25 @@ __device__ __forceinline__ v4i expand_q8(v4i n) {
     return b;
 }
 
+// The same operand from a q5 slice of 16 codes (quant.zig:253-269): 8 bytes
+// of nibbles (column 2j in the low nibble of byte j) and the slice's 16 fifth
+// bits (bit j for column j). The fifth bits of the columns {0,2,4,6} (or
+// {1,3,5,7}) of an 8-column block sit at bits 0, 2, 4, 6 of one byte and move
+// to bit 4 of bytes 0..3 with one multiply (no carry reaches those bits);
+// u = nibble | fifth << 4 in [0, 31], and (u + 0x70) ^ 0x80 is u - 16 as a
+// two's complement byte.
+__device__ __forceinline__ uint32_t spread_fifths(uint32_t b) { return ((b & 0x55u) * 0x00410410u) & 0x10101010u; }
+
+__device__ __forceinline__ v4i expand_q5(uint2 nib, uint32_t fifth) {
+    const uint32_t fe = fifth & 0x5555u, fo = (fifth >> 1) & 0x5555u;
+    v4i b;
+    b.x = (int)((((nib.x & 0x0f0f0f0fu) | spread_fifths(fe)) + 0x70707070u) ^ 0x80808080u);
+    b.y = (int)(((((nib.x >> 4) & 0x0f0f0f0fu) | spread_fifths(fo)) + 0x70707070u) ^ 0x80808080u);
+    b.z = (int)((((nib.y & 0x0f0f0f0fu) | spread_fifths(fe >> 8)) + 0x70707070u) ^ 0x80808080u);
+    b.w = (int)(((((nib.y >> 4) & 0x0f0f0f0fu) | spread_fifths(fo >> 8)) + 0x70707070u) ^ 0x80808080u);
+    return b;
+}
+
 // The weight operand of group i, rows r of a wavefront's LDS transpose
 // (PPR 16-byte pieces per row, piece p of row r at slot p ^ (r mod PPR)):
 // BPG = 32 (q4) or 64 (q8) code bytes per group.
@@ -314,6 +333,44 @@ struct SplitShape {
     static_assert(DPIECES % 256 == 0 && (PPR & (PPR - 1)) == 0 && ROWS % RPI == 0, "chunk shape");
 };
 
+// The end of a split GEMV workgroup: lane l holds tokens 4 (l / 16) + r of
+// row l % 16 of each of its TW tiles; it writes its K slice's partial sums,
+// or (one slice) the outputs plus residual, or silu pairs.
+template <int TW>
+__device__ __forceinline__ void split_epilogue(const SplitArgs &a, const float (&acc)[TW][4], uint32_t tile,
+                                               uint32_t row0, int col, int blk) {
+    if (a.part) {
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            const uint32_t out_row = row0 + t * kRowTile + col;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = tile * kTokenTile + blk * 4 + r;
+                if (tok < a.tokens && out_row < a.n)
+                    a.part[((size_t)blockIdx.y * a.tokens + tok) * a.n + out_row] = acc[t][r];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const uint32_t out_row = row0 + t * kRowTile + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = tile * kTokenTile + blk * 4 + r;
+            const float total = acc[t][r];
+            if (a.pairs) {
+                const float partner = __shfl_down(total, 1, 64);
+                if (tok < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
+                    a.out[(size_t)tok * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
+            } else if (tok < a.tokens && out_row < a.n) {
+                const float res = a.residual ? a.residual[(size_t)tok * a.n + out_row] : 0.0f;
+                a.out[(size_t)tok * a.n + out_row] = res + total;
+            }
+        }
+    }
+}
+
 template <int TW, int KC, int BPG>
 __global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
     using S = SplitShape<TW, KC, BPG>;
@@ -433,36 +490,7 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int t = 0; t < TW; ++t) acc[t][r] = __fmul_rn(acc[t][r], inv[r]);
-    if (a.part) {
-#pragma unroll
-        for (int t = 0; t < TW; ++t) {
-            const uint32_t out_row = row0 + t * kRowTile + col;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t tok = tile * kTokenTile + blk * 4 + r;
-                if (tok < a.tokens && out_row < a.n)
-                    a.part[((size_t)blockIdx.y * a.tokens + tok) * a.n + out_row] = acc[t][r];
-            }
-        }
-        return;
-    }
-#pragma unroll
-    for (int t = 0; t < TW; ++t) {
-        const uint32_t out_row = row0 + t * kRowTile + col;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t tok = tile * kTokenTile + blk * 4 + r;
-            const float total = acc[t][r];
-            if (a.pairs) {
-                const float partner = __shfl_down(total, 1, 64);
-                if (tok < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
-                    a.out[(size_t)tok * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
-            } else if (tok < a.tokens && out_row < a.n) {
-                const float res = a.residual ? a.residual[(size_t)tok * a.n + out_row] : 0.0f;
-                a.out[(size_t)tok * a.n + out_row] = res + total;
-            }
-        }
-    }
+    split_epilogue<TW>(a, acc, tile, row0, col, blk);
 }
 
 // Sum over the K slices, in slice order, of the partial sums at p (slices
@@ -494,6 +522,121 @@ __device__ __forceinline__ float4 slice_sum4(const float *p, uint32_t slices, si
             v.w += w[s].w;
         }
     return v;
+}
+
+// The split form over q5 codes. A 40-byte group does not cut into the
+// 16-byte pieces of the LDS weight transpose, so each lane loads its own
+// operand bytes (the 8 nibble bytes and 2 fifth-bit bytes of its 16 columns,
+// for each of its tiles and the chunk's groups) straight into registers, one
+// chunk ahead; the digits, multipliers, scales, split and epilogue are those
+// of gemv_split_kernel with chunks of 4 groups.
+template <int TW>
+__global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
+    constexpr int KC = 4;
+    using S = SplitShape<TW, KC, 32>;  // (digit staging only)
+    constexpr int ROWS = S::ROWS, DPT = S::DPT;
+    __shared__ v4i dl[2][S::DPIECES];
+    __shared__ float4 ml[2][KC * 4];
+    __shared__ float ssl[kTokenTile * 16];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 15;
+    const int blk = lane >> 4;
+    const uint32_t gpr = a.k >> 6;
+    const uint32_t tile = blockIdx.z;
+    const uint32_t row0 = (blockIdx.x * 4 + wave) * ROWS;
+    const size_t row_bytes = (size_t)gpr * 40;
+    const uint32_t g_first = blockIdx.y * a.slice_groups;
+    const uint32_t chunks = a.slice_groups / KC;
+    const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes;
+    const float *mul = a.mult + (size_t)tile * gpr * kTokenTile;
+
+    uint2 rn[TW][KC];
+    uint32_t rf[TW][KC];
+    v4i rd[DPT];
+    float4 rm = {};
+    uint32_t rs[TW][KC / 2];
+    // One chunk's loads (rows past the matrix read its last row; their
+    // results are never stored).
+    auto load = [&](uint32_t g0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            uint32_t row = row0 + t * kRowTile + col;
+            if (row >= a.n) row = a.n - 1;
+            const uint8_t *grp = a.data + row * row_bytes + (size_t)g0 * 40;
+#pragma unroll
+            for (int i = 0; i < KC; ++i) {
+                rn[t][i] = *reinterpret_cast<const uint2 *>(grp + i * 40 + 8 * blk);
+                rf[t][i] = *reinterpret_cast<const uint16_t *>(grp + i * 40 + 32 + 2 * blk);
+            }
+            __builtin_memcpy(rs[t], a.scales + (size_t)row * gpr + g0, 2 * KC);
+        }
+#pragma unroll
+        for (int m = 0; m < DPT; ++m) {
+            const int q = tid + 256 * m;
+            const int L = q & 63;
+            rd[m] = *reinterpret_cast<const v4i *>(dig + ((size_t)g0 * 3 + (q >> 6)) * kPlaneBytes +
+                                                     (L & 15) * 64 + (L >> 4) * 16);
+        }
+        rm = *reinterpret_cast<const float4 *>(mul + (size_t)g0 * kTokenTile + (tid % (KC * 4)) * 4);
+    };
+
+    float acc[TW][4] = {};
+    float inv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    const bool has_ss = a.ss && (uint32_t)tid < kTokenTile * a.ss_parts;
+    const float ssv = has_ss ? a.ss[(size_t)tile * kTokenTile * a.ss_parts + tid] : 0.0f;
+    load(g_first);
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const int buf = c & 1;
+        if (c == 0 && has_ss) ssl[tid] = ssv;
+#pragma unroll
+        for (int m = 0; m < DPT; ++m) dl[buf][tid + 256 * m] = rd[m];
+        if (tid < KC * 4) ml[buf][tid] = rm;
+        // This chunk's operands and scales, out of the registers the next
+        // chunk's loads are about to fill.
+        v4i wop[TW][KC];
+        float sc[TW][KC];
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int i = 0; i < KC; ++i) {
+                wop[t][i] = expand_q5(rn[t][i], rf[t][i]);
+                sc[t][i] = dev::f16_bits_to_f32((uint16_t)(rs[t][i / 2] >> (16 * (i % 2))));
+            }
+        __syncthreads();
+        load(g_first + (c + 1 < chunks ? c + 1 : c) * KC);
+        if (c == 0 && a.ss) tile_rms_inverse(ssl, a.ss_parts, a.k, a.eps, lane, inv);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            const v4i d0 = dl[buf][(i * 3 + 0) * 64 + lane];
+            const v4i d1 = dl[buf][(i * 3 + 1) * 64 + lane];
+            const v4i d2 = dl[buf][(i * 3 + 2) * 64 + lane];
+            const float4 mm = ml[buf][i * 4 + blk];
+            const float m[4] = {mm.x, mm.y, mm.z, mm.w};
+#pragma unroll
+            for (int t = 0; t < TW; ++t) {
+                const v4i zero = {0, 0, 0, 0};
+                const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d0, wop[t][i], zero, 0, 0, 0);
+                const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d1, wop[t][i], zero, 0, 0, 0);
+                const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(d2, wop[t][i], zero, 0, 0, 0);
+                const int q0[4] = {p0.x, p0.y, p0.z, p0.w};
+                const int q1[4] = {p1.x, p1.y, p1.z, p1.w};
+                const int q2[4] = {p2.x, p2.y, p2.z, p2.w};
+#pragma unroll
+                for (int r2 = 0; r2 < 4; ++r2) {
+                    const float f = (float)(q0[r2] + q1[r2] * 256) + 65536.0f * (float)q2[r2];
+                    acc[t][r2] = fmaf(f, sc[t][i] * m[r2], acc[t][r2]);
+                }
+            }
+        }
+    }
+    if (a.ss)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < TW; ++t) acc[t][r] = __fmul_rn(acc[t][r], inv[r]);
+    split_epilogue<TW>(a, acc, tile, row0, col, blk);
 }
 
 // out = residual + the slice sum (pairs: silu(sum of row 2j) * sum of row
@@ -766,13 +909,23 @@ void launch_split_bpg(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, 
 void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint32_t tiles, int format) {
     const uint32_t row_tiles = (a.n + kRowTile - 1) / kRowTile;
     const dim3 grid((row_tiles + 4u * plan.tw - 1) / (4u * plan.tw), plan.slices, tiles);
-    if (format == QWH_FORMAT_Q8) launch_split_bpg<64>(s, plan, a, grid);
-    else launch_split_bpg<32>(s, plan, a, grid);
+    if (format == QWH_FORMAT_Q5) {
+        // (Chunks of 4 groups: a slice is a whole number of them.)
+        if (plan.tw == 2) gemv_split_q5_kernel<2><<<grid, 256, 0, s>>>(a);
+        else gemv_split_q5_kernel<1><<<grid, 256, 0, s>>>(a);
+    } else if (format == QWH_FORMAT_Q8) {
+        launch_split_bpg<64>(s, plan, a, grid);
+    } else {
+        launch_split_bpg<32>(s, plan, a, grid);
+    }
 }
 
-// Formats with a matrix-core form: q4 and q8 (the codes are whole bytes or
-// nibbles; q5's 40-byte groups are not 16-byte pieces).
-bool batch_format(int format) { return format == QWH_FORMAT_Q4 || format == QWH_FORMAT_Q8; }
+// Formats with a matrix-core form: q4, q8, and q5 in the split form only
+// (its 40-byte groups are not 16-byte pieces for the unsplit kernel's LDS
+// transpose).
+bool batch_format(int format) {
+    return format == QWH_FORMAT_Q4 || format == QWH_FORMAT_Q8 || format == QWH_FORMAT_Q5;
+}
 
 SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const SplitPlan &plan,
                      const BatchNorm &norm) {
@@ -795,7 +948,9 @@ SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const
 
 }  // namespace
 
-bool gemv_batch_supported(const Matrix &w) { return batch_format(w.format) && w.cols % 64 == 0; }
+bool gemv_batch_supported(const Matrix &w) {
+    return batch_format(w.format) && w.cols % 64 == 0 && (w.format != QWH_FORMAT_Q5 || split_plan(w).tw);
+}
 
 uint32_t batch_slices(const Matrix &w) {
     if (!batch_format(w.format)) return 0;
@@ -826,6 +981,7 @@ hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w,
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     const SplitPlan plan = split_plan(w);
+    if (w.format == QWH_FORMAT_Q5 && !(plan.tw && (plan.slices == 1 || partials))) return hipErrorInvalidValue;
     if (plan.tw && (plan.slices == 1 || partials)) {
         SplitArgs a = split_args(digits, w, tokens, plan, norm);
         a.out = out;

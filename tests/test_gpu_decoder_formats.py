@@ -55,7 +55,7 @@ def oracle_greedy(ref, b, token, steps):
     (o.Q8, "q8", 3, ODD, ()),       # unsplit matrix-core form (K not a multiple of 256) and the generic GEMV
     (o.Q8, "q8", 3, TINY, ("QWH_DECODER_NO_SPLIT",)),
     (o.Q5, "q8", 1, TINY, ()),      # q5 byte-plane GEMV
-    (o.Q5, "q8", 3, TINY, ()),      # q5 at batch > 1 runs the per-token byte-plane GEMV
+    (o.Q5, "q8", 3, TINY, ()),      # q5 on the matrix-core batch GEMV (split form)
     (o.Q5, "q8", 2, ODD, ()),
     (o.Q4, "f32", 1, TINY, ()),     # f32 cache
     (o.Q4, "f32", 3, TINY, ()),

@@ -171,6 +171,23 @@ def test_q5_gemv_shapes(ctx, rows, cols, tokens):
     check(ctx, o.Q5, w, x, tokens, f"q5 {rows}x{cols} tokens {tokens}")
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [
+    (256, 2048, 16),     # one 16-token tile, K split into slices (partial sums + reduce)
+    (100, 1024, 17),     # two token tiles, a partial row tile
+    (8240, 1024, 3),     # two row tiles per wavefront
+    (2048, 6144, 40),    # three token tiles, the widest row
+])
+def test_q5_multi_token_on_matrix_cores(ctx, rows, cols, tokens):
+    # Several tokens over q5 codes (K a multiple of 256): u - 16 expanded to
+    # signed bytes with the fifth bits, one v_mfma_i32_16x16x64_i8 per
+    # activation digit plane, W streamed once per 16 tokens.
+    w = o.normal(rows * cols, 13, rows, 0.02).reshape(rows, cols)
+    w[rows // 2, :64] = np.float32(-1.0)   # codes at the bottom of the range
+    w[rows // 2, 64:128] = np.float32(1.0)
+    x = o.normal(tokens * cols, 13, 2000 + cols)
+    check(ctx, o.Q5, w, x, tokens, f"q5 {rows}x{cols} tokens {tokens}")
+
+
 def test_q5_gemv_awkward_values(ctx):
     # Codes at both ends (-16 and 15 in one group), a zero row, a zero group
     # of activations, a huge dynamic range inside one chunk.
