@@ -156,8 +156,8 @@ struct BatchNorm {
     bool rms = false;
     float eps = 0.0f;
 };
-// K slices the GEMV splits this shape into (0: no split form, K not a
-// multiple of 256), and the bytes of partial sums that takes.
+// K slices the GEMV splits this shape into (0: no split form, an odd
+// number of 64-value groups), and the bytes of partial sums that takes.
 uint32_t batch_slices(const Matrix &w);
 size_t batch_partial_bytes(uint32_t tokens, const Matrix &w);
 bool gemv_batch_supported(const Matrix &w);

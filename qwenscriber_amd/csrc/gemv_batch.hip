@@ -329,8 +329,8 @@ struct SplitShape {
     static constexpr int RPI = 64 / PPR;            // rows per load instruction
     static constexpr int NW = (ROWS + RPI - 1) / RPI;
     static constexpr int DPIECES = KC * 3 * 64;     // 16-byte digit pieces per chunk
-    static constexpr int DPT = DPIECES / 256;       // ... per thread
-    static_assert(DPIECES % 256 == 0 && (PPR & (PPR - 1)) == 0 && ROWS % RPI == 0, "chunk shape");
+    static constexpr int DPT = (DPIECES + 255) / 256;  // ... per thread (the last round partly idle)
+    static_assert(DPIECES % 128 == 0 && (PPR & (PPR - 1)) == 0 && ROWS % RPI == 0, "chunk shape");
 };
 
 // The end of a split GEMV workgroup: lane l holds tokens 4 (l / 16) + r of
@@ -410,8 +410,10 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
 #pragma unroll
         for (int m = 0; m < DPT; ++m) {
             // Piece q = (group, plane, lane L) of lane order; lane L reads
-            // column block L / 16 of token L % 16.
-            const int q = tid + 256 * m;
+            // column block L / 16 of token L % 16. (Threads past the
+            // chunk's pieces load the last one again and do not store it:
+            // the load stays unconditional.)
+            const int q = tid + 256 * m < S::DPIECES ? tid + 256 * m : S::DPIECES - 1;
             const int L = q & 63;
             rd[m] = *reinterpret_cast<const v4i *>(dig + ((size_t)g0 * 3 + (q >> 6)) * kPlaneBytes +
                                                      (L & 15) * 64 + (L >> 4) * 16);
@@ -437,7 +439,8 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
         const int buf = c & 1;
         if (c == 0 && has_ss) ssl[tid] = ssv;
 #pragma unroll
-        for (int m = 0; m < DPT; ++m) dl[buf][tid + 256 * m] = rd[m];
+        for (int m = 0; m < DPT; ++m)
+            if (tid + 256 * m < S::DPIECES) dl[buf][tid + 256 * m] = rd[m];
         if (tid < KC * 4) ml[buf][tid] = rm;
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
@@ -863,7 +866,7 @@ hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens
 namespace {
 
 // Split-form plan: TW tiles per wavefront, chunks of KC groups, K slices.
-// tw == 0: no split form for this shape (K not a multiple of 4 groups).
+// tw == 0: no split form for this shape (an odd number of groups).
 struct SplitPlan {
     int tw = 0, kc = 4;
     uint32_t slices = 1, slice_groups = 0;
@@ -874,23 +877,29 @@ int env_int(const char *name, int fallback) {
     return v ? atoi(v) : fallback;
 }
 
-SplitPlan split_plan(const Matrix &w) {
+// `tiles`: the 16-token tiles of the call, which multiply the workgroups as
+// the K slices do (the decoder's slice counts are planned for one tile).
+SplitPlan split_plan(const Matrix &w, uint32_t tiles = 1) {
     // Tuning overrides, read once.
     static const int env_tw = env_int("QWH_SPLIT_TW", 0), env_kc = env_int("QWH_SPLIT_KC", 0),
                      env_s = env_int("QWH_SPLIT_S", 0), env_off = env_int("QWH_SPLIT_OFF", 0);
     SplitPlan p;
     const uint32_t gpr = w.cols / 64;
-    if (gpr % 4u || env_off) return p;
+    if (gpr % 2u || env_off) return p;
+    // Chunks of 4 groups, or of 2 where the group count is not a multiple of
+    // 4 (the audio tower's 896-wide rows: 14 groups).
+    p.kc = gpr % 4u ? 2 : 4;
     const uint32_t row_tiles = (w.rows + kRowTile - 1) / kRowTile;
     // Two tiles per wavefront once that still leaves 64 workgroups, else one.
     p.tw = row_tiles >= 4u * 2u * 64u ? 2 : 1;
     if (env_tw == 1 || env_tw == 2) p.tw = env_tw;
     if ((env_kc == 4 || env_kc == 8) && gpr % (uint32_t)env_kc == 0) p.kc = env_kc;
     const uint32_t chunks = gpr / (uint32_t)p.kc;
-    const uint32_t blocks = (row_tiles + 4u * p.tw - 1) / (4u * p.tw);
-    // K slices: about 512 workgroups in all, a divisor of the chunk count,
-    // at most kMaxSlices.
-    uint32_t want = env_s > 0 ? (uint32_t)env_s : (512u + blocks - 1) / blocks;
+    const uint32_t blocks = (row_tiles + 4u * p.tw - 1) / (4u * p.tw) * (tiles ? tiles : 1);
+    // K slices: about 512 workgroups in all and at most about 4 chunks in
+    // a row per workgroup (its chunks are one memory round trip each), a
+    // divisor of the chunk count, at most kMaxSlices.
+    uint32_t want = env_s > 0 ? (uint32_t)env_s : std::max((512u + blocks - 1) / blocks, (chunks + 3) / 4);
     p.slices = 1;
     for (uint32_t c = 1; c <= chunks && c <= want && c <= kMaxSlices; ++c)
         if (chunks % c == 0) p.slices = c;
@@ -900,10 +909,18 @@ SplitPlan split_plan(const Matrix &w) {
 
 template <int BPG>
 void launch_split_bpg(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, dim3 grid) {
-    if (plan.tw == 2 && plan.kc == 4) gemv_split_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(a);
-    else if (plan.tw == 2) gemv_split_kernel<2, 8, BPG><<<grid, 256, 0, s>>>(a);
-    else if (plan.kc == 4) gemv_split_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(a);
-    else gemv_split_kernel<1, 8, BPG><<<grid, 256, 0, s>>>(a);
+    if (plan.kc == 2) {
+        if (plan.tw == 2) gemv_split_kernel<2, 2, BPG><<<grid, 256, 0, s>>>(a);
+        else gemv_split_kernel<1, 2, BPG><<<grid, 256, 0, s>>>(a);
+    } else if (plan.tw == 2 && plan.kc == 4) {
+        gemv_split_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(a);
+    } else if (plan.tw == 2) {
+        gemv_split_kernel<2, 8, BPG><<<grid, 256, 0, s>>>(a);
+    } else if (plan.kc == 4) {
+        gemv_split_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(a);
+    } else {
+        gemv_split_kernel<1, 8, BPG><<<grid, 256, 0, s>>>(a);
+    }
 }
 
 void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint32_t tiles, int format) {
@@ -949,7 +966,10 @@ SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const
 }  // namespace
 
 bool gemv_batch_supported(const Matrix &w) {
-    return batch_format(w.format) && w.cols % 64 == 0 && (w.format != QWH_FORMAT_Q5 || split_plan(w).tw);
+    if (!batch_format(w.format) || w.cols % 64) return false;
+    if (w.format != QWH_FORMAT_Q5) return true;
+    const SplitPlan p = split_plan(w);
+    return p.tw && p.kc == 4;  // (the q5 kernel's chunks are 4 groups)
 }
 
 uint32_t batch_slices(const Matrix &w) {
@@ -966,7 +986,7 @@ hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matr
                                    float *partials, const BatchNorm &norm) {
     if (!batch_format(w.format)) return hipErrorNotSupported;
     const SplitPlan plan = split_plan(w);
-    if (!plan.tw || !partials) return hipErrorInvalidValue;
+    if (!plan.tw || !partials || (w.format == QWH_FORMAT_Q5 && plan.kc != 4)) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     SplitArgs a = split_args(digits, w, tokens, plan, norm);
     a.part = partials;
@@ -980,8 +1000,9 @@ hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w,
     if (pairs && (w.rows & 1u)) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
-    const SplitPlan plan = split_plan(w);
-    if (w.format == QWH_FORMAT_Q5 && !(plan.tw && (plan.slices == 1 || partials))) return hipErrorInvalidValue;
+    const SplitPlan plan = split_plan(w, tiles);
+    if (w.format == QWH_FORMAT_Q5 && !(plan.tw && plan.kc == 4 && (plan.slices == 1 || partials)))
+        return hipErrorInvalidValue;
     if (plan.tw && (plan.slices == 1 || partials)) {
         SplitArgs a = split_args(digits, w, tokens, plan, norm);
         a.out = out;
@@ -996,7 +1017,7 @@ hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w,
         }
         return hipGetLastError();
     }
-    // K not a multiple of 256: the unsplit form, one tile per workgroup.
+    // An odd number of groups: the unsplit form, one tile per workgroup.
     BatchArgs a{};
     a.digits = static_cast<const uint8_t *>(digits);
     a.mult = mult_of(const_cast<void *>(digits), tokens, w.cols);

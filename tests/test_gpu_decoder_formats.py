@@ -52,7 +52,7 @@ def oracle_greedy(ref, b, token, steps):
     (o.Q8, "q8", 1, TINY, ()),      # byte-plane GEMV, fused RMSNorm prologue, pairs epilogue
     (o.Q8, "q8", 3, TINY, ()),      # q8 on the matrix-core batch GEMV (split form)
     (o.Q8, "q8", 18, TINY, ()),     # two token tiles
-    (o.Q8, "q8", 3, ODD, ()),       # unsplit matrix-core form (K not a multiple of 256) and the generic GEMV
+    (o.Q8, "q8", 3, ODD, ()),       # unsplit matrix-core form (an odd number of groups) and the generic GEMV
     (o.Q8, "q8", 3, TINY, ("QWH_DECODER_NO_SPLIT",)),
     (o.Q5, "q8", 1, TINY, ()),      # q5 byte-plane GEMV
     (o.Q5, "q8", 3, TINY, ()),      # q5 on the matrix-core batch GEMV (split form)

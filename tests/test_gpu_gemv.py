@@ -115,8 +115,11 @@ def test_q4_gemv_edge_shapes(ctx, rows, cols, tokens):
     (64, 256, 2),
     (40, 10240, 3),     # K past 8192: activation prep stretch by stretch, two units per wave
     (65600, 256, 2),    # over 4096 row tiles: four tiles per workgroup
-    (65600, 128, 3),    # four tiles, two groups per unit
+    (65600, 128, 3),    # two groups: chunks of 2 groups, two row tiles per wavefront
     (300, 1024, 40),    # K split into 4 slices over three token tiles, partial row block
+    (896, 896, 390),    # the 0.6B audio tower's projection: 14 groups in chunks of 2, 25 token tiles
+    (3584, 896, 40),    # its ffn_in
+    (100, 384, 17),     # six groups in chunks of 2, split into slices
 ])
 def test_q4_batch_gemv(ctx, rows, cols, tokens):
     # Two or more tokens run on the matrix-core kernel.
@@ -307,6 +310,8 @@ def test_linear_rejects_shape_mismatch(ctx):
     (1001, 1024, 2),      # rows not a multiple of the tile
     (130, 320, 5),        # five groups: the unsplit matrix-core form
     (64, 448, 17),        # seven groups, two token tiles
+    (896, 896, 390),      # fourteen groups in chunks of 2
+    (300, 384, 5),        # six groups in chunks of 2
 ])
 def test_q8_multi_token_on_matrix_cores(ctx, rows, cols, tokens):
     # kernels.zig:118-158 with tokens > 1 over q8 weights (the audio tower's
