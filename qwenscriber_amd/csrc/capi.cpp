@@ -207,6 +207,7 @@ int32_t qwh_destroy(qwh_ctx *ctx) {
     if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
     if (ctx->audio.ptr) (void)hipFree(ctx->audio.ptr);
     if (ctx->front.ptr) (void)hipFree(ctx->front.ptr);
+    if (ctx->front_table.ptr) (void)hipFree(ctx->front_table.ptr);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QWH_OK;
@@ -1012,26 +1013,33 @@ int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *w, co
     auto align = [](size_t n) { return (n + 63) & ~(size_t)63; };  // floats: 256-byte aligned pieces
     const size_t off1 = align(group * mel_plane), off2 = off1 + align(group * p1), off3 = off2 + align(group * p2);
     const size_t off_flat = off3 + align(group * p3);
-    const size_t off_table = off_flat + align((size_t)group * chunk_steps * features);
-    const size_t total = off_table + align((size_t)chunk_steps * d_model);
+    const size_t total = off_flat + align((size_t)group * chunk_steps * features);
     QWH_TRY(ensure_workspace(ctx, ctx->front, total * sizeof(float)));
     float *ws = static_cast<float *>(ctx->front.ptr);
-    // addSinusoidalPosition (model.zig:751-763) for the steps of a chunk, in
-    // f64 on the host, narrowed to f32 as the reference does.
-    std::vector<float> table((size_t)chunk_steps * d_model, 0.0f);
-    const uint32_t half = d_model / 2;
-    const double increment = std::log(10000.0) / ((double)half - 1.0);
-    for (uint32_t step = 0; step < chunk_steps; ++step)
-        for (uint32_t i = 0; i < half; ++i) {
-            const double angle = (double)step * std::exp(-increment * (double)i);
-            table[(size_t)step * d_model + i] = (float)std::sin(angle);
-            table[(size_t)step * d_model + half + i] = (float)std::cos(angle);
-        }
     hipStream_t s = ctx->stream;
-    QWH_TRY(check_hip(ctx, hipMemcpyAsync(ws + off_table, table.data(), table.size() * 4, hipMemcpyHostToDevice, s),
-                      "position table"));
-    // The table copy reads host memory owned by this call.
-    QWH_TRY(check_hip(ctx, hipStreamSynchronize(s), "position table"));
+    if (!ctx->front_table.ptr || ctx->front_table_steps != chunk_steps || ctx->front_table_width != d_model) {
+        // addSinusoidalPosition (model.zig:751-763) for the steps of a chunk,
+        // in f64 on the host, narrowed to f32 as the reference does; built
+        // once per shape and kept on the device.
+        std::vector<float> table((size_t)chunk_steps * d_model, 0.0f);
+        const uint32_t half = d_model / 2;
+        const double increment = std::log(10000.0) / ((double)half - 1.0);
+        for (uint32_t step = 0; step < chunk_steps; ++step)
+            for (uint32_t i = 0; i < half; ++i) {
+                const double angle = (double)step * std::exp(-increment * (double)i);
+                table[(size_t)step * d_model + i] = (float)std::sin(angle);
+                table[(size_t)step * d_model + half + i] = (float)std::cos(angle);
+            }
+        ctx->front_table_steps = 0;
+        QWH_TRY(ensure_workspace(ctx, ctx->front_table, table.size() * sizeof(float)));
+        QWH_TRY(check_hip(ctx, hipMemcpyAsync(ctx->front_table.ptr, table.data(), table.size() * 4,
+                                              hipMemcpyHostToDevice, s), "position table"));
+        // The copy reads host memory owned by this call.
+        QWH_TRY(check_hip(ctx, hipStreamSynchronize(s), "position table"));
+        ctx->front_table_steps = chunk_steps;
+        ctx->front_table_width = d_model;
+    }
+    const float *pos_table = static_cast<const float *>(ctx->front_table.ptr);
     for (uint32_t c0 = 0; c0 < chunks; c0 += group) {
         const uint32_t count = chunks - c0 < group ? chunks - c0 : group;
         const uint32_t row0 = c0 * chunk_steps;  // every chunk before the last is whole
@@ -1048,7 +1056,7 @@ int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *w, co
                           "front-end flatten"));
         float *out = encoder_dev + (size_t)row0 * d_model;
         QWH_TRY(qwh_linear(ctx, w->conv_out, ws + off_flat, features, rows, out));
-        QWH_TRY(check_hip(ctx, launch_add_positions(s, out, ws + off_table, row0, rows, d_model, chunk_steps),
+        QWH_TRY(check_hip(ctx, launch_add_positions(s, out, pos_table, row0, rows, d_model, chunk_steps),
                           "front-end positions"));
     }
     *steps_out = (uint32_t)steps;

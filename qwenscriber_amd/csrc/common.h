@@ -73,7 +73,12 @@ struct qwh_ctx {
     qwh::Workspace digits;  // x digit planes for the q4 GEMV
     qwh::Workspace scratch; // attention partials and other per-call scratch
     qwh::Workspace audio;   // audio tower layer / projector activations
-    qwh::Workspace front;   // audio front end: chunk planes, flattened steps, position table
+    qwh::Workspace front;   // audio front end: chunk planes, flattened steps
+    // The audio front end's sinusoidal position table for chunks of
+    // front_table_steps steps of front_table_width values (built once per
+    // shape on the host, model.zig:751-763).
+    qwh::Workspace front_table;
+    uint32_t front_table_steps = 0, front_table_width = 0;
 };
 
 namespace qwh {
