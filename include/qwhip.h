@@ -271,6 +271,13 @@ int32_t qwh_kv_append_q8(qwh_ctx *ctx, const float *key_dev, const float *value_
                          uint32_t kv_width, uint32_t position, uint8_t *k_scales_dev,
                          uint8_t *k_codes_dev, uint8_t *v_scales_dev, uint8_t *v_codes_dev);
 
+/* decoder.zig:290-301 argmaxLogits for `rows` rows of `count` logits
+ * (rows back to back): ids_dev[r] = the index of the row's largest value, the
+ * lowest such index among equal maxima; a row whose first value is NaN, or
+ * with no value above -FLT_MAX, gives 0 (the reference's scan keeps index 0
+ * unless a later value compares greater). The decoder step's argmax. */
+int32_t qwh_argmax_rows(qwh_ctx *ctx, const float *logits_dev, uint32_t rows, uint32_t count, uint32_t *ids_dev);
+
 /* ---------------------------------------------------------------------- */
 /* Audio tower and projector (model.zig:646-735)                           */
 /* ---------------------------------------------------------------------- */

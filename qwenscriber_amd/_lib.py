@@ -148,6 +148,7 @@ SIGNATURES = {
     "qwh_synth_normal": (_I32, [_P, _U32, _U32, _U64, _F, _P]),
     "qwh_decode_attention_q8": (_I32, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U64, _U64]),
     "qwh_kv_append_q8": (_I32, [_P, _P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "qwh_argmax_rows": (_I32, [_P, _P, _U32, _U32, _P]),
     "qwh_layer_norm": (_I32, [_P, _P, _P, _P, _P, _U32, _U32, _F]),
     "qwh_add_bias": (_I32, [_P, _P, _P, _U32, _U32]),
     "qwh_gelu": (_I32, [_P, _P, _U64]),
@@ -498,6 +499,10 @@ class Context:
     def kv_append_q8(self, key_dev, value_dev, kv_width, position, k_scales, k_codes, v_scales, v_codes) -> None:
         self._check(self.lib.qwh_kv_append_q8(self.handle, key_dev, value_dev, kv_width, position, k_scales,
                                               k_codes, v_scales, v_codes))
+
+    def argmax_rows(self, logits_dev: int, rows: int, count: int, ids_dev: int) -> None:
+        """decoder.zig:290-301 argmaxLogits of each of `rows` rows (qwh_argmax_rows)."""
+        self._check(self.lib.qwh_argmax_rows(self.handle, logits_dev, rows, count, ids_dev))
 
 
 class Decoder:

@@ -1063,6 +1063,18 @@ int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *w, co
     return QWH_OK;
 }
 
+int32_t qwh_argmax_rows(qwh_ctx *ctx, const float *logits_dev, uint32_t rows, uint32_t count, uint32_t *ids_dev) {
+    if (!ctx) return QWH_E_INVALID_ARGUMENT;
+    if (rows == 0) return QWH_OK;
+    if (count == 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "argmax over an empty row");
+    if (rows > 65535) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "rows %u > 65535", rows);
+    QWH_TRY(check_device_ptr(ctx, logits_dev, "logits"));
+    QWH_TRY(check_device_ptr(ctx, ids_dev, "ids"));
+    QWH_TRY(ensure_workspace(ctx, ctx->scratch, argmax_scratch_bytes(rows, count)));
+    return check_hip(ctx, launch_argmax_rows(ctx->stream, logits_dev, rows, count, ctx->scratch.ptr, ids_dev),
+                     "argmax");
+}
+
 int32_t qwh_audio_projector(qwh_ctx *ctx, uint64_t in_matrix, const float *in_bias_dev, uint64_t out_matrix,
                             const float *out_bias_dev, const float *encoder_dev, uint32_t steps, float *out_dev) {
     if (!ctx) return QWH_E_INVALID_ARGUMENT;

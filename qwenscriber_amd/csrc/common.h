@@ -211,6 +211,11 @@ struct AttentionArgs {
     void *digits = nullptr;
 };
 bool attention_supported(uint32_t head_dim, uint32_t ratio);
+// argmaxLogits (decoder.zig:290-301) of `rows` rows of `count` logits into
+// ids (the decoder step's kernels); scratch holds argmax_scratch_bytes.
+size_t argmax_scratch_bytes(uint32_t rows, uint32_t count);
+hipError_t launch_argmax_rows(hipStream_t s, const float *logits, uint32_t rows, uint32_t count, void *scratch,
+                              uint32_t *ids);
 // Scratch bytes for the range records of either form of the attention.
 size_t attention_scratch_bytes(int cus, const AttentionArgs &a);
 // Fails with hipErrorInvalidValue, launching nothing, when scratch_bytes

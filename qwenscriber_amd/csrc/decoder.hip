@@ -166,7 +166,10 @@ __global__ __launch_bounds__(256) void rmsnorm_digits_kernel(const float *x, con
 }
 
 // argmaxLogits (decoder.zig:290-301): the largest value, the lowest index
-// among equal maxima. Stage 1: one partial per block.
+// among equal maxima. Stage 1: one partial per block of kArgmaxPerBlock
+// logits.
+constexpr uint32_t kArgmaxPerBlock = 4096;
+
 __device__ __forceinline__ void better(float &v, uint32_t &i, float v2, uint32_t i2) {
     if (v2 > v || (v2 == v && i2 < i)) {
         v = v2;
@@ -200,9 +203,30 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        pv[(size_t)b * gridDim.x + blockIdx.x] = sv[0];
-        pi[(size_t)b * gridDim.x + blockIdx.x] = si[0];
+        // A NaN first logit stays the reference's best (no value compares
+        // greater than it): index 0 then wins outright.
+        const bool nan_first = blockIdx.x == 0 && row[0] != row[0];
+        pv[(size_t)b * gridDim.x + blockIdx.x] = nan_first ? INFINITY : sv[0];
+        pi[(size_t)b * gridDim.x + blockIdx.x] = nan_first ? 0u : si[0];
     }
+}
+
+// argmaxLogits of each row from the partials: ids[b].
+__global__ __launch_bounds__(64) void argmax_rows_finish_kernel(const float *pv, const uint32_t *pi, uint32_t parts,
+                                                                uint32_t *ids) {
+    const uint32_t b = blockIdx.x;
+    float bv = -FLT_MAX;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t p = threadIdx.x; p < parts; p += 64) better(bv, bi, pv[(size_t)b * parts + p], pi[(size_t)b * parts + p]);
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const float v2 = __shfl_xor(bv, mask, 64);
+        const uint32_t i2 = __shfl_xor(bi, mask, 64);
+        better(bv, bi, v2, i2);
+    }
+    // A row with no value above -FLT_MAX (all -inf or NaN) is the
+    // reference's index 0.
+    if (threadIdx.x == 0) ids[b] = bi == 0xffffffffu ? 0u : bi;
 }
 
 // Greedy generation with stop rules (wasm/model.zig:423-451 decodeStep,
@@ -685,6 +709,22 @@ int32_t check_matrix(qwh_decoder *d, const Matrix *m, uint32_t rows, uint32_t co
 }
 
 }  // namespace
+size_t argmax_scratch_bytes(uint32_t rows, uint32_t count) {
+    const uint32_t parts = (count + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
+    return (size_t)rows * parts * (sizeof(float) + sizeof(uint32_t));
+}
+
+hipError_t launch_argmax_rows(hipStream_t s, const float *logits, uint32_t rows, uint32_t count, void *scratch,
+                              uint32_t *ids) {
+    if (!rows || !count) return hipErrorInvalidValue;
+    const uint32_t parts = (count + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
+    float *pv = static_cast<float *>(scratch);
+    uint32_t *pi = reinterpret_cast<uint32_t *>(pv + (size_t)rows * parts);
+    argmax_partial_kernel<<<dim3(parts, rows), 256, 0, s>>>(logits, count, kArgmaxPerBlock, pv, pi);
+    argmax_rows_finish_kernel<<<rows, 64, 0, s>>>(pv, pi, parts, ids);
+    return hipGetLastError();
+}
+
 }  // namespace qwh
 
 using namespace qwh;
@@ -813,7 +853,7 @@ int32_t qwh_decoder_create_cache(qwh_ctx *ctx, const qwh_decoder_config *config,
     aa.f32_cache = cache_format == QWH_CACHE_F32;
     d->attn_scratch_bytes = attention_scratch_bytes(ctx->cus, aa);
     if (st == QWH_OK) st = dalloc(d, d->attn_scratch_bytes, &d->attn_scratch);
-    d->arg_per_block = 4096;
+    d->arg_per_block = kArgmaxPerBlock;
     d->arg_parts = (c.vocab + d->arg_per_block - 1) / d->arg_per_block;
     if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_v));
     if (st == QWH_OK) st = dalloc(d, 4 * (size_t)batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_i));
