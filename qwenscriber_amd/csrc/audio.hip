@@ -24,16 +24,6 @@ namespace {
 
 constexpr int kNormThreads = 256;
 
-// Sum over a 256-thread workgroup; every thread gets the total.
-__device__ __forceinline__ float block_sum_256(float v, float *lds) {
-    v = dev::wave_sum(v);
-    const int wave = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) lds[wave] = v;
-    __syncthreads();
-    return (lds[0] + lds[1]) + (lds[2] + lds[3]);
-}
-
 // LayerNorm of one row per workgroup: mean, centred variance,
 // 1 / sqrt(variance + eps), then (x - mean) * inverse_std * weight + bias.
 // `out` may alias `x` (each thread rewrites only the elements it read last).
@@ -42,16 +32,8 @@ __global__ __launch_bounds__(kNormThreads) void layer_norm_kernel(const float *x
     __shared__ float lds[4];
     const float *row = x + (size_t)blockIdx.x * width;
     float *dst = out + (size_t)blockIdx.x * width;
-    float sum = 0.0f;
-    for (uint32_t i = threadIdx.x; i < width; i += kNormThreads) sum += row[i];
-    const float mean = block_sum_256(sum, lds) / (float)width;
-    float squares = 0.0f;
-    for (uint32_t i = threadIdx.x; i < width; i += kNormThreads) {
-        const float centered = row[i] - mean;
-        squares += centered * centered;
-    }
-    const float variance = block_sum_256(squares, lds) / (float)width;
-    const float inverse_std = 1.0f / sqrtf(variance + eps);
+    float mean, inverse_std;
+    dev::layer_norm_stats(row, width, eps, lds, mean, inverse_std);
     for (uint32_t i = threadIdx.x; i < width; i += kNormThreads)
         dst[i] = (row[i] - mean) * inverse_std * weight[i] + bias[i];
 }

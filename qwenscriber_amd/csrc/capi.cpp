@@ -834,14 +834,19 @@ namespace {
 // more tokens the digit planes are prepared once and each matrix reads them
 // (qwh_linear would prepare them per matrix); q5 goes through qwh_linear one
 // by one.
-int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handles, const float *x, uint32_t cols,
-                            uint32_t tokens, std::initializer_list<float *> outs) {
-    bool shared = tokens >= 2 && ((uintptr_t)x & 15u) == 0;
+// True when every matrix takes `cols`-wide rows and has a batch GEMV form.
+bool batch_ready(qwh_ctx *ctx, std::initializer_list<uint64_t> handles, uint32_t cols) {
     for (uint64_t h : handles) {
         const Matrix *m = find_matrix(ctx, h);
-        shared = shared && m && gemv_batch_supported(*m) && ((uintptr_t)m->data & 15u) == 0 && m->cols == cols &&
-                 m->rows > 0;
+        if (!m || !gemv_batch_supported(*m) || ((uintptr_t)m->data & 15u) != 0 || m->cols != cols || m->rows == 0)
+            return false;
     }
+    return true;
+}
+
+int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handles, const float *x, uint32_t cols,
+                            uint32_t tokens, std::initializer_list<float *> outs) {
+    const bool shared = tokens >= 2 && ((uintptr_t)x & 15u) == 0 && batch_ready(ctx, handles, cols);
     auto out = outs.begin();
     if (!shared) {
         for (uint64_t h : handles) QWH_TRY(qwh_linear(ctx, h, x, cols, tokens, *out++));
@@ -860,6 +865,54 @@ int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handle
                                                     nullptr, false, static_cast<float *>(ctx->scratch.ptr)),
                           "gemv batch"));
     return QWH_OK;
+}
+
+// qwh_audio_layer when every linear has a batch GEMV form: the two
+// LayerNorms write the GEMVs' activation digits directly, q / k / v read one
+// set of digits, the GELU of ffn_in + bias is applied as ffn_out's digits are
+// prepared, and o and ffn_out add their bias and the residual stream in their
+// own epilogue (out = encoder + (W x + bias), the order of the reference's
+// addBias then addInPlace). Nine launches instead of fourteen, and no f32
+// pass over the normed rows or the projections' outputs.
+int32_t audio_layer_batch(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *encoder_dev, uint32_t steps,
+                          uint32_t d_model, uint32_t ffn_dim, float eps, const AudioAttentionArgs &a, float *wide) {
+    hipStream_t s = ctx->stream;
+    size_t parts = 0;
+    for (uint64_t h : {w->q, w->k, w->v, w->o, w->ffn_in, w->ffn_out})
+        parts = std::max(parts, batch_partial_bytes(steps, *find_matrix(ctx, h)));
+    QWH_TRY(ensure_workspace(ctx, ctx->digits,
+                             std::max(batch_digit_bytes(steps, d_model), batch_digit_bytes(steps, ffn_dim))));
+    if (parts) QWH_TRY(ensure_workspace(ctx, ctx->scratch, parts));
+    void *digits = ctx->digits.ptr;
+    float *partials = static_cast<float *>(ctx->scratch.ptr);
+    auto gemv = [&](uint64_t h, float *out, const float *residual, const float *bias, const char *what) {
+        return check_hip(ctx, launch_gemv_batch(s, digits, *find_matrix(ctx, h), steps, out, residual, false, partials,
+                                                BatchNorm{}, bias),
+                         what);
+    };
+    // model.zig:657-665 layerNormInto, :765-786 projectQkv (biases join in the attention's loads).
+    QWH_TRY(check_hip(ctx, launch_layer_norm_digits(s, encoder_dev, w->attention_norm_weight, w->attention_norm_bias,
+                                                    d_model, steps, eps, digits),
+                      "audio attention norm"));
+    QWH_TRY(gemv(w->q, const_cast<float *>(a.q), nullptr, nullptr, "audio q"));
+    QWH_TRY(gemv(w->k, const_cast<float *>(a.k), nullptr, nullptr, "audio k"));
+    QWH_TRY(gemv(w->v, const_cast<float *>(a.v), nullptr, nullptr, "audio v"));
+    QWH_TRY(check_hip(ctx, launch_audio_attention(s, a), "audio attention"));
+    // :824-848 projectAttentionOutput + o bias, :669 addInPlace.
+    GemvInput in;
+    in.mode = GemvInput::F32;
+    in.x = a.out;
+    QWH_TRY(check_hip(ctx, launch_prep_batch(s, in, steps, d_model, digits), "audio o prep"));
+    QWH_TRY(gemv(w->o, encoder_dev, encoder_dev, w->o_bias, "audio o"));
+    // :671-679 layerNormInto, :852-872 activateFfn, :692 addInPlace.
+    QWH_TRY(check_hip(ctx, launch_layer_norm_digits(s, encoder_dev, w->final_norm_weight, w->final_norm_bias, d_model,
+                                                    steps, eps, digits),
+                      "audio final norm"));
+    QWH_TRY(gemv(w->ffn_in, wide, nullptr, nullptr, "audio ffn_in"));
+    in.x = wide;
+    in.gelu_bias = w->ffn_in_bias;
+    QWH_TRY(check_hip(ctx, launch_prep_batch(s, in, steps, ffn_dim, digits), "audio ffn prep"));
+    return gemv(w->ffn_out, encoder_dev, encoder_dev, w->ffn_out_bias, "audio ffn_out");
 }
 
 }  // namespace
@@ -906,6 +959,10 @@ int32_t qwh_audio_layer(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *e
     a.heads = heads, a.head_dim = d_model / heads;
     a.scaling = 1.0f / sqrtf((float)a.head_dim);
     QWH_TRY(check_audio_attention(ctx, a));
+
+    if (steps >= 2 && d_model % 64 == 0 && batch_ready(ctx, {w->q, w->k, w->v, w->o, w->ffn_in}, d_model) &&
+        batch_ready(ctx, {w->ffn_out}, ffn_dim))
+        return audio_layer_batch(ctx, w, encoder_dev, steps, d_model, ffn_dim, eps, a, wide);
 
     // model.zig:657-665 layerNormInto, :765-786 projectQkv (biases join in the attention's loads).
     QWH_TRY(check_hip(ctx, launch_layer_norm(s, encoder_dev, normed, w->attention_norm_weight, w->attention_norm_bias,

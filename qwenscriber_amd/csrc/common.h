@@ -170,7 +170,12 @@ bool gemv_batch_supported(const Matrix &w);
 // required and a reduce kernel adds them.
 hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
                              float *out, const float *residual, bool pairs = false, float *partials = nullptr,
-                             const BatchNorm &norm = BatchNorm{});
+                             const BatchNorm &norm = BatchNorm{}, const float *bias = nullptr);
+// math.zig:99-116 layerNorm of `tokens` rows of `width` values (width a
+// multiple of 64; the statistics of launch_layer_norm) written straight as
+// the batch GEMV's activation digits (batch_digit_bytes(tokens, width)).
+hipError_t launch_layer_norm_digits(hipStream_t s, const float *x, const float *weight, const float *bias,
+                                    uint32_t width, uint32_t tokens, float eps, void *digits);
 // Partial sums only: batch_slices(w) planes [slice][token][row], for a prep
 // to add (the shape must have a split form).
 hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,

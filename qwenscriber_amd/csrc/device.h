@@ -199,6 +199,34 @@ __device__ __forceinline__ void encode_digits8(const float v[8], int e, uint32_t
     for (int j = 0; j < 6; ++j) planes[j] = w[j];
 }
 
+// Sum over a 256-thread workgroup; every thread gets the total (lds: 4
+// floats, reused after the call).
+__device__ __forceinline__ float block_sum_256(float v, float *lds) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    return (lds[0] + lds[1]) + (lds[2] + lds[3]);
+}
+
+// math.zig:99-116 layerNorm statistics of one row by a 256-thread workgroup:
+// the mean, then the centred variance, then 1 / sqrt(variance + eps). A row
+// value is then (x - mean) * inverse_std * weight + bias.
+__device__ __forceinline__ void layer_norm_stats(const float *row, uint32_t width, float eps, float *lds,
+                                                 float &mean, float &inverse_std) {
+    float sum = 0.0f;
+    for (uint32_t i = threadIdx.x; i < width; i += 256) sum += row[i];
+    mean = block_sum_256(sum, lds) / (float)width;
+    float squares = 0.0f;
+    for (uint32_t i = threadIdx.x; i < width; i += 256) {
+        const float centered = row[i] - mean;
+        squares += centered * centered;
+    }
+    const float variance = block_sum_256(squares, lds) / (float)width;
+    inverse_std = 1.0f / sqrtf(variance + eps);
+}
+
 // Exponent e with |x| <= 2^e for the chunk maximum `amax` (clamped so that
 // 2^(22-e) stays finite; an all-zero chunk uses e = 0).
 __device__ __forceinline__ int chunk_exponent(float amax) {

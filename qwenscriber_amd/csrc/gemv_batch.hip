@@ -105,6 +105,7 @@ struct BatchArgs {
     const uint8_t *data;     // N * K/64 * BPG
     float *out;              // tokens x N, or tokens x N/2 with pairs
     const float *residual;   // optional, tokens x N (may alias out); not with pairs
+    const float *bias;       // optional, N: out = residual + (W x + bias); not with pairs
     const float *ss;         // non-null: RMSNorm sums of squares [token][ss_parts]; results x 1/rms
     uint32_t ss_parts;
     float eps;
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(64 * max_waves<TILES>()) void gemv_batch_kernel(con
                 if (tok < a.tokens && (out_row & 1u) == 0 && out_row < a.n)
                     a.out[(size_t)tok * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
             } else if (tok < a.tokens && out_row < a.n) {
-                a.out[(size_t)tok * a.n + out_row] = res[t][r] + total;
+                a.out[(size_t)tok * a.n + out_row] = res[t][r] + (a.bias ? total + a.bias[out_row] : total);
             }
         }
     }
@@ -312,6 +313,7 @@ struct SplitArgs {
     const uint8_t *data;
     float *out;
     const float *residual;
+    const float *bias;       // optional, n: out = residual + (W x + bias) (one slice, no pairs)
     float *part;             // non-null: partial sums [slices][tokens][n] instead of out
     const float *ss;         // non-null: RMSNorm sums of squares [token][ss_parts]; results x 1/rms
     uint32_t ss_parts;
@@ -365,7 +367,7 @@ __device__ __forceinline__ void split_epilogue(const SplitArgs &a, const float (
                     a.out[(size_t)tok * (a.n / 2) + (out_row >> 1)] = silu_mul(total, partner);
             } else if (tok < a.tokens && out_row < a.n) {
                 const float res = a.residual ? a.residual[(size_t)tok * a.n + out_row] : 0.0f;
-                a.out[(size_t)tok * a.n + out_row] = res + total;
+                a.out[(size_t)tok * a.n + out_row] = res + (a.bias ? total + a.bias[out_row] : total);
             }
         }
     }
@@ -646,7 +648,7 @@ __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
 // 2j + 1), one output per thread.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, uint32_t slices, uint32_t tokens,
                                                            uint32_t n, const float *residual, float *out,
-                                                           uint32_t pairs) {
+                                                           uint32_t pairs, const float *bias) {
     const uint32_t width = pairs ? n / 2 : n;
     const size_t plane = (size_t)tokens * n;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -657,7 +659,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, ui
         out[i] = silu_mul(slice_sum(part + at, slices, plane), slice_sum(part + at + 1, slices, plane));
     } else {
         const size_t at = tok * n + j;
-        const float v = slice_sum(part + at, slices, plane);
+        float v = slice_sum(part + at, slices, plane);
+        if (bias) v += bias[j];
         out[i] = residual ? residual[at] + v : v;
     }
 }
@@ -740,6 +743,67 @@ __device__ __forceinline__ void input8(const PrepArgs &a, uint32_t t, uint32_t e
     }
 }
 
+// Activation digits of values e .. e + 7 (e a multiple of 8) of token tt of
+// a 16-token tile: per 64-value group (8 consecutive lanes, which must all
+// run this) x_int = rint(x * 2^(22-e)) with 2^e bounding the group's largest
+// |x|, three signed base-256 digit planes; within each 8-value block the even
+// columns' bytes come first, then the odd ones'. The group's multiplier
+// 2^(e-22) is written by its first lane.
+__device__ __forceinline__ void encode_digits8(const float (&v)[8], uint32_t tile, uint32_t tt, uint32_t e,
+                                               uint32_t gpr, uint8_t *digits, float *mult) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, dev::xor_lane<1>(amax));
+    amax = fmaxf(amax, dev::xor_lane<2>(amax));
+    amax = fmaxf(amax, dev::xor_lane<4>(amax));
+    const int ex = dev::chunk_exponent(amax);
+    const float up = __builtin_ldexpf(1.0f, 22 - ex);
+    uint32_t u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
+    const uint32_t g = e >> 6;
+    const uint32_t j = (e >> 3) & 7u;  // 8-value block within the group
+    uint8_t *dst = digits + ((size_t)tile * gpr + g) * kGroupBytes + tt * 64 + j * 8;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const int sh = 8 * p;
+        uint2 w;
+        w.x = ((u[0] >> sh) & 0xffu) | (((u[2] >> sh) & 0xffu) << 8) | (((u[4] >> sh) & 0xffu) << 16) |
+              (((u[6] >> sh) & 0xffu) << 24);
+        w.y = ((u[1] >> sh) & 0xffu) | (((u[3] >> sh) & 0xffu) << 8) | (((u[5] >> sh) & 0xffu) << 16) |
+              (((u[7] >> sh) & 0xffu) << 24);
+        *reinterpret_cast<uint2 *>(dst + p * kPlaneBytes) = w;
+    }
+    if (j == 0) mult[((size_t)tile * gpr + g) * kTokenTile + tt] = __builtin_ldexpf(1.0f, ex - 22);
+}
+
+// math.zig:99-116 layerNorm of each token row (one 256-thread workgroup per
+// token, the statistics of layer_norm_kernel) written straight as the batch
+// GEMV's activation digits (padding tokens of the last tile write zeros).
+__global__ __launch_bounds__(256) void layer_norm_digits_kernel(const float *x, const float *weight,
+                                                                const float *bias, uint32_t width, uint32_t tokens,
+                                                                float eps, uint8_t *digits, float *mult) {
+    __shared__ float lds[4];
+    const uint32_t t = blockIdx.x;
+    const bool real = t < tokens;
+    const float *row = x + (size_t)(real ? t : 0) * width;
+    float mean, inverse_std;
+    dev::layer_norm_stats(row, width, eps, lds, mean, inverse_std);
+    const uint32_t gpr = width >> 6;
+    for (uint32_t base = 0; base < width; base += 8 * 256) {
+        const uint32_t e = base + 8 * threadIdx.x;
+        const bool in_row = e < width;  // (whole groups: width is a multiple of 64)
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = in_row ? e + i : 0;
+            v[i] = real && in_row ? (row[c] - mean) * inverse_std * weight[c] + bias[c] : 0.0f;
+        }
+        if (in_row) encode_digits8(v, t / kTokenTile, t % kTokenTile, e, gpr, digits, mult);
+    }
+}
+
 template <Prep M>
 __global__ __launch_bounds__(64) void prep_batch_kernel(const PrepArgs a) {
     const uint32_t t = blockIdx.y;
@@ -767,31 +831,7 @@ __global__ __launch_bounds__(64) void prep_batch_kernel(const PrepArgs a) {
         for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(v[i], w[i]);
     }
     if (!in_row) return;
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, dev::xor_lane<1>(amax));
-    amax = fmaxf(amax, dev::xor_lane<2>(amax));
-    amax = fmaxf(amax, dev::xor_lane<4>(amax));
-    const int ex = dev::chunk_exponent(amax);
-    const float up = __builtin_ldexpf(1.0f, 22 - ex);
-    uint32_t u[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)__builtin_rintf(v[i] * up) + 0x808080) ^ 0x808080u;
-    const uint32_t g = e >> 6;
-    const uint32_t j = (e >> 3) & 7u;  // 8-value block within the group
-    uint8_t *dst = a.digits + ((size_t)tile * gpr + g) * kGroupBytes + tt * 64 + j * 8;
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-        const int sh = 8 * p;
-        uint2 w;
-        w.x = ((u[0] >> sh) & 0xffu) | (((u[2] >> sh) & 0xffu) << 8) | (((u[4] >> sh) & 0xffu) << 16) |
-              (((u[6] >> sh) & 0xffu) << 24);
-        w.y = ((u[1] >> sh) & 0xffu) | (((u[3] >> sh) & 0xffu) << 8) | (((u[5] >> sh) & 0xffu) << 16) |
-              (((u[7] >> sh) & 0xffu) << 24);
-        *reinterpret_cast<uint2 *>(dst + p * kPlaneBytes) = w;
-    }
-    if (j == 0) a.mult[((size_t)tile * gpr + g) * kTokenTile + tt] = __builtin_ldexpf(1.0f, ex - 22);
+    encode_digits8(v, tile, tt, e, gpr, a.digits, a.mult);
 }
 
 }  // namespace
@@ -819,6 +859,16 @@ size_t batch_digit_bytes(uint32_t tokens, uint32_t cols) {
     const size_t groups = cols / 64;
     return tiles * groups * kGroupBytes + tiles * groups * kTokenTile * sizeof(float) +
            tiles * kTokenTile * ss_parts_of(cols) * sizeof(float) + 256;
+}
+
+hipError_t launch_layer_norm_digits(hipStream_t s, const float *x, const float *weight, const float *bias,
+                                    uint32_t width, uint32_t tokens, float eps, void *digits) {
+    if (!tokens || width % 64) return hipErrorInvalidValue;
+    const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+    layer_norm_digits_kernel<<<tiles * kTokenTile, 256, 0, s>>>(x, weight, bias, width, tokens, eps,
+                                                                static_cast<uint8_t *>(digits),
+                                                                mult_of(digits, tokens, width));
+    return hipGetLastError();
 }
 
 hipError_t launch_prep_batch(hipStream_t s, const GemvInput &in, uint32_t tokens, uint32_t cols, void *digits,
@@ -995,9 +1045,11 @@ hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matr
 }
 
 hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens, float *out,
-                             const float *residual, bool pairs, float *partials, const BatchNorm &norm) {
+                             const float *residual, bool pairs, float *partials, const BatchNorm &norm,
+                             const float *bias) {
     if (!batch_format(w.format)) return hipErrorNotSupported;
     if (pairs && (w.rows & 1u)) return hipErrorInvalidValue;
+    if (pairs && bias) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     const SplitPlan plan = split_plan(w, tiles);
@@ -1007,13 +1059,14 @@ hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w,
         SplitArgs a = split_args(digits, w, tokens, plan, norm);
         a.out = out;
         a.residual = residual;
+        a.bias = bias;
         a.pairs = pairs ? 1u : 0u;
         if (plan.slices > 1) a.part = partials;
         launch_split(s, plan, a, tiles, w.format);
         if (plan.slices > 1) {
             const size_t items = (size_t)tokens * (pairs ? w.rows / 2 : w.rows);
             split_reduce_kernel<<<(uint32_t)((items + 255) / 256), 256, 0, s>>>(partials, plan.slices, tokens, w.rows,
-                                                                               residual, out, pairs ? 1u : 0u);
+                                                                               residual, out, pairs ? 1u : 0u, bias);
         }
         return hipGetLastError();
     }
@@ -1030,6 +1083,7 @@ hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w,
     a.data = w.data;
     a.out = out;
     a.residual = residual;
+    a.bias = bias;
     a.n = w.rows;
     a.k = w.cols;
     a.tokens = tokens;

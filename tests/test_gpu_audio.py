@@ -160,6 +160,7 @@ def make_layer(ctx, fmt, d_model, ffn_dim, seed):
     (qa.FORMAT_Q4, 256, 4, 512, 50, 13),
     (qa.FORMAT_Q8, 256, 4, 512, 50, 13),
     (qa.FORMAT_Q5, 256, 4, 512, 21, 8),
+    (qa.FORMAT_Q4, 256, 4, 512, 1, 8),  # one step: the per-linear path, separate bias and norm kernels
     (qa.FORMAT_Q4, 896, 14, 3584, 390, 104),  # Qwen3-ASR-0.6B audio layer, 30 s
 ])
 def test_audio_layer(ctx, fmt, d_model, heads, ffn_dim, steps, window):
