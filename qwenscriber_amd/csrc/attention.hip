@@ -358,7 +358,61 @@ __device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, cons
     }
 }
 
-template <int D, int R, bool Decoder>
+// Early: the second tile's loads are issued before the query prologue too
+// (a range of two tiles per wavefront then waits for memory once), at the
+// cost of that tile's registers during the prologue.
+// The end of a range kernel whose wavefronts each keep one maximum per head
+// (shared by all lane groups): every lane stores its accumulators to LDS as
+// they are, and the record's R*D sums are formed by one thread each, over
+// the wavefronts (rescaled to the range's maximum) and their lane groups --
+// no cross-lane reductions. 16 KB of LDS per query head.
+template <int D, int R>
+__device__ __forceinline__ void write_range_record_lds(const AttnKernelArgs &a, const SoftmaxState<R> &st,
+                                                       const float (&acc)[R][16], uint32_t b, uint32_t kvh,
+                                                       uint32_t split, int wave, int sub, int group) {
+    constexpr int LPP = D / 16;
+    constexpr int PPW = 64 / LPP;
+    constexpr int REC = R * D + 4 * R;
+    __shared__ float lds_part[kWaves][PPW][R][D];
+    __shared__ float lds_ml[kWaves][R][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+            *reinterpret_cast<float4 *>(&lds_part[wave][group][r][sub * 16 + i]) =
+                make_float4(acc[r][i], acc[r][i + 1], acc[r][i + 2], acc[r][i + 3]);
+        if ((threadIdx.x & 63) == 0) {
+            lds_ml[wave][r][0] = st.m[r];
+            lds_ml[wave][r][1] = st.l[r];
+        }
+    }
+    __syncthreads();
+    float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
+    for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
+        const int r = idx / D;
+        const int d = idx % D;
+        float M = lds_ml[0][r][0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds_ml[w][r][0]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            float part = 0.0f;
+#pragma unroll
+            for (int g = 0; g < PPW; ++g) part += lds_part[w][g][r][d];
+            const float f = fast_exp2(lds_ml[w][r][0] - M);
+            L += lds_ml[w][r][1] * f;
+            A += part * f;
+        }
+        rec[idx] = A;
+        if (d == 0) {
+            rec[R * D + 4 * r + 0] = M;
+            rec[R * D + 4 * r + 1] = L;
+        }
+    }
+}
+
+template <int D, int R, bool Decoder, bool Early>
 __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     constexpr int LPP = D / 16;              // value layout: lanes per position
     constexpr int PPW = 64 / LPP;            // value layout: lane groups per wave
@@ -432,6 +486,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     // either. Lane group r < R of wavefront 0 takes query head r.
     Tile cur, nxt;
     load_tile(cur, begin, a.rows);
+    if constexpr (Early) load_tile(nxt, begin + kSpan, a.rows);
     const bool prologue = wave == 0 && group < R;
     const int qh = prologue ? group : 0;
     const float *row = a.query + (size_t)b * a.query_stride;
@@ -590,14 +645,26 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     // compiler's wait for the current tile also wait for the loads issued
     // after it. The scheduling barriers keep the work on the current tile
     // (which waits for its data) from moving above the next tile's loads.
-    for (uint32_t base = begin; base < end; base += 2 * kSpan) {
-        load_tile(nxt, base + kSpan, end);
-        __builtin_amdgcn_sched_barrier(0);
-        use_tile(cur, base);
-        if (base + kSpan >= end) break;
-        load_tile(cur, base + 2 * kSpan, end);
-        __builtin_amdgcn_sched_barrier(0);
-        use_tile(nxt, base + kSpan);
+    if (begin < end) {
+        if constexpr (!Early) {
+            load_tile(nxt, begin + kSpan, end);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        use_tile(cur, begin);
+        if (begin + kSpan < end) {
+            load_tile(cur, begin + 2 * kSpan, end);
+            __builtin_amdgcn_sched_barrier(0);
+            use_tile(nxt, begin + kSpan);
+            for (uint32_t base = begin + 2 * kSpan; base < end; base += 2 * kSpan) {
+                load_tile(nxt, base + kSpan, end);
+                __builtin_amdgcn_sched_barrier(0);
+                use_tile(cur, base);
+                if (base + kSpan >= end) break;
+                load_tile(cur, base + 2 * kSpan, end);
+                __builtin_amdgcn_sched_barrier(0);
+                use_tile(nxt, base + kSpan);
+            }
+        }
     }
 
     // The wave's state: the lane groups share each head's maximum, so their
@@ -616,26 +683,33 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             st.l[4 * hs + k] = lane_value(lsum, 16 * k);
         }
     }
+    if constexpr (R <= 2) {
+        write_range_record_lds<D, R>(a, st, acc, b, kvh, split, wave, sub, group);
+    } else {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st.acc[r][i] = sum_over_groups<LPP>(acc[r][i]);
-    write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
+            for (int i = 0; i < 16; ++i) st.acc[r][i] = sum_over_groups<LPP>(acc[r][i]);
+        write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
+    }
 }
 
 // The q8 range kernel. Forms that fit three wavefronts per SIMD (168
-// registers) without spilling are compiled for that occupancy.
+// registers) without spilling are compiled for that occupancy (and load the
+// second tile after the prologue); the others, and every form when the grid
+// is at most one workgroup per CU (occupancy does not matter there), use
+// the full register budget and load both tiles first.
 template <int D, int R, bool Decoder>
 constexpr bool kThreeWaves = R <= 2 && (D == 64 || (D == 128 && Decoder));
 
 template <int D, int R, bool Decoder>
 __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) {
-    attention_range<D, R, Decoder>(a);
+    attention_range<D, R, Decoder, true>(a);
 }
 
 template <int D, int R, bool Decoder>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel3(const AttnKernelArgs a) {
-    attention_range<D, R, Decoder>(a);
+    attention_range<D, R, Decoder, false>(a);
 }
 
 // The range kernel over an f32 cache (kernels.zig:572-627): the same lane
@@ -1033,9 +1107,10 @@ bool attention_supported(uint32_t head_dim, uint32_t ratio) {
 }
 
 template <int D, int R>
-void launch_attention_pair(hipStream_t s, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
+void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
                            uint32_t kv_heads, uint32_t heads, uint32_t batch) {
     const dim3 ranges(splits, kv_heads, batch), merge(heads, batch);
+    const bool sparse = (uint64_t)splits * kv_heads * batch <= (uint64_t)(cus > 0 ? cus : 256);
     if (f32) {
         if (decoder) {
             attention_f32_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
@@ -1045,19 +1120,27 @@ void launch_attention_pair(hipStream_t s, const AttnKernelArgs &k, bool decoder,
             attention_combine_kernel<D, R, false, true><<<merge, 256, 0, s>>>(k);
         }
     } else if (decoder) {
-        if constexpr (kThreeWaves<D, R, true>) attention_kernel3<D, R, true><<<ranges, 256, 0, s>>>(k);
-        else attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
+        bool three = false;
+        if constexpr (kThreeWaves<D, R, true>) {
+            three = !sparse;
+            if (three) attention_kernel3<D, R, true><<<ranges, 256, 0, s>>>(k);
+        }
+        if (!three) attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
         attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
     } else {
-        if constexpr (kThreeWaves<D, R, false>) attention_kernel3<D, R, false><<<ranges, 256, 0, s>>>(k);
-        else attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
+        bool three = false;
+        if constexpr (kThreeWaves<D, R, false>) {
+            three = !sparse;
+            if (three) attention_kernel3<D, R, false><<<ranges, 256, 0, s>>>(k);
+        }
+        if (!three) attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
         attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     }
 }
 
 #define QWH_ATTN_CASE(D_, R_)                                                                       \
     if (a.head_dim == D_ && R == R_) {                                                              \
-        launch_attention_pair<D_, R_>(s, k, decoder, a.f32_cache, splits, a.kv_heads, a.heads, a.batch); \
+        launch_attention_pair<D_, R_>(s, cus, k, decoder, a.f32_cache, splits, a.kv_heads, a.heads, a.batch); \
         return hipGetLastError();                                                                   \
     }
 
