@@ -869,11 +869,12 @@ int32_t linear_shared_input(qwh_ctx *ctx, std::initializer_list<uint64_t> handle
 
 // qwh_audio_layer when every linear has a batch GEMV form: the two
 // LayerNorms write the GEMVs' activation digits directly, q / k / v read one
-// set of digits, the GELU of ffn_in + bias is applied as ffn_out's digits are
-// prepared, and o and ffn_out add their bias and the residual stream in their
-// own epilogue (out = encoder + (W x + bias), the order of the reference's
-// addBias then addInPlace). Nine launches instead of fourteen, and no f32
-// pass over the normed rows or the projections' outputs.
+// set of digits in one launch, the GELU of ffn_in + bias is applied as
+// ffn_out's digits are prepared, and o and ffn_out add their bias and the
+// residual stream in their own epilogue (out = encoder + (W x + bias), the
+// order of the reference's addBias then addInPlace). Seven launches instead
+// of fourteen, and no f32 pass over the normed rows or the projections'
+// outputs.
 int32_t audio_layer_batch(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float *encoder_dev, uint32_t steps,
                           uint32_t d_model, uint32_t ffn_dim, float eps, const AudioAttentionArgs &a, float *wide) {
     hipStream_t s = ctx->stream;
@@ -894,9 +895,17 @@ int32_t audio_layer_batch(qwh_ctx *ctx, const qwh_audio_layer_weights *w, float 
     QWH_TRY(check_hip(ctx, launch_layer_norm_digits(s, encoder_dev, w->attention_norm_weight, w->attention_norm_bias,
                                                     d_model, steps, eps, digits),
                       "audio attention norm"));
-    QWH_TRY(gemv(w->q, const_cast<float *>(a.q), nullptr, nullptr, "audio q"));
-    QWH_TRY(gemv(w->k, const_cast<float *>(a.k), nullptr, nullptr, "audio k"));
-    QWH_TRY(gemv(w->v, const_cast<float *>(a.v), nullptr, nullptr, "audio v"));
+    // q, k and v in one launch where their plans agree (one K slice each).
+    const Matrix *qkv[3] = {find_matrix(ctx, w->q), find_matrix(ctx, w->k), find_matrix(ctx, w->v)};
+    float *const qkv_out[3] = {const_cast<float *>(a.q), const_cast<float *>(a.k), const_cast<float *>(a.v)};
+    const hipError_t fused = launch_gemv_batch_multi(s, digits, qkv, qkv_out, 3, steps);
+    if (fused == hipErrorNotSupported) {
+        QWH_TRY(gemv(w->q, qkv_out[0], nullptr, nullptr, "audio q"));
+        QWH_TRY(gemv(w->k, qkv_out[1], nullptr, nullptr, "audio k"));
+        QWH_TRY(gemv(w->v, qkv_out[2], nullptr, nullptr, "audio v"));
+    } else {
+        QWH_TRY(check_hip(ctx, fused, "audio q|k|v"));
+    }
     QWH_TRY(check_hip(ctx, launch_audio_attention(s, a), "audio attention"));
     // :824-848 projectAttentionOutput + o bias, :669 addInPlace.
     GemvInput in;

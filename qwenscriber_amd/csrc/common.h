@@ -171,6 +171,11 @@ bool gemv_batch_supported(const Matrix &w);
 hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
                              float *out, const float *residual, bool pairs = false, float *partials = nullptr,
                              const BatchNorm &norm = BatchNorm{}, const float *bias = nullptr);
+// Up to three matrices of one format, K and split plan, each with a single K
+// slice, over the same digits in one launch (out[i] = W_i x); returns
+// hipErrorNotSupported, launching nothing, for any other set.
+hipError_t launch_gemv_batch_multi(hipStream_t s, const void *digits, const Matrix *const *w, float *const *out,
+                                   uint32_t count, uint32_t tokens);
 // math.zig:99-116 layerNorm of `tokens` rows of `width` values (width a
 // multiple of 64; the statistics of launch_layer_norm) written straight as
 // the batch GEMV's activation digits (batch_digit_bytes(tokens, width)).

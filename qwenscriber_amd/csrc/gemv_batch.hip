@@ -373,8 +373,9 @@ __device__ __forceinline__ void split_epilogue(const SplitArgs &a, const float (
     }
 }
 
+// The split workgroup for row block `bx` of `a`'s matrix.
 template <int TW, int KC, int BPG>
-__global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
+__device__ __forceinline__ void split_block(const SplitArgs &a, uint32_t bx) {
     using S = SplitShape<TW, KC, BPG>;
     constexpr int ROWS = S::ROWS, PPR = S::PPR, RPI = S::RPI, NW = S::NW, DPT = S::DPT;
     __shared__ v4i dl[2][S::DPIECES];          // digit planes, [group][plane][lane]
@@ -388,7 +389,7 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
     const int blk = lane >> 4;
     const uint32_t gpr = a.k >> 6;
     const uint32_t tile = blockIdx.z;
-    const uint32_t row0 = (blockIdx.x * 4 + wave) * ROWS;
+    const uint32_t row0 = (bx * 4 + wave) * ROWS;
     const size_t row_bytes = (size_t)gpr * BPG;
     const uint32_t g_first = blockIdx.y * a.slice_groups;
     const uint32_t chunks = a.slice_groups / KC;
@@ -496,6 +497,28 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
 #pragma unroll
             for (int t = 0; t < TW; ++t) acc[t][r] = __fmul_rn(acc[t][r], inv[r]);
     split_epilogue<TW>(a, acc, tile, row0, col, blk);
+}
+
+template <int TW, int KC, int BPG>
+__global__ __launch_bounds__(256) void gemv_split_kernel(const SplitArgs a) {
+    split_block<TW, KC, BPG>(a, blockIdx.x);
+}
+
+// Up to three matrices of one shape class (format, K, plan; one K slice)
+// over the same activation digits in one launch: grid.x runs over the
+// matrices' row blocks in order.
+constexpr int kMaxMulti = 3;
+struct SplitMulti {
+    SplitArgs m[kMaxMulti];
+    uint32_t blocks[kMaxMulti];
+    uint32_t count;
+};
+
+template <int TW, int KC, int BPG>
+__global__ __launch_bounds__(256) void gemv_split_multi_kernel(const SplitMulti s) {
+    uint32_t bx = blockIdx.x, i = 0;
+    while (i + 1 < s.count && bx >= s.blocks[i]) bx -= s.blocks[i++];
+    split_block<TW, KC, BPG>(s.m[i], bx);
 }
 
 // Sum over the K slices, in slice order, of the partial sums at p (slices
@@ -804,6 +827,62 @@ __global__ __launch_bounds__(256) void layer_norm_digits_kernel(const float *x, 
     }
 }
 
+// The same for rows of at most kLnWavePasses * 512 values: one wavefront per
+// step (four per workgroup), the row read once into registers (lane l holds
+// values 512 p + 8 l .. +7 of each pass p), the statistics by wavefront
+// reductions, no LDS or barriers.
+constexpr int kLnWavePasses = 4;
+__global__ __launch_bounds__(256) void layer_norm_digits_wave_kernel(const float *x, const float *weight,
+                                                                     const float *bias, uint32_t width,
+                                                                     uint32_t tokens, float eps, uint8_t *digits,
+                                                                     float *mult) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t padded = (tokens + kTokenTile - 1) / kTokenTile * kTokenTile;
+    if (t >= padded) return;  // (whole wavefronts)
+    const bool real = t < tokens;
+    const float *row = x + (size_t)(real ? t : 0) * width;
+    const uint32_t gpr = width >> 6;
+    float v[kLnWavePasses][8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kLnWavePasses; ++p) {
+        const uint32_t e = 512 * p + 8 * lane;
+        const bool in_row = e < width;
+        load8(row + (in_row ? e : 0), v[p]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[p][i] = in_row ? v[p][i] : 0.0f;
+            sum += v[p][i];
+        }
+    }
+    const float mean = dev::wave_sum(sum) / (float)width;
+    float squares = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kLnWavePasses; ++p) {
+        const bool in_row = 512 * p + 8 * lane < width;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float centered = v[p][i] - mean;
+            squares += in_row ? centered * centered : 0.0f;
+        }
+    }
+    const float inverse_std = 1.0f / sqrtf(dev::wave_sum(squares) / (float)width + eps);
+#pragma unroll
+    for (int p = 0; p < kLnWavePasses; ++p) {
+        const uint32_t e = 512 * p + 8 * lane;
+        if (512 * p >= width) break;  // (uniform)
+        const bool in_row = e < width;
+        float w[8], b[8];
+        load8(weight + (in_row ? e : 0), w);
+        load8(bias + (in_row ? e : 0), b);
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = real ? (v[p][i] - mean) * inverse_std * w[i] + b[i] : 0.0f;
+        if (in_row) encode_digits8(y, t / kTokenTile, t % kTokenTile, e, gpr, digits, mult);
+    }
+}
+
 template <Prep M>
 __global__ __launch_bounds__(64) void prep_batch_kernel(const PrepArgs a) {
     const uint32_t t = blockIdx.y;
@@ -865,9 +944,15 @@ hipError_t launch_layer_norm_digits(hipStream_t s, const float *x, const float *
                                     uint32_t width, uint32_t tokens, float eps, void *digits) {
     if (!tokens || width % 64) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
-    layer_norm_digits_kernel<<<tiles * kTokenTile, 256, 0, s>>>(x, weight, bias, width, tokens, eps,
-                                                                static_cast<uint8_t *>(digits),
-                                                                mult_of(digits, tokens, width));
+    uint8_t *d = static_cast<uint8_t *>(digits);
+    float *m = mult_of(digits, tokens, width);
+    // The wavefront form loads 16 bytes at a time from each row.
+    const bool aligned = (((uintptr_t)x | (uintptr_t)weight | (uintptr_t)bias) & 15u) == 0 && width % 4 == 0;
+    if (width <= 512u * kLnWavePasses && aligned)
+        layer_norm_digits_wave_kernel<<<tiles * kTokenTile / 4, 256, 0, s>>>(x, weight, bias, width, tokens, eps, d,
+                                                                             m);
+    else
+        layer_norm_digits_kernel<<<tiles * kTokenTile, 256, 0, s>>>(x, weight, bias, width, tokens, eps, d, m);
     return hipGetLastError();
 }
 
@@ -973,6 +1058,22 @@ void launch_split_bpg(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, 
     }
 }
 
+template <int BPG>
+void launch_split_multi_bpg(hipStream_t s, const SplitPlan &plan, const SplitMulti &m, dim3 grid) {
+    if (plan.kc == 2) {
+        if (plan.tw == 2) gemv_split_multi_kernel<2, 2, BPG><<<grid, 256, 0, s>>>(m);
+        else gemv_split_multi_kernel<1, 2, BPG><<<grid, 256, 0, s>>>(m);
+    } else if (plan.tw == 2 && plan.kc == 4) {
+        gemv_split_multi_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(m);
+    } else if (plan.tw == 2) {
+        gemv_split_multi_kernel<2, 8, BPG><<<grid, 256, 0, s>>>(m);
+    } else if (plan.kc == 4) {
+        gemv_split_multi_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(m);
+    } else {
+        gemv_split_multi_kernel<1, 8, BPG><<<grid, 256, 0, s>>>(m);
+    }
+}
+
 void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint32_t tiles, int format) {
     const uint32_t row_tiles = (a.n + kRowTile - 1) / kRowTile;
     const dim3 grid((row_tiles + 4u * plan.tw - 1) / (4u * plan.tw), plan.slices, tiles);
@@ -1041,6 +1142,33 @@ hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matr
     SplitArgs a = split_args(digits, w, tokens, plan, norm);
     a.part = partials;
     launch_split(s, plan, a, (tokens + kTokenTile - 1) / kTokenTile, w.format);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_batch_multi(hipStream_t s, const void *digits, const Matrix *const *w, float *const *out,
+                                   uint32_t count, uint32_t tokens) {
+    if (count == 0 || count > (uint32_t)kMaxMulti || tokens == 0) return hipErrorInvalidValue;
+    const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
+    const SplitPlan plan = split_plan(*w[0], tiles);
+    if (!plan.tw || plan.slices != 1 || (w[0]->format != QWH_FORMAT_Q4 && w[0]->format != QWH_FORMAT_Q8))
+        return hipErrorNotSupported;
+    SplitMulti m{};
+    m.count = count;
+    uint32_t blocks = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const SplitPlan p = split_plan(*w[i], tiles);
+        if (w[i]->format != w[0]->format || w[i]->cols != w[0]->cols || p.tw != plan.tw || p.kc != plan.kc ||
+            p.slices != 1)
+            return hipErrorNotSupported;
+        m.m[i] = split_args(digits, *w[i], tokens, plan, BatchNorm{});
+        m.m[i].out = out[i];
+        const uint32_t row_tiles = (w[i]->rows + kRowTile - 1) / kRowTile;
+        m.blocks[i] = (row_tiles + 4u * plan.tw - 1) / (4u * plan.tw);
+        blocks += m.blocks[i];
+    }
+    const dim3 grid(blocks, 1, tiles);
+    if (w[0]->format == QWH_FORMAT_Q8) launch_split_multi_bpg<64>(s, plan, m, grid);
+    else launch_split_multi_bpg<32>(s, plan, m, grid);
     return hipGetLastError();
 }
 
