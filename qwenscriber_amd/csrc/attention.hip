@@ -34,7 +34,10 @@
 namespace qwh {
 namespace {
 
-constexpr float kNeg = -1.0e30f;  // running-max sentinel: finite, so exp2(kNeg - kNeg) is defined
+constexpr float kNeg = -1.0e30f;
+// Word 3 of a raw buffer resource (gfx9 family: 32-bit data format; the
+// range check is on byte offsets, stride 0).
+constexpr int kBufferWord3 = 0x00020000;  // running-max sentinel: finite, so exp2(kNeg - kNeg) is defined
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr int kWaves = 4;
 constexpr uint32_t kMaxSplits = 512;
@@ -455,10 +458,32 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         uint4 vc[NV];
         uint32_t vs[NV];
     };
-    // A row at or past `limit` (>= 1) loads row limit - 1 instead and is
-    // masked out when the tile is used. Every load is unconditional, so all
-    // of them are in flight together.
-    auto load_tile = [&](Tile &t, uint32_t base, uint32_t limit) {
+    // Every load is unconditional, so all of a tile's loads are in flight
+    // together. Plain form: tiles are read through buffer resources that
+    // start at the tile's first row and end at `limit` (the allocated rows,
+    // or `end` once the position is known): a lane's byte offsets within a
+    // tile are the same for every tile and the resource is scalar
+    // arithmetic, so a tile costs no vector address arithmetic, and a row at
+    // or past `limit` reads zeros through the hardware range check without
+    // touching memory (batch 16 and batch 8 at 4096 / 8192 positions: 31.3
+    // -> 29.3 us and 31.5 -> 28.9 us). Decoder form: global loads with each
+    // row at or past `limit` clamped to row limit - 1 (one cached line) and
+    // masked when the tile is used; the buffer form measured 1-3 % slower
+    // there (33.4 against 32.3 us per batch-16 layer, same box).
+    uint32_t key_off[kTileBlocks], kscale_off[kTileBlocks], val_off[NV], vscale_off[NV];
+#pragma unroll
+    for (int blk = 0; blk < kTileBlocks; ++blk) {
+        const uint32_t rel = wave * kTile + 16 * blk + n;
+        key_off[blk] = rel * kv_width + key_col;
+        kscale_off[blk] = (rel * gpr + kvh * G) * 2;
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const uint32_t rel = wave * kTile + NV * group + v;
+        val_off[v] = rel * kv_width + code_col;
+        vscale_off[v] = (rel * gpr + vscale_col) * 2;
+    }
+    auto load_tile_global = [&](Tile &t, uint32_t base, uint32_t limit) {
         const uint32_t first = base + wave * kTile;
 #pragma unroll
         for (int blk = 0; blk < kTileBlocks; ++blk) {
@@ -476,6 +501,39 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             const uint32_t row = p < limit ? p : limit - 1;
             t.vc[v] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)row * kv_width + code_col);
             t.vs[v] = v_scales[(size_t)row * gpr + vscale_col];
+        }
+    };
+    auto load_tile = [&](Tile &t, uint32_t base_in, uint32_t limit) {
+        if constexpr (Decoder) {
+            load_tile_global(t, base_in, limit);
+            return;
+        }
+        // (Scalars: the resources must be uniform.)
+        const uint32_t base = __builtin_amdgcn_readfirstlane(base_in);
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(base < limit ? limit - base : 0u);
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(k_codes + (size_t)base * kv_width), 0, (int)(rows * kv_width), kBufferWord3);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(v_codes + (size_t)base * kv_width), 0, (int)(rows * kv_width), kBufferWord3);
+        const __amdgpu_buffer_rsrc_t ksr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(k_scales + (size_t)base * gpr), 0, (int)(rows * gpr * 2), kBufferWord3);
+        const __amdgpu_buffer_rsrc_t vsr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(v_scales + (size_t)base * gpr), 0, (int)(rows * gpr * 2), kBufferWord3);
+#pragma unroll
+        for (int blk = 0; blk < kTileBlocks; ++blk) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const v4i c = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)key_off[blk] + 64 * g, 0, 0));
+                t.kc[blk][g] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
+                t.ks[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(ksr, (int)kscale_off[blk] + 2 * g, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const v4i c = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)val_off[v], 0, 0));
+            t.vc[v] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
+            t.vs[v] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)vscale_off[v], 0, 0);
         }
     };
 
@@ -640,10 +698,10 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
 
     // Double buffered, two tiles per trip: the next tile's loads are in
     // flight while the current one is scored and accumulated. The loads are
-    // issued whether or not the tile holds positions (past `end` every lane
-    // reads row end - 1, one cached line): a load under a branch makes the
-    // compiler's wait for the current tile also wait for the loads issued
-    // after it. The scheduling barriers keep the work on the current tile
+    // issued whether or not the tile holds positions (past `end` they read
+    // zeros without a memory access, or one cached line): a load under a
+    // branch makes the compiler's wait for the current tile also wait for
+    // the loads issued after it. The scheduling barriers keep the work on the current tile
     // (which waits for its data) from moving above the next tile's loads.
     if (begin < end) {
         if constexpr (!Early) {
