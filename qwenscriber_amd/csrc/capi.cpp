@@ -1025,6 +1025,16 @@ int32_t qwh_conv3x3s2_gelu(qwh_ctx *ctx, float *out_dev, const float *in_dev, co
     QWH_TRY(check_device_ptr(ctx, in_dev, "input"));
     QWH_TRY(check_device_ptr(ctx, weights_dev, "weights"));
     QWH_TRY(check_device_ptr(ctx, bias_dev, "bias"));
+    if (conv_mfma_supported(in_channels, in_height, in_width)) {
+        // The matrix-core form: the weights prepared into the context's
+        // scratch, then the convolution.
+        QWH_TRY(ensure_workspace(ctx, ctx->scratch, conv_mfma_prep_bytes(out_channels, in_channels)));
+        QWH_TRY(check_hip(ctx, launch_conv_mfma_prep(ctx->stream, weights_dev, out_channels, in_channels,
+                                                     ctx->scratch.ptr), "conv weight prep"));
+        return check_hip(ctx, launch_conv3x3s2_gelu_mfma(ctx->stream, out_dev, in_dev, ctx->scratch.ptr, bias_dev, batch,
+                                                         out_channels, in_channels, in_height, in_width),
+                         "conv3x3 stride 2");
+    }
     return check_hip(ctx, launch_conv3x3s2_gelu(ctx->stream, out_dev, in_dev, weights_dev, bias_dev, batch, out_channels,
                                                 in_channels, in_height, in_width), "conv3x3 stride 2");
 }
@@ -1079,10 +1089,22 @@ int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *w, co
     auto align = [](size_t n) { return (n + 63) & ~(size_t)63; };  // floats: 256-byte aligned pieces
     const size_t off1 = align(group * mel_plane), off2 = off1 + align(group * p1), off3 = off2 + align(group * p2);
     const size_t off_flat = off3 + align(group * p3);
-    const size_t total = off_flat + align((size_t)group * chunk_steps * features);
+    // conv2 / conv3 on the matrix cores where their shapes allow: their
+    // weights prepared once per call after the planes.
+    const bool mfma2 = conv_mfma_supported(downsample, h1, w1), mfma3 = conv_mfma_supported(downsample, h2, w2);
+    const size_t prep_floats = align(conv_mfma_prep_bytes(downsample, downsample) / sizeof(float));
+    const size_t off_prep2 = off_flat + align((size_t)group * chunk_steps * features);
+    const size_t off_prep3 = off_prep2 + (mfma2 ? prep_floats : 0);
+    const size_t total = off_prep3 + (mfma3 ? prep_floats : 0);
     QWH_TRY(ensure_workspace(ctx, ctx->front, total * sizeof(float)));
     float *ws = static_cast<float *>(ctx->front.ptr);
     hipStream_t s = ctx->stream;
+    if (mfma2)
+        QWH_TRY(check_hip(ctx, launch_conv_mfma_prep(s, w->conv2_weight, downsample, downsample, ws + off_prep2),
+                          "conv2 weight prep"));
+    if (mfma3)
+        QWH_TRY(check_hip(ctx, launch_conv_mfma_prep(s, w->conv3_weight, downsample, downsample, ws + off_prep3),
+                          "conv3 weight prep"));
     if (!ctx->front_table.ptr || ctx->front_table_steps != chunk_steps || ctx->front_table_width != d_model) {
         // addSinusoidalPosition (model.zig:751-763) for the steps of a chunk,
         // in f64 on the host, narrowed to f32 as the reference does; built
@@ -1114,10 +1136,16 @@ int32_t qwh_audio_frontend(qwh_ctx *ctx, const qwh_audio_frontend_weights *w, co
                           "front-end chunks"));
         QWH_TRY(check_hip(ctx, launch_conv3x3s2_gelu(s, ws + off1, ws, w->conv1_weight, w->conv1_bias, count, downsample,
                                                      1, mel_bins, chunk_frames), "conv1"));
-        QWH_TRY(check_hip(ctx, launch_conv3x3s2_gelu(s, ws + off2, ws + off1, w->conv2_weight, w->conv2_bias, count,
-                                                     downsample, downsample, h1, w1), "conv2"));
-        QWH_TRY(check_hip(ctx, launch_conv3x3s2_gelu(s, ws + off3, ws + off2, w->conv3_weight, w->conv3_bias, count,
-                                                     downsample, downsample, h2, w2), "conv3"));
+        QWH_TRY(check_hip(ctx, mfma2 ? launch_conv3x3s2_gelu_mfma(s, ws + off2, ws + off1, ws + off_prep2,
+                                                                  w->conv2_bias, count, downsample, downsample, h1, w1)
+                                     : launch_conv3x3s2_gelu(s, ws + off2, ws + off1, w->conv2_weight, w->conv2_bias,
+                                                             count, downsample, downsample, h1, w1),
+                          "conv2"));
+        QWH_TRY(check_hip(ctx, mfma3 ? launch_conv3x3s2_gelu_mfma(s, ws + off3, ws + off2, ws + off_prep3,
+                                                                  w->conv3_bias, count, downsample, downsample, h2, w2)
+                                     : launch_conv3x3s2_gelu(s, ws + off3, ws + off2, w->conv3_weight, w->conv3_bias,
+                                                             count, downsample, downsample, h2, w2),
+                          "conv3"));
         QWH_TRY(check_hip(ctx, launch_pack_steps(s, ws + off3, downsample, bins, chunk_steps, rows, ws + off_flat),
                           "front-end flatten"));
         float *out = encoder_dev + (size_t)row0 * d_model;

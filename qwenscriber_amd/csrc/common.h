@@ -241,6 +241,14 @@ hipError_t launch_kv_append_q8(hipStream_t s, const float *key, const float *val
 // [out_ch][in_ch][9] f16 bits.
 hipError_t launch_conv3x3s2_gelu(hipStream_t s, float *out, const float *in, const uint16_t *weights, const float *bias,
                                  uint32_t batch, uint32_t out_ch, uint32_t in_ch, uint32_t h, uint32_t w);
+// The matrix-core form for input channels a multiple of 16 (planes small
+// enough for its LDS patch: conv_mfma_supported): weights prepared once per
+// weight set into `wprep` (conv_mfma_prep_bytes) by launch_conv_mfma_prep.
+bool conv_mfma_supported(uint32_t in_ch, uint32_t h, uint32_t w);
+size_t conv_mfma_prep_bytes(uint32_t out_ch, uint32_t in_ch);
+hipError_t launch_conv_mfma_prep(hipStream_t s, const uint16_t *weights, uint32_t out_ch, uint32_t in_ch, void *wprep);
+hipError_t launch_conv3x3s2_gelu_mfma(hipStream_t s, float *out, const float *in, const void *wprep, const float *bias,
+                                     uint32_t batch, uint32_t out_ch, uint32_t in_ch, uint32_t h, uint32_t w);
 hipError_t launch_gather_chunks(hipStream_t s, const float *mel, uint32_t bins, uint32_t frames, uint32_t chunk_frames,
                                 uint32_t first, uint32_t count, float *out);
 hipError_t launch_pack_steps(hipStream_t s, const float *conv3, uint32_t channels, uint32_t bins, uint32_t steps_per_chunk,

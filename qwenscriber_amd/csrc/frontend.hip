@@ -18,6 +18,8 @@
 // 4 positions in f32 FMAs (the reference sums each input channel's nine taps
 // before adding them to the output; the order here differs, within f32
 // rounding), then adds the bias and applies GELU (the reference's erf fit).
+#include <type_traits>
+
 #include "common.h"
 #include "device.h"
 
@@ -101,6 +103,198 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_kernel(const ConvArgs a) {
     }
 }
 
+// ---- Matrix-core form (input channels a multiple of 16) ----
+//
+// The convolution as an implicit GEMM on v_mfma_f32_32x32x16_bf16: rows are
+// output channels, columns are output positions (row-major over the output
+// plane), and the reduction runs over (tap, input channel) in stages of 16
+// input channels, one 16-deep MFMA step per tap. Both operands are split into
+// two bf16 terms: a weight (f16, 11 significant bits) is exactly hi + lo
+// (hi = its bf16 rounding, lo = the exact remainder, at most 4 bits); an
+// activation is hi + lo with hi its bf16 rounding and lo the bf16 rounding of
+// the exact remainder (|x - hi - lo| <= 2^-17 |x|). The four products are
+// accumulated in f32 by the MFMA, so each term is an exact product summed in
+// f32: within 2^-17 of the f32 convolution per term, no overflow range of its
+// own (bf16 has f32's exponent range).
+//
+// Workgroup: 128 output channels (four wavefronts of 32) x 32 positions. Per
+// stage the 32 positions' input rows (at most 2 * ceil(31 / ow) + 3 of them,
+// zero padding included) x 16 channels go into LDS as [row][col][channel]
+// (channel padded to 24 for the reads' banks) in both terms, double buffered,
+// the next stage's values loaded into registers while this one multiplies.
+// Weights come prepared [stage][tap][term][oc][16] (conv_mfma_prep_kernel)
+// and each wavefront loads its 32 rows' 18 operands one stage ahead.
+typedef __bf16 cbf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 cbf16x2 __attribute__((ext_vector_type(2)));
+typedef float cf32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMfOc = 128;       // output channels per workgroup
+constexpr int kMfPos = 32;       // output positions per workgroup
+constexpr int kMfIc = 16;        // input channels per stage
+constexpr int kMfIcPad = 24;     // channel stride of a patch cell (bf16)
+constexpr int kMfRounds = 4;     // patch items per thread at most (256 threads)
+constexpr size_t kMfLdsMax = 80 * 1024;  // the patch buffers' LDS, two workgroups per CU
+
+struct ConvMfmaArgs {
+    float *out;                  // [batch][out_ch][oh * ow]
+    const float *in;             // [batch][in_ch][h][w]
+    const uint16_t *wprep;       // [in_ch / 16][9][2][oc_pad][16] bf16 bits
+    const float *bias;
+    uint32_t out_ch, oc_pad, in_ch, h, w, oh, ow, positions;
+    uint32_t patch_rows, patch_cols;
+};
+
+// Prepared weights: f16 -> f32 (exact), hi = bf16(w), lo = bf16(w - hi)
+// (exact), laid out for the A operand; rows past out_ch are zero.
+__global__ void conv_mfma_prep_kernel(const uint16_t *weights, uint32_t out_ch, uint32_t oc_pad, uint32_t in_ch,
+                                      uint16_t *wprep) {
+    const uint64_t n = (uint64_t)oc_pad * in_ch * 9;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t icl = (uint32_t)(i % kMfIc);
+        const uint32_t oc = (uint32_t)((i / kMfIc) % oc_pad);
+        const uint32_t tap = (uint32_t)((i / ((uint64_t)kMfIc * oc_pad)) % 9);
+        const uint32_t stage = (uint32_t)(i / ((uint64_t)kMfIc * oc_pad * 9));
+        const uint32_t ic = stage * kMfIc + icl;
+        const float v = oc < out_ch ? dev::f16_bits_to_f32(weights[((size_t)oc * in_ch + ic) * 9 + tap]) : 0.0f;
+        const __bf16 hi = (__bf16)v;
+        const __bf16 lo = (__bf16)(v - (float)hi);
+        const size_t base = (((size_t)stage * 9 + tap) * 2) * oc_pad;
+        wprep[(base + oc) * kMfIc + icl] = __builtin_bit_cast(uint16_t, hi);
+        wprep[(base + oc_pad + oc) * kMfIc + icl] = __builtin_bit_cast(uint16_t, lo);
+    }
+}
+
+__global__ __launch_bounds__(256) void conv3x3s2_gelu_mfma_kernel(const ConvMfmaArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t patch_lds[];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const uint32_t oc0 = blockIdx.x * kMfOc + wave * 32;
+    const uint32_t p0 = blockIdx.y * kMfPos;
+    const uint32_t b = blockIdx.z;
+    const uint32_t cells = a.patch_rows * a.patch_cols;
+    const uint32_t term_elems = cells * kMfIcPad;          // one term of one buffer
+    const uint32_t r_first = p0 / a.ow;
+    const int in_r0 = 2 * (int)r_first - 1;                // input row of patch row 0
+    const float *in = a.in + (size_t)b * a.in_ch * a.h * a.w;
+    const uint32_t stages = a.in_ch / kMfIc;
+
+    // B operand: this lane's position (column lane % 32) and channel half.
+    uint32_t p = p0 + (lane & 31);
+    if (p >= a.positions) p = a.positions - 1;              // (never stored)
+    const uint32_t oh = p / a.ow, ow = p % a.ow;
+    const uint32_t cell0 = (2 * (oh - r_first)) * a.patch_cols + 2 * ow;   // + kh * cols + kw
+    const uint32_t kq = (lane >> 5) * 8;
+    // A operand: output channel oc0 + lane % 32, channels kq .. kq + 7.
+    const uint16_t *wl = a.wprep + (size_t)(oc0 + (lane & 31)) * kMfIc + kq;
+    const size_t wtap = (size_t)2 * a.oc_pad * kMfIc;      // elements per tap (both terms)
+    const size_t wterm = (size_t)a.oc_pad * kMfIc;
+
+    // Patch items: (channel half, row, col); a thread takes items
+    // t, t + 256, ... (kMfRounds at most; the host checks 2 * cells fits).
+    float stage_v[kMfRounds][8];
+    auto load_patch = [&](uint32_t stage) {
+#pragma unroll
+        for (int k = 0; k < kMfRounds; ++k) {
+            const uint32_t item = t + 256 * k;
+            const uint32_t half = item / cells, cell = item % cells;
+            const int r = in_r0 + (int)(cell / a.patch_cols);
+            const int c = (int)(cell % a.patch_cols) - 1;
+            const bool inside = half < 2 && r >= 0 && r < (int)a.h && c >= 0 && c < (int)a.w;
+            const int rr = r < 0 ? 0 : (r >= (int)a.h ? (int)a.h - 1 : r);
+            const int cc = c < 0 ? 0 : (c >= (int)a.w ? (int)a.w - 1 : c);
+            const uint32_t ic = stage * kMfIc + (half < 2 ? half : 0) * 8;
+            const float *src = in + ((size_t)ic * a.h + rr) * a.w + cc;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = src[(size_t)j * a.h * a.w];   // (unconditional: clamped inside the plane)
+                stage_v[k][j] = inside ? v : 0.0f;
+            }
+        }
+    };
+    auto store_patch = [&](int buf) {
+        uint16_t *hi_base = patch_lds + (size_t)buf * 2 * term_elems;
+        uint16_t *lo_base = hi_base + term_elems;
+#pragma unroll
+        for (int k = 0; k < kMfRounds; ++k) {
+            const uint32_t item = t + 256 * k;
+            if (item >= 2 * cells) break;
+            const uint32_t half = item / cells, cell = item % cells;
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float x0 = stage_v[k][2 * j], x1 = stage_v[k][2 * j + 1];
+                const cbf16x2 h2 = {(__bf16)x0, (__bf16)x1};
+                const cbf16x2 l2 = {(__bf16)(x0 - (float)h2[0]), (__bf16)(x1 - (float)h2[1])};
+                hw[j] = __builtin_bit_cast(uint32_t, h2);
+                lw[j] = __builtin_bit_cast(uint32_t, l2);
+            }
+            const size_t at = (size_t)cell * kMfIcPad + half * 8;
+            *reinterpret_cast<uint4 *>(hi_base + at) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            *reinterpret_cast<uint4 *>(lo_base + at) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
+    };
+    cbf16x8 wa[2][9][2];  // [stage buffer][tap][term]
+    auto load_weights = [&](uint32_t stage, int buf) {
+        const uint16_t *src = wl + (size_t)stage * 9 * wtap;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+            for (int term = 0; term < 2; ++term)
+                wa[buf][tap][term] = *reinterpret_cast<const cbf16x8 *>(src + tap * wtap + term * wterm);
+    };
+
+    cf32x16 acc = {}, acc2 = {};
+    // One stage: the next stage's values and weights are loaded (the last
+    // stage reloads its own: the loads stay unconditional), this stage is
+    // multiplied out of LDS buffer BUF, and the next stage's values go into
+    // the other buffer; every wavefront read that buffer in the previous
+    // stage, before the barrier that ended it.
+    auto stage_step = [&](uint32_t s, auto buf_tag) {
+        constexpr int BUF = decltype(buf_tag)::value;
+        const uint32_t nxt = s + 1 < stages ? s + 1 : s;
+        load_patch(nxt);
+        load_weights(nxt, BUF ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint16_t *hb = patch_lds + (size_t)BUF * 2 * term_elems;
+        const uint16_t *lb = hb + term_elems;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const uint32_t cell = cell0 + (tap / 3) * a.patch_cols + (tap % 3);
+            const cbf16x8 bh = *reinterpret_cast<const cbf16x8 *>(hb + (size_t)cell * kMfIcPad + kq);
+            const cbf16x8 bl = *reinterpret_cast<const cbf16x8 *>(lb + (size_t)cell * kMfIcPad + kq);
+            // (Two accumulators, so consecutive products do not wait on
+            // each other's results.)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][0], bh, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][0], bl, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][1], bh, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][1], bl, acc2, 0, 0, 0);
+        }
+        store_patch(BUF ^ 1);
+        __syncthreads();
+    };
+    load_patch(0);
+    load_weights(0, 0);
+    store_patch(0);
+    __syncthreads();
+    uint32_t s = 0;
+    for (; s + 1 < stages; s += 2) {
+        stage_step(s, std::integral_constant<int, 0>{});
+        stage_step(s + 1, std::integral_constant<int, 1>{});
+    }
+    if (s < stages) stage_step(s, std::integral_constant<int, 0>{});
+    // Value r of a lane: output channel row 8 (r / 4) + 4 (lane / 32) + r % 4
+    // of the wavefront's 32, position column lane % 32.
+    const uint32_t pos = p0 + (lane & 31);
+    if (pos >= a.positions) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t oc = oc0 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+        if (oc < a.out_ch)
+            a.out[((size_t)b * a.out_ch + oc) * a.positions + pos] = dev::gelu(a.bias[oc] + (acc[r] + acc2[r]));
+    }
+}
+
 // Chunks [first, first + count) of the log-mel [bins][frames] into
 // [count][bins][chunk_frames], frames past the clip zero (model.zig:557-563).
 __global__ void gather_chunks_kernel(const float *mel, uint32_t bins, uint32_t frames, uint32_t chunk_frames,
@@ -160,6 +354,55 @@ hipError_t launch_conv3x3s2_gelu(hipStream_t s, float *out, const float *in, con
     const uint32_t tiles_h = (a.oh + kTile - 1) / kTile;
     const dim3 grid((out_ch + kOcTile - 1) / kOcTile, tiles_h * a.tiles_w, batch);
     conv3x3s2_gelu_kernel<<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+namespace {
+
+// Patch rows for kMfPos positions starting anywhere in a row of `ow`.
+uint32_t mfma_patch_rows(uint32_t ow) { return 2 * ((kMfPos - 1 + ow - 1) / ow) + 3; }
+
+}  // namespace
+
+size_t conv_mfma_prep_bytes(uint32_t out_ch, uint32_t in_ch) {
+    const uint32_t oc_pad = (out_ch + kMfOc - 1) / kMfOc * kMfOc;
+    return (size_t)oc_pad * in_ch * 9 * 2 * sizeof(uint16_t);
+}
+
+bool conv_mfma_supported(uint32_t in_ch, uint32_t h, uint32_t w) {
+    if (in_ch == 0 || in_ch % kMfIc || h == 0 || w == 0) return false;
+    const uint32_t ow = (w - 1) / 2 + 1;
+    const uint64_t cells = (uint64_t)mfma_patch_rows(ow) * (w + 2);
+    // Two channel halves per cell in kMfRounds rounds of 256 threads; two
+    // buffers of two terms in LDS.
+    return 2 * cells <= 256u * kMfRounds && cells * kMfIcPad * 2 * 2 * sizeof(uint16_t) <= kMfLdsMax;
+}
+
+hipError_t launch_conv_mfma_prep(hipStream_t s, const uint16_t *weights, uint32_t out_ch, uint32_t in_ch, void *wprep) {
+    const uint32_t oc_pad = (out_ch + kMfOc - 1) / kMfOc * kMfOc;
+    conv_mfma_prep_kernel<<<blocks_for((uint64_t)oc_pad * in_ch * 9), 256, 0, s>>>(weights, out_ch, oc_pad, in_ch,
+                                                                                   static_cast<uint16_t *>(wprep));
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3x3s2_gelu_mfma(hipStream_t s, float *out, const float *in, const void *wprep, const float *bias,
+                                     uint32_t batch, uint32_t out_ch, uint32_t in_ch, uint32_t h, uint32_t w) {
+    if (!conv_mfma_supported(in_ch, h, w) || batch == 0 || batch > 65535) return hipErrorInvalidValue;
+    ConvMfmaArgs a{};
+    a.out = out, a.in = in, a.wprep = static_cast<const uint16_t *>(wprep), a.bias = bias;
+    a.out_ch = out_ch, a.oc_pad = (out_ch + kMfOc - 1) / kMfOc * kMfOc, a.in_ch = in_ch, a.h = h, a.w = w;
+    a.oh = (h - 1) / 2 + 1, a.ow = (w - 1) / 2 + 1;
+    a.positions = a.oh * a.ow;
+    a.patch_rows = mfma_patch_rows(a.ow);
+    a.patch_cols = w + 2;
+    const size_t lds = (size_t)a.patch_rows * a.patch_cols * kMfIcPad * 2 * 2 * sizeof(uint16_t);
+    // (Above the default 64 KB of dynamic LDS: raised once, to the most any
+    // supported shape asks for.)
+    static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void *>(&conv3x3s2_gelu_mfma_kernel),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfLdsMax);
+    if (raised != hipSuccess) return raised;
+    const dim3 grid(a.oc_pad / kMfOc, (a.positions + kMfPos - 1) / kMfPos, batch);
+    conv3x3s2_gelu_mfma_kernel<<<grid, 256, lds, s>>>(a);
     return hipGetLastError();
 }
 

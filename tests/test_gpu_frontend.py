@@ -58,6 +58,14 @@ def test_conv_known_answers(ctx):
     (3, 70, 13, 17, 9),       # channel counts off the tiles, odd planes
     (1, 5, 3, 1, 1),          # a single input position
     (2, 65, 9, 2, 31),
+    # The matrix-core form (input channels a multiple of 16): output
+    # channels and positions off its 128 x 32 tiles, a one-row output, a
+    # two-column output (a 32-position tile spans 16 output rows), and a
+    # plane too wide for its LDS patch (the f32 kernel).
+    (3, 70, 16, 17, 9),
+    (2, 130, 32, 2, 31),
+    (1, 200, 48, 40, 3),
+    (1, 8, 16, 4, 300),
 ])
 def test_conv_against_oracle(ctx, batch, cout, cin, h, w):
     x = normal(batch * cin * h * w, 71, cin)
