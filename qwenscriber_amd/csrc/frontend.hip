@@ -117,21 +117,25 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_kernel(const ConvArgs a) {
 // f32: within 2^-17 of the f32 convolution per term, no overflow range of its
 // own (bf16 has f32's exponent range).
 //
-// Workgroup: 128 output channels (four wavefronts of 32) x 32 positions. Per
-// stage the 32 positions' input rows (at most 2 * ceil(31 / ow) + 3 of them,
-// zero padding included) x 16 channels go into LDS as [row][col][channel]
-// (channel padded to 24 for the reads' banks) in both terms, double buffered,
-// the next stage's values loaded into registers while this one multiplies.
-// Weights come prepared [stage][tap][term][oc][16] (conv_mfma_prep_kernel)
-// and each wavefront loads its 32 rows' 18 operands one stage ahead.
+// Workgroup: 128 output channels (four wavefronts of 32) x 64 positions (two
+// 32-column MFMA tiles per wavefront, so each weight operand serves both).
+// Per stage the 64 positions' input rows (at most 2 * ceil(63 / ow) + 3 of
+// them, zero padding included) x 16 channels go into LDS as
+// [row][col][channel] in both terms, double buffered, the next stage's values
+// loaded into registers while this one multiplies. Weights come prepared
+// [stage][tap][term][oc][16] (conv_mfma_prep_kernel) and each wavefront loads
+// its 32 rows' 18 operands one stage ahead. (32-position workgroups measured
+// 1.33 ms for the 30 s front end against 1.15 ms: every position tile reads
+// the weights again.)
 typedef __bf16 cbf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 cbf16x2 __attribute__((ext_vector_type(2)));
 typedef float cf32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMfOc = 128;       // output channels per workgroup
-constexpr int kMfPos = 32;       // output positions per workgroup
+constexpr int kMfPos = 64;       // output positions per workgroup (two 32-column MFMA tiles)
+constexpr int kMfNt = kMfPos / 32;
 constexpr int kMfIc = 16;        // input channels per stage
-constexpr int kMfIcPad = 24;     // channel stride of a patch cell (bf16)
+constexpr int kMfIcPad = 16;     // channel stride of a patch cell (bf16)
 constexpr int kMfRounds = 4;     // patch items per thread at most (256 threads)
 constexpr size_t kMfLdsMax = 80 * 1024;  // the patch buffers' LDS, two workgroups per CU
 
@@ -180,10 +184,14 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_mfma_kernel(const ConvMfma
     const uint32_t stages = a.in_ch / kMfIc;
 
     // B operand: this lane's position (column lane % 32) and channel half.
-    uint32_t p = p0 + (lane & 31);
-    if (p >= a.positions) p = a.positions - 1;              // (never stored)
-    const uint32_t oh = p / a.ow, ow = p % a.ow;
-    const uint32_t cell0 = (2 * (oh - r_first)) * a.patch_cols + 2 * ow;   // + kh * cols + kw
+    uint32_t cell0[kMfNt];
+#pragma unroll
+    for (int j = 0; j < kMfNt; ++j) {
+        uint32_t p = p0 + 32 * j + (lane & 31);
+        if (p >= a.positions) p = a.positions - 1;              // (never stored)
+        const uint32_t oh = p / a.ow, ow = p % a.ow;
+        cell0[j] = (2 * (oh - r_first)) * a.patch_cols + 2 * ow;   // + kh * cols + kw
+    }
     const uint32_t kq = (lane >> 5) * 8;
     // A operand: output channel oc0 + lane % 32, channels kq .. kq + 7.
     const uint16_t *wl = a.wprep + (size_t)(oc0 + (lane & 31)) * kMfIc + kq;
@@ -244,7 +252,7 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_mfma_kernel(const ConvMfma
                 wa[buf][tap][term] = *reinterpret_cast<const cbf16x8 *>(src + tap * wtap + term * wterm);
     };
 
-    cf32x16 acc = {}, acc2 = {};
+    cf32x16 acc[kMfNt] = {}, acc2[kMfNt] = {};
     // One stage: the next stage's values and weights are loaded (the last
     // stage reloads its own: the loads stay unconditional), this stage is
     // multiplied out of LDS buffer BUF, and the next stage's values go into
@@ -260,15 +268,18 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_mfma_kernel(const ConvMfma
         const uint16_t *lb = hb + term_elems;
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap) {
-            const uint32_t cell = cell0 + (tap / 3) * a.patch_cols + (tap % 3);
-            const cbf16x8 bh = *reinterpret_cast<const cbf16x8 *>(hb + (size_t)cell * kMfIcPad + kq);
-            const cbf16x8 bl = *reinterpret_cast<const cbf16x8 *>(lb + (size_t)cell * kMfIcPad + kq);
-            // (Two accumulators, so consecutive products do not wait on
-            // each other's results.)
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][0], bh, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][0], bl, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][1], bh, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][1], bl, acc2, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < kMfNt; ++j) {
+                const uint32_t cell = cell0[j] + (tap / 3) * a.patch_cols + (tap % 3);
+                const cbf16x8 bh = *reinterpret_cast<const cbf16x8 *>(hb + (size_t)cell * kMfIcPad + kq);
+                const cbf16x8 bl = *reinterpret_cast<const cbf16x8 *>(lb + (size_t)cell * kMfIcPad + kq);
+                // (Two accumulators, so consecutive products do not wait on
+                // each other's results.)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][0], bh, acc[j], 0, 0, 0);
+                acc2[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][0], bl, acc2[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][1], bh, acc[j], 0, 0, 0);
+                acc2[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[BUF][tap][1], bl, acc2[j], 0, 0, 0);
+            }
         }
         store_patch(BUF ^ 1);
         __syncthreads();
@@ -285,13 +296,17 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_mfma_kernel(const ConvMfma
     if (s < stages) stage_step(s, std::integral_constant<int, 0>{});
     // Value r of a lane: output channel row 8 (r / 4) + 4 (lane / 32) + r % 4
     // of the wavefront's 32, position column lane % 32.
-    const uint32_t pos = p0 + (lane & 31);
-    if (pos >= a.positions) return;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const uint32_t oc = oc0 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-        if (oc < a.out_ch)
-            a.out[((size_t)b * a.out_ch + oc) * a.positions + pos] = dev::gelu(a.bias[oc] + (acc[r] + acc2[r]));
+    for (int j = 0; j < kMfNt; ++j) {
+        const uint32_t pos = p0 + 32 * j + (lane & 31);
+        if (pos >= a.positions) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t oc = oc0 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+            if (oc < a.out_ch)
+                a.out[((size_t)b * a.out_ch + oc) * a.positions + pos] =
+                    dev::gelu(a.bias[oc] + (acc[j][r] + acc2[j][r]));
+        }
     }
 }
 
