@@ -310,6 +310,48 @@ __global__ __launch_bounds__(256) void conv3x3s2_gelu_mfma_kernel(const ConvMfma
     }
 }
 
+// One input channel (conv1 of the tower, on the log-mel): each thread takes
+// one output position of one image and a range of output channels; its nine
+// input samples are read once, each output is bias + the taps in the
+// reference's order (rows, then columns; taps outside the plane skipped),
+// then GELU. Stores are coalesced over positions.
+constexpr uint32_t kC1Oc = 64;   // output channels per workgroup column
+__global__ __launch_bounds__(256) void conv1_gelu_kernel(const ConvArgs a) {
+    __shared__ float wts[kC1Oc][9];
+    __shared__ float bs[kC1Oc];
+    const uint32_t t = threadIdx.x;
+    const uint32_t oc0 = blockIdx.y * kC1Oc;
+    const uint32_t b = blockIdx.z;
+    const uint32_t positions = a.oh * a.ow;
+    const uint32_t p = blockIdx.x * 256 + t;
+    for (uint32_t i = t; i < kC1Oc * 9; i += 256) {
+        const uint32_t oc = oc0 + i / 9;
+        wts[i / 9][i % 9] = oc < a.out_ch ? dev::f16_bits_to_f32(a.weights[(size_t)oc * 9 + i % 9]) : 0.0f;
+    }
+    if (t < kC1Oc) bs[t] = oc0 + t < a.out_ch ? a.bias[oc0 + t] : 0.0f;
+    __syncthreads();
+    if (p >= positions) return;
+    const uint32_t orow = p / a.ow, ocol = p % a.ow;
+    const float *in = a.in + (size_t)b * a.h * a.w;
+    float x[9];
+    bool ok[9];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+        const int r = (int)orow * 2 + tap / 3 - 1, c = (int)ocol * 2 + tap % 3 - 1;
+        ok[tap] = r >= 0 && r < (int)a.h && c >= 0 && c < (int)a.w;
+        x[tap] = ok[tap] ? in[(size_t)r * a.w + c] : 0.0f;
+    }
+    const uint32_t end = a.out_ch - oc0 < kC1Oc ? a.out_ch - oc0 : kC1Oc;
+    float *out = a.out + ((size_t)b * a.out_ch + oc0) * positions + p;
+    for (uint32_t k = 0; k < end; ++k) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+            if (ok[tap]) acc = fmaf(wts[k][tap], x[tap], acc);
+        out[(size_t)k * positions] = dev::gelu(bs[k] + acc);
+    }
+}
+
 // Chunks [first, first + count) of the log-mel [bins][frames] into
 // [count][bins][chunk_frames], frames past the clip zero (model.zig:557-563).
 __global__ void gather_chunks_kernel(const float *mel, uint32_t bins, uint32_t frames, uint32_t chunk_frames,
@@ -367,6 +409,11 @@ hipError_t launch_conv3x3s2_gelu(hipStream_t s, float *out, const float *in, con
     a.oh = (h - 1) / 2 + 1, a.ow = (w - 1) / 2 + 1;
     a.tiles_w = (a.ow + kTile - 1) / kTile;
     const uint32_t tiles_h = (a.oh + kTile - 1) / kTile;
+    if (in_ch == 1) {
+        const dim3 grid1((a.oh * a.ow + 255) / 256, (out_ch + kC1Oc - 1) / kC1Oc, batch);
+        conv1_gelu_kernel<<<grid1, 256, 0, s>>>(a);
+        return hipGetLastError();
+    }
     const dim3 grid((out_ch + kOcTile - 1) / kOcTile, tiles_h * a.tiles_w, batch);
     conv3x3s2_gelu_kernel<<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
