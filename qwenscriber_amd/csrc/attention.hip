@@ -537,14 +537,14 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         }
     };
 
-    // The first tile is loaded before the sequence's position is known (in
-    // the decoder it is a device value, one memory round trip away): every
-    // allocated row is readable, and rows past the position are dropped once
-    // it has arrived. The query slices and norm weights do not depend on it
-    // either. Lane group r < R of wavefront 0 takes query head r.
-    Tile cur, nxt;
-    load_tile(cur, begin, a.rows);
-    if constexpr (Early) load_tile(nxt, begin + kSpan, a.rows);
+    // The query slices, norm weights and RoPE row are requested first and the
+    // first tile right after them, before the sequence's position is known
+    // (in the decoder it is a device value, one memory round trip away):
+    // every allocated row is readable, and rows past the position are
+    // dropped once it has arrived. Loads complete in issue order, so the
+    // query prologue waits only for its own values while the tile is in
+    // flight (tile first measured 1-3 % slower at batch 1). Lane group r < R
+    // of wavefront 0 takes query head r.
     const bool prologue = wave == 0 && group < R;
     const int qh = prologue ? group : 0;
     const float *row = a.query + (size_t)b * a.query_stride;
@@ -557,6 +557,9 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         load16(a.rope_now + (size_t)b * D + j0, rc);
         load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
     }
+    Tile cur, nxt;
+    load_tile(cur, begin, a.rows);
+    if constexpr (Early) load_tile(nxt, begin + kSpan, a.rows);
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
     // The decoder form leaves the newest row (cached - 1) to the merge kernel.
     const uint32_t attended = Decoder ? cached - 1 : cached;
