@@ -63,7 +63,38 @@ struct AttnKernelArgs {
     // Optional digit-plane copy of the output (small-batch GEMV layout).
     uint8_t *digits;
     float *digit_mult;
+    // Query rows as a K-split GEMV's partial sums (query_slices > 1): the
+    // planes are query_plane floats apart and are summed in slice order.
+    uint32_t query_slices;
+    uint64_t query_plane;
 };
+
+constexpr uint32_t kMaxQuerySlices = 8;
+
+// The partial values of query-row element `off`, one per slice (loads for
+// slices past the count repeat the last one: they stay unconditional).
+__device__ __forceinline__ void query_parts(const AttnKernelArgs &a, size_t off, float (&w)[kMaxQuerySlices]) {
+#pragma unroll
+    for (uint32_t s = 0; s < kMaxQuerySlices; ++s)
+        w[s] = a.query[(size_t)(s < a.query_slices ? s : a.query_slices - 1) * a.query_plane + off];
+}
+
+// Their sum in slice order (the order of the GEMV's own slice reduce).
+__device__ __forceinline__ float query_sum(const AttnKernelArgs &a, const float (&w)[kMaxQuerySlices]) {
+    float v = w[0];
+#pragma unroll
+    for (uint32_t s = 1; s < kMaxQuerySlices; ++s)
+        if (s < a.query_slices) v += w[s];
+    return v;
+}
+
+// Element `off` of the query rows.
+__device__ __forceinline__ float query_value(const AttnKernelArgs &a, size_t off) {
+    if (a.query_slices <= 1) return a.query[off];
+    float w[kMaxQuerySlices];
+    query_parts(a, off, w);
+    return query_sum(a, w);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -549,7 +580,20 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     const int qh = prologue ? group : 0;
     const float *row = a.query + (size_t)b * a.query_stride;
     float q[16];
-    load16(row + (kvh * R + qh) * D + sub * 16, q);
+    // Sliced query rows: the workgroup sums the R heads' values, QP per
+    // thread, into LDS once the tile loads are out.
+    constexpr int QP = (R * D + 255) / 256;
+    const bool sliced = a.query_slices > 1;
+    float qparts[QP][kMaxQuerySlices];
+    if (sliced) {
+#pragma unroll
+        for (int i = 0; i < QP; ++i) {
+            const uint32_t idx = threadIdx.x + 256 * i < (uint32_t)(R * D) ? threadIdx.x + 256 * i : 0;
+            query_parts(a, (size_t)b * a.query_stride + kvh * R * D + idx, qparts[i]);
+        }
+    } else {
+        load16(row + (kvh * R + qh) * D + sub * 16, q);
+    }
     float wq[16], rc[16], rs[16];
     if (Decoder) {
         const int j0 = (sub % (LPP / 2)) * 16;
@@ -560,6 +604,15 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     Tile cur, nxt;
     load_tile(cur, begin, a.rows);
     if constexpr (Early) load_tile(nxt, begin + kSpan, a.rows);
+    if (sliced) {
+#pragma unroll
+        for (int i = 0; i < QP; ++i)
+            if (threadIdx.x + 256 * i < (uint32_t)(R * D))
+                (&lds_q[0][0])[threadIdx.x + 256 * i] = query_sum(a, qparts[i]);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = lds_q[qh][sub * 16 + i];
+    }
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
     // The decoder form leaves the newest row (cached - 1) to the merge kernel.
     const uint32_t attended = Decoder ? cached - 1 : cached;
@@ -837,8 +890,20 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(const AttnKernelArgs
     load_block(cur, begin, a.rows);
     const float *row = a.query + (size_t)b * a.query_stride;
     float q[R][16];
+    if (a.query_slices > 1) {
+        // Sliced query rows: summed by the workgroup into LDS first.
+        __shared__ float lds_q32[R * D];
+        for (uint32_t idx = threadIdx.x; idx < (uint32_t)(R * D); idx += blockDim.x)
+            lds_q32[idx] = query_value(a, (size_t)b * a.query_stride + kvh * R * D + idx);
+        __syncthreads();
 #pragma unroll
-    for (int r = 0; r < R; ++r) load16(row + (kvh * R + r) * D + sub * 16, q[r]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[r][i] = lds_q32[r * D + sub * 16 + i];
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) load16(row + (kvh * R + r) * D + sub * 16, q[r]);
+    }
     float wq[16], rc[16], rs[16];
     if (Decoder) {
         const int j0 = (sub % (LPP / 2)) * 16;
@@ -975,12 +1040,12 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
         v[q] = *reinterpret_cast<const float4 *>(rec + r * D + 4 * col);
     }
     const uint32_t kv_width = a.kv_heads * D;
-    const float *row = a.query + (size_t)b * a.query_stride;
     float qx = 0.0f, kx = 0.0f, vx = 0.0f, wq = 0.0f, wk = 0.0f, rope_c = 0.0f, rope_s = 0.0f;
     if (Decoder && t < D) {
-        qx = row[h * D + t];
-        kx = row[a.heads * D + kvh * D + t];
-        vx = row[a.heads * D + kv_width + kvh * D + t];
+        const size_t base = (size_t)b * a.query_stride;
+        qx = query_value(a, base + h * D + t);
+        kx = query_value(a, base + a.heads * D + kvh * D + t);
+        vx = query_value(a, base + a.heads * D + kv_width + kvh * D + t);
         wq = a.q_norm[t];
         wk = a.k_norm[t];
         rope_c = a.rope_now[(size_t)b * D + (t % (D / 2))];
@@ -1216,6 +1281,9 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
     AttnKernelArgs k{};
     k.query = a.query;
     k.query_stride = a.query_stride ? a.query_stride : a.heads * a.head_dim;
+    if (a.query_slices > kMaxQuerySlices) return hipErrorInvalidValue;
+    k.query_slices = a.query_slices;
+    k.query_plane = a.query_plane;
     k.k_scales = a.k_scales;
     k.k_codes = a.k_codes;
     k.v_scales = a.v_scales;

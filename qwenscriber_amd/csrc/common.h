@@ -219,6 +219,11 @@ struct AttentionArgs {
     // digit planes (launch_prep_batch's layout for batch rows of heads *
     // head_dim values), so the output projection needs no separate pass.
     void *digits = nullptr;
+    // Optional: the query rows as a K-split GEMV's partial sums (the decoder
+    // form's q | k | v projection): query_slices (at most 8) planes of rows,
+    // query_plane floats apart, added in slice order as its reduce would.
+    uint32_t query_slices = 0;
+    uint64_t query_plane = 0;
 };
 bool attention_supported(uint32_t head_dim, uint32_t ratio);
 // argmaxLogits (decoder.zig:290-301) of `rows` rows of `count` logits into

@@ -361,7 +361,7 @@ struct qwh_decoder {
     // sums here and the prep that follows adds them (q|k|v reduces its own).
     float *parts = nullptr;
     bool split_parts = false;
-    uint32_t slices_o = 0, slices_gu = 0, slices_down = 0;
+    uint32_t slices_o = 0, slices_gu = 0, slices_down = 0, slices_qkv = 0;
 };
 
 namespace qwh {
@@ -462,9 +462,10 @@ int32_t plan_step(qwh_decoder *d) {
     d->fused = q4_fused;
     d->batched = batch_form;
     d->split_parts = false;
-    d->slices_o = d->slices_gu = d->slices_down = 0;
+    d->slices_o = d->slices_gu = d->slices_down = d->slices_qkv = 0;
     if (d->batched) {
         const qwh_decoder::Layer &L0 = d->layers[0];
+        d->slices_qkv = batch_slices(L0.qkv);
         d->slices_o = batch_slices(L0.o);
         d->slices_gu = batch_slices(L0.gu);
         d->slices_down = batch_slices(L0.down);
@@ -531,7 +532,25 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
                                    c.head_dim / 2, d->rope_now, d->rows_dev, d->row_flags_dev);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
-        err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
+        // Batched with a K split: q | k | v stay partial sums, added by the
+        // attention kernels as they read them (no reduce launch).
+        const bool qkv_parts = d->batched && d->slices_qkv > 1 && d->parts;
+        if (qkv_parts) {
+            GemvInput in;
+            in.mode = GemvInput::RmsNorm;
+            in.x = d->hidden;
+            in.norm = L.attn_norm;
+            in.eps = c.eps;
+            err = launch_prep_batch(s, in, B, c.hidden, d->batch_digits, &pending);
+            pending = PartialSums{};
+            if (err != hipSuccess) break;
+            BatchNorm bn;
+            bn.rms = true;
+            bn.eps = c.eps;
+            err = launch_gemv_batch_parts(s, d->batch_digits, L.qkv, B, d->parts, bn);
+        } else {
+            err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
+        }
         if (err != hipSuccess) break;
         // Per-head norms, RoPE, the cache append and the attention itself
         // (decoder.zig:180-253) in one launch.
@@ -539,8 +558,12 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         uint8_t *vl = d->values + (size_t)l * d->layer_stride;
         AttentionArgs aa{};
         aa.out = d->attn;
-        aa.query = d->qkv;
+        aa.query = qkv_parts ? d->parts : d->qkv;
         aa.query_stride = d->qw + 2 * d->kvw;
+        if (qkv_parts) {
+            aa.query_slices = d->slices_qkv;
+            aa.query_plane = (uint64_t)B * (d->qw + 2 * d->kvw);
+        }
         aa.q_norm = L.q_norm;
         aa.k_norm = L.k_norm;
         aa.rope_now = d->rope_now;
