@@ -482,6 +482,23 @@ int32_t qwh_decoder_forward(qwh_decoder *decoder, const uint32_t *tokens, int32_
  * sequence advances one position; logits are kept when want_logits. */
 int32_t qwh_decoder_forward_rows(qwh_decoder *decoder, const uint32_t *tokens, const float *rows_dev,
                                  const uint8_t *row_mask, int32_t want_logits);
+/* decoder.zig:308-333 Decoder.prefill for sequence `seq`: its `count`
+ * prompt tokens (host array) at positions position(seq) .. + count - 1, each
+ * audio_pad_token taking the next of audio_steps projected audio rows
+ * (audio_rows_dev: audio_steps x hidden f32, device) in place of its
+ * embedding; every position's key and value rows are appended to the cache,
+ * the sequence's position advances by count, and *next_token receives the
+ * greedy token after the prompt (argmaxLogits of its last position; those
+ * logits stay on the device). An empty prompt, or audio pads that do not
+ * match audio_steps, give QWH_E_SHAPE_MISMATCH (the reference's
+ * UnexpectedShape / PromptMismatch). The positions are processed together,
+ * in chunks of 256: each layer's products run over all of them, their cache
+ * rows are appended, then each attends to the cache rows up to its own.
+ * Needs a matrix-core form of every layer matrix (QWH_E_UNSUPPORTED
+ * otherwise: use qwh_decoder_forward_rows per position). */
+int32_t qwh_decoder_prefill(qwh_decoder *decoder, uint32_t seq, const uint32_t *tokens, uint32_t count,
+                            uint32_t audio_pad_token, const float *audio_rows_dev, uint32_t audio_steps,
+                            uint32_t *next_token);
 /* decoder.zig:336-339 step: forwardToken then argmaxLogits (:290-301, first
  * maximum wins) for every sequence; next_tokens receives batch ids. */
 int32_t qwh_decoder_step(qwh_decoder *decoder, const uint32_t *tokens, uint32_t *next_tokens);

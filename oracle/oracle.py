@@ -112,6 +112,8 @@ _SIGNATURES = {
     "qwref_decoder_weights_hash": (_U64, [_P]),
     "qwref_decoder_cache_hash": (_U64, [_P, _U32]),
     "qwref_decoder_cache_row": (_U64, [_P, _U32, _U32, _U32, _P, _U64]),
+    "qwref_decoder_set_cache_row": (_I32, [_P, _U32, _U32, _U32, _P, _U64]),
+    "qwref_decoder_set_position": (_I32, [_P, _U32, _U32]),
     "qwref_synthetic_start_token": (_U32, [_U32, _U32, _U32]),
     "qwref_set_threads": (None, [_I32]),
     "qwref_erf": (ctypes.c_float, [ctypes.c_float]),
@@ -389,6 +391,19 @@ class Decoder:
         if n == 0:
             raise ValueError("cache_row: bad argument")
         return out[:n].tobytes()
+
+    def set_cache_row(self, seq: int, layer: int, position: int, row) -> None:
+        """Stores a row in cache_row's layout (test plumbing: the next
+        forward reads exactly these bytes)."""
+        buf = np.ascontiguousarray(np.frombuffer(bytes(row), np.uint8))
+        status = lib().qwref_decoder_set_cache_row(self.handle, seq, layer, position, buf.ctypes.data, buf.size)
+        if status != 0:
+            raise ValueError(f"set_cache_row status {status}")
+
+    def set_position(self, seq: int, position: int) -> None:
+        status = lib().qwref_decoder_set_position(self.handle, seq, position)
+        if status != 0:
+            raise ValueError(f"set_position status {status}")
 
 
 def start_token(seed: int, seq: int, vocab: int) -> int:

@@ -1285,6 +1285,44 @@ uint64_t qwref_decoder_cache_row(qwref_decoder *d, uint32_t seq, uint32_t layer,
     return 2 * (scale_bytes + kvw);
 }
 
+/* The inverse of qwref_decoder_cache_row: stores `len` bytes in that layout
+ * as the row `position` of a layer. Test plumbing (no decoder.zig
+ * counterpart): a checker writes another implementation's cache rows here,
+ * so the next forward reads exactly those rows. Returns 0, or
+ * QWREF_INVALID_ARGUMENT for a bad argument or a wrong length. */
+int32_t qwref_decoder_set_cache_row(qwref_decoder *d, uint32_t seq, uint32_t layer, uint32_t position,
+                                    const uint8_t *row, uint64_t len) {
+    if (seq >= d->batch || layer >= d->c.layers || position >= d->c.max_positions) return QWREF_INVALID_ARGUMENT;
+    const uint32_t kvw = d->c.kv_heads * d->c.head_dim;
+    const size_t layer_offset = (size_t)layer * d->cache_stride;
+    sequence_state *s = &d->seqs[seq];
+    if (d->cache_format == QWREF_CACHE_F32) {
+        const size_t bytes = (size_t)kvw * sizeof(float);
+        if (len != 2 * bytes) return QWREF_INVALID_ARGUMENT;
+        memcpy(s->keys + layer_offset + (size_t)position * bytes, row, bytes);
+        memcpy(s->values + layer_offset + (size_t)position * bytes, row + bytes, bytes);
+        return QWREF_OK;
+    }
+    const size_t scale_bytes = (size_t)(kvw / QWREF_GROUP) * 2u;
+    if (len != 2 * (scale_bytes + kvw)) return QWREF_INVALID_ARGUMENT;
+    uint8_t *planes[2] = {s->keys, s->values};
+    for (int kv = 0; kv < 2; ++kv) {
+        const uint8_t *src = row + kv * (scale_bytes + kvw);
+        memcpy(planes[kv] + layer_offset + (size_t)position * scale_bytes, src, scale_bytes);
+        memcpy(planes[kv] + layer_offset + d->cache_scales + (size_t)position * kvw, src + scale_bytes, kvw);
+    }
+    return QWREF_OK;
+}
+
+/* Sets a sequence's position (the next forward writes cache row `position`
+ * and attends to the rows below it). Test plumbing, as above. */
+int32_t qwref_decoder_set_position(qwref_decoder *d, uint32_t seq, uint32_t position) {
+    if (seq >= d->batch) return QWREF_INVALID_ARGUMENT;
+    if (position > d->c.max_positions) return QWREF_LIMIT_EXCEEDED;
+    d->seqs[seq].position = position;
+    return QWREF_OK;
+}
+
 uint64_t qwref_decoder_cache_hash(qwref_decoder *d, uint32_t seq) {
     if (seq >= d->batch) return 0;
     uint64_t h = 0xcbf29ce484222325ull;

@@ -213,6 +213,11 @@ uint64_t qwref_decoder_cache_hash(qwref_decoder *decoder, uint32_t seq);
  * key row, value row); returns the bytes written, 0 on a bad argument. */
 uint64_t qwref_decoder_cache_row(qwref_decoder *decoder, uint32_t seq, uint32_t layer, uint32_t position,
                                  uint8_t *out, uint64_t capacity);
+/* Test plumbing: store a row in the cache_row layout (0, or
+ * QWREF_INVALID_ARGUMENT), and set a sequence's position. */
+int32_t qwref_decoder_set_cache_row(qwref_decoder *decoder, uint32_t seq, uint32_t layer, uint32_t position,
+                                    const uint8_t *row, uint64_t len);
+int32_t qwref_decoder_set_position(qwref_decoder *decoder, uint32_t seq, uint32_t position);
 uint32_t qwref_synthetic_start_token(uint32_t seed, uint32_t seq, uint32_t vocab);
 
 void qwref_set_threads(int32_t threads);

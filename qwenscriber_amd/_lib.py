@@ -173,6 +173,7 @@ SIGNATURES = {
     "qwh_decoder_set_position": (_I32, [_P, _U32, _U32]),
     "qwh_decoder_forward": (_I32, [_P, _P, _I32]),
     "qwh_decoder_forward_rows": (_I32, [_P, _P, _P, _P, _I32]),
+    "qwh_decoder_prefill": (_I32, [_P, _U32, _P, _U32, _U32, _P, _U32, _P]),
     "qwh_decoder_step": (_I32, [_P, _P, _P]),
     "qwh_decoder_generate": (_I32, [_P, _P, _U32, _P]),
     "qwh_decoder_logits": (_I32, [_P, _U32, _P, _U32]),
@@ -572,6 +573,17 @@ class Decoder:
         m = None if mask is None else np.ascontiguousarray(np.asarray(mask, bool).astype(np.uint8))
         self._check(self.ctx.lib.qwh_decoder_forward_rows(self.handle, _ptr(tokens), rows_dev,
                                                           None if m is None else _ptr(m), int(want_logits)))
+
+    def prefill(self, seq: int, tokens, audio_pad: int = 0xFFFFFFFF, audio_rows_dev: int = 0,
+                audio_steps: int = 0) -> int:
+        """Decoder.prefill (decoder.zig:308-333) of one sequence: the prompt
+        tokens, audio pads taking the device audio rows in order; returns the
+        greedy next token."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        out = np.zeros(1, np.uint32)
+        self._check(self.ctx.lib.qwh_decoder_prefill(self.handle, seq, _ptr(tokens), tokens.size, audio_pad,
+                                                     audio_rows_dev or None, audio_steps, _ptr(out)))
+        return int(out[0])
 
     def step(self, tokens) -> np.ndarray:
         tokens = np.ascontiguousarray(tokens, np.uint32)

@@ -67,6 +67,9 @@ struct AttnKernelArgs {
     // planes are query_plane floats apart and are summed in slice order.
     uint32_t query_slices;
     uint64_t query_plane;
+    // Decoder form with the newest row already in the cache (a prefill):
+    // the range kernels attend to it like any other row.
+    uint32_t attend_newest;
 };
 
 constexpr uint32_t kMaxQuerySlices = 8;
@@ -615,7 +618,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     }
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
     // The decoder form leaves the newest row (cached - 1) to the merge kernel.
-    const uint32_t attended = Decoder ? cached - 1 : cached;
+    const uint32_t attended = Decoder && !a.attend_newest ? cached - 1 : cached;
     uint32_t end = begin + a.chunk;
     if (end > attended) end = attended;
 
@@ -912,7 +915,7 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(const AttnKernelArgs
         load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
     }
     const uint32_t cached = a.cached_dev ? a.cached_dev[b] + a.cached_bias : a.cached;
-    const uint32_t attended = Decoder ? cached - 1 : cached;
+    const uint32_t attended = Decoder && !a.attend_newest ? cached - 1 : cached;
     uint32_t end = begin + a.chunk;
     if (end > attended) end = attended;
     if (begin >= cached) return;
@@ -1153,6 +1156,55 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnKernel
     }
 }
 
+// decoder.zig:180-216 and :77-105 for a run of new positions of one
+// sequence (a prefill): for position i and kv head blockIdx.x, the key row
+// (from the q | k | v rows, or the sum of their K-slice partials) gets
+// RMSNorm and RoPE at its position (rope row i), and the key and value rows
+// are stored at cache row first + i -- q8 per 64-value group (one wavefront
+// per group), or as they are in an f32 cache. The arithmetic of the step's
+// merge kernel, one thread per dimension.
+template <int D, bool F32C>
+__global__ __launch_bounds__(D) void prefill_append_kernel(const AttnKernelArgs a, uint32_t first) {
+    const uint32_t kvh = blockIdx.x;
+    const uint32_t i = blockIdx.y;
+    const int t = threadIdx.x;
+    const uint32_t kv_width = a.kv_heads * D;
+    const size_t base = (size_t)i * a.query_stride;
+    const float kx = query_value(a, base + a.heads * D + kvh * D + t);
+    const float vx = query_value(a, base + a.heads * D + kv_width + kvh * D + t);
+    const float wk = a.k_norm[t];
+    const float rope_c = a.rope_now[(size_t)i * D + (t % (D / 2))];
+    const float rope_s = a.rope_now[(size_t)i * D + D / 2 + (t % (D / 2))];
+    __shared__ float lds_k[D];
+    __shared__ float lds_sum[D / 64];
+    const float ssk = head_sum<D>(__fmul_rn(kx, kx), lds_sum);
+    const float inv_k = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssk, (float)D), a.eps)));
+    lds_k[t] = __fmul_rn(__fmul_rn(kx, inv_k), wk);
+    __syncthreads();
+    const int half = D / 2;
+    const float kn = lds_k[t], kp = lds_k[t ^ half];
+    const float kr = t < half ? __fsub_rn(__fmul_rn(kn, rope_c), __fmul_rn(kp, rope_s))
+                              : __fadd_rn(__fmul_rn(kn, rope_c), __fmul_rn(kp, rope_s));
+    const uint32_t row = first + i;
+    const size_t pos_codes = (size_t)row * kv_width + kvh * D + t;
+    if constexpr (F32C) {
+        reinterpret_cast<float *>(a.k_codes)[pos_codes] = kr;
+        reinterpret_cast<float *>(a.v_codes)[pos_codes] = vx;
+    } else {
+        const uint16_t kbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(kr)), 128.0f));
+        const uint16_t vbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(vx)), 128.0f));
+        const int ck = dev::quantize_one(kr, dev::f16_bits_to_f32(kbits), -128, 127);
+        const int cv = dev::quantize_one(vx, dev::f16_bits_to_f32(vbits), -128, 127);
+        a.k_codes[pos_codes] = (uint8_t)(ck + 128);
+        a.v_codes[pos_codes] = (uint8_t)(cv + 128);
+        if ((t & 63) == 0) {
+            const size_t pos_scales = (size_t)row * (kv_width / 64) + kvh * (D / 64) + (t >> 6);
+            reinterpret_cast<uint16_t *>(a.k_scales)[pos_scales] = kbits;
+            reinterpret_cast<uint16_t *>(a.v_scales)[pos_scales] = vbits;
+        }
+    }
+}
+
 // decoder.zig:94-105: quantizeRow(.q8) of one key row and one value row into
 // row `position`. One wavefront per group; waves [0, gpr) take the key.
 __global__ __launch_bounds__(256) void kv_append_kernel(const float *key, const float *value,
@@ -1232,15 +1284,20 @@ bool attention_supported(uint32_t head_dim, uint32_t ratio) {
            (head_dim == 256 && (ratio == 1 || ratio == 2));
 }
 
+// The range kernel and the merge. The decoder form's range kernel
+// normalizes and rotates the queries; with k.attend_newest (a prefill, whose
+// rows are all in the cache) the plain merge follows it.
 template <int D, int R>
 void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
                            uint32_t kv_heads, uint32_t heads, uint32_t batch) {
+    const bool merge_new = decoder && !k.attend_newest;
     const dim3 ranges(splits, kv_heads, batch), merge(heads, batch);
     const bool sparse = (uint64_t)splits * kv_heads * batch <= (uint64_t)(cus > 0 ? cus : 256);
     if (f32) {
         if (decoder) {
             attention_f32_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
-            attention_combine_kernel<D, R, true, true><<<merge, 256, 0, s>>>(k);
+            if (merge_new) attention_combine_kernel<D, R, true, true><<<merge, 256, 0, s>>>(k);
+            else attention_combine_kernel<D, R, false, true><<<merge, 256, 0, s>>>(k);
         } else {
             attention_f32_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
             attention_combine_kernel<D, R, false, true><<<merge, 256, 0, s>>>(k);
@@ -1252,7 +1309,8 @@ void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool
             if (three) attention_kernel3<D, R, true><<<ranges, 256, 0, s>>>(k);
         }
         if (!three) attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
-        attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
+        if (merge_new) attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
+        else attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     } else {
         bool three = false;
         if constexpr (kThreeWaves<D, R, false>) {
@@ -1284,6 +1342,8 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
     if (a.query_slices > kMaxQuerySlices) return hipErrorInvalidValue;
     k.query_slices = a.query_slices;
     k.query_plane = a.query_plane;
+    if (a.prefill && !decoder) return hipErrorInvalidValue;
+    k.attend_newest = a.prefill ? 1u : 0u;
     k.k_scales = a.k_scales;
     k.k_codes = a.k_codes;
     k.v_scales = a.v_scales;
@@ -1319,6 +1379,37 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
     QWH_ATTN_CASE(128, 8)
     QWH_ATTN_CASE(256, 1)
     QWH_ATTN_CASE(256, 2)
+    return hipErrorNotSupported;
+}
+
+hipError_t launch_prefill_append(hipStream_t s, const AttentionArgs &a, uint32_t first, uint32_t count) {
+    if (count == 0) return hipSuccess;
+    if (!a.k_norm || !a.rope_now || count > 65535 || a.query_slices > kMaxQuerySlices) return hipErrorInvalidValue;
+    AttnKernelArgs k{};
+    k.query = a.query;
+    k.query_stride = a.query_stride;
+    k.query_slices = a.query_slices;
+    k.query_plane = a.query_plane;
+    k.k_scales = a.k_scales;
+    k.k_codes = a.k_codes;
+    k.v_scales = a.v_scales;
+    k.v_codes = a.v_codes;
+    k.heads = a.heads;
+    k.kv_heads = a.kv_heads;
+    k.k_norm = a.k_norm;
+    k.rope_now = a.rope_now;
+    k.eps = a.eps;
+    const dim3 grid(a.kv_heads, count);
+#define QWH_APPEND_CASE(D_)                                                                   \
+    if (a.head_dim == D_) {                                                                   \
+        if (a.f32_cache) prefill_append_kernel<D_, true><<<grid, D_, 0, s>>>(k, first);      \
+        else prefill_append_kernel<D_, false><<<grid, D_, 0, s>>>(k, first);                 \
+        return hipGetLastError();                                                             \
+    }
+    QWH_APPEND_CASE(64)
+    QWH_APPEND_CASE(128)
+    QWH_APPEND_CASE(256)
+#undef QWH_APPEND_CASE
     return hipErrorNotSupported;
 }
 

@@ -224,7 +224,18 @@ struct AttentionArgs {
     // query_plane floats apart, added in slice order as its reduce would.
     uint32_t query_slices = 0;
     uint64_t query_plane = 0;
+    // Decoder form for a prefill: every query row's own key / value row is
+    // already in the cache (launch_prefill_append), so the range kernels
+    // attend to rows below cached including the newest, and the plain merge
+    // follows.
+    bool prefill = false;
 };
+// The prefill's cache append (decoder.zig:180-216, :77-105): for query rows
+// i < count of one sequence (query_stride apart, optionally as K-slice
+// partials), the key row normalized (k_norm) and rotated (rope_now row i),
+// key and value stored at cache row first + i (q8 or f32 by f32_cache);
+// the cache planes are the sequence's own.
+hipError_t launch_prefill_append(hipStream_t s, const AttentionArgs &a, uint32_t first, uint32_t count);
 bool attention_supported(uint32_t head_dim, uint32_t ratio);
 // argmaxLogits (decoder.zig:290-301) of `rows` rows of `count` logits into
 // ids (the decoder step's kernels); scratch holds argmax_scratch_bytes.

@@ -78,30 +78,11 @@ __device__ __forceinline__ float block_sum256(float v, float *lds) {
     return total;
 }
 
-// decoder.zig:346-376 embeddingRow (quant.zig:315-345 dequantizeGroup in the
-// matrix's format): f32(u - bias) then times the group's scale; or, for a
-// sequence whose row flag is set, decoder.zig:144-147: the given audio row
-// replaces the embedding. Also copies the RoPE table row of the sequence's
-// position (cos then sin, 2 * half values) to rope_now, so the step's
-// attention kernels read it without first waiting for the position.
-__global__ __launch_bounds__(256) void embed_kernel(const uint32_t *tokens, int32_t format, const uint16_t *scales,
-                                                    const uint8_t *data, uint32_t cols, float *hidden,
-                                                    const uint32_t *pos, const float *rope_cos,
-                                                    const float *rope_sin, uint32_t half, float *rope_now,
-                                                    const float *rows, const uint32_t *row_flags) {
-    const uint32_t b = blockIdx.x;
-    if (threadIdx.x < 2 * half) {
-        const uint32_t p = pos[b];
-        const uint32_t t = threadIdx.x;
-        rope_now[(size_t)b * 2 * half + t] = t < half ? rope_cos[(size_t)p * half + t] : rope_sin[(size_t)p * half + t - half];
-    }
-    float *out = hidden + (size_t)b * cols;
-    if (row_flags[b]) {
-        const float *src = rows + (size_t)b * cols;
-        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = src[i];
-        return;
-    }
-    const uint32_t token = tokens[b];
+// decoder.zig:346-376 embeddingRow of one token (quant.zig:315-345
+// dequantizeGroup in the matrix's format): f32(u - bias) times the group's
+// scale; the workgroup's threads stride over the row.
+__device__ __forceinline__ void embed_row(uint32_t token, int32_t format, const uint16_t *scales, const uint8_t *data,
+                                          uint32_t cols, float *out) {
     const uint32_t gpr = cols / 64;
     const uint16_t *row_scales = scales + (size_t)token * gpr;
     if (format == QWH_FORMAT_Q4) {
@@ -127,6 +108,55 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t *tokens, int3
             out[i] = __fmul_rn((float)((int)(low | (high << 4)) - 16), dev::f16_bits_to_f32(row_scales[i / 64]));
         }
     }
+}
+
+// The step's embedding: embed_row of each sequence's token; or, for a
+// sequence whose row flag is set, decoder.zig:144-147: the given audio row
+// replaces the embedding. Also copies the RoPE table row of the sequence's
+// position (cos then sin, 2 * half values) to rope_now, so the step's
+// attention kernels read it without first waiting for the position.
+__global__ __launch_bounds__(256) void embed_kernel(const uint32_t *tokens, int32_t format, const uint16_t *scales,
+                                                    const uint8_t *data, uint32_t cols, float *hidden,
+                                                    const uint32_t *pos, const float *rope_cos,
+                                                    const float *rope_sin, uint32_t half, float *rope_now,
+                                                    const float *rows, const uint32_t *row_flags) {
+    const uint32_t b = blockIdx.x;
+    if (threadIdx.x < 2 * half) {
+        const uint32_t p = pos[b];
+        const uint32_t t = threadIdx.x;
+        rope_now[(size_t)b * 2 * half + t] = t < half ? rope_cos[(size_t)p * half + t] : rope_sin[(size_t)p * half + t - half];
+    }
+    float *out = hidden + (size_t)b * cols;
+    if (row_flags[b]) {
+        const float *src = rows + (size_t)b * cols;
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = src[i];
+        return;
+    }
+    embed_row(tokens[b], format, scales, data, cols, out);
+}
+
+// The prompt rows of a prefill (decoder.zig:308-333): row i is the embedding
+// of tokens[i], or, where row_index[i] is not ~0u, that row of the projected
+// audio features; rope_rows[i] gets the RoPE table row of position first + i.
+__global__ __launch_bounds__(256) void embed_prompt_kernel(const uint32_t *tokens, const uint32_t *row_index,
+                                                           int32_t format, const uint16_t *scales,
+                                                           const uint8_t *data, uint32_t cols, float *hidden,
+                                                           uint32_t first, const float *rope_cos,
+                                                           const float *rope_sin, uint32_t half, float *rope_rows,
+                                                           const float *audio_rows) {
+    const uint32_t i = blockIdx.x;
+    if (threadIdx.x < 2 * half) {
+        const uint32_t p = first + i;
+        const uint32_t t = threadIdx.x;
+        rope_rows[(size_t)i * 2 * half + t] = t < half ? rope_cos[(size_t)p * half + t] : rope_sin[(size_t)p * half + t - half];
+    }
+    float *out = hidden + (size_t)i * cols;
+    if (row_index[i] != ~0u) {
+        const float *src = audio_rows + (size_t)row_index[i] * cols;
+        for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) out[c] = src[c];
+        return;
+    }
+    embed_row(tokens[i], format, scales, data, cols, out);
 }
 
 // kernels.zig:274-300 rmsNormInto + math.zig:120-130, emitting the
@@ -362,6 +392,16 @@ struct qwh_decoder {
     float *parts = nullptr;
     bool split_parts = false;
     uint32_t slices_o = 0, slices_gu = 0, slices_down = 0, slices_qkv = 0;
+    // qwh_decoder_prefill's buffers, for up to kPrefillChunk prompt positions
+    // of one sequence, allocated at its first call.
+    struct PrefillBuffers {
+        float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *rope = nullptr, *parts = nullptr;
+        void *digits = nullptr, *attn_scratch = nullptr, *arg_scratch = nullptr;
+        size_t attn_scratch_bytes = 0;
+        uint32_t *staged_dev = nullptr;  // tokens, audio row indices, positions
+        uint32_t *id_dev = nullptr;
+        uint32_t *host = nullptr;        // pinned: the same three arrays, then the id
+    } pf;
 };
 
 namespace qwh {
@@ -899,6 +939,7 @@ int32_t qwh_decoder_destroy(qwh_decoder *d) {
         if (g) (void)hipGraphExecDestroy(g);
     for (void *p : d->allocations) (void)hipFree(p);
     if (d->host_stage) (void)hipHostFree(d->host_stage);
+    if (d->pf.host) (void)hipHostFree(d->pf.host);
     delete d;
     return QWH_OK;
 }
@@ -1229,6 +1270,247 @@ int32_t qwh_decoder_forward_rows(qwh_decoder *d, const uint32_t *tokens, const f
     QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "forward rows"));
     for (uint32_t &p : d->pos_host) p += 1;
     return QWH_OK;
+}
+
+namespace {
+
+constexpr uint32_t kPrefillChunk = 256;
+
+// Every layer product has a matrix-core form, o / gate|up / down a K split,
+// and the attention and the prefill append take the head shape.
+bool prefill_supported(const qwh_decoder *d) {
+    for (const qwh_decoder::Layer &L : d->layers)
+        for (const Matrix *m : {&L.qkv, &L.o, &L.gu, &L.down})
+            if (!gemv_batch_supported(*m)) return false;
+    const qwh_decoder::Layer &L0 = d->layers[0];
+    const uint32_t D = d->c.head_dim;
+    return batch_slices(L0.o) && batch_slices(L0.gu) && batch_slices(L0.down) &&
+           attention_supported(D, d->c.heads / d->c.kv_heads) && (D == 64 || D == 128 || D == 256);
+}
+
+int32_t prefill_buffers(qwh_decoder *d) {
+    qwh_decoder::PrefillBuffers &pf = d->pf;
+    if (pf.host) return QWH_OK;
+    const qwh_decoder_config &c = d->c;
+    const size_t P = kPrefillChunk;
+    const uint32_t qkv_n = d->qw + 2 * d->kvw;
+    const uint32_t widest = std::max(std::max(c.hidden, c.ffn), d->qw);
+    QWH_TRY(dalloc(d, sizeof(float) * P * c.hidden, reinterpret_cast<void **>(&pf.hidden)));
+    QWH_TRY(dalloc(d, sizeof(float) * P * qkv_n, reinterpret_cast<void **>(&pf.qkv)));
+    QWH_TRY(dalloc(d, sizeof(float) * P * d->qw, reinterpret_cast<void **>(&pf.attn)));
+    QWH_TRY(dalloc(d, sizeof(float) * P * c.head_dim, reinterpret_cast<void **>(&pf.rope)));
+    QWH_TRY(dalloc(d, batch_digit_bytes((uint32_t)P, widest), &pf.digits));
+    const qwh_decoder::Layer &L0 = d->layers[0];
+    size_t parts = 4;
+    for (const Matrix *m : {&L0.qkv, &L0.o, &L0.gu, &L0.down})
+        parts = std::max(parts, batch_partial_bytes((uint32_t)P, *m));
+    QWH_TRY(dalloc(d, parts, reinterpret_cast<void **>(&pf.parts)));
+    // The attention records: sized per chunk (the range count depends on
+    // the chunk's rows and positions), grown by prefill_chunk when a chunk
+    // needs more.
+    pf.attn_scratch_bytes = 0;
+    QWH_TRY(dalloc(d, argmax_scratch_bytes(1, c.vocab), &pf.arg_scratch));
+    QWH_TRY(dalloc(d, 3 * 4 * P, reinterpret_cast<void **>(&pf.staged_dev)));
+    QWH_TRY(dalloc(d, 4, reinterpret_cast<void **>(&pf.id_dev)));
+    void *host = nullptr;
+    QWH_TRY(check_hip(d->ctx, hipHostMalloc(&host, 4 * (3 * P + 8), hipHostMallocDefault), "pinned prefill staging"));
+    pf.host = static_cast<uint32_t *>(host);
+    return QWH_OK;
+}
+
+// One row's W * RMSNorm(x) with the batch-1 kernels of the matrix's format.
+hipError_t single_row_norm_gemv(qwh_decoder *d, const float *x, const float *norm, const Matrix &w, float *out) {
+    hipStream_t s = d->ctx->stream;
+    GemvInput in;
+    in.mode = GemvInput::RmsNorm;
+    in.x = x;
+    in.norm = norm;
+    in.eps = d->c.eps;
+    if (w.format != QWH_FORMAT_Q4) return launch_gemv_b8(s, d->ctx->cus, in, w, 1, out, nullptr);
+    if (gemv_q4_fused_supported(w.rows, w.cols)) return launch_gemv_q4_src(s, d->ctx->cus, in, w, 1, out, nullptr);
+    uint32_t *words = static_cast<uint32_t *>(d->digits);
+    rmsnorm_digits_kernel<<<1, 256, 0, s>>>(x, norm, w.cols, d->c.eps, words,
+                                            reinterpret_cast<float *>(words + (size_t)(w.cols / 32) * dev::kChunkWords));
+    GemvInput pre;
+    pre.mode = GemvInput::Digits;
+    pre.digits = words;
+    return launch_gemv_q4_src(s, d->ctx->cus, pre, w, 1, out, nullptr);
+}
+
+// One chunk of a prefill: prompt rows [c0, c0 + n) of sequence seq at
+// positions first .. first + n - 1 through every layer; the last chunk's
+// final hidden rows stay in pf.hidden with the last down projection added.
+int32_t prefill_chunk(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, const float *audio_rows, bool last) {
+    qwh_decoder::PrefillBuffers &pf = d->pf;
+    const qwh_decoder_config &c = d->c;
+    hipStream_t s = d->ctx->stream;
+    const uint32_t H = c.hidden, qkv_n = d->qw + 2 * d->kvw;
+    const uint32_t *tokens_dev = pf.staged_dev, *index_dev = pf.staged_dev + kPrefillChunk;
+    const uint32_t *pos_dev = pf.staged_dev + 2 * kPrefillChunk;
+    embed_prompt_kernel<<<n, 256, 0, s>>>(tokens_dev, index_dev, d->embed.format,
+                                          reinterpret_cast<const uint16_t *>(d->embed.scales), d->embed.data, H,
+                                          pf.hidden, first, d->rope_cos, d->rope_sin, c.head_dim / 2, pf.rope,
+                                          audio_rows);
+    QWH_TRY(check_hip(d->ctx, hipGetLastError(), "prefill embedding"));
+    BatchNorm bn;
+    bn.rms = true;
+    bn.eps = c.eps;
+    PartialSums pending{};
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        qwh_decoder::Layer &L = d->layers[l];
+        GemvInput in;
+        in.mode = GemvInput::RmsNorm;
+        in.x = pf.hidden;
+        in.norm = L.attn_norm;
+        in.eps = c.eps;
+        QWH_TRY(check_hip(d->ctx, launch_prep_batch(s, in, n, H, pf.digits, &pending), "prefill prep"));
+        pending = PartialSums{};
+        const uint32_t sq = batch_slices(L.qkv);
+        if (sq > 1)
+            QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.qkv, n, pf.parts, bn), "prefill q|k|v"));
+        else
+            QWH_TRY(check_hip(d->ctx, launch_gemv_batch(s, pf.digits, L.qkv, n, pf.qkv, nullptr, false, pf.parts, bn),
+                              "prefill q|k|v"));
+        // The rows are n pseudo-sequences sharing the sequence's cache:
+        // row i attends to the cache rows below first + i + 1 (its own
+        // appended first), decoder.zig:180-253 for each prompt position.
+        uint8_t *kl = d->keys + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
+        uint8_t *vl = d->values + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
+        AttentionArgs aa{};
+        aa.out = pf.attn;
+        aa.query = sq > 1 ? pf.parts : pf.qkv;
+        aa.query_stride = qkv_n;
+        if (sq > 1) {
+            aa.query_slices = sq;
+            aa.query_plane = (uint64_t)n * qkv_n;
+        }
+        aa.q_norm = L.q_norm;
+        aa.k_norm = L.k_norm;
+        aa.rope_now = pf.rope;
+        aa.eps = c.eps;
+        aa.k_scales = kl;
+        aa.k_codes = kl + d->cache_scales;
+        aa.v_scales = vl;
+        aa.v_codes = vl + d->cache_scales;
+        aa.cached_dev = pos_dev;
+        aa.cached_bias = 1;
+        aa.capacity = first + n;
+        aa.heads = c.heads;
+        aa.kv_heads = c.kv_heads;
+        aa.head_dim = c.head_dim;
+        aa.batch = n;
+        aa.scale_stride = 0;
+        aa.code_stride = 0;
+        aa.f32_cache = d->cache_format == QWH_CACHE_F32;
+        aa.digits = pf.digits;
+        aa.prefill = true;
+        const size_t records = attention_scratch_bytes(d->ctx->cus, aa);
+        if (records > pf.attn_scratch_bytes) {
+            // The previous chunk's kernels may still read the old records.
+            QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "prefill scratch"));
+            dfree(d, pf.attn_scratch);
+            pf.attn_scratch = nullptr;
+            pf.attn_scratch_bytes = 0;
+            QWH_TRY(dalloc(d, records, &pf.attn_scratch));
+            pf.attn_scratch_bytes = records;
+        }
+        QWH_TRY(check_hip(d->ctx, launch_prefill_append(s, aa, first, n), "prefill cache append"));
+        QWH_TRY(check_hip(d->ctx, launch_decode_attention_q8(s, d->ctx->cus, aa, pf.attn_scratch, pf.attn_scratch_bytes),
+                          "prefill attention"));
+        // o, gate|up, down as partial sums, each added by the prep that
+        // follows (the batched step's sequence).
+        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.o, n, pf.parts), "prefill o"));
+        GemvInput norm_in;
+        norm_in.mode = GemvInput::RmsNorm;
+        norm_in.x = pf.hidden;
+        norm_in.norm = L.ffn_norm;
+        norm_in.eps = c.eps;
+        const PartialSums o_sums{pf.parts, batch_slices(L.o), H, false, pf.hidden};
+        QWH_TRY(check_hip(d->ctx, launch_prep_batch(s, norm_in, n, H, pf.digits, &o_sums), "prefill prep"));
+        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.gu, n, pf.parts, bn), "prefill gate|up"));
+        GemvInput pairs_in;
+        pairs_in.mode = GemvInput::F32;
+        const PartialSums gu_sums{pf.parts, batch_slices(L.gu), 2 * c.ffn, true, nullptr};
+        QWH_TRY(check_hip(d->ctx, launch_prep_batch(s, pairs_in, n, c.ffn, pf.digits, &gu_sums), "prefill prep"));
+        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.down, n, pf.parts), "prefill down"));
+        pending = PartialSums{pf.parts, batch_slices(L.down), H, false, pf.hidden};
+    }
+    if (!last) return QWH_OK;  // (only the cache rows of earlier chunks matter)
+    // The residual stream after the last layer: the final prep adds the
+    // down projection (its digits are not used).
+    GemvInput fin;
+    fin.mode = GemvInput::RmsNorm;
+    fin.x = pf.hidden;
+    fin.norm = d->final_norm;
+    fin.eps = c.eps;
+    return check_hip(d->ctx, launch_prep_batch(s, fin, n, H, pf.digits, &pending), "prefill final");
+}
+
+}  // namespace
+
+int32_t qwh_decoder_prefill(qwh_decoder *d, uint32_t seq, const uint32_t *tokens, uint32_t count,
+                            uint32_t audio_pad_token, const float *audio_rows_dev, uint32_t audio_steps,
+                            uint32_t *next_token) {
+    if (!d || !tokens || !next_token || seq >= d->batch) return QWH_E_INVALID_ARGUMENT;
+    const qwh_decoder_config &c = d->c;
+    // decoder.zig:317: an empty prompt.
+    if (count == 0) return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "empty prompt");
+    if (audio_steps && !audio_rows_dev) return QWH_E_INVALID_ARGUMENT;
+    // decoder.zig:320-331: each audio pad takes the next row, and every row
+    // is taken (PromptMismatch otherwise: the reference ABI's shape_mismatch).
+    uint32_t pads = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (tokens[i] >= c.vocab) return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "token %u >= vocab %u", tokens[i], c.vocab);
+        if (tokens[i] == audio_pad_token && ++pads > audio_steps)
+            return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "more audio pads than the %u audio rows", audio_steps);
+    }
+    if (pads != audio_steps)
+        return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "%u audio pads for %u audio rows", pads, audio_steps);
+    const uint32_t pos0 = d->pos_host[seq];
+    // decoder.zig:142 PositionExceeded.
+    if ((uint64_t)pos0 + count > c.max_positions)
+        return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "position %u + %u prompt tokens exceeds %u", pos0, count,
+                    c.max_positions);
+    if (!d->planned) QWH_TRY(plan_step(d));
+    if (!prefill_supported(d))
+        return fail(d->ctx, QWH_E_UNSUPPORTED, "prefill needs matrix-core forms of every layer matrix");
+    QWH_TRY(prefill_buffers(d));
+    qwh_decoder::PrefillBuffers &pf = d->pf;
+    hipStream_t s = d->ctx->stream;
+    uint32_t audio_index = 0;
+    for (uint32_t c0 = 0; c0 < count; c0 += kPrefillChunk) {
+        const uint32_t n = std::min(kPrefillChunk, count - c0);
+        // The pinned staging is reused per chunk: the previous chunk's copy
+        // has completed (the stream was synchronized below).
+        uint32_t *h_tokens = pf.host, *h_index = pf.host + kPrefillChunk, *h_pos = pf.host + 2 * kPrefillChunk;
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t t = tokens[c0 + i];
+            h_tokens[i] = t;
+            h_index[i] = t == audio_pad_token ? audio_index++ : ~0u;
+            h_pos[i] = pos0 + c0 + i;
+        }
+        QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(pf.staged_dev, pf.host, 3 * 4 * (size_t)kPrefillChunk,
+                                                 hipMemcpyHostToDevice, s), "prefill tokens"));
+        const bool last = c0 + n == count;
+        QWH_TRY(prefill_chunk(d, seq, pos0 + c0, n, audio_rows_dev, last));
+        if (last) {
+            // decoder.zig:332 argmaxLogits of the last position.
+            float *logits = d->logits + (size_t)seq * c.vocab;
+            QWH_TRY(check_hip(d->ctx, single_row_norm_gemv(d, pf.hidden + (size_t)(n - 1) * c.hidden, d->final_norm,
+                                                           d->lm_head, logits), "prefill lm_head"));
+            QWH_TRY(check_hip(d->ctx, launch_argmax_rows(s, logits, 1, c.vocab, pf.arg_scratch, pf.id_dev),
+                              "prefill argmax"));
+            QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(pf.host + 3 * kPrefillChunk, pf.id_dev, 4, hipMemcpyDeviceToHost, s),
+                              "prefill id"));
+        }
+        QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "prefill"));
+    }
+    *next_token = pf.host[3 * kPrefillChunk];
+    // The sequence's position, also on the device for the steps that follow.
+    d->pos_host[seq] = pos0 + count;
+    d->host_stage[0] = pos0 + count;
+    QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->pos_dev + seq, d->host_stage, 4, hipMemcpyHostToDevice, s), "position"));
+    return check_hip(d->ctx, hipStreamSynchronize(s), "prefill");
 }
 
 int32_t qwh_decoder_step(qwh_decoder *d, const uint32_t *tokens, uint32_t *next_tokens) {

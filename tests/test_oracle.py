@@ -640,3 +640,41 @@ def test_decoder_cache_row_reads_the_prefilled_rows():
                 d.cache_row(2, 0, 0)
         finally:
             d.close()
+
+
+def test_decoder_set_cache_row_and_position():
+    # The checker's plumbing (teacher forcing on another implementation's
+    # rows): rows stored through set_cache_row read back as they were, a
+    # decoder given another's rows and position then steps exactly as that
+    # decoder does, and a planted wrong row changes the next logits.
+    cfg = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=1000,
+               max_positions=16, eps=1e-6, theta=1e6)
+    for cache in (o.CACHE_Q8, o.CACHE_F32):
+        a = o.Decoder(3, 1, o.Q4, cache, **cfg)
+        b = o.Decoder(3, 1, o.Q4, cache, **cfg)
+        try:
+            a.prefill_random(0, 5)
+            a.forward(0, 11, False)
+            for layer in range(2):
+                for p in range(6):
+                    b.set_cache_row(0, layer, p, a.cache_row(0, layer, p))
+            b.set_position(0, 6)
+            assert a.cache_hash(0) == b.cache_hash(0) and b.position(0) == 6
+            a.forward(0, 7)
+            b.forward(0, 7)
+            assert np.array_equal(a.logits(0), b.logits(0))
+            row = bytearray(a.cache_row(0, 1, 3))
+            row[len(row) // 2 - 1] ^= 0x40            # one code (q8) / one value byte (f32)
+            b.set_position(0, 7)
+            b.set_cache_row(0, 1, 3, bytes(row))
+            assert b.cache_row(0, 1, 3) == bytes(row)
+            a.forward(0, 9)
+            b.forward(0, 9)
+            assert not np.array_equal(a.logits(0), b.logits(0))
+            with pytest.raises(ValueError):
+                b.set_cache_row(0, 0, 0, bytes(row[:-1]))
+            with pytest.raises(ValueError):
+                b.set_position(0, 17)
+        finally:
+            a.close()
+            b.close()
