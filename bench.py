@@ -255,6 +255,51 @@ def bench_decoder(ctx, qa, batch, steps, warmup, fmt=None, cache=None):
                 context=f"4096..{4096 + warmup + steps}")
 
 
+def bench_prefill(ctx, qa, audio_steps=390, text_tokens=12, repeats=5):
+    """qwh_decoder_prefill of a 30 s transcription prompt (390 audio pads, as
+    the encoder emits for 30 s of audio, inside a short text template) on the
+    1.7B decoder at batch 1, against the same prompt fed one position at a
+    time through the step (decoder.zig:319-331 runs it that way)."""
+    cfg = dict(hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151936,
+               max_positions=4352, eps=1e-6, theta=1e6)
+    pad = 151676
+    dec = qa.Decoder(ctx, batch=1, **cfg)
+    dec.init_synthetic(4)
+    count = audio_steps + text_tokens
+    tokens = (np.arange(count, dtype=np.uint32) * 7919 + 13) % cfg["vocab"]
+    tokens[tokens == pad] = pad + 1
+    tokens[text_tokens // 2:text_tokens // 2 + audio_steps] = pad
+    rows = ctx.to_device((np.random.default_rng(5).standard_normal((audio_steps, cfg["hidden"])) * 0.02)
+                         .astype(np.float32))
+    times = []
+    for i in range(repeats + 1):
+        dec.set_position(0, 0)
+        t0 = time.perf_counter()
+        dec.prefill(0, tokens, pad, rows.ptr, audio_steps)
+        if i:
+            times.append(time.perf_counter() - t0)
+    # The same prompt one position at a time (forward / forward_rows).
+    dec.set_position(0, 0)
+    ctx.sync()
+    t0 = time.perf_counter()
+    used = 0
+    for i, t in enumerate(tokens):
+        if t == pad:
+            dec.forward_rows([int(t)], rows.ptr + used * cfg["hidden"] * 4, None, i + 1 == count)
+            used += 1
+        else:
+            dec.forward([int(t)], i + 1 == count)
+    ctx.sync()
+    per_token_s = time.perf_counter() - t0
+    rows.free()
+    dec.close()
+    best = min(times)
+    return dict(prompt_positions=count, audio_steps=audio_steps, ms=round(best * 1e3, 3),
+                positions_per_s=round(count / best, 1), median_ms=round(float(np.median(times)) * 1e3, 3),
+                one_position_at_a_time_ms=round(per_token_s * 1e3, 3),
+                speedup=round(per_token_s / best, 2))
+
+
 def bench_small(ctx, qa, steps):
     from_seed = 1
     out = {}
@@ -446,8 +491,9 @@ def main():
     ap.add_argument("--decoder-batches", default="1,16", help="comma-separated decoder batch sizes")
     ap.add_argument("--decoders", default="q4,q8,q5,f32kv",
                     help="decoder variants: q4 (q4 weights, q8 cache), q8 (q8 weights), q5 (q5 weights), "
-                         "f32kv (q4, f32 cache)")
+                         "f32kv (q4, f32 cache); 'none' for no step lines")
     ap.add_argument("--skip-headline", action="store_true", help="skip the lm_head GEMV and its read ceiling")
+    ap.add_argument("--skip-prefill", action="store_true", help="skip the 30 s prompt prefill")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -535,6 +581,10 @@ def main():
         log("decoder 1.7B, f32 cache, batch 1")
         result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=64, warmup=8,
                                                                        cache=qa.CACHE_F32)}
+    if not args.skip_decoder and not args.skip_prefill:
+        log("decoder 1.7B prefill of a 30 s prompt")
+        result["prefill_1p7b_30s_prompt"] = bench_prefill(ctx, qa)
+        log(f"prefill: {result['prefill_1p7b_30s_prompt']}")
     if not args.skip_extra:
         log("configs 1, 2 (small shapes), 3, 4")
         result["kernels"] = bench_small(ctx, qa, max(10, args.steps // 2))
