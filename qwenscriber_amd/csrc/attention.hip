@@ -245,6 +245,8 @@ __device__ __forceinline__ void attend_f32(SoftmaxState<R> &st, const float (&q)
 // maximum stands still), and merge at the end by plain sums.
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kTile = 32;                 // positions per wavefront per iteration
 constexpr int kTileBlocks = kTile / 16;   // 16-position MFMA blocks per tile
@@ -449,7 +451,7 @@ __device__ __forceinline__ void write_range_record_lds(const AttnKernelArgs &a, 
     }
 }
 
-template <int D, int R, bool Decoder, bool Early>
+template <int D, int R, bool Decoder, bool Early, bool MV>
 __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     constexpr int LPP = D / 16;              // value layout: lanes per position
     constexpr int PPW = 64 / LPP;            // value layout: lane groups per wave
@@ -480,8 +482,23 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
 
     __shared__ float lds_q[R][D];
     __shared__ int lds_exp[R][G];
-    __shared__ float lds_w[kWaves][R][kWRow];
-    float(&wrow)[R][kWRow] = lds_w[wave];
+    __shared__ float lds_w[MV ? 1 : kWaves][R][kWRow];
+    float(&wrow)[R][kWRow] = lds_w[MV ? 0 : wave];
+    // MV: the values' products on the matrix cores. Per wavefront, the
+    // tile's value codes (signed bytes, [position][dimension], rows padded
+    // by 16 bytes so a transposing read's eight rows fall on distinct
+    // banks) and the weights' digit planes ([group][head * 4 + plane]
+    // [position]; rows of plane 3 and of heads past R stay zero). The
+    // range record's partial sums reuse the same bytes after the loop.
+    constexpr int kVcRow = D + 16;
+    constexpr int kVcBytes = kTile * kVcRow;
+    constexpr int kPlBytes = G * 32 * kTile;
+    constexpr int kMvWave = kVcBytes + kPlBytes;
+    constexpr int kMvRecord = (kWaves * R * D + kWaves * R * 2) * 4;
+    constexpr int kMvBytes = kWaves * kMvWave > kMvRecord ? kWaves * kMvWave : kMvRecord;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_mv[MV ? kMvBytes : 16];
+    uint8_t *vcl = lds_mv + (MV ? wave * kMvWave : 0);
+    uint8_t *pll = vcl + kVcBytes;
 
     // A tile: the wavefront's kTile positions from base + wave * kTile; keys
     // and key scales in the score layout, values and value scales in the
@@ -490,7 +507,8 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         uint4 kc[kTileBlocks][G];
         uint32_t ks[kTileBlocks][G];
         uint4 vc[NV];
-        uint32_t vs[NV];
+        uint32_t vs[MV ? 1 : NV];                       // value scales, value layout
+        uint32_t vsc[MV ? kTileBlocks : 1][MV ? G : 1];  // MV: value scales, score layout
     };
     // Every load is unconditional, so all of a tile's loads are in flight
     // together. Plain form: tiles are read through buffer resources that
@@ -527,6 +545,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             for (int g = 0; g < G; ++g) {
                 t.kc[blk][g] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)row * kv_width + key_col + 64 * g);
                 t.ks[blk][g] = k_scales[(size_t)row * gpr + kvh * G + g];
+                if constexpr (MV) t.vsc[blk][g] = v_scales[(size_t)row * gpr + kvh * G + g];
             }
         }
 #pragma unroll
@@ -534,7 +553,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             const uint32_t p = first + NV * group + v;
             const uint32_t row = p < limit ? p : limit - 1;
             t.vc[v] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)row * kv_width + code_col);
-            t.vs[v] = v_scales[(size_t)row * gpr + vscale_col];
+            if constexpr (!MV) t.vs[v] = v_scales[(size_t)row * gpr + vscale_col];
         }
     };
     auto load_tile = [&](Tile &t, uint32_t base_in, uint32_t limit) {
@@ -561,13 +580,15 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                     v4i, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)key_off[blk] + 64 * g, 0, 0));
                 t.kc[blk][g] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
                 t.ks[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(ksr, (int)kscale_off[blk] + 2 * g, 0, 0);
+                if constexpr (MV)
+                    t.vsc[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)kscale_off[blk] + 2 * g, 0, 0);
             }
         }
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const v4i c = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)val_off[v], 0, 0));
             t.vc[v] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
-            t.vs[v] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)vscale_off[v], 0, 0);
+            if constexpr (!MV) t.vs[v] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)vscale_off[v], 0, 0);
         }
     };
 
@@ -659,18 +680,125 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     }
 
     // Running state: m (the same in every lane of a head's score row), the
-    // lane's share of l (score layout), acc (value layout).
+    // lane's share of l (score layout), acc (value layout; MV: the product
+    // layout, dimension 32 j + lane % 32 of head 2 q + lane / 32 in
+    // acc[j][q], the wavefront's whole sum).
+    constexpr int NB = D / 32;               // MV: 32-dimension blocks of a head row
+    constexpr int HQ = (R + 1) / 2;          // MV: heads per lane in the product layout
+    constexpr int AR = MV ? NB : R, AC = MV ? HQ : 16;
     float m[HS], l[HS];
-    float acc[R][16];
+    float acc[AR][AC];
 #pragma unroll
     for (int hs = 0; hs < HS; ++hs) {
         m[hs] = kNeg;
         l[hs] = 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < AR; ++r)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
+        for (int i = 0; i < AC; ++i) acc[r][i] = 0.0f;
+    if constexpr (MV) {
+        // Zero digit planes: plane 3 and heads past R are never written.
+#pragma unroll
+        for (int g = 0; g < G; ++g) *reinterpret_cast<v4i *>(pll + g * 32 * kTile + 16 * lane) = v4i{0, 0, 0, 0};
+    }
+
+    // MV: the tile's values, acc += sum over its positions of (w * scale) *
+    // (u - 128), on the matrix cores. The weights times their position's
+    // value scale, per head and 64-dimension group, become three signed
+    // digit planes of x = rint(w s 2^(22 - e)) (e from the largest of the
+    // head's tile values, so x <= 2^22; zero weights, rows past `end`, give
+    // zero digits whatever their codes); one v_mfma_i32_32x32x32_i8 per 32
+    // dimensions multiplies [head * 4 + plane][position] digits by the codes
+    // [position][dimension] (read transposed from LDS, eight positions of a
+    // dimension per lane and read), and the three planes' integer sums are
+    // combined as in the scores: (c0 + 256 c1) + 65536 c2, times 2^(e - 22).
+    auto use_values_mfma = [&](const Tile &t, const float (&wv)[HS][kTileBlocks], const bool (&valid)[kTileBlocks],
+                               const float (&alpha)[R]) __attribute__((always_inline)) {
+        // The tile's codes (signed) into this wavefront's rows.
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+            *reinterpret_cast<v4i *>(vcl + (NV * group + v) * kVcRow + sub * 16) = signed_codes(t.vc[v]);
+        float mult[HS][G];
+#pragma unroll
+        for (int hs = 0; hs < HS; ++hs) {
+            const int rq = 4 * hs + quarter;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float W[kTileBlocks];
+                float wmax = 0.0f;
+#pragma unroll
+                for (int blk = 0; blk < kTileBlocks; ++blk) {
+                    W[blk] = valid[blk] ? wv[hs][blk] * dev::f16_bits_to_f32((uint16_t)t.vsc[blk][g]) : 0.0f;
+                    wmax = fmaxf(wmax, W[blk]);
+                }
+                wmax = row16_max(wmax);
+                // wmax < 2^e (e kept above -100 so 2^(22 - e) stays finite).
+                int e = (int)((__builtin_bit_cast(uint32_t, wmax) >> 23) & 0xffu) - 126;
+                e = e < -100 ? -100 : e;
+                const float up = wmax > 0.0f ? __builtin_ldexpf(1.0f, 22 - e) : 0.0f;
+                mult[hs][g] = wmax > 0.0f ? __builtin_ldexpf(1.0f, e - 22) : 0.0f;
+                if (rq < R) {
+#pragma unroll
+                    for (int blk = 0; blk < kTileBlocks; ++blk) {
+                        const uint32_t y = (uint32_t)((int)__builtin_rintf(W[blk] * up) + 0x808080) ^ 0x808080u;
+                        uint8_t *dst = pll + (g * 32 + rq * 4) * kTile + 16 * blk + n;
+                        dst[0] = (uint8_t)y;
+                        dst[kTile] = (uint8_t)(y >> 8);
+                        dst[2 * kTile] = (uint8_t)(y >> 16);
+                    }
+                }
+            }
+        }
+        wave_lds_sync();
+        // Rescale to the new maxima (head 2 q + lane / 32 of acc[.][q]).
+        bool moved = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) moved |= alpha[r] != 1.0f;
+        if (moved) {
+#pragma unroll
+            for (int q = 0; q < HQ; ++q) {
+                const float al = lane < 32 ? alpha[2 * q] : alpha[2 * q + 1 < R ? 2 * q + 1 : 2 * q];
+#pragma unroll
+                for (int j = 0; j < NB; ++j) acc[j][q] *= al;
+            }
+        }
+        v4i A[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            A[g] = *reinterpret_cast<const v4i *>(pll + (g * 32 + (lane & 31)) * kTile + 16 * (lane >> 5));
+        float mh[HQ][G];
+#pragma unroll
+        for (int q = 0; q < HQ; ++q)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int h0 = 2 * q, h1 = 2 * q + 1;
+                const float m0 = lane_value(mult[h0 / 4][g], 16 * (h0 % 4));
+                const float m1 = h1 < R ? lane_value(mult[h1 / 4][g], 16 * (h1 % 4)) : 0.0f;
+                mh[q][g] = lane < 32 ? m0 : m1;
+            }
+        // Transposed code reads: in each 16-lane group, lane i takes byte i
+        // of the eight 16-byte rows that lanes (2 b, 2 b + 1) address.
+        const int ti = lane & 15;
+        const uint8_t *src0 = vcl + (16 * (lane >> 5) + (ti >> 1)) * kVcRow + 16 * ((lane >> 4) & 1) + 8 * (ti & 1);
+        const v16i zero16 = {};
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int g = j / 2;
+            const uint8_t *src = src0 + 32 * j;
+            const v2i b0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)src);
+            const v2i b1 =
+                __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(src + 8 * kVcRow));
+            const v4i B = {b0.x, b0.y, b1.x, b1.y};
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[g], B, zero16, 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < HQ; ++q) {
+                const float val = (float)(c[4 * q] + 256 * c[4 * q + 1]) + 65536.0f * (float)c[4 * q + 2];
+                acc[j][q] = fmaf(val, mh[q][g], acc[j][q]);
+            }
+        }
+        wave_lds_sync();
+    };
 
     // Rows below `end` take part; the others (possibly never written, so
     // their bits are arbitrary) get no weight and a zero value scale.
@@ -702,8 +830,10 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             }
         }
         // Online softmax per head over the tile; the weights go to this
-        // wavefront's LDS rows, the rescale factors become scalars.
+        // wavefront's LDS rows (MV: stay in registers), the rescale factors
+        // become scalars.
         float alpha[R];
+        float wv[HS][kTileBlocks];
 #pragma unroll
         for (int hs = 0; hs < HS; ++hs) {
             float mx = s[hs][0];
@@ -717,12 +847,17 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             for (int blk = 0; blk < kTileBlocks; ++blk) {
                 const float w = valid[blk] ? fast_exp2(s[hs][blk] - m_new) : 0.0f;
                 sum += w;
-                if (rq < R) wrow[rq][16 * blk + n] = w;
+                if constexpr (MV) wv[hs][blk] = w;
+                else if (rq < R) wrow[rq][16 * blk + n] = w;
             }
             l[hs] = l[hs] * al + sum;
             m[hs] = m_new;
 #pragma unroll
             for (int k = 0; k < 4 && 4 * hs + k < R; ++k) alpha[4 * hs + k] = lane_value(al, 16 * k);
+        }
+        if constexpr (MV) {
+            use_values_mfma(t, wv, valid, alpha);
+            return;
         }
         wave_lds_sync();
         bool moved = false;
@@ -800,7 +935,48 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             st.l[4 * hs + k] = lane_value(lsum, 16 * k);
         }
     }
-    if constexpr (R <= 2) {
+    if constexpr (MV) {
+        // Every wavefront is past its loop: the tile bytes hold the record's
+        // parts now. Each lane's sums are its wavefront's whole sums.
+        __syncthreads();
+        float *part = reinterpret_cast<float *>(lds_mv);  // [kWaves][R][D]
+        float *ml = part + kWaves * R * D;                  // [kWaves][R][2]
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) {
+            const int h = 2 * q + (lane >> 5);
+            if (h < R)
+#pragma unroll
+                for (int j = 0; j < NB; ++j) part[(wave * R + h) * D + 32 * j + (lane & 31)] = acc[j][q];
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                ml[(wave * R + r) * 2 + 0] = st.m[r];
+                ml[(wave * R + r) * 2 + 1] = st.l[r];
+            }
+        __syncthreads();
+        constexpr int REC = R * D + 4 * R;
+        float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
+        for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
+            const int r = idx / D;
+            const int d = idx % D;
+            float M = ml[r * 2];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml[(w * R + r) * 2]);
+            float L = 0.0f, A = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float f = fast_exp2(ml[(w * R + r) * 2] - M);
+                L += ml[(w * R + r) * 2 + 1] * f;
+                A += part[(w * R + r) * D + d] * f;
+            }
+            rec[idx] = A;
+            if (d == 0) {
+                rec[R * D + 4 * r + 0] = M;
+                rec[R * D + 4 * r + 1] = L;
+            }
+        }
+    } else if constexpr (R <= 2) {
         write_range_record_lds<D, R>(a, st, acc, b, kvh, split, wave, sub, group);
     } else {
 #pragma unroll
@@ -819,15 +995,16 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
 template <int D, int R, bool Decoder>
 constexpr bool kThreeWaves = R <= 2 && (D == 64 || (D == 128 && Decoder));
 
-template <int D, int R, bool Decoder>
+template <int D, int R, bool Decoder, bool MV>
 __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) {
-    attention_range<D, R, Decoder, true>(a);
+    attention_range<D, R, Decoder, true, MV>(a);
 }
 
-template <int D, int R, bool Decoder>
+template <int D, int R, bool Decoder, bool MV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel3(const AttnKernelArgs a) {
-    attention_range<D, R, Decoder, false>(a);
+    attention_range<D, R, Decoder, false, MV>(a);
 }
+
 
 // The range kernel over an f32 cache (kernels.zig:572-627): the same lane
 // mapping (a lane group of D/16 lanes per position, 16 dimensions per lane,
@@ -1228,8 +1405,18 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float *key, const 
     if (lane == 0) reinterpret_cast<uint16_t *>(scales)[(size_t)position * gpr + g] = bits;
 }
 
+// The values' products on the matrix cores; QWH_ATTN_VALU_VALUES=1 keeps
+// them on the vector ALUs (the earlier form, for comparison).
+bool mfma_values() {
+    static const bool mv = getenv("QWH_ATTN_VALU_VALUES") == nullptr;
+    return mv;
+}
+
 // Workgroups of the range kernel resident per CU: three where the kernel is
-// compiled for three wavefronts per SIMD (kThreeWaves), else two.
+// compiled for three wavefronts per SIMD (kThreeWaves), else two. (With the
+// values on the matrix cores the decoder form also fits four wavefronts per
+// SIMD; four resident workgroups, with the ranges that many more need, ran
+// batch 16 at 7008 tokens/s against 7290.)
 uint32_t resident_groups(const AttentionArgs &a, bool decoder) {
     const uint32_t ratio = a.heads / a.kv_heads;
     return !a.f32_cache && ratio <= 2 && (a.head_dim == 64 || (a.head_dim == 128 && decoder)) ? 3 : 2;
@@ -1291,6 +1478,7 @@ template <int D, int R>
 void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
                            uint32_t kv_heads, uint32_t heads, uint32_t batch) {
     const bool merge_new = decoder && !k.attend_newest;
+    const bool mv = mfma_values();
     const dim3 ranges(splits, kv_heads, batch), merge(heads, batch);
     const bool sparse = (uint64_t)splits * kv_heads * batch <= (uint64_t)(cus > 0 ? cus : 256);
     if (f32) {
@@ -1303,21 +1491,33 @@ void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool
             attention_combine_kernel<D, R, false, true><<<merge, 256, 0, s>>>(k);
         }
     } else if (decoder) {
-        bool three = false;
+        bool launched = false;
         if constexpr (kThreeWaves<D, R, true>) {
-            three = !sparse;
-            if (three) attention_kernel3<D, R, true><<<ranges, 256, 0, s>>>(k);
+            if (!launched && !sparse) {
+                if (mv) attention_kernel3<D, R, true, true><<<ranges, 256, 0, s>>>(k);
+                else attention_kernel3<D, R, true, false><<<ranges, 256, 0, s>>>(k);
+                launched = true;
+            }
         }
-        if (!three) attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
+        if (!launched) {
+            if (mv) attention_kernel<D, R, true, true><<<ranges, 256, 0, s>>>(k);
+            else attention_kernel<D, R, true, false><<<ranges, 256, 0, s>>>(k);
+        }
         if (merge_new) attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
         else attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     } else {
         bool three = false;
         if constexpr (kThreeWaves<D, R, false>) {
             three = !sparse;
-            if (three) attention_kernel3<D, R, false><<<ranges, 256, 0, s>>>(k);
+            if (three) {
+                if (mv) attention_kernel3<D, R, false, true><<<ranges, 256, 0, s>>>(k);
+                else attention_kernel3<D, R, false, false><<<ranges, 256, 0, s>>>(k);
+            }
         }
-        if (!three) attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
+        if (!three) {
+            if (mv) attention_kernel<D, R, false, true><<<ranges, 256, 0, s>>>(k);
+            else attention_kernel<D, R, false, false><<<ranges, 256, 0, s>>>(k);
+        }
         attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     }
 }
