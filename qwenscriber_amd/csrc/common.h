@@ -182,9 +182,13 @@ hipError_t launch_gemv_batch_multi(hipStream_t s, const void *digits, const Matr
 hipError_t launch_layer_norm_digits(hipStream_t s, const float *x, const float *weight, const float *bias,
                                     uint32_t width, uint32_t tokens, float eps, void *digits);
 // Partial sums only: batch_slices(w) planes [slice][token][row], for a prep
-// to add (the shape must have a split form).
+// to add (the shape must have a split form). With `slices_used`, the K split
+// is chosen for all of the tokens' tiles (never more slices than
+// batch_slices(w), so the same buffer holds them) and its slice count is
+// returned there for the reader of the partial sums.
 hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                   float *partials, const BatchNorm &norm = BatchNorm{});
+                                   float *partials, const BatchNorm &norm = BatchNorm{},
+                                   uint32_t *slices_used = nullptr);
 
 // q4 / q5 GEMM with bf16 activations (gemm.hip). `scratch` holds the split-K
 // partials: gemm_scratch_bytes (0 when the tiles alone fill the device).

@@ -1365,9 +1365,12 @@ int32_t prefill_chunk(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, 
         in.eps = c.eps;
         QWH_TRY(check_hip(d->ctx, launch_prep_batch(s, in, n, H, pf.digits, &pending), "prefill prep"));
         pending = PartialSums{};
-        const uint32_t sq = batch_slices(L.qkv);
-        if (sq > 1)
-            QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.qkv, n, pf.parts, bn), "prefill q|k|v"));
+        // K splits chosen for the chunk's token tiles (fewer slices than the
+        // step's, each workgroup walking more of K).
+        const bool qkv_parts = batch_slices(L.qkv) > 1;
+        uint32_t sq = 1;  // planes of q|k|v partial sums in pf.parts (one: the products themselves)
+        if (qkv_parts)
+            QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.qkv, n, pf.parts, bn, &sq), "prefill q|k|v"));
         else
             QWH_TRY(check_hip(d->ctx, launch_gemv_batch(s, pf.digits, L.qkv, n, pf.qkv, nullptr, false, pf.parts, bn),
                               "prefill q|k|v"));
@@ -1378,7 +1381,7 @@ int32_t prefill_chunk(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, 
         uint8_t *vl = d->values + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
         AttentionArgs aa{};
         aa.out = pf.attn;
-        aa.query = sq > 1 ? pf.parts : pf.qkv;
+        aa.query = qkv_parts ? pf.parts : pf.qkv;
         aa.query_stride = qkv_n;
         if (sq > 1) {
             aa.query_slices = sq;
@@ -1419,21 +1422,23 @@ int32_t prefill_chunk(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, 
                           "prefill attention"));
         // o, gate|up, down as partial sums, each added by the prep that
         // follows (the batched step's sequence).
-        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.o, n, pf.parts), "prefill o"));
+        uint32_t so = 0, sgu = 0, sd = 0;
+        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.o, n, pf.parts, BatchNorm{}, &so), "prefill o"));
         GemvInput norm_in;
         norm_in.mode = GemvInput::RmsNorm;
         norm_in.x = pf.hidden;
         norm_in.norm = L.ffn_norm;
         norm_in.eps = c.eps;
-        const PartialSums o_sums{pf.parts, batch_slices(L.o), H, false, pf.hidden};
+        const PartialSums o_sums{pf.parts, so, H, false, pf.hidden};
         QWH_TRY(check_hip(d->ctx, launch_prep_batch(s, norm_in, n, H, pf.digits, &o_sums), "prefill prep"));
-        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.gu, n, pf.parts, bn), "prefill gate|up"));
+        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.gu, n, pf.parts, bn, &sgu), "prefill gate|up"));
         GemvInput pairs_in;
         pairs_in.mode = GemvInput::F32;
-        const PartialSums gu_sums{pf.parts, batch_slices(L.gu), 2 * c.ffn, true, nullptr};
+        const PartialSums gu_sums{pf.parts, sgu, 2 * c.ffn, true, nullptr};
         QWH_TRY(check_hip(d->ctx, launch_prep_batch(s, pairs_in, n, c.ffn, pf.digits, &gu_sums), "prefill prep"));
-        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.down, n, pf.parts), "prefill down"));
-        pending = PartialSums{pf.parts, batch_slices(L.down), H, false, pf.hidden};
+        QWH_TRY(check_hip(d->ctx, launch_gemv_batch_parts(s, pf.digits, L.down, n, pf.parts, BatchNorm{}, &sd),
+                          "prefill down"));
+        pending = PartialSums{pf.parts, sd, H, false, pf.hidden};
     }
     if (!last) return QWH_OK;  // (only the cache rows of earlier chunks matter)
     // The residual stream after the last layer: the final prep adds the

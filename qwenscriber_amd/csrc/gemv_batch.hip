@@ -1134,9 +1134,10 @@ size_t batch_partial_bytes(uint32_t tokens, const Matrix &w) {
 }
 
 hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matrix &w, uint32_t tokens,
-                                   float *partials, const BatchNorm &norm) {
+                                   float *partials, const BatchNorm &norm, uint32_t *slices_used) {
     if (!batch_format(w.format)) return hipErrorNotSupported;
-    const SplitPlan plan = split_plan(w);
+    const SplitPlan plan = split_plan(w, slices_used ? (tokens + kTokenTile - 1) / kTokenTile : 1);
+    if (slices_used) *slices_used = plan.slices;
     if (!plan.tw || !partials || (w.format == QWH_FORMAT_Q5 && plan.kc != 4)) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     SplitArgs a = split_args(digits, w, tokens, plan, norm);
