@@ -353,24 +353,12 @@ __device__ __forceinline__ void merge_lane_groups(SoftmaxState<R> &st) {
     merge_step<32, R>(st);
 }
 
-// The decoder step's new row joins a range's merged state last: score s
-// (per head, in base 2) with weight 1 and value v (as merge_state does).
-__device__ __forceinline__ void join_new_row(float &M, float &L, float &A, float s, float v) {
-    const float m_new = fmaxf(M, s);
-    const float fa = fast_exp2(M - m_new);
-    const float fb = fast_exp2(s - m_new);
-    L = L * fa + fb;
-    A = A * fa + v * fb;
-    M = m_new;
-}
-
 // The end of a range kernel: the lanes of lane group 0 hold their wave's
 // merged state for their slice (the lane groups already merged), and the
 // waves merge in wave order through LDS into this range's (acc, m, l) record.
 template <int D, int R>
 __device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, const SoftmaxState<R> &st, uint32_t b,
-                                                   uint32_t kvh, uint32_t split, int wave, int sub, int group,
-                                                   const float *new_score, const float *new_value) {
+                                                   uint32_t kvh, uint32_t split, int wave, int sub, int group) {
     constexpr int REC = R * D + 4 * R;
     __shared__ float lds_acc[kWaves][R][D];
     __shared__ float lds_ml[kWaves][R][2];
@@ -401,7 +389,6 @@ __device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, cons
             L += lds_ml[w2][r][1] * f;
             A += lds_acc[w2][r][d] * f;
         }
-        if (new_score) join_new_row(M, L, A, new_score[r], new_value[d]);
         rec[idx] = A;
         if (d == 0) {
             rec[R * D + 4 * r + 0] = M;
@@ -421,8 +408,7 @@ __device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, cons
 template <int D, int R>
 __device__ __forceinline__ void write_range_record_lds(const AttnKernelArgs &a, const SoftmaxState<R> &st,
                                                        const float (&acc)[R][16], uint32_t b, uint32_t kvh,
-                                                       uint32_t split, int wave, int sub, int group,
-                                                       const float *new_score, const float *new_value) {
+                                                       uint32_t split, int wave, int sub, int group) {
     constexpr int LPP = D / 16;
     constexpr int PPW = 64 / LPP;
     constexpr int REC = R * D + 4 * R;
@@ -457,7 +443,6 @@ __device__ __forceinline__ void write_range_record_lds(const AttnKernelArgs &a, 
             L += lds_ml[w][r][1] * f;
             A += part * f;
         }
-        if (new_score) join_new_row(M, L, A, new_score[r], new_value[d]);
         rec[idx] = A;
         if (d == 0) {
             rec[R * D + 4 * r + 0] = M;
@@ -640,30 +625,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         load16(a.rope_now + (size_t)b * D + j0, rc);
         load16(a.rope_now + (size_t)b * D + D / 2 + j0, rs);
     }
-    // The decoder step's new row (position cached - 1, decoder.zig:180-253):
-    // wavefront 1 of each kv head's first range normalizes and rotates its
-    // key, appends the q8 key and value, and joins the row's score and
-    // dequantized value to the range's record, so the merge has records only.
-    // Dimension lane + 64 i per lane; its loads go out with the query's,
-    // before the tiles.
-    constexpr int NI = D / 64;
-    const bool new_row = Decoder && !a.attend_newest && split == 0;
-    const bool nr_wave = new_row && wave == 1;
-    float nkx[NI], nvx[NI], nwk[NI], nrc[NI], nrs[NI];
-    __shared__ float lds_nv[Decoder ? D : 1];   // the new row's dequantized value
-    __shared__ float lds_ns[Decoder ? R : 1];   // its score per query head
-    if (Decoder && nr_wave) {
-        const size_t base = (size_t)b * a.query_stride + (size_t)a.heads * D;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int t = lane + 64 * i;
-            nkx[i] = query_value(a, base + kvh * D + t);
-            nvx[i] = query_value(a, base + kv_width + kvh * D + t);
-            nwk[i] = a.k_norm[t];
-            nrc[i] = a.rope_now[(size_t)b * D + (t % (D / 2))];
-            nrs[i] = a.rope_now[(size_t)b * D + D / 2 + (t % (D / 2))];
-        }
-    }
     Tile cur, nxt;
     load_tile(cur, begin, a.rows);
     if constexpr (Early) load_tile(nxt, begin + kSpan, a.rows);
@@ -687,51 +648,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         rms_norm16<D>(q, wq, a.eps);
         rope16<D>(q, rc, rs, sub);
     }
-    // New row: key codes and group scales stay in wavefront 1's registers
-    // for its scores; the dequantized value goes to LDS for the record.
-    float ncode[NI], nscale[NI];
-    if (Decoder && nr_wave) {
-        // math.rmsNormInPlace over the head (sum of squares in 64-dimension
-        // wavefront sums, added in order), then RoPE (rotate_half).
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) ss += dev::wave_sum(__fmul_rn(nkx[i], nkx[i]));
-        const float inv_k = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
-        float kn[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) kn[i] = __fmul_rn(__fmul_rn(nkx[i], inv_k), nwk[i]);
-        const uint32_t newest = cached - 1;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int t = lane + 64 * i;
-            constexpr int half = D / 2;
-            // Partner dimension t ^ half: another of this lane's values, or
-            // (D = 64) the lane 32 away.
-            float kp;
-            if constexpr (half >= 64) kp = kn[i ^ (half / 64)];
-            else kp = dev::xor_lane<half>(kn[i]);
-            const float c = nrc[i], sn = nrs[i];
-            const float kr = t < half ? __fsub_rn(__fmul_rn(kn[i], c), __fmul_rn(kp, sn))
-                                      : __fadd_rn(__fmul_rn(kn[i], c), __fmul_rn(kp, sn));
-            // quantizeRow(.q8): dimensions 64 i .. 64 i + 63 are one group.
-            const uint16_t kbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(kr)), 128.0f));
-            const uint16_t vbits = dev::f32_to_f16_bits(__fdiv_rn(dev::wave_max(fabsf(nvx[i])), 128.0f));
-            nscale[i] = dev::f16_bits_to_f32(kbits);
-            const float scale_v = dev::f16_bits_to_f32(vbits);
-            const int ck = dev::quantize_one(kr, nscale[i], -128, 127);
-            const int cv = dev::quantize_one(nvx[i], scale_v, -128, 127);
-            ncode[i] = (float)ck;
-            lds_nv[t] = (float)cv * scale_v;
-            const size_t pos_codes = (size_t)newest * kv_width + kvh * D + t;
-            a.k_codes[b * a.code_stride + pos_codes] = (uint8_t)(ck + 128);
-            a.v_codes[b * a.code_stride + pos_codes] = (uint8_t)(cv + 128);
-            if (lane == 0) {
-                const size_t pos_scales = (size_t)newest * gpr + kvh * G + i;
-                reinterpret_cast<uint16_t *>(a.k_scales + b * a.scale_stride)[pos_scales] = kbits;
-                reinterpret_cast<uint16_t *>(a.v_scales + b * a.scale_stride)[pos_scales] = vbits;
-            }
-        }
-    }
     // The query heads and each group's exponent into LDS.
     float amax = 0.0f;
 #pragma unroll
@@ -745,18 +661,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
         if (sub % 4 == 0) lds_exp[qh][sub / 4] = dev::chunk_exponent(amax);
     }
     __syncthreads();
-    if (Decoder && nr_wave) {
-        // The new row's score per query head (kernels.zig:727-735): per
-        // group scale * sum (u - 128) q, the groups added in order, times
-        // the scaling.
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float sc = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NI; ++i) sc += dev::wave_sum(ncode[i] * lds_q[r][lane + 64 * i]) * nscale[i];
-            if (lane == 0) lds_ns[r] = sc * a.scaling;
-        }
-    }
     // Operand rows of this lane: head 4 hs + n / 4, plane n % 4; its values
     // 64 g + 16 quarter .. +15. Score-layout multipliers: head 4 hs + quarter.
     v4i qa[HS][G];
@@ -1031,8 +935,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             st.l[4 * hs + k] = lane_value(lsum, 16 * k);
         }
     }
-    const float *new_score = new_row ? lds_ns : nullptr;
-    const float *new_value = lds_nv;
     if constexpr (MV) {
         // Every wavefront is past its loop: the tile bytes hold the record's
         // parts now. Each lane's sums are its wavefront's whole sums.
@@ -1068,7 +970,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                 L += ml[(w * R + r) * 2 + 1] * f;
                 A += part[(w * R + r) * D + d] * f;
             }
-            if (new_score) join_new_row(M, L, A, new_score[r], new_value[d]);
             rec[idx] = A;
             if (d == 0) {
                 rec[R * D + 4 * r + 0] = M;
@@ -1076,13 +977,13 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             }
         }
     } else if constexpr (R <= 2) {
-        write_range_record_lds<D, R>(a, st, acc, b, kvh, split, wave, sub, group, new_score, new_value);
+        write_range_record_lds<D, R>(a, st, acc, b, kvh, split, wave, sub, group);
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int i = 0; i < 16; ++i) st.acc[r][i] = sum_over_groups<LPP>(acc[r][i]);
-        write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group, new_score, new_value);
+        write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
     }
 }
 
@@ -1217,7 +1118,7 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(const AttnKernelArgs
         if (more) cur = nxt;
     }
     merge_lane_groups<LPP, R>(st);
-    write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group, nullptr, nullptr);
+    write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
 }
 
 // Sum over the D threads 0..D-1 (D/64 whole wavefronts) of the workgroup,
@@ -1571,10 +1472,8 @@ bool attention_supported(uint32_t head_dim, uint32_t ratio) {
 }
 
 // The range kernel and the merge. The decoder form's range kernel
-// normalizes and rotates the queries, and over a q8 cache its first range
-// also appends the step's new row and joins it to its record, so the plain
-// merge follows (so it does after a prefill, whose rows are all in the
-// cache); over an f32 cache the merge forms the new row.
+// normalizes and rotates the queries; with k.attend_newest (a prefill, whose
+// rows are all in the cache) the plain merge follows it.
 template <int D, int R>
 void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
                            uint32_t kv_heads, uint32_t heads, uint32_t batch) {
@@ -1604,8 +1503,8 @@ void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool
             if (mv) attention_kernel<D, R, true, true><<<ranges, 256, 0, s>>>(k);
             else attention_kernel<D, R, true, false><<<ranges, 256, 0, s>>>(k);
         }
-        // (The new row joined the first range's record.)
-        attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
+        if (merge_new) attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
+        else attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     } else {
         bool three = false;
         if constexpr (kThreeWaves<D, R, false>) {
