@@ -300,6 +300,108 @@ def bench_prefill(ctx, qa, audio_steps=390, text_tokens=12, repeats=5):
                 speedup=round(per_token_s / best, 2))
 
 
+def bench_transcribe(ctx, qa, fmt, max_tokens=128, repeats=3):
+    """A 30 s clip through the whole device path, as transcribe.zig:120-219
+    runs it: the convolution front end (3000 mel frames -> 390 encoder rows),
+    the 18 audio layers and the final LayerNorm, the projector, the prompt
+    prefill (390 audio pads in a 12-token template; decoder.zig:308-333) and
+    greedy generation with the stop rules (wasm/model.zig:423-451), on the
+    Qwen3-ASR-0.6B shapes with synthetic weights in `fmt` (q8: the format the
+    reference's status page transcribes with). Synthetic weights rarely
+    predict a stop token, so generation usually runs the full budget."""
+    d, heads, ffn, T, window, layers = 896, 14, 3584, 390, 104, 18
+    mel_bins, frames, n_window, ds = 128, 3000, 50, 480
+    hidden = 1024
+    release, bufs = [], []
+
+    def vec(n, stream, scale):
+        b = ctx.buffer(n * 4)
+        ctx.synth_normal(7, stream, n, scale, b.ptr)
+        bufs.append(b)
+        return b.ptr
+
+    fw = qa.AudioFrontendWeights()
+    for j, (name, cin) in enumerate((("conv1", 1), ("conv2", ds), ("conv3", ds))):
+        wb = ctx.buffer(ds * cin * 9 * 4)
+        ctx.synth_normal(7, 10 + j, ds * cin * 9, 1.0 / math.sqrt(9 * cin), wb.ptr)
+        w16 = ctx.to_device(wb.download(np.float32).astype(np.float16).view(np.uint16))
+        wb.free()
+        bufs.append(w16)
+        setattr(fw, name + "_weight", w16.ptr)
+        setattr(fw, name + "_bias", vec(ds, 20 + j, 0.1))
+    fw.conv_out = ctx.matrix_synthetic(fmt, d, ds * 16, 7, 30, 0.02)
+    release.append(fw.conv_out)
+    tower = []
+    for layer in range(layers):
+        w = qa.AudioLayerWeights()
+        for i, (name, rows, cols) in enumerate((("q", d, d), ("k", d, d), ("v", d, d), ("o", d, d),
+                                                ("ffn_in", ffn, d), ("ffn_out", d, ffn))):
+            m = ctx.matrix_synthetic(fmt, rows, cols, 7, 100 + 16 * layer + i, 0.02)
+            release.append(m)
+            setattr(w, name, m)
+        for j, name in enumerate(qa.AudioLayerWeights.VECTORS):
+            # (Norm weights and biases alike N(0, 0.1): the work does not
+            # depend on the values.)
+            setattr(w, name, vec(ffn if name == "ffn_in_bias" else d, 1000 + 16 * layer + j, 0.1))
+        tower.append(w)
+    ln_w, ln_b = vec(d, 2000, 0.1), vec(d, 2001, 0.1)
+    p_in = ctx.matrix_synthetic(fmt, d, d, 7, 2002, 0.02)
+    p_out = ctx.matrix_synthetic(fmt, hidden, d, 7, 2003, 0.02)
+    release += [p_in, p_out]
+    p_in_b, p_out_b = vec(d, 2004, 0.1), vec(hidden, 2005, 0.1)
+    mel = ctx.buffer(mel_bins * frames * 4)
+    ctx.synth_normal(7, 2006, mel_bins * frames, 1.0, mel.ptr)
+    enc = ctx.buffer(T * d * 4)
+    proj = ctx.buffer(T * hidden * 4)
+    bufs += [mel, enc, proj]
+    cfg = dict(hidden=hidden, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=3072, vocab=151936,
+               max_positions=1024, eps=1e-6, theta=1e6)
+    dec = qa.Decoder(ctx, batch=1, **cfg)
+    dec.init_synthetic(7, fmt)
+    pad, stops = 151676, (151645, 151643)
+    text = 12
+    prompt = (np.arange(T + text, dtype=np.uint32) * 7919 + 13) % cfg["vocab"]
+    prompt[np.isin(prompt, (pad,) + stops)] += 1
+    prompt[text // 2:text // 2 + T] = pad
+    runs = []
+    for i in range(repeats + 1):
+        dec.set_position(0, 0)
+        ctx.sync()
+        t0 = time.perf_counter()
+        steps = ctx.audio_frontend(fw, mel.ptr, mel_bins, frames, n_window, ds, d, enc.ptr, T)
+        for w in tower:
+            ctx.audio_layer(w, enc.ptr, steps, d, heads, ffn, window, 1e-5)
+        ctx.layer_norm(enc.ptr, enc.ptr, ln_w, ln_b, d, steps, 1e-5)
+        ctx.audio_projector(p_in, p_in_b, p_out, p_out_b, enc.ptr, steps, proj.ptr)
+        ctx.sync()
+        t1 = time.perf_counter()
+        first = dec.prefill(0, prompt, pad, proj.ptr, steps)
+        t2 = time.perf_counter()
+        if first in stops:
+            ids, counts = np.zeros((0, 1), np.uint32), np.zeros(1, np.uint32)
+        else:
+            # The first id is emitted as it is; the loop predicts the rest.
+            ids, counts = dec.generate_until([first], max_tokens - 1, stops)
+        t3 = time.perf_counter()
+        if i:
+            runs.append((t1 - t0, t2 - t1, t3 - t2, int(counts[0]) + 1))
+    dec.close()
+    for m in release:
+        ctx.matrix_release(m)
+    for b in bufs:
+        b.free()
+    audio_s, prefill_s, gen_s, tokens = min(runs, key=lambda r: sum(r[:3]))
+    total = audio_s + prefill_s + gen_s
+    return dict(workload="30 s clip, Qwen3-ASR-0.6B shapes, %s weights, q8 cache: front end + 18 audio layers + "
+                          "projector, 402-position prompt prefill, greedy generation with stop rules"
+                          % {qa.FORMAT_Q4: "q4", qa.FORMAT_Q8: "q8"}[fmt],
+                audio_ms=round(audio_s * 1e3, 3), prefill_ms=round(prefill_s * 1e3, 3),
+                first_token_ms=round((audio_s + prefill_s) * 1e3, 3),
+                generated_tokens=tokens, generate_ms=round(gen_s * 1e3, 3),
+                generate_tokens_per_s=round((tokens - 1) / gen_s, 1) if gen_s > 0 else None,
+                total_ms=round(total * 1e3, 3), real_time_factor=round(30.0 / total, 1))
+
+
 def bench_small(ctx, qa, steps):
     from_seed = 1
     out = {}
@@ -494,6 +596,7 @@ def main():
                          "f32kv (q4, f32 cache); 'none' for no step lines")
     ap.add_argument("--skip-headline", action="store_true", help="skip the lm_head GEMV and its read ceiling")
     ap.add_argument("--skip-prefill", action="store_true", help="skip the 30 s prompt prefill")
+    ap.add_argument("--skip-transcribe", action="store_true", help="skip the 30 s clip end to end")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -585,6 +688,10 @@ def main():
         log("decoder 1.7B prefill of a 30 s prompt")
         result["prefill_1p7b_30s_prompt"] = bench_prefill(ctx, qa)
         log(f"prefill: {result['prefill_1p7b_30s_prompt']}")
+    if not args.skip_decoder and not args.skip_transcribe:
+        log("30 s clip end to end (0.6B shapes, q8 weights)")
+        result["transcribe_0p6b_30s_q8"] = bench_transcribe(ctx, qa, qa.FORMAT_Q8)
+        log(f"transcribe: {result['transcribe_0p6b_30s_q8']}")
     if not args.skip_extra:
         log("configs 1, 2 (small shapes), 3, 4")
         result["kernels"] = bench_small(ctx, qa, max(10, args.steps // 2))
