@@ -451,6 +451,9 @@ __device__ __forceinline__ void write_range_record_lds(const AttnKernelArgs &a, 
     }
 }
 
+template <int D>
+__device__ __forceinline__ void write_digits(const AttnKernelArgs &a, uint32_t b, uint32_t h, int col, float4 o);
+
 template <int D, int R, bool Decoder, bool Early, bool MV>
 __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     constexpr int LPP = D / 16;              // value layout: lanes per position
@@ -955,6 +958,36 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                 ml[(wave * R + r) * 2 + 1] = st.l[r];
             }
         __syncthreads();
+        if (Decoder && a.attend_newest && a.splits == 1) {
+            // A prefill row's only range: the merge would read this one
+            // record, so the output (and the next GEMV's digits) is formed
+            // here, as the merge forms it: A * (1 / L), four dimensions per
+            // thread, whole 16-lane rows per 64-value group.
+            for (int t = threadIdx.x; t < R * D / 4; t += blockDim.x) {
+                const int r = t / (D / 4), col = t % (D / 4);
+                float M = ml[r * 2];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml[(w * R + r) * 2]);
+                float L = 0.0f;
+                float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    const float f = fast_exp2(ml[(w * R + r) * 2] - M);
+                    L += ml[(w * R + r) * 2 + 1] * f;
+                    const float4 p = *reinterpret_cast<const float4 *>(&part[(w * R + r) * D + 4 * col]);
+                    A.x += p.x * f;
+                    A.y += p.y * f;
+                    A.z += p.z * f;
+                    A.w += p.w * f;
+                }
+                const float inv = 1.0f / L;
+                const float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+                const uint32_t h = kvh * R + r;
+                *reinterpret_cast<float4 *>(a.out + ((size_t)b * a.heads + h) * D + 4 * col) = o;
+                if (a.digits) write_digits<D>(a, b, h, col, o);
+            }
+            return;
+        }
         constexpr int REC = R * D + 4 * R;
         float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
         for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
@@ -1503,6 +1536,9 @@ void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool
             if (mv) attention_kernel<D, R, true, true><<<ranges, 256, 0, s>>>(k);
             else attention_kernel<D, R, true, false><<<ranges, 256, 0, s>>>(k);
         }
+        // A prefill whose rows each fit one range: the range kernel wrote
+        // the output itself.
+        if (mv && k.attend_newest && splits == 1) return;
         if (merge_new) attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
         else attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     } else {
