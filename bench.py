@@ -431,7 +431,9 @@ def bench_small(ctx, qa, steps):
         x = ctx.buffer(cols * 4)
         ctx.synth_normal(from_seed, 101, cols, 1.0, x.ptr)
         y = ctx.buffer(rows * 4)
-        ms = time_events(ctx, lambda i: ctx.linear(m, x.ptr, cols, 1, y.ptr), steps)
+        # (Host-issued calls of a few us each: 200 of them, after 20
+        # untimed, so one slow host call does not set the mean.)
+        ms = time_events(ctx, lambda i: ctx.linear(m, x.ptr, cols, 1, y.ptr), max(steps, 200), warm=20)
         sweep[name] = dict(us=ms * 1e3, GBs=q4_gemv_bytes(rows, cols) / (ms * 1e-3) / 1e9)
         ctx.matrix_release(m)
         x.free()
