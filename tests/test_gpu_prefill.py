@@ -207,6 +207,8 @@ def device_per_token(ctx, dec, tokens, rows, hidden):
     ("three chunks", TINY, o.Q4, "q8", 600, 0, range(3, 403)),
     ("text only, f32 cache", TINY, o.Q4, "f32", 20, 3, ()),
     ("q8 weights", TINY, o.Q8, "q8", 40, 2, range(5, 25)),
+    ("q5 weights", TINY, o.Q5, "q8", 30, 1, range(3, 13)),
+    ("q5 weights, f32 cache", TINY, o.Q5, "f32", 18, 4, range(2, 8)),
     ("one position", TINY, o.Q4, "q8", 1, 7, ()),
     ("one audio position", TINY, o.Q4, "q8", 1, 0, (0,)),
     ("0.6B head layout", WIDE, o.Q4, "q8", 150, 11, range(4, 124)),
