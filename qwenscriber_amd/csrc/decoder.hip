@@ -1477,8 +1477,32 @@ int32_t qwh_decoder_prefill(qwh_decoder *d, uint32_t seq, const uint32_t *tokens
         return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "position %u + %u prompt tokens exceeds %u", pos0, count,
                     c.max_positions);
     if (!d->planned) QWH_TRY(plan_step(d));
-    if (!prefill_supported(d))
-        return fail(d->ctx, QWH_E_UNSUPPORTED, "prefill needs matrix-core forms of every layer matrix");
+    if (!prefill_supported(d)) {
+        // Shapes without the matrix-core forms (a row whose group count is
+        // not a whole number of chunks): at batch 1 the prompt goes through
+        // the step one position at a time, as decoder.zig:319-331 runs it
+        // (with more sequences the step would advance them as well).
+        if (d->batch != 1)
+            return fail(d->ctx, QWH_E_UNSUPPORTED,
+                        "prefill of a batch > 1 decoder needs matrix-core forms of every layer matrix");
+        uint32_t audio_index = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            const uint32_t t = tokens[i];
+            const int32_t last = i + 1 == count;
+            if (t == audio_pad_token)
+                QWH_TRY(qwh_decoder_forward_rows(d, &t, audio_rows_dev + (size_t)audio_index++ * c.hidden, nullptr, last));
+            else
+                QWH_TRY(qwh_decoder_forward(d, &t, last));
+        }
+        // decoder.zig:332 argmaxLogits, on the device.
+        if (!d->pf.id_dev) QWH_TRY(dalloc(d, 4, reinterpret_cast<void **>(&d->pf.id_dev)));
+        QWH_TRY(qwh_argmax_rows(d->ctx, d->logits, 1, c.vocab, d->pf.id_dev));
+        QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(d->host_stage, d->pf.id_dev, 4, hipMemcpyDeviceToHost, d->ctx->stream),
+                          "prefill id"));
+        QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(d->ctx->stream), "prefill"));
+        *next_token = d->host_stage[0];
+        return QWH_OK;
+    }
     QWH_TRY(prefill_buffers(d));
     qwh_decoder::PrefillBuffers &pf = d->pf;
     hipStream_t s = d->ctx->stream;

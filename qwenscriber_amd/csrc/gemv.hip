@@ -484,9 +484,9 @@ __global__ __launch_bounds__(256) void gemv_q4_generic_kernel(const GemvQ4Args a
     const uint32_t T = a.t;
     const uint32_t gpr = a.k >> 6;
     const size_t row_bytes = a.k >> 1;
-    float *out = a.out + (size_t)token * a.n;
+    float *out = a.out + (size_t)token * (a.pairs ? a.n / 2 : a.n);
     const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
-    for (uint32_t row = wave; row < a.n; row += nwaves) {
+    auto row_dot = [&](uint32_t row) {
         float acc = 0.0f;
         for (uint32_t c = lane; c < T; c += 64) {
             const uint4 code = reinterpret_cast<const uint4 *>(a.data + row * row_bytes)[c];
@@ -500,7 +500,18 @@ __global__ __launch_bounds__(256) void gemv_q4_generic_kernel(const GemvQ4Args a
             const float mult = a.mult[(size_t)token * T + c];
             acc += (float)q4_slice_dot(code, d) * (dev::f16_bits_to_f32(a.scales[(size_t)row * gpr + (c >> 1)]) * mult);
         }
-        acc = dev::wave_sum(acc);
+        return dev::wave_sum(acc);
+    };
+    if (a.pairs) {
+        // Rows 2 j (gate) and 2 j + 1 (up) in one wavefront: siluMul.
+        for (uint32_t j = wave; 2 * j + 1 < a.n; j += nwaves) {
+            const float g = row_dot(2 * j), u = row_dot(2 * j + 1);
+            if (lane == 0) out[j] = silu_mul(g, u);
+        }
+        return;
+    }
+    for (uint32_t row = wave; row < a.n; row += nwaves) {
+        const float acc = row_dot(row);
         if (lane == 0) out[row] = (residual ? residual[row] : 0.0f) + acc;
     }
 }
@@ -1189,7 +1200,7 @@ hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const
         }
     }
     if (done) return err;
-    if (in.mode != GemvInput::Digits || in.pairs) return hipErrorNotSupported;
+    if (in.mode != GemvInput::Digits || (in.pairs && residual)) return hipErrorNotSupported;
     args.row_groups = w.rows;
     gemv_q4_generic_kernel<<<dim3(grid_blocks(gemv_q4_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
     return hipGetLastError();

@@ -291,6 +291,44 @@ def test_prefill_then_prefill_again(ctx):
         ref.close()
 
 
+# A shape without the matrix-core forms (320 = 5 groups of 64 per row).
+ODD = dict(hidden=320, layers=2, heads=5, kv_heads=5, head_dim=64, ffn=448, vocab=1000,
+           max_positions=64, eps=1e-6, theta=1e6)
+
+
+@pytest.mark.parametrize("fmt", [o.Q8, o.Q4])
+def test_prefill_on_a_shape_without_matrix_core_forms(ctx, fmt):
+    # Batch 1: the prompt runs through the step one position at a time
+    # (decoder.zig:319-331 as written), the same checks hold; batch 2 is
+    # refused (the step would advance the other sequence too). At this K the
+    # q4 step takes the generic GEMV (a wavefront per row, per gate / up row
+    # pair for siluMul).
+    seed = 33
+    gpu, ref = make_pair(ctx, ODD, 1, seed, fmt, "q8", [3])
+    try:
+        tokens = prompt(20, ODD["vocab"], range(4, 10), 5)
+        rows = normal(6 * ODD["hidden"], 79, 0, 0.02).reshape(6, ODD["hidden"])
+        rb = ctx.to_device(rows)
+        try:
+            got = gpu.prefill(0, tokens, PAD, rb.ptr, 6)
+        finally:
+            rb.free()
+        want = teacher_forced(ctx, gpu, ref, 0, tokens, rows, 3, ODD, "q8")
+        assert_close(gpu.logits(0), ref.logits(0), what="odd shape, last position (teacher-forced)")
+        assert got == want and gpu.position(0) == 23
+    finally:
+        gpu.close()
+        ref.close()
+    d = qa.Decoder(ctx, batch=2, **ODD)
+    try:
+        d.init_synthetic(seed, fmt)
+        with pytest.raises(qa.QwhError) as err:
+            d.prefill(0, prompt(5, ODD["vocab"], (), 6))
+        assert err.value.status == -3 and d.position(0) == 0
+    finally:
+        d.close()
+
+
 def test_prefill_errors_leave_the_sequence_alone(ctx):
     # decoder.zig:316-317 (UnexpectedShape: an empty prompt), :322 / :331
     # (PromptMismatch: audio pads and rows not one to one) and :142
