@@ -494,8 +494,12 @@ int32_t qwh_decoder_forward_rows(qwh_decoder *decoder, const uint32_t *tokens, c
  * UnexpectedShape / PromptMismatch). The positions are processed together,
  * in chunks of 256: each layer's products run over all of them, their cache
  * rows are appended, then each attends to the cache rows up to its own.
- * Needs a matrix-core form of every layer matrix (QWH_E_UNSUPPORTED
- * otherwise: use qwh_decoder_forward_rows per position). */
+ * Where a layer matrix has no matrix-core form, a batch-1 decoder runs the
+ * prompt through its step one position at a time; a larger batch gets
+ * QWH_E_UNSUPPORTED (the step would advance its other sequences). Tokens
+ * past the vocabulary give QWH_E_SHAPE_MISMATCH and a prompt past
+ * max_positions QWH_E_LIMIT_EXCEEDED; every check runs before any position,
+ * so a refused prompt leaves the sequence as it was. */
 int32_t qwh_decoder_prefill(qwh_decoder *decoder, uint32_t seq, const uint32_t *tokens, uint32_t count,
                             uint32_t audio_pad_token, const float *audio_rows_dev, uint32_t audio_steps,
                             uint32_t *next_token);
