@@ -197,8 +197,11 @@ __global__ __launch_bounds__(256) void rmsnorm_digits_kernel(const float *x, con
 
 // argmaxLogits (decoder.zig:290-301): the largest value, the lowest index
 // among equal maxima. Stage 1: one partial per block of kArgmaxPerBlock
-// logits.
-constexpr uint32_t kArgmaxPerBlock = 4096;
+// logits, four consecutive logits per thread (one 16-byte load where the row
+// is 16-byte aligned), merged across the wavefront and then the workgroup.
+// The merge order does not matter: `better` picks the same (value, index)
+// from any order, and never takes a NaN.
+constexpr uint32_t kArgmaxPerBlock = 1024;
 
 __device__ __forceinline__ void better(float &v, uint32_t &i, float v2, uint32_t i2) {
     if (v2 > v || (v2 == v && i2 < i)) {
@@ -207,37 +210,51 @@ __device__ __forceinline__ void better(float &v, uint32_t &i, float v2, uint32_t
     }
 }
 
+__device__ __forceinline__ void wave_better(float &v, uint32_t &i) {
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const float v2 = __shfl_xor(v, mask, 64);
+        const uint32_t i2 = __shfl_xor(i, mask, 64);
+        better(v, i, v2, i2);
+    }
+}
+
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits, uint32_t count,
                                                              uint32_t per_block, float *pv, uint32_t *pi) {
     const uint32_t b = blockIdx.y;
     const float *row = logits + (size_t)b * count;
     const uint32_t start = blockIdx.x * per_block;
-    uint32_t end = start + per_block;
-    if (end > count) end = count;
+    const uint32_t end = min(start + per_block, count);
+    const bool aligned = (((size_t)b * count + start) & 3) == 0;
     float bv = -FLT_MAX;
     uint32_t bi = 0xffffffffu;
-    for (uint32_t i = start + threadIdx.x; i < end; i += blockDim.x) better(bv, bi, row[i], i);
-    __shared__ float sv[256];
-    __shared__ uint32_t si[256];
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int w = 128; w >= 1; w >>= 1) {
-        if ((int)threadIdx.x < w) {
-            float v = sv[threadIdx.x];
-            uint32_t i = si[threadIdx.x];
-            better(v, i, sv[threadIdx.x + w], si[threadIdx.x + w]);
-            sv[threadIdx.x] = v;
-            si[threadIdx.x] = i;
+    for (uint32_t i = start + threadIdx.x * 4; i < end; i += blockDim.x * 4) {
+        if (aligned && i + 4 <= end) {
+            const float4 v = *reinterpret_cast<const float4 *>(row + i);
+            better(bv, bi, v.x, i);
+            better(bv, bi, v.y, i + 1);
+            better(bv, bi, v.z, i + 2);
+            better(bv, bi, v.w, i + 3);
+        } else {
+            for (uint32_t e = i; e < i + 4 && e < end; ++e) better(bv, bi, row[e], e);
         }
-        __syncthreads();
     }
+    wave_better(bv, bi);
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) better(bv, bi, sv[w], si[w]);
         // A NaN first logit stays the reference's best (no value compares
         // greater than it): index 0 then wins outright.
         const bool nan_first = blockIdx.x == 0 && row[0] != row[0];
-        pv[(size_t)b * gridDim.x + blockIdx.x] = nan_first ? INFINITY : sv[0];
-        pi[(size_t)b * gridDim.x + blockIdx.x] = nan_first ? 0u : si[0];
+        pv[(size_t)b * gridDim.x + blockIdx.x] = nan_first ? INFINITY : bv;
+        pi[(size_t)b * gridDim.x + blockIdx.x] = nan_first ? 0u : bi;
     }
 }
 
@@ -248,12 +265,7 @@ __global__ __launch_bounds__(64) void argmax_rows_finish_kernel(const float *pv,
     float bv = -FLT_MAX;
     uint32_t bi = 0xffffffffu;
     for (uint32_t p = threadIdx.x; p < parts; p += 64) better(bv, bi, pv[(size_t)b * parts + p], pi[(size_t)b * parts + p]);
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        const float v2 = __shfl_xor(bv, mask, 64);
-        const uint32_t i2 = __shfl_xor(bi, mask, 64);
-        better(bv, bi, v2, i2);
-    }
+    wave_better(bv, bi);
     // A row with no value above -FLT_MAX (all -inf or NaN) is the
     // reference's index 0.
     if (threadIdx.x == 0) ids[b] = bi == 0xffffffffu ? 0u : bi;
@@ -295,12 +307,7 @@ __global__ __launch_bounds__(64) void argmax_finish_kernel(const float *pv, cons
     float bv = -FLT_MAX;
     uint32_t bi = 0xffffffffu;
     for (uint32_t p = threadIdx.x; p < parts; p += 64) better(bv, bi, pv[(size_t)b * parts + p], pi[(size_t)b * parts + p]);
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        const float v2 = __shfl_xor(bv, mask, 64);
-        const uint32_t i2 = __shfl_xor(bi, mask, 64);
-        better(bv, bi, v2, i2);
-    }
+    wave_better(bv, bi);
     if (threadIdx.x == 0) {
         // A row of NaN logits leaves no index; the reference then returns 0.
         const uint32_t token = bi == 0xffffffffu ? 0u : bi;

@@ -35,7 +35,7 @@ def test_harness_tie_case(ctx):
 def test_ties_nans_and_infinities(ctx):
     vocab = 151936
     rows = normal(12 * vocab, 41).reshape(12, vocab)
-    rows[0, [4095, 4096, 9000]] = 9.0          # a tie across a block boundary: the first
+    rows[0, [1023, 1024, 4096, 9000]] = 9.0    # a tie across a block boundary: the first
     rows[1, [150000, 70000]] = 9.0              # a later block holds the lower index
     rows[2, 0] = np.nan                          # NaN first: the reference keeps index 0
     rows[3, 5] = np.nan                          # NaN elsewhere is never the maximum
@@ -54,7 +54,7 @@ def test_ties_nans_and_infinities(ctx):
     assert got == want, (got, want)
 
 
-@pytest.mark.parametrize("count", [1, 2, 4095, 4096, 4097, 1000])
+@pytest.mark.parametrize("count", [1, 2, 3, 1000, 1023, 1024, 1025, 1027, 4095, 4096, 4097])
 def test_row_lengths(ctx, count):
     rows = normal(3 * count, 42 + count).reshape(3, count)
     assert device_argmax(ctx, rows) == [o.argmax(r) for r in rows]
