@@ -21,6 +21,8 @@
 // Split K: when the tiles alone cannot fill the device (few tokens, or few
 // weight rows), grid.z splits the groups into ranges; each range writes a
 // partial tile and a second kernel adds the ranges in order (deterministic).
+// When there are a little more tiles than the device holds at once, only
+// the tiles past the last full wave are split (gemm_plan).
 #include "common.h"
 #include "device.h"
 
@@ -43,6 +45,13 @@ struct GemmArgs {
     float *out;              // M x N, or splits x M x N partials
     uint32_t m, n, k;
     uint32_t splits;
+    // Tail form (tail_splits > 0, one-dimensional grid): workgroups 0 ..
+    // full - 1 take tiles 0 .. full - 1 whole (tile t = n tile t % tiles_x,
+    // m tile t / tiles_x) and write `out`; the remaining tiles are split into
+    // tail_splits group ranges each, written as 128 x 128 partial tiles to
+    // `tail` ([tile - full][range][row][column]).
+    uint32_t tail_splits, full, tiles_x;
+    float *tail;
 };
 
 // A group's tile data held in registers between its global loads and its
@@ -143,11 +152,27 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
     const int wave = tid >> 6;
     const int wm = wave >> 1;  // wave's 64-row half of the tile
     const int wn = wave & 1;   // wave's 64-column half
-    const uint32_t n0 = blockIdx.x * BN;
-    const uint32_t m0 = blockIdx.y * BM;
+    uint32_t tx = blockIdx.x, ty = blockIdx.y, z = blockIdx.z, ranges = a.splits, tile = 0;
+    bool partial_tile = false;
+    if (a.tail_splits) {
+        tile = blockIdx.x;
+        z = 0;
+        ranges = 1;
+        if (tile >= a.full) {
+            const uint32_t j = tile - a.full;
+            tile = a.full + j / a.tail_splits;
+            z = j % a.tail_splits;
+            ranges = a.tail_splits;
+            partial_tile = true;
+        }
+        tx = tile % a.tiles_x;
+        ty = tile / a.tiles_x;
+    }
+    const uint32_t n0 = tx * BN;
+    const uint32_t m0 = ty * BM;
     const uint32_t gpr = a.k / BK;
-    const uint32_t g0 = blockIdx.z * gpr / a.splits;
-    const uint32_t g1 = (blockIdx.z + 1) * gpr / a.splits;
+    const uint32_t g0 = z * gpr / ranges;
+    const uint32_t g1 = (z + 1) * gpr / ranges;
 
     // MFMA operand coordinates (32x32x16 layout): lane -> row/col l % 32,
     // k block 8 * (l / 32).
@@ -245,7 +270,22 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
 
     // Store: value r of a lane is row 8 * (r / 4) + 4 * (l / 32) + r % 4 of the
     // 32x32 tile, column l % 32.
-    float *out = a.out + (size_t)blockIdx.z * a.m * a.n;
+    if (partial_tile) {
+        // The whole 128 x 128 partial tile, rows and columns past the
+        // matrix included (the reduce drops them).
+        float *dst = a.tail + ((size_t)(tile - a.full) * a.tail_splits + z) * BM * BN;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                    dst[row * BN + wn * 64 + j * 32 + li] = acc[i][j][r];
+                }
+        return;
+    }
+    float *out = a.out + (size_t)z * a.m * a.n;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -292,6 +332,33 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *partial, 
     }
 }
 
+// The tail tiles' partials, summed over their ranges in order into `out`
+// (rows and columns inside the matrix only): 16 workgroups of 256 threads
+// per tile, four consecutive columns per thread.
+__global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *tail, uint32_t splits, uint32_t full,
+                                                               uint32_t tiles_x, uint32_t m, uint32_t n, float *out) {
+    const uint32_t t = blockIdx.x / 16;
+    const uint32_t e = ((blockIdx.x % 16) * 256 + threadIdx.x) * 4;
+    const uint32_t tile = full + t;
+    const uint32_t mm = (tile / tiles_x) * BM + e / BN;
+    const uint32_t nn = (tile % tiles_x) * BN + e % BN;
+    if (mm >= m) return;
+    const float *src = tail + (size_t)t * splits * BM * BN + e;
+    float4 s = *reinterpret_cast<const float4 *>(src);
+    for (uint32_t z = 1; z < splits; ++z) {
+        const float4 v = *reinterpret_cast<const float4 *>(src + (size_t)z * BM * BN);
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    }
+    float *dst = out + (size_t)mm * n + nn;
+    const float vals[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (nn + c < n) dst[c] = vals[c];
+}
+
 // Ranges of groups per tile so that the grid holds about one workgroup per
 // compute unit, each range at least two groups long, at most 8 ranges (the
 // partials cost 8 bytes of traffic per output per range).
@@ -305,11 +372,40 @@ uint32_t gemm_splits(int cus, uint32_t tokens, const Matrix &w) {
     return splits < 1 ? 1 : splits;
 }
 
+// With more tiles than the device holds at once (two workgroups per CU),
+// the tiles past the last full wave would run as a nearly empty wave of
+// their own: they are split into group ranges instead (at most one
+// workgroup per CU, at most 4 ranges, each at least two groups long).
+struct GemmPlan {
+    uint32_t splits = 1, tail_splits = 0, full = 0, tiles_x = 0, tiles = 0;
+};
+
+GemmPlan gemm_plan(int cus, uint32_t tokens, const Matrix &w) {
+    GemmPlan p;
+    const uint32_t units = (uint32_t)(cus > 0 ? cus : 256);
+    p.tiles_x = (w.rows + BN - 1) / BN;
+    p.tiles = p.tiles_x * ((tokens + BM - 1) / BM);
+    p.splits = gemm_splits(cus, tokens, w);
+    const uint32_t slots = 2 * units;
+    if (p.splits == 1 && p.tiles > slots && getenv("QWH_GEMM_NO_TAIL") == nullptr) {
+        const uint32_t rem = p.tiles % slots;
+        uint32_t ts = rem ? units / rem : 0;
+        if (ts > 4) ts = 4;
+        if (ts > w.cols / BK / 2) ts = w.cols / BK / 2;
+        if (ts >= 2) {
+            p.tail_splits = ts;
+            p.full = p.tiles - rem;
+        }
+    }
+    return p;
+}
+
 }  // namespace
 
 size_t gemm_scratch_bytes(int cus, uint32_t tokens, const Matrix &w) {
-    const uint32_t splits = gemm_splits(cus, tokens, w);
-    return splits > 1 ? (size_t)splits * tokens * w.rows * sizeof(float) : 0;
+    const GemmPlan p = gemm_plan(cus, tokens, w);
+    if (p.tail_splits) return (size_t)(p.tiles - p.full) * p.tail_splits * BM * BN * sizeof(float);
+    return p.splits > 1 ? (size_t)p.splits * tokens * w.rows * sizeof(float) : 0;
 }
 
 hipError_t launch_gemm_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w, uint32_t tokens,
@@ -322,14 +418,25 @@ hipError_t launch_gemm_bf16(hipStream_t s, int cus, const uint16_t *x, const Mat
     args.m = tokens;
     args.n = w.rows;
     args.k = w.cols;
-    args.splits = gemm_splits(cus, tokens, w);
+    const GemmPlan plan = gemm_plan(cus, tokens, w);
+    args.splits = plan.splits;
     args.out = args.splits > 1 ? static_cast<float *>(scratch) : out;
     dim3 grid((w.rows + BN - 1) / BN, (tokens + BM - 1) / BM, args.splits);
+    if (plan.tail_splits) {
+        args.tail_splits = plan.tail_splits;
+        args.full = plan.full;
+        args.tiles_x = plan.tiles_x;
+        args.tail = static_cast<float *>(scratch);
+        grid = dim3(plan.full + (plan.tiles - plan.full) * plan.tail_splits);
+    }
     if (w.format == QWH_FORMAT_Q5)
         gemm_bf16_kernel<true><<<grid, 256, 0, s>>>(args);
     else
         gemm_bf16_kernel<false><<<grid, 256, 0, s>>>(args);
-    if (args.splits > 1) {
+    if (plan.tail_splits) {
+        gemm_tail_reduce_kernel<<<(plan.tiles - plan.full) * 16, 256, 0, s>>>(
+            args.tail, plan.tail_splits, plan.full, plan.tiles_x, tokens, w.rows, out);
+    } else if (args.splits > 1) {
         const size_t count = (size_t)tokens * w.rows;
         gemm_reduce_kernel<<<(unsigned)((count + 1023) / 1024), 256, 0, s>>>(args.out, args.splits, count, out);
     }
