@@ -359,17 +359,34 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *tail
         if (nn + c < n) dst[c] = vals[c];
 }
 
-// Ranges of groups per tile so that the grid holds about one workgroup per
-// compute unit, each range at least two groups long, at most 8 ranges (the
-// partials cost 8 bytes of traffic per output per range).
+// Ranges of groups per tile (1 .. 8, each at least two groups long), chosen
+// by an estimate of the launch's time: the grid runs in waves of two
+// workgroups per CU, a group step taking about 1.7 us when a CU holds two
+// workgroups and 1.0 us when it holds one; each range past the first adds
+// its partials' traffic (8 bytes per output, at about 6.5 TB/s) and the
+// reduce launch. (Measured on MI355X over the configs' shapes, the estimate
+// ranks the split counts in the measured order.) The smallest count wins a
+// tie.
 uint32_t gemm_splits(int cus, uint32_t tokens, const Matrix &w) {
+    const uint32_t units = (uint32_t)(cus > 0 ? cus : 256);
     const uint32_t tiles = ((w.rows + BN - 1) / BN) * ((tokens + BM - 1) / BM);
     const uint32_t groups = w.cols / BK;
-    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256);
-    uint32_t splits = (target + tiles - 1) / tiles;
-    if (splits > groups / 2) splits = groups / 2;
-    if (splits > kMaxSplits) splits = kMaxSplits;
-    return splits < 1 ? 1 : splits;
+    uint32_t most = groups / 2 < kMaxSplits ? groups / 2 : kMaxSplits;
+    if (most < 1) most = 1;
+    uint32_t best = 1;
+    double best_us = 0.0;
+    for (uint32_t s = 1; s <= most; ++s) {
+        const uint64_t items = (uint64_t)tiles * s;
+        const double steps = (double)((groups + s - 1) / s);
+        const uint64_t waves = items / (2 * units), rest = items % (2 * units);
+        double us = (double)waves * steps * 1.7 + (rest ? steps * (rest > units ? 1.7 : 1.0) : 0.0);
+        if (s > 1) us += (double)tokens * w.rows * 4.0 * (s + 1) / 6.5e6 + 2.0;
+        if (s == 1 || us < best_us) {
+            best = s;
+            best_us = us;
+        }
+    }
+    return best;
 }
 
 // With more tiles than the device holds at once (two workgroups per CU),
