@@ -28,6 +28,7 @@
 // lane holds its 16 query values for every head of the group in registers.
 #include <cfloat>
 
+#include "attention_plan.h"
 #include "common.h"
 #include "device.h"
 
@@ -39,8 +40,7 @@ constexpr float kNeg = -1.0e30f;
 // range check is on byte offsets, stride 0).
 constexpr int kBufferWord3 = 0x00020000;  // running-max sentinel: finite, so exp2(kNeg - kNeg) is defined
 constexpr float kLog2e = 1.44269504088896340736f;
-constexpr int kWaves = 4;
-constexpr uint32_t kMaxSplits = 512;
+constexpr int kWaves = (int)plan::kWaves;
 
 struct AttnKernelArgs {
     const float *query;  // row of sequence b at query + b * query_stride; head h at h * D
@@ -100,17 +100,6 @@ __device__ __forceinline__ float query_value(const AttnKernelArgs &a, size_t off
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// The 16 codes of a 16-byte slice as the exact signed values u - 128:
-// XOR 0x80 makes each byte the two's complement of u - 128.
-__device__ __forceinline__ void unpack16(const uint4 w, float (&c)[16]) {
-    const uint32_t v[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) c[i * 4 + b] = (float)(signed char)(v[i] >> (8 * b));
-    }
-}
 
 using dev::group_sum;
 
@@ -248,9 +237,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kTile = 32;                 // positions per wavefront per iteration
+constexpr int kTile = (int)plan::kTile;    // positions per wavefront per iteration
 constexpr int kTileBlocks = kTile / 16;   // 16-position MFMA blocks per tile
-constexpr int kWRow = kTile + 4;          // LDS row of a head's weights (floats)
 
 // LDS stores of this wavefront before its later LDS loads of other lanes'
 // data (LDS operations of one wavefront complete in order; the fences keep
@@ -397,64 +385,13 @@ __device__ __forceinline__ void write_range_record(const AttnKernelArgs &a, cons
     }
 }
 
-// Early: the second tile's loads are issued before the query prologue too
-// (a range of two tiles per wavefront then waits for memory once), at the
-// cost of that tile's registers during the prologue.
-// The end of a range kernel whose wavefronts each keep one maximum per head
-// (shared by all lane groups): every lane stores its accumulators to LDS as
-// they are, and the record's R*D sums are formed by one thread each, over
-// the wavefronts (rescaled to the range's maximum) and their lane groups --
-// no cross-lane reductions. 16 KB of LDS per query head.
-template <int D, int R>
-__device__ __forceinline__ void write_range_record_lds(const AttnKernelArgs &a, const SoftmaxState<R> &st,
-                                                       const float (&acc)[R][16], uint32_t b, uint32_t kvh,
-                                                       uint32_t split, int wave, int sub, int group) {
-    constexpr int LPP = D / 16;
-    constexpr int PPW = 64 / LPP;
-    constexpr int REC = R * D + 4 * R;
-    __shared__ float lds_part[kWaves][PPW][R][D];
-    __shared__ float lds_ml[kWaves][R][2];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-#pragma unroll
-        for (int i = 0; i < 16; i += 4)
-            *reinterpret_cast<float4 *>(&lds_part[wave][group][r][sub * 16 + i]) =
-                make_float4(acc[r][i], acc[r][i + 1], acc[r][i + 2], acc[r][i + 3]);
-        if ((threadIdx.x & 63) == 0) {
-            lds_ml[wave][r][0] = st.m[r];
-            lds_ml[wave][r][1] = st.l[r];
-        }
-    }
-    __syncthreads();
-    float *rec = a.partial + (((size_t)b * a.kv_heads + kvh) * a.splits + split) * REC;
-    for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
-        const int r = idx / D;
-        const int d = idx % D;
-        float M = lds_ml[0][r][0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds_ml[w][r][0]);
-        float L = 0.0f, A = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            float part = 0.0f;
-#pragma unroll
-            for (int g = 0; g < PPW; ++g) part += lds_part[w][g][r][d];
-            const float f = fast_exp2(lds_ml[w][r][0] - M);
-            L += lds_ml[w][r][1] * f;
-            A += part * f;
-        }
-        rec[idx] = A;
-        if (d == 0) {
-            rec[R * D + 4 * r + 0] = M;
-            rec[R * D + 4 * r + 1] = L;
-        }
-    }
-}
-
 template <int D>
 __device__ __forceinline__ void write_digits(const AttnKernelArgs &a, uint32_t b, uint32_t h, int col, float4 o);
 
-template <int D, int R, bool Decoder, bool Early, bool MV>
+// The range kernel. Early: the second tile's loads are issued before the
+// query prologue too (a range of two tiles per wavefront then waits for
+// memory once), at the cost of that tile's registers during the prologue.
+template <int D, int R, bool Decoder, bool Early>
 __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     constexpr int LPP = D / 16;              // value layout: lanes per position
     constexpr int PPW = 64 / LPP;            // value layout: lane groups per wave
@@ -481,13 +418,10 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     const uint8_t *v_codes = a.v_codes + b * a.code_stride;
     const uint32_t key_col = kvh * D + quarter * 16;   // + 64 g
     const uint32_t code_col = kvh * D + sub * 16;
-    const uint32_t vscale_col = kvh * G + sub / 4;
 
     __shared__ float lds_q[R][D];
     __shared__ int lds_exp[R][G];
-    __shared__ float lds_w[MV ? 1 : kWaves][R][kWRow];
-    float(&wrow)[R][kWRow] = lds_w[MV ? 0 : wave];
-    // MV: the values' products on the matrix cores. Per wavefront, the
+    // The values' products run on the matrix cores. Per wavefront, the
     // tile's value codes (signed bytes, [position][dimension], rows padded
     // by 16 bytes so a transposing read's eight rows fall on distinct
     // banks) and the weights' digit planes ([group][head * 4 + plane]
@@ -499,19 +433,18 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     constexpr int kMvWave = kVcBytes + kPlBytes;
     constexpr int kMvRecord = (kWaves * R * D + kWaves * R * 2) * 4;
     constexpr int kMvBytes = kWaves * kMvWave > kMvRecord ? kWaves * kMvWave : kMvRecord;
-    __shared__ __attribute__((aligned(16))) uint8_t lds_mv[MV ? kMvBytes : 16];
-    uint8_t *vcl = lds_mv + (MV ? wave * kMvWave : 0);
+    __shared__ __attribute__((aligned(16))) uint8_t lds_mv[kMvBytes];
+    uint8_t *vcl = lds_mv + wave * kMvWave;
     uint8_t *pll = vcl + kVcBytes;
 
     // A tile: the wavefront's kTile positions from base + wave * kTile; keys
-    // and key scales in the score layout, values and value scales in the
-    // value layout, scales as raw f16 bits.
+    // and key and value scales in the score layout, values in the value
+    // layout, scales as raw f16 bits.
     struct Tile {
         uint4 kc[kTileBlocks][G];
         uint32_t ks[kTileBlocks][G];
         uint4 vc[NV];
-        uint32_t vs[MV ? 1 : NV];                       // value scales, value layout
-        uint32_t vsc[MV ? kTileBlocks : 1][MV ? G : 1];  // MV: value scales, score layout
+        uint32_t vsc[kTileBlocks][G];
     };
     // Every load is unconditional, so all of a tile's loads are in flight
     // together. Plain form: tiles are read through buffer resources that
@@ -525,7 +458,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     // row at or past `limit` clamped to row limit - 1 (one cached line) and
     // masked when the tile is used; the buffer form measured 1-3 % slower
     // there (33.4 against 32.3 us per batch-16 layer, same box).
-    uint32_t key_off[kTileBlocks], kscale_off[kTileBlocks], val_off[NV], vscale_off[NV];
+    uint32_t key_off[kTileBlocks], kscale_off[kTileBlocks], val_off[NV];
 #pragma unroll
     for (int blk = 0; blk < kTileBlocks; ++blk) {
         const uint32_t rel = wave * kTile + 16 * blk + n;
@@ -536,7 +469,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     for (int v = 0; v < NV; ++v) {
         const uint32_t rel = wave * kTile + NV * group + v;
         val_off[v] = rel * kv_width + code_col;
-        vscale_off[v] = (rel * gpr + vscale_col) * 2;
     }
     auto load_tile_global = [&](Tile &t, uint32_t base, uint32_t limit) {
         const uint32_t first = base + wave * kTile;
@@ -548,7 +480,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             for (int g = 0; g < G; ++g) {
                 t.kc[blk][g] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)row * kv_width + key_col + 64 * g);
                 t.ks[blk][g] = k_scales[(size_t)row * gpr + kvh * G + g];
-                if constexpr (MV) t.vsc[blk][g] = v_scales[(size_t)row * gpr + kvh * G + g];
+                t.vsc[blk][g] = v_scales[(size_t)row * gpr + kvh * G + g];
             }
         }
 #pragma unroll
@@ -556,7 +488,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             const uint32_t p = first + NV * group + v;
             const uint32_t row = p < limit ? p : limit - 1;
             t.vc[v] = *reinterpret_cast<const uint4 *>(v_codes + (size_t)row * kv_width + code_col);
-            if constexpr (!MV) t.vs[v] = v_scales[(size_t)row * gpr + vscale_col];
         }
     };
     auto load_tile = [&](Tile &t, uint32_t base_in, uint32_t limit) {
@@ -583,15 +514,13 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                     v4i, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)key_off[blk] + 64 * g, 0, 0));
                 t.kc[blk][g] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
                 t.ks[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(ksr, (int)kscale_off[blk] + 2 * g, 0, 0);
-                if constexpr (MV)
-                    t.vsc[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)kscale_off[blk] + 2 * g, 0, 0);
+                t.vsc[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)kscale_off[blk] + 2 * g, 0, 0);
             }
         }
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const v4i c = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)val_off[v], 0, 0));
             t.vc[v] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
-            if constexpr (!MV) t.vs[v] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)vscale_off[v], 0, 0);
         }
     };
 
@@ -683,30 +612,27 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
     }
 
     // Running state: m (the same in every lane of a head's score row), the
-    // lane's share of l (score layout), acc (value layout; MV: the product
-    // layout, dimension 32 j + lane % 32 of head 2 q + lane / 32 in
-    // acc[j][q], the wavefront's whole sum).
-    constexpr int NB = D / 32;               // MV: 32-dimension blocks of a head row
-    constexpr int HQ = (R + 1) / 2;          // MV: heads per lane in the product layout
-    constexpr int AR = MV ? NB : R, AC = MV ? HQ : 16;
+    // lane's share of l (score layout), acc (the product layout: dimension
+    // 32 j + lane % 32 of head 2 q + lane / 32 in acc[j][q], the wavefront's
+    // whole sum).
+    constexpr int NB = D / 32;               // 32-dimension blocks of a head row
+    constexpr int HQ = (R + 1) / 2;          // heads per lane in the product layout
     float m[HS], l[HS];
-    float acc[AR][AC];
+    float acc[NB][HQ];
 #pragma unroll
     for (int hs = 0; hs < HS; ++hs) {
         m[hs] = kNeg;
         l[hs] = 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < AR; ++r)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int i = 0; i < AC; ++i) acc[r][i] = 0.0f;
-    if constexpr (MV) {
-        // Zero digit planes: plane 3 and heads past R are never written.
+        for (int q = 0; q < HQ; ++q) acc[j][q] = 0.0f;
+    // Zero digit planes: plane 3 and heads past R are never written.
 #pragma unroll
-        for (int g = 0; g < G; ++g) *reinterpret_cast<v4i *>(pll + g * 32 * kTile + 16 * lane) = v4i{0, 0, 0, 0};
-    }
+    for (int g = 0; g < G; ++g) *reinterpret_cast<v4i *>(pll + g * 32 * kTile + 16 * lane) = v4i{0, 0, 0, 0};
 
-    // MV: the tile's values, acc += sum over its positions of (w * scale) *
+    // The tile's values, acc += sum over its positions of (w * scale) *
     // (u - 128), on the matrix cores. The weights times their position's
     // value scale, per head and 64-dimension group, become three signed
     // digit planes of x = rint(w s 2^(22 - e)) (e from the largest of the
@@ -832,9 +758,8 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                 s[hs][blk] = valid[blk] ? sc : kNeg;
             }
         }
-        // Online softmax per head over the tile; the weights go to this
-        // wavefront's LDS rows (MV: stay in registers), the rescale factors
-        // become scalars.
+        // Online softmax per head over the tile; the weights stay in
+        // registers, the rescale factors become scalars.
         float alpha[R];
         float wv[HS][kTileBlocks];
 #pragma unroll
@@ -845,52 +770,18 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             const float m_new = fmaxf(m[hs], row16_max(mx));
             const float al = fast_exp2(m[hs] - m_new);
             float sum = 0.0f;
-            const int rq = 4 * hs + quarter;
 #pragma unroll
             for (int blk = 0; blk < kTileBlocks; ++blk) {
                 const float w = valid[blk] ? fast_exp2(s[hs][blk] - m_new) : 0.0f;
                 sum += w;
-                if constexpr (MV) wv[hs][blk] = w;
-                else if (rq < R) wrow[rq][16 * blk + n] = w;
+                wv[hs][blk] = w;
             }
             l[hs] = l[hs] * al + sum;
             m[hs] = m_new;
 #pragma unroll
             for (int k = 0; k < 4 && 4 * hs + k < R; ++k) alpha[4 * hs + k] = lane_value(al, 16 * k);
         }
-        if constexpr (MV) {
-            use_values_mfma(t, wv, valid, alpha);
-            return;
-        }
-        wave_lds_sync();
-        bool moved = false;
-#pragma unroll
-        for (int r = 0; r < R; ++r) moved |= alpha[r] != 1.0f;
-        if (moved) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[r][i] *= alpha[r];
-        }
-        // Values: acc += (w * scale) * (u - 128).
-        float w[R][NV];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int v = 0; v < NV; ++v) w[r][v] = wrow[r][NV * group + v];
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const float vs = first + NV * group + v < end ? dev::f16_bits_to_f32((uint16_t)t.vs[v]) : 0.0f;
-            float c[16];
-            unpack16(t.vc[v], c);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float wv = w[r][v] * vs;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[r][i] = fmaf(wv, c[i], acc[r][i]);
-            }
-        }
-        wave_lds_sync();
+        use_values_mfma(t, wv, valid, alpha);
     };
 
     // Double buffered, two tiles per trip: the next tile's loads are in
@@ -938,7 +829,7 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             st.l[4 * hs + k] = lane_value(lsum, 16 * k);
         }
     }
-    if constexpr (MV) {
+    {
         // Every wavefront is past its loop: the tile bytes hold the record's
         // parts now. Each lane's sums are its wavefront's whole sums.
         __syncthreads();
@@ -1009,14 +900,6 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                 rec[R * D + 4 * r + 1] = L;
             }
         }
-    } else if constexpr (R <= 2) {
-        write_range_record_lds<D, R>(a, st, acc, b, kvh, split, wave, sub, group);
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) st.acc[r][i] = sum_over_groups<LPP>(acc[r][i]);
-        write_range_record<D, R>(a, st, b, kvh, split, wave, sub, group);
     }
 }
 
@@ -1028,14 +911,14 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
 template <int D, int R, bool Decoder>
 constexpr bool kThreeWaves = R <= 2 && (D == 64 || (D == 128 && Decoder));
 
-template <int D, int R, bool Decoder, bool MV>
+template <int D, int R, bool Decoder>
 __global__ __launch_bounds__(256) void attention_kernel(const AttnKernelArgs a) {
-    attention_range<D, R, Decoder, true, MV>(a);
+    attention_range<D, R, Decoder, true>(a);
 }
 
-template <int D, int R, bool Decoder, bool MV>
+template <int D, int R, bool Decoder>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel3(const AttnKernelArgs a) {
-    attention_range<D, R, Decoder, false, MV>(a);
+    attention_range<D, R, Decoder, false>(a);
 }
 
 
@@ -1438,65 +1321,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float *key, const 
     if (lane == 0) reinterpret_cast<uint16_t *>(scales)[(size_t)position * gpr + g] = bits;
 }
 
-// The values' products on the matrix cores; QWH_ATTN_VALU_VALUES=1 keeps
-// them on the vector ALUs (the earlier form, for comparison).
-bool mfma_values() {
-    static const bool mv = getenv("QWH_ATTN_VALU_VALUES") == nullptr;
-    return mv;
-}
-
-// Workgroups of the range kernel resident per CU: three where the kernel is
-// compiled for three wavefronts per SIMD (kThreeWaves), else two. (With the
-// values on the matrix cores the decoder form also fits four wavefronts per
-// SIMD; four resident workgroups, with the ranges that many more need, ran
-// batch 16 at 7008 tokens/s against 7290.)
-uint32_t resident_groups(const AttentionArgs &a, bool decoder) {
-    const uint32_t ratio = a.heads / a.kv_heads;
-    return !a.f32_cache && ratio <= 2 && (a.head_dim == 64 || (a.head_dim == 128 && decoder)) ? 3 : 2;
-}
-
-// Ranges of `chunk` positions for the decoder form (q/k norms given: the
-// decoder step) or the plain form.
-void attention_shape(int cus, const AttentionArgs &a, bool decoder, uint32_t &chunk, uint32_t &splits) {
-    // Positions per workgroup: a multiple of one workgroup iteration of the
-    // q8 kernel (kTile * kWaves = 128 positions; the f32 kernel's iteration
-    // divides it), at least two of them; as many workgroups as the device
-    // holds at once, at most kMaxSplits ranges. (At batch 1, 128-position ranges
-    // spend more on the per-range query prologue and the combine than their
-    // extra workgroups win back: 17 ranges of 256 beat 34 of 128 at 4096
-    // positions.)
-    const uint32_t step = kTile * kWaves;
-    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256) * resident_groups(a, decoder);
-    const uint32_t pairs = a.batch * a.kv_heads;
-    uint32_t want_splits = (target + pairs - 1) / pairs;
-    if (want_splits < 1) want_splits = 1;
-    if (want_splits > kMaxSplits) want_splits = kMaxSplits;
-    const uint32_t per = (a.capacity + want_splits - 1) / want_splits;
-    chunk = ((per + step - 1) / step) * step;
-    if (chunk < 2 * step) chunk = 2 * step;
-    splits = (a.capacity + chunk - 1) / chunk;
-    if (splits < 1) splits = 1;
-}
-
 }  // namespace
 
-namespace {
-
-size_t record_bytes(const AttentionArgs &a, uint32_t splits) {
-    const uint32_t R = a.heads / a.kv_heads;
-    return (size_t)a.batch * a.kv_heads * splits * (R * a.head_dim + 4 * R) * sizeof(float) + 256;
-}
-
-}  // namespace
-
-// Enough for either form's ranges, so a buffer sized before the norm
-// pointers are known (the decoder's) holds the decoder form's records.
-size_t attention_scratch_bytes(int cus, const AttentionArgs &a) {
-    uint32_t chunk, plain, decoder;
-    attention_shape(cus, a, false, chunk, plain);
-    attention_shape(cus, a, true, chunk, decoder);
-    return record_bytes(a, plain > decoder ? plain : decoder);
-}
+size_t attention_scratch_bytes(int cus, const AttentionArgs &a) { return plan::scratch_bytes(cus, a); }
 
 bool attention_supported(uint32_t head_dim, uint32_t ratio) {
     return (head_dim == 64 && (ratio == 1 || ratio == 2 || ratio == 4)) ||
@@ -1511,7 +1338,6 @@ template <int D, int R>
 void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool decoder, bool f32, uint32_t splits,
                            uint32_t kv_heads, uint32_t heads, uint32_t batch) {
     const bool merge_new = decoder && !k.attend_newest;
-    const bool mv = mfma_values();
     const dim3 ranges(splits, kv_heads, batch), merge(heads, batch);
     const bool sparse = (uint64_t)splits * kv_heads * batch <= (uint64_t)(cus > 0 ? cus : 256);
     if (f32) {
@@ -1526,34 +1352,24 @@ void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool
     } else if (decoder) {
         bool launched = false;
         if constexpr (kThreeWaves<D, R, true>) {
-            if (!launched && !sparse) {
-                if (mv) attention_kernel3<D, R, true, true><<<ranges, 256, 0, s>>>(k);
-                else attention_kernel3<D, R, true, false><<<ranges, 256, 0, s>>>(k);
+            if (!sparse) {
+                attention_kernel3<D, R, true><<<ranges, 256, 0, s>>>(k);
                 launched = true;
             }
         }
-        if (!launched) {
-            if (mv) attention_kernel<D, R, true, true><<<ranges, 256, 0, s>>>(k);
-            else attention_kernel<D, R, true, false><<<ranges, 256, 0, s>>>(k);
-        }
+        if (!launched) attention_kernel<D, R, true><<<ranges, 256, 0, s>>>(k);
         // A prefill whose rows each fit one range: the range kernel wrote
         // the output itself.
-        if (mv && k.attend_newest && splits == 1) return;
+        if (k.attend_newest && splits == 1) return;
         if (merge_new) attention_combine_kernel<D, R, true, false><<<merge, 256, 0, s>>>(k);
         else attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     } else {
         bool three = false;
         if constexpr (kThreeWaves<D, R, false>) {
             three = !sparse;
-            if (three) {
-                if (mv) attention_kernel3<D, R, false, true><<<ranges, 256, 0, s>>>(k);
-                else attention_kernel3<D, R, false, false><<<ranges, 256, 0, s>>>(k);
-            }
+            if (three) attention_kernel3<D, R, false><<<ranges, 256, 0, s>>>(k);
         }
-        if (!three) {
-            if (mv) attention_kernel<D, R, false, true><<<ranges, 256, 0, s>>>(k);
-            else attention_kernel<D, R, false, false><<<ranges, 256, 0, s>>>(k);
-        }
+        if (!three) attention_kernel<D, R, false><<<ranges, 256, 0, s>>>(k);
         attention_combine_kernel<D, R, false, false><<<merge, 256, 0, s>>>(k);
     }
 }
@@ -1568,9 +1384,9 @@ hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArg
                                       size_t scratch_bytes) {
     const bool decoder = a.q_norm != nullptr;
     uint32_t chunk, splits;
-    attention_shape(cus, a, decoder, chunk, splits);
+    plan::attention_shape(cus, a, decoder, chunk, splits);
     // Every range writes a record: refuse a scratch that cannot hold them.
-    if (record_bytes(a, splits) > scratch_bytes) return hipErrorInvalidValue;
+    if (plan::record_bytes(a, splits) > scratch_bytes) return hipErrorInvalidValue;
     const uint32_t R = a.heads / a.kv_heads;
     AttnKernelArgs k{};
     k.query = a.query;

@@ -107,7 +107,8 @@ std::mutex g_scratch_mutex;
 void *g_scratch_address[kMaxDevices] = {};
 
 // Resolves this device's copy of `scratch`, once per device, with that device
-// current (called from qwh_create after hipSetDevice).
+// current (tried by qwh_create after hipSetDevice; a failure there is
+// recorded only by the no-alloc entry point, which tries again).
 int32_t resolve_scratch(int device) {
     if (device < 0 || device >= kMaxDevices) return QWH_E_UNSUPPORTED;
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
@@ -174,12 +175,9 @@ int32_t qwh_create(uint32_t device_index, qwh_ctx **out) {
         delete ctx;
         return QWH_E_DEVICE;
     }
-    // The device's copy of the allocation-free entry point's scratch.
-    if (resolve_scratch(ctx->device) != QWH_OK) {
-        (void)hipStreamDestroy(ctx->stream);
-        delete ctx;
-        return QWH_E_DEVICE;
-    }
+    // The device's copy of the allocation-free entry point's scratch. Only
+    // that entry point needs it: it reports a failure itself.
+    (void)resolve_scratch(ctx->device);
     for (auto &e : ctx->events) {
         if (hipEventCreate(&e) != hipSuccess) {
             qwh_destroy(ctx);
@@ -654,7 +652,16 @@ int32_t qwh_decode_attention_q8_noalloc(qwh_ctx *ctx, float *out_dev, const floa
         return fail(ctx, QWH_E_LIMIT_EXCEEDED, "attention records need %zu bytes; the static scratch holds %zu", need,
                     kNoAllocScratchBytes);
     void *ptr = scratch_address(ctx->device);
-    if (!ptr) return fail(ctx, QWH_E_DEVICE, "device %d has no resolved scratch", ctx->device);
+    if (!ptr) {
+        // Not resolved at qwh_create: once more, with the context's device
+        // current.
+        if (hipSetDevice(ctx->device) != hipSuccess || resolve_scratch(ctx->device) != QWH_OK) {
+            (void)hipGetLastError();
+            return fail(ctx, QWH_E_DEVICE, "device %d: the static scratch's address could not be resolved",
+                        ctx->device);
+        }
+        ptr = scratch_address(ctx->device);
+    }
     // The records need no clearing: each range writes its record before the
     // merge reads it, and ranges past `cached` are never read.
     return check_hip(ctx, launch_decode_attention_q8(ctx->stream, ctx->cus, a, ptr, kNoAllocScratchBytes),

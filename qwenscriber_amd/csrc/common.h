@@ -111,7 +111,7 @@ hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32
 // (kernels.zig:233-239 siluMul): the GEMV writes silu(gate_j) * up_j to
 // out[t][j] (N/2 values per token) instead of the N products.
 struct GemvInput {
-    enum Mode { Digits = 0, F32 = 1, RmsNorm = 2 } mode = Digits;
+    enum Mode { Digits = 0, F32 = 1, RmsNorm = 2, Embed = 4 } mode = Digits;
     const void *digits = nullptr;
     const float *x = nullptr;
     const float *norm = nullptr;
@@ -120,7 +120,31 @@ struct GemvInput {
     // launch_prep_batch, F32 mode only: the values it encodes are
     // gelu(x + bias[col]) (model.zig:866-868) instead of x.
     const float *gelu_bias = nullptr;
+    // Embed (q4, K <= 2048): token t's activations are RMSNorm(norm, eps) of
+    // row tokens[t] of `embed` (decoder.zig:346-376), or of row t of `rows`
+    // where row_flags[t] is set; the row itself is stored to embed_out[t]
+    // and the RoPE table row of position pos[t] (rope_half cos, then sin) to
+    // rope_now[t].
+    const uint32_t *tokens = nullptr;
+    const Matrix *embed = nullptr;
+    const float *rows = nullptr;
+    const uint32_t *row_flags = nullptr;
+    float *embed_out = nullptr;
+    const uint32_t *pos = nullptr;
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    uint32_t rope_half = 0;
+    float *rope_now = nullptr;
+    // Optional output (q4 GEMV, no pairs, no residual): argmaxLogits
+    // partials of each token's outputs, gemv_q4_partials() per token.
+    float *arg_value = nullptr;
+    uint32_t *arg_index = nullptr;
 };
+// Argmax partials per token a q4 GEMV with arg_value leaves (at most 1024).
+constexpr uint32_t kGemvMaxPartials = 1024;
+uint32_t gemv_q4_partials(int cus, const Matrix &w, const GemvInput &in);
+// True when a q4 matrix of this shape has a kernel for the input form
+// `mode` (the Embed form takes rows of at most 2048 values).
+bool gemv_q4_source_supported(int mode, uint32_t rows, uint32_t cols);
 // True when a q4 matrix of this shape has a kernel for the f32 input forms.
 bool gemv_q4_fused_supported(uint32_t rows, uint32_t cols);
 // y[t][n] (+)= W x; residual may alias out.

@@ -197,8 +197,9 @@ __global__ __launch_bounds__(256) void rmsnorm_digits_kernel(const float *x, con
 
 // argmaxLogits (decoder.zig:290-301): the largest value, the lowest index
 // among equal maxima. Stage 1: one partial per block of kArgmaxPerBlock
-// logits, four consecutive logits per thread (one 16-byte load where the row
-// is 16-byte aligned), merged across the wavefront and then the workgroup.
+// logits, four consecutive logits per thread (one 16-byte load where the
+// block's logits start 16-byte aligned), merged across the wavefront and
+// then the workgroup.
 // The merge order does not matter: `better` picks the same (value, index)
 // from any order, and never takes a NaN.
 constexpr uint32_t kArgmaxPerBlock = 1024;
@@ -225,7 +226,9 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits
     const float *row = logits + (size_t)b * count;
     const uint32_t start = blockIdx.x * per_block;
     const uint32_t end = min(start + per_block, count);
-    const bool aligned = (((size_t)b * count + start) & 3) == 0;
+    // 16-byte loads where the block's first logit is 16-byte aligned (every
+    // later load of the thread then is too: the stride is 4 KiB).
+    const bool aligned = (reinterpret_cast<uintptr_t>(row + start) & 15u) == 0;
     float bv = -FLT_MAX;
     uint32_t bi = 0xffffffffu;
     for (uint32_t i = start + threadIdx.x * 4; i < end; i += blockDim.x * 4) {
@@ -258,14 +261,48 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits
     }
 }
 
-// argmaxLogits of each row from the partials: ids[b].
-__global__ __launch_bounds__(64) void argmax_rows_finish_kernel(const float *pv, const uint32_t *pi, uint32_t parts,
-                                                                uint32_t *ids) {
-    const uint32_t b = blockIdx.x;
-    float bv = -FLT_MAX;
-    uint32_t bi = 0xffffffffu;
-    for (uint32_t p = threadIdx.x; p < parts; p += 64) better(bv, bi, pv[(size_t)b * parts + p], pi[(size_t)b * parts + p]);
+// The best of row b's `parts` partials, by a 256-thread workgroup: four
+// partials per thread requested together, merged over the wavefront and
+// then the four wavefronts; the result is valid in thread 0.
+__device__ __forceinline__ void best_of_partials(const float *pv, const uint32_t *pi, uint32_t parts, uint32_t b,
+                                                 float &bv, uint32_t &bi) {
+    bv = -FLT_MAX;
+    bi = 0xffffffffu;
+    const float *rv = pv + (size_t)b * parts;
+    const uint32_t *ri = pi + (size_t)b * parts;
+    for (uint32_t p0 = 0; p0 < parts; p0 += 1024) {
+        float v[4];
+        uint32_t idx[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t p = p0 + threadIdx.x + 256 * q;
+            const uint32_t pc = p < parts ? p : parts - 1;
+            v[q] = rv[pc];
+            idx[q] = ri[pc];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (p0 + threadIdx.x + 256 * q < parts) better(bv, bi, v[q], idx[q]);
+    }
     wave_better(bv, bi);
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < 4; ++w) better(bv, bi, sv[w], si[w]);
+}
+
+// argmaxLogits of each row from the partials: ids[b].
+__global__ __launch_bounds__(256) void argmax_rows_finish_kernel(const float *pv, const uint32_t *pi, uint32_t parts,
+                                                                 uint32_t *ids) {
+    const uint32_t b = blockIdx.x;
+    float bv;
+    uint32_t bi;
+    best_of_partials(pv, pi, parts, b, bv, bi);
     // A row with no value above -FLT_MAX (all -inf or NaN) is the
     // reference's index 0.
     if (threadIdx.x == 0) ids[b] = bi == 0xffffffffu ? 0u : bi;
@@ -298,16 +335,15 @@ __device__ __forceinline__ bool is_stop(const GenState *g, uint32_t token) {
 // emitted; otherwise it is emitted at row count[b], and the sequence ends
 // once it has emitted `budget` ids. A finished sequence is left unchanged
 // (its step recomputes the same row and writes nothing).
-__global__ __launch_bounds__(64) void argmax_finish_kernel(const float *pv, const uint32_t *pi,
-                                                           uint32_t parts, uint32_t *tokens, uint32_t *pos,
-                                                           const uint32_t *hist_base, uint32_t *history,
-                                                           uint32_t batch, uint32_t history_rows,
-                                                           const GenState *gen, uint32_t *done, uint32_t *count) {
+__global__ __launch_bounds__(256) void argmax_finish_kernel(const float *pv, const uint32_t *pi,
+                                                            uint32_t parts, uint32_t *tokens, uint32_t *pos,
+                                                            const uint32_t *hist_base, uint32_t *history,
+                                                            uint32_t batch, uint32_t history_rows,
+                                                            const GenState *gen, uint32_t *done, uint32_t *count) {
     const uint32_t b = blockIdx.x;
-    float bv = -FLT_MAX;
-    uint32_t bi = 0xffffffffu;
-    for (uint32_t p = threadIdx.x; p < parts; p += 64) better(bv, bi, pv[(size_t)b * parts + p], pi[(size_t)b * parts + p]);
-    wave_better(bv, bi);
+    float bv;
+    uint32_t bi;
+    best_of_partials(pv, pi, parts, b, bv, bi);
     if (threadIdx.x == 0) {
         // A row of NaN logits leaves no index; the reference then returns 0.
         const uint32_t token = bi == 0xffffffffu ? 0u : bi;
@@ -392,6 +428,9 @@ struct qwh_decoder {
     bool planned = false;
     bool fused = true;  // every q4 GEMV forms its own activations (no norm / prep kernels)
     bool batched = false;  // batch > 1: int8 digit planes + matrix-core GEMV
+    // Per-token q4 GEMVs (fused, not batched): the embedding gathered by the
+    // first q | k | v GEMV, the argmax partials formed by the lm_head GEMV.
+    bool fold_embed = false, fold_argmax = false;
     void *batch_digits = nullptr;
     // Batched: K-slice partial sums. When every layer matrix has a split
     // form (split_parts), the o, gate|up and down GEMVs leave their partial
@@ -508,6 +547,11 @@ int32_t plan_step(qwh_decoder *d) {
     }
     d->fused = q4_fused;
     d->batched = batch_form;
+    const bool per_token_q4 = q4_fused && !batch_form;
+    const qwh_decoder::Layer &first = d->layers[0];
+    d->fold_embed = per_token_q4 && first.qkv.format == QWH_FORMAT_Q4 &&
+                    gemv_q4_source_supported(GemvInput::Embed, first.qkv.rows, first.qkv.cols);
+    d->fold_argmax = per_token_q4 && d->lm_head.format == QWH_FORMAT_Q4;
     d->split_parts = false;
     d->slices_o = d->slices_gu = d->slices_down = d->slices_qkv = 0;
     if (d->batched) {
@@ -574,9 +618,11 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
         pre.pairs = pairs;
         return launch_gemv_q4_src(s, ctx->cus, pre, w, B, out, residual);
     };
-    embed_kernel<<<B, 256, 0, s>>>(d->tokens_dev, d->embed.format, reinterpret_cast<const uint16_t *>(d->embed.scales),
-                                   d->embed.data, c.hidden, d->hidden, d->pos_dev, d->rope_cos, d->rope_sin,
-                                   c.head_dim / 2, d->rope_now, d->rows_dev, d->row_flags_dev);
+    if (!d->fold_embed)
+        embed_kernel<<<B, 256, 0, s>>>(d->tokens_dev, d->embed.format,
+                                       reinterpret_cast<const uint16_t *>(d->embed.scales), d->embed.data, c.hidden,
+                                       d->hidden, d->pos_dev, d->rope_cos, d->rope_sin, c.head_dim / 2, d->rope_now,
+                                       d->rows_dev, d->row_flags_dev);
     for (uint32_t l = 0; l < c.layers && err == hipSuccess; ++l) {
         qwh_decoder::Layer &L = d->layers[l];
         // Batched with a K split: q | k | v stay partial sums, added by the
@@ -595,6 +641,24 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             bn.rms = true;
             bn.eps = c.eps;
             err = launch_gemv_batch_parts(s, d->batch_digits, L.qkv, B, d->parts, bn);
+        } else if (l == 0 && d->fold_embed) {
+            // embeddingRow (or the audio row) formed by every workgroup; the
+            // first stores it to the residual stream, with the RoPE row.
+            GemvInput in;
+            in.mode = GemvInput::Embed;
+            in.norm = L.attn_norm;
+            in.eps = c.eps;
+            in.tokens = d->tokens_dev;
+            in.embed = &d->embed;
+            in.rows = d->rows_dev;
+            in.row_flags = d->row_flags_dev;
+            in.embed_out = d->hidden;
+            in.pos = d->pos_dev;
+            in.rope_cos = d->rope_cos;
+            in.rope_sin = d->rope_sin;
+            in.rope_half = c.head_dim / 2;
+            in.rope_now = d->rope_now;
+            err = launch_gemv_q4_src(s, ctx->cus, in, L.qkv, B, d->qkv, nullptr);
         } else {
             err = gemv(GemvInput::RmsNorm, d->hidden, L.attn_norm, L.qkv, d->qkv, nullptr, false);
         }
@@ -673,15 +737,32 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
     }
     if (err == hipSuccess) {
         if (want_logits) {
-            err = gemv(GemvInput::RmsNorm, d->hidden, d->final_norm, d->lm_head, d->logits, nullptr, false);
+            uint32_t parts = d->arg_parts;
+            if (d->fold_argmax) {
+                // The lm_head GEMV leaves a (value, row) partial per workgroup.
+                GemvInput in;
+                in.mode = GemvInput::RmsNorm;
+                in.x = d->hidden;
+                in.norm = d->final_norm;
+                in.eps = c.eps;
+                in.arg_value = d->arg_v;
+                in.arg_index = d->arg_i;
+                parts = gemv_q4_partials(ctx->cus, d->lm_head, in);
+                err = parts && parts <= kGemvMaxPartials
+                          ? launch_gemv_q4_src(s, ctx->cus, in, d->lm_head, B, d->logits, nullptr)
+                          : hipErrorInvalidValue;
+            } else {
+                err = gemv(GemvInput::RmsNorm, d->hidden, d->final_norm, d->lm_head, d->logits, nullptr, false);
+                if (err == hipSuccess)
+                    argmax_partial_kernel<<<dim3(d->arg_parts, B), 256, 0, s>>>(d->logits, c.vocab, d->arg_per_block,
+                                                                                 d->arg_v, d->arg_i);
+            }
             if (err == hipSuccess) {
-                argmax_partial_kernel<<<dim3(d->arg_parts, B), 256, 0, s>>>(d->logits, c.vocab, d->arg_per_block,
-                                                                             d->arg_v, d->arg_i);
                 const GenState *gen = static_cast<const GenState *>(d->gen);
                 uint32_t *done = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(d->gen) + sizeof(GenState));
-                argmax_finish_kernel<<<B, 64, 0, s>>>(d->arg_v, d->arg_i, d->arg_parts, d->tokens_dev, d->pos_dev,
-                                                      d->hist_base_dev, d->history_dev, B, d->history_rows, gen, done,
-                                                      done + B);
+                argmax_finish_kernel<<<B, 256, 0, s>>>(d->arg_v, d->arg_i, parts, d->tokens_dev, d->pos_dev,
+                                                       d->hist_base_dev, d->history_dev, B, d->history_rows, gen, done,
+                                                       done + B);
                 err = hipGetLastError();
             }
         } else {
@@ -791,7 +872,7 @@ hipError_t launch_argmax_rows(hipStream_t s, const float *logits, uint32_t rows,
     float *pv = static_cast<float *>(scratch);
     uint32_t *pi = reinterpret_cast<uint32_t *>(pv + (size_t)rows * parts);
     argmax_partial_kernel<<<dim3(parts, rows), 256, 0, s>>>(logits, count, kArgmaxPerBlock, pv, pi);
-    argmax_rows_finish_kernel<<<rows, 64, 0, s>>>(pv, pi, parts, ids);
+    argmax_rows_finish_kernel<<<rows, 256, 0, s>>>(pv, pi, parts, ids);
     return hipGetLastError();
 }
 
@@ -925,8 +1006,10 @@ int32_t qwh_decoder_create_cache(qwh_ctx *ctx, const qwh_decoder_config *config,
     if (st == QWH_OK) st = dalloc(d, d->attn_scratch_bytes, &d->attn_scratch);
     d->arg_per_block = kArgmaxPerBlock;
     d->arg_parts = (c.vocab + d->arg_per_block - 1) / d->arg_per_block;
-    if (st == QWH_OK) st = dalloc(d, sizeof(float) * batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_v));
-    if (st == QWH_OK) st = dalloc(d, 4 * (size_t)batch * d->arg_parts, reinterpret_cast<void **>(&d->arg_i));
+    // Room for either the partial kernel's or the lm_head epilogue's partials.
+    const size_t arg_room = (size_t)batch * std::max(d->arg_parts, kGemvMaxPartials);
+    if (st == QWH_OK) st = dalloc(d, sizeof(float) * arg_room, reinterpret_cast<void **>(&d->arg_v));
+    if (st == QWH_OK) st = dalloc(d, 4 * arg_room, reinterpret_cast<void **>(&d->arg_i));
     if (st == QWH_OK) {
         void *p = nullptr;
         st = check_hip(ctx, hipHostMalloc(&p, 20 * (size_t)batch + sizeof(GenState) + 64, hipHostMallocDefault),

@@ -404,7 +404,7 @@ GemmPlan gemm_plan(int cus, uint32_t tokens, const Matrix &w) {
     p.tiles = p.tiles_x * ((tokens + BM - 1) / BM);
     p.splits = gemm_splits(cus, tokens, w);
     const uint32_t slots = 2 * units;
-    if (p.splits == 1 && p.tiles > slots && getenv("QWH_GEMM_NO_TAIL") == nullptr) {
+    if (p.splits == 1 && p.tiles > slots) {
         const uint32_t rem = p.tiles % slots;
         uint32_t ts = rem ? units / rem : 0;
         if (ts > 4) ts = 4;

@@ -34,7 +34,10 @@
 // for a matrix whose rows alternate gate and up rows, siluMul of each pair
 // (kernels.zig:233-239), so the gate/up projection hands the down projection
 // its f32 input directly.
+#include <cfloat>
 #include <cstdlib>
+#include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 #include "device.h"
@@ -177,8 +180,10 @@ __device__ __forceinline__ int q4_slice_dot(const uint4 codes, const uint32_t (&
     return hi * 4096 + lo;
 }
 
-// Forms of the q4 GEMV's activations.
-enum class Src : int { Digits = 0, F32 = 1, RmsNorm = 2 };
+// Forms of the q4 GEMV's activations: prepared digit planes; f32 values;
+// f32 values after RMSNorm; a token's embedding row (or an audio row) after
+// RMSNorm (Embed: the first q | k | v projection of a decoder step).
+enum class Src : int { Digits = 0, F32 = 1, RmsNorm = 2, Embed = 4 };
 
 struct GemvQ4Args {
     const uint32_t *words;  // Digits: planes, per token T * 24 words
@@ -192,7 +197,38 @@ struct GemvQ4Args {
     const float *residual;  // optional, tokens x N (may alias out); not with pairs
     uint32_t n, k, t, row_groups;
     uint32_t pairs;         // rows 2j, 2j+1 are gate_j, up_j: write silu(gate_j) * up_j
+    // Embed: tokens[token]'s row of the embedding matrix (format
+    // embed_format), or, where row_flags[token] is set, row `token` of
+    // rows; workgroup 0 of each token also stores the row to hidden_out and
+    // the RoPE table row of position pos[token] (rope_half cos, then sin) to
+    // rope_now.
+    const uint32_t *tokens;
+    int32_t embed_format;
+    const uint16_t *embed_scales;
+    const uint8_t *embed_data;
+    const float *rows;
+    const uint32_t *row_flags;
+    float *hidden_out;
+    const uint32_t *pos;
+    const float *rope_cos, *rope_sin;
+    uint32_t rope_half;
+    float *rope_now;
+    // Optional argmax partials of the outputs (decoder.zig:290-301
+    // argmaxLogits, no residual, no pairs): per token and workgroup the
+    // largest output and its lowest row among equal maxima, at
+    // [token * gridDim.x + blockIdx.x].
+    float *arg_value;
+    uint32_t *arg_index;
 };
+
+// The better of two (value, row) candidates of argmaxLogits: the larger
+// value, the lower row among equal values; a NaN is never taken.
+__device__ __forceinline__ void arg_better(float &v, uint32_t &i, float v2, uint32_t i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
 
 // siluMul of one gate / up pair (math.zig:69-71: silu(g) = g / (1 + exp(-g))).
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -217,6 +253,13 @@ struct ActLds {
     float partial[4];
 };
 
+// A value no kernel writes while this one runs (a sequence's position, its
+// token), read through the scalar cache: the wait for it then does not wait
+// for the vector loads issued before it.
+__device__ __forceinline__ uint32_t load_uniform(const uint32_t *p) {
+    return *(const __attribute__((address_space(4))) uint32_t *)p;
+}
+
 // The row's values (and RMSNorm weights) this thread encodes, fetched before
 // the first unit's weights are requested: the wait for them then leaves the
 // weight loads in flight (loads complete in issue order). Threads past the
@@ -224,22 +267,64 @@ struct ActLds {
 struct RowValues {
     float v[3][8];
     float w[3][8];
+    uint32_t tok, audio, pos;  // Embed: the token, its row flag and position
 };
+
+// Embed: values 8 e8 .. 8 e8 + 7 of row `tok` of the embedding matrix
+// (decoder.zig:346-376 embeddingRow; quant.zig:315-345 dequantizeGroup):
+// f32(u - bias) times the group's scale.
+__device__ __forceinline__ void embed_fetch(const GemvQ4Args &a, uint32_t tok, uint32_t e8, float (&out)[8]) {
+    const uint32_t gpr = a.k >> 6;
+    const float scale = dev::f16_bits_to_f32(a.embed_scales[(size_t)tok * gpr + e8 / 8]);
+    if (a.embed_format == QWH_FORMAT_Q4) {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(a.embed_data + (size_t)tok * (a.k / 2) + 4 * e8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = __fmul_rn((float)((int)((w >> (4 * i)) & 0xfu) - 8), scale);
+    } else if (a.embed_format == QWH_FORMAT_Q8) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(a.embed_data + (size_t)tok * a.k + 8 * e8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t word = i < 4 ? w.x : w.y;
+            out[i] = __fmul_rn((float)((int)((word >> (8 * (i & 3))) & 0xffu) - 128), scale);
+        }
+    } else {
+        // q5: the low nibbles as q4, the fifth bit of value j in bit j % 8 of
+        // byte 32 + j / 8 of the group.
+        const uint8_t *g = a.embed_data + ((size_t)tok * gpr + e8 / 8) * 40;
+        const uint32_t j0 = (e8 % 8) * 8;
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(g + j0 / 2);
+        const uint32_t high = g[32 + j0 / 8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = ((w >> (4 * i)) & 0xfu) | (((high >> i) & 1u) << 4);
+            out[i] = __fmul_rn((float)((int)u - 16), scale);
+        }
+    }
+}
 
 template <Src M>
 __device__ __forceinline__ void block_fetch(const GemvQ4Args &a, uint32_t token, RowValues &rv) {
     const int tid = threadIdx.x;
     const uint32_t k8 = a.k / 8;
-    const float4 *row = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k);
     const float4 *norm = reinterpret_cast<const float4 *>(a.norm);
+    if constexpr (M == Src::Embed) {
+        // The token, its row flag and position (scalar loads); the row
+        // itself is requested by embed_issue, after the first unit's weights.
+        rv.tok = load_uniform(a.tokens + token);
+        rv.audio = load_uniform(a.row_flags + token);
+        rv.pos = load_uniform(a.pos + token);
+    }
+    const float4 *row = reinterpret_cast<const float4 *>(a.x + (size_t)token * a.k);
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
         if (p * 256 >= (int)k8) break;  // uniform: no thread has values in this stretch
         const uint32_t e8 = tid + p * 256 < k8 ? tid + p * 256 : k8 - 1;
-        const float4 lo = row[e8 * 2], hi = row[e8 * 2 + 1];
-        rv.v[p][0] = lo.x; rv.v[p][1] = lo.y; rv.v[p][2] = lo.z; rv.v[p][3] = lo.w;
-        rv.v[p][4] = hi.x; rv.v[p][5] = hi.y; rv.v[p][6] = hi.z; rv.v[p][7] = hi.w;
-        if constexpr (M == Src::RmsNorm) {
+        if constexpr (M != Src::Embed) {
+            const float4 lo = row[e8 * 2], hi = row[e8 * 2 + 1];
+            rv.v[p][0] = lo.x; rv.v[p][1] = lo.y; rv.v[p][2] = lo.z; rv.v[p][3] = lo.w;
+            rv.v[p][4] = hi.x; rv.v[p][5] = hi.y; rv.v[p][6] = hi.z; rv.v[p][7] = hi.w;
+        }
+        if constexpr (M == Src::RmsNorm || M == Src::Embed) {
             const float4 wl = norm[e8 * 2], wh = norm[e8 * 2 + 1];
             rv.w[p][0] = wl.x; rv.w[p][1] = wl.y; rv.w[p][2] = wl.z; rv.w[p][3] = wl.w;
             rv.w[p][4] = wh.x; rv.w[p][5] = wh.y; rv.w[p][6] = wh.z; rv.w[p][7] = wh.w;
@@ -247,8 +332,33 @@ __device__ __forceinline__ void block_fetch(const GemvQ4Args &a, uint32_t token,
     }
 }
 
+// Embed's second phase, after the first unit's weights are requested: the
+// token's embedding row (or its audio row) and, in workgroup 0, its RoPE
+// row.
 template <Src M>
-__device__ __forceinline__ void block_encode(const GemvQ4Args &a, const RowValues &rv, ActLds &lds) {
+__device__ __forceinline__ void block_late(const GemvQ4Args &a, uint32_t token, RowValues &rv, float &rope) {
+    const int tid = threadIdx.x;
+    const uint32_t k8 = a.k / 8;
+    const uint32_t e8 = (uint32_t)tid < k8 ? tid : k8 - 1;  // one stretch (K <= 2048)
+    if constexpr (M == Src::Embed) {
+        if (rv.audio) {
+            const float4 *row = reinterpret_cast<const float4 *>(a.rows + (size_t)token * a.k);
+            const float4 lo = row[e8 * 2], hi = row[e8 * 2 + 1];
+            rv.v[0][0] = lo.x; rv.v[0][1] = lo.y; rv.v[0][2] = lo.z; rv.v[0][3] = lo.w;
+            rv.v[0][4] = hi.x; rv.v[0][5] = hi.y; rv.v[0][6] = hi.z; rv.v[0][7] = hi.w;
+        } else {
+            embed_fetch(a, rv.tok, e8, rv.v[0]);
+        }
+        if (blockIdx.x == 0 && tid < (int)(2 * a.rope_half)) {
+            const uint32_t p = rv.pos;
+            rope = tid < (int)a.rope_half ? a.rope_cos[(size_t)p * a.rope_half + tid]
+                                          : a.rope_sin[(size_t)p * a.rope_half + tid - a.rope_half];
+        }
+    }
+}
+
+template <Src M>
+__device__ __forceinline__ void block_encode(const GemvQ4Args &a, const RowValues &rv, ActLds &lds, float rope) {
     const int tid = threadIdx.x;
     const uint32_t k8 = a.k / 8;
     float v[3][8];
@@ -258,7 +368,22 @@ __device__ __forceinline__ void block_encode(const GemvQ4Args &a, const RowValue
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[p][i] = in ? rv.v[p][i] : 0.0f;
     }
-    if constexpr (M == Src::RmsNorm) {
+    if constexpr (M == Src::Embed) {
+        // Workgroup 0 of the token stores its row (the residual stream the
+        // later projections add to) and its RoPE table row.
+        if (blockIdx.x == 0) {
+            const uint32_t token = blockIdx.y;
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                if (p * 256 >= (int)k8 || tid + p * 256 >= (int)k8) break;
+                float4 *dst = reinterpret_cast<float4 *>(a.hidden_out + (size_t)token * a.k + 8 * (tid + p * 256));
+                dst[0] = make_float4(v[p][0], v[p][1], v[p][2], v[p][3]);
+                dst[1] = make_float4(v[p][4], v[p][5], v[p][6], v[p][7]);
+            }
+            if (tid < (int)(2 * a.rope_half)) a.rope_now[(size_t)token * 2 * a.rope_half + tid] = rope;
+        }
+    }
+    if constexpr (M == Src::RmsNorm || M == Src::Embed) {
         // math.zig:120-130: x * (1 / sqrt(mean(x^2) + eps)) * w, the sum of
         // squares reduced over the block (threads, then the four waves in
         // order).
@@ -419,13 +544,19 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
             }
     }
 
+    float rope = 0.0f;
+    if constexpr (M == Src::Embed) block_late<M>(a, token, rv, rope);
     __shared__ __attribute__((aligned(16))) ActLds lds;
-    if constexpr (M != Src::Digits) block_encode<M>(a, rv, lds);
+    if constexpr (M != Src::Digits) block_encode<M>(a, rv, lds, rope);
     uint32_t D[S][24];
     float m[S];
     lane_activations<S, L, M>(a, li, token, D, m, lds);
     if (count) resA = load_res(wave);
 
+    // Argmax partials: this lane's best (value, row) of the rows it writes.
+    const bool track = a.arg_value != nullptr;
+    float best_v = -FLT_MAX;
+    uint32_t best_i = 0xffffffffu;
     auto process = [&](const Slice (&src)[U][S], float res, uint32_t unit) {
         float acc[U];
 #pragma unroll
@@ -446,7 +577,11 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
             const float partner = __shfl_down(total, RG > 1 ? L : (L >> log_u), kWave);
             if (writer && (row & 1u) == 0 && row < a.n) out[row >> 1] = silu_mul(total, partner);
         } else if (writer && row < a.n) {
-            out[row] = res + total;
+            const float y = res + total;
+            out[row] = y;
+            // A NaN first output is argmaxLogits' answer (no value compares
+            // greater than it): row 0 then wins outright.
+            if (track) arg_better(best_v, best_i, row == 0 && y != y ? INFINITY : y, row);
         }
     };
 
@@ -471,6 +606,25 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const GemvQ4Args a) {
     if (full_units < units && full_units % nwaves == wave) {
         load_tail(B, full_units);
         process(B, load_res(full_units), full_units);
+    }
+    if (track) {
+        // The workgroup's best: the wavefront's lanes, then its four waves.
+#pragma unroll
+        for (int mask = 32; mask >= 1; mask >>= 1)
+            arg_better(best_v, best_i, __shfl_xor(best_v, mask, kWave), __shfl_xor(best_i, mask, kWave));
+        __shared__ float arg_v[4];
+        __shared__ uint32_t arg_i[4];
+        if (lane == 0) {
+            arg_v[threadIdx.x >> 6] = best_v;
+            arg_i[threadIdx.x >> 6] = best_i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int w = 1; w < 4; ++w) arg_better(best_v, best_i, arg_v[w], arg_i[w]);
+            a.arg_value[(size_t)token * gridDim.x + blockIdx.x] = best_v;
+            a.arg_index[(size_t)token * gridDim.x + blockIdx.x] = best_i;
+        }
     }
 }
 
@@ -1048,53 +1202,38 @@ uint32_t gcd_u32(uint32_t a, uint32_t b) {
 }
 
 // At most this many blocks (of four wavefronts) per compute unit: fewer
-// concurrent streams keep HBM pages open. QWH_GEMV_BLOCKS_PER_CU overrides it
-// for tuning.
+// concurrent streams keep HBM pages open.
 constexpr int kBlocksPerCu = 4;
 // Row groups per unit for the one-slice q4 kernels (the common shapes).
 constexpr int kUnitRows = 4;
 
 // Units each wavefront takes at least, when the kernel forms its own
-// activations (that prologue is paid once per wavefront). QWH_GEMV_MIN_UNITS
-// overrides it for tuning.
-int min_units_per_wave() {
-    static int units = 0;
-    if (units == 0) {
-        units = 1;
-        if (const char *env = getenv("QWH_GEMV_MIN_UNITS")) {
-            const int v = atoi(env);
-            if (v > 0) units = v;
-        }
-    }
-    return units;
-}
+// activations (that prologue is paid once per wavefront).
+int min_units_per_wave() { return 1; }
 
-int blocks_per_cu_cap() {
-    static int cap = 0;
-    if (cap == 0) {
-        cap = kBlocksPerCu;
-        if (const char *env = getenv("QWH_GEMV_BLOCKS_PER_CU")) {
-            const int v = atoi(env);
-            if (v > 0) cap = v;
-        }
+// Blocks of 256 threads of `kernel` resident per compute unit (at most
+// kBlocksPerCu), from the occupancy of that kernel, asked once per kernel.
+int resident_blocks(const void *kernel) {
+    static std::mutex lock;
+    static std::unordered_map<const void *, int> known;
+    std::lock_guard<std::mutex> guard(lock);
+    auto it = known.find(kernel);
+    if (it != known.end()) return it->second;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0) {
+        (void)hipGetLastError();
+        per_cu = 4;
     }
-    return cap;
+    const int resident = per_cu < kBlocksPerCu ? per_cu : kBlocksPerCu;
+    known.emplace(kernel, resident);
+    return resident;
 }
 
 // Blocks to launch: every unit covered, no more blocks than can be resident
 // at once (each wave then walks its share of the units).
 template <typename Kernel>
 unsigned grid_blocks(Kernel kernel, uint32_t units, int cus, uint32_t per_wave = 1) {
-    static int resident = 0;
-    if (resident == 0) {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0) {
-            (void)hipGetLastError();
-            per_cu = 4;
-        }
-        const int cap = blocks_per_cu_cap();
-        resident = per_cu < cap ? per_cu : cap;
-    }
+    const int resident = resident_blocks(reinterpret_cast<const void *>(kernel));
     uint32_t blocks = (units + 4 * per_wave - 1) / (4 * per_wave);
     uint32_t limit = (uint32_t)(cus > 0 ? cus : 256) * (uint32_t)resident;
     // At most 4096 wavefronts: with rows * 4096 < 2^32 (checked by the
@@ -1105,31 +1244,45 @@ unsigned grid_blocks(Kernel kernel, uint32_t units, int cus, uint32_t per_wave =
     return blocks;
 }
 
+// Launches the kernel (or, with `blocks`, only reports its grid's width).
 template <int S, int L, int U, Src M>
-hipError_t launch_q4(hipStream_t s, int cus, GemvQ4Args args, uint32_t tokens) {
+hipError_t launch_q4(hipStream_t s, int cus, GemvQ4Args args, uint32_t tokens, uint32_t *blocks) {
     args.row_groups = (args.n + (64 / L) - 1) / (64 / L);
     const uint32_t units = (args.row_groups + U - 1) / U;
     auto kernel = gemv_q4_kernel<S, L, U, M>;
     const uint32_t per_wave = M == Src::Digits ? 1u : (uint32_t)min_units_per_wave();
-    kernel<<<dim3(grid_blocks(kernel, units, cus, per_wave), tokens), 256, 0, s>>>(args);
+    const uint32_t grid = grid_blocks(kernel, units, cus, per_wave);
+    if (blocks) {
+        *blocks = grid;
+        return hipSuccess;
+    }
+    kernel<<<dim3(grid, tokens), 256, 0, s>>>(args);
     return hipGetLastError();
 }
 
 template <Src M>
 hipError_t dispatch_q4(hipStream_t s, int cus, const GemvQ4Args &args, uint32_t tokens, uint32_t S, uint32_t L,
-                       bool &done) {
+                       bool &done, uint32_t *blocks = nullptr) {
     done = true;
-    if (S == 1 && L == 64) return launch_q4<1, 64, kUnitRows, M>(s, cus, args, tokens);
-    if (S == 1 && L == 32) return launch_q4<1, 32, kUnitRows, M>(s, cus, args, tokens);
-    if (S == 1 && L == 16) return launch_q4<1, 16, kUnitRows, M>(s, cus, args, tokens);
-    if (S == 1 && L == 8) return launch_q4<1, 8, 4, M>(s, cus, args, tokens);
-    if (S == 1 && L == 4) return launch_q4<1, 4, 4, M>(s, cus, args, tokens);
-    if (S == 1 && L == 2) return launch_q4<1, 2, 2, M>(s, cus, args, tokens);
-    if (S == 2 && L == 64) return launch_q4<2, 64, 4, M>(s, cus, args, tokens);
-    if (S == 3 && L == 64) return launch_q4<3, 64, 2, M>(s, cus, args, tokens);
-    if (S == 3 && L == 32) return launch_q4<3, 32, 2, M>(s, cus, args, tokens);
-    if (S == 3 && L == 16) return launch_q4<3, 16, 2, M>(s, cus, args, tokens);
-    if (S == 3 && L == 2) return launch_q4<3, 2, 2, M>(s, cus, args, tokens);
+    if constexpr (M == Src::Embed) {
+        // One stretch of activations per thread: rows of K <= 2048.
+        if (S == 1 && L == 64) return launch_q4<1, 64, kUnitRows, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 32) return launch_q4<1, 32, kUnitRows, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 16) return launch_q4<1, 16, kUnitRows, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 8) return launch_q4<1, 8, 4, M>(s, cus, args, tokens, blocks);
+    } else {
+        if (S == 1 && L == 64) return launch_q4<1, 64, kUnitRows, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 32) return launch_q4<1, 32, kUnitRows, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 16) return launch_q4<1, 16, kUnitRows, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 8) return launch_q4<1, 8, 4, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 4) return launch_q4<1, 4, 4, M>(s, cus, args, tokens, blocks);
+        if (S == 1 && L == 2) return launch_q4<1, 2, 2, M>(s, cus, args, tokens, blocks);
+        if (S == 2 && L == 64) return launch_q4<2, 64, 4, M>(s, cus, args, tokens, blocks);
+        if (S == 3 && L == 64) return launch_q4<3, 64, 2, M>(s, cus, args, tokens, blocks);
+        if (S == 3 && L == 32) return launch_q4<3, 32, 2, M>(s, cus, args, tokens, blocks);
+        if (S == 3 && L == 16) return launch_q4<3, 16, 2, M>(s, cus, args, tokens, blocks);
+        if (S == 3 && L == 2) return launch_q4<3, 2, 2, M>(s, cus, args, tokens, blocks);
+    }
     done = false;
     return hipSuccess;
 }
@@ -1158,6 +1311,14 @@ bool gemv_q4_fused_supported(uint32_t rows, uint32_t cols) {
     return fused_shape(rows, cols, S, L);
 }
 
+bool gemv_q4_source_supported(int mode, uint32_t rows, uint32_t cols) {
+    uint32_t S, L;
+    if (!fused_shape(rows, cols, S, L)) return false;
+    if (mode == GemvInput::Embed)
+        return cols <= 2048 && S == 1 && (L == 64 || L == 32 || L == 16 || L == 8);
+    return true;
+}
+
 hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32_t cols, void *digits) {
     const uint32_t total8 = tokens * (cols / 8);
     const size_t chunks = (size_t)tokens * (cols / 32);
@@ -1167,9 +1328,21 @@ hipError_t launch_prep_q4(hipStream_t s, const float *x, uint32_t tokens, uint32
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
-                              float *out, const float *residual) {
+namespace {
+
+// Fills the kernel's arguments and launches it (with `blocks`, only reports
+// the grid's width).
+hipError_t q4_src(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens, float *out,
+                  const float *residual, uint32_t *blocks) {
     if (in.pairs && (w.rows & 1u)) return hipErrorInvalidValue;
+    if (in.arg_value && (in.pairs || residual || !in.arg_index)) return hipErrorInvalidValue;
+    if (in.mode == GemvInput::Embed) {
+        const Matrix *e = in.embed;
+        if (!e || e->cols != w.cols || w.cols > 2048 || !in.norm || !in.tokens || !in.rows || !in.row_flags ||
+            !in.embed_out || !in.pos || !in.rope_cos || !in.rope_sin || !in.rope_now || 2 * in.rope_half > 256 ||
+            (e->format != QWH_FORMAT_Q4 && e->format != QWH_FORMAT_Q5 && e->format != QWH_FORMAT_Q8))
+            return hipErrorInvalidValue;
+    }
     GemvQ4Args args{};
     const uint32_t T = w.cols / 32;
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
@@ -1188,22 +1361,57 @@ hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const
         args.words = static_cast<const uint32_t *>(in.digits);
         args.mult = reinterpret_cast<const float *>(args.words + chunks * dev::kChunkWords);
     }
+    if (in.embed) {
+        args.tokens = in.tokens;
+        args.embed_format = in.embed->format;
+        args.embed_scales = reinterpret_cast<const uint16_t *>(in.embed->scales);
+        args.embed_data = in.embed->data;
+    }
+    args.rows = in.rows;
+    args.row_flags = in.row_flags;
+    args.hidden_out = in.embed_out;
+    args.pos = in.pos;
+    args.rope_cos = in.rope_cos;
+    args.rope_sin = in.rope_sin;
+    args.rope_half = in.rope_half;
+    args.rope_now = in.rope_now;
+    args.arg_value = in.arg_value;
+    args.arg_index = in.arg_index;
     uint32_t S = 0, L = 0;
     const bool fused = fused_shape(w.rows, w.cols, S, L);
     bool done = false;
     hipError_t err = hipSuccess;
     if (fused) {
         switch (in.mode) {
-        case GemvInput::Digits: err = dispatch_q4<Src::Digits>(s, cus, args, tokens, S, L, done); break;
-        case GemvInput::F32: err = dispatch_q4<Src::F32>(s, cus, args, tokens, S, L, done); break;
-        case GemvInput::RmsNorm: err = dispatch_q4<Src::RmsNorm>(s, cus, args, tokens, S, L, done); break;
+        case GemvInput::Digits: err = dispatch_q4<Src::Digits>(s, cus, args, tokens, S, L, done, blocks); break;
+        case GemvInput::F32: err = dispatch_q4<Src::F32>(s, cus, args, tokens, S, L, done, blocks); break;
+        case GemvInput::RmsNorm: err = dispatch_q4<Src::RmsNorm>(s, cus, args, tokens, S, L, done, blocks); break;
+        case GemvInput::Embed: err = dispatch_q4<Src::Embed>(s, cus, args, tokens, S, L, done, blocks); break;
         }
     }
     if (done) return err;
-    if (in.mode != GemvInput::Digits || (in.pairs && residual)) return hipErrorNotSupported;
+    if (in.mode != GemvInput::Digits || (in.pairs && residual) || in.arg_value) return hipErrorNotSupported;
     args.row_groups = w.rows;
-    gemv_q4_generic_kernel<<<dim3(grid_blocks(gemv_q4_generic_kernel, w.rows, cus), tokens), 256, 0, s>>>(args);
+    const uint32_t grid = grid_blocks(gemv_q4_generic_kernel, w.rows, cus);
+    if (blocks) {
+        *blocks = grid;
+        return hipSuccess;
+    }
+    gemv_q4_generic_kernel<<<dim3(grid, tokens), 256, 0, s>>>(args);
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_q4_src(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
+                              float *out, const float *residual) {
+    return q4_src(s, cus, in, w, tokens, out, residual, nullptr);
+}
+
+uint32_t gemv_q4_partials(int cus, const Matrix &w, const GemvInput &in) {
+    uint32_t blocks = 0;
+    if (q4_src(nullptr, cus, in, w, 1, nullptr, nullptr, &blocks) != hipSuccess) return 0;
+    return blocks;
 }
 
 hipError_t launch_gemv_q4(hipStream_t s, int cus, const void *digits, const Matrix &w, uint32_t tokens,

@@ -1007,34 +1007,24 @@ struct SplitPlan {
     uint32_t slices = 1, slice_groups = 0;
 };
 
-int env_int(const char *name, int fallback) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : fallback;
-}
-
 // `tiles`: the 16-token tiles of the call, which multiply the workgroups as
 // the K slices do (the decoder's slice counts are planned for one tile).
 SplitPlan split_plan(const Matrix &w, uint32_t tiles = 1) {
-    // Tuning overrides, read once.
-    static const int env_tw = env_int("QWH_SPLIT_TW", 0), env_kc = env_int("QWH_SPLIT_KC", 0),
-                     env_s = env_int("QWH_SPLIT_S", 0), env_off = env_int("QWH_SPLIT_OFF", 0);
     SplitPlan p;
     const uint32_t gpr = w.cols / 64;
-    if (gpr % 2u || env_off) return p;
+    if (gpr % 2u) return p;
     // Chunks of 4 groups, or of 2 where the group count is not a multiple of
     // 4 (the audio tower's 896-wide rows: 14 groups).
     p.kc = gpr % 4u ? 2 : 4;
     const uint32_t row_tiles = (w.rows + kRowTile - 1) / kRowTile;
     // Two tiles per wavefront once that still leaves 64 workgroups, else one.
     p.tw = row_tiles >= 4u * 2u * 64u ? 2 : 1;
-    if (env_tw == 1 || env_tw == 2) p.tw = env_tw;
-    if ((env_kc == 4 || env_kc == 8) && gpr % (uint32_t)env_kc == 0) p.kc = env_kc;
     const uint32_t chunks = gpr / (uint32_t)p.kc;
     const uint32_t blocks = (row_tiles + 4u * p.tw - 1) / (4u * p.tw) * (tiles ? tiles : 1);
     // K slices: about 512 workgroups in all and at most about 4 chunks in
     // a row per workgroup (its chunks are one memory round trip each), a
     // divisor of the chunk count, at most kMaxSlices.
-    uint32_t want = env_s > 0 ? (uint32_t)env_s : std::max((512u + blocks - 1) / blocks, (chunks + 3) / 4);
+    uint32_t want = std::max((512u + blocks - 1) / blocks, (chunks + 3) / 4);
     p.slices = 1;
     for (uint32_t c = 1; c <= chunks && c <= want && c <= kMaxSlices; ++c)
         if (chunks % c == 0) p.slices = c;
@@ -1044,17 +1034,14 @@ SplitPlan split_plan(const Matrix &w, uint32_t tiles = 1) {
 
 template <int BPG>
 void launch_split_bpg(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, dim3 grid) {
+    // Chunks of 2 or 4 groups (split_plan), one or two row tiles per wave.
     if (plan.kc == 2) {
         if (plan.tw == 2) gemv_split_kernel<2, 2, BPG><<<grid, 256, 0, s>>>(a);
         else gemv_split_kernel<1, 2, BPG><<<grid, 256, 0, s>>>(a);
-    } else if (plan.tw == 2 && plan.kc == 4) {
-        gemv_split_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(a);
     } else if (plan.tw == 2) {
-        gemv_split_kernel<2, 8, BPG><<<grid, 256, 0, s>>>(a);
-    } else if (plan.kc == 4) {
-        gemv_split_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(a);
+        gemv_split_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(a);
     } else {
-        gemv_split_kernel<1, 8, BPG><<<grid, 256, 0, s>>>(a);
+        gemv_split_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(a);
     }
 }
 

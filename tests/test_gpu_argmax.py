@@ -58,3 +58,23 @@ def test_ties_nans_and_infinities(ctx):
 def test_row_lengths(ctx, count):
     rows = normal(3 * count, 42 + count).reshape(3, count)
     assert device_argmax(ctx, rows) == [o.argmax(r) for r in rows]
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_rows_not_16_byte_aligned(ctx, offset):
+    # Logits that start 4, 8 or 12 bytes past a 16-byte boundary (a slice of
+    # a larger buffer): every row and block then starts unaligned, and the
+    # kernel reads them without 16-byte loads.
+    count = 4099
+    rows = normal(2 * count, 43 + offset).reshape(2, count)
+    rows[1, 2050] = 9.0
+    flat = np.concatenate([np.zeros(offset, np.float32), rows.reshape(-1)])
+    x = ctx.to_device(flat)
+    ids = ctx.buffer(8)
+    try:
+        ctx.argmax_rows(x.ptr + 4 * offset, 2, count, ids.ptr)
+        got = ids.download(np.uint32).tolist()
+    finally:
+        x.free()
+        ids.free()
+    assert got == [o.argmax(r) for r in rows]

@@ -136,6 +136,7 @@ def test_free_running_token_ids(ctx, tiny_pair):
     (1, ()),                                                   # lane-per-row GEMVs, fused inputs
     (2, ("QWH_DECODER_PER_TOKEN",)),                           # batch > 1 on the per-token GEMVs
     (2, ("QWH_DECODER_PER_TOKEN", "QWH_DECODER_UNFUSED")),     # separate norm / SiLU / digit kernels
+    (1, ("QWH_NO_GRAPH",)),                                    # kernels launched one by one, no graph replay
 ])
 def test_token_ids_on_each_gemv_path(ctx, batch, env, monkeypatch):
     # The default batch > 1 path (matrix-core GEMVs) is covered above; the
@@ -174,6 +175,7 @@ ODD = dict(hidden=320, layers=2, heads=5, kv_heads=5, head_dim=64, ffn=448, voca
     (18, TINY, ()),                             # two 16-token tiles of partial sums and digit planes
     (3, TINY, ("QWH_DECODER_NO_SPLIT",)),      # o / gate|up / down add their own slices
     (3, ODD, ()),                               # unsplit kernel, RMSNorm factor in its epilogue
+    (3, TINY, ("QWH_NO_GRAPH",)),              # kernels launched one by one, no graph replay
 ])
 def test_token_ids_on_each_batched_form(ctx, batch, config, env, monkeypatch):
     for name in env:

@@ -7,9 +7,12 @@ prefilled to 4096 positions, seed 4) against the CPU oracle:
     sample across the vocabulary), within 1e-3 relative and within the
     per-step error bound below;
   - 256 greedy steps per sequence against the oracle's ids in
-    tests/golden/decoder_1p7b_ids.json (tests/golden/make_decoder_ids.py),
-    identical but for runner-up picks inside the tie window the error bound
-    gives (44 of the fixture's 4096 steps lie inside it).
+    tests/golden/decoder_1p7b_ids.json (tests/golden/make_decoder_ids.py):
+    at batch 1 all 256 identical; at batch 16 at least 15 of the 16
+    sequences and 3967 of the 4096 steps identical (the one sequence that
+    differs takes the oracle's runner-up at step 127, inside the tie window
+    the error bound gives; 44 of the fixture's 4096 steps lie inside it);
+    the q8-weight fixture identical in full at both batches.
 
 decoder.zig:133-339 (forwardToken, step, argmaxLogits)."""
 import json
@@ -69,13 +72,15 @@ def run(ctx, golden, batch):
         dec.close()
 
 
-def check(ids, golden, batch):
+def check(ids, golden, batch, min_sequences, min_steps):
     """Every sequence matches the oracle's greedy ids, but for a near tie: at
     the first differing step the GPU took the oracle's runner-up, and the
     oracle's two best logits lie within tie_window(step) of each other. From
     there the sequence continues from another token, so its comparison ends;
-    the other sequences are still compared in full. Returns (identical
-    sequences, identical steps)."""
+    the other sequences are still compared in full. At least min_sequences
+    sequences and min_steps steps (summed up to each sequence's first
+    difference) must be identical: a flip inside the window still counts
+    against them."""
     same_seqs = same_steps = 0
     for b in range(batch):
         expected = golden["ids"][b][1:]
@@ -93,7 +98,8 @@ def check(ids, golden, batch):
             f"{msg}: oracle logits {top} and {second} are not a near tie"
         print(f"{msg}: the oracle's runner-up, {(top - second) / abs(top):.2e} below its best")
     print(f"identical: {same_seqs} of {batch} sequences, {same_steps} of {batch * golden['steps']} steps")
-    return same_seqs, same_steps
+    assert same_seqs >= min_sequences and same_steps >= min_steps, \
+        f"identical {same_seqs} sequences / {same_steps} steps, fewer than {min_sequences} / {min_steps}"
 
 
 def check_logits(ctx, golden, ref, batch):
@@ -141,7 +147,7 @@ def test_batch16_teacher_forced_logits(ctx):
 def test_batch1_greedy_ids_match_oracle(ctx):
     # Batch 1 runs the lane-per-row GEMVs with fused activation forms.
     golden = load(IDS)
-    check(run(ctx, golden, 1), golden, 1)
+    check(run(ctx, golden, 1), golden, 1, 1, golden["steps"])
 
 
 def test_batch16_greedy_ids_match_oracle(ctx):
@@ -150,7 +156,9 @@ def test_batch16_greedy_ids_match_oracle(ctx):
     batch = len(golden["ids"])
     if batch < 2:
         pytest.skip("golden file holds one sequence")
-    check(run(ctx, golden, batch), golden, batch)
+    # Measured: 15 of 16 sequences, 3967 of 4096 steps (sequence 11 takes
+    # the runner-up at step 127, 1.9e-5 below the best logit).
+    check(run(ctx, golden, batch), golden, batch, batch - 1, 3967)
 
 
 def test_q8_model_greedy_ids_match_oracle(ctx):
@@ -159,7 +167,8 @@ def test_q8_model_greedy_ids_match_oracle(ctx):
     # batch 1 (byte-plane GEMV) and at the fixture's batch (q8 on the matrix
     # cores).
     golden = load(os.path.join(HERE, "decoder_1p7b_q8_ids.json"))
-    check(run(ctx, golden, 1), golden, 1)
+    steps = golden["steps"]
+    check(run(ctx, golden, 1), golden, 1, 1, steps)
     batch = len(golden["ids"])
     if batch > 1:
-        check(run(ctx, golden, batch), golden, batch)
+        check(run(ctx, golden, batch), golden, batch, batch, batch * steps)

@@ -62,11 +62,14 @@ def test_gemm_edge_shapes(ctx, rows, cols, m):
     assert_close(actual, expected, what=f"gemm {m}x{rows}x{cols}")
 
 
-@pytest.mark.parametrize("rows,cols,m", [(6144, 2048, 390), (2048, 6144, 128), (100, 128, 1), (130, 256, 7),
-                                         (257, 192, 33), (64, 64, 130)])
+@pytest.mark.parametrize("rows,cols,m", [(6144, 2048, 390), (6144, 2048, 1500), (2048, 6144, 128), (100, 128, 1),
+                                         (130, 256, 7), (257, 192, 33), (64, 64, 130)])
 def test_q5_gemm(ctx, rows, cols, m):
     # q5 planes (quant.zig:253-269): 40-byte groups, fifth bits in the last 8.
-    # M = 390 is the audio-token count of a 30 s window.
+    # M = 390 is the audio-token count of a 30 s window. M = 1500 at
+    # [6144 x 2048] is 576 tiles, more than the two per CU a 256-CU device
+    # holds at once: the tiles past the last full wave run as group ranges
+    # whose partial tiles a reduce kernel adds (the tail form).
     w = o.normal(rows * cols, 15, rows, 0.02).reshape(rows, cols)
     w[0, :64] = np.float32(-1.0)   # codes at both ends of [-16, 15]
     w[0, 64:128] = np.float32(1.0)

@@ -242,9 +242,13 @@ def test_prefill_matches_per_token_reference(ctx, name, config, fmt, cache, coun
         # step agrees within the same bar.
         assert_close(logits, twin.logits(1), what=f"{name}: against the device step")
         if got != want:
-            # Only a near tie between the two best logits may change the id.
+            # The device may pick another id only where the oracle's logits
+            # of the two ids lie within twice this test's measured logit
+            # error of each other (each of the two carries at most that
+            # error).
+            err = float(np.max(np.abs(logits.astype(np.float64) - expected)))
             best = float(np.max(expected))
-            assert best - float(expected[got]) <= 2e-3 * float(np.abs(expected).max()), (got, want)
+            assert best - float(expected[got]) <= 2 * err, (got, want, best - float(expected[got]), err)
         # Greedy steps after the prompt (the other sequence steps beside it).
         tokens = [o.start_token(seed, 0, config["vocab"]), want]
         for step in range(4):
