@@ -251,7 +251,12 @@ def bench_decoder(ctx, qa, batch, steps, warmup, fmt=None, cache=None):
         dec.prefill_random(b, 4096, 4)
     log(f"decoder B={batch}: model + cache ready in {time.perf_counter() - t0:.1f} s")
     tokens = np.arange(batch, dtype=np.uint32) * 7919 % cfg["vocab"]
+    # Untimed steps capture the step graph; the caches are then prefilled
+    # again, so the timed steps are configs[4]'s: positions 4096 .. 4096 +
+    # steps - 1 from a 4096-position cache.
     ids = dec.generate(tokens, warmup)
+    for b in range(batch):
+        dec.prefill_random(b, 4096, 4)
     ctx.sync()
     ctx.event_record(2)
     ids = dec.generate(ids[-1], steps)
@@ -262,14 +267,14 @@ def bench_decoder(ctx, qa, batch, steps, warmup, fmt=None, cache=None):
     hs, ffn, qw, kvw, vocab = 2048, 6144, 2048, 1024, 151936
     per_layer = qw * hs + 2 * kvw * hs + hs * qw + 2 * ffn * hs + hs * ffn
     weights = (28 * per_layer + vocab * hs) * (qa.DATA_BYTES[fmt] + 2) // 64
-    pos_mid = 4096 + warmup + steps / 2
+    pos_mid = 4096 + (steps - 1) / 2 + 1  # rows attended, averaged over the timed steps
     row = kvw + kvw // 64 * 2 if cache == qa.CACHE_Q8 else 4 * kvw
     kv = batch * 28 * 2 * pos_mid * row
     step_ms = ms / steps
     gbs = (weights + kv) / (step_ms * 1e-3) / 1e9
     return dict(batch=batch, tokens_per_s=batch * steps / (ms * 1e-3), ms_per_step=step_ms,
                 bytes_per_step=int(weights + kv), achieved_GBs=gbs, frac=gbs / HBM_PEAK_GBS,
-                context=f"4096..{4096 + warmup + steps}")
+                context=f"positions 4096..{4096 + steps - 1} (cache of 4096 rows prefilled, then {steps} greedy steps)")
 
 
 def bench_prefill(ctx, qa, audio_steps=390, text_tokens=12, repeats=5):
@@ -534,6 +539,18 @@ def bench_audio(ctx, qa, steps):
     # The residual stream changes every call (as a tower's layers do); the
     # work per call does not depend on the values.
     layer_ms = time_events(ctx, lambda i: ctx.audio_layer(weights, enc.ptr, T, d, heads, ffn, window, 1e-5), steps)
+    # The same layer in q5 (the WebGPU path's format for every quantized tower
+    # matrix, passes.ts:63-67): 896-wide rows of 14 groups.
+    q5 = {}
+    for i, (name, rows, cols) in enumerate((("q", d, d), ("k", d, d), ("v", d, d), ("o", d, d),
+                                            ("ffn_in", ffn, d), ("ffn_out", d, ffn))):
+        q5[name] = ctx.matrix_synthetic(qa.FORMAT_Q5, rows, cols, 5, i, 0.02)
+        setattr(weights, name, q5[name])
+    ctx.synth_normal(5, 200, T * d, 1.0, enc.ptr)
+    layer_q5_ms = time_events(ctx, lambda i: ctx.audio_layer(weights, enc.ptr, T, d, heads, ffn, window, 1e-5),
+                              steps)
+    for m in q5.values():
+        ctx.matrix_release(m)
     qkv = ctx.buffer(T * 3 * d * 4)
     ctx.synth_normal(5, 201, T * 3 * d, 1.0, qkv.ptr)
     att = ctx.buffer(T * d * 4)
@@ -589,6 +606,7 @@ def bench_audio(ctx, qa, steps):
         "frontend_workload": "3000 mel frames x 128 bins, 30 chunks, 3 convolutions of 480 channels (f16 weights, "
                              "f32 FMA), conv_out 896 x 7680 q4, 390 rows",
         "layer_us": layer_ms * 1e3, "layer_TFLOPs": (layer_flops + att_flops) / (layer_ms * 1e-3) / 1e12,
+        "layer_q5_us": layer_q5_ms * 1e3, "layer_q5_TFLOPs": (layer_flops + att_flops) / (layer_q5_ms * 1e-3) / 1e12,
         "tower_18_layers_ms": 18 * layer_ms,
         "attention_us": att_ms * 1e3, "attention_GFLOPs": att_flops / (att_ms * 1e-3) / 1e9,
         "projector_us": proj_ms * 1e3,
@@ -657,7 +675,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i4 x i4 -> i32 dot products, f32 combine and accumulate (q4 weights, f32 activations)",
+        "dtype": "q4 weights x f32 activations: each 32-value activation chunk as exact 23-bit block integers "
+                 "(six signed hex digits, power-of-two chunk scale), exact integer dot products per 32 weights "
+                 "(v_dot8_i32_i4), f32 group scale and accumulate",
         "data": "synthetic",
         "config": {"workload": "q4 GEMV, Qwen3-0.6B lm_head [151936 x 1024], batch 1, group-64 f16 scales "
                                "(configs[1] graded shape), weights rotated over %d copies (%.2f GB)"
@@ -681,7 +701,7 @@ def main():
         dec = {}
         for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
             log(f"decoder 1.7B, batch {batch}")
-            dec[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8)
+            dec[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=256, warmup=8)
             log(f"decoder batch {batch}: {dec[f'b{batch}']['tokens_per_s']:.0f} tok/s")
         result["decoder_1p7b_q4_q8kv_ctx4096"] = dec
     # The same model with q8 weights (the format the reference's status page
@@ -691,17 +711,17 @@ def main():
         q8 = {}
         for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
             log(f"decoder 1.7B q8 weights, batch {batch}")
-            q8[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8, fmt=qa.FORMAT_Q8)
+            q8[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=256, warmup=8, fmt=qa.FORMAT_Q8)
         result["decoder_1p7b_q8_q8kv_ctx4096"] = q8
     if not args.skip_decoder and "q5" in variants:
         q5 = {}
         for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
             log(f"decoder 1.7B q5 weights, batch {batch}")
-            q5[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=64, warmup=8, fmt=qa.FORMAT_Q5)
+            q5[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=256, warmup=8, fmt=qa.FORMAT_Q5)
         result["decoder_1p7b_q5_q8kv_ctx4096"] = q5
     if not args.skip_decoder and "f32kv" in variants:
         log("decoder 1.7B, f32 cache, batch 1")
-        result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=64, warmup=8,
+        result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=256, warmup=8,
                                                                        cache=qa.CACHE_F32)}
     if not args.skip_decoder and not args.skip_prefill:
         log("decoder 1.7B prefill of a 30 s prompt")

@@ -557,10 +557,11 @@ __device__ __forceinline__ float4 slice_sum4(const float *p, uint32_t slices, si
 // operand bytes (the 8 nibble bytes and 2 fifth-bit bytes of its 16 columns,
 // for each of its tiles and the chunk's groups) straight into registers, one
 // chunk ahead; the digits, multipliers, scales, split and epilogue are those
-// of gemv_split_kernel with chunks of 4 groups.
-template <int TW>
+// of gemv_split_kernel, with chunks of KC = 4 groups, or 2 for rows whose
+// group count is not a multiple of 4 (the 0.6B audio tower's 896-wide rows:
+// 14 groups).
+template <int TW, int KC>
 __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
-    constexpr int KC = 4;
     using S = SplitShape<TW, KC, 32>;  // (digit staging only)
     constexpr int ROWS = S::ROWS, DPT = S::DPT;
     __shared__ v4i dl[2][S::DPIECES];
@@ -602,7 +603,9 @@ __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
         }
 #pragma unroll
         for (int m = 0; m < DPT; ++m) {
-            const int q = tid + 256 * m;
+            // (Threads past the chunk's pieces load the last one again and
+            // do not store it: the load stays unconditional.)
+            const int q = tid + 256 * m < S::DPIECES ? tid + 256 * m : S::DPIECES - 1;
             const int L = q & 63;
             rd[m] = *reinterpret_cast<const v4i *>(dig + ((size_t)g0 * 3 + (q >> 6)) * kPlaneBytes +
                                                      (L & 15) * 64 + (L >> 4) * 16);
@@ -619,7 +622,8 @@ __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
         const int buf = c & 1;
         if (c == 0 && has_ss) ssl[tid] = ssv;
 #pragma unroll
-        for (int m = 0; m < DPT; ++m) dl[buf][tid + 256 * m] = rd[m];
+        for (int m = 0; m < DPT; ++m)
+            if (tid + 256 * m < S::DPIECES) dl[buf][tid + 256 * m] = rd[m];
         if (tid < KC * 4) ml[buf][tid] = rm;
         // This chunk's operands and scales, out of the registers the next
         // chunk's loads are about to fill.
@@ -1047,17 +1051,14 @@ void launch_split_bpg(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, 
 
 template <int BPG>
 void launch_split_multi_bpg(hipStream_t s, const SplitPlan &plan, const SplitMulti &m, dim3 grid) {
+    // Chunks of 2 or 4 groups (split_plan), one or two row tiles per wave.
     if (plan.kc == 2) {
         if (plan.tw == 2) gemv_split_multi_kernel<2, 2, BPG><<<grid, 256, 0, s>>>(m);
         else gemv_split_multi_kernel<1, 2, BPG><<<grid, 256, 0, s>>>(m);
-    } else if (plan.tw == 2 && plan.kc == 4) {
-        gemv_split_multi_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(m);
     } else if (plan.tw == 2) {
-        gemv_split_multi_kernel<2, 8, BPG><<<grid, 256, 0, s>>>(m);
-    } else if (plan.kc == 4) {
-        gemv_split_multi_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(m);
+        gemv_split_multi_kernel<2, 4, BPG><<<grid, 256, 0, s>>>(m);
     } else {
-        gemv_split_multi_kernel<1, 8, BPG><<<grid, 256, 0, s>>>(m);
+        gemv_split_multi_kernel<1, 4, BPG><<<grid, 256, 0, s>>>(m);
     }
 }
 
@@ -1065,9 +1066,14 @@ void launch_split(hipStream_t s, const SplitPlan &plan, const SplitArgs &a, uint
     const uint32_t row_tiles = (a.n + kRowTile - 1) / kRowTile;
     const dim3 grid((row_tiles + 4u * plan.tw - 1) / (4u * plan.tw), plan.slices, tiles);
     if (format == QWH_FORMAT_Q5) {
-        // (Chunks of 4 groups: a slice is a whole number of them.)
-        if (plan.tw == 2) gemv_split_q5_kernel<2><<<grid, 256, 0, s>>>(a);
-        else gemv_split_q5_kernel<1><<<grid, 256, 0, s>>>(a);
+        // (A slice is a whole number of chunks.)
+        if (plan.kc == 2) {
+            if (plan.tw == 2) gemv_split_q5_kernel<2, 2><<<grid, 256, 0, s>>>(a);
+            else gemv_split_q5_kernel<1, 2><<<grid, 256, 0, s>>>(a);
+        } else {
+            if (plan.tw == 2) gemv_split_q5_kernel<2, 4><<<grid, 256, 0, s>>>(a);
+            else gemv_split_q5_kernel<1, 4><<<grid, 256, 0, s>>>(a);
+        }
     } else if (format == QWH_FORMAT_Q8) {
         launch_split_bpg<64>(s, plan, a, grid);
     } else {
@@ -1106,8 +1112,7 @@ SplitArgs split_args(const void *digits, const Matrix &w, uint32_t tokens, const
 bool gemv_batch_supported(const Matrix &w) {
     if (!batch_format(w.format) || w.cols % 64) return false;
     if (w.format != QWH_FORMAT_Q5) return true;
-    const SplitPlan p = split_plan(w);
-    return p.tw && p.kc == 4;  // (the q5 kernel's chunks are 4 groups)
+    return split_plan(w).tw != 0;  // (q5: the split form, an even number of groups)
 }
 
 uint32_t batch_slices(const Matrix &w) {
@@ -1125,7 +1130,7 @@ hipError_t launch_gemv_batch_parts(hipStream_t s, const void *digits, const Matr
     if (!batch_format(w.format)) return hipErrorNotSupported;
     const SplitPlan plan = split_plan(w, slices_used ? (tokens + kTokenTile - 1) / kTokenTile : 1);
     if (slices_used) *slices_used = plan.slices;
-    if (!plan.tw || !partials || (w.format == QWH_FORMAT_Q5 && plan.kc != 4)) return hipErrorInvalidValue;
+    if (!plan.tw || !partials) return hipErrorInvalidValue;
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     SplitArgs a = split_args(digits, w, tokens, plan, norm);
     a.part = partials;
@@ -1169,8 +1174,7 @@ hipError_t launch_gemv_batch(hipStream_t s, const void *digits, const Matrix &w,
     if (norm.rms && ss_parts_of(w.cols) > kTokenTile) return hipErrorInvalidValue;
     const uint32_t tiles = (tokens + kTokenTile - 1) / kTokenTile;
     const SplitPlan plan = split_plan(w, tiles);
-    if (w.format == QWH_FORMAT_Q5 && !(plan.tw && plan.kc == 4 && (plan.slices == 1 || partials)))
-        return hipErrorInvalidValue;
+    if (w.format == QWH_FORMAT_Q5 && !(plan.tw && (plan.slices == 1 || partials))) return hipErrorInvalidValue;
     if (plan.tw && (plan.slices == 1 || partials)) {
         SplitArgs a = split_args(digits, w, tokens, plan, norm);
         a.out = out;

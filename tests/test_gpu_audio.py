@@ -162,6 +162,7 @@ def make_layer(ctx, fmt, d_model, ffn_dim, seed):
     (qa.FORMAT_Q5, 256, 4, 512, 21, 8),
     (qa.FORMAT_Q4, 256, 4, 512, 1, 8),  # one step: the per-linear path, separate bias and norm kernels
     (qa.FORMAT_Q4, 896, 14, 3584, 390, 104),  # Qwen3-ASR-0.6B audio layer, 30 s
+    (qa.FORMAT_Q5, 896, 14, 3584, 390, 104),  # the same in q5 (896-wide rows: 14 groups)
 ])
 def test_audio_layer(ctx, fmt, d_model, heads, ffn_dim, steps, window):
     eps = 1e-5

@@ -179,6 +179,9 @@ def test_q5_gemv_shapes(ctx, rows, cols, tokens):
     (100, 1024, 17),     # two token tiles, a partial row tile
     (8240, 1024, 3),     # two row tiles per wavefront
     (2048, 6144, 40),    # three token tiles, the widest row
+    (896, 896, 390),     # the 0.6B audio tower's 896-wide rows (14 groups: chunks of 2 groups), 30 s of steps
+    (3584, 896, 390),    # its ffn_in
+    (896, 3584, 390),    # its ffn_out (56 groups: chunks of 4)
 ])
 def test_q5_multi_token_on_matrix_cores(ctx, rows, cols, tokens):
     # Several tokens over q5 codes (K a multiple of 256): u - 16 expanded to
