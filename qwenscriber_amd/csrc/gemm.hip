@@ -16,7 +16,8 @@
 // multiplied out of one LDS buffer, group g+1's activations and codes wait in
 // registers to be written (codes decoded to bf16) into the other buffer
 // before the iteration's single barrier, and group g+2's are in flight from
-// global memory.
+// global memory. Within an iteration the decode and the scale FMAs (of the
+// other 32-row half of the wave's tile) run between the MFMAs.
 //
 // Split K: when the tiles alone cannot fill the device (few tokens, or few
 // weight rows), grid.z splits the groups into ranges; each range writes a
@@ -91,24 +92,15 @@ __device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32
     }
 }
 
-// Activations as they are; codes decoded to the bf16 of u - 8 (q5: u - 16).
+// The thread's 32 codes decoded to the bf16 of u - 8 (q5: u - 16), two per
+// word.
 template <bool Q5>
-__device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, uint16_t *lds_b, int tid) {
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int idx = tid + it * 256;
-        const int row = idx >> 3;
-        const int col = (idx & 7) * 8;
-        *reinterpret_cast<u32x4 *>(&lds_a[row * LDS_STRIDE + col]) = st.a[it];
-    }
-    const int row = tid >> 1;
-    const int half = tid & 1;
+__device__ __forceinline__ void stage_decode(const Staged &st, uint32_t (&packed)[16]) {
     // (The codes count as changed here, so their decode is not moved up to
     // their load: using a load's value waits for every load issued before it.)
     u32x4 codes = st.codes;
     asm volatile("" : "+v"(codes));
     const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
-    uint32_t packed[16];
     if constexpr (Q5) {
         uint32_t fifth = st.fifth;
         asm volatile("" : "+v"(fifth));
@@ -138,9 +130,30 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, u
         }
     }
     }
+}
+
+// Activations as they are, decoded codes, into one LDS buffer.
+__device__ __forceinline__ void stage_write(const Staged &st, const uint32_t (&packed)[16], uint16_t *lds_a,
+                                            uint16_t *lds_b, int tid) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int idx = tid + it * 256;
+        const int row = idx >> 3;
+        const int col = (idx & 7) * 8;
+        *reinterpret_cast<u32x4 *>(&lds_a[row * LDS_STRIDE + col]) = st.a[it];
+    }
+    const int row = tid >> 1;
+    const int half = tid & 1;
     u32x4 *dst = reinterpret_cast<u32x4 *>(&lds_b[row * LDS_STRIDE + half * 32]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dst[q] = u32x4{packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]};
+}
+
+template <bool Q5>
+__device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, uint16_t *lds_b, int tid) {
+    uint32_t packed[16];
+    stage_decode<Q5>(st, packed);
+    stage_write(st, packed, lds_a, lds_b, tid);
 }
 
 template <bool Q5>
@@ -201,9 +214,21 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
     stage_store<Q5>(st0, lds_a[0], lds_b[0], tid);
     __syncthreads();
 
+    // Each group's partial product is scaled by its weight row's scale (in
+    // the 32x32 output layout every value a lane holds lies in column l % 32)
+    // on the vector ALUs, one FMA per output value. The two 32-row halves of
+    // the wave's tile run half a group apart, so those FMAs always have
+    // products in flight beside them: the MFMAs of group g's first half run
+    // while the second half of group g - 1 (part1, s_prev) is scaled, those of
+    // its second half while its first half is scaled. Each value is scaled
+    // and summed in group order, as before the split.
+    f32x16 part1[2] = {f32x16{}, f32x16{}};
+    float s_prev[2] = {0.0f, 0.0f};
+
     // One group: loads for g + 2 into `next2` (its previous content, group
     // g, is already in LDS), multiply group g from LDS buffer `buf`, then
-    // store group g + 1 (in `next1`) into the other buffer.
+    // store group g + 1 (in `next1`) into the other buffer; group g + 1's
+    // decode is spread between the MFMAs.
     // The scales of group g come from the step before, issued ahead of that
     // step's tile loads (waiting for a load waits for every older one, so
     // scales fetched in their own step would drain the tile prefetch).
@@ -216,32 +241,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
 
         const uint16_t *la = lds_a[buf];
         const uint16_t *lb = lds_b[buf];
-        f32x16 part[2][2];
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            bf16x8 fa[2], fb[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + li;
-                fa[i] = *reinterpret_cast<const bf16x8 *>(&la[row * LDS_STRIDE + ks * 16 + kb]);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = wn * 64 + j * 32 + li;
-                fb[j] = *reinterpret_cast<const bf16x8 *>(&lb[row * LDS_STRIDE + ks * 16 + kb]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], ks == 0 ? f32x16{} : part[i][j],
-                                                                         0, 0, 0);
-        }
-        // Group g + 1 into the other buffer first: its decode runs while the
-        // products above are still in the matrix pipeline.
-        stage_store<Q5>(next1, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
-        // Scale each group's partial product by its weight row's scale: in the
-        // 32x32 output layout every value a lane holds lies in column l % 32.
+        uint32_t packed[16];
+        stage_decode<Q5>(next1, packed);
         float s[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -249,12 +250,55 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
             asm volatile("" : "+v"(bits));  // (converted here, not at its load)
             s[j] = dev::f16_bits_to_f32((uint16_t)bits);
         }
+        // The weight operands serve both halves: q4 reads them once into
+        // registers; q5 (whose staged fifth bits and decode hold more
+        // registers) reads them again for the second half rather than spill.
+        auto read_b = [&](int ks, int j) {
+            return *reinterpret_cast<const bf16x8 *>(&lb[(wn * 64 + j * 32 + li) * LDS_STRIDE + ks * 16 + kb]);
+        };
+        bf16x8 fb[BK / 16][2];
+        if constexpr (!Q5) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int ks = 0; ks < BK / 16; ++ks)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) fb[ks][j] = read_b(ks, j);
+        }
+        f32x16 part0[2];
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const bf16x8 fa = *reinterpret_cast<const bf16x8 *>(&la[(wm * 64 + li) * LDS_STRIDE + ks * 16 + kb]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
+                part0[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, Q5 ? read_b(ks, j) : fb[ks][j],
+                                                                 ks == 0 ? f32x16{} : part0[j], 0, 0, 0);
+        }
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(s[j], part[i][j][r], acc[i][j][r]);
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[1][j][r] = fmaf(s_prev[j], part1[j][r], acc[1][j][r]);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const bf16x8 fa = *reinterpret_cast<const bf16x8 *>(&la[(wm * 64 + 32 + li) * LDS_STRIDE + ks * 16 + kb]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                part1[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, Q5 ? read_b(ks, j) : fb[ks][j],
+                                                                 ks == 0 ? f32x16{} : part1[j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[0][j][r] = fmaf(s[j], part0[j][r], acc[0][j][r]);
+        // Scheduling: each of the 16 MFMAs followed by up to six vector-ALU
+        // instructions (the decode and the FMAs), as their operands allow
+        // (measured against two, ten and the compiler's own order).
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+        }
+        stage_write(next1, packed, lds_a[buf ^ 1], lds_b[buf ^ 1], tid);
+        s_prev[0] = s[0];
+        s_prev[1] = s[1];
         __syncthreads();
     };
     // Unrolled by two so the staging registers are addressed statically.
@@ -267,6 +311,11 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
         step(g + 1, 1, st1, st0, sc1, sc0);
     }
     if (g < g1) step(g, 0, st0, st1, sc0, sc1);
+    // The last group's second half.
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[1][j][r] = fmaf(s_prev[j], part1[j][r], acc[1][j][r]);
 
     // Store: value r of a lane is row 8 * (r / 4) + 4 * (l / 32) + r % 4 of the
     // 32x32 tile, column l % 32.
