@@ -467,26 +467,32 @@ def bench_small(ctx, qa, steps):
     g5 = bench_gemv(ctx, qa, 151936, 1024, steps, 10, 2.1e9, stream=9, fmt=qa.FORMAT_Q5)
     gbs = g5["bytes"] / (g5["call_ms"] * 1e-3) / 1e9
     out["q5_gemv_lm_head_0p6b"] = dict(us=g5["call_ms"] * 1e3, GBs=gbs, frac=gbs / 8000.0)
-    # q4 GEMM, bf16 activations, M = 1500 at [6144 x 2048].
-    gemm = {}
-    for rows, cols in ((6144, 2048), (2048, 6144)):
-        m = ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, 2, 1, 0.02)
-        for M in (128, 512, 1500):
-            xf = ctx.buffer(M * cols * 4)
-            ctx.synth_normal(2, 10 + M, M * cols, 1.0, xf.ptr)
-            xb = ctx.buffer(M * cols * 2)
-            # bf16 bits: the top half of each f32 (the bench only needs a
-            # valid bf16 input of the right shape).
-            host = xf.download(np.float32)
-            xb.upload((host.view(np.uint32) >> 16).astype(np.uint16))
-            y = ctx.buffer(M * rows * 4)
-            ms = time_events(ctx, lambda i: ctx.linear_bf16(m, xb.ptr, cols, M, y.ptr), max(3, steps // 3))
-            tflops = 2 * M * rows * cols / (ms * 1e-3) / 1e12
-            gemm[f"M{M}_{rows}x{cols}"] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / MFMA_BF16_PEAK_TFLOPS)
-            for b in (xf, xb, y):
-                b.free()
-        ctx.matrix_release(m)
-    out["q4_gemm_bf16"] = gemm
+    # q4 GEMM, bf16 activations, M = 128 / 512 / 1500 at
+    # [6144 x 2048] and [2048 x 6144]; the same GEMM for a q8 model's
+    # matrices at M = 1500.
+    def gemm_lines(fmt, sizes):
+        lines = {}
+        for rows, cols in ((6144, 2048), (2048, 6144)):
+            m = ctx.matrix_synthetic(fmt, rows, cols, 2, 1, 0.02)
+            for M in sizes:
+                xf = ctx.buffer(M * cols * 4)
+                ctx.synth_normal(2, 10 + M, M * cols, 1.0, xf.ptr)
+                xb = ctx.buffer(M * cols * 2)
+                # bf16 bits: the top half of each f32 (the bench only needs a
+                # valid bf16 input of the right shape).
+                host = xf.download(np.float32)
+                xb.upload((host.view(np.uint32) >> 16).astype(np.uint16))
+                y = ctx.buffer(M * rows * 4)
+                ms = time_events(ctx, lambda i: ctx.linear_bf16(m, xb.ptr, cols, M, y.ptr), max(3, steps // 3))
+                tflops = 2 * M * rows * cols / (ms * 1e-3) / 1e12
+                lines[f"M{M}_{rows}x{cols}"] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / MFMA_BF16_PEAK_TFLOPS)
+                for b in (xf, xb, y):
+                    b.free()
+            ctx.matrix_release(m)
+        return lines
+
+    out["q4_gemm_bf16"] = gemm_lines(qa.FORMAT_Q4, (128, 512, 1500))
+    out["q8_gemm_bf16"] = gemm_lines(qa.FORMAT_Q8, (1500,))
     # q8 attention, 16 / 8 heads, head_dim 128.
     att = {}
     heads, kvh, hd = 16, 8, 128

@@ -204,7 +204,8 @@ int32_t qwh_linear_prepared(qwh_ctx *ctx, uint64_t matrix, const void *prepared_
 /* The same product with bf16 activations (the prefill / audio-token GEMM of
  * the reference's tokens > 1 path, kernels.zig:118-158 with tokens = M). The
  * reference widens each bf16 to f32 (half_float.zig:42-45) before the dot.
- * q4 and q5 matrices (q5 with an 8-byte aligned data plane). */
+ * q4, q5 and q8 matrices (q5 with an 8-byte, q8 with a 16-byte aligned data
+ * plane). */
 int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, uint32_t cols,
                         uint32_t tokens, float *out_dev);
 

@@ -530,10 +530,12 @@ int32_t qwh_linear_bf16(qwh_ctx *ctx, uint64_t matrix, const uint16_t *x_dev, ui
     const Matrix *m = find_matrix(ctx, matrix);
     if (!m) return fail(ctx, QWH_E_NOT_FOUND, "unknown matrix handle %llu", (unsigned long long)matrix);
     if (cols != m->cols) return fail(ctx, QWH_E_SHAPE_MISMATCH, "x has %u columns, the matrix %u", cols, m->cols);
-    if (m->format != QWH_FORMAT_Q4 && m->format != QWH_FORMAT_Q5)
-        return fail(ctx, QWH_E_UNSUPPORTED, "bf16 GEMM is built for q4 and q5");
+    if (m->format != QWH_FORMAT_Q4 && m->format != QWH_FORMAT_Q5 && m->format != QWH_FORMAT_Q8)
+        return fail(ctx, QWH_E_UNSUPPORTED, "bf16 GEMM is built for q4, q5 and q8");
     if (m->format == QWH_FORMAT_Q5 && ((uintptr_t)m->data & 7u) != 0)
         return fail(ctx, QWH_E_INVALID_ARGUMENT, "q5 data plane must be 8-byte aligned");
+    if (m->format == QWH_FORMAT_Q8 && ((uintptr_t)m->data & 15u) != 0)
+        return fail(ctx, QWH_E_INVALID_ARGUMENT, "q8 data plane must be 16-byte aligned");
     if (tokens == 0 || m->rows == 0) return QWH_OK;
     if (tokens > 65535u * 128u) return fail(ctx, QWH_E_LIMIT_EXCEEDED, "tokens %u", tokens);
     QWH_TRY(check_device_ptr(ctx, x_dev, "x"));

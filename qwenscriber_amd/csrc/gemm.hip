@@ -1,14 +1,15 @@
-// q4 / q5 GEMM with bf16 activations on the bf16 MFMA units: the prefill /
-// audio-token product of kernels.zig:118-158 with tokens = M > 1.
+// q4 / q5 / q8 GEMM with bf16 activations on the bf16 MFMA units: the
+// prefill / audio-token product of kernels.zig:118-158 with tokens = M > 1.
 //
 // out[m][n] = sum_k x[m][k] * (u[n][k] - bias) * s[n][k/64]
 //
 // The codes (q4: u - 8 in [-8, 7]; q5: u - 16 in [-16, 15], the fifth bit of
-// each code in its group's last 8 bytes, quant.zig:253-269) are exact in
-// bf16, so the MFMA multiplies the
-// exact decoded integers by the exact bf16 activations; each 64-wide group's
-// partial product is accumulated in f32 on its own and then scaled by the
-// group's f16 scale (folding the scale into bf16 weights would round it).
+// each code in its group's last 8 bytes, quant.zig:253-269; q8: u - 128 in
+// [-128, 127], quant.zig:270-275, 336-340) are exact in bf16, so the MFMA
+// multiplies the exact decoded integers by the exact bf16 activations; each
+// 64-wide group's partial product is accumulated in f32 on its own and then
+// scaled by the group's f16 scale (folding the scale into bf16 weights would
+// round it).
 //
 // Tiling: a 256-thread workgroup computes a 128 x 128 tile of out; each wave a
 // 64 x 64 quarter as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16. The K loop runs
@@ -55,12 +56,17 @@ struct GemmArgs {
     float *tail;
 };
 
+// Weight formats of the kernel: q4 (32-byte groups), q5 (40), q8 (64).
+constexpr int kQ4 = 0, kQ5 = 1, kQ8 = 2;
+
 // A group's tile data held in registers between its global loads and its
-// LDS stores: 4 x 16 B of activations and 16 B of codes per thread (q5: and
-// the 4 bytes of those 32 codes' fifth bits).
+// LDS stores: 4 x 16 B of activations and the codes of half a group row per
+// thread: 16 B (q4), 16 B and the 4 bytes of those 32 codes' fifth bits
+// (q5), or 32 B (q8: codes, then codes2).
 struct Staged {
     u32x4 a[4];
     u32x4 codes;
+    u32x4 codes2;
     uint32_t fifth;
 };
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -68,7 +74,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Rows past the matrix (tokens past M, weight rows past N) load its last row:
 // they only reach output rows or columns that are never stored. Every load
 // is unconditional, so all of them are in flight together.
-template <bool Q5>
+template <int F>
 __device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32_t m0, uint32_t n0, uint32_t g,
                                            int tid) {
 #pragma unroll
@@ -80,28 +86,48 @@ __device__ __forceinline__ void stage_load(const GemmArgs &a, Staged &st, uint32
     }
     const uint32_t row = min(n0 + (tid >> 1), a.n - 1);
     const int half = tid & 1;
-    if constexpr (Q5) {
+    if constexpr (F == kQ5) {
         // A 40-byte group: the half row's nibbles are only 8-byte aligned.
         const uint8_t *grp = a.data + (size_t)row * (a.k / 64) * 40 + g * 40;
         const u32x2 lo = *reinterpret_cast<const u32x2 *>(grp + half * 16);
         const u32x2 hi = *reinterpret_cast<const u32x2 *>(grp + half * 16 + 8);
         st.codes = u32x4{lo.x, lo.y, hi.x, hi.y};
         st.fifth = *reinterpret_cast<const uint32_t *>(grp + 32 + half * 4);
+    } else if constexpr (F == kQ8) {
+        // A 64-byte group: the half row is 32 bytes.
+        const uint8_t *grp = a.data + (size_t)row * a.k + g * 64 + half * 32;
+        st.codes = *reinterpret_cast<const u32x4 *>(grp);
+        st.codes2 = *reinterpret_cast<const u32x4 *>(grp + 16);
     } else {
         st.codes = *reinterpret_cast<const u32x4 *>(a.data + (size_t)row * (a.k / 2) + g * 32 + half * 16);
     }
 }
 
-// The thread's 32 codes decoded to the bf16 of u - 8 (q5: u - 16), two per
-// word.
-template <bool Q5>
+// The thread's 32 codes decoded to the bf16 of u - 8 (q5: u - 16, q8:
+// u - 128), two per word: packed[j] holds codes 2j and 2j + 1.
+template <int F>
 __device__ __forceinline__ void stage_decode(const Staged &st, uint32_t (&packed)[16]) {
     // (The codes count as changed here, so their decode is not moved up to
     // their load: using a load's value waits for every load issued before it.)
     u32x4 codes = st.codes;
     asm volatile("" : "+v"(codes));
     const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
-    if constexpr (Q5) {
+    if constexpr (F == kQ8) {
+        u32x4 codes2 = st.codes2;
+        asm volatile("" : "+v"(codes2));
+        const uint32_t w8[8] = {codes.x, codes.y, codes.z, codes.w, codes2.x, codes2.y, codes2.z, codes2.w};
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                // Bytes 2p and 2p + 1 of the word: codes 4d + 2p, 4d + 2p + 1;
+                // a byte converts to f32 exactly, minus 128 exactly.
+                const float c0 = (float)((w8[d] >> (16 * p)) & 0xffu) - 128.0f;
+                const float c1 = (float)((w8[d] >> (16 * p + 8)) & 0xffu) - 128.0f;
+                packed[2 * d + p] = (__float_as_uint(c0) >> 16) | (__float_as_uint(c1) & 0xffff0000u);
+            }
+        }
+    } else if constexpr (F == kQ5) {
         uint32_t fifth = st.fifth;
         asm volatile("" : "+v"(fifth));
 #pragma unroll
@@ -149,14 +175,14 @@ __device__ __forceinline__ void stage_write(const Staged &st, const uint32_t (&p
     for (int q = 0; q < 4; ++q) dst[q] = u32x4{packed[q * 4 + 0], packed[q * 4 + 1], packed[q * 4 + 2], packed[q * 4 + 3]};
 }
 
-template <bool Q5>
+template <int F>
 __device__ __forceinline__ void stage_store(const Staged &st, uint16_t *lds_a, uint16_t *lds_b, int tid) {
     uint32_t packed[16];
-    stage_decode<Q5>(st, packed);
+    stage_decode<F>(st, packed);
     stage_write(st, packed, lds_a, lds_b, tid);
 }
 
-template <bool Q5>
+template <int F>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * LDS_STRIDE];
@@ -209,9 +235,9 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
     // Two groups in flight ahead of the one being multiplied: group g + 2's
     // loads are issued while g is multiplied and g + 1 waits in registers.
     Staged st0, st1;
-    stage_load<Q5>(a, st0, m0, n0, g0, tid);
-    stage_load<Q5>(a, st1, m0, n0, min(g0 + 1, g1 - 1), tid);
-    stage_store<Q5>(st0, lds_a[0], lds_b[0], tid);
+    stage_load<F>(a, st0, m0, n0, g0, tid);
+    stage_load<F>(a, st1, m0, n0, min(g0 + 1, g1 - 1), tid);
+    stage_store<F>(st0, lds_a[0], lds_b[0], tid);
     __syncthreads();
 
     // Each group's partial product is scaled by its weight row's scale (in
@@ -237,12 +263,12 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) s_next[j] = srow[j][min(g + 1, g1 - 1)];
         // (Past the range: the last group again, never used.)
-        stage_load<Q5>(a, next2, m0, n0, min(g + 2, g1 - 1), tid);
+        stage_load<F>(a, next2, m0, n0, min(g + 2, g1 - 1), tid);
 
         const uint16_t *la = lds_a[buf];
         const uint16_t *lb = lds_b[buf];
         uint32_t packed[16];
-        stage_decode<Q5>(next1, packed);
+        stage_decode<F>(next1, packed);
         float s[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -251,13 +277,14 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
             s[j] = dev::f16_bits_to_f32((uint16_t)bits);
         }
         // The weight operands serve both halves: q4 reads them once into
-        // registers; q5 (whose staged fifth bits and decode hold more
-        // registers) reads them again for the second half rather than spill.
+        // registers; q5 and q8 (whose staging and decode hold more
+        // registers) read them again for the second half rather than spill.
+        constexpr bool kLazyB = F != kQ4;
         auto read_b = [&](int ks, int j) {
             return *reinterpret_cast<const bf16x8 *>(&lb[(wn * 64 + j * 32 + li) * LDS_STRIDE + ks * 16 + kb]);
         };
         bf16x8 fb[BK / 16][2];
-        if constexpr (!Q5) {
+        if constexpr (!kLazyB) {
 #pragma unroll
             for (int ks = 0; ks < BK / 16; ++ks)
 #pragma unroll
@@ -269,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
             const bf16x8 fa = *reinterpret_cast<const bf16x8 *>(&la[(wm * 64 + li) * LDS_STRIDE + ks * 16 + kb]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                part0[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, Q5 ? read_b(ks, j) : fb[ks][j],
+                part0[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, kLazyB ? read_b(ks, j) : fb[ks][j],
                                                                  ks == 0 ? f32x16{} : part0[j], 0, 0, 0);
         }
 #pragma unroll
@@ -281,7 +308,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const GemmArgs a) {
             const bf16x8 fa = *reinterpret_cast<const bf16x8 *>(&la[(wm * 64 + 32 + li) * LDS_STRIDE + ks * 16 + kb]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                part1[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, Q5 ? read_b(ks, j) : fb[ks][j],
+                part1[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, kLazyB ? read_b(ks, j) : fb[ks][j],
                                                                  ks == 0 ? f32x16{} : part1[j], 0, 0, 0);
         }
 #pragma unroll
@@ -476,7 +503,8 @@ size_t gemm_scratch_bytes(int cus, uint32_t tokens, const Matrix &w) {
 
 hipError_t launch_gemm_bf16(hipStream_t s, int cus, const uint16_t *x, const Matrix &w, uint32_t tokens,
                             float *out, void *scratch) {
-    if (w.format != QWH_FORMAT_Q4 && w.format != QWH_FORMAT_Q5) return hipErrorNotSupported;
+    if (w.format != QWH_FORMAT_Q4 && w.format != QWH_FORMAT_Q5 && w.format != QWH_FORMAT_Q8)
+        return hipErrorNotSupported;
     GemmArgs args{};
     args.x = x;
     args.scales = reinterpret_cast<const uint16_t *>(w.scales);
@@ -496,9 +524,11 @@ hipError_t launch_gemm_bf16(hipStream_t s, int cus, const uint16_t *x, const Mat
         grid = dim3(plan.full + (plan.tiles - plan.full) * plan.tail_splits);
     }
     if (w.format == QWH_FORMAT_Q5)
-        gemm_bf16_kernel<true><<<grid, 256, 0, s>>>(args);
+        gemm_bf16_kernel<kQ5><<<grid, 256, 0, s>>>(args);
+    else if (w.format == QWH_FORMAT_Q8)
+        gemm_bf16_kernel<kQ8><<<grid, 256, 0, s>>>(args);
     else
-        gemm_bf16_kernel<false><<<grid, 256, 0, s>>>(args);
+        gemm_bf16_kernel<kQ4><<<grid, 256, 0, s>>>(args);
     if (plan.tail_splits) {
         gemm_tail_reduce_kernel<<<(plan.tiles - plan.full) * 16, 256, 0, s>>>(
             args.tail, plan.tail_splits, plan.full, plan.tiles_x, tokens, w.rows, out);

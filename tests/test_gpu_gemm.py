@@ -1,4 +1,4 @@
-"""GPU parity of the q4 GEMM with bf16 activations (kernels.zig:118-158 with
+"""GPU parity of the q4 / q5 / q8 GEMM with bf16 activations (kernels.zig:118-158 with
 tokens = M; the oracle consumes the same bf16 values widened to f32)."""
 import os
 
@@ -82,3 +82,22 @@ def test_q5_gemm(ctx, rows, cols, m):
     d_sub = np.concatenate([data[r * gpr * 40:(r + 1) * gpr * 40] for r in sample])
     expected = o.linear_quantized(o.Q5, s_sub, d_sub, len(sample), cols, widen(xb16), m)
     assert_close(actual[:, sample], expected, what=f"q5 GEMM M {m} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("rows,cols,m", [(6144, 2048, 1500), (2048, 6144, 512), (6144, 2048, 128), (100, 128, 1),
+                                         (130, 256, 7), (257, 192, 33), (64, 64, 130)])
+def test_q8_gemm(ctx, rows, cols, m):
+    # q8 planes (quant.zig:270-275, 336-340): 64 bytes per group, u - 128.
+    # M = 1500 at [6144 x 2048] reaches the tail form on a 256-CU device.
+    w = o.normal(rows * cols, 16, rows, 0.02).reshape(rows, cols)
+    w[0, :64] = np.float32(-1.0)   # codes at both ends of the q8 range
+    w[0, 64:128] = np.float32(1.0)
+    scales, data = o.quantize_rows(o.Q8, w)
+    xb16 = to_bf16_bits(o.normal(m * cols, 16, 11))
+    actual = run_gemm(ctx, rows, cols, scales, data, xb16, m, fmt=o.Q8)
+    gpr = cols // 64
+    sample = np.unique(np.linspace(0, rows - 1, min(rows, 256)).astype(int))
+    s_sub = np.concatenate([scales[r * gpr * 2:(r + 1) * gpr * 2] for r in sample])
+    d_sub = np.concatenate([data[r * gpr * 64:(r + 1) * gpr * 64] for r in sample])
+    expected = o.linear_quantized(o.Q8, s_sub, d_sub, len(sample), cols, widen(xb16), m)
+    assert_close(actual[:, sample], expected, what=f"q8 GEMM M {m} {rows}x{cols}")
