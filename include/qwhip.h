@@ -233,7 +233,11 @@ int32_t qwh_synth_normal(qwh_ctx *ctx, uint32_t seed, uint32_t stream, uint64_t 
  * f16, k/v codes [positions][kv_heads*head_dim] u8), `cached` positions read.
  * `batch` independent sequences are laid out back to back: query and out
  * advance by heads*head_dim floats, the planes by `plane_stride_bytes`
- * (scales) and `code_stride_bytes` (codes) per sequence. */
+ * (scales) and `code_stride_bytes` (codes) per sequence. Any head_dim that
+ * is a multiple of 64 up to 1024 and any heads / kv_heads ratio (head_dim
+ * 64 / 128 / 256 with ratios up to 8, or 2 at 256, run the split-range
+ * kernels; the other shapes a one-workgroup-per-head kernel); a wider head
+ * returns QWH_E_UNSUPPORTED. */
 int32_t qwh_decode_attention_q8(qwh_ctx *ctx, float *out_dev, const float *query_dev,
                                 const uint8_t *k_scales_dev, const uint8_t *k_codes_dev,
                                 const uint8_t *v_scales_dev, const uint8_t *v_codes_dev,
@@ -259,8 +263,10 @@ int32_t qwh_decode_attention_q8_noalloc(qwh_ctx *ctx, float *out_dev, const floa
  * default cache, model_config.zig:44-68): keys_dev / values_dev are
  * [positions][kv_heads*head_dim] f32 (decoder.zig:77-83), `cached` positions
  * read; `batch` sequences back to back, query and out advancing by
- * heads*head_dim floats, keys and values by `stride_bytes`. Built for
- * head_dim 64, 128, 256 (else QWH_E_UNSUPPORTED). */
+ * heads*head_dim floats, keys and values by `stride_bytes`. Any head_dim up
+ * to 1024 and any heads / kv_heads ratio (split-range kernels for head_dim
+ * 64 / 128 / 256, a one-workgroup-per-head kernel otherwise); a wider head
+ * returns QWH_E_UNSUPPORTED. */
 int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *query_dev, const float *keys_dev,
                                  const float *values_dev, uint32_t cached, uint32_t heads, uint32_t kv_heads,
                                  uint32_t head_dim, uint32_t batch, uint64_t stride_bytes);

@@ -1321,9 +1321,107 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float *key, const 
     if (lane == 0) reinterpret_cast<uint16_t *>(scales)[(size_t)position * gpr + g] = bits;
 }
 
+// ---- Any head shape (the range kernels' lane mapping needs head_dim 64,
+// 128 or 256): kernels.zig:697-767 (q8) and :572-627 (f32) for every
+// head_dim (a multiple of 64 for q8) up to kGenericMaxDim and every ratio of
+// heads to kv heads. One workgroup per (query head, sequence) walks the
+// positions 256 at a time: thread i scores position base + i over the whole
+// head row (the q8 form per 64-value group: scale times the sum of
+// (u - 128) q), the workgroup keeps an online softmax in base 2 (the running
+// maximum and sum), and each thread accumulates the dimensions
+// i, i + 256, ... over the block's positions with the weights from LDS.
+constexpr uint32_t kGenericMaxDim = 1024;
+
+__device__ __forceinline__ float block_max_256(float v, float *lds) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(lds[0], lds[1]), fmaxf(lds[2], lds[3]));
+}
+
+template <bool F32C>
+__global__ __launch_bounds__(256) void attention_generic_kernel(const AttnKernelArgs a, uint32_t head_dim) {
+    constexpr int kDims = kGenericMaxDim / 256;  // dimensions per thread
+    __shared__ float q[kGenericMaxDim];
+    __shared__ float w[256];
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const uint32_t D = head_dim;
+    const uint32_t kvh = h / (a.heads / a.kv_heads);
+    const uint32_t kv_width = a.kv_heads * D;
+    const uint32_t gpr = kv_width / 64;
+    const float *query = a.query + (size_t)b * a.query_stride + (size_t)h * D;
+    for (uint32_t d = tid; d < D; d += 256) q[d] = query[d];
+    __syncthreads();
+    const uint8_t *k_codes = a.k_codes + b * a.code_stride;
+    const uint8_t *v_codes = a.v_codes + b * a.code_stride;
+    const uint16_t *k_scales = reinterpret_cast<const uint16_t *>(a.k_scales + b * a.scale_stride);
+    const uint16_t *v_scales = reinterpret_cast<const uint16_t *>(a.v_scales + b * a.scale_stride);
+    float acc[kDims];
+#pragma unroll
+    for (int j = 0; j < kDims; ++j) acc[j] = 0.0f;
+    float m = kNeg, l = 0.0f;
+    for (uint32_t base = 0; base < a.cached; base += 256) {
+        const uint32_t p = base + tid;
+        float s = kNeg;
+        if (p < a.cached) {
+            float dot = 0.0f;
+            if constexpr (F32C) {
+                const float *k = reinterpret_cast<const float *>(k_codes) + (size_t)p * kv_width + kvh * D;
+                for (uint32_t d = 0; d < D; ++d) dot = fmaf(q[d], k[d], dot);
+            } else {
+                const uint8_t *k = k_codes + (size_t)p * kv_width + kvh * D;
+                for (uint32_t g = 0; g < D / 64; ++g) {
+                    float part = 0.0f;
+                    for (uint32_t d = 0; d < 64; ++d) part = fmaf(q[64 * g + d], (float)((int)k[64 * g + d] - 128), part);
+                    dot = fmaf(dev::f16_bits_to_f32(k_scales[(size_t)p * gpr + kvh * (D / 64) + g]), part, dot);
+                }
+            }
+            s = dot * a.scaling;
+        }
+        const float m_new = fmaxf(m, block_max_256(s, red));
+        const float e = p < a.cached ? fast_exp2(s - m_new) : 0.0f;
+        const float alpha = fast_exp2(m - m_new);
+        w[tid] = e;
+        l = l * alpha + dev::block_sum_256(e, red);  // (its barriers also publish w)
+        m = m_new;
+        const uint32_t n = a.cached - base < 256 ? a.cached - base : 256;
+#pragma unroll
+        for (int j = 0; j < kDims; ++j) {
+            const uint32_t d = tid + 256 * j;
+            if (d >= D) break;
+            float sum = 0.0f;
+            for (uint32_t i = 0; i < n; ++i) {
+                const size_t row = (size_t)(base + i) * kv_width + kvh * D;
+                float v;
+                if constexpr (F32C) {
+                    v = reinterpret_cast<const float *>(v_codes)[row + d];
+                } else {
+                    v = (float)((int)v_codes[row + d] - 128) *
+                        dev::f16_bits_to_f32(v_scales[(size_t)(base + i) * gpr + (kvh * D + d) / 64]);
+                }
+                sum = fmaf(w[i], v, sum);
+            }
+            acc[j] = acc[j] * alpha + sum;
+        }
+        __syncthreads();  // w is rewritten by the next block
+    }
+    const float inv = 1.0f / l;
+    float *out = a.out + ((size_t)b * a.heads + h) * D;
+#pragma unroll
+    for (int j = 0; j < kDims; ++j) {
+        const uint32_t d = tid + 256 * j;
+        if (d < D) out[d] = acc[j] * inv;
+    }
+}
+
 }  // namespace
 
 size_t attention_scratch_bytes(int cus, const AttentionArgs &a) { return plan::scratch_bytes(cus, a); }
+
+bool attention_generic_supported(uint32_t head_dim) { return head_dim >= 1 && head_dim <= kGenericMaxDim; }
 
 bool attention_supported(uint32_t head_dim, uint32_t ratio) {
     return (head_dim == 64 && (ratio == 1 || ratio == 2 || ratio == 4)) ||
@@ -1383,11 +1481,36 @@ void launch_attention_pair(hipStream_t s, int cus, const AttnKernelArgs &k, bool
 hipError_t launch_decode_attention_q8(hipStream_t s, int cus, const AttentionArgs &a, void *scratch,
                                       size_t scratch_bytes) {
     const bool decoder = a.q_norm != nullptr;
+    const uint32_t R = a.heads / a.kv_heads;
+    if (!attention_supported(a.head_dim, R)) {
+        // The entry points' other shapes: the one-workgroup-per-head kernel
+        // (no records, no merge).
+        if (decoder || a.prefill || !attention_generic_supported(a.head_dim) ||
+            (!a.f32_cache && a.head_dim % 64 != 0) || a.batch > 65535)
+            return hipErrorNotSupported;
+        AttnKernelArgs g{};
+        g.query = a.query;
+        g.query_stride = a.query_stride ? a.query_stride : a.heads * a.head_dim;
+        g.k_scales = a.k_scales;
+        g.k_codes = a.k_codes;
+        g.v_scales = a.v_scales;
+        g.v_codes = a.v_codes;
+        g.cached = a.cached;
+        g.heads = a.heads;
+        g.kv_heads = a.kv_heads;
+        g.scale_stride = a.scale_stride;
+        g.code_stride = a.code_stride;
+        g.scaling = kLog2e / sqrtf((float)a.head_dim);  // kernels.zig:727, in base 2
+        g.out = a.out;
+        const dim3 grid(a.heads, a.batch);
+        if (a.f32_cache) attention_generic_kernel<true><<<grid, 256, 0, s>>>(g, a.head_dim);
+        else attention_generic_kernel<false><<<grid, 256, 0, s>>>(g, a.head_dim);
+        return hipGetLastError();
+    }
     uint32_t chunk, splits;
     plan::attention_shape(cus, a, decoder, chunk, splits);
     // Every range writes a record: refuse a scratch that cannot hold them.
     if (plan::record_bytes(a, splits) > scratch_bytes) return hipErrorInvalidValue;
-    const uint32_t R = a.heads / a.kv_heads;
     AttnKernelArgs k{};
     k.query = a.query;
     k.query_stride = a.query_stride ? a.query_stride : a.heads * a.head_dim;

@@ -601,7 +601,8 @@ int32_t attention_q8_args(qwh_ctx *ctx, float *out_dev, const float *query_dev, 
     if (batch > 1 && ((scale_stride_bytes & 1u) || (code_stride_bytes & 15u)))
         return fail(ctx, QWH_E_INVALID_ARGUMENT, "sequence strides must keep the plane alignment");
     const uint32_t ratio = heads / kv_heads;
-    if (!attention_supported(head_dim, ratio)) return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim, ratio);
+    if (!attention_supported(head_dim, ratio) && !attention_generic_supported(head_dim))
+        return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u is not built", head_dim);
     a.out = out_dev;
     a.query = query_dev;
     // The kernel only reads the cache planes in this form.
@@ -691,9 +692,8 @@ int32_t qwh_decode_attention_f32(qwh_ctx *ctx, float *out_dev, const float *quer
     if (batch > 1 && (stride_bytes & 15u))
         return fail(ctx, QWH_E_INVALID_ARGUMENT, "the sequence stride must keep 16-byte alignment");
     const uint32_t ratio = heads / kv_heads;
-    if (!attention_supported(head_dim, ratio))
-        return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u, %u heads per kv head is not built", head_dim,
-                    ratio);
+    if (!attention_supported(head_dim, ratio) && !attention_generic_supported(head_dim))
+        return fail(ctx, QWH_E_UNSUPPORTED, "attention for head_dim %u is not built", head_dim);
     AttentionArgs a{};
     a.out = out_dev;
     a.query = query_dev;

@@ -264,7 +264,11 @@ struct AttentionArgs {
 // key and value stored at cache row first + i (q8 or f32 by f32_cache);
 // the cache planes are the sequence's own.
 hipError_t launch_prefill_append(hipStream_t s, const AttentionArgs &a, uint32_t first, uint32_t count);
+// Head shapes with the range kernels (every form, the decoder's included).
 bool attention_supported(uint32_t head_dim, uint32_t ratio);
+// Head widths the plain entry points also take for other shapes (any ratio;
+// q8: a multiple of 64), through a one-workgroup-per-head kernel.
+bool attention_generic_supported(uint32_t head_dim);
 // argmaxLogits (decoder.zig:290-301) of `rows` rows of `count` logits into
 // ids (the decoder step's kernels); scratch holds argmax_scratch_bytes.
 size_t argmax_scratch_bytes(uint32_t rows, uint32_t count);

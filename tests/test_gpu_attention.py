@@ -119,3 +119,43 @@ def test_attention_rejects_bad_shapes(ctx):
         ctx.decode_attention_q8(buf.ptr, buf.ptr, buf.ptr, buf.ptr, buf.ptr, buf.ptr, 4, 12, 8, 128)
     assert err.value.status == -7
     buf.free()
+
+
+@pytest.mark.parametrize("cached,hd,heads,kvh,batch", [(300, 192, 6, 2, 1), (257, 320, 3, 1, 1), (1, 64, 12, 4, 1),
+                                                       (600, 128, 24, 8, 1), (1030, 512, 4, 2, 1), (50, 1024, 2, 1, 1),
+                                                       (700, 64, 10, 2, 1), (333, 192, 9, 3, 3)])
+def test_attention_any_head_shape(ctx, cached, hd, heads, kvh, batch):
+    # kernels.zig:712-716 takes any head_dim that is a multiple of 64 and any
+    # heads / kv_heads ratio: these (head_dim 192 / 320 / 512 / 1024, ratios
+    # 3 and 5) run the one-workgroup-per-head kernel.
+    kvw = kvh * hd
+    planes = [make_cache(cached, kvw, 21, 10 * b) for b in range(batch)]
+    q = o.normal(batch * heads * hd, 21, 7)
+    expected = np.concatenate([o.decode_attention_q8(q[b * heads * hd:(b + 1) * heads * hd], *planes[b], cached,
+                                                     heads, kvh, hd) for b in range(batch)])
+    stacked = [np.concatenate([planes[b][i] for b in range(batch)]) for i in range(4)]
+    actual = run_attention(ctx, q, stacked, cached, heads, kvh, hd, batch, planes[0][0].nbytes, planes[0][1].nbytes)
+    assert_close(actual, expected, what=f"attention cached {cached} hd {hd} {heads}/{kvh} batch {batch}")
+
+
+def test_any_head_shape_identical_keys_give_the_mean_of_values(ctx):
+    heads, kvh, hd, cached = 6, 2, 192, 300
+    kvw = kvh * hd
+    k = np.tile(o.normal(kvw, 22, 1), (cached, 1))
+    v = o.normal(cached * kvw, 22, 2).reshape(cached, kvw)
+    ks, kc = o.quantize_rows(o.Q8, k)
+    vs, vc = o.quantize_rows(o.Q8, v)
+    vd = o.dequantize_rows(o.Q8, vs, vc, cached, kvw).astype(np.float64)
+    q = o.normal(heads * hd, 22, 3)
+    actual = run_attention(ctx, q, (ks, kc, vs, vc), cached, heads, kvh, hd).reshape(heads, hd)
+    for h in range(heads):
+        g = h // (heads // kvh)
+        assert np.allclose(actual[h], vd[:, g * hd:(g + 1) * hd].mean(0), rtol=1e-5, atol=1e-5)
+
+
+def test_attention_rejects_heads_wider_than_built(ctx):
+    buf = ctx.buffer(1 << 20)
+    with pytest.raises(qa.QwhError) as err:
+        ctx.decode_attention_q8(buf.ptr, buf.ptr, buf.ptr, buf.ptr, buf.ptr, buf.ptr, 4, 2, 1, 1088)
+    assert err.value.status == -3
+    buf.free()

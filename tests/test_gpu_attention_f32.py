@@ -74,3 +74,22 @@ def test_f32_identical_keys_give_the_mean_of_values(ctx):
     mean = values.astype(np.float64).mean(axis=0).reshape(kvh, hd)
     for h in range(heads):
         assert np.allclose(actual[h], mean[h // (heads // kvh)], atol=1e-5), h
+
+
+@pytest.mark.parametrize("cached,hd,heads,kvh,batch", [(300, 192, 6, 2, 1), (129, 96, 3, 1, 1), (77, 40, 10, 2, 1),
+                                                       (513, 1024, 2, 1, 1), (200, 320, 9, 3, 2)])
+def test_f32_attention_any_head_shape(ctx, cached, hd, heads, kvh, batch):
+    # kernels.zig:583-593 takes any head_dim and any heads / kv_heads ratio:
+    # these run the one-workgroup-per-head kernel.
+    kvw = kvh * hd
+    keys = [o.normal(cached * kvw, 23, 10 * b) for b in range(batch)]
+    values = [o.normal(cached * kvw, 23, 10 * b + 1) for b in range(batch)]
+    q = o.normal(batch * heads * hd, 23, 5)
+    expected = np.concatenate([o.decode_attention(q[b * heads * hd:(b + 1) * heads * hd], keys[b], values[b], cached,
+                                                  heads, kvh, hd) for b in range(batch)])
+    stride = (keys[0].nbytes + 15) // 16 * 16
+    pad = np.zeros((stride - keys[0].nbytes) // 4, np.float32)
+    kcat = np.concatenate([np.concatenate([k, pad]) for k in keys])
+    vcat = np.concatenate([np.concatenate([v, pad]) for v in values])
+    actual = run_f32(ctx, q, kcat, vcat, cached, heads, kvh, hd, batch, stride if batch > 1 else 0)
+    assert_close(actual, expected, what=f"f32 attention cached {cached} hd {hd} {heads}/{kvh} batch {batch}")
