@@ -424,6 +424,35 @@ def bench_transcribe(ctx, qa, fmt, max_tokens=128, repeats=3):
                 total_ms=round(total * 1e3, 3), real_time_factor=round(30.0 / total, 1))
 
 
+def bench_dense_gemv(ctx, qa, rows, cols, tokens, steps, rotate_bytes, fmt):
+    """f32 / f16 weights (kernels.zig:54-112 linearF32 / linearF16): one call
+    per launch over a rotation of synthetic copies (>= rotate_bytes, so each
+    call streams its weights from HBM). Algorithmic bytes per call: the
+    weights once (up to four tokens share one pass), the activations and the
+    outputs."""
+    elem = 2 if fmt == qa.FORMAT_F16 else 4
+    per = rows * cols * elem
+    copies = max(1, math.ceil(rotate_bytes / per))
+    mats = [ctx.matrix_synthetic(fmt, rows, cols, 5, 40 + c, 0.02) for c in range(copies)]
+    x = ctx.buffer(tokens * cols * 4)
+    ctx.synth_normal(5, 39, tokens * cols, 1.0, x.ptr)
+    y = ctx.buffer(tokens * rows * 4)
+
+    def call(i):
+        ctx.linear(mats[i % copies], x.ptr, cols, tokens, y.ptr)
+
+    for i in range(10):
+        call(i)
+    ms = time_events(ctx, lambda i: call(10 + i), steps, warm=0)
+    for m in mats:
+        ctx.matrix_release(m)
+    x.free()
+    y.free()
+    nbytes = per + tokens * (cols + rows) * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(copies=copies, tokens=tokens, us=ms * 1e3, bytes=nbytes, GBs=gbs, frac=gbs / HBM_PEAK_GBS)
+
+
 def bench_small(ctx, qa, steps):
     from_seed = 1
     out = {}
@@ -467,6 +496,11 @@ def bench_small(ctx, qa, steps):
     g5 = bench_gemv(ctx, qa, 151936, 1024, steps, 10, 2.1e9, stream=9, fmt=qa.FORMAT_Q5)
     gbs = g5["bytes"] / (g5["call_ms"] * 1e-3) / 1e9
     out["q5_gemv_lm_head_0p6b"] = dict(us=g5["call_ms"] * 1e3, GBs=gbs, frac=gbs / 8000.0)
+    # The same shape with f16 weights (the converter's unquantized form), at
+    # one token and at four (one pass over the weights for the four).
+    for tokens in (1, 4):
+        out[f"f16_gemv_lm_head_0p6b_t{tokens}"] = bench_dense_gemv(ctx, qa, 151936, 1024, tokens, steps, 2.1e9,
+                                                                   qa.FORMAT_F16)
     # q4 GEMM, bf16 activations, M = 128 / 512 / 1500 at
     # [6144 x 2048] and [2048 x 6144]; the same GEMM for a q8 model's
     # matrices at M = 1500.

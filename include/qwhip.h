@@ -53,7 +53,10 @@ extern "C" {
 /* A HIP runtime error. Not in the reference (it has no device runtime). */
 #define QWH_E_DEVICE (-64)
 
-/* Format ids: src/core/dtype.zig:17-108 (on-disk values, never renumbered). */
+/* Format ids: src/core/dtype.zig:17-108 (on-disk values, never renumbered).
+ * Matrices hold f32, f16 (kernels.zig:160-166 Matrix) or a quantized format. */
+#define QWH_FORMAT_F32 0
+#define QWH_FORMAT_F16 1
 #define QWH_FORMAT_Q4 16
 #define QWH_FORMAT_Q5 17
 #define QWH_FORMAT_Q8 18
@@ -105,7 +108,7 @@ int32_t qwh_stream_read(qwh_ctx *ctx, const void *src_dev, uint64_t bytes, uint3
                         uint32_t *sink_dev);
 
 /* ---------------------------------------------------------------------- */
-/* Quantized matrices (quant.zig planeLayout + kernels.zig Matrix)          */
+/* Weight matrices (kernels.zig Matrix, quant.zig planeLayout)             */
 /* ---------------------------------------------------------------------- */
 
 /* Uploads a rows x cols quantized matrix given as the two planes
@@ -113,22 +116,29 @@ int32_t qwh_stream_read(qwh_ctx *ctx, const void *src_dev, uint64_t bytes, uint3
  * cols/64 f16 values (little endian, groups row major), `data` the packed
  * codes. The row count must agree with the scale plane as Matrix.rows
  * derives it (kernels.zig:170-178). Replaces Binding.matrix
- * (model.zig:92-114) for the device. */
+ * (model.zig:92-114) for the device. For QWH_FORMAT_F32 / QWH_FORMAT_F16
+ * (the Matrix .f32 / .f16 arms, kernels.zig:161-166) there is no scale plane
+ * (scales may be NULL, scales_len must be 0) and `data` holds the rows * cols
+ * elements row major (f16 as little-endian bit patterns), any cols >= 1. */
 int32_t qwh_matrix_upload(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols,
                           const uint8_t *scales, uint64_t scales_len, const uint8_t *data,
                           uint64_t data_len, uint64_t *out_matrix);
 /* Borrows planes already resident on the device (for example a whole .qw
  * shard uploaded at once): the caller keeps them alive until release, as the
- * reference's Matrix borrows shard bytes (wasm/model.zig:28-42). */
+ * reference's Matrix borrows shard bytes (wasm/model.zig:28-42). Quantized
+ * data planes 16-byte aligned; f32 / f16 elements aligned to their size
+ * (model.zig:79-90), scales_dev ignored. */
 int32_t qwh_matrix_wrap(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols,
                         const void *scales_dev, const void *data_dev, uint64_t *out_matrix);
 /* A matrix whose values are f32(N(0,1)) * value_scale from the synthetic
  * generator (seed, stream), quantized on the device bit-exactly as
- * quant.quantizeRow. For benchmarks and tests with random-init weights. */
+ * quant.quantizeRow (f16: rounded to nearest even, half_float.zig:12-16;
+ * f32: as generated). For benchmarks and tests with random-init weights. */
 int32_t qwh_matrix_synthetic(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols,
                              uint32_t seed, uint32_t stream, float value_scale,
                              uint64_t *out_matrix);
-/* Device addresses of a matrix's two planes. */
+/* Device addresses of a matrix's two planes (no scale plane, NULL, for f32
+ * and f16). */
 int32_t qwh_matrix_planes(qwh_ctx *ctx, uint64_t matrix, void **scales_dev, void **data_dev);
 int32_t qwh_matrix_release(qwh_ctx *ctx, uint64_t matrix);
 
@@ -175,9 +185,11 @@ int32_t qwh_shard_load(qwh_ctx *ctx, const void *bytes, uint64_t len, uint64_t *
  * tensor inside the loaded payload (and its entry, when `entry` is set). */
 int32_t qwh_shard_tensor(qwh_ctx *ctx, uint64_t shard, uint16_t kind, uint16_t layer, void **dev,
                          qwh_tensor_entry *entry);
-/* File.quantizedPlanes (container.zig:245-262) as a matrix handle that
- * borrows the two planes inside the loaded payload (no copy); element-format
- * tensors return QWH_E_NOT_FOUND, as quantizedPlanes returns null. */
+/* File.quantizedPlanes (container.zig:248-266) as a matrix handle that
+ * borrows the two planes inside the loaded payload (no copy). f32 / f16
+ * tensors of rank 2 become matrices over their elements in place, as
+ * Binding.matrix makes them (model.zig:92-96); other element tensors (bf16,
+ * vectors) return QWH_E_NOT_FOUND, as quantizedPlanes returns null. */
 int32_t qwh_shard_matrix(qwh_ctx *ctx, uint64_t shard, uint16_t kind, uint16_t layer,
                          uint64_t *out_matrix);
 /* Frees the device payload; QWH_E_INVALID_STATE while a matrix borrows from
@@ -188,7 +200,9 @@ int32_t qwh_shard_release(qwh_ctx *ctx, uint64_t shard);
  * out[tokens][rows] = W[rows][cols] * x[tokens][cols], f32 in, f32 out.
  * `cols` must equal the matrix's column count. Formats q4 and q8 at any
  * shape; q5 (the WebGPU decoder's format, passes.ts:63-67) for cols <= 6144
- * with an 8-byte aligned data plane below 4 GiB, else QWH_E_UNSUPPORTED. */
+ * with an 8-byte aligned data plane below 4 GiB; f32 and f16
+ * (linearF32 / linearF16, :54-112) for cols <= 16380; else
+ * QWH_E_UNSUPPORTED. */
 int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t cols,
                    uint32_t tokens, float *out_dev);
 /* qwh_linear in two halves, for callers that apply several matrices to the

@@ -84,6 +84,7 @@ _SIGNATURES = {
     "qwref_dot_f32": (_F, [_P, _P, _U32]),
     "qwref_linear_quantized": (_I32, [_P, _P, _I32, _P, _U64, _P, _U64, _U32, _U32, _U32]),
     "qwref_linear_f32": (_I32, [_P, _P, _P, _U32, _U32, _U32]),
+    "qwref_linear_f16": (_I32, [_P, _P, _P, _U32, _U32, _U32]),
     "qwref_add_in_place": (None, [_P, _P, _U32]),
     "qwref_silu_mul": (None, [_P, _P, _P, _U32]),
     "qwref_silu": (_F, [_F]),
@@ -231,6 +232,18 @@ def linear_f32(weights: np.ndarray, x: np.ndarray, tokens: int = 1) -> np.ndarra
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     out = np.zeros(tokens * rows, np.float32)
     lib().qwref_linear_f32(_ptr(out), _ptr(x), _ptr(weights), rows, cols, tokens)
+    return out.reshape(tokens, rows)
+
+
+def linear_f16(weights: np.ndarray, x: np.ndarray, tokens: int = 1) -> np.ndarray:
+    """kernels.zig:82-112 linearF16 over f16 bit patterns [rows, cols] (uint16)."""
+    weights = np.ascontiguousarray(weights, np.uint16)
+    rows, cols = weights.shape
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(tokens * rows, np.float32)
+    status = lib().qwref_linear_f16(_ptr(out), _ptr(x), _ptr(weights), rows, cols, tokens)
+    if status != 0:
+        raise ValueError(f"linear_f16 status {status}")
     return out.reshape(tokens, rows)
 
 

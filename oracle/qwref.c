@@ -349,6 +349,21 @@ int32_t qwref_linear_f32(float *out, const float *x, const float *weights, uint3
     return QWREF_OK;
 }
 
+/* kernels.zig:82-112 `linearF16`: each weight row widened into scratch
+ * (half_float.fromF16), then dotF32 against every token. */
+int32_t qwref_linear_f16(float *out, const float *x, const uint16_t *weights, uint32_t rows,
+                         uint32_t cols, uint32_t tokens) {
+    float *scratch = (float *)malloc(sizeof(float) * (cols ? cols : 1));
+    if (!scratch) return QWREF_LIMIT_EXCEEDED;
+    for (uint32_t row = 0; row < rows; ++row) {
+        for (uint32_t k = 0; k < cols; ++k) scratch[k] = qwref_from_f16(weights[(size_t)row * cols + k]);
+        for (uint32_t token = 0; token < tokens; ++token)
+            out[(size_t)token * rows + row] = qwref_dot_f32(scratch, x + (size_t)token * cols, cols);
+    }
+    free(scratch);
+    return QWREF_OK;
+}
+
 /* kernels.zig:118-158 `linearQuantized` (reached through Matrix.apply,
  * kernels.zig:182-206): shape checks, then per row dequantizeRow into
  * scratch and dotF32 against every token. Rows are independent, so the

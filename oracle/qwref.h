@@ -104,6 +104,8 @@ int32_t qwref_linear_quantized(float *out, const float *x, int32_t format, const
                                uint32_t rows, uint32_t cols, uint32_t tokens);
 int32_t qwref_linear_f32(float *out, const float *x, const float *weights, uint32_t rows,
                          uint32_t cols, uint32_t tokens);
+int32_t qwref_linear_f16(float *out, const float *x, const uint16_t *weights, uint32_t rows,
+                         uint32_t cols, uint32_t tokens);
 void qwref_add_in_place(float *x, const float *y, uint32_t len);
 void qwref_silu_mul(float *out, const float *gate, const float *up, uint32_t len);
 float qwref_silu(float x);

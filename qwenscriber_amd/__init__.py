@@ -11,6 +11,8 @@ from ._lib import (  # noqa: F401
     CACHE_F32,
     CACHE_Q8,
     DATA_BYTES,
+    FORMAT_F16,
+    FORMAT_F32,
     FORMAT_Q4,
     FORMAT_Q5,
     FORMAT_Q8,

@@ -14,6 +14,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
+FORMAT_F32, FORMAT_F16 = 0, 1
 FORMAT_Q4, FORMAT_Q5, FORMAT_Q8 = 16, 17, 18
 GROUP_SIZE = 64
 DATA_BYTES = {FORMAT_Q4: 32, FORMAT_Q5: 40, FORMAT_Q8: 64}
@@ -359,11 +360,17 @@ class Context:
         return out.value
 
     # -- matrices (kernels.zig Matrix) ------------------------------------
-    def matrix_upload(self, fmt: int, rows: int, cols: int, scales: np.ndarray, data: np.ndarray) -> int:
-        scales = np.ascontiguousarray(scales, np.uint8)
-        data = np.ascontiguousarray(data, np.uint8)
+    def matrix_upload(self, fmt: int, rows: int, cols: int, scales: Optional[np.ndarray], data: np.ndarray) -> int:
+        """Quantized planes, or for f32 / f16 (scales None) the elements as
+        bytes or as a float32 / uint16 array."""
+        data = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
         out = ctypes.c_uint64()
-        self._check(self.lib.qwh_matrix_upload(self.handle, fmt, rows, cols, _ptr(scales), scales.size,
+        if scales is None:
+            s_ptr, s_len = None, 0
+        else:
+            scales = np.ascontiguousarray(scales, np.uint8)
+            s_ptr, s_len = _ptr(scales), scales.size
+        self._check(self.lib.qwh_matrix_upload(self.handle, fmt, rows, cols, s_ptr, s_len,
                                                _ptr(data), data.size, ctypes.byref(out)))
         return out.value
 

@@ -79,6 +79,18 @@ int32_t plane_sizes(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, 
     return QWH_OK;
 }
 
+// Plane sizes of any matrix: the quantized planes above, or for f32 / f16
+// (kernels.zig:160-166 Matrix .f32 / .f16) no scale plane and rows * cols
+// elements.
+int32_t matrix_bytes(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, size_t &scales, size_t &data) {
+    if (!is_dense_format(format)) return plane_sizes(ctx, format, rows, cols, scales, data);
+    // Matrix.rows divides the element count by cols (kernels.zig:170-172).
+    if (cols == 0) return fail(ctx, QWH_E_SHAPE_MISMATCH, "cols is 0");
+    scales = 0;
+    data = (size_t)rows * cols * dense_element_bytes(format);
+    return QWH_OK;
+}
+
 }  // namespace
 
 uint64_t add_matrix(qwh_ctx *ctx, const Matrix &m) {
@@ -290,9 +302,10 @@ int32_t qwh_event_elapsed(qwh_ctx *ctx, uint32_t start, uint32_t end, float *out
 
 int32_t qwh_matrix_upload(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t cols, const uint8_t *scales,
                           uint64_t scales_len, const uint8_t *data, uint64_t data_len, uint64_t *out_matrix) {
-    if (!ctx || !out_matrix || !scales || !data) return QWH_E_INVALID_ARGUMENT;
+    const bool dense = is_dense_format(format);
+    if (!ctx || !out_matrix || (!scales && !dense) || !data) return QWH_E_INVALID_ARGUMENT;
     size_t s_bytes, d_bytes;
-    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
+    QWH_TRY(matrix_bytes(ctx, format, rows, cols, s_bytes, d_bytes));
     if (scales_len != s_bytes)
         return fail(ctx, QWH_E_SHAPE_MISMATCH, "scale plane is %llu bytes, a %ux%u matrix needs %zu",
                     (unsigned long long)scales_len, rows, cols, s_bytes);
@@ -304,12 +317,15 @@ int32_t qwh_matrix_upload(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t 
     m.rows = rows;
     m.cols = cols;
     m.owned = true;
-    if (hipMalloc(&m.scales, s_bytes ? s_bytes : 1) != hipSuccess || hipMalloc(&m.data, d_bytes ? d_bytes : 1) != hipSuccess) {
+    if ((!dense && hipMalloc(&m.scales, s_bytes ? s_bytes : 1) != hipSuccess) ||
+        hipMalloc(&m.data, d_bytes ? d_bytes : 1) != hipSuccess) {
         (void)hipGetLastError();
         if (m.scales) (void)hipFree(m.scales);
         return fail(ctx, QWH_E_OUT_OF_MEMORY, "matrix planes of %zu + %zu bytes", s_bytes, d_bytes);
     }
-    int32_t st = check_hip(ctx, hipMemcpyAsync(m.scales, scales, s_bytes, hipMemcpyHostToDevice, ctx->stream), "upload scales");
+    int32_t st = QWH_OK;
+    if (s_bytes)
+        st = check_hip(ctx, hipMemcpyAsync(m.scales, scales, s_bytes, hipMemcpyHostToDevice, ctx->stream), "upload scales");
     if (st == QWH_OK)
         st = check_hip(ctx, hipMemcpyAsync(m.data, data, d_bytes, hipMemcpyHostToDevice, ctx->stream), "upload data");
     if (st == QWH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "upload sync");
@@ -326,12 +342,20 @@ int32_t qwh_matrix_wrap(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32_t co
                         const void *data_dev, uint64_t *out_matrix) {
     if (!ctx || !out_matrix) return QWH_E_INVALID_ARGUMENT;
     size_t s_bytes, d_bytes;
-    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
-    QWH_TRY(check_device_ptr(ctx, scales_dev, "scales"));
+    QWH_TRY(matrix_bytes(ctx, format, rows, cols, s_bytes, d_bytes));
     QWH_TRY(check_device_ptr(ctx, data_dev, "data"));
-    if (((uintptr_t)data_dev & 15u) != 0)
-        return fail(ctx, QWH_E_INVALID_ARGUMENT, "data plane must be 16-byte aligned (quant.zig:61-63)");
-    if (((uintptr_t)scales_dev & 1u) != 0) return fail(ctx, QWH_E_INVALID_ARGUMENT, "scale plane must be 2-byte aligned");
+    if (is_dense_format(format)) {
+        // model.zig:79-90 Binding f32Values / f16Values: element-aligned.
+        if (((uintptr_t)data_dev & (dense_element_bytes(format) - 1)) != 0)
+            return fail(ctx, QWH_E_INVALID_ARGUMENT, "f32 / f16 elements must be aligned to their size");
+        scales_dev = nullptr;
+    } else {
+        QWH_TRY(check_device_ptr(ctx, scales_dev, "scales"));
+        if (((uintptr_t)data_dev & 15u) != 0)
+            return fail(ctx, QWH_E_INVALID_ARGUMENT, "data plane must be 16-byte aligned (quant.zig:61-63)");
+        if (((uintptr_t)scales_dev & 1u) != 0)
+            return fail(ctx, QWH_E_INVALID_ARGUMENT, "scale plane must be 2-byte aligned");
+    }
     Matrix m;
     m.format = format;
     m.rows = rows;
@@ -347,28 +371,38 @@ int32_t qwh_matrix_synthetic(qwh_ctx *ctx, int32_t format, uint32_t rows, uint32
                              float value_scale, uint64_t *out_matrix) {
     if (!ctx || !out_matrix) return QWH_E_INVALID_ARGUMENT;
     size_t s_bytes, d_bytes;
-    QWH_TRY(plane_sizes(ctx, format, rows, cols, s_bytes, d_bytes));
+    QWH_TRY(matrix_bytes(ctx, format, rows, cols, s_bytes, d_bytes));
+    const bool dense = is_dense_format(format);
     Matrix m;
     m.format = format;
     m.rows = rows;
     m.cols = cols;
     m.owned = true;
-    if (hipMalloc(&m.scales, s_bytes ? s_bytes : 1) != hipSuccess || hipMalloc(&m.data, d_bytes ? d_bytes : 1) != hipSuccess) {
+    if ((!dense && hipMalloc(&m.scales, s_bytes ? s_bytes : 1) != hipSuccess) ||
+        hipMalloc(&m.data, d_bytes ? d_bytes : 1) != hipSuccess) {
         (void)hipGetLastError();
         if (m.scales) (void)hipFree(m.scales);
         return fail(ctx, QWH_E_OUT_OF_MEMORY, "matrix planes of %zu + %zu bytes", s_bytes, d_bytes);
     }
+    // f32 values go straight into the data plane; f16 and quantized ones
+    // through a slab of f32 values.
     const size_t slab_values = (size_t)64 << 20;
     float *temp = nullptr;
-    int32_t st = check_hip(ctx, hipMalloc(&temp, slab_values * 4), "synthetic temp");
+    int32_t st = format == QWH_FORMAT_F32 ? QWH_OK : check_hip(ctx, hipMalloc(&temp, slab_values * 4), "synthetic temp");
     const uint32_t slab_rows = (uint32_t)(slab_values / cols) ? (uint32_t)(slab_values / cols) : 1;
     const size_t gpr = cols / kGroup;
     const int db = data_bytes_per_group(format);
     for (uint32_t r = 0; r < rows && st == QWH_OK; r += slab_rows) {
         const uint32_t n = rows - r < slab_rows ? rows - r : slab_rows;
-        st = check_hip(ctx, launch_synth_normal(ctx->stream, seed, stream, (uint64_t)r * cols, (uint64_t)n * cols,
-                                                value_scale, temp), "synthetic values");
-        if (st == QWH_OK)
+        const uint64_t first = (uint64_t)r * cols, count = (uint64_t)n * cols;
+        float *values = format == QWH_FORMAT_F32 ? reinterpret_cast<float *>(m.data) + first : temp;
+        st = check_hip(ctx, launch_synth_normal(ctx->stream, seed, stream, first, count, value_scale, values),
+                       "synthetic values");
+        if (st != QWH_OK || format == QWH_FORMAT_F32) continue;
+        if (format == QWH_FORMAT_F16)
+            st = check_hip(ctx, launch_f32_to_f16(ctx->stream, temp, count, reinterpret_cast<uint16_t *>(m.data) + first),
+                           "f16 values");
+        else
             st = check_hip(ctx, launch_quantize_rows(ctx->stream, format, temp, (uint64_t)n * gpr,
                                                      m.scales + (size_t)r * gpr * 2, m.data + (size_t)r * gpr * db),
                            "quantize");
@@ -487,6 +521,16 @@ int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t c
         in.mode = GemvInput::F32;
         in.x = x_dev;
         return check_hip(ctx, launch_gemv_b8(ctx->stream, ctx->cus, in, *m, tokens, out_dev, nullptr), "gemv q5");
+    }
+    if (is_dense_format(m->format)) {
+        // kernels.zig:54-112 linearF32 / linearF16: up to four tokens per
+        // pass over the weights.
+        if (!gemv_dense_supported(m->format, m->cols))
+            return fail(ctx, QWH_E_UNSUPPORTED, "f32 / f16 linear is built for rows of at most %u values", kDenseMaxCols);
+        GemvInput in;
+        in.mode = GemvInput::F32;
+        in.x = x_dev;
+        return check_hip(ctx, launch_gemv_dense(ctx->stream, ctx->cus, in, *m, tokens, out_dev, nullptr), "gemv dense");
     }
     return fail(ctx, QWH_E_UNSUPPORTED, "linear over format %d is not built", m->format);
 }

@@ -25,6 +25,10 @@ inline int data_bytes_per_group(int format) {
     }
 }
 
+// Element formats a Matrix may hold (kernels.zig:160-166: f32, f16).
+inline bool is_dense_format(int format) { return format == QWH_FORMAT_F32 || format == QWH_FORMAT_F16; }
+inline size_t dense_element_bytes(int format) { return format == QWH_FORMAT_F32 ? 4 : 2; }
+
 inline int format_bias(int format) {  // quant.zig:111-118
     switch (format) {
     case QWH_FORMAT_Q4: return 8;
@@ -38,8 +42,11 @@ struct Matrix {
     int32_t format = 0;
     uint32_t rows = 0;
     uint32_t cols = 0;
-    uint8_t *scales = nullptr;  // rows * cols/64 f16, little endian, row major
-    uint8_t *data = nullptr;    // rows * cols/64 * data_bytes_per_group
+    // Quantized formats: rows * cols/64 f16 scales, little endian, row major,
+    // and rows * cols/64 * data_bytes_per_group code bytes. f32 / f16: no
+    // scale plane, data holds the rows * cols elements, row major.
+    uint8_t *scales = nullptr;
+    uint8_t *data = nullptr;
     bool owned = false;
     uint64_t shard = 0;         // the shard whose payload it borrows, or 0
 };
@@ -162,6 +169,18 @@ hipError_t launch_gemv_b8(hipStream_t s, int cus, const GemvInput &in, const Mat
                           float *out, const float *residual);
 hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &w,
                           uint32_t tokens, float *out, const float *residual);
+
+// f16 / f32 weights (gemv_dense.hip, kernels.zig:54-112 linearF32 /
+// linearF16): F32 and RmsNorm input forms, pairs and residual as the q4
+// GEMV, rows of 1..kDenseMaxCols values (one token's activations in LDS),
+// token counts up to 65535 groups of four (two for rows of more than 4092
+// values, one for rows of more than 8188).
+constexpr uint32_t kDenseMaxCols = 16380;
+bool gemv_dense_supported(int format, uint32_t cols);
+hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
+                             float *out, const float *residual);
+// out[i] = f16 bits of in[i], round to nearest even (half_float.zig:12-16).
+hipError_t launch_f32_to_f16(hipStream_t s, const float *in, uint64_t count, uint16_t *out);
 
 // Small-batch q4 / q8 GEMV on the matrix cores (gemv_batch.hip): activations
 // as int8 digit planes per 16-token tile, then one MFMA pass over the

@@ -260,8 +260,22 @@ int32_t qwh_shard_matrix(qwh_ctx *ctx, uint64_t shard, uint16_t kind, uint16_t l
     void *dev = nullptr;
     qwh_tensor_entry e{};
     QWH_TRY(qwh_shard_tensor(ctx, shard, kind, layer, &dev, &e));
-    // File.quantizedPlanes (container.zig:245-262): none for element formats.
-    if (!quantized(e.format)) return fail(ctx, QWH_E_NOT_FOUND, "tensor kind %u layer %u is not quantized", kind, layer);
+    if (is_dense_format(e.format) && e.rank == 2) {
+        // model.zig:92-96 Binding.matrix: an f32 / f16 tensor's elements, in
+        // place, as a dims[0] x dims[1] matrix.
+        Matrix m;
+        m.format = e.format;
+        m.rows = e.dims[0];
+        m.cols = e.dims[1];
+        m.data = static_cast<uint8_t *>(dev);
+        m.owned = false;
+        m.shard = shard;
+        *out_matrix = add_matrix(ctx, m);
+        return QWH_OK;
+    }
+    // File.quantizedPlanes (container.zig:248-266): none for other element
+    // tensors (bf16, or vectors).
+    if (!quantized(e.format)) return fail(ctx, QWH_E_NOT_FOUND, "tensor kind %u layer %u is not a matrix", kind, layer);
     Planes p;
     plane_layout(e.format, e.dims[0], e.dims[1], e.offset_bytes, p);
     Matrix m;

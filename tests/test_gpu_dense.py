@@ -1,0 +1,194 @@
+"""GPU parity of f16 / f32 weight matrices (kernels.zig:160-206 Matrix .f16 /
+.f32 arms: linearF16 :82-112, linearF32 :54-80) against the oracle on the
+same seeded inputs. Both sides form the same exact f32 products (an f16
+weight widens exactly); only the summation order differs (the reference's
+four-lane dotF32 against a wavefront reduction), so the bound is tight:
+|a - r| <= 1e-4 |r| + 1e-4 rms(r) (util.assert_close)."""
+import os
+
+import numpy as np
+import pytest
+
+import qwenscriber_amd as qa
+from oracle import oracle as o
+from oracle import shard as sh
+from util import assert_close
+
+pytestmark = pytest.mark.gpu
+o.set_threads(min(16, os.cpu_count() or 1))
+
+TOL = dict(rtol=1e-4, atol_rms=1e-4)
+
+
+def weights(fmt, rows, cols, seed, stream=0):
+    """Seeded weights as the matrix stores them (f16 bits or f32 values)."""
+    w = o.normal(rows * cols, seed, stream, 0.02).reshape(rows, cols)
+    return w.astype(np.float16).view(np.uint16) if fmt == qa.FORMAT_F16 else w
+
+
+def expected(fmt, w, x, tokens):
+    return o.linear_f16(w, x, tokens) if fmt == qa.FORMAT_F16 else o.linear_f32(w, x, tokens)
+
+
+def run(ctx, handle, x, cols, tokens, rows):
+    xb = ctx.to_device(np.ascontiguousarray(x, np.float32))
+    ob = ctx.buffer(tokens * rows * 4)
+    try:
+        ctx.linear(handle, xb.ptr, cols, tokens, ob.ptr)
+        return ob.download(np.float32).reshape(tokens, rows)
+    finally:
+        xb.free()
+        ob.free()
+
+
+FORMATS = [qa.FORMAT_F16, qa.FORMAT_F32]
+SHAPES = [  # (rows, cols, tokens): one, four, two or one token per workgroup
+    (1024, 1024, 1),    # decoder k / v (0.6B)
+    (3072, 1024, 1),    # gate / up (0.6B)
+    (1024, 3072, 5),    # down, a four-token group and a one-token tail
+    (40, 6144, 3),      # rows too wide for four tokens: groups of two
+    (64, 16380, 2),     # the widest rows: one token per workgroup
+    (257, 67, 3),       # rows that are not whole 16-byte slices
+    (7, 1, 9),          # one column
+]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("rows,cols,tokens", SHAPES)
+def test_dense_linear(ctx, fmt, rows, cols, tokens):
+    w = weights(fmt, rows, cols, 31, rows + cols)
+    x = o.normal(tokens * cols, 32, tokens)
+    handle = ctx.matrix_upload(fmt, rows, cols, None, w)
+    try:
+        actual = run(ctx, handle, x, cols, tokens, rows)
+    finally:
+        ctx.matrix_release(handle)
+    assert_close(actual, expected(fmt, w, x, tokens), what=f"format {fmt} {rows}x{cols} tokens {tokens}", **TOL)
+
+
+def test_dense_matrix_dispatch_ones(ctx):
+    # kernels.zig:932-948: 2 x 64 ones against ones give exactly 64.
+    x = np.ones(64, np.float32)
+    for fmt, w in ((qa.FORMAT_F32, np.ones((2, 64), np.float32)),
+                   (qa.FORMAT_F16, np.full((2, 64), o.to_f16(1.0), np.uint16))):
+        handle = ctx.matrix_upload(fmt, 2, 64, None, w)
+        try:
+            assert run(ctx, handle, x, 64, 1, 2).tolist() == [[64.0, 64.0]]
+        finally:
+            ctx.matrix_release(handle)
+
+
+@pytest.mark.parametrize("fmt,offset", [(qa.FORMAT_F16, 2), (qa.FORMAT_F16, 6), (qa.FORMAT_F32, 4)])
+def test_dense_wrap_unaligned_rows(ctx, fmt, offset):
+    # Elements aligned to their size but not to 16 bytes take the
+    # element-wise form.
+    rows, cols, tokens = 96, 512, 3
+    w = weights(fmt, rows, cols, 33)
+    x = o.normal(tokens * cols, 34)
+    buf = ctx.buffer(w.nbytes + 16)
+    buf.upload(w, offset)
+    handle = ctx.matrix_wrap(fmt, rows, cols, 0, buf.ptr + offset)
+    try:
+        actual = run(ctx, handle, x, cols, tokens, rows)
+    finally:
+        ctx.matrix_release(handle)
+        buf.free()
+    assert_close(actual, expected(fmt, w, x, tokens), what=f"wrapped format {fmt} at +{offset}", **TOL)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_dense_synthetic(ctx, fmt):
+    # f32(N(0,1)) * scale from the synthetic generator, rounded to f16 (RNE,
+    # half_float.zig:12-16) for f16 matrices: bit exact against the oracle's
+    # generator and numpy's f16 rounding.
+    rows, cols, seed, stream, scale = 300, 1000, 9, 4, 0.05
+    handle = ctx.matrix_synthetic(fmt, rows, cols, seed, stream, scale)
+    try:
+        scales_dev, data_dev = ctx.matrix_planes(handle)
+        assert scales_dev is None
+        values = o.normal(rows * cols, seed, stream, scale).reshape(rows, cols)
+        if fmt == qa.FORMAT_F16:
+            want = values.astype(np.float16).view(np.uint16)
+            sample = np.array([o.to_f16(float(v)) for v in values.flat[:512]], np.uint16)
+            assert np.array_equal(sample, want.flat[:512])
+        else:
+            want = values
+        got = np.empty_like(want)
+        ctx._check(ctx.lib.qwh_download(ctx.handle, got.ctypes.data, data_dev, got.nbytes))
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+        x = o.normal(2 * cols, 35)
+        actual = run(ctx, handle, x, cols, 2, rows)
+    finally:
+        ctx.matrix_release(handle)
+    assert_close(actual, expected(fmt, want, x, 2), what=f"synthetic format {fmt}", **TOL)
+
+
+def test_dense_shard_matrices(ctx):
+    # model.zig:92-96 Binding.matrix: f32 / f16 tensors of rank 2 are
+    # matrices over their elements in place; vectors are not matrices.
+    specs = [(sh.KIND_DECODER_Q, 1, qa.FORMAT_F16, 200, 1024), (sh.KIND_DECODER_FFN_DOWN, 1, qa.FORMAT_F32, 130, 520)]
+    tensors, mats = [], {}
+    for i, (kind, layer, fmt, rows, cols) in enumerate(specs):
+        w = weights(fmt, rows, cols, 36, i)
+        mats[(kind, layer)] = (fmt, rows, cols, w)
+        tensors.append(dict(kind=kind, layer=layer, format=fmt, dims=(rows, cols), payload=w.tobytes()))
+    tensors.append(dict(kind=sh.KIND_DECODER_FINAL_NORM, layer=0, format=sh.F16, dims=(1024,),
+                        payload=np.ones(1024, np.float16).tobytes()))
+    shard = ctx.shard_load(sh.build(tensors))
+    handles = []
+    try:
+        for (kind, layer), (fmt, rows, cols, w) in mats.items():
+            m = ctx.shard_matrix(shard, kind, layer)
+            handles.append(m)
+            x = o.normal(3 * cols, 37, kind)
+            assert_close(run(ctx, m, x, cols, 3, rows), expected(fmt, w, x, 3), what=f"shard kind {kind}", **TOL)
+        with pytest.raises(qa.QwhError) as err:
+            ctx.shard_matrix(shard, sh.KIND_DECODER_FINAL_NORM, 0)
+        assert err.value.status == sh.NOT_FOUND
+    finally:
+        for m in handles:
+            ctx.matrix_release(m)
+        ctx.shard_release(shard)
+
+
+def test_dense_errors(ctx):
+    f16 = np.zeros((4, 64), np.uint16)
+    # A scale plane for an element format.
+    with pytest.raises(qa.QwhError) as err:
+        ctx.matrix_upload(qa.FORMAT_F16, 4, 64, np.zeros(2, np.uint8), f16)
+    assert err.value.status == -7
+    # Elements not aligned to their size.
+    buf = ctx.buffer(1024)
+    try:
+        with pytest.raises(qa.QwhError) as err:
+            ctx.matrix_wrap(qa.FORMAT_F16, 4, 64, 0, buf.ptr + 1)
+        assert err.value.status == -1
+        with pytest.raises(qa.QwhError) as err:
+            ctx.matrix_wrap(qa.FORMAT_F32, 4, 64, 0, buf.ptr + 2)
+        assert err.value.status == -1
+        # No columns.
+        with pytest.raises(qa.QwhError) as err:
+            ctx.matrix_wrap(qa.FORMAT_F32, 4, 0, 0, buf.ptr)
+        assert err.value.status == -7
+        # Device quantization only writes quantized planes.
+        with pytest.raises(qa.QwhError) as err:
+            ctx.quantize_rows(qa.FORMAT_F16, buf.ptr, 1, 64, buf.ptr, buf.ptr)
+        assert err.value.status == -3
+    finally:
+        buf.free()
+    # Rows wider than one token's activations in LDS.
+    wide = 16381
+    handle = ctx.matrix_upload(qa.FORMAT_F32, 1, wide, None, np.zeros(wide, np.float32))
+    xb = ctx.buffer(wide * 4)
+    ob = ctx.buffer(64)
+    try:
+        with pytest.raises(qa.QwhError) as err:
+            ctx.linear(handle, xb.ptr, wide, 1, ob.ptr)
+        assert err.value.status == -3
+        with pytest.raises(qa.QwhError) as err:
+            ctx.linear_bf16(handle, xb.ptr, wide, 1, ob.ptr)
+        assert err.value.status == -3
+    finally:
+        ctx.matrix_release(handle)
+        xb.free()
+        ob.free()

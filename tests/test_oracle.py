@@ -218,6 +218,33 @@ def test_linear_f32_hand_computed():
     assert out.tolist() == [[1.0, 5.0], [4.0, 11.0]]
 
 
+def test_matrix_dispatch_every_storage_kind():
+    # kernels.zig:932-948: 2 x 64 ones against ones give 64 for f32 and f16.
+    x = np.ones(64, np.float32)
+    assert o.linear_f32(np.ones((2, 64), np.float32), x).tolist() == [[64.0, 64.0]]
+    ones_f16 = np.full((2, 64), o.to_f16(1.0), np.uint16)
+    assert o.linear_f16(ones_f16, x).tolist() == [[64.0, 64.0]]
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(5, 67, 3), (9, 256, 2), (3, 1, 4)])
+def test_linear_f16_against_numpy_widening_and_f64(rows, cols, tokens):
+    # Every finite f16 class (subnormals, the largest normal, both signs):
+    # numpy's own f16 -> f32 widening then the f32 linear must agree bit for
+    # bit, and the result must sit within f32 rounding of the f64 product.
+    rng = np.random.default_rng(rows * 1000 + cols)
+    bits = rng.integers(0, 1 << 16, size=(rows, cols), dtype=np.uint16)
+    bits[(bits & 0x7C00) == 0x7C00] &= 0x83FF  # inf / NaN -> subnormals
+    bits.flat[0] = 0x7BFF  # 65504
+    bits.flat[-1] = 0x0001  # the smallest subnormal
+    x = (normal(tokens * cols, 5, 3) * np.float32(1e-3)).reshape(tokens, cols)
+    widened = bits.view(np.float16).astype(np.float32)
+    actual = o.linear_f16(bits, x, tokens)
+    assert np.array_equal(actual, o.linear_f32(widened, x, tokens))
+    expected = x.astype(np.float64) @ widened.astype(np.float64).T
+    scale = np.abs(x.astype(np.float64)) @ np.abs(widened.astype(np.float64)).T
+    assert np.all(np.abs(actual - expected) <= 1e-6 * scale + 1e-30)
+
+
 def test_linear_shape_mismatch():
     s, d = o.quantize_rows(o.Q4, np.ones((2, 64), np.float32))
     lib = o.lib()
