@@ -445,9 +445,11 @@ int32_t qwh_decoder_create(qwh_ctx *ctx, const qwh_decoder_config *config, uint3
 int32_t qwh_decoder_create_cache(qwh_ctx *ctx, const qwh_decoder_config *config, uint32_t batch,
                                  uint32_t cache_format, qwh_decoder **out);
 int32_t qwh_decoder_destroy(qwh_decoder *decoder);
-/* Binds a quantized matrix (QWH_T_EMBED..QWH_T_LM_HEAD) in q4, q5 or q8:
+/* Binds a matrix (QWH_T_EMBED..QWH_T_LM_HEAD) in q4, q5, q8, f16 or f32:
  * each matrix is applied in its own format, as Matrix.apply applies whatever
- * storage it holds (kernels.zig:182-206). The decoder copies the planes into
+ * storage it holds (kernels.zig:182-206), and an f32 / f16 embedding gives
+ * its rows as embeddingRow does (decoder.zig:346-360). f32 / f16 rows of up
+ * to 16380 values. The decoder copies the planes into
  * its own blocks: q / k / v into one fused row block and gate / up into one
  * block with their rows interleaved (gate row j, then up row j). A fused
  * block holds one format, so binding a member in another format re-creates
@@ -462,7 +464,8 @@ int32_t qwh_decoder_set_vector(qwh_decoder *decoder, uint32_t kind, uint32_t lay
  * container.TensorKind 30..43 (container.zig:367-380) at layer 0 (embedding,
  * final norm, output projection) and layers 1..layers (the decoder's layer
  * L - 1); other kinds (audio tower, projector) are skipped. Matrices may be
- * q4, q5 or q8 (the converter writes one format for all, layout.zig:49-53)
+ * q4, q5, q8, or f16 / f32 tensors of rank 2 (the converter writes one
+ * format for all, layout.zig:49-53, f16 for --quantization none)
  * and are copied (the shard may be released afterwards); norm vectors
  * may be f32, f16 or bf16 and are widened to f32. With
  * QWH_BIND_OUTPUT_TIED (config.bin flags bit 0, model_config.zig) the
@@ -475,8 +478,9 @@ int32_t qwh_decoder_bind_shard(qwh_decoder *decoder, uint64_t shard, uint32_t fl
  * values f32(N(0,1)) * 0.02, stream ids as the oracle's synthetic model.
  * Norm weights are left as they are (1.0 unless set). */
 int32_t qwh_decoder_init_synthetic(qwh_decoder *decoder, uint32_t seed);
-/* The same synthetic values quantized to `format` (q4, q5 or q8) for every
- * matrix, the embedding included. */
+/* The same synthetic values quantized to `format` (q4, q5 or q8), or stored
+ * as f32 / f16 (rounded to nearest even), for every matrix, the embedding
+ * included. */
 int32_t qwh_decoder_init_synthetic_format(qwh_decoder *decoder, uint32_t seed, int32_t format);
 /* decoder.zig:109-121 reset: zeroes every cache and sets positions to 0. */
 int32_t qwh_decoder_reset(qwh_decoder *decoder);

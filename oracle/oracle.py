@@ -15,6 +15,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "build", "libqwref.so")
 
+F32, F16 = 0, 1
 Q4, Q5, Q8 = 16, 17, 18
 GROUP = 64
 # Cache formats (model_config.zig:44-68 CacheFormat).
@@ -85,6 +86,7 @@ _SIGNATURES = {
     "qwref_linear_quantized": (_I32, [_P, _P, _I32, _P, _U64, _P, _U64, _U32, _U32, _U32]),
     "qwref_linear_f32": (_I32, [_P, _P, _P, _U32, _U32, _U32]),
     "qwref_linear_f16": (_I32, [_P, _P, _P, _U32, _U32, _U32]),
+    "qwref_embedding_row": (_I32, [_I32, _P, _P, _U32, _U32, _U32, _P]),
     "qwref_add_in_place": (None, [_P, _P, _U32]),
     "qwref_silu_mul": (None, [_P, _P, _P, _U32]),
     "qwref_silu": (_F, [_F]),
@@ -245,6 +247,18 @@ def linear_f16(weights: np.ndarray, x: np.ndarray, tokens: int = 1) -> np.ndarra
     if status != 0:
         raise ValueError(f"linear_f16 status {status}")
     return out.reshape(tokens, rows)
+
+
+def embedding_row(fmt: int, scales, data, rows: int, cols: int, row: int) -> np.ndarray:
+    """decoder.zig:346-376 embeddingRow: row `row` of a matrix in `fmt` (f32
+    values or f16 bits as `data` for the element formats, scales None)."""
+    out = np.zeros(cols, np.float32)
+    data = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
+    s_ptr = None if scales is None else _ptr(np.ascontiguousarray(scales, np.uint8))
+    status = lib().qwref_embedding_row(fmt, s_ptr, _ptr(data), rows, cols, row, _ptr(out))
+    if status != 0:
+        raise ValueError(f"embedding_row status {status}")
+    return out
 
 
 def silu(x: float) -> float:

@@ -904,7 +904,8 @@ void qwref_add_sinusoidal_position(float *row, uint32_t step, uint32_t channels)
 /* ------------------------------------------------------------------------ */
 
 typedef struct {
-    int32_t format; /* QWREF_Q4, QWREF_Q5 or QWREF_Q8 */
+    int32_t format; /* QWREF_Q4, QWREF_Q5, QWREF_Q8, or QWREF_F32 / QWREF_F16
+                       (kernels.zig:161-166: the elements in `data`, no scales) */
     uint8_t *scales;
     uint8_t *data;
     uint64_t scales_len;
@@ -958,6 +959,27 @@ static int make_qmat(qmat *m, int32_t format, uint32_t rows, uint32_t cols, uint
     m->format = format;
     m->rows = rows;
     m->cols = cols;
+    if (format == QWREF_F32 || format == QWREF_F16) {
+        /* The generator's values as they are, or rounded to f16
+         * (half_float.zig:14-17). */
+        const uint64_t count = (uint64_t)rows * cols;
+        m->scales = NULL;
+        m->scales_len = 0;
+        m->data_len = count * (format == QWREF_F32 ? 4u : 2u);
+        m->data = (uint8_t *)malloc(m->data_len);
+        if (!m->data) return -1;
+        if (format == QWREF_F32) {
+            qwref_fill_normal((float *)m->data, count, seed, stream, 0.02f);
+            return 0;
+        }
+        float *values = (float *)malloc(sizeof(float) * count);
+        if (!values) return -1;
+        qwref_fill_normal(values, count, seed, stream, 0.02f);
+        uint16_t *bits = (uint16_t *)m->data;
+        for (uint64_t i = 0; i < count; ++i) bits[i] = qwref_to_f16(values[i]);
+        free(values);
+        return 0;
+    }
     m->scales_len = (uint64_t)rows * (cols / QWREF_GROUP) * 2u;
     m->data_len = (uint64_t)rows * (cols / QWREF_GROUP) * (uint64_t)qwref_data_bytes_per_group(format);
     m->scales = (uint8_t *)malloc(m->scales_len);
@@ -996,7 +1018,8 @@ qwref_decoder *qwref_decoder_create_synthetic(const qwref_decoder_config *config
 qwref_decoder *qwref_decoder_create_synthetic_as(const qwref_decoder_config *config, uint32_t seed,
                                                  uint32_t batch, int32_t weight_format,
                                                  int32_t cache_format) {
-    if (qwref_data_bytes_per_group(weight_format) == 0 || weight_format == QWREF_F32) return NULL;
+    if (qwref_data_bytes_per_group(weight_format) == 0 && weight_format != QWREF_F32 && weight_format != QWREF_F16)
+        return NULL;
     if (cache_format != QWREF_CACHE_F32 && cache_format != QWREF_CACHE_Q8) return NULL;
     qwref_decoder *d = (qwref_decoder *)calloc(1, sizeof *d);
     d->c = *config;
@@ -1105,7 +1128,10 @@ int32_t qwref_decoder_set_vector(qwref_decoder *d, uint32_t kind, uint32_t layer
     return QWREF_OK;
 }
 
+/* kernels.zig:182-206 Matrix.apply: the arm of the matrix's storage. */
 static int32_t apply(const qmat *m, float *out, const float *x) {
+    if (m->format == QWREF_F32) return qwref_linear_f32(out, x, (const float *)m->data, m->rows, m->cols, 1);
+    if (m->format == QWREF_F16) return qwref_linear_f16(out, x, (const uint16_t *)m->data, m->rows, m->cols, 1);
     return qwref_linear_quantized(out, x, m->format, m->scales, m->scales_len, m->data, m->data_len,
                                   m->rows, m->cols, 1);
 }
@@ -1151,13 +1177,31 @@ int32_t qwref_decoder_prefill_random(qwref_decoder *d, uint32_t seq, uint32_t co
 
 /* decoder.zig:346-376 `embeddingRow` (quantized branch): the row
  * dequantized in the matrix's own format. */
-static int32_t embedding_row(const qmat *m, uint32_t row, float *out) {
-    if (row >= m->rows) return QWREF_SHAPE_MISMATCH;
-    uint32_t gpr = m->cols / QWREF_GROUP;
-    size_t data_row = (size_t)gpr * (size_t)qwref_data_bytes_per_group(m->format);
-    qwref_dequantize_row(m->format, m->scales + (size_t)row * gpr * 2, m->data + (size_t)row * data_row, out,
-                         m->cols);
+/* decoder.zig:346-376 `embeddingRow`: f32 rows copied, f16 rows widened
+ * (half_float.fromF16), quantized rows dequantized (quant.dequantizeRow).
+ * A row past the end is refused. */
+int32_t qwref_embedding_row(int32_t format, const uint8_t *scales, const uint8_t *data, uint32_t rows,
+                            uint32_t cols, uint32_t row, float *out) {
+    if (row >= rows) return QWREF_SHAPE_MISMATCH;
+    if (format == QWREF_F32) {
+        memcpy(out, data + (size_t)row * cols * 4u, sizeof(float) * cols);
+        return QWREF_OK;
+    }
+    if (format == QWREF_F16) {
+        const uint16_t *bits = (const uint16_t *)data + (size_t)row * cols;
+        for (uint32_t i = 0; i < cols; ++i) out[i] = qwref_from_f16(bits[i]);
+        return QWREF_OK;
+    }
+    if (qwref_data_bytes_per_group(format) == 0) return QWREF_UNSUPPORTED;
+    if (cols % QWREF_GROUP != 0) return QWREF_SHAPE_MISMATCH;
+    uint32_t gpr = cols / QWREF_GROUP;
+    size_t data_row = (size_t)gpr * (size_t)qwref_data_bytes_per_group(format);
+    qwref_dequantize_row(format, scales + (size_t)row * gpr * 2, data + (size_t)row * data_row, out, cols);
     return QWREF_OK;
+}
+
+static int32_t embedding_row(const qmat *m, uint32_t row, float *out) {
+    return qwref_embedding_row(m->format, m->scales, m->data, m->rows, m->cols, row, out);
 }
 
 /* decoder.zig:133-287 `forwardToken`; with an audio row (:133-150) the row

@@ -20,6 +20,10 @@
  *                    quant.zig:527-554 exact values, plane offsets :423-448.
  *   dequant / dot    kernels.zig:932-971 (ones row -> 56.0), f64 brute force.
  *   linear           kernels.zig:840-930, f64 brute force on small shapes.
+ *   linear f16 / f32 kernels.zig:932-948 (ones -> 64), numpy's f16 widening
+ *                    bit for bit, f64 brute force over every finite f16 class.
+ *   embedding row    decoder.zig:378-420 known answers (f32 exact, f16 within
+ *                    1e-3, q4 within 0.2), numpy's widening bit for bit.
  *   attention (q8)   kernels.zig:769-836 (q8 vs f32 within 0.05), closed forms
  *                    (one-hot query on identical keys = mean of V), f64 brute force.
  *   glue             math.zig:174-214 known answers, RoPE norm invariance.
@@ -33,7 +37,7 @@
  *                    model_config.zig:431 (3000 frames -> 375 steps), f64
  *                    brute force of the convolution, and the composition
  *                    (chunks, flatten, projection, positions) against float64.
- *   decoder step     composition of the pinned parts (q4 / q5 / q8 weights,
+ *   decoder step     composition of the pinned parts (q4 / q5 / q8 / f16 / f32 weights,
  *                    f32 / q8 cache, non-unit norm weights) checked against an
  *                    independent float64 restatement; no reference-held
  *                    vectors exist for random weights (parity unpinned end to
@@ -52,7 +56,7 @@ extern "C" {
 #endif
 
 /* dtype.zig:17-108 format ids, quant.zig:47-63 group constants. */
-enum { QWREF_F32 = 0, QWREF_Q4 = 16, QWREF_Q5 = 17, QWREF_Q8 = 18 };
+enum { QWREF_F32 = 0, QWREF_F16 = 1, QWREF_Q4 = 16, QWREF_Q5 = 17, QWREF_Q8 = 18 };
 enum { QWREF_GROUP = 64 };
 
 typedef struct {
@@ -106,6 +110,8 @@ int32_t qwref_linear_f32(float *out, const float *x, const float *weights, uint3
                          uint32_t cols, uint32_t tokens);
 int32_t qwref_linear_f16(float *out, const float *x, const uint16_t *weights, uint32_t rows,
                          uint32_t cols, uint32_t tokens);
+int32_t qwref_embedding_row(int32_t format, const uint8_t *scales, const uint8_t *data, uint32_t rows,
+                            uint32_t cols, uint32_t row, float *out);
 void qwref_add_in_place(float *x, const float *y, uint32_t len);
 void qwref_silu_mul(float *out, const float *gate, const float *up, uint32_t len);
 float qwref_silu(float x);
@@ -184,8 +190,9 @@ enum {
 qwref_decoder *qwref_decoder_create_synthetic(const qwref_decoder_config *config, uint32_t seed,
                                               uint32_t batch);
 /* The same synthetic values with every linear (and the embedding) quantized
- * to `weight_format` (q4, q5 or q8), and the key/value cache in
- * `cache_format`. NULL for an unknown format. */
+ * to `weight_format` (q4, q5 or q8) or stored as f32 / f16 (rounded to
+ * nearest even), and the key/value cache in `cache_format`. NULL for an
+ * unknown format. */
 qwref_decoder *qwref_decoder_create_synthetic_as(const qwref_decoder_config *config, uint32_t seed,
                                                  uint32_t batch, int32_t weight_format,
                                                  int32_t cache_format);

@@ -24,8 +24,9 @@
 //
 // Every matrix keeps the format it was bound in (kernels.zig:182-206 applies
 // whatever storage a Matrix holds): q4 runs the hex-digit GEMV, q5 and q8 the
-// byte-plane GEMV (batch 1 and the per-token path), and at batch > 1 q4 and
-// q8 share the matrix-core GEMV. The key/value cache is q8 or f32
+// byte-plane GEMV (batch 1 and the per-token path), f32 and f16 the dense
+// GEMV (every batch), and at batch > 1 q4, q5 and q8 share the matrix-core
+// GEMV when every matrix has that form. The key/value cache is q8 or f32
 // (model_config.zig:44-68 CacheFormat; decoder.zig:68-106, :220-253).
 #include <algorithm>
 #include <cfloat>
@@ -78,11 +79,22 @@ __device__ __forceinline__ float block_sum256(float v, float *lds) {
     return total;
 }
 
-// decoder.zig:346-376 embeddingRow of one token (quant.zig:315-345
-// dequantizeGroup in the matrix's format): f32(u - bias) times the group's
-// scale; the workgroup's threads stride over the row.
+// decoder.zig:346-376 embeddingRow of one token: f32 rows copied, f16 rows
+// widened, quantized rows dequantized (quant.zig:315-345 dequantizeGroup in
+// the matrix's format: f32(u - bias) times the group's scale); the
+// workgroup's threads stride over the row.
 __device__ __forceinline__ void embed_row(uint32_t token, int32_t format, const uint16_t *scales, const uint8_t *data,
                                           uint32_t cols, float *out) {
+    if (format == QWH_FORMAT_F32) {  // decoder.zig:349-353: the row as it is
+        const float *row = reinterpret_cast<const float *>(data) + (size_t)token * cols;
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = row[i];
+        return;
+    }
+    if (format == QWH_FORMAT_F16) {  // :354-360: each value widened (fromF16)
+        const uint16_t *row = reinterpret_cast<const uint16_t *>(data) + (size_t)token * cols;
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = dev::f16_bits_to_f32(row[i]);
+        return;
+    }
     const uint32_t gpr = cols / 64;
     const uint16_t *row_scales = scales + (size_t)token * gpr;
     if (format == QWH_FORMAT_Q4) {
@@ -480,6 +492,10 @@ int32_t alloc_matrix(qwh_decoder *d, Matrix &m, uint32_t rows, uint32_t cols, in
     m.rows = rows;
     m.cols = cols;
     m.owned = false;  // freed with the decoder's allocations
+    if (is_dense_format(format)) {
+        m.scales = nullptr;
+        return dalloc(d, (size_t)rows * cols * dense_element_bytes(format), reinterpret_cast<void **>(&m.data));
+    }
     const size_t groups = (size_t)rows * (cols / 64);
     QWH_TRY(dalloc(d, groups * 2, reinterpret_cast<void **>(&m.scales)));
     QWH_TRY(dalloc(d, groups * (size_t)data_bytes_per_group(format), reinterpret_cast<void **>(&m.data)));
@@ -539,6 +555,10 @@ int32_t plan_step(qwh_decoder *d) {
     for (const Matrix *m : all) {
         if (m->format == QWH_FORMAT_Q4) {
             q4_fused = q4_fused && gemv_q4_fused_supported(m->rows, m->cols);
+        } else if (is_dense_format(m->format)) {
+            if (!gemv_dense_supported(m->format, m->cols))
+                return fail(d->ctx, QWH_E_UNSUPPORTED, "no GEMV for a %ux%u matrix of format %d", m->rows, m->cols,
+                            m->format);
         } else if (!gemv_b8_supported(m->format, m->rows, m->cols)) {
             return fail(d->ctx, QWH_E_UNSUPPORTED, "no GEMV for a %ux%u matrix of format %d", m->rows, m->cols,
                         m->format);
@@ -604,6 +624,7 @@ int32_t enqueue_step(qwh_decoder *d, bool want_logits) {
             bn.eps = c.eps;
             return launch_gemv_batch(s, d->batch_digits, w, B, out, residual, pairs, d->parts, bn);
         }
+        if (is_dense_format(w.format)) return launch_gemv_dense(s, ctx->cus, in, w, B, out, residual);
         if (w.format != QWH_FORMAT_Q4) return launch_gemv_b8(s, ctx->cus, in, w, B, out, residual);
         if (d->fused) return launch_gemv_q4_src(s, ctx->cus, in, w, B, out, residual);
         if (mode == GemvInput::RmsNorm) {
@@ -817,8 +838,13 @@ void build_rope_tables(std::vector<float> &cos_t, std::vector<float> &sin_t, uin
 // Copies src's rows to rows row_offset + i * stride of dst (stride 1: a
 // contiguous block; stride 2: every other row, for the gate / up pairs).
 int32_t copy_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, const Matrix &src, uint32_t stride = 1) {
-    const size_t gpr = dst.cols / 64;
     hipStream_t s = d->ctx->stream;
+    if (is_dense_format(dst.format)) {
+        const size_t rb = (size_t)dst.cols * dense_element_bytes(dst.format);  // bytes per row
+        return check_hip(d->ctx, hipMemcpy2DAsync(dst.data + (size_t)row_offset * rb, rb * stride, src.data, rb, rb,
+                                                  src.rows, hipMemcpyDeviceToDevice, s), "copy rows");
+    }
+    const size_t gpr = dst.cols / 64;
     const size_t sb = gpr * 2, db = gpr * (size_t)data_bytes_per_group(dst.format);  // scale and code bytes per row
     QWH_TRY(check_hip(d->ctx, hipMemcpy2DAsync(dst.scales + (size_t)row_offset * sb, sb * stride, src.scales, sb, sb,
                                                src.rows, hipMemcpyDeviceToDevice, s), "copy scales"));
@@ -840,8 +866,17 @@ int32_t synth_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, uint32_t ro
     hipStream_t s = d->ctx->stream;
     for (uint32_t r = 0; r < rows; r += slab) {
         const uint32_t n = rows - r < slab ? rows - r : slab;
-        QWH_TRY(check_hip(d->ctx, launch_synth_normal(s, seed, stream, (uint64_t)r * cols, (uint64_t)n * cols, scale, temp),
+        const uint64_t count = (uint64_t)n * cols, at = (uint64_t)(row_offset + r) * cols;
+        // f32 rows are the values themselves; f16 rows their RNE bits.
+        float *values = dst.format == QWH_FORMAT_F32 ? reinterpret_cast<float *>(dst.data) + at : temp;
+        QWH_TRY(check_hip(d->ctx, launch_synth_normal(s, seed, stream, (uint64_t)r * cols, count, scale, values),
                           "synthetic values"));
+        if (dst.format == QWH_FORMAT_F32) continue;
+        if (dst.format == QWH_FORMAT_F16) {
+            QWH_TRY(check_hip(d->ctx, launch_f32_to_f16(s, temp, count, reinterpret_cast<uint16_t *>(dst.data) + at),
+                              "f16 values"));
+            continue;
+        }
         QWH_TRY(check_hip(d->ctx, launch_quantize_rows(s, dst.format, temp, (uint64_t)n * gpr,
                                                       dst.scales + (size_t)(row_offset + r) * gpr * 2,
                                                       dst.data + (size_t)(row_offset + r) * gpr * bpg),
@@ -852,8 +887,10 @@ int32_t synth_rows(qwh_decoder *d, Matrix &dst, uint32_t row_offset, uint32_t ro
 
 int32_t check_matrix(qwh_decoder *d, const Matrix *m, uint32_t rows, uint32_t cols) {
     if (!m) return fail(d->ctx, QWH_E_NOT_FOUND, "unknown matrix handle");
-    if (m->format != QWH_FORMAT_Q4 && m->format != QWH_FORMAT_Q5 && m->format != QWH_FORMAT_Q8)
-        return fail(d->ctx, QWH_E_UNSUPPORTED, "decoder matrices are q4, q5 or q8 (formats 16-18), got %d", m->format);
+    if (m->format != QWH_FORMAT_Q4 && m->format != QWH_FORMAT_Q5 && m->format != QWH_FORMAT_Q8 &&
+        !is_dense_format(m->format))
+        return fail(d->ctx, QWH_E_UNSUPPORTED, "decoder matrices are f32, f16, q4, q5 or q8 (formats 0, 1, 16-18), got %d",
+                    m->format);
     if (m->rows != rows || m->cols != cols)
         return fail(d->ctx, QWH_E_SHAPE_MISMATCH, "matrix is %ux%u, expected %ux%u", m->rows, m->cols, rows, cols);
     return QWH_OK;
@@ -1176,8 +1213,8 @@ int32_t qwh_decoder_init_synthetic(qwh_decoder *d, uint32_t seed) {
 
 int32_t qwh_decoder_init_synthetic_format(qwh_decoder *d, uint32_t seed, int32_t format) {
     if (!d) return QWH_E_INVALID_ARGUMENT;
-    if (format != QWH_FORMAT_Q4 && format != QWH_FORMAT_Q5 && format != QWH_FORMAT_Q8)
-        return fail(d->ctx, QWH_E_UNSUPPORTED, "synthetic decoder format %d is not q4, q5 or q8", format);
+    if (format != QWH_FORMAT_Q4 && format != QWH_FORMAT_Q5 && format != QWH_FORMAT_Q8 && !is_dense_format(format))
+        return fail(d->ctx, QWH_E_UNSUPPORTED, "synthetic decoder format %d is not f32, f16, q4, q5 or q8", format);
     const qwh_decoder_config &c = d->c;
     QWH_TRY(ensure_format(d, d->embed, format));
     QWH_TRY(ensure_format(d, d->lm_head, format));
@@ -1192,12 +1229,15 @@ int32_t qwh_decoder_init_synthetic_format(qwh_decoder *d, uint32_t seed, int32_t
     stage.rows = c.ffn;
     stage.cols = c.hidden;
     const size_t stage_gpr = (size_t)c.hidden / 64;
-    int32_t st = check_hip(d->ctx, hipMalloc(reinterpret_cast<void **>(&stage.scales), (size_t)c.ffn * stage_gpr * 2),
-                           "synthetic staging");
+    const bool dense = is_dense_format(format);
+    int32_t st = dense ? QWH_OK
+                       : check_hip(d->ctx, hipMalloc(reinterpret_cast<void **>(&stage.scales), (size_t)c.ffn * stage_gpr * 2),
+                                   "synthetic staging");
     if (st == QWH_OK)
         st = check_hip(d->ctx,
                        hipMalloc(reinterpret_cast<void **>(&stage.data),
-                                 (size_t)c.ffn * stage_gpr * (size_t)data_bytes_per_group(format)),
+                                 dense ? (size_t)c.ffn * c.hidden * dense_element_bytes(format)
+                                       : (size_t)c.ffn * stage_gpr * (size_t)data_bytes_per_group(format)),
                        "synthetic staging");
     if (st == QWH_OK) st = synth_rows(d, d->embed, 0, c.vocab, seed, kStreamEmbed, 0.02f, temp, temp_values);
     if (st == QWH_OK) st = synth_rows(d, d->lm_head, 0, c.vocab, seed, kStreamLmHead, 0.02f, temp, temp_values);
@@ -1416,6 +1456,7 @@ hipError_t single_row_norm_gemv(qwh_decoder *d, const float *x, const float *nor
     in.x = x;
     in.norm = norm;
     in.eps = d->c.eps;
+    if (is_dense_format(w.format)) return launch_gemv_dense(s, d->ctx->cus, in, w, 1, out, nullptr);
     if (w.format != QWH_FORMAT_Q4) return launch_gemv_b8(s, d->ctx->cus, in, w, 1, out, nullptr);
     if (gemv_q4_fused_supported(w.rows, w.cols)) return launch_gemv_q4_src(s, d->ctx->cus, in, w, 1, out, nullptr);
     uint32_t *words = static_cast<uint32_t *>(d->digits);

@@ -1,5 +1,5 @@
-"""GPU parity of the decoder step with q5 and q8 weights and with the f32
-key/value cache, against the oracle holding the same model.
+"""GPU parity of the decoder step with q5, q8, f16 and f32 weights and with
+the f32 key/value cache, against the oracle holding the same model.
 
 kernels.zig:182-206 (Matrix.apply runs whatever format a matrix holds; the
 converter writes every matrix in one format, layout.zig:49-53),
@@ -62,6 +62,10 @@ def oracle_greedy(ref, b, token, steps):
     (o.Q4, "f32", 18, TINY, ()),
     (o.Q8, "f32", 2, TINY, ()),
     (o.Q5, "f32", 1, ODD, ()),      # head_dim 64, one query head per kv head
+    (o.F16, "q8", 1, TINY, ()),     # f16 weights (--quantization none): the dense GEMV
+    (o.F16, "q8", 3, TINY, ()),     # a group of three tokens per pass over the weights
+    (o.F16, "q8", 18, TINY, ()),    # four-token groups and a tail of two
+    (o.F32, "f32", 2, ODD, ()),     # f32 weights and cache, head_dim 64
 ])
 def test_formats_teacher_forced_and_greedy(ctx, fmt, cache, batch, config, env, monkeypatch):
     for name in env:

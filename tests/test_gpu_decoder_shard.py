@@ -1,6 +1,7 @@
 """A decoder bound from `.qw` shards (qwh_decoder_bind_shard, container.zig
 TensorKind 30..43) runs the same model as one bound tensor by tensor: the
-synthetic model's exact planes and norm weights written into two shards give
+synthetic model's exact planes (q4) or elements (f16, the converter's
+--quantization none) and norm weights written into two shards give
 bit-identical logits and the same greedy token ids."""
 import numpy as np
 import pytest
@@ -19,10 +20,16 @@ T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(9)
 T_ATTN_NORM, T_Q_NORM, T_K_NORM, T_FFN_NORM, T_FINAL_NORM = 16, 17, 18, 19, 20
 
 
-def planes(ctx, rows, cols, stream):
-    """The synthetic generator's q4 matrix (the streams init_synthetic uses)."""
-    m = ctx.matrix_synthetic(qa.FORMAT_Q4, rows, cols, SEED, stream, 0.02)
+def planes(ctx, rows, cols, stream, fmt):
+    """The synthetic generator's matrix in `fmt` (the streams init_synthetic
+    uses) as a shard payload."""
+    m = ctx.matrix_synthetic(fmt, rows, cols, SEED, stream, 0.02)
     sp, dp = ctx.matrix_planes(m)
+    if fmt == qa.FORMAT_F16:
+        bits = np.empty(rows * cols, np.uint16)
+        ctx._check(ctx.lib.qwh_download(ctx.handle, bits.ctypes.data, dp, bits.nbytes))
+        ctx.matrix_release(m)
+        return bits.tobytes()
     groups = rows * cols // 64
     s = np.empty(groups * 2, np.uint8)
     d = np.empty(groups * 32, np.uint8)
@@ -47,24 +54,24 @@ def norms():
     return out
 
 
-def build_shards(ctx, with_output=True):
+def build_shards(ctx, with_output=True, fmt=qa.FORMAT_Q4):
     c = TINY
     qw, kvw = c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
     nv = norms()
-    glob = [dict(kind=sh.KIND_DECODER_EMBED_TOKENS, layer=0, format=sh.o.Q4, dims=(c["vocab"], c["hidden"]),
-                 payload=planes(ctx, c["vocab"], c["hidden"], 1)),
+    glob = [dict(kind=sh.KIND_DECODER_EMBED_TOKENS, layer=0, format=fmt, dims=(c["vocab"], c["hidden"]),
+                 payload=planes(ctx, c["vocab"], c["hidden"], 1, fmt)),
             dict(kind=sh.KIND_DECODER_FINAL_NORM, layer=0, format=sh.F32, dims=(c["hidden"],),
                  payload=nv[(T_FINAL_NORM, 0)].tobytes())]
     if with_output:
-        glob.append(dict(kind=sh.KIND_DECODER_OUTPUT, layer=0, format=sh.o.Q4, dims=(c["vocab"], c["hidden"]),
-                         payload=planes(ctx, c["vocab"], c["hidden"], 2)))
+        glob.append(dict(kind=sh.KIND_DECODER_OUTPUT, layer=0, format=fmt, dims=(c["vocab"], c["hidden"]),
+                         payload=planes(ctx, c["vocab"], c["hidden"], 2, fmt)))
     per_layer = []
     for layer in range(c["layers"]):
         sb = 16 + 16 * layer
         shapes = {33: (qw, c["hidden"], sb), 34: (kvw, c["hidden"], sb + 1), 35: (kvw, c["hidden"], sb + 2),
                   36: (c["hidden"], qw, sb + 3), 41: (c["ffn"], c["hidden"], sb + 4),
                   42: (c["ffn"], c["hidden"], sb + 5), 43: (c["hidden"], c["ffn"], sb + 6)}
-        tensors = [dict(kind=k, layer=layer + 1, format=sh.o.Q4, dims=(r, cc), payload=planes(ctx, r, cc, st))
+        tensors = [dict(kind=k, layer=layer + 1, format=fmt, dims=(r, cc), payload=planes(ctx, r, cc, st, fmt))
                    for k, (r, cc, st) in shapes.items()]
         tensors += [
             dict(kind=39, layer=layer + 1, format=sh.F32, dims=(c["hidden"],), payload=nv[(T_ATTN_NORM, layer)].tobytes()),
@@ -79,13 +86,13 @@ def build_shards(ctx, with_output=True):
     return [sh.build(glob + per_layer[0]), sh.build(per_layer[1])], nv
 
 
-def reference_decoder(ctx, nv, tied=False):
+def reference_decoder(ctx, nv, tied=False, fmt=qa.FORMAT_Q4):
     d = qa.Decoder(ctx, batch=2, **TINY)
-    d.init_synthetic(SEED)
+    d.init_synthetic(SEED, fmt)
     for (kind, layer), values in nv.items():
         d.set_vector(kind, layer, values)
     if tied:
-        m = ctx.matrix_synthetic(qa.FORMAT_Q4, TINY["vocab"], TINY["hidden"], SEED, 1, 0.02)
+        m = ctx.matrix_synthetic(fmt, TINY["vocab"], TINY["hidden"], SEED, 1, 0.02)
         d.set_matrix(T_LM_HEAD, 0, m)
         ctx.matrix_release(m)
     return d
@@ -103,12 +110,13 @@ def config_bin(tied: bool) -> bytes:
                         **tokens))
 
 
-@pytest.mark.parametrize("tied", [False, True])
-def test_decoder_bound_from_shards(ctx, tied):
-    blobs, nv = build_shards(ctx, with_output=not tied)
+@pytest.mark.parametrize("tied,fmt", [(False, qa.FORMAT_Q4), (True, qa.FORMAT_Q4), (False, qa.FORMAT_F16),
+                                      (True, qa.FORMAT_F16)])
+def test_decoder_bound_from_shards(ctx, tied, fmt):
+    blobs, nv = build_shards(ctx, with_output=not tied, fmt=fmt)
     for blob in blobs:
         assert sh.parse(blob)[0] == sh.OK
-    ref = reference_decoder(ctx, nv, tied)
+    ref = reference_decoder(ctx, nv, tied, fmt)
     # The model as a loader sees it: config.bin, then the shards.
     status, reason, model = qa.config_parse(config_bin(tied))
     assert (status, reason) == (0, 0)

@@ -300,7 +300,7 @@ ODD = dict(hidden=320, layers=2, heads=5, kv_heads=5, head_dim=64, ffn=448, voca
            max_positions=64, eps=1e-6, theta=1e6)
 
 
-@pytest.mark.parametrize("fmt", [o.Q8, o.Q4])
+@pytest.mark.parametrize("fmt", [o.Q8, o.Q4, o.F16])
 def test_prefill_on_a_shape_without_matrix_core_forms(ctx, fmt):
     # Batch 1: the prompt runs through the step one position at a time
     # (decoder.zig:319-331 as written), the same checks hold; batch 2 is

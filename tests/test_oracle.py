@@ -245,6 +245,24 @@ def test_linear_f16_against_numpy_widening_and_f64(rows, cols, tokens):
     assert np.all(np.abs(actual - expected) <= 1e-6 * scale + 1e-30)
 
 
+def test_embedding_row_every_storage_kind():
+    # decoder.zig:378-420: sin(0.03 i) over 3 x 64 values; f32 rows exact,
+    # f16 rows within 1e-3 (and numpy's widening of the same bits exactly),
+    # q4 rows within 0.2; decoder.zig:423-435: a row past the end is refused.
+    cols, rows = 64, 3
+    values = np.sin(np.arange(rows * cols, dtype=np.float32) * np.float32(0.03)).astype(np.float32)
+    m = values.reshape(rows, cols)
+    assert np.array_equal(o.embedding_row(o.F32, None, values, rows, cols, 1), m[1])
+    bits = np.array([o.to_f16(float(v)) for v in values], np.uint16)
+    got = o.embedding_row(o.F16, None, bits, rows, cols, 2)
+    assert np.max(np.abs(got - m[2])) <= 1e-3
+    assert np.array_equal(got, bits.reshape(rows, cols)[2].view(np.float16).astype(np.float32))
+    s, d = o.quantize_rows(o.Q4, m)
+    assert np.max(np.abs(o.embedding_row(o.Q4, s, d, rows, cols, 1) - m[1])) <= 0.2
+    with pytest.raises(ValueError):
+        o.embedding_row(o.F32, None, np.zeros(64, np.float32), 1, cols, 1)
+
+
 def test_linear_shape_mismatch():
     s, d = o.quantize_rows(o.Q4, np.ones((2, 64), np.float32))
     lib = o.lib()
@@ -480,7 +498,12 @@ def _tiny_weights(seed, fmt=o.Q4):
     qw, kvw = c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
 
     def mat(rows, cols, stream):
-        s, d = o.quantize_rows(fmt, o.normal(rows * cols, seed, stream, 0.02).reshape(rows, cols))
+        values = o.normal(rows * cols, seed, stream, 0.02).reshape(rows, cols)
+        if fmt == o.F32:
+            return values.astype(np.float64)
+        if fmt == o.F16:  # numpy's own f16 rounding, not the oracle's
+            return values.astype(np.float16).astype(np.float64)
+        s, d = o.quantize_rows(fmt, values)
         return o.dequantize_rows(fmt, s, d, rows, cols).astype(np.float64)
 
     w = {"embed": mat(c["vocab"], c["hidden"], 1), "lm_head": mat(c["vocab"], c["hidden"], 2), "layers": []}
@@ -581,6 +604,8 @@ def _forward_f64(w, tokens, c, norms=None, cache="q8"):
     (o.Q8, o.CACHE_Q8, True),
     (o.Q5, o.CACHE_F32, True),
     (o.Q4, o.CACHE_F32, False),
+    (o.F16, o.CACHE_Q8, True),
+    (o.F32, o.CACHE_F32, True),
 ])
 def test_decoder_composition_against_f64_restatement(fmt, cache, with_norms):
     seed = 9
