@@ -261,6 +261,17 @@ def embedding_row(fmt: int, scales, data, rows: int, cols: int, row: int) -> np.
     return out
 
 
+def linear_any(fmt: int, scales, data, rows: int, cols: int, x: np.ndarray, tokens: int = 1) -> np.ndarray:
+    """kernels.zig:182-206 Matrix.apply: the arm of the matrix's storage.
+    Quantized (fmt, scales, data) planes, or f32 values / f16 bits as `data`
+    (scales None) for the element formats."""
+    if fmt == F32:
+        return linear_f32(np.asarray(data, np.float32).reshape(rows, cols), x, tokens)
+    if fmt == F16:
+        return linear_f16(np.asarray(data).reshape(-1).view(np.uint16).reshape(rows, cols), x, tokens)
+    return linear_quantized(fmt, scales, data, rows, cols, x, tokens)
+
+
 def silu(x: float) -> float:
     return lib().qwref_silu(x)
 
@@ -503,14 +514,14 @@ def audio_layer(encoder: np.ndarray, layer: dict, steps: int, d_model: int, head
                 window_steps: int, eps: float) -> np.ndarray:
     """One audio tower layer (model.zig:656-693 runAudioTower loop body).
 
-    `layer` holds (fmt, scales, data) triples under q, k, v, o, ffn_in, ffn_out
+    `layer` holds (fmt, scales, data) triples (linear_any) under q, k, v, o, ffn_in, ffn_out
     and f32 vectors under q_bias ... ffn_out_bias, attention_norm_weight / _bias
     and final_norm_weight / _bias. Returns the new residual stream."""
     enc = np.array(encoder, np.float32).reshape(-1)
 
     def apply(name, x, rows, cols):
         fmt, scales, data = layer[name]
-        return linear_quantized(fmt, scales, data, rows, cols, x, steps).reshape(-1)
+        return linear_any(fmt, scales, data, rows, cols, x, steps).reshape(-1)
 
     normed = layer_norm(enc, layer["attention_norm_weight"], layer["attention_norm_bias"], d_model, eps)
     # model.zig:765-786 projectQkv: each projection, then its bias.
@@ -532,12 +543,12 @@ def audio_layer(encoder: np.ndarray, layer: dict, steps: int, d_model: int, head
 def audio_projector(encoder: np.ndarray, proj_in, in_bias, proj_out, out_bias, steps: int, d_model: int,
                     hidden: int) -> np.ndarray:
     """model.zig:707-735 runProjector: linear, bias, GELU, linear, bias.
-    proj_in / proj_out are (fmt, scales, data); proj_in is [d_model x d_model]."""
+    proj_in / proj_out are (fmt, scales, data) (linear_any); proj_in is [d_model x d_model]."""
     fmt, scales, data = proj_in
-    mid = linear_quantized(fmt, scales, data, d_model, d_model, np.asarray(encoder, np.float32), steps)
+    mid = linear_any(fmt, scales, data, d_model, d_model, np.asarray(encoder, np.float32), steps)
     mid = gelu_array(add_bias(mid, in_bias, d_model, steps))
     fmt, scales, data = proj_out
-    out = linear_quantized(fmt, scales, data, hidden, d_model, mid, steps)
+    out = linear_any(fmt, scales, data, hidden, d_model, mid, steps)
     return add_bias(out, out_bias, hidden, steps)
 
 
@@ -597,6 +608,6 @@ def audio_frontend(log_mel: np.ndarray, mel_bins: int, frames: int, n_window: in
             h, w = (h - 1) // 2 + 1, (w - 1) // 2 + 1
         for step in range(min(chunk_steps, post_convolution_steps(valid))):
             flat = np.ascontiguousarray(x[:, :, step].reshape(features))
-            row = linear_quantized(fmt, scales, data, d_model, features, flat, 1)[0]
+            row = linear_any(fmt, scales, data, d_model, features, flat, 1)[0]
             rows.append(add_sinusoidal_position(row, step))
     return np.stack(rows) if rows else np.zeros((0, d_model), np.float32)

@@ -342,7 +342,8 @@ float qwref_dot_f32(const float *left, const float *right, uint32_t len) {
 /* kernels.zig:54-75 `linearF32`. */
 int32_t qwref_linear_f32(float *out, const float *x, const float *weights, uint32_t rows,
                          uint32_t cols, uint32_t tokens) {
-    for (uint32_t row = 0; row < rows; ++row)
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t row = 0; row < (int64_t)rows; ++row)
         for (uint32_t token = 0; token < tokens; ++token)
             out[(size_t)token * rows + row] =
                 qwref_dot_f32(weights + (size_t)row * cols, x + (size_t)token * cols, cols);
@@ -350,18 +351,29 @@ int32_t qwref_linear_f32(float *out, const float *x, const float *weights, uint3
 }
 
 /* kernels.zig:82-112 `linearF16`: each weight row widened into scratch
- * (half_float.fromF16), then dotF32 against every token. */
+ * (half_float.fromF16), then dotF32 against every token. Rows are
+ * independent, so the optional thread split changes no output's
+ * arithmetic. */
 int32_t qwref_linear_f16(float *out, const float *x, const uint16_t *weights, uint32_t rows,
                          uint32_t cols, uint32_t tokens) {
-    float *scratch = (float *)malloc(sizeof(float) * (cols ? cols : 1));
-    if (!scratch) return QWREF_LIMIT_EXCEEDED;
-    for (uint32_t row = 0; row < rows; ++row) {
-        for (uint32_t k = 0; k < cols; ++k) scratch[k] = qwref_from_f16(weights[(size_t)row * cols + k]);
-        for (uint32_t token = 0; token < tokens; ++token)
-            out[(size_t)token * rows + row] = qwref_dot_f32(scratch, x + (size_t)token * cols, cols);
+    int32_t status = QWREF_OK;
+#pragma omp parallel num_threads(g_threads)
+    {
+        float *scratch = (float *)malloc(sizeof(float) * (cols ? cols : 1));
+        if (!scratch) {
+#pragma omp atomic write
+            status = QWREF_LIMIT_EXCEEDED;
+        }
+#pragma omp for schedule(static)
+        for (int64_t row = 0; row < (int64_t)rows; ++row) {
+            if (!scratch) continue;
+            for (uint32_t k = 0; k < cols; ++k) scratch[k] = qwref_from_f16(weights[(size_t)row * cols + k]);
+            for (uint32_t token = 0; token < tokens; ++token)
+                out[(size_t)token * rows + row] = qwref_dot_f32(scratch, x + (size_t)token * cols, cols);
+        }
+        free(scratch);
     }
-    free(scratch);
-    return QWREF_OK;
+    return status;
 }
 
 /* kernels.zig:118-158 `linearQuantized` (reached through Matrix.apply,

@@ -134,14 +134,22 @@ def test_audio_attention_window_inside_a_larger_buffer(ctx):
     assert_close(got, expected, rtol=1e-4, atol_rms=1e-4, what="audio attention window")
 
 
+def layer_matrix(fmt, rows, cols, seed, stream):
+    """(fmt, scales, data) of seeded 0.05 N(0,1) weights: quantized planes, or
+    f16 bits (scales None) for the converter's unquantized form."""
+    if fmt == qa.FORMAT_F16:
+        return fmt, None, normal(rows * cols, seed, stream, 0.05).astype(np.float16).view(np.uint16)
+    _, scales, data = quantized_matrix(fmt, rows, cols, seed, stream, 0.05)
+    return fmt, scales, data
+
+
 def make_layer(ctx, fmt, d_model, ffn_dim, seed):
     host, dev, keep = {}, {}, []
     for i, (name, rows, cols) in enumerate((("q", d_model, d_model), ("k", d_model, d_model), ("v", d_model, d_model),
                                              ("o", d_model, d_model), ("ffn_in", ffn_dim, d_model),
                                              ("ffn_out", d_model, ffn_dim))):
-        _, scales, data = quantized_matrix(fmt, rows, cols, seed, i, 0.05)
-        host[name] = (fmt, scales, data)
-        dev[name] = ctx.matrix_upload(fmt, rows, cols, scales, data)
+        host[name] = layer_matrix(fmt, rows, cols, seed, i)
+        dev[name] = ctx.matrix_upload(fmt, rows, cols, host[name][1], host[name][2])
         host[name + "_bias"] = normal(rows, seed, 10 + i, 0.1)
     for j, name in enumerate(("attention_norm", "final_norm")):
         host[name + "_weight"] = np.float32(1.0) + normal(d_model, seed, 20 + j, 0.1)
@@ -163,6 +171,8 @@ def make_layer(ctx, fmt, d_model, ffn_dim, seed):
     (qa.FORMAT_Q4, 256, 4, 512, 1, 8),  # one step: the per-linear path, separate bias and norm kernels
     (qa.FORMAT_Q4, 896, 14, 3584, 390, 104),  # Qwen3-ASR-0.6B audio layer, 30 s
     (qa.FORMAT_Q5, 896, 14, 3584, 390, 104),  # the same in q5 (896-wide rows: 14 groups)
+    (qa.FORMAT_F16, 256, 4, 512, 50, 13),     # f16 weights: the dense GEMV per linear
+    (qa.FORMAT_F16, 896, 14, 3584, 390, 104),
 ])
 def test_audio_layer(ctx, fmt, d_model, heads, ffn_dim, steps, window):
     eps = 1e-5
@@ -185,16 +195,17 @@ def test_audio_layer_rejects_mismatched_matrices(ctx):
         ctx.audio_layer(weights, eb.ptr, 4, 256, 4, 1024, 4, 1e-5)
 
 
-def test_audio_projector(ctx):
+@pytest.mark.parametrize("fmt", [qa.FORMAT_Q4, qa.FORMAT_F16])
+def test_audio_projector(ctx, fmt):
     # model.zig:707-735 at the 0.6B shapes: d_model 896 -> text hidden 1024, 390 steps.
     steps, d_model, hidden = 390, 896, 1024
-    _, s_in, d_in = quantized_matrix(qa.FORMAT_Q4, d_model, d_model, 50, 0, 0.05)
-    _, s_out, d_out = quantized_matrix(qa.FORMAT_Q4, hidden, d_model, 50, 1, 0.05)
+    _, s_in, d_in = layer_matrix(fmt, d_model, d_model, 50, 0)
+    _, s_out, d_out = layer_matrix(fmt, hidden, d_model, 50, 1)
     b_in, b_out = normal(d_model, 50, 2, 0.1), normal(hidden, 50, 3, 0.1)
     enc = normal(steps * d_model, 51)
-    expected = o.audio_projector(enc, (o.Q4, s_in, d_in), b_in, (o.Q4, s_out, d_out), b_out, steps, d_model, hidden)
-    m_in = ctx.matrix_upload(qa.FORMAT_Q4, d_model, d_model, s_in, d_in)
-    m_out = ctx.matrix_upload(qa.FORMAT_Q4, hidden, d_model, s_out, d_out)
+    expected = o.audio_projector(enc, (fmt, s_in, d_in), b_in, (fmt, s_out, d_out), b_out, steps, d_model, hidden)
+    m_in = ctx.matrix_upload(fmt, d_model, d_model, s_in, d_in)
+    m_out = ctx.matrix_upload(fmt, hidden, d_model, s_out, d_out)
     bi, bo, eb = ctx.to_device(b_in), ctx.to_device(b_out), ctx.to_device(enc)
     ob = ctx.buffer(steps * hidden * 4)
     ctx.audio_projector(m_in, bi.ptr, m_out, bo.ptr, eb.ptr, steps, ob.ptr)

@@ -84,7 +84,11 @@ def frontend_weights(ctx, seed, downsample, mel_bins, d_model, fmt):
         host[name + "_weight"] = f16_fast(normal(downsample * cin * 9, seed, 10 + i, 1.0 / np.sqrt(9 * cin)))
         host[name + "_bias"] = normal(downsample, seed, 20 + i, 0.1)
     features = downsample * bins
-    s, d = o.quantize_rows(fmt, normal(d_model * features, seed, 30, 0.02).reshape(d_model, features))
+    values = normal(d_model * features, seed, 30, 0.02).reshape(d_model, features)
+    if fmt == o.F16:  # the converter's unquantized form: f16 elements, no scales
+        s, d = None, values.astype(np.float16).view(np.uint16)
+    else:
+        s, d = o.quantize_rows(fmt, values)
     host["conv_out"] = (fmt, s, d)
     w = qa.AudioFrontendWeights()
     for name in ("conv1_weight", "conv2_weight", "conv3_weight", "conv1_bias", "conv2_bias", "conv3_bias"):
@@ -99,6 +103,7 @@ def frontend_weights(ctx, seed, downsample, mel_bins, d_model, fmt):
     (128, 250, 50, 480, 896, o.Q4),    # Qwen3-ASR-0.6B: two whole chunks and 50 frames
     (32, 19, 4, 16, 64, o.Q8),         # ragged third chunk of 3 frames, q8 projection
     (64, 8, 4, 64, 128, o.Q5),         # exactly one chunk, q5 projection
+    (128, 250, 50, 480, 896, o.F16),   # the 0.6B shape with an f16 projection (7680-wide rows)
 ])
 def test_frontend_against_oracle(ctx, mel_bins, frames, n_window, downsample, d_model, fmt):
     host, w, keep = frontend_weights(ctx, 81, downsample, mel_bins, d_model, fmt)
