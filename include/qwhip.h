@@ -519,7 +519,10 @@ int32_t qwh_decoder_forward_rows(qwh_decoder *decoder, const uint32_t *tokens, c
  * UnexpectedShape / PromptMismatch). The positions are processed together,
  * in chunks of 256: each layer's products run over all of them, their cache
  * rows are appended, then each attends to the cache rows up to its own.
- * Where a layer matrix has no matrix-core form, a batch-1 decoder runs the
+ * Layer matrices without a matrix-core form run their per-token GEMV once
+ * over a chunk's rows (f32 / f16, q5 / q8, and q4 rows its fused GEMV
+ * takes). Where some matrix has neither (a q4 row of an odd number of
+ * 32-value slices the fused GEMV does not take), a batch-1 decoder runs the
  * prompt through its step one position at a time; a larger batch gets
  * QWH_E_UNSUPPORTED (the step would advance its other sequences). Tokens
  * past the vocabulary give QWH_E_SHAPE_MISMATCH and a prompt past

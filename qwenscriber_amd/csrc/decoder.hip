@@ -454,6 +454,7 @@ struct qwh_decoder {
     // of one sequence, allocated at its first call.
     struct PrefillBuffers {
         float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *rope = nullptr, *parts = nullptr;
+        float *wide = nullptr;  // the rows form's siluMul(gate, up) rows
         void *digits = nullptr, *attn_scratch = nullptr, *arg_scratch = nullptr;
         size_t attn_scratch_bytes = 0;
         uint32_t *staged_dev = nullptr;  // tokens, audio row indices, positions
@@ -1406,16 +1407,37 @@ namespace {
 
 constexpr uint32_t kPrefillChunk = 256;
 
-// Every layer product has a matrix-core form, o / gate|up / down a K split,
-// and the attention and the prefill append take the head shape.
-bool prefill_supported(const qwh_decoder *d) {
-    for (const qwh_decoder::Layer &L : d->layers)
-        for (const Matrix *m : {&L.qkv, &L.o, &L.gu, &L.down})
-            if (!gemv_batch_supported(*m)) return false;
-    const qwh_decoder::Layer &L0 = d->layers[0];
+// How a prompt runs through the layers:
+//   MatrixCores  every layer product has a matrix-core form, o / gate|up /
+//                down a K split: int8 digit planes and split GEMVs whose
+//                partial sums the next prep adds (prefill_chunk);
+//   Rows         every layer matrix has a per-token GEMV that takes the
+//                chunk's rows in one launch (f32 / f16 dense, q5 / q8 byte
+//                planes, q4 in its fused activation forms): prefill_chunk_rows;
+//   Positions    otherwise: the step, one position at a time (batch 1 only).
+// The first two also need the attention and the prefill append for the head
+// shape.
+enum class PrefillForm { MatrixCores, Rows, Positions };
+
+bool rows_gemv_supported(const Matrix &m) {
+    if (is_dense_format(m.format)) return gemv_dense_supported(m.format, m.cols);
+    if (m.format == QWH_FORMAT_Q4) return gemv_q4_fused_supported(m.rows, m.cols);
+    return gemv_b8_supported(m.format, m.rows, m.cols);
+}
+
+PrefillForm prefill_form(const qwh_decoder *d) {
     const uint32_t D = d->c.head_dim;
-    return batch_slices(L0.o) && batch_slices(L0.gu) && batch_slices(L0.down) &&
-           attention_supported(D, d->c.heads / d->c.kv_heads) && (D == 64 || D == 128 || D == 256);
+    if (!attention_supported(D, d->c.heads / d->c.kv_heads) || !(D == 64 || D == 128 || D == 256))
+        return PrefillForm::Positions;
+    bool cores = true, rows = true;
+    for (const qwh_decoder::Layer &L : d->layers)
+        for (const Matrix *m : {&L.qkv, &L.o, &L.gu, &L.down}) {
+            cores = cores && gemv_batch_supported(*m);
+            rows = rows && rows_gemv_supported(*m);
+        }
+    const qwh_decoder::Layer &L0 = d->layers[0];
+    if (cores && batch_slices(L0.o) && batch_slices(L0.gu) && batch_slices(L0.down)) return PrefillForm::MatrixCores;
+    return rows ? PrefillForm::Rows : PrefillForm::Positions;
 }
 
 int32_t prefill_buffers(qwh_decoder *d) {
@@ -1428,6 +1450,7 @@ int32_t prefill_buffers(qwh_decoder *d) {
     QWH_TRY(dalloc(d, sizeof(float) * P * c.hidden, reinterpret_cast<void **>(&pf.hidden)));
     QWH_TRY(dalloc(d, sizeof(float) * P * qkv_n, reinterpret_cast<void **>(&pf.qkv)));
     QWH_TRY(dalloc(d, sizeof(float) * P * d->qw, reinterpret_cast<void **>(&pf.attn)));
+    QWH_TRY(dalloc(d, sizeof(float) * P * c.ffn, reinterpret_cast<void **>(&pf.wide)));
     QWH_TRY(dalloc(d, sizeof(float) * P * c.head_dim, reinterpret_cast<void **>(&pf.rope)));
     QWH_TRY(dalloc(d, batch_digit_bytes((uint32_t)P, widest), &pf.digits));
     const qwh_decoder::Layer &L0 = d->layers[0];
@@ -1468,6 +1491,111 @@ hipError_t single_row_norm_gemv(qwh_decoder *d, const float *x, const float *nor
     return launch_gemv_q4_src(s, d->ctx->cus, pre, w, 1, out, nullptr);
 }
 
+// Layer l's attention over a chunk's rows (decoder.zig:180-253 for each
+// prompt position): the rows are n pseudo-sequences sharing the sequence's
+// cache, row i attending to the cache rows below first + i + 1 (its own
+// appended first). `query` holds the q | k | v rows, in `slices` planes of
+// partial sums when above one; the output goes to pf.attn, and also to
+// `digits` as the o projection's activation digits when that is set.
+int32_t prefill_attention(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, uint32_t l, const float *query,
+                          uint32_t slices, void *digits) {
+    qwh_decoder::PrefillBuffers &pf = d->pf;
+    const qwh_decoder_config &c = d->c;
+    const qwh_decoder::Layer &L = d->layers[l];
+    hipStream_t s = d->ctx->stream;
+    const uint32_t qkv_n = d->qw + 2 * d->kvw;
+    uint8_t *kl = d->keys + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
+    uint8_t *vl = d->values + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
+    AttentionArgs aa{};
+    aa.out = pf.attn;
+    aa.query = query;
+    aa.query_stride = qkv_n;
+    if (slices > 1) {
+        aa.query_slices = slices;
+        aa.query_plane = (uint64_t)n * qkv_n;
+    }
+    aa.q_norm = L.q_norm;
+    aa.k_norm = L.k_norm;
+    aa.rope_now = pf.rope;
+    aa.eps = c.eps;
+    aa.k_scales = kl;
+    aa.k_codes = kl + d->cache_scales;
+    aa.v_scales = vl;
+    aa.v_codes = vl + d->cache_scales;
+    aa.cached_dev = pf.staged_dev + 2 * kPrefillChunk;  // the rows' positions
+    aa.cached_bias = 1;
+    aa.capacity = first + n;
+    aa.heads = c.heads;
+    aa.kv_heads = c.kv_heads;
+    aa.head_dim = c.head_dim;
+    aa.batch = n;
+    aa.scale_stride = 0;
+    aa.code_stride = 0;
+    aa.f32_cache = d->cache_format == QWH_CACHE_F32;
+    aa.digits = digits;
+    aa.prefill = true;
+    const size_t records = attention_scratch_bytes(d->ctx->cus, aa);
+    if (records > pf.attn_scratch_bytes) {
+        // The previous chunk's kernels may still read the old records.
+        QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "prefill scratch"));
+        dfree(d, pf.attn_scratch);
+        pf.attn_scratch = nullptr;
+        pf.attn_scratch_bytes = 0;
+        QWH_TRY(dalloc(d, records, &pf.attn_scratch));
+        pf.attn_scratch_bytes = records;
+    }
+    QWH_TRY(check_hip(d->ctx, launch_prefill_append(s, aa, first, n), "prefill cache append"));
+    return check_hip(d->ctx, launch_decode_attention_q8(s, d->ctx->cus, aa, pf.attn_scratch, pf.attn_scratch_bytes),
+                     "prefill attention");
+}
+
+// W * f(x) over a chunk's n rows with the per-token GEMV of w's format
+// (rows_gemv_supported): f32 / f16 dense, q5 / q8 byte planes, q4 fused.
+hipError_t rows_gemv(qwh_decoder *d, GemvInput::Mode mode, const float *x, const float *norm, const Matrix &w,
+                     uint32_t n, float *out, const float *residual, bool pairs) {
+    hipStream_t s = d->ctx->stream;
+    GemvInput in;
+    in.mode = mode;
+    in.x = x;
+    in.norm = norm;
+    in.eps = d->c.eps;
+    in.pairs = pairs;
+    if (is_dense_format(w.format)) return launch_gemv_dense(s, d->ctx->cus, in, w, n, out, residual);
+    if (w.format != QWH_FORMAT_Q4) return launch_gemv_b8(s, d->ctx->cus, in, w, n, out, residual);
+    return launch_gemv_q4_src(s, d->ctx->cus, in, w, n, out, residual);
+}
+
+// One chunk of a prefill in the Rows form: the prompt rows [c0, c0 + n) at
+// positions first .. first + n - 1 through every layer, each projection one
+// launch over the chunk's rows (RMSNorm formed in the q|k|v and gate|up
+// GEMVs, siluMul in gate|up's epilogue, the residual added by o and down);
+// the final hidden rows end in pf.hidden.
+int32_t prefill_chunk_rows(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, const float *audio_rows) {
+    qwh_decoder::PrefillBuffers &pf = d->pf;
+    const qwh_decoder_config &c = d->c;
+    hipStream_t s = d->ctx->stream;
+    const uint32_t H = c.hidden;
+    const uint32_t *tokens_dev = pf.staged_dev, *index_dev = pf.staged_dev + kPrefillChunk;
+    embed_prompt_kernel<<<n, 256, 0, s>>>(tokens_dev, index_dev, d->embed.format,
+                                          reinterpret_cast<const uint16_t *>(d->embed.scales), d->embed.data, H,
+                                          pf.hidden, first, d->rope_cos, d->rope_sin, c.head_dim / 2, pf.rope,
+                                          audio_rows);
+    QWH_TRY(check_hip(d->ctx, hipGetLastError(), "prefill embedding"));
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const qwh_decoder::Layer &L = d->layers[l];
+        QWH_TRY(check_hip(d->ctx, rows_gemv(d, GemvInput::RmsNorm, pf.hidden, L.attn_norm, L.qkv, n, pf.qkv, nullptr,
+                                            false), "prefill q|k|v"));
+        QWH_TRY(prefill_attention(d, seq, first, n, l, pf.qkv, 1, nullptr));
+        QWH_TRY(check_hip(d->ctx, rows_gemv(d, GemvInput::F32, pf.attn, nullptr, L.o, n, pf.hidden, pf.hidden, false),
+                          "prefill o"));
+        QWH_TRY(check_hip(d->ctx, rows_gemv(d, GemvInput::RmsNorm, pf.hidden, L.ffn_norm, L.gu, n, pf.wide, nullptr,
+                                            true), "prefill gate|up"));
+        QWH_TRY(check_hip(d->ctx, rows_gemv(d, GemvInput::F32, pf.wide, nullptr, L.down, n, pf.hidden, pf.hidden,
+                                            false), "prefill down"));
+    }
+    return QWH_OK;
+}
+
 // One chunk of a prefill: prompt rows [c0, c0 + n) of sequence seq at
 // positions first .. first + n - 1 through every layer; the last chunk's
 // final hidden rows stay in pf.hidden with the last down projection added.
@@ -1475,9 +1603,8 @@ int32_t prefill_chunk(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, 
     qwh_decoder::PrefillBuffers &pf = d->pf;
     const qwh_decoder_config &c = d->c;
     hipStream_t s = d->ctx->stream;
-    const uint32_t H = c.hidden, qkv_n = d->qw + 2 * d->kvw;
+    const uint32_t H = c.hidden;
     const uint32_t *tokens_dev = pf.staged_dev, *index_dev = pf.staged_dev + kPrefillChunk;
-    const uint32_t *pos_dev = pf.staged_dev + 2 * kPrefillChunk;
     embed_prompt_kernel<<<n, 256, 0, s>>>(tokens_dev, index_dev, d->embed.format,
                                           reinterpret_cast<const uint16_t *>(d->embed.scales), d->embed.data, H,
                                           pf.hidden, first, d->rope_cos, d->rope_sin, c.head_dim / 2, pf.rope,
@@ -1505,52 +1632,7 @@ int32_t prefill_chunk(qwh_decoder *d, uint32_t seq, uint32_t first, uint32_t n, 
         else
             QWH_TRY(check_hip(d->ctx, launch_gemv_batch(s, pf.digits, L.qkv, n, pf.qkv, nullptr, false, pf.parts, bn),
                               "prefill q|k|v"));
-        // The rows are n pseudo-sequences sharing the sequence's cache:
-        // row i attends to the cache rows below first + i + 1 (its own
-        // appended first), decoder.zig:180-253 for each prompt position.
-        uint8_t *kl = d->keys + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
-        uint8_t *vl = d->values + (size_t)l * d->layer_stride + (size_t)seq * d->seq_stride;
-        AttentionArgs aa{};
-        aa.out = pf.attn;
-        aa.query = qkv_parts ? pf.parts : pf.qkv;
-        aa.query_stride = qkv_n;
-        if (sq > 1) {
-            aa.query_slices = sq;
-            aa.query_plane = (uint64_t)n * qkv_n;
-        }
-        aa.q_norm = L.q_norm;
-        aa.k_norm = L.k_norm;
-        aa.rope_now = pf.rope;
-        aa.eps = c.eps;
-        aa.k_scales = kl;
-        aa.k_codes = kl + d->cache_scales;
-        aa.v_scales = vl;
-        aa.v_codes = vl + d->cache_scales;
-        aa.cached_dev = pos_dev;
-        aa.cached_bias = 1;
-        aa.capacity = first + n;
-        aa.heads = c.heads;
-        aa.kv_heads = c.kv_heads;
-        aa.head_dim = c.head_dim;
-        aa.batch = n;
-        aa.scale_stride = 0;
-        aa.code_stride = 0;
-        aa.f32_cache = d->cache_format == QWH_CACHE_F32;
-        aa.digits = pf.digits;
-        aa.prefill = true;
-        const size_t records = attention_scratch_bytes(d->ctx->cus, aa);
-        if (records > pf.attn_scratch_bytes) {
-            // The previous chunk's kernels may still read the old records.
-            QWH_TRY(check_hip(d->ctx, hipStreamSynchronize(s), "prefill scratch"));
-            dfree(d, pf.attn_scratch);
-            pf.attn_scratch = nullptr;
-            pf.attn_scratch_bytes = 0;
-            QWH_TRY(dalloc(d, records, &pf.attn_scratch));
-            pf.attn_scratch_bytes = records;
-        }
-        QWH_TRY(check_hip(d->ctx, launch_prefill_append(s, aa, first, n), "prefill cache append"));
-        QWH_TRY(check_hip(d->ctx, launch_decode_attention_q8(s, d->ctx->cus, aa, pf.attn_scratch, pf.attn_scratch_bytes),
-                          "prefill attention"));
+        QWH_TRY(prefill_attention(d, seq, first, n, l, qkv_parts ? pf.parts : pf.qkv, sq, pf.digits));
         // o, gate|up, down as partial sums, each added by the prep that
         // follows (the batched step's sequence).
         uint32_t so = 0, sgu = 0, sd = 0;
@@ -1608,14 +1690,16 @@ int32_t qwh_decoder_prefill(qwh_decoder *d, uint32_t seq, const uint32_t *tokens
         return fail(d->ctx, QWH_E_LIMIT_EXCEEDED, "position %u + %u prompt tokens exceeds %u", pos0, count,
                     c.max_positions);
     if (!d->planned) QWH_TRY(plan_step(d));
-    if (!prefill_supported(d)) {
-        // Shapes without the matrix-core forms (a row whose group count is
-        // not a whole number of chunks): at batch 1 the prompt goes through
-        // the step one position at a time, as decoder.zig:319-331 runs it
-        // (with more sequences the step would advance them as well).
+    const PrefillForm form = prefill_form(d);
+    if (form == PrefillForm::Positions) {
+        // Matrices with neither a matrix-core nor a per-token rows form (a
+        // q4 row of an odd K), or a head shape the prefill append does not
+        // take: at batch 1 the prompt goes through the step one position at
+        // a time, as decoder.zig:319-331 runs it (with more sequences the
+        // step would advance them as well).
         if (d->batch != 1)
             return fail(d->ctx, QWH_E_UNSUPPORTED,
-                        "prefill of a batch > 1 decoder needs matrix-core forms of every layer matrix");
+                        "prefill of a batch > 1 decoder needs a matrix-core or rows form of every layer matrix");
         uint32_t audio_index = 0;
         for (uint32_t i = 0; i < count; ++i) {
             const uint32_t t = tokens[i];
@@ -1652,7 +1736,8 @@ int32_t qwh_decoder_prefill(qwh_decoder *d, uint32_t seq, const uint32_t *tokens
         QWH_TRY(check_hip(d->ctx, hipMemcpyAsync(pf.staged_dev, pf.host, 3 * 4 * (size_t)kPrefillChunk,
                                                  hipMemcpyHostToDevice, s), "prefill tokens"));
         const bool last = c0 + n == count;
-        QWH_TRY(prefill_chunk(d, seq, pos0 + c0, n, audio_rows_dev, last));
+        if (form == PrefillForm::MatrixCores) QWH_TRY(prefill_chunk(d, seq, pos0 + c0, n, audio_rows_dev, last));
+        else QWH_TRY(prefill_chunk_rows(d, seq, pos0 + c0, n, audio_rows_dev));
         if (last) {
             // decoder.zig:332 argmaxLogits of the last position.
             float *logits = d->logits + (size_t)seq * c.vocab;

@@ -4,8 +4,9 @@ position (audio pads taking the projected audio rows in order), then
 argmaxLogits of the last position.
 
 The device runs the prompt's positions together (each layer's products as
-one batched GEMM over the prompt rows, the rows' attention as causal
-pseudo-sequences over the one cache). Two checks per prompt:
+one batched GEMM over the prompt rows -- or, for matrices without that form,
+one launch of their per-token GEMV over the rows -- the rows' attention as
+causal pseudo-sequences over the one cache). Two checks per prompt:
 
   - against the oracle, position by position and teacher-forced on the
     device's cache rows (the oracle's forwardToken for position p reads the
@@ -40,6 +41,14 @@ TINY = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, ffn=512, vo
 # The 0.6B decoder's head layout (16 query heads over 8 KV heads of 128).
 WIDE = dict(hidden=1024, layers=2, heads=16, kv_heads=8, head_dim=128, ffn=3072, vocab=2000,
             max_positions=512, eps=1e-6, theta=1e6)
+# Shapes without the matrix-core prefill (rows of an odd number of groups):
+# 320 = 5 groups of 64 per row (q4 there has no fused GEMV either, so a
+# q4 prompt runs position by position), and 192 = 3 groups (q4 fused: the
+# rows form).
+ODD = dict(hidden=320, layers=2, heads=5, kv_heads=5, head_dim=64, ffn=448, vocab=1000,
+           max_positions=64, eps=1e-6, theta=1e6)
+Q4ROWS = dict(hidden=192, layers=2, heads=3, kv_heads=3, head_dim=64, ffn=192, vocab=1000,
+              max_positions=128, eps=1e-6, theta=1e6)
 PAD = 997
 CACHE = {"q8": o.CACHE_Q8, "f32": o.CACHE_F32}
 
@@ -212,6 +221,13 @@ def device_per_token(ctx, dec, tokens, rows, hidden):
     ("one position", TINY, o.Q4, "q8", 1, 7, ()),
     ("one audio position", TINY, o.Q4, "q8", 1, 0, (0,)),
     ("0.6B head layout", WIDE, o.Q4, "q8", 150, 11, range(4, 124)),
+    # The rows form: each projection one launch of the matrix's per-token
+    # GEMV over the chunk's rows.
+    ("f16 weights", TINY, o.F16, "q8", 40, 2, range(5, 25)),
+    ("f16 weights, two chunks", TINY, o.F16, "q8", 300, 5, range(9, 109)),
+    ("f32 weights and cache", TINY, o.F32, "f32", 20, 3, ()),
+    ("q8, 320-wide rows", ODD, o.Q8, "q8", 30, 2, range(3, 13)),
+    ("q4, 192-wide rows", Q4ROWS, o.Q4, "q8", 40, 1, range(2, 12)),
 ])
 def test_prefill_matches_per_token_reference(ctx, name, config, fmt, cache, count, start, pads):
     seed = 9
@@ -295,19 +311,14 @@ def test_prefill_then_prefill_again(ctx):
         ref.close()
 
 
-# A shape without the matrix-core forms (320 = 5 groups of 64 per row).
-ODD = dict(hidden=320, layers=2, heads=5, kv_heads=5, head_dim=64, ffn=448, vocab=1000,
-           max_positions=64, eps=1e-6, theta=1e6)
-
-
-@pytest.mark.parametrize("fmt", [o.Q8, o.Q4, o.F16])
-def test_prefill_on_a_shape_without_matrix_core_forms(ctx, fmt):
-    # Batch 1: the prompt runs through the step one position at a time
-    # (decoder.zig:319-331 as written), the same checks hold; batch 2 is
+def test_prefill_position_by_position(ctx):
+    # q4 rows of 320 values have neither a matrix-core nor a fused per-token
+    # GEMV: at batch 1 the prompt runs through the step one position at a
+    # time (decoder.zig:319-331 as written), the same checks hold; batch 2 is
     # refused (the step would advance the other sequence too). At this K the
     # q4 step takes the generic GEMV (a wavefront per row, per gate / up row
     # pair for siluMul).
-    seed = 33
+    seed, fmt = 33, o.Q4
     gpu, ref = make_pair(ctx, ODD, 1, seed, fmt, "q8", [3])
     try:
         tokens = prompt(20, ODD["vocab"], range(4, 10), 5)
