@@ -266,7 +266,11 @@ def bench_decoder(ctx, qa, batch, steps, warmup, fmt=None, cache=None):
     weights = 0
     hs, ffn, qw, kvw, vocab = 2048, 6144, 2048, 1024, 151936
     per_layer = qw * hs + 2 * kvw * hs + hs * qw + 2 * ffn * hs + hs * ffn
-    weights = (28 * per_layer + vocab * hs) * (qa.DATA_BYTES[fmt] + 2) // 64
+    params = 28 * per_layer + vocab * hs
+    if fmt in (qa.FORMAT_F16, qa.FORMAT_F32):
+        weights = params * (2 if fmt == qa.FORMAT_F16 else 4)
+    else:
+        weights = params * (qa.DATA_BYTES[fmt] + 2) // 64
     pos_mid = 4096 + (steps - 1) / 2 + 1  # rows attended, averaged over the timed steps
     row = kvw + kvw // 64 * 2 if cache == qa.CACHE_Q8 else 4 * kvw
     kv = batch * 28 * 2 * pos_mid * row
@@ -277,16 +281,17 @@ def bench_decoder(ctx, qa, batch, steps, warmup, fmt=None, cache=None):
                 context=f"positions 4096..{4096 + steps - 1} (cache of 4096 rows prefilled, then {steps} greedy steps)")
 
 
-def bench_prefill(ctx, qa, audio_steps=390, text_tokens=12, repeats=5):
+def bench_prefill(ctx, qa, audio_steps=390, text_tokens=12, repeats=5, fmt=None):
     """qwh_decoder_prefill of a 30 s transcription prompt (390 audio pads, as
     the encoder emits for 30 s of audio, inside a short text template) on the
-    1.7B decoder at batch 1, against the same prompt fed one position at a
-    time through the step (decoder.zig:319-331 runs it that way)."""
+    1.7B decoder at batch 1 (q4 weights unless `fmt`), against the same
+    prompt fed one position at a time through the step (decoder.zig:319-331
+    runs it that way)."""
     cfg = dict(hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151936,
                max_positions=4352, eps=1e-6, theta=1e6)
     pad = 151676
     dec = qa.Decoder(ctx, batch=1, **cfg)
-    dec.init_synthetic(4)
+    dec.init_synthetic(4, qa.FORMAT_Q4 if fmt is None else fmt)
     count = audio_steps + text_tokens
     tokens = (np.arange(count, dtype=np.uint32) * 7919 + 13) % cfg["vocab"]
     tokens[tokens == pad] = pad + 1
@@ -668,9 +673,10 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true")
     ap.add_argument("--decoder-batches", default="1,16", help="comma-separated decoder batch sizes")
-    ap.add_argument("--decoders", default="q4,q8,q5,f32kv",
+    ap.add_argument("--decoders", default="q4,q8,q5,f16,f32kv",
                     help="decoder variants: q4 (q4 weights, q8 cache), q8 (q8 weights), q5 (q5 weights), "
-                         "f32kv (q4, f32 cache); 'none' for no step lines")
+                         "f16 (f16 weights, with its prompt prefill), f32kv (q4, f32 cache); 'none' for no "
+                         "step lines")
     ap.add_argument("--skip-headline", action="store_true", help="skip the lm_head GEMV and its read ceiling")
     ap.add_argument("--skip-prefill", action="store_true", help="skip the 30 s prompt prefill")
     ap.add_argument("--skip-transcribe", action="store_true", help="skip the 30 s clip end to end")
@@ -759,6 +765,18 @@ def main():
             log(f"decoder 1.7B q5 weights, batch {batch}")
             q5[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=256, warmup=8, fmt=qa.FORMAT_Q5)
         result["decoder_1p7b_q5_q8kv_ctx4096"] = q5
+    # f16 weights (the converter's --quantization none): every product on
+    # the dense GEMV, the prompt in the prefill's rows form.
+    if not args.skip_decoder and "f16" in variants:
+        f16 = {}
+        for batch in [int(b) for b in args.decoder_batches.split(",") if b]:
+            log(f"decoder 1.7B f16 weights, batch {batch}")
+            f16[f"b{batch}"] = bench_decoder(ctx, qa, batch, steps=256, warmup=8, fmt=qa.FORMAT_F16)
+        result["decoder_1p7b_f16_q8kv_ctx4096"] = f16
+        if not args.skip_prefill:
+            log("decoder 1.7B f16 weights, prefill of a 30 s prompt")
+            result["prefill_1p7b_30s_prompt_f16"] = bench_prefill(ctx, qa, repeats=3, fmt=qa.FORMAT_F16)
+            log(f"prefill f16: {result['prefill_1p7b_30s_prompt_f16']}")
     if not args.skip_decoder and "f32kv" in variants:
         log("decoder 1.7B, f32 cache, batch 1")
         result["decoder_1p7b_q4_f32kv_ctx4096"] = {"b1": bench_decoder(ctx, qa, 1, steps=256, warmup=8,

@@ -6,22 +6,26 @@
 // rounding of it).
 //
 // HBM bound: the weights stream once per group of up to four tokens (two for
-// rows of more than 4092 values, one beyond 8188). Each
-// workgroup forms its tokens' activations in LDS once (as they are, or after
-// RMSNorm, math.zig:118-130), and its wavefronts walk rows grid-stride: lane
-// l takes the row's 16-byte slices l, l + 64, ... (8 f16 or 4 f32 values),
-// four slices' loads in flight at a time, multiplies each slice by every
-// token's activations and the row sums are reduced over the wavefront. For
-// f16 rows the activations of a slice's two 16-byte halves sit in two LDS
-// planes so that the lanes' LDS reads are consecutive 16-byte words. Rows
-// that are not whole 16-byte slices, or a plane that is not 16-byte aligned,
-// take the element-wise form. Epilogues as the q4 GEMV: + residual, or
-// siluMul of gate / up row pairs (kernels.zig:233-239).
+// rows of more than 4092 values, one beyond 8188). Each workgroup forms its
+// tokens' activations in LDS once (as they are, or after RMSNorm,
+// math.zig:118-130), and its wavefronts walk outputs grid-stride. A row is
+// read in chunks of four 16-byte slices per lane (8 f16 or 4 f32 values
+// each): the first chunk is requested before the activations are formed,
+// and each next chunk while the current one is multiplied by every token's
+// activations. An output's row sums (gate and up with pairs, each token's)
+// are reduced over the wavefront in one transposed butterfly. For f16 rows
+// the activations of a slice's two 16-byte halves sit in two LDS planes so
+// that the lanes' LDS reads are consecutive 16-byte words. Rows that are not
+// whole 16-byte slices, or a plane that is not 16-byte aligned, take the
+// element-wise form. Epilogues as the q4 GEMV: + residual, or siluMul of
+// gate / up row pairs (kernels.zig:233-239).
 #include "common.h"
 #include "device.h"
 
 namespace qwh {
 namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // native: stays in registers
 
 struct DenseArgs {
     const uint8_t *w;       // rows x cols f16 or f32, row major
@@ -48,7 +52,7 @@ __device__ __forceinline__ float dense_weight(const uint8_t *w, size_t i) {
 // Sum of one 16-byte slice's products with its activations: lo holds the
 // first four (f16: values 0-3 of the slice, f32: all four), hi values 4-7.
 template <bool Half>
-__device__ __forceinline__ float slice_dot(const uint4 v, const float4 lo, const float4 hi) {
+__device__ __forceinline__ float slice_dot(const u32x4 v, const float4 lo, const float4 hi) {
     float s;
     if constexpr (Half) {
         s = dev::f16_bits_to_f32((uint16_t)(v.x & 0xffffu)) * lo.x;
@@ -69,61 +73,100 @@ __device__ __forceinline__ float slice_dot(const uint4 v, const float4 lo, const
     return s;
 }
 
-// Row `row` times each of the TOK tokens' activations in LDS (token t's at
-// xs + t * cols, in the sliced layout when `sliced`), complete in every lane.
-template <bool Half, int TOK>
-__device__ __forceinline__ void row_dot(const DenseArgs &a, const float *xs, uint32_t row, bool sliced, int lane,
-                                        float (&s)[TOK]) {
-    constexpr uint32_t kPer = Half ? 8 : 4;  // values per 16-byte slice
-    const size_t elem = Half ? 2 : 4;
-    const uint8_t *base = a.w + (size_t)row * a.cols * elem;
+// The first N sums of v, each over the wavefront, in one transposed
+// butterfly: each of the first log2 N exchanges halves the values a lane
+// holds (a lane keeps the half its lane bit selects and adds the other lane's
+// copy of it), the rest add the one value left. Lane l ends with the sum of
+// v[l >> (6 - log2 N)], complete in every lane of its group of 64 / N.
+template <int M, int N, int CAP>
+__device__ __forceinline__ void halve(float (&w)[CAP], int lane) {
+    const bool up = (lane & M) != 0;
 #pragma unroll
-    for (int t = 0; t < TOK; ++t) s[t] = 0.0f;
-    if (sliced) {
-        const uint32_t slices = a.cols / kPer;
-        const uint32_t hi_off = Half ? a.cols / 2 : 0;
-        const uint4 *src = reinterpret_cast<const uint4 *>(base);
-        for (uint32_t c0 = lane; c0 < slices; c0 += 4 * 64) {
-            uint4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                // Slices past the row load its last slice again (not used).
-                const uint32_t c = min(c0 + 64u * u, slices - 1);
-                v[u] = src[c];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t c = c0 + 64u * u;
-                if (c < slices) {
-#pragma unroll
-                    for (int t = 0; t < TOK; ++t) {
-                        const float *xt = xs + (size_t)t * a.cols + c * 4;
-                        const float4 lo = *reinterpret_cast<const float4 *>(xt);
-                        const float4 hi = Half ? *reinterpret_cast<const float4 *>(xt + hi_off) : lo;
-                        s[t] += slice_dot<Half>(v[u], lo, hi);
-                    }
-                }
-            }
-        }
-    } else {
-        for (uint32_t k = lane; k < a.cols; k += 64) {
-            const float w = dense_weight<Half>(base, k);
-#pragma unroll
-            for (int t = 0; t < TOK; ++t) s[t] = fmaf(w, xs[(size_t)t * a.cols + k], s[t]);
-        }
+    for (int i = 0; i < N / 2; ++i) {
+        const float keep = up ? w[i + N / 2] : w[i];
+        const float send = up ? w[i] : w[i + N / 2];
+        w[i] = keep + dev::xor_lane<M>(send);
     }
-#pragma unroll
-    for (int t = 0; t < TOK; ++t) s[t] = dev::wave_sum(s[t]);
 }
 
-// s[lane] for lanes below TOK (a register select, no indexed access).
+template <int N, int CAP>
+__device__ __forceinline__ float reduce_scatter(float (&w)[CAP], int lane) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8, "one to eight sums");
+    if constexpr (N >= 8) halve<32, 8>(w, lane);
+    if constexpr (N >= 4) halve<N >= 8 ? 16 : 32, 4>(w, lane);
+    if constexpr (N >= 2) halve<N >= 8 ? 8 : N >= 4 ? 16 : 32, 2>(w, lane);
+    float v = w[0];
+    if constexpr (N <= 1) v += dev::xor_lane<32>(v);
+    if constexpr (N <= 2) v += dev::xor_lane<16>(v);
+    if constexpr (N <= 4) v += dev::xor_lane<8>(v);
+    v += dev::xor_lane<4>(v);
+    v += dev::xor_lane<2>(v);
+    return v + dev::xor_lane<1>(v);
+}
+
+constexpr int log2_tokens(int tok) { return tok == 4 ? 2 : tok == 2 ? 1 : 0; }
+
+// Stores a unit's outputs from its reduced sums: acc[0] the (gate) row's
+// TOK token sums, acc[1] the up row's with pairs. Without pairs lane l holds
+// token l >> (6 - log2 TOK)'s sum; with pairs the gate sums come first, so a
+// gate lane's up sum is 32 lanes away.
 template <int TOK>
-__device__ __forceinline__ float lane_pick(const float (&s)[TOK], int lane) {
-    float y = s[0];
+__device__ __forceinline__ void store_unit(const DenseArgs &a, float (&acc)[2][TOK], uint32_t o, uint32_t first,
+                                           int lane) {
+    constexpr int LT = log2_tokens(TOK);
+    if (a.pairs) {
+        float w[2 * TOK];
 #pragma unroll
-    for (int t = 1; t < TOK; ++t)
-        if (lane == t) y = s[t];
-    return y;
+        for (int t = 0; t < TOK; ++t) {
+            w[t] = acc[0][t];
+            w[TOK + t] = acc[1][t];
+        }
+        const float g = reduce_scatter<2 * TOK>(w, lane);
+        const float u = dev::xor_lane<32>(g);
+        const uint32_t t = (uint32_t)lane >> (5 - LT);
+        if ((lane & ((32 >> LT) - 1)) == 0 && lane < 32 && first + t < a.tokens)
+            a.out[(size_t)(first + t) * (a.rows / 2) + o] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+    } else {
+        float w[TOK];
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) w[t] = acc[0][t];
+        const float y = reduce_scatter<TOK>(w, lane);
+        const uint32_t t = (uint32_t)lane >> (6 - LT);
+        if ((lane & ((64 >> LT) - 1)) == 0 && first + t < a.tokens) {
+            const size_t at = (size_t)(first + t) * a.rows + o;
+            a.out[at] = a.residual ? a.residual[at] + y : y;
+        }
+    }
+}
+
+// A wavefront's work in 16-byte slices: units (one output: a row, or with
+// pairs its gate and up rows) in grid-stride order, each row in chunks of
+// four slices per lane (lane l takes slices l, l + 64, l + 128, l + 192 of
+// the chunk's 256). Chunk j of the sequence is (unit, row r, chunk c).
+struct ChunkPos {
+    uint32_t unit, r, c;
+};
+
+__device__ __forceinline__ void chunk_next(ChunkPos &p, uint32_t rows_per_unit, uint32_t cpr) {
+    if (++p.c == cpr) {
+        p.c = 0;
+        if (++p.r == rows_per_unit) {
+            p.r = 0;
+            ++p.unit;
+        }
+    }
+}
+
+// The chunk's four 16-byte loads (slices past the row load its last slice
+// again: not used).
+template <bool Half>
+__device__ __forceinline__ void load_chunk(const DenseArgs &a, const ChunkPos &p, uint32_t wave, uint32_t nwaves,
+                                           uint32_t rows_per_unit, uint32_t slices, int lane, u32x4 (&v)[4]) {
+    const uint32_t o = wave + p.unit * nwaves;
+    const uint32_t row = rows_per_unit * o + p.r;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.w) + (size_t)row * slices;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(src + min(p.c * 256u + lane + 64u * u, slices - 1));
 }
 
 template <bool Half, bool Norm, int TOK>
@@ -135,11 +178,77 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(const DenseArgs a) {
     const uint32_t first = blockIdx.y * TOK;
     constexpr uint32_t kPer = Half ? 8 : 4;
     const bool sliced = cols % kPer == 0 && ((uintptr_t)a.w & 15u) == 0;
+    const uint32_t wave = blockIdx.x * 4 + (tid >> 6), nwaves = gridDim.x * 4;
+    const uint32_t rows_per_unit = a.pairs ? 2u : 1u;
+    const uint32_t outputs = a.rows / rows_per_unit;
+    const uint32_t units = wave < outputs ? (outputs - wave + nwaves - 1) / nwaves : 0;
+    const uint32_t slices = cols / kPer;
+    const uint32_t cpr = (slices + 255) / 256;  // chunks per row
+    const uint32_t total = sliced ? units * rows_per_unit * cpr : 0;
     // Token groups past the last token repeat it (their sums are not stored).
     uint32_t token[TOK];
 #pragma unroll
     for (int t = 0; t < TOK; ++t) token[t] = min(first + t, a.tokens - 1);
-    float inv[TOK];
+    // f16 slices: value j of slice c at c * 4 + (j & 3), in the second plane
+    // (cols / 2 further on) for j >= 4, so each lane's LDS reads are whole
+    // 16-byte words.
+    const bool split = Half && sliced;
+    auto slot = [&](uint32_t k) { return split ? ((k & 4u) ? cols / 2 : 0u) + (k >> 3) * 4 + (k & 3u) : k; };
+    // The prologue's loads in the order they are needed: the thread's first
+    // kBatch activations of each token (and their RMSNorm weights), then the
+    // first chunk's weights, so that using the activations waits only for
+    // their own loads (loads complete in issue order) while the weights stay
+    // in flight. Columns past the row load its last column (not stored).
+    constexpr int kBatch = 8;
+    constexpr uint32_t kSpan = 256u * kBatch;  // columns per batch of the workgroup
+    // One token's first batch stays in registers until RMSNorm scales it;
+    // with more tokens it goes to LDS as it is (fewer registers held).
+    constexpr bool kKeep = TOK == 1;
+    float v[TOK][kBatch], nw[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+        const uint32_t k = min(tid + 256u * i, cols - 1);
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) v[t][i] = a.x[(size_t)token[t] * cols + k];
+        if constexpr (Norm) nw[i] = a.norm[k];
+    }
+    ChunkPos pos{0, 0, 0};
+    u32x4 cur[4];
+    if (total) load_chunk<Half>(a, pos, wave, nwaves, rows_per_unit, slices, lane, cur);
+    float ss[TOK];
+#pragma unroll
+    for (int t = 0; t < TOK; ++t) {
+        ss[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const uint32_t k = tid + 256u * i;
+            if (k < cols) {
+                if constexpr (Norm) ss[t] = __fadd_rn(ss[t], __fmul_rn(v[t][i], v[t][i]));
+                if constexpr (!Norm || !kKeep) xs[(size_t)t * cols + slot(k)] = v[t][i];
+            }
+        }
+    }
+    // Rows wider than one batch: the rest in batches of kBatch loads in
+    // flight together, stored as they are (RMSNorm scales them below).
+    for (uint32_t base = kSpan; base < cols; base += kSpan) {
+        float r[TOK][kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const uint32_t k = min(base + tid + 256u * i, cols - 1);
+#pragma unroll
+            for (int t = 0; t < TOK; ++t) r[t][i] = a.x[(size_t)token[t] * cols + k];
+        }
+#pragma unroll
+        for (int t = 0; t < TOK; ++t)
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                const uint32_t k = base + tid + 256u * i;
+                if (k < cols) {
+                    if constexpr (Norm) ss[t] = __fadd_rn(ss[t], __fmul_rn(r[t][i], r[t][i]));
+                    xs[(size_t)t * cols + slot(k)] = r[t][i];
+                }
+            }
+    }
     if constexpr (Norm) {
         // math.zig:118-130: x * (1 / sqrt(mean(x^2) + eps)) * w, the sum of
         // squares reduced over the block (threads, then the four waves in
@@ -147,54 +256,118 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(const DenseArgs a) {
         float *partial = xs + (size_t)TOK * cols;
 #pragma unroll
         for (int t = 0; t < TOK; ++t) {
-            const float *x = a.x + (size_t)token[t] * cols;
-            float ss = 0.0f;
-            for (uint32_t k = tid; k < cols; k += 256) ss = __fadd_rn(ss, __fmul_rn(x[k], x[k]));
-            ss = dev::wave_sum(ss);
-            if (lane == 0) partial[t * 4 + (tid >> 6)] = ss;
+            const float w = dev::wave_sum(ss[t]);
+            if (lane == 0) partial[t * 4 + (tid >> 6)] = w;
         }
         __syncthreads();
+        float inv[TOK];
 #pragma unroll
         for (int t = 0; t < TOK; ++t) {
             const float *p = partial + t * 4;
-            const float ss = ((p[0] + p[1]) + p[2]) + p[3];
-            inv[t] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)cols), a.eps)));
+            const float sum = ((p[0] + p[1]) + p[2]) + p[3];
+            inv[t] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), a.eps)));
         }
-    }
-    // f16 slices: value j of slice c at c * 4 + (j & 3), in the second plane
-    // (cols / 2 further on) for j >= 4.
-    const bool split = Half && sliced;
+        // The first batch from registers (or LDS), the rest from LDS with
+        // their weights loaded a batch at a time.
 #pragma unroll
-    for (int t = 0; t < TOK; ++t) {
-        const float *x = a.x + (size_t)token[t] * cols;
-        float *dst = xs + (size_t)t * cols;
-        for (uint32_t k = tid; k < cols; k += 256) {
-            float v = x[k];
-            if constexpr (Norm) v = __fmul_rn(__fmul_rn(v, inv[t]), a.norm[k]);
-            const uint32_t idx = split ? ((k & 4u) ? cols / 2 : 0u) + (k >> 3) * 4 + (k & 3u) : k;
-            dst[idx] = v;
+        for (int t = 0; t < TOK; ++t)
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                const uint32_t k = tid + 256u * i;
+                if (k < cols) {
+                    float &x = xs[(size_t)t * cols + slot(k)];
+                    x = __fmul_rn(__fmul_rn(kKeep ? v[t][i] : x, inv[t]), nw[i]);
+                }
+            }
+        for (uint32_t base = kSpan; base < cols; base += kSpan) {
+            float w[kBatch];
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) w[i] = a.norm[min(base + tid + 256u * i, cols - 1)];
+#pragma unroll
+            for (int t = 0; t < TOK; ++t)
+#pragma unroll
+                for (int i = 0; i < kBatch; ++i) {
+                    const uint32_t k = base + tid + 256u * i;
+                    if (k < cols) {
+                        float &x = xs[(size_t)t * cols + slot(k)];
+                        x = __fmul_rn(__fmul_rn(x, inv[t]), w[i]);
+                    }
+                }
         }
     }
     __syncthreads();
-    const uint32_t wave = blockIdx.x * 4 + (tid >> 6), nwaves = gridDim.x * 4;
-    const uint32_t outputs = a.pairs ? a.rows / 2 : a.rows;
-    const bool store = lane < TOK && first + lane < a.tokens;
-    const uint32_t my_token = first + (uint32_t)lane;
-    for (uint32_t o = wave; o < outputs; o += nwaves) {
-        if (a.pairs) {
-            float g[TOK], u[TOK];
-            row_dot<Half, TOK>(a, xs, 2 * o, sliced, lane, g);
-            row_dot<Half, TOK>(a, xs, 2 * o + 1, sliced, lane, u);
-            const float gv = lane_pick<TOK>(g, lane), uv = lane_pick<TOK>(u, lane);
-            if (store) a.out[(size_t)my_token * outputs + o] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), uv);
-        } else {
-            float y[TOK];
-            row_dot<Half, TOK>(a, xs, o, sliced, lane, y);
-            const float yv = lane_pick<TOK>(y, lane);
-            if (store) {
-                const size_t at = (size_t)my_token * a.rows + o;
-                a.out[at] = a.residual ? a.residual[at] + yv : yv;
+    float acc[2][TOK];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) acc[r][t] = 0.0f;
+    if (sliced) {
+        const uint32_t hi_off = Half ? cols / 2 : 0;
+        ChunkPos next = pos;
+        for (uint32_t j = 0; j < total; ++j) {
+            // The next chunk's loads go out before this one is multiplied
+            // (the last chunk loads itself again).
+            if (j + 1 < total) chunk_next(next, rows_per_unit, cpr);
+            u32x4 nxt[4];
+            load_chunk<Half>(a, next, wave, nwaves, rows_per_unit, slices, lane, nxt);
+            float part[TOK];
+#pragma unroll
+            for (int t = 0; t < TOK; ++t) part[t] = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t c = pos.c * 256u + lane + 64u * u;
+                if (c < slices) {
+#pragma unroll
+                    for (int t = 0; t < TOK; ++t) {
+                        const float *xt = xs + (size_t)t * cols + c * 4;
+                        const float4 lo = *reinterpret_cast<const float4 *>(xt);
+                        const float4 hi = Half ? *reinterpret_cast<const float4 *>(xt + hi_off) : lo;
+                        part[t] += slice_dot<Half>(cur[u], lo, hi);
+                    }
+                }
             }
+            if (pos.r == 0) {
+#pragma unroll
+                for (int t = 0; t < TOK; ++t) acc[0][t] += part[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < TOK; ++t) acc[1][t] += part[t];
+            }
+            if (pos.c + 1 == cpr && pos.r + 1 == rows_per_unit) {
+                store_unit<TOK>(a, acc, wave + pos.unit * nwaves, first, lane);
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int t = 0; t < TOK; ++t) acc[r][t] = 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+            pos = next;
+        }
+    } else {
+        // Rows that are not whole 16-byte slices: element by element.
+        const size_t elem = Half ? 2 : 4;
+        for (uint32_t i = 0; i < units; ++i) {
+            const uint32_t o = wave + i * nwaves;
+            for (uint32_t r = 0; r < rows_per_unit; ++r) {
+                const uint8_t *base = a.w + (size_t)(rows_per_unit * o + r) * cols * elem;
+                float part[TOK];
+#pragma unroll
+                for (int t = 0; t < TOK; ++t) part[t] = 0.0f;
+                for (uint32_t k = lane; k < cols; k += 64) {
+                    const float w = dense_weight<Half>(base, k);
+#pragma unroll
+                    for (int t = 0; t < TOK; ++t) part[t] = fmaf(w, xs[(size_t)t * cols + k], part[t]);
+                }
+                if (r == 0) {
+#pragma unroll
+                    for (int t = 0; t < TOK; ++t) acc[0][t] = part[t];
+                } else {
+#pragma unroll
+                    for (int t = 0; t < TOK; ++t) acc[1][t] = part[t];
+                }
+            }
+            store_unit<TOK>(a, acc, o, first, lane);
         }
     }
 }
@@ -242,10 +415,16 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
     const int tok = tokens >= 2 && w.cols <= dense_max_cols(4) ? 4 : tokens >= 2 && w.cols <= dense_max_cols(2) ? 2 : 1;
     const uint32_t groups = (tokens + tok - 1) / tok;
     if (groups > 65535) return hipErrorInvalidValue;
-    // About eight workgroups per CU in all: with many token groups each
-    // workgroup walks more rows (its activations staged once for them).
+    // Workgroups per CU in all: eight for matrices of 128 MB and more (the
+    // most weight bytes in flight) and for eight or more token groups (a
+    // prompt's rows), four otherwise, where each workgroup's activation
+    // prologue is worth spreading over more rows (measured on the 1.7B
+    // decoder's matrices at batch 1 and 16, its prompt prefill and the 0.6B
+    // lm_head shape).
     const uint32_t outputs = in.pairs ? w.rows / 2 : w.rows;
-    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256) * 8;
+    const uint64_t wbytes = (uint64_t)w.rows * w.cols * dense_element_bytes(w.format);
+    const uint32_t per_cu = wbytes >= (128ull << 20) || groups >= 8 ? 8u : 4u;
+    const uint32_t target = (uint32_t)(cus > 0 ? cus : 256) * per_cu;
     uint32_t blocks = (target + groups - 1) / groups;
     const uint32_t most = (outputs + 3) / 4;
     if (blocks > most) blocks = most;
