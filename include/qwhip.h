@@ -201,7 +201,7 @@ int32_t qwh_shard_release(qwh_ctx *ctx, uint64_t shard);
  * `cols` must equal the matrix's column count. Formats q4 and q8 at any
  * shape; q5 (the WebGPU decoder's format, passes.ts:63-67) for cols <= 6144
  * with an 8-byte aligned data plane below 4 GiB; f32 and f16
- * (linearF32 / linearF16, :54-112) for cols <= 16380; else
+ * (linearF32 / linearF16, :54-112) for cols <= 40956; else
  * QWH_E_UNSUPPORTED. */
 int32_t qwh_linear(qwh_ctx *ctx, uint64_t matrix, const float *x_dev, uint32_t cols,
                    uint32_t tokens, float *out_dev);
@@ -449,7 +449,7 @@ int32_t qwh_decoder_destroy(qwh_decoder *decoder);
  * each matrix is applied in its own format, as Matrix.apply applies whatever
  * storage it holds (kernels.zig:182-206), and an f32 / f16 embedding gives
  * its rows as embeddingRow does (decoder.zig:346-360). f32 / f16 rows of up
- * to 16380 values. The decoder copies the planes into
+ * to 40956 values. The decoder copies the planes into
  * its own blocks: q / k / v into one fused row block and gate / up into one
  * block with their rows interleaved (gate row j, then up row j). A fused
  * block holds one format, so binding a member in another format re-creates

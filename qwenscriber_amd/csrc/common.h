@@ -172,10 +172,10 @@ hipError_t launch_gemv_q8(hipStream_t s, int cus, const float *x, const Matrix &
 
 // f16 / f32 weights (gemv_dense.hip, kernels.zig:54-112 linearF32 /
 // linearF16): F32 and RmsNorm input forms, pairs and residual as the q4
-// GEMV, rows of 1..kDenseMaxCols values (one token's activations in LDS),
-// token counts up to 65535 groups of four (two for rows of more than 4092
-// values, one for rows of more than 8188).
-constexpr uint32_t kDenseMaxCols = 16380;
+// GEMV, rows of 1..kDenseMaxCols values (one token's activations in a
+// workgroup's 160 KiB of LDS), token counts up to 65535 groups of up to
+// four (fewer for wider rows).
+constexpr uint32_t kDenseMaxCols = 40956;
 bool gemv_dense_supported(int format, uint32_t cols);
 hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const Matrix &w, uint32_t tokens,
                              float *out, const float *residual);

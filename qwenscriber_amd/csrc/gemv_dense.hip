@@ -5,8 +5,8 @@
 // kernels.zig:38-51; this sum runs over a wavefront's lanes, within f32
 // rounding of it).
 //
-// HBM bound: the weights stream once per group of up to four tokens (two for
-// rows of more than 4092 values, one beyond 8188). Each workgroup forms its
+// HBM bound: the weights stream once per group of up to four tokens (fewer
+// for rows too wide for four tokens' activations in LDS). Each workgroup forms its
 // tokens' activations in LDS once (as they are, or after RMSNorm,
 // math.zig:118-130), and its wavefronts walk outputs grid-stride. A row is
 // read in chunks of four 16-byte slices per lane (8 f16 or 4 f32 values
@@ -39,9 +39,17 @@ struct DenseArgs {
     uint32_t pairs;
 };
 
-// The widest rows a workgroup of TOK tokens takes: its activations and
-// partial sums fill at most 64 KiB of LDS.
-constexpr uint32_t dense_max_cols(int tok) { return (65536u - 16u * (uint32_t)tok) / (4u * (uint32_t)tok); }
+// The widest rows a workgroup of TOK tokens takes: one token's activations
+// and partial sums may fill the 160 KiB of LDS a gfx950 workgroup can use;
+// a group of several stays within 64 KiB, so that at least two workgroups
+// share a CU (groups of eight tokens, or four at 98 KiB, measured slower on
+// the 1.7B decoder's batch-16 step and prompt prefill than more passes over
+// the weights with more wavefronts in flight).
+constexpr uint32_t dense_lds_limit(int tok) { return tok == 1 ? 160u << 10 : 64u << 10; }
+constexpr uint32_t dense_max_cols(int tok) {
+    return (dense_lds_limit(tok) - 16u * (uint32_t)tok) / (4u * (uint32_t)tok);
+}
+static_assert(dense_max_cols(1) == kDenseMaxCols, "one token's activations fill the LDS");
 
 template <bool Half>
 __device__ __forceinline__ float dense_weight(const uint8_t *w, size_t i) {
@@ -91,15 +99,18 @@ __device__ __forceinline__ void halve(float (&w)[CAP], int lane) {
 
 template <int N, int CAP>
 __device__ __forceinline__ float reduce_scatter(float (&w)[CAP], int lane) {
-    static_assert(N == 1 || N == 2 || N == 4 || N == 8, "one to eight sums");
-    if constexpr (N >= 8) halve<32, 8>(w, lane);
-    if constexpr (N >= 4) halve<N >= 8 ? 16 : 32, 4>(w, lane);
-    if constexpr (N >= 2) halve<N >= 8 ? 8 : N >= 4 ? 16 : 32, 2>(w, lane);
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "one to sixteen sums");
+    // The first log2 N exchanges use masks 32, 16, ... in turn.
+    constexpr int L = N == 16 ? 4 : N == 8 ? 3 : N == 4 ? 2 : N == 2 ? 1 : 0;
+    if constexpr (L >= 4) halve<32, 16>(w, lane);
+    if constexpr (L >= 3) halve<(32 >> (L - 3)), 8>(w, lane);
+    if constexpr (L >= 2) halve<(32 >> (L - 2)), 4>(w, lane);
+    if constexpr (L >= 1) halve<(32 >> (L - 1)), 2>(w, lane);
     float v = w[0];
-    if constexpr (N <= 1) v += dev::xor_lane<32>(v);
-    if constexpr (N <= 2) v += dev::xor_lane<16>(v);
-    if constexpr (N <= 4) v += dev::xor_lane<8>(v);
-    v += dev::xor_lane<4>(v);
+    if constexpr (L < 1) v += dev::xor_lane<32>(v);
+    if constexpr (L < 2) v += dev::xor_lane<16>(v);
+    if constexpr (L < 3) v += dev::xor_lane<8>(v);
+    if constexpr (L < 4) v += dev::xor_lane<4>(v);
     v += dev::xor_lane<2>(v);
     return v + dev::xor_lane<1>(v);
 }
@@ -373,11 +384,17 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(const DenseArgs a) {
 }
 
 template <int TOK>
-void launch_dense(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
-    if (half && norm) gemv_dense_kernel<true, true, TOK><<<grid, 256, lds, s>>>(a);
-    else if (half) gemv_dense_kernel<true, false, TOK><<<grid, 256, lds, s>>>(a);
-    else if (norm) gemv_dense_kernel<false, true, TOK><<<grid, 256, lds, s>>>(a);
-    else gemv_dense_kernel<false, false, TOK><<<grid, 256, lds, s>>>(a);
+hipError_t launch_dense(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
+    void (*kernel)(const DenseArgs) = half ? (norm ? gemv_dense_kernel<true, true, TOK> : gemv_dense_kernel<true, false, TOK>)
+                                           : (norm ? gemv_dense_kernel<false, true, TOK> : gemv_dense_kernel<false, false, TOK>);
+    if (lds > (64u << 10)) {
+        // Beyond 64 KiB a launch's dynamic LDS has to be allowed per kernel.
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, s, a);
+    return hipGetLastError();
 }
 
 // f16 bits of each value, round to nearest even (half_float.zig:12-16).
@@ -410,9 +427,12 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
     a.out = out;
     a.residual = residual;
     a.pairs = in.pairs ? 1u : 0u;
-    // Tokens per workgroup: four, or two for rows too wide for four (one
-    // pass over the weights per group), or one.
-    const int tok = tokens >= 2 && w.cols <= dense_max_cols(4) ? 4 : tokens >= 2 && w.cols <= dense_max_cols(2) ? 2 : 1;
+    // Tokens per workgroup (one pass over the weights per group): four from
+    // three tokens on, two for two, each where its rows fit the LDS, else
+    // the next smaller.
+    int tok = 1;
+    if (tokens >= 3 && w.cols <= dense_max_cols(4)) tok = 4;
+    else if (tokens >= 2 && w.cols <= dense_max_cols(2)) tok = 2;
     const uint32_t groups = (tokens + tok - 1) / tok;
     if (groups > 65535) return hipErrorInvalidValue;
     // Workgroups per CU in all: eight for matrices of 128 MB and more (the
@@ -433,10 +453,9 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
     const size_t lds = (size_t)tok * ((size_t)w.cols + 4) * sizeof(float);
     const bool half = w.format == QWH_FORMAT_F16;
     const bool norm = in.mode == GemvInput::RmsNorm;
-    if (tok == 4) launch_dense<4>(s, grid, lds, half, norm, a);
-    else if (tok == 2) launch_dense<2>(s, grid, lds, half, norm, a);
-    else launch_dense<1>(s, grid, lds, half, norm, a);
-    return hipGetLastError();
+    if (tok == 4) return launch_dense<4>(s, grid, lds, half, norm, a);
+    if (tok == 2) return launch_dense<2>(s, grid, lds, half, norm, a);
+    return launch_dense<1>(s, grid, lds, half, norm, a);
 }
 
 hipError_t launch_f32_to_f16(hipStream_t s, const float *in, uint64_t count, uint16_t *out) {

@@ -42,12 +42,15 @@ def run(ctx, handle, x, cols, tokens, rows):
 
 
 FORMATS = [qa.FORMAT_F16, qa.FORMAT_F32]
-SHAPES = [  # (rows, cols, tokens): one, four, two or one token per workgroup
+SHAPES = [  # (rows, cols, tokens): four, two or one token per workgroup
     (1024, 1024, 1),    # decoder k / v (0.6B)
     (3072, 1024, 1),    # gate / up (0.6B)
-    (1024, 3072, 5),    # down, a four-token group and a one-token tail
-    (40, 6144, 3),      # rows too wide for four tokens: groups of two
-    (64, 16380, 2),     # the widest rows: one token per workgroup
+    (1024, 3072, 5),    # down: a group of four and a group of one
+    (1024, 2048, 19),   # four groups of four and a tail of three
+    (96, 2048, 3),      # a group of four, one past the last
+    (40, 6144, 9),      # rows too wide for four tokens: groups of two
+    (64, 12000, 2),     # rows too wide for two: one token per workgroup
+    (24, 40956, 2),     # the widest rows (160 KiB of LDS)
     (257, 67, 3),       # rows that are not whole 16-byte slices
     (7, 1, 9),          # one column
 ]
@@ -177,7 +180,7 @@ def test_dense_errors(ctx):
     finally:
         buf.free()
     # Rows wider than one token's activations in LDS.
-    wide = 16381
+    wide = 40957
     handle = ctx.matrix_upload(qa.FORMAT_F32, 1, wide, None, np.zeros(wide, np.float32))
     xb = ctx.buffer(wide * 4)
     ob = ctx.buffer(64)
