@@ -81,6 +81,56 @@ def test_dense_matrix_dispatch_ones(ctx):
             ctx.matrix_release(handle)
 
 
+def test_dense_exact_weights_agree(ctx):
+    # kernels.zig:863-876: f16 and f32 layers of exactly representable
+    # weights give the same outputs; every partial sum is exact in f32, so
+    # the device's summation order cannot change a bit.
+    x = np.array([0.5, -1.5, 2.0, 1.0, -0.5, 0.25, 1.0, -2.0], np.float32)
+    w = np.array([[2.0, 0.5, -1.0, 0.0], [1.0, 1.0, 0.5, -2.0]], np.float32)
+    bits = np.array([[o.to_f16(float(v)) for v in row] for row in w], np.uint16)
+    for fmt, data in ((qa.FORMAT_F32, w), (qa.FORMAT_F16, bits)):
+        handle = ctx.matrix_upload(fmt, 2, 4, None, data)
+        try:
+            assert run(ctx, handle, x, 4, 2, 2).tolist() == [[-1.75, -2.0], [-1.875, 4.25]], fmt
+        finally:
+            ctx.matrix_release(handle)
+
+
+@pytest.mark.parametrize("fmt,rows,cols,tokens", [
+    (qa.FORMAT_Q4, 4, 128, 3),      # kernels.zig:878-931's own case
+    (qa.FORMAT_Q4, 512, 2048, 1),   # the q4 GEMV
+    (qa.FORMAT_Q4, 512, 2048, 5),   # the matrix-core batch GEMV
+    (qa.FORMAT_Q5, 300, 1024, 1),   # the byte-plane GEMV
+    (qa.FORMAT_Q5, 256, 2048, 4),
+    (qa.FORMAT_Q8, 300, 1024, 1),
+    (qa.FORMAT_Q8, 256, 2048, 3),
+])
+def test_quantized_matches_dequantized_dense(ctx, fmt, rows, cols, tokens):
+    # kernels.zig:878-931 on the device: a quantized matrix and the f32
+    # matrix of its dequantized values (exact: an integer code times an f16
+    # scale) give the same products, through two independent kernels.
+    if (rows, cols) == (4, 128):
+        idx = np.arange(rows * cols, dtype=np.float32)
+        values = (np.cos(idx * np.float32(0.07)) * np.float32(1.25)).reshape(rows, cols).astype(np.float32)
+        xi = np.arange(tokens * cols, dtype=np.float32)
+        x = (np.sin(xi * np.float32(0.11)) * np.float32(0.75)).astype(np.float32)
+    else:
+        values = o.normal(rows * cols, 38, fmt, 0.05).reshape(rows, cols)
+        x = o.normal(tokens * cols, 39, fmt)
+    scales, data = o.quantize_rows(fmt, values)
+    dense = o.dequantize_rows(fmt, scales, data, rows, cols).astype(np.float32)
+    hq = ctx.matrix_upload(fmt, rows, cols, scales, data)
+    hd = ctx.matrix_upload(qa.FORMAT_F32, rows, cols, None, dense)
+    try:
+        got_q = run(ctx, hq, x, cols, tokens, rows)
+        got_d = run(ctx, hd, x, cols, tokens, rows)
+    finally:
+        ctx.matrix_release(hq)
+        ctx.matrix_release(hd)
+    assert_close(got_q, got_d, what=f"format {fmt} against its dequantized f32 matrix", **TOL)
+    assert_close(got_d, o.linear_f32(dense, x, tokens), what="dense against the oracle", **TOL)
+
+
 @pytest.mark.parametrize("fmt,offset", [(qa.FORMAT_F16, 2), (qa.FORMAT_F16, 6), (qa.FORMAT_F32, 4)])
 def test_dense_wrap_unaligned_rows(ctx, fmt, offset):
     # Elements aligned to their size but not to 16 bytes take the

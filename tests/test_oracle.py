@@ -226,6 +226,17 @@ def test_matrix_dispatch_every_storage_kind():
     assert o.linear_f16(ones_f16, x).tolist() == [[64.0, 64.0]]
 
 
+def test_f16_and_f32_linear_agree_on_exact_weights():
+    # kernels.zig:863-876: two tokens of four columns; weights exact in f16,
+    # so linearF16 equals linearF32, and every sum here is exact in f32.
+    x = np.array([0.5, -1.5, 2.0, 1.0, -0.5, 0.25, 1.0, -2.0], np.float32)
+    w = np.array([[2.0, 0.5, -1.0, 0.0], [1.0, 1.0, 0.5, -2.0]], np.float32)
+    bits = np.array([[o.to_f16(float(v)) for v in row] for row in w], np.uint16)
+    out32 = o.linear_f32(w, x, 2)
+    assert np.array_equal(o.linear_f16(bits, x, 2), out32)
+    assert out32.tolist() == [[-1.75, -2.0], [-1.875, 4.25]]
+
+
 @pytest.mark.parametrize("rows,cols,tokens", [(5, 67, 3), (9, 256, 2), (3, 1, 4)])
 def test_linear_f16_against_numpy_widening_and_f64(rows, cols, tokens):
     # Every finite f16 class (subnormals, the largest normal, both signs):
