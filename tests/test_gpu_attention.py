@@ -92,6 +92,24 @@ def test_attention_edge_shapes(ctx, cached, hd, heads, kvh):
     assert_close(actual, expected, what=f"attention cached {cached} hd {hd} {heads}/{kvh}")
 
 
+@pytest.mark.parametrize("cached,hd,heads,kvh", [(2, 64, 2, 1), (37, 128, 16, 8), (300, 64, 4, 4)])
+def test_attention_reads_only_the_cached_positions(ctx, cached, hd, heads, kvh):
+    # kernels.zig:1119-1138 for the q8 cache: rows past the cached count hold
+    # NaN scales and codes 0xFF; the output must be finite and equal the
+    # attention over the cached rows alone.
+    kvw = kvh * hd
+    extra = 40
+    ks, kc, vs, vc = make_cache(cached, kvw, 17, cached)
+    nan_scales = np.full(extra * kvw // 64, 0x7E00, np.uint16).view(np.uint8)
+    planes = [np.concatenate([ks, nan_scales]), np.concatenate([kc, np.full(extra * kvw, 0xFF, np.uint8)]),
+              np.concatenate([vs, nan_scales]), np.concatenate([vc, np.full(extra * kvw, 0xFF, np.uint8)])]
+    q = o.normal(heads * hd, 17, 99)
+    out = run_attention(ctx, q, planes, cached, heads, kvh, hd)
+    assert np.all(np.isfinite(out))
+    expected = o.decode_attention_q8(q, ks, kc, vs, vc, cached, heads, kvh, hd)
+    assert_close(out, expected, what=f"{cached} cached rows before NaN rows")
+
+
 def test_identical_keys_give_the_mean_of_values(ctx):
     heads, kvh, hd, cached = 16, 8, 128, 333
     kvw = kvh * hd

@@ -63,6 +63,25 @@ def test_f32_attention_edge_shapes(ctx, cached, hd, heads, kvh):
     assert_close(actual, expected, what=f"f32 attention cached {cached} hd {hd} {heads}/{kvh}")
 
 
+def test_f32_attention_reads_only_the_cached_positions(ctx):
+    # kernels.zig:1119-1138: two query heads over one kv head of two
+    # dimensions and two cached rows; head 0 leans to value 0, head 1 to
+    # value 1, and the two mirror each other. The buffers hold four more rows
+    # of NaN past the cached two: reading any of them would show in the
+    # output.
+    q = np.array([1.0, 0.0, 0.0, 1.0], np.float32)
+    keys = np.full(12, np.nan, np.float32)
+    values = np.full(12, np.nan, np.float32)
+    keys[:4] = [1.0, 0.0, 0.0, 1.0]
+    values[:4] = [1.0, 1.0, 3.0, 3.0]
+    out = run_f32(ctx, q, keys, values, 2, 2, 1, 2)
+    assert np.all(np.isfinite(out))
+    assert out[0] < 2.0 and out[2] > 2.0
+    assert abs(out[0] + out[2] - 4.0) <= 1e-5 and abs(out[1] + out[3] - 4.0) <= 1e-5
+    expected = o.decode_attention(q, keys[:4], values[:4], 2, 2, 1, 2)
+    assert_close(out, expected, rtol=1e-5, atol_rms=1e-6, what="two cached rows")
+
+
 def test_f32_identical_keys_give_the_mean_of_values(ctx):
     # Equal scores: softmax weights 1/cached, the output the mean of V.
     heads, kvh, hd, cached = 16, 8, 128, 333
