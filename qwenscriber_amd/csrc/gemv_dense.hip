@@ -383,12 +383,147 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(const DenseArgs a) {
     }
 }
 
+// ---- Sixteen tokens at a time on the matrix cores ----
+//
+// A workgroup computes a 16-row x 16-token tile with v_mfma_f32_16x16x4_f32:
+// lane l supplies A[m = l % 16][k = l / 16] (token m's activation) and
+// B[k = l / 16][n = l % 16] (row n's weight), and holds C[4 (l / 16) + i]
+// [l % 16] in value i. Each K-step covers four lane groups of one 16-byte
+// weight load each (8 f16 or 4 f32 columns): MFMA e of the step multiplies
+// column step + 8 g + e (f16; 4 g + e for f32) for lane group g. The four
+// wavefronts split the K-steps into quarters and their tiles are summed in
+// order through LDS, so the result does not depend on timing. RMSNorm's
+// weights multiply the activations as they are read; the 1 / rms factor of
+// each token, from the sums of squares the wavefronts gather on the way,
+// scales the tile once at the end (a rounding apart from the reference's
+// (x * inv) * w, like the int8 batch GEMV's RMSNorm form).
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kMmaDepth = 8;  // K-steps of loads in flight per wavefront
+
+template <bool Half, bool Norm>
+__global__ __launch_bounds__(256) void gemm_dense_kernel(const DenseArgs a) {
+    constexpr uint32_t kPer = Half ? 8 : 4;   // values per 16-byte weight load
+    constexpr uint32_t kCols = 4 * kPer;      // columns per K-step
+    constexpr int kX = kPer / 4;              // float4 activation loads per lane per step
+    extern __shared__ float4 lds_dyn[];
+    float *lds_norm = reinterpret_cast<float *>(lds_dyn);  // RMSNorm weights, cols values
+    __shared__ float part[4][16][17];
+    __shared__ float ssp[4][16];
+    __shared__ float sums[16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, g = lane >> 4;
+    const uint32_t row0 = blockIdx.x * 16, tok0 = blockIdx.y * 16;
+    const uint32_t row = min(row0 + li, a.rows - 1);    // B operand row (rows past the matrix repeat the last)
+    const uint32_t tok = min(tok0 + li, a.tokens - 1);  // A operand token (likewise)
+    const uint32_t steps = a.cols / kCols;
+    const uint32_t s_begin = wave * steps / 4, n_steps = (wave + 1) * steps / 4 - s_begin;
+    const u32x4 *wrow = reinterpret_cast<const u32x4 *>(a.w) + (size_t)row * (a.cols / kPer);
+    const float4 *xrow = reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.cols);
+    u32x4 wb[kMmaDepth];
+    float4 xa[kMmaDepth][kX];
+    // Step s of this wavefront's quarter into slot `slot` (steps past the
+    // quarter load its last step again: not used).
+    auto issue = [&](uint32_t s, int slot) {
+        const uint32_t col = (s_begin + min(s, n_steps - 1)) * kCols + g * kPer;
+        wb[slot] = __builtin_nontemporal_load(wrow + col / kPer);
+#pragma unroll
+        for (int h = 0; h < kX; ++h) xa[slot][h] = xrow[col / 4 + h];
+    };
+#pragma unroll
+    for (int i = 0; i < kMmaDepth; ++i) issue(i, i);
+    if constexpr (Norm) {
+        // The norm weights into LDS: requested after the first steps'
+        // weights, so waiting for them leaves nothing of those in flight
+        // that was not already due.
+        for (uint32_t k = 4 * tid; k < a.cols; k += 4 * 256 * 8) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = reinterpret_cast<const float4 *>(a.norm)[min(k + 1024u * j, a.cols - 4) / 4];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (k + 1024u * j < a.cols) reinterpret_cast<float4 *>(lds_norm)[(k + 1024u * j) / 4] = v[j];
+        }
+        __syncthreads();
+    }
+    v4f c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ss = 0.0f;
+    for (uint32_t base = 0; base < n_steps; base += kMmaDepth) {
+#pragma unroll
+        for (int i = 0; i < kMmaDepth; ++i) {
+            if (base + i < n_steps) {
+                const uint32_t col = (s_begin + base + i) * kCols + g * kPer;
+                const u32x4 w = wb[i];
+                const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < (int)kPer; ++e) {
+                    const float4 xv4 = xa[i][e / 4];
+                    float xv = (e & 3) == 0 ? xv4.x : (e & 3) == 1 ? xv4.y : (e & 3) == 2 ? xv4.z : xv4.w;
+                    if constexpr (Norm) {
+                        ss = __fadd_rn(ss, __fmul_rn(xv, xv));
+                        xv = __fmul_rn(xv, lds_norm[col + e]);
+                    }
+                    const float wv = Half ? dev::f16_bits_to_f32((uint16_t)(words[e / 2] >> (16 * (e & 1))))
+                                          : __uint_as_float(words[e]);
+                    if (e & 1) c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv, wv, c1, 0, 0, 0);
+                    else c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv, wv, c0, 0, 0, 0);
+                }
+            }
+            issue(base + i + kMmaDepth, i);
+        }
+    }
+    const v4f c = c0 + c1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wave][4 * g + i][li] = c[i];
+    if constexpr (Norm) {
+        // Lanes li, li + 16, li + 32, li + 48 hold token li's squares.
+        ss += dev::xor_lane<16>(ss);
+        ss += dev::xor_lane<32>(ss);
+        if (g == 0) ssp[wave][li] = ss;
+    }
+    __syncthreads();
+    const int m = tid >> 4, n = tid & 15;  // this thread's token and row in the tile
+    float y = ((part[0][m][n] + part[1][m][n]) + part[2][m][n]) + part[3][m][n];
+    if constexpr (Norm) {
+        const float sum = ((ssp[0][m] + ssp[1][m]) + ssp[2][m]) + ssp[3][m];
+        y = __fmul_rn(y, __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)a.cols), a.eps))));
+    }
+    const uint32_t t_out = tok0 + m, r_out = row0 + n;
+    if (a.pairs) {
+        sums[m][n] = y;
+        __syncthreads();
+        if ((n & 1) == 0 && t_out < a.tokens && r_out < a.rows) {
+            const float gt = sums[m][n], up = sums[m][n + 1];
+            a.out[(size_t)t_out * (a.rows / 2) + r_out / 2] = __fmul_rn(__fdiv_rn(gt, __fadd_rn(1.0f, expf(-gt))), up);
+        }
+    } else if (t_out < a.tokens && r_out < a.rows) {
+        const size_t at = (size_t)t_out * a.rows + r_out;
+        a.out[at] = a.residual ? a.residual[at] + y : y;
+    }
+}
+
 template <int TOK>
 hipError_t launch_dense(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
     void (*kernel)(const DenseArgs) = half ? (norm ? gemv_dense_kernel<true, true, TOK> : gemv_dense_kernel<true, false, TOK>)
                                            : (norm ? gemv_dense_kernel<false, true, TOK> : gemv_dense_kernel<false, false, TOK>);
     if (lds > (64u << 10)) {
         // Beyond 64 KiB a launch's dynamic LDS has to be allowed per kernel.
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+// From this many tokens the matrix-core form runs; its RMSNorm weights
+// stay in LDS (the static tiles take about 5 KiB of the 160 KiB).
+constexpr uint32_t kMmaMinTokens = 8;
+constexpr uint32_t kMmaMaxNormCols = 36864;
+
+hipError_t launch_mma(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
+    void (*kernel)(const DenseArgs) = half ? (norm ? gemm_dense_kernel<true, true> : gemm_dense_kernel<true, false>)
+                                           : (norm ? gemm_dense_kernel<false, true> : gemm_dense_kernel<false, false>);
+    if (lds > (48u << 10)) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
@@ -427,6 +562,19 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
     a.out = out;
     a.residual = residual;
     a.pairs = in.pairs ? 1u : 0u;
+    // Eight tokens and more: the matrix cores, the weights streamed once per
+    // sixteen tokens (whole 16-byte loads of at least four K-steps per
+    // wavefront, 16-byte aligned weights, activations and norm weights).
+    const bool half = w.format == QWH_FORMAT_F16;
+    const bool norm = in.mode == GemvInput::RmsNorm;
+    const uint32_t step_cols = half ? 32u : 16u;
+    const bool aligned = (((uintptr_t)w.data | (uintptr_t)in.x | (norm ? (uintptr_t)in.norm : 0u)) & 15u) == 0;
+    if (tokens >= kMmaMinTokens && w.cols % step_cols == 0 && w.cols / step_cols >= 4 && aligned &&
+        (!norm || w.cols <= kMmaMaxNormCols)) {
+        const dim3 grid((w.rows + 15) / 16, (tokens + 15) / 16);
+        if (grid.y > 65535) return hipErrorInvalidValue;
+        return launch_mma(s, grid, norm ? (size_t)w.cols * 4 : 0, half, norm, a);
+    }
     // Tokens per workgroup (one pass over the weights per group): four from
     // three tokens on, two for two, each where its rows fit the LDS, else
     // the next smaller.
@@ -451,8 +599,6 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
     if (blocks == 0) blocks = 1;
     const dim3 grid(blocks, groups);
     const size_t lds = (size_t)tok * ((size_t)w.cols + 4) * sizeof(float);
-    const bool half = w.format == QWH_FORMAT_F16;
-    const bool norm = in.mode == GemvInput::RmsNorm;
     if (tok == 4) return launch_dense<4>(s, grid, lds, half, norm, a);
     if (tok == 2) return launch_dense<2>(s, grid, lds, half, norm, a);
     return launch_dense<1>(s, grid, lds, half, norm, a);

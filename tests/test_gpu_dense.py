@@ -53,6 +53,12 @@ SHAPES = [  # (rows, cols, tokens): four, two or one token per workgroup
     (24, 40956, 2),     # the widest rows (160 KiB of LDS)
     (257, 67, 3),       # rows that are not whole 16-byte slices
     (7, 1, 9),          # one column
+    # Eight tokens and more: the matrix cores, 16 x 16 tiles.
+    (1000, 1024, 8),    # half a token tile
+    (2048, 2048, 16),   # one whole tile of tokens
+    (333, 3072, 33),    # rows and tokens past whole tiles
+    (64, 128, 40),      # the fewest K-steps the form takes (four per wavefront)
+    (96, 6144, 200),    # rows too wide for a token group of four
 ]
 
 
