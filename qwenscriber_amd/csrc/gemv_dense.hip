@@ -440,8 +440,7 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(const DenseArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = reinterpret_cast<const float4 *>(a.norm)[min(k + 1024u * j, a.cols - 4) / 4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (k + 1024u * j < a.cols) reinterpret_cast<float4 *>(lds_norm)[(k + 1024u * j) / 4] = v[j];
+            for (int j = 0; j < 8; ++j) reinterpret_cast<float4 *>(lds_norm)[min(k + 1024u * j, a.cols - 4) / 4] = v[j];
         }
         __syncthreads();
     }
@@ -501,6 +500,228 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(const DenseArgs a) {
     }
 }
 
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+// One K-step of a lane's activations (16 of its token's 64 in the step) as
+// f16 operands, hi + lo = x * s to within 2^-22 of the step's largest
+// magnitude, and the 1 / s that undoes the scale. s = 2^(14 - E) for the
+// largest magnitude's exponent E over the token's 64 values (the lanes l,
+// l ^ 16, l ^ 32, l ^ 48 hold them), so the scaled values stay below 2^15,
+// inside the f16 range, and keep their f32 precision in the pair: hi is x * s
+// rounded to f16, lo the exact f32 remainder rounded to f16. Exponents are
+// clamped to [2^-112, inf], so s and 1 / s are normal powers of two and the
+// scaling is exact. A NaN or inf in the step carries through to the sums: an
+// inf is its own hi (lo 0, where the remainder would be NaN), a NaN makes
+// both NaN.
+__device__ __forceinline__ float split_step(const float (&xv)[16], h8 (&hi)[2], h8 (&lo)[2]) {
+    float m[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        m[q] = fmaxf(fmaxf(fabsf(xv[4 * q]), fabsf(xv[4 * q + 1])), fmaxf(fabsf(xv[4 * q + 2]), fabsf(xv[4 * q + 3])));
+    float mx = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+    mx = fmaxf(mx, dev::xor_lane<16>(mx));
+    mx = fmaxf(mx, dev::xor_lane<32>(mx));
+    const uint32_t e = max(__float_as_uint(mx) & 0x7F800000u, 15u << 23);
+    const bool inf = e == 0x7F800000u;
+    const float s = __uint_as_float((268u << 23) - e);  // 2^(141 - biased exponent)
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+        const f2 v = {__fmul_rn(xv[j], s), __fmul_rn(xv[j + 1], s)};
+        const h2 h = __builtin_convertvector(v, h2);
+        const h2 l = __builtin_convertvector(v - __builtin_convertvector(h, f2), h2);
+        hi[j / 8][j % 8] = h.x;
+        hi[j / 8][j % 8 + 1] = h.y;
+        lo[j / 8][j % 8] = inf ? (_Float16)0.0f : l.x;
+        lo[j / 8][j % 8 + 1] = inf ? (_Float16)0.0f : l.y;
+    }
+    return __uint_as_float(e - (14u << 23));  // 1 / s
+}
+
+// f16 weights on the f16 matrix cores (v_mfma_f32_16x16x32_f16), from eight
+// tokens: the products w * hi and w * lo are exact in f32, so the sums carry
+// f32 precision. A workgroup holds 16 * R rows x 16 tokens; its W wavefronts
+// split K in steps of 64 values and add their tiles through LDS in a fixed
+// order. Per step a lane holds, for each row tile, 16 weights of row l % 16:
+// values 8 (l / 16) .. + 7 of each half of the step, the A operands of two
+// MFMAs (each load covers 64 contiguous bytes of 16 rows). The activations
+// are loaded whole rows at a time (each load covers 256 contiguous bytes of
+// four tokens), passed through a per-wavefront LDS tile, and read back as
+// the same 16 positions of token l % 16 (the B operands), so a lane's
+// accumulators are rows 4 (l / 16) + i of its own token and take that
+// token's 1 / s. Loads go through buffer resources bounded by the tile:
+// rows and tokens past the matrix or batch, and the steps past a
+// wavefront's range that keep the pipeline's shape, read zeros and touch no
+// memory. D steps of loads are in flight per wavefront. With RMSNorm the
+// norm weights sit in LDS, each activation is scaled as it is read, and the
+// token's inverse RMS multiplies the sums at the end.
+template <bool Norm, int R, int W, int D>
+__global__ __launch_bounds__(64 * W) void gemm_f16_kernel(const DenseArgs a) {
+    extern __shared__ float4 lds_dyn[];      // RMSNorm weights, cols values
+    __shared__ float4 xtile[W][16 * 17];     // per wavefront: 16 tokens x 64 values (+ 4 of padding)
+    __shared__ float part[W][16 * R][17];
+    __shared__ float ssp[W][16];
+    constexpr uint32_t kFar = 0x7FFFFF00u;  // an offset past every tile
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, g = lane >> 4;
+    const uint32_t row0 = blockIdx.x * (16u * R), tok0 = blockIdx.y * 16;
+    const uint32_t nrows = min(16u * R, a.rows - row0), ntok = min(16u, a.tokens - tok0);
+    const uint32_t steps = a.cols / 64;
+    const uint32_t s_begin = wave * steps / W, n_steps = (wave + 1) * steps / W - s_begin;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.w) + (size_t)row0 * a.cols * 2, (short)0, (int)(nrows * a.cols * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.x) + (size_t)tok0 * a.cols, (short)0, (int)(ntok * a.cols * 4), 0x00020000);
+    const uint32_t w_lane = (uint32_t)li * a.cols * 2 + 16u * g + 128u * s_begin;
+    const uint32_t x_lane = (uint32_t)g * a.cols * 4 + 16u * li + 256u * s_begin;
+    u32x4 wb[D][R][2];
+    u32x4 xa[D][4];
+    // Step s of this wavefront's range into slot `slot` (past the range: no
+    // memory is read), the same loads every iteration, so each step waits
+    // only for its own.
+    auto issue = [&](uint32_t s, int slot) {
+        const bool valid = s < n_steps;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                wb[slot][r][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                    wres, valid ? w_lane + 16u * r * a.cols * 2 + 128u * s + 64u * h : kFar, 0, 2 /* nt */);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            xa[slot][b] = __builtin_amdgcn_raw_buffer_load_b128(
+                xres, valid ? x_lane + 4u * b * a.cols * 4 + 256u * s : kFar, 0, 0);
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        issue(i, i);
+        __builtin_amdgcn_sched_barrier(0);  // slots in order: step 0's loads first
+    }
+    if constexpr (Norm) {
+        // The RMSNorm weights into LDS, requested after the first steps'
+        // loads: waiting for them coincides with those. Each batch's stores
+        // are unconditional (past the row, the last four values again, to
+        // their own place), so its loads go out together (2048 values per
+        // pass, J loads per thread: more would not stay in registers beside
+        // the slots in flight).
+        constexpr int J = W >= 8 ? 1 : 8 / W;
+        const float4 *norm4 = reinterpret_cast<const float4 *>(a.norm);
+        for (uint32_t k = 4 * tid; k < a.cols; k += 256u * W * J) {
+            float4 v[J];
+#pragma unroll
+            for (int j = 0; j < J; ++j) v[j] = norm4[min(k + 256u * W * j, a.cols - 4) / 4];
+            __builtin_amdgcn_sched_barrier(0);  // all J loads before the first store
+#pragma unroll
+            for (int j = 0; j < J; ++j) lds_dyn[min(k + 256u * W * j, a.cols - 4) / 4] = v[j];
+        }
+        __syncthreads();
+    }
+    float4 *xt = xtile[wave];
+    v4f acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float ss = 0.0f;
+    // Every iteration runs the same straight-line code; a step past the
+    // range (zeros) leaves the sums unchanged.
+    for (uint32_t base = 0; base < n_steps; base += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const bool valid = base + i < n_steps;
+            // Tokens g + 4 b, 4 values at 4 li, into the tile; read back
+            // token li's values at 8 g and 32 + 8 g.
+#pragma unroll
+            for (int b = 0; b < 4; ++b) xt[(g + 4 * b) * 17 + li] = __builtin_bit_cast(float4, xa[i][b]);
+            float xv[16];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const float4 v = xt[li * 17 + 8 * (h >> 1) + 2 * g + (h & 1)];
+                xv[4 * h] = v.x;
+                xv[4 * h + 1] = v.y;
+                xv[4 * h + 2] = v.z;
+                xv[4 * h + 3] = v.w;
+            }
+            if constexpr (Norm) {
+                const uint32_t st = s_begin + min(base + i, n_steps - 1);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const float4 n4 = lds_dyn[st * 16 + 8 * (h >> 1) + 2 * g + (h & 1)];
+                    const float nv[4] = {n4.x, n4.y, n4.z, n4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float sq = __fadd_rn(ss, __fmul_rn(xv[4 * h + j], xv[4 * h + j]));
+                        ss = valid ? sq : ss;
+                        xv[4 * h + j] = __fmul_rn(xv[4 * h + j], nv[j]);
+                    }
+                }
+            }
+            h8 hi[2], lo[2];
+            const float inv = split_step(xv, hi, lo);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const h8 w0 = __builtin_bit_cast(h8, wb[i][r][0]), w1 = __builtin_bit_cast(h8, wb[i][r][1]);
+                v4f t = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, hi[0], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, hi[1], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, lo[0], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, lo[1], t, 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float sum = __fmaf_rn(t[c], inv, acc[r][c]);
+                    acc[r][c] = valid ? sum : acc[r][c];
+                }
+            }
+            issue(base + i + D, i);
+            // The next step's work stays after this step's loads are issued
+            // (moved up, it would wait for the next slot's loads early).
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) part[wave][16 * r + 4 * g + c][li] = acc[r][c];
+    if constexpr (Norm) {
+        // Lanes li, li + 16, li + 32, li + 48 hold token li's squares.
+        ss += dev::xor_lane<16>(ss);
+        ss += dev::xor_lane<32>(ss);
+        if (g == 0) ssp[wave][li] = ss;
+    }
+    __syncthreads();
+    auto total = [&](int n, int m) {
+        float y = part[0][n][m];
+#pragma unroll
+        for (int v = 1; v < W; ++v) y += part[v][n][m];
+        if constexpr (Norm) {
+            float sum = ssp[0][m];
+#pragma unroll
+            for (int v = 1; v < W; ++v) sum += ssp[v][m];
+            y = __fmul_rn(y, __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)a.cols), a.eps))));
+        }
+        return y;
+    };
+    if (a.pairs) {
+        // 8 R gate / up pairs x 16 tokens.
+        for (int idx = tid; idx < 128 * R; idx += 64 * W) {
+            const int m = idx / (8 * R), p = idx % (8 * R);
+            const uint32_t t_out = tok0 + m, r_out = row0 + 2 * p;
+            if (t_out < a.tokens && r_out < a.rows) {
+                const float gt = total(2 * p, m), up = total(2 * p + 1, m);
+                a.out[(size_t)t_out * (a.rows / 2) + r_out / 2] = __fmul_rn(__fdiv_rn(gt, __fadd_rn(1.0f, expf(-gt))), up);
+            }
+        }
+    } else {
+        for (int idx = tid; idx < 256 * R; idx += 64 * W) {
+            const int m = idx / (16 * R), n = idx % (16 * R);
+            const uint32_t t_out = tok0 + m, r_out = row0 + n;
+            if (t_out < a.tokens && r_out < a.rows) {
+                const float y = total(n, m);
+                const size_t at = (size_t)t_out * a.rows + r_out;
+                a.out[at] = a.residual ? a.residual[at] + y : y;
+            }
+        }
+    }
+}
+
 template <int TOK>
 hipError_t launch_dense(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
     void (*kernel)(const DenseArgs) = half ? (norm ? gemv_dense_kernel<true, true, TOK> : gemv_dense_kernel<true, false, TOK>)
@@ -529,6 +750,19 @@ hipError_t launch_mma(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(kernel, grid, dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+template <bool Norm, int R, int W, int D>
+hipError_t launch_f16_mma(hipStream_t s, uint32_t tokens, size_t lds, const DenseArgs &a) {
+    const dim3 grid((a.rows + 16 * R - 1) / (16 * R), (tokens + 15) / 16);
+    void (*kernel)(const DenseArgs) = gemm_f16_kernel<Norm, R, W, D>;
+    if (lds > (48u << 10)) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * W), lds, s, a);
     return hipGetLastError();
 }
 
@@ -573,7 +807,20 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
         (!norm || w.cols <= kMmaMaxNormCols)) {
         const dim3 grid((w.rows + 15) / 16, (tokens + 15) / 16);
         if (grid.y > 65535) return hipErrorInvalidValue;
-        return launch_mma(s, grid, norm ? (size_t)w.cols * 4 : 0, half, norm, a);
+        const size_t lds = norm ? (size_t)w.cols * 4 : 0;
+        if (half && w.cols % 64 == 0 && w.cols / 64 >= 4) {
+            // f16 weights: the split-activation f16 form, with 1, 2 or 4 row
+            // tiles per workgroup by the count of 16 x 16 tiles (more rows
+            // per workgroup share each activation load; fewer keep every CU
+            // busy on a small matrix).
+            const uint64_t tiles = (uint64_t)grid.x * grid.y;
+            if (tiles >= 2048) return norm ? launch_f16_mma<true, 4, 4, 2>(s, tokens, lds, a)
+                                           : launch_f16_mma<false, 4, 4, 2>(s, tokens, lds, a);
+            if (tiles >= 1024) return norm ? launch_f16_mma<true, 2, 4, 2>(s, tokens, lds, a)
+                                           : launch_f16_mma<false, 2, 4, 2>(s, tokens, lds, a);
+            return norm ? launch_f16_mma<true, 1, 4, 2>(s, tokens, lds, a) : launch_f16_mma<false, 1, 4, 2>(s, tokens, lds, a);
+        }
+        return launch_mma(s, grid, lds, half, norm, a);
     }
     // Tokens per workgroup (one pass over the weights per group): four from
     // three tokens on, two for two, each where its rows fit the LDS, else

@@ -59,6 +59,12 @@ SHAPES = [  # (rows, cols, tokens): four, two or one token per workgroup
     (333, 3072, 33),    # rows and tokens past whole tiles
     (64, 128, 40),      # the fewest K-steps the form takes (four per wavefront)
     (96, 6144, 200),    # rows too wide for a token group of four
+    # f16 rows of whole 64-value steps: 1, 2 or 4 row tiles per workgroup by
+    # the count of 16 x 16 tiles (below 1024, from 1024, from 2048).
+    (520, 4096, 16),    # one row tile, a half tile of rows past the last
+    (2000, 1024, 136),  # two row tiles, half a pair and half a token tile past the last
+    (4000, 1024, 130),  # four row tiles, two of them past the last, two tokens past
+    (300, 1056, 12),    # f16 rows of 16.5 steps: the f32 matrix-core form
 ]
 
 
@@ -73,6 +79,58 @@ def test_dense_linear(ctx, fmt, rows, cols, tokens):
     finally:
         ctx.matrix_release(handle)
     assert_close(actual, expected(fmt, w, x, tokens), what=f"format {fmt} {rows}x{cols} tokens {tokens}", **TOL)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_dense_activation_range(ctx, fmt):
+    # Tokens of very different magnitudes in one batch, past the f16 range
+    # and far below it: the matrix-core forms scale each token's activations
+    # on their own (the f16 form splits them into two f16 halves per step).
+    rows, cols, tokens = 256, 2048, 16
+    w = weights(fmt, rows, cols, 41, 7)
+    x = o.normal(tokens * cols, 42, tokens).reshape(tokens, cols)
+    x[0] *= 6.0e4          # past the f16 range
+    x[1] *= 1.0e-30        # far below it
+    x[2, ::64] *= 1.0e6    # one large value per step
+    x[3, :1000] = 0.0      # steps of zeros
+    handle = ctx.matrix_upload(fmt, rows, cols, None, w)
+    try:
+        actual = run(ctx, handle, x.reshape(-1), cols, tokens, rows)
+    finally:
+        ctx.matrix_release(handle)
+    ref = expected(fmt, w, x.reshape(-1), tokens)
+    for t in range(tokens):
+        assert_close(actual[t], ref[t], what=f"format {fmt} token {t}", **TOL)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_dense_non_finite_activations(ctx, fmt):
+    # An inf activation makes its token's sums +-inf (NaN where the weight
+    # is 0), a NaN makes them NaN, as f32 products and sums do; the other
+    # tokens are untouched.
+    rows, cols, tokens = 64, 1024, 16
+    w = weights(fmt, rows, cols, 43, 9)
+    wf = w.view(np.float16).astype(np.float32) if fmt == qa.FORMAT_F16 else w
+    wf[:, 5][:3] = (0.5, -0.25, 0.0)
+    w = wf.astype(np.float16).view(np.uint16) if fmt == qa.FORMAT_F16 else wf
+    x = o.normal(tokens * cols, 44, tokens).reshape(tokens, cols)
+    x[3, 5] = np.inf
+    x[7, 100] = np.nan
+    handle = ctx.matrix_upload(fmt, rows, cols, None, w)
+    try:
+        actual = run(ctx, handle, x.reshape(-1), cols, tokens, rows)
+    finally:
+        ctx.matrix_release(handle)
+    col5 = (w.view(np.float16).astype(np.float32) if fmt == qa.FORMAT_F16 else w)[:, 5]
+    assert np.all(np.isposinf(actual[3][col5 > 0])) and np.all(np.isneginf(actual[3][col5 < 0]))
+    assert np.all(np.isnan(actual[3][col5 == 0])) and (col5 == 0).any()
+    assert np.all(np.isnan(actual[7]))
+    finite = [t for t in range(tokens) if t not in (3, 7)]
+    xf = x.copy()
+    xf[3] = 0.0
+    xf[7] = 0.0
+    ref = expected(fmt, w, xf.reshape(-1), tokens)
+    assert_close(actual[finite], ref[finite], what=f"format {fmt} finite tokens", **TOL)
 
 
 def test_dense_matrix_dispatch_ones(ctx):
