@@ -3,7 +3,9 @@
 // each f16 weight widened exactly to f32 (half_float.zig:20-23 fromF16), f32
 // products and sums (the reference sums in dotF32's four-lane order,
 // kernels.zig:38-51; this sum runs over a wavefront's lanes, within f32
-// rounding of it).
+// rounding of it). From eight tokens the matrix cores take the product:
+// f32 with widened weights, or for f16 weights f16 operands that carry each
+// activation to 2^-22 of its 64-value step's largest magnitude.
 //
 // HBM bound: the weights stream once per group of up to four tokens (fewer
 // for rows too wide for four tokens' activations in LDS). Each workgroup forms its

@@ -1,8 +1,11 @@
 """GPU parity of f16 / f32 weight matrices (kernels.zig:160-206 Matrix .f16 /
 .f32 arms: linearF16 :82-112, linearF32 :54-80) against the oracle on the
-same seeded inputs. Both sides form the same exact f32 products (an f16
-weight widens exactly); only the summation order differs (the reference's
-four-lane dotF32 against a wavefront reduction), so the bound is tight:
+same seeded inputs. Below eight tokens, and for f32 weights, both sides
+form the same exact f32 products (an f16 weight widens exactly) and only the
+summation order differs (the reference's four-lane dotF32 against a
+wavefront reduction or MFMA sums). From eight tokens the f16 form multiplies
+each activation as two f16 halves carrying it to 2^-22 of its 64-value
+step's largest magnitude. The bound is tight either way:
 |a - r| <= 1e-4 |r| + 1e-4 rms(r) (util.assert_close)."""
 import os
 
