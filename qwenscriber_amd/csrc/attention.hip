@@ -477,10 +477,22 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
             const uint32_t p = first + 16 * blk + n;
             const uint32_t row = p < limit ? p : limit - 1;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
+            for (int g = 0; g < G; ++g)
                 t.kc[blk][g] = *reinterpret_cast<const uint4 *>(k_codes + (size_t)row * kv_width + key_col + 64 * g);
-                t.ks[blk][g] = k_scales[(size_t)row * gpr + kvh * G + g];
-                t.vsc[blk][g] = v_scales[(size_t)row * gpr + kvh * G + g];
+            if constexpr (G == 2) {
+                // Both groups' scales of a row in one 4-byte load each.
+                const uint32_t kk = *reinterpret_cast<const uint32_t *>(k_scales + (size_t)row * gpr + kvh * G);
+                const uint32_t vv = *reinterpret_cast<const uint32_t *>(v_scales + (size_t)row * gpr + kvh * G);
+                t.ks[blk][0] = kk & 0xffffu;
+                t.ks[blk][1] = kk >> 16;
+                t.vsc[blk][0] = vv & 0xffffu;
+                t.vsc[blk][1] = vv >> 16;
+            } else {
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    t.ks[blk][g] = k_scales[(size_t)row * gpr + kvh * G + g];
+                    t.vsc[blk][g] = v_scales[(size_t)row * gpr + kvh * G + g];
+                }
             }
         }
 #pragma unroll
@@ -513,8 +525,20 @@ __device__ __forceinline__ void attention_range(const AttnKernelArgs &a) {
                 const v4i c = __builtin_bit_cast(
                     v4i, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)key_off[blk] + 64 * g, 0, 0));
                 t.kc[blk][g] = make_uint4((uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w);
-                t.ks[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(ksr, (int)kscale_off[blk] + 2 * g, 0, 0);
-                t.vsc[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)kscale_off[blk] + 2 * g, 0, 0);
+            }
+            if constexpr (G == 2) {
+                const uint32_t kk = __builtin_amdgcn_raw_buffer_load_b32(ksr, (int)kscale_off[blk], 0, 0);
+                const uint32_t vv = __builtin_amdgcn_raw_buffer_load_b32(vsr, (int)kscale_off[blk], 0, 0);
+                t.ks[blk][0] = kk & 0xffffu;
+                t.ks[blk][1] = kk >> 16;
+                t.vsc[blk][0] = vv & 0xffffu;
+                t.vsc[blk][1] = vv >> 16;
+            } else {
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    t.ks[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(ksr, (int)kscale_off[blk] + 2 * g, 0, 0);
+                    t.vsc[blk][g] = __builtin_amdgcn_raw_buffer_load_b16(vsr, (int)kscale_off[blk] + 2 * g, 0, 0);
+                }
             }
         }
 #pragma unroll
