@@ -724,6 +724,243 @@ __global__ __launch_bounds__(64 * W) void gemm_f16_kernel(const DenseArgs a) {
     }
 }
 
+// f16 weights, many rows or tokens: the same split activations, with each
+// of the workgroup's W wavefronts on its own R row tiles (all of K) and T
+// token tiles sharing every weight load. The activations are loaded, scaled
+// and split once per workgroup, C steps at a time, into LDS in the MFMA
+// operand layout (double buffered, one barrier per chunk), so the address
+// unit moves each activation once per 16 R W rows. A unit of staging is one
+// step of one token tile: 128 threads, each with 8 consecutive values of
+// one token (two 16-byte loads; the token's 64 values are 8 neighbouring
+// lanes, whose maximum three DPP exchanges give), writing one 16-byte hi and
+// one lo operand lane. Operand lane 16 g + li of half h sits at position
+// 16 g + ((li + 2 g + 8 h) mod 16) of its 64: a wavefront reads an operand
+// as 64 distinct 16-byte words, and the writers of one pass hit 16
+// distinct bank groups. The weights stream C steps ahead through a bounded
+// buffer resource (rows past the matrix and steps past the row read zeros,
+// no memory). A lane's accumulators are rows 4 (l / 16) + i of its tile for
+// token l % 16, so the epilogue needs no cross-wavefront sum: residual,
+// siluMul of gate / up pairs (rows 2p, 2p + 1 sit in the same lane), or
+// RMSNorm's inverse RMS per token.
+template <bool Norm, int R, int T, int W>
+__global__ __launch_bounds__(64 * W) void gemm_f16_rows_kernel(const DenseArgs a) {
+    constexpr int C = 2;                      // steps per chunk, and steps of weight loads in flight
+    constexpr int kUnits = C * T;             // staging units per chunk: [tile][step]
+    constexpr int kGroups = W / 2;            // 128-thread staging groups
+    constexpr int NU = kUnits / kGroups;      // units per thread per chunk
+    static_assert(kUnits % kGroups == 0, "whole units per staging group");
+    constexpr int kOps = kUnits * 4 * 64;     // u32x4 operands per buffer: [step][tile][half][hi/lo][64]
+    constexpr int kInv = kUnits * 16;         // 1 / s per buffer: [step][tile][token]
+    constexpr uint32_t kFar = 0x7FFFFF00u;
+    extern __shared__ float4 lds_dyn[];       // RMSNorm weights (cols values), then the two buffers
+    __shared__ float sspart[kGroups][T][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, g = lane >> 4;
+    const uint32_t rows_wg = 16u * R * W;
+    const uint32_t row0 = blockIdx.x * rows_wg, tok0 = blockIdx.y * (16u * T);
+    const uint32_t nrows = min(rows_wg, a.rows - row0), ntok = min(16u * T, a.tokens - tok0);
+    const uint32_t steps = a.cols / 64, chunks = (steps + C - 1) / C;
+    u32x4 *ops = reinterpret_cast<u32x4 *>(lds_dyn + (Norm ? a.cols / 4 : 0));
+    float *invs = reinterpret_cast<float *>(ops + 2 * kOps);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.w) + (size_t)row0 * a.cols * 2, (short)0, (int)(nrows * a.cols * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.x) + (size_t)tok0 * a.cols, (short)0, (int)(ntok * a.cols * 4), 0x00020000);
+    const uint32_t w_lane = ((uint32_t)wave * 16u * R + li) * a.cols * 2 + 16u * g;
+    // Staging thread: group gamma, token tt of the unit's tile, values 8 q8 .. + 7 of its step.
+    const int gamma = tid >> 7, tt = (tid >> 3) & 15, q8 = tid & 7;
+    const int hf = q8 >> 2, gq = q8 & 3;
+    const int pos = 16 * gq + ((tt + 2 * gq + 8 * hf) & 15);  // operand word of this thread
+    u32x4 wb[C][R][2];
+    auto issue_w = [&](uint32_t s, int slot) {
+        const bool valid = s < steps;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                wb[slot][r][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                    wres, valid ? w_lane + 16u * r * a.cols * 2 + 128u * s + 64u * h : kFar, 0, 2 /* nt */);
+        asm volatile("" ::: "memory");
+    };
+    u32x4 xr[NU][2];
+    // Unit u = gamma + kGroups j of a chunk: tile u / C, step u % C.
+    auto issue_x = [&](uint32_t chunk) {
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = gamma + kGroups * j, t = u / C, i = u % C;
+            const uint32_t s = chunk * C + i;
+            const uint32_t off = ((16u * t + tt) * a.cols + 64u * s + 8u * q8) * 4;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                xr[j][h] = __builtin_amdgcn_raw_buffer_load_b128(xres, s < steps ? off + 16u * h : kFar, 0, 0);
+        }
+        asm volatile("" ::: "memory");
+    };
+    float ss[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) ss[t] = 0.0f;
+    auto stage_x = [&](uint32_t chunk, int buf) {
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = gamma + kGroups * j, t = u / C, i = u % C;
+            const uint32_t s = min(chunk * C + i, steps - 1);
+            const float4 x0 = __builtin_bit_cast(float4, xr[j][0]), x1 = __builtin_bit_cast(float4, xr[j][1]);
+            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            if constexpr (Norm) {
+                // (Steps past the row read zeros and add nothing.)
+                const float4 n0 = lds_dyn[s * 16 + 2 * q8], n1 = lds_dyn[s * 16 + 2 * q8 + 1];
+                const float nv[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    ss[t] = __fadd_rn(ss[t], __fmul_rn(v[k], v[k]));
+                    v[k] = __fmul_rn(v[k], nv[k]);
+                }
+            }
+            float mx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(v[k]));
+            mx = fmaxf(mx, dev::xor_lane<1>(mx));
+            mx = fmaxf(mx, dev::xor_lane<2>(mx));
+            mx = fmaxf(mx, dev::xor_lane<4>(mx));
+            const uint32_t e = max(__float_as_uint(mx) & 0x7F800000u, 15u << 23);
+            const bool inf = e == 0x7F800000u;
+            const float sc = __uint_as_float((268u << 23) - e);
+            u32x4 hw, lw;
+#pragma unroll
+            for (int k = 0; k < 8; k += 2) {
+                const f2 fv = {__fmul_rn(v[k], sc), __fmul_rn(v[k + 1], sc)};
+                const h2 h = __builtin_convertvector(fv, h2);
+                h2 l = __builtin_convertvector(fv - __builtin_convertvector(h, f2), h2);
+                if (inf) l = h2{(_Float16)0.0f, (_Float16)0.0f};
+                hw[k / 2] = __builtin_bit_cast(uint32_t, h);
+                lw[k / 2] = __builtin_bit_cast(uint32_t, l);
+            }
+            u32x4 *dst = ops + buf * kOps + ((i * T + t) * 2 + hf) * 2 * 64 + pos;
+            dst[0] = hw;
+            dst[64] = lw;
+            if (q8 == 0) invs[buf * kInv + (i * T + t) * 16 + tt] = __uint_as_float(e - (14u << 23));
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        issue_w(i, i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    issue_x(0);
+    if constexpr (Norm) {
+        // The RMSNorm weights into LDS (two loads per thread per pass,
+        // stored unconditionally: past the row, the last four again).
+        const float4 *norm4 = reinterpret_cast<const float4 *>(a.norm);
+        for (uint32_t k = 4 * tid; k < a.cols; k += 512u * W) {
+            const float4 v0 = norm4[min(k, a.cols - 4) / 4], v1 = norm4[min(k + 256u * W, a.cols - 4) / 4];
+            __builtin_amdgcn_sched_barrier(0);
+            lds_dyn[min(k, a.cols - 4) / 4] = v0;
+            lds_dyn[min(k + 256u * W, a.cols - 4) / 4] = v1;
+        }
+        __syncthreads();
+    }
+    stage_x(0, 0);
+    __syncthreads();
+    v4f acc[R][T];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[r][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // Operand lane `lane` of a 64-word operand.
+    const int rpos = 16 * g + ((li + 2 * g) & 15);
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < chunks) issue_x(c + 1);
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const u32x4 *op = ops + buf * kOps + (i * T + t) * 4 * 64;
+                const h8 hi0 = __builtin_bit_cast(h8, op[rpos]), lo0 = __builtin_bit_cast(h8, op[64 + rpos]);
+                const int rpos1 = 16 * g + ((li + 2 * g + 8) & 15);
+                const h8 hi1 = __builtin_bit_cast(h8, op[128 + rpos1]), lo1 = __builtin_bit_cast(h8, op[192 + rpos1]);
+                const float inv = invs[buf * kInv + (i * T + t) * 16 + li];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const h8 w0 = __builtin_bit_cast(h8, wb[i][r][0]), w1 = __builtin_bit_cast(h8, wb[i][r][1]);
+                    v4f m = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, hi0, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    m = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, hi1, m, 0, 0, 0);
+                    m = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, lo0, m, 0, 0, 0);
+                    m = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, lo1, m, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[r][t][e] = __fmaf_rn(m[e], inv, acc[r][t][e]);
+                }
+            }
+            issue_w((c + 1) * C + i, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c + 1 < chunks) stage_x(c + 1, buf ^ 1);
+        __syncthreads();
+    }
+    if constexpr (Norm) {
+        // Each token's squares: the 8 lanes of its values, then the staging
+        // groups in order.
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float v = ss[t];
+            v += dev::xor_lane<1>(v);
+            v += dev::xor_lane<2>(v);
+            v += dev::xor_lane<4>(v);
+            if (q8 == 0) sspart[gamma][t][tt] = v;
+        }
+        __syncthreads();
+    }
+    const uint32_t wrow = row0 + (uint32_t)wave * 16u * R;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const uint32_t tok = tok0 + 16u * t + li;
+        if (tok >= a.tokens) continue;
+        float inv_rms = 1.0f;
+        if constexpr (Norm) {
+            float sum = sspart[0][t][li];
+#pragma unroll
+            for (int k = 1; k < kGroups; ++k) sum += sspart[k][t][li];
+            inv_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)a.cols), a.eps)));
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t rbase = wrow + 16u * r + 4u * g;
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = Norm ? __fmul_rn(acc[r][t][e], inv_rms) : acc[r][t][e];
+            if (a.pairs) {
+#pragma unroll
+                for (int e = 0; e < 4; e += 2)
+                    if (rbase + e < a.rows)
+                        a.out[(size_t)tok * (a.rows / 2) + (rbase + e) / 2] =
+                            __fmul_rn(__fdiv_rn(y[e], __fadd_rn(1.0f, expf(-y[e]))), y[e + 1]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (rbase + e < a.rows) {
+                        const size_t at = (size_t)tok * a.rows + rbase + e;
+                        a.out[at] = a.residual ? a.residual[at] + y[e] : y[e];
+                    }
+            }
+        }
+    }
+}
+
+template <bool Norm, int R, int T, int W>
+hipError_t launch_f16_rows(hipStream_t s, uint32_t tokens, const DenseArgs &a) {
+    constexpr int C = 2;
+    const dim3 grid((a.rows + 16 * R * W - 1) / (16 * R * W), (tokens + 16 * T - 1) / (16 * T));
+    const size_t lds = (Norm ? (size_t)a.cols * 4 : 0) + 2 * ((size_t)C * T * 4 * 64 * 16 + (size_t)C * T * 16 * 4);
+    void (*kernel)(const DenseArgs) = gemm_f16_rows_kernel<Norm, R, T, W>;
+    if (lds > (48u << 10)) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * W), lds, s, a);
+    return hipGetLastError();
+}
+
 template <int TOK>
 hipError_t launch_dense(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
     void (*kernel)(const DenseArgs) = half ? (norm ? gemv_dense_kernel<true, true, TOK> : gemv_dense_kernel<true, false, TOK>)
@@ -815,6 +1052,17 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
             // tiles per workgroup by the count of 16 x 16 tiles (more rows
             // per workgroup share each activation load; fewer keep every CU
             // busy on a small matrix).
+            // More than 16 tokens: the rows form, T token tiles sharing each
+            // weight load (measured best on the 1.7B shapes at 32 to 256
+            // tokens and the lm_head at 64).
+            if (tokens > 16) {
+                if (w.rows < 8192)
+                    return w.rows >= 4096 ? (norm ? launch_f16_rows<true, 1, 2, 8>(s, tokens, a) : launch_f16_rows<false, 1, 2, 8>(s, tokens, a))
+                                          : (norm ? launch_f16_rows<true, 1, 2, 4>(s, tokens, a) : launch_f16_rows<false, 1, 2, 4>(s, tokens, a));
+                if (tokens >= 128) return norm ? launch_f16_rows<true, 2, 4, 8>(s, tokens, a) : launch_f16_rows<false, 2, 4, 8>(s, tokens, a);
+                if (w.rows >= 65536) return norm ? launch_f16_rows<true, 1, 4, 8>(s, tokens, a) : launch_f16_rows<false, 1, 4, 8>(s, tokens, a);
+                return norm ? launch_f16_rows<true, 1, 2, 8>(s, tokens, a) : launch_f16_rows<false, 1, 2, 8>(s, tokens, a);
+            }
             const uint64_t tiles = (uint64_t)grid.x * grid.y;
             if (tiles >= 2048) return norm ? launch_f16_mma<true, 4, 4, 2>(s, tokens, lds, a)
                                            : launch_f16_mma<false, 4, 4, 2>(s, tokens, lds, a);

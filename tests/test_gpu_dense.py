@@ -62,11 +62,18 @@ SHAPES = [  # (rows, cols, tokens): four, two or one token per workgroup
     (333, 3072, 33),    # rows and tokens past whole tiles
     (64, 128, 40),      # the fewest K-steps the form takes (four per wavefront)
     (96, 6144, 200),    # rows too wide for a token group of four
-    # f16 rows of whole 64-value steps: 1, 2 or 4 row tiles per workgroup by
-    # the count of 16 x 16 tiles (below 1024, from 1024, from 2048).
+    # f16 rows of whole 64-value steps, up to 16 tokens: K split over the
+    # wavefronts, 1, 2 or 4 row tiles per workgroup by the count of 16 x 16
+    # tiles (below 1024, from 1024, from 2048).
     (520, 4096, 16),    # one row tile, a half tile of rows past the last
-    (2000, 1024, 136),  # two row tiles, half a pair and half a token tile past the last
-    (4000, 1024, 130),  # four row tiles, two of them past the last, two tokens past
+    (16400, 512, 16),   # two row tiles, half a pair past the last
+    (32800, 256, 12),   # four row tiles, two and a half past the last, four tokens short
+    # More than 16 tokens: each wavefront on its own rows, T token tiles per
+    # workgroup (R row tiles per wavefront, W wavefronts).
+    (2000, 1024, 136),  # R 1, T 2, W 4; a half row tile and half a token tile past the last
+    (4100, 1024, 40),   # R 1, T 2, W 8; four rows and 24 tokens short of the last workgroup
+    (8200, 1024, 130),  # R 2, T 4, W 8; rows and tokens past whole workgroups
+    (65600, 256, 20),   # R 1, T 4, W 8: the lm_head form at 17..127 tokens
     (300, 1056, 12),    # f16 rows of 16.5 steps: the f32 matrix-core form
 ]
 
