@@ -433,8 +433,9 @@ def bench_dense_gemv(ctx, qa, rows, cols, tokens, steps, rotate_bytes, fmt):
     """f32 / f16 weights (kernels.zig:54-112 linearF32 / linearF16): one call
     per launch over a rotation of synthetic copies (>= rotate_bytes, so each
     call streams its weights from HBM). Algorithmic bytes per call: the
-    weights once (up to four tokens share one pass), the activations and the
-    outputs."""
+    weights once, the activations and the outputs (up to four tokens share a
+    pass over the weights on the vector ALUs; from eight, 16 or 64 on the
+    matrix cores)."""
     elem = 2 if fmt == qa.FORMAT_F16 else 4
     per = rows * cols * elem
     copies = max(1, math.ceil(rotate_bytes / per))
@@ -502,8 +503,10 @@ def bench_small(ctx, qa, steps):
     gbs = g5["bytes"] / (g5["call_ms"] * 1e-3) / 1e9
     out["q5_gemv_lm_head_0p6b"] = dict(us=g5["call_ms"] * 1e3, GBs=gbs, frac=gbs / 8000.0)
     # The same shape with f16 weights (the converter's unquantized form), at
-    # one token and at four (one pass over the weights for the four).
-    for tokens in (1, 4):
+    # one token and at four (one pass over the weights for the four); at 16
+    # on the f16 matrix cores (K split, one pass for the 16) and at 64 (the
+    # rows form, one pass for the 64).
+    for tokens in (1, 4, 16, 64):
         out[f"f16_gemv_lm_head_0p6b_t{tokens}"] = bench_dense_gemv(ctx, qa, 151936, 1024, tokens, steps, 2.1e9,
                                                                    qa.FORMAT_F16)
     # q4 GEMM, bf16 activations, M = 128 / 512 / 1500 at
