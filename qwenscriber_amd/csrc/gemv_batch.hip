@@ -564,9 +564,20 @@ template <int TW, int KC>
 __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
     using S = SplitShape<TW, KC, 32>;  // (digit staging only)
     constexpr int ROWS = S::ROWS, DPT = S::DPT;
+    // The wavefront's rows of a chunk (KC 40-byte groups each) are loaded as
+    // whole 16-byte pieces, consecutive lanes on consecutive pieces, and
+    // passed through its own LDS rows (stride RS pieces: the 16 rows one
+    // operand read touches fall on distinct banks), from which each lane
+    // reads its 8 nibble bytes and 2 fifth-bit bytes per group.
+    constexpr int PPR = KC * 40 / 16;          // pieces of a row's chunk
+    constexpr int RS = KC == 4 ? 11 : 7;       // LDS row stride, pieces
+    constexpr int NP = ROWS * PPR;             // pieces per wavefront and chunk
+    constexpr int NWQ = (NP + 63) / 64;        // loads per lane
+    static_assert(KC * 40 % 16 == 0 && RS >= PPR, "whole pieces per row");
     __shared__ v4i dl[2][S::DPIECES];
     __shared__ float4 ml[2][KC * 4];
     __shared__ float ssl[kTokenTile * 16];
+    __shared__ v4i wq[4][ROWS * RS];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -580,25 +591,26 @@ __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
     const uint32_t chunks = a.slice_groups / KC;
     const uint8_t *dig = a.digits + (size_t)tile * gpr * kGroupBytes;
     const float *mul = a.mult + (size_t)tile * gpr * kTokenTile;
+    v4i *wl = wq[wave];
 
-    uint2 rn[TW][KC];
-    uint32_t rf[TW][KC];
+    v4i rw[NWQ];
     v4i rd[DPT];
     float4 rm = {};
     uint32_t rs[TW][KC / 2];
-    // One chunk's loads (rows past the matrix read its last row; their
-    // results are never stored).
+    // One chunk's loads (rows past the matrix read its last row, pieces
+    // past the wavefront's the last piece again; neither is stored).
     auto load = [&](uint32_t g0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < NWQ; ++m) {
+            const int q = lane + 64 * m < NP ? lane + 64 * m : NP - 1;
+            uint32_t row = row0 + q / PPR;
+            if (row >= a.n) row = a.n - 1;
+            rw[m] = *reinterpret_cast<const v4i *>(a.data + row * row_bytes + (size_t)g0 * 40 + 16 * (q % PPR));
+        }
 #pragma unroll
         for (int t = 0; t < TW; ++t) {
             uint32_t row = row0 + t * kRowTile + col;
             if (row >= a.n) row = a.n - 1;
-            const uint8_t *grp = a.data + row * row_bytes + (size_t)g0 * 40;
-#pragma unroll
-            for (int i = 0; i < KC; ++i) {
-                rn[t][i] = *reinterpret_cast<const uint2 *>(grp + i * 40 + 8 * blk);
-                rf[t][i] = *reinterpret_cast<const uint16_t *>(grp + i * 40 + 32 + 2 * blk);
-            }
             __builtin_memcpy(rs[t], a.scales + (size_t)row * gpr + g0, 2 * KC);
         }
 #pragma unroll
@@ -625,15 +637,22 @@ __global__ __launch_bounds__(256) void gemv_split_q5_kernel(const SplitArgs a) {
         for (int m = 0; m < DPT; ++m)
             if (tid + 256 * m < S::DPIECES) dl[buf][tid + 256 * m] = rd[m];
         if (tid < KC * 4) ml[buf][tid] = rm;
-        // This chunk's operands and scales, out of the registers the next
-        // chunk's loads are about to fill.
+#pragma unroll
+        for (int m = 0; m < NWQ; ++m) {
+            const int q = lane + 64 * m;
+            if (q < NP) wl[(q / PPR) * RS + q % PPR] = rw[m];
+        }
+        // This chunk's operands and scales, out of the registers and LDS
+        // rows the next chunk's loads are about to fill.
         v4i wop[TW][KC];
         float sc[TW][KC];
 #pragma unroll
         for (int t = 0; t < TW; ++t)
 #pragma unroll
             for (int i = 0; i < KC; ++i) {
-                wop[t][i] = expand_q5(rn[t][i], rf[t][i]);
+                const uint8_t *grp = reinterpret_cast<const uint8_t *>(wl + (t * kRowTile + col) * RS) + i * 40;
+                wop[t][i] = expand_q5(*reinterpret_cast<const uint2 *>(grp + 8 * blk),
+                                      *reinterpret_cast<const uint16_t *>(grp + 32 + 2 * blk));
                 sc[t][i] = dev::f16_bits_to_f32((uint16_t)(rs[t][i / 2] >> (16 * (i % 2))));
             }
         __syncthreads();
