@@ -979,6 +979,15 @@ hipError_t launch_dense(hipStream_t s, dim3 grid, size_t lds, bool half, bool no
 // stay in LDS (the static tiles take about 5 KiB of the 160 KiB).
 constexpr uint32_t kMmaMinTokens = 8;
 constexpr uint32_t kMmaMaxNormCols = 36864;
+constexpr size_t kMaxWorkgroupLds = 160u << 10;  // gfx950
+
+// LDS of the f16 forms apart from RMSNorm weights: the rows form's two
+// operand buffers and its per-group squares; the K-split form's
+// activation tiles, partial tiles and squares (four wavefronts).
+constexpr size_t rows_form_lds(int t, int w) {
+    return 2 * ((size_t)2 * t * 4 * 64 * 16 + (size_t)2 * t * 16 * 4) + (size_t)(w / 2) * t * 16 * 4;
+}
+constexpr size_t ksplit_form_lds(int r) { return (size_t)4 * 16 * 17 * 16 + (size_t)4 * 16 * r * 17 * 4 + 4 * 16 * 4; }
 
 hipError_t launch_mma(hipStream_t s, dim3 grid, size_t lds, bool half, bool norm, const DenseArgs &a) {
     void (*kernel)(const DenseArgs) = half ? (norm ? gemm_dense_kernel<true, true> : gemm_dense_kernel<true, false>)
@@ -1048,27 +1057,39 @@ hipError_t launch_gemv_dense(hipStream_t s, int cus, const GemvInput &in, const 
         if (grid.y > 65535) return hipErrorInvalidValue;
         const size_t lds = norm ? (size_t)w.cols * 4 : 0;
         if (half && w.cols % 64 == 0 && w.cols / 64 >= 4) {
-            // f16 weights: the split-activation f16 form, with 1, 2 or 4 row
-            // tiles per workgroup by the count of 16 x 16 tiles (more rows
-            // per workgroup share each activation load; fewer keep every CU
-            // busy on a small matrix).
+            // f16 weights: the split-activation f16 forms, where their LDS
+            // (with RMSNorm, the norm weights beside the operand buffers)
+            // fits a workgroup's 160 KiB.
+            const size_t norm_lds = norm ? (size_t)w.cols * 4 : 0;
+            auto fits = [&](size_t bytes) { return norm_lds + bytes <= kMaxWorkgroupLds; };
             // More than 16 tokens: the rows form, T token tiles sharing each
             // weight load (measured best on the 1.7B shapes at 32 to 256
             // tokens and the lm_head at 64).
             if (tokens > 16) {
-                if (w.rows < 8192)
-                    return w.rows >= 4096 ? (norm ? launch_f16_rows<true, 1, 2, 8>(s, tokens, a) : launch_f16_rows<false, 1, 2, 8>(s, tokens, a))
-                                          : (norm ? launch_f16_rows<true, 1, 2, 4>(s, tokens, a) : launch_f16_rows<false, 1, 2, 4>(s, tokens, a));
-                if (tokens >= 128) return norm ? launch_f16_rows<true, 2, 4, 8>(s, tokens, a) : launch_f16_rows<false, 2, 4, 8>(s, tokens, a);
-                if (w.rows >= 65536) return norm ? launch_f16_rows<true, 1, 4, 8>(s, tokens, a) : launch_f16_rows<false, 1, 4, 8>(s, tokens, a);
-                return norm ? launch_f16_rows<true, 1, 2, 8>(s, tokens, a) : launch_f16_rows<false, 1, 2, 8>(s, tokens, a);
+                if (w.rows < 8192) {
+                    if (w.rows >= 4096 && fits(rows_form_lds(2, 8)))
+                        return norm ? launch_f16_rows<true, 1, 2, 8>(s, tokens, a) : launch_f16_rows<false, 1, 2, 8>(s, tokens, a);
+                    if (w.rows < 4096 && fits(rows_form_lds(2, 4)))
+                        return norm ? launch_f16_rows<true, 1, 2, 4>(s, tokens, a) : launch_f16_rows<false, 1, 2, 4>(s, tokens, a);
+                } else if (tokens >= 128 && fits(rows_form_lds(4, 8))) {
+                    return norm ? launch_f16_rows<true, 2, 4, 8>(s, tokens, a) : launch_f16_rows<false, 2, 4, 8>(s, tokens, a);
+                } else if (tokens < 128 && w.rows >= 65536 && fits(rows_form_lds(4, 8))) {
+                    return norm ? launch_f16_rows<true, 1, 4, 8>(s, tokens, a) : launch_f16_rows<false, 1, 4, 8>(s, tokens, a);
+                } else if (tokens < 128 && w.rows < 65536 && fits(rows_form_lds(2, 8))) {
+                    return norm ? launch_f16_rows<true, 1, 2, 8>(s, tokens, a) : launch_f16_rows<false, 1, 2, 8>(s, tokens, a);
+                }
             }
+            // Up to 16 tokens (or rows-form LDS too large): K split over the
+            // wavefronts, with 1, 2 or 4 row tiles per workgroup by the
+            // count of 16 x 16 tiles (more rows per workgroup share each
+            // activation load; fewer keep every CU busy on a small matrix).
             const uint64_t tiles = (uint64_t)grid.x * grid.y;
-            if (tiles >= 2048) return norm ? launch_f16_mma<true, 4, 4, 2>(s, tokens, lds, a)
-                                           : launch_f16_mma<false, 4, 4, 2>(s, tokens, lds, a);
-            if (tiles >= 1024) return norm ? launch_f16_mma<true, 2, 4, 2>(s, tokens, lds, a)
-                                           : launch_f16_mma<false, 2, 4, 2>(s, tokens, lds, a);
-            return norm ? launch_f16_mma<true, 1, 4, 2>(s, tokens, lds, a) : launch_f16_mma<false, 1, 4, 2>(s, tokens, lds, a);
+            if (tiles >= 2048 && fits(ksplit_form_lds(4)))
+                return norm ? launch_f16_mma<true, 4, 4, 2>(s, tokens, lds, a) : launch_f16_mma<false, 4, 4, 2>(s, tokens, lds, a);
+            if (tiles >= 1024 && fits(ksplit_form_lds(2)))
+                return norm ? launch_f16_mma<true, 2, 4, 2>(s, tokens, lds, a) : launch_f16_mma<false, 2, 4, 2>(s, tokens, lds, a);
+            if (fits(ksplit_form_lds(1)))
+                return norm ? launch_f16_mma<true, 1, 4, 2>(s, tokens, lds, a) : launch_f16_mma<false, 1, 4, 2>(s, tokens, lds, a);
         }
         return launch_mma(s, grid, lds, half, norm, a);
     }
