@@ -63,10 +63,12 @@ SHAPES = [  # (rows, cols, tokens): four, two or one token per workgroup
     (64, 128, 40),      # the fewest K-steps the form takes (four per wavefront)
     (96, 6144, 200),    # rows too wide for a token group of four
     # f16 rows of whole 64-value steps, up to 16 tokens: K split over the
-    # wavefronts, 1, 2 or 4 row tiles per workgroup by the count of 16 x 16
-    # tiles (below 1024, from 1024, from 2048).
+    # wavefronts, 1, 2, 3 or 4 row tiles per workgroup by the 16 x 16 tiles
+    # per CU (up to 1, 2, 3, more; the counts below are for 256 CUs).
     (520, 4096, 16),    # one row tile, a half tile of rows past the last
-    (16400, 512, 16),   # two row tiles, half a pair past the last
+    (6000, 512, 16),    # two row tiles, a half tile past the last
+    (12008, 256, 9),    # three row tiles, the last workgroup's 8 rows of 48
+    (16400, 512, 16),   # four row tiles, one past the last
     (32800, 256, 12),   # four row tiles, two and a half past the last, four tokens short
     # More than 16 tokens: each wavefront on its own rows, T token tiles per
     # workgroup (R row tiles per wavefront, W wavefronts).
