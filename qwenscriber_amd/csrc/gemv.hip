@@ -1156,6 +1156,127 @@ __global__ __launch_bounds__(256) void gemv_b8_kernel(const GemvB8Args a) {
     }
 }
 
+// q5 with the unit's bytes loaded whole: a unit's U RG rows are one
+// contiguous stretch of the data plane (1280 U S bytes, a whole number of
+// 16-byte pieces), which the wavefront loads as consecutive 16-byte pieces
+// (clamped to the plane's end) and passes through its own LDS, from which
+// each lane reads its slices' 16 nibble bytes and 4 fifth-bit bytes. The
+// per-lane form needs four loads per slice (two 8-byte, one 4-byte and the
+// scale); this one 1.25 plus the scale. Otherwise as gemv_b8_kernel.
+template <int S, int L, int U, Src M>
+__global__ __launch_bounds__(256) void gemv_q5_staged_kernel(const GemvB8Args a) {
+    constexpr int RG = 64 / L;
+    constexpr int log_l = Log2<L>::value;
+    constexpr int log_u = Log2<U>::value;
+    constexpr uint32_t UB = 1280u * U * S;  // bytes per unit: U RG rows of 20 S L bytes
+    constexpr int P = UB / 16, NWQ = (P + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    const int rr = lane >> log_l;
+    const int li = lane & (L - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t token = blockIdx.y;
+    const uint32_t gpr = a.k >> 6;
+    const uint32_t row_bytes = b8_row_bytes<Fmt8::Q5>(gpr);
+    const uint32_t units = (a.row_groups + U - 1) / U;
+    const uint32_t full_units = a.n / (U * RG);
+    const uint32_t count = full_units > wave ? (full_units - wave + nwaves - 1) / nwaves : 0;
+    const uint32_t last_piece = a.n * row_bytes - 16;
+    float *out = a.out + (size_t)token * (a.pairs ? a.n / 2 : a.n);
+    const float *residual = a.residual ? a.residual + (size_t)token * a.n : nullptr;
+    __shared__ u32x4 wst[4][P];
+    u32x4 *wl = wst[threadIdx.x >> 6];
+
+    struct Unit {
+        u32x4 w[NWQ];
+        uint16_t scale[U][S];
+    };
+    // Pieces past the plane's end read its last piece again; rows past the
+    // end are dropped at the store.
+    auto load = [&](Unit &dst, uint32_t unit) __attribute__((always_inline)) {
+        const uint32_t base = unit * UB;
+#pragma unroll
+        for (int m = 0; m < NWQ; ++m) {
+            const uint32_t q = lane + 64 * m < P ? lane + 64 * m : P - 1;
+            const uint32_t off = min(base + 16u * q, last_piece);
+            dst.w[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(a.data + off));
+        }
+        const uint32_t row0 = unit * (U * RG) + rr;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const uint32_t row = row0 + u * RG < a.n ? row0 + u * RG : a.n - 1;
+                dst.scale[u][s] = load_scale(a.scales, row * gpr + ((li + s * L) >> 1));
+            }
+    };
+    auto load_res = [&](uint32_t unit) -> float {
+        const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+        return residual && row < a.n ? residual[row] : 0.0f;
+    };
+
+    Unit A, B;
+    RowValues rv;
+    fetch_row<M>(a.x + (size_t)token * a.k, a.norm, a.k, rv);
+    load(A, count ? wave : (full_units ? full_units - 1 : 0));
+    __shared__ __attribute__((aligned(16))) Act8Lds lds;
+    block_encode8<M>(rv, a.k, a.eps, lds);
+    Act8 X[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) load_act8<Fmt8::Q5>(lds, li + s * L, X[s]);
+    float resA = count ? load_res(wave) : 0.0f, resB = 0.0f;
+
+    auto process = [&](const Unit &src, float res, uint32_t unit) __attribute__((always_inline)) {
+        // The unit's bytes into this wavefront's LDS (its reads of the
+        // previous unit came before, in program order).
+#pragma unroll
+        for (int m = 0; m < NWQ; ++m)
+            if (lane + 64 * m < P) wl[lane + 64 * m] = src.w[m];
+        const uint8_t *lb = reinterpret_cast<const uint8_t *>(wl);
+        float acc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const uint32_t c = li + s * L;
+                const uint8_t *g = lb + (u * RG + rr) * row_bytes + (c >> 1) * 40u;
+                Slice8<Fmt8::Q5> sl;
+                sl.lo0 = *reinterpret_cast<const u32x2 *>(g + (c & 1u) * 16u);
+                sl.lo1 = *reinterpret_cast<const u32x2 *>(g + (c & 1u) * 16u + 8u);
+                sl.hi = *reinterpret_cast<const uint32_t *>(g + 32u + (c & 1u) * 4u);
+                const float part = b8_slice_dot(sl, X[s]) * (dev::f16_bits_to_f32(src.scale[u][s]) * X[s].mult);
+                acc[u] = s == 0 ? part : acc[u] + part;
+            }
+        }
+        const float total = reduce_rows<U, L>(acc, lane);
+        const bool writer = (li & ((L >> log_u) - 1)) == 0;
+        const uint32_t row = (unit * U + (li >> (log_l - log_u))) * RG + rr;
+        if (a.pairs) {
+            const float partner = __shfl_down(total, RG > 1 ? L : (L >> log_u), kWave);
+            if (writer && (row & 1u) == 0 && row < a.n) out[row >> 1] = silu_mul(total, partner);
+        } else if (writer && row < a.n) {
+            out[row] = res + total;
+        }
+    };
+
+    uint32_t i = 0;
+    for (; i + 1 < count; i += 2) {
+        const uint32_t ua = wave + i * nwaves, ub = ua + nwaves;
+        load(B, ub);
+        resB = load_res(ub);
+        process(A, resA, ua);
+        const uint32_t un = i + 2 < count ? ub + nwaves : ub;
+        load(A, un);
+        resA = load_res(un);
+        process(B, resB, ub);
+    }
+    if (i < count) process(A, resA, wave + i * nwaves);
+    if (full_units < units && full_units % nwaves == wave) {
+        load(B, full_units);
+        process(B, load_res(full_units), full_units);
+    }
+}
+
 // Any K up to the LDS encoding's 6144: one wavefront per row (per row pair
 // with pairs), lanes striding over the row's slices.
 template <Fmt8 F, Src M>
@@ -1473,10 +1594,22 @@ template <Fmt8 F, Src M>
 hipError_t dispatch_b8(hipStream_t s, int cus, GemvB8Args args, uint32_t tokens) {
     const uint32_t L = gcd_u32(args.t, 64);
     const uint32_t S = args.t / L;
+    // q5 planes on 16-byte boundaries, up to 32768 rows: the staged form
+    // (whole pieces). Measured on one box: the 1.7B q5 batch-1 step
+    // 0.975-0.977 -> 0.965-0.966 ms; the 0.6B lm_head shape [151936 x 1024]
+    // 22.8-23.1 us without it, 23.1-24.1 us with it, so longer matrices keep
+    // the per-lane loads.
+    const bool staged = F == Fmt8::Q5 && ((uintptr_t)args.data & 15u) == 0 && args.n <= 32768u;
 #define QWH_GEMV_B8_CASE(S_, L_, U_)                                                               \
     if (S == S_ && L == L_) {                                                                      \
         args.row_groups = (args.n + (64 / L_) - 1) / (64 / L_);                                    \
         const uint32_t units = (args.row_groups + U_ - 1) / U_;                                    \
+        if constexpr (F == Fmt8::Q5)                                                               \
+            if (staged) {                                                                          \
+                auto kernel = gemv_q5_staged_kernel<S_, L_, U_, M>;                                \
+                kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);        \
+                return hipGetLastError();                                                          \
+            }                                                                                      \
         auto kernel = gemv_b8_kernel<F, S_, L_, U_, M>;                                            \
         kernel<<<dim3(grid_blocks(kernel, units, cus), tokens), 256, 0, s>>>(args);                \
         return hipGetLastError();                                                                  \
