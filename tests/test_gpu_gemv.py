@@ -157,6 +157,7 @@ def test_q8_gemv_edge_shapes(ctx, rows, cols, tokens):
 
 
 @pytest.mark.parametrize("rows,cols,tokens", [
+    # (Planes on 16-byte boundaries up to 32768 rows: the staged form.)
     (1001, 1024, 1),    # one slice per lane, 32 lanes per row (0.6B shapes)
     (130, 2048, 2),     # one slice, 64 lanes per row
     (64, 512, 1),       # 16 lanes per row
@@ -172,6 +173,16 @@ def test_q5_gemv_shapes(ctx, rows, cols, tokens):
     w = o.normal(rows * cols, 10, rows, 0.02).reshape(rows, cols)
     x = o.normal(tokens * cols, 10, 1000 + cols)
     check(ctx, o.Q5, w, x, tokens, f"q5 {rows}x{cols} tokens {tokens}")
+
+
+@pytest.mark.parametrize("rows,cols", [(32770, 1024), (32800, 3072)])
+def test_q5_gemv_per_lane_form(ctx, rows, cols):
+    # Past 32768 rows a q5 matrix keeps the per-lane loads (the staged whole
+    # pieces measured slower on the long lm_head stream): one and three
+    # slices per lane, rows past a whole unit.
+    w = o.normal(rows * cols, 14, rows, 0.02).reshape(rows, cols)
+    x = o.normal(cols, 14, 3000 + cols)
+    check(ctx, o.Q5, w, x, 1, f"q5 {rows}x{cols}")
 
 
 @pytest.mark.parametrize("rows,cols,tokens", [
