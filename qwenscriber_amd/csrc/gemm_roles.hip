@@ -8,12 +8,12 @@ namespace qwh {
 namespace {
 
 // Producer / consumer form of the same tile, one 512-thread workgroup per CU:
-// wavefronts 0-3 only multiply and scale (each its 64 x 64 quarter, the
-// half-tile offset as above), wavefronts 4-7 only load, decode and stage the
-// next group into the other LDS buffer. A SIMD then holds one wavefront of
+// wavefronts 0-3 only multiply and scale (each its 64 x 64 quarter, with
+// the half-tile offset of gemm.hip's gemm_bf16_kernel), wavefronts 4-7 only
+// load, decode and stage the next group into the other LDS buffer. A SIMD then holds one wavefront of
 // each kind, so the decode's vector-ALU work and the loads' waits run beside
 // the matrix-core work instead of between it. One barrier per group, as
-// above; both kinds pass the same number of barriers. Each output value is
+// there; both kinds pass the same number of barriers. Each output value is
 // scaled and summed in the same group order as gemm_bf16_kernel, so the two
 // forms give the same bits.
 template <int F>
